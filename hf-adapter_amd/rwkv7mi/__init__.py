@@ -1,0 +1,31 @@
+"""rwkv7mi — MI355X (gfx950) native RWKV-7 inference hot path.
+
+Drop-in operators and quantized modules with the names and signatures of the
+reference adapter (rwkv-rs/hf-adapter 0.8.1), each backed by a hand-written
+HIP kernel in librwkv7mi.so (C ABI: include/rwkv7mi.h).  GPU tensors only.
+"""
+from __future__ import annotations
+
+from . import _lib
+from .fused_recurrent_update import (
+    fused_recurrent_output_prepare,
+    fused_recurrent_output_prepare_raw,
+    fused_recurrent_scan,
+    fused_recurrent_update,
+)
+from .native_quant_mm8 import MM8Linear, mm8_matmul, mm8_matmul_triton, quantize_mm8, quantize_model_mm8
+from .sm70_quant import quantize_w4_groupwise, w4_groupwise_linear
+
+__all__ = [
+    "fused_recurrent_update",
+    "fused_recurrent_output_prepare",
+    "fused_recurrent_output_prepare_raw",
+    "fused_recurrent_scan",
+    "quantize_mm8",
+    "mm8_matmul",
+    "mm8_matmul_triton",
+    "MM8Linear",
+    "quantize_model_mm8",
+    "quantize_w4_groupwise",
+    "w4_groupwise_linear",
+]

@@ -1,0 +1,181 @@
+"""Native MM8 (uint8 affine) quantization with the reference's API.
+
+Mirrors rwkv7_hf/native_quant_mm8.py (rwkv-rs/hf-adapter 0.8.1):
+``quantize_mm8`` (:62), ``mm8_matmul`` (:111), ``mm8_linear`` (:122),
+``mm8_gemv_triton`` (:383), ``mm8_matmul_triton`` (:468), ``MM8Linear``
+(:564) and ``quantize_model_mm8`` (:631).  Packing runs as a gfx950 kernel
+that reproduces the reference's fp32 op sequence bit for bit; every matmul runs
+the fused HIP dequant GEMV/GEMM (fp32 accumulation).  Inputs must be GPU
+tensors: there is no CPU path.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from . import workspace as _ws
+from .native_quant_policy import normalize_native_mm_policy, should_quantize_linear
+
+
+def quantize_mm8(weight: torch.Tensor):
+    """Quantize ``weight: [N, M]`` to the rwkv fp16i8 format.
+
+    Returns ``(w_u8 [N,M] uint8, mx [M], rx [M], my [N,1], ry [N,1])`` in
+    ``weight.dtype``, identical to the reference packer.
+    """
+    if weight.dim() != 2:
+        raise ValueError("quantize_mm8 expects a 2-D weight")
+    _lib.require_gpu(weight, name="quantize_mm8")
+    w = weight.contiguous()
+    n, m = (int(s) for s in w.shape)
+    dev, dt = w.device, w.dtype
+    w_u8 = torch.empty((n, m), device=dev, dtype=torch.uint8)
+    mx = torch.empty(m, device=dev, dtype=dt)
+    rx = torch.empty(m, device=dev, dtype=dt)
+    my = torch.empty((n, 1), device=dev, dtype=dt)
+    ry = torch.empty((n, 1), device=dev, dtype=dt)
+    ws = torch.empty(2 * n + 2 * m, device=dev, dtype=torch.float32)
+    _lib.call(
+        "rwkv7mi_mm8_pack", _lib.ptr(w), n, m, _lib.dtype_code(w), _lib.ptr(w_u8), _lib.ptr(mx),
+        _lib.ptr(rx), _lib.ptr(my), _lib.ptr(ry), _lib.ptr(ws), _lib.stream_of(w),
+    )
+    return w_u8, mx, rx, my, ry
+
+
+def mm8_workspace_bytes(rows: int, n: int, m: int) -> int:
+    return int(_lib.load().rwkv7mi_mm8_workspace_bytes(int(rows), int(n), int(m)))
+
+
+def mm8_matmul_into(x2, w_u8, mx, rx, my, ry, out, *, bias=None, residual=None, epilogue=_lib.EPI_NONE):
+    """``out[rows, M] = epilogue(x2[rows, N] @ dequant(W))`` with no allocation."""
+    rows, n = (int(s) for s in x2.shape)
+    m = int(w_u8.shape[1])
+    if int(w_u8.shape[0]) != n:
+        raise ValueError(f"mm8: x has {n} features but w_u8 is {tuple(w_u8.shape)}")
+    if tuple(out.shape) != (rows, m) or not out.is_contiguous() or out.dtype != x2.dtype:
+        raise ValueError("mm8: out must be a contiguous [rows, M] tensor of x's dtype")
+    _lib.require_gpu(x2, w_u8, out, name="mm8_matmul")
+    need = mm8_workspace_bytes(rows, n, m)
+    ws = _ws.reserve(x2.device, need)
+    meta = mx
+    if residual is not None:
+        residual = residual.reshape(rows, m)
+        if not residual.is_contiguous() or residual.dtype != x2.dtype:
+            raise ValueError("mm8: residual must be contiguous with x's dtype")
+    _lib.call(
+        "rwkv7mi_mm8_matmul", _lib.ptr(x2), _lib.ptr(w_u8), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my),
+        _lib.ptr(ry), _lib.ptr(bias), _lib.ptr(residual), _lib.ptr(out), rows, n, m, int(epilogue),
+        _lib.dtype_code(x2), _lib.dtype_code(meta), _lib.ptr(ws), int(ws.numel()), _lib.stream_of(x2),
+    )
+    return out
+
+
+def _meta_1d(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    t = t.reshape(-1)
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()
+
+
+def mm8_matmul(x, w_u8, mx, rx, my, ry):
+    """``y = x @ dequant(W)`` for ``x: [..., N]`` -> ``[..., M]`` (fused HIP kernel)."""
+    n, m = (int(s) for s in w_u8.shape)
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, n).contiguous()
+    mdt = mx.dtype
+    out = torch.empty((x2.shape[0], m), device=x.device, dtype=x.dtype)
+    mm8_matmul_into(x2, w_u8, _meta_1d(mx, mdt), _meta_1d(rx, mdt), _meta_1d(my, mdt), _meta_1d(ry, mdt), out)
+    return out.reshape(*lead, m)
+
+
+mm8_linear = mm8_matmul
+
+
+def mm8_gemv_triton(x, w_u8, mx, rx, my, ry):
+    """Reference name of the B=1 GEMV; runs the same HIP kernel."""
+    return mm8_matmul(x, w_u8, mx, rx, my, ry)
+
+
+def mm8_matmul_triton(x, w_u8, mx, rx, my, ry, *, max_gemv_rows: int | None = None):
+    """Reference name of the routed matmul; one HIP kernel for every row count."""
+    return mm8_matmul(x, w_u8, mx, rx, my, ry)
+
+
+class MM8Linear(torch.nn.Module):
+    """Drop-in for ``nn.Linear`` storing int8 (mm8) weights, dequantized on the fly.
+
+    Buffers match the reference module: ``w_u8 [in, out]``, ``mx, rx [out]``,
+    ``my, ry [in, 1]`` and optional ``bias``.
+    """
+
+    def __init__(self, linear, *, fused=True):
+        super().__init__()
+        self.in_features, self.out_features = int(linear.weight.shape[1]), int(linear.weight.shape[0])
+        wu8, mx, rx, my, ry = quantize_mm8(linear.weight.data.t().contiguous())
+        self.register_buffer("w_u8", wu8)
+        self.register_buffer("mx", mx)
+        self.register_buffer("rx", rx)
+        self.register_buffer("my", my)
+        self.register_buffer("ry", ry)
+        if linear.bias is not None:
+            self.register_buffer("bias", linear.bias.data.clone())
+        else:
+            self.bias = None
+        self.fused = bool(fused)
+        self.sm7x_rowwise = False
+
+    def _run(self, x, out=None, residual=None, epilogue=_lib.EPI_NONE):
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        rows = int(x2.shape[0])
+        if out is None:
+            out2 = torch.empty((rows, self.out_features), device=x.device, dtype=x.dtype)
+        else:
+            out2 = out.reshape(rows, self.out_features)
+        mm8_matmul_into(x2, self.w_u8, self.mx, self.rx, self.my.reshape(-1), self.ry.reshape(-1), out2,
+                        bias=self.bias, residual=residual, epilogue=epilogue)
+        return out2.reshape(*lead, self.out_features) if out is None else out
+
+    def forward(self, x):
+        return self._run(x)
+
+    def rwkv7_forward_into(self, x, out):
+        return self._run(x, out=out)
+
+    def rwkv7_forward_relu2(self, x):
+        return self._run(x, epilogue=_lib.EPI_RELU2)
+
+    def rwkv7_forward_add(self, x, residual):
+        return self._run(x, residual=residual.contiguous(), epilogue=_lib.EPI_RESIDUAL)
+
+    def rwkv7_workspace_bytes(self, rows: int) -> int:
+        return mm8_workspace_bytes(rows, self.in_features, self.out_features)
+
+    def extra_repr(self):
+        return f"in={self.in_features}, out={self.out_features}, mm8(fused={self.fused}, hip=gfx950)"
+
+
+def quantize_model_mm8(model, *, min_params: int = 8_000_000, fused: bool = True, policy: str = "memory") -> int:
+    """Swap eligible ``nn.Linear`` modules for :class:`MM8Linear`; returns the count."""
+    policy = normalize_native_mm_policy(policy)
+    targets = [
+        name for name, mod in model.named_modules()
+        if isinstance(mod, torch.nn.Linear)
+        and should_quantize_linear(name, int(mod.weight.numel()), min_params=min_params, policy=policy)
+    ]
+    for full_name in targets:
+        parent_name, _, attr = full_name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        setattr(parent, attr, MM8Linear(getattr(parent, attr), fused=fused))
+    setattr(model, "_rwkv7_native_mm_quantization", "mm8")
+    setattr(model, "_rwkv7_native_mm_replaced_modules", len(targets))
+    setattr(model, "_rwkv7_native_mm_block_replaced_modules", sum(n.startswith("model.layers.") for n in targets))
+    return len(targets)
+
+
+__all__ = [
+    "quantize_mm8", "mm8_matmul", "mm8_linear", "mm8_matmul_into", "mm8_gemv_triton",
+    "mm8_matmul_triton", "mm8_workspace_bytes", "MM8Linear", "quantize_model_mm8",
+]

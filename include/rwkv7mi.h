@@ -1,0 +1,161 @@
+/*
+ * rwkv7mi — C ABI of the MI355X (gfx950) RWKV-7 inference hot path.
+ *
+ * Every entry point takes raw device pointers, element counts and a
+ * hipStream_t passed as `void*` (NULL = the legacy default stream), launches
+ * asynchronously, and returns 0 on success or a negative RWKV7MI_E* code.
+ * On failure `rwkv7mi_last_error()` returns a message for the calling thread.
+ * No entry point allocates device memory unless its comment says so; callers
+ * own every buffer.  Nothing here touches torch types.
+ *
+ * Layout conventions (match the reference adapter, rwkv-rs/hf-adapter 0.8.1):
+ *   vectors  r,w,k,v,kk,a,g : [B, H, N] (decode) or [B, T, H, N] (sequence),
+ *                             contiguous, N = 64 (head size).
+ *   state                   : [B, H, N, N] fp32, row = value channel,
+ *                             column = key channel ("native V x K").
+ *   MM8 weight              : w_u8 [I, O] uint8, O contiguous (= Linear.weight.T),
+ *                             mx, rx [O]; my, ry [I] (stored [I,1] by the reference).
+ *   W4 group weight         : packed [O, I/2] uint8 (low nibble = even input),
+ *                             scales [O, I/group] .
+ *   MM4 affine weight       : packed [I, O_pad/2] uint8 (low nibble = even output),
+ *                             mx, rx [O_pad]; my, ry [I].
+ *
+ * dtype codes: RWKV7MI_F32 = 0, RWKV7MI_F16 = 1, RWKV7MI_BF16 = 2.
+ */
+#ifndef RWKV7MI_H
+#define RWKV7MI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  RWKV7MI_F32 = 0,
+  RWKV7MI_F16 = 1,
+  RWKV7MI_BF16 = 2
+};
+
+enum {
+  RWKV7MI_OK = 0,
+  RWKV7MI_EINVAL = -1,   /* bad shape / dtype / pointer argument          */
+  RWKV7MI_ELAUNCH = -2,  /* the HIP runtime rejected a launch or call     */
+  RWKV7MI_ESIZE = -3     /* workspace or scratch too small                */
+};
+
+/* GEMV/GEMM epilogues (MM8, W4 group, MM4). */
+enum {
+  RWKV7MI_EPI_NONE = 0,      /* y = x @ W (+ bias)                         */
+  RWKV7MI_EPI_RELU2 = 1,     /* y = relu(x @ W (+ bias))^2                 */
+  RWKV7MI_EPI_RESIDUAL = 2   /* y = residual + x @ W (+ bias)              */
+};
+
+/* ---------------------------------------------------------------- status */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* rwkv7mi_last_error(void);
+/* Library ABI version (major * 100 + minor). */
+int rwkv7mi_abi_version(void);
+
+/* ------------------------------------------------ wkv7 single-token decode */
+
+/* One-token DPLR update + readout.
+ *   S' = S * w[None,:] - (S @ kk) (kk * a)^T + v k^T ;  y = S' r
+ * Replaces fused_recurrent_update / torch_recurrent_update
+ * (rwkv7_hf/fused_recurrent_update.py:1214, :757) and the torch graph-body
+ * form _recurrent_update_batched (rwkv7_hf/native_jit_recurrent.py:60).
+ * state_out may equal state_in (in-place update).  y has act_dtype. */
+int rwkv7mi_wkv7_decode_update(const void* r, const void* w, const void* k,
+                               const void* v, const void* kk, const void* a,
+                               const float* state_in, float* state_out,
+                               void* y, int64_t B, int64_t H, int64_t N,
+                               int act_dtype, int w_dtype, void* stream);
+
+/* Update + readout + per-head GroupNorm(eps) + bonus (sum r*k*r_k)*v + gate g.
+ * Replaces fused_recurrent_output_prepare
+ * (rwkv7_hf/fused_recurrent_update.py:967) / torch_recurrent_output_prepare
+ * (:846).  r_k [H,N], gn_w/gn_b [H*N] have param_dtype. */
+int rwkv7mi_wkv7_decode_output_prepare(
+    const void* r, const void* w, const void* k, const void* v,
+    const void* kk, const void* a, const float* state_in, float* state_out,
+    const void* g, const void* r_k, const void* gn_w, const void* gn_b,
+    void* out, int64_t B, int64_t H, int64_t N, float eps, int act_dtype,
+    int w_dtype, int param_dtype, void* stream);
+
+/* Raw-input decode fusion: kk = normalize(k_raw * k_k), k = k_raw*(1+(a-1)k_a),
+ * w = exp(-0.606531*sigmoid(w_raw)), then as output_prepare.
+ * Replaces fused_recurrent_output_prepare_raw
+ * (rwkv7_hf/fused_recurrent_update.py:1089, kernel :155).
+ * v_mode: 0 = use v as given; 1 = layer 0: copy v into v_first;
+ *         2 = v = v + (v_first - v) * v_gate (v_gate already sigmoid'd),
+ *             the V interpolation of rwkv7_hf/native.py:219-223.
+ * v_first / v_gate may be NULL when v_mode == 0. */
+int rwkv7mi_wkv7_decode_output_prepare_raw(
+    const void* r, const void* w_raw, const void* k_raw, const void* v,
+    const void* a, const float* state_in, float* state_out, const void* g,
+    const void* k_k, const void* k_a, const void* r_k, const void* gn_w,
+    const void* gn_b, void* out, void* v_first, const void* v_gate,
+    int v_mode, int64_t B, int64_t H, int64_t N, float eps, int act_dtype,
+    int param_dtype, void* stream);
+
+/* ----------------------------------------------------- wkv7 sequence scans */
+
+/* Sequential on-chip scan over T tokens (T x the decode update), y [B,T,H,N].
+ * Replaces fused_recurrent_scan / torch_recurrent_scan
+ * (rwkv7_hf/fused_recurrent_update.py:1299, :800). */
+int rwkv7mi_wkv7_scan(const void* r, const void* w, const void* k,
+                      const void* v, const void* kk, const void* a,
+                      const float* state_in, float* state_out, void* y,
+                      int64_t B, int64_t T, int64_t H, int64_t N,
+                      int act_dtype, int w_dtype, void* stream);
+
+/* ------------------------------------------------------------------- MM8 */
+
+/* Device packer of the uint8 affine format.  weight [I,O] (= Linear.weight.T)
+ * in w_dtype; outputs w_u8 [I,O]; mx, rx [O]; my, ry [I] in w_dtype, with
+ * rx/16 and ry/16 stored exactly as rwkv7_hf/native_quant_mm8.py:62-97.
+ * Needs a float workspace of (2*I + 2*O) floats. */
+int rwkv7mi_mm8_pack(const void* weight, int64_t I, int64_t O, int w_dtype,
+                     uint8_t* w_u8, void* mx, void* rx, void* my, void* ry,
+                     float* workspace, void* stream);
+
+/* Bytes of workspace rwkv7mi_mm8_matmul needs for `rows` activation rows. */
+size_t rwkv7mi_mm8_workspace_bytes(int64_t rows, int64_t I, int64_t O);
+
+/* y[rows,O] = epilogue(x[rows,I] @ dequant(W)), dequant as
+ * (w+0.5)*ry[i]*rx[o] + my[i] + mx[o] with fp32 accumulation.
+ * Replaces mm8_matmul_triton / mm8_gemv_triton / MM8Linear.forward
+ * (rwkv7_hf/native_quant_mm8.py:468, :383, :594).  `workspace` holds
+ * split-K partials and per-tile counters; its counter region must be zero on
+ * the first call and is left zero by every call (see rwkv7mi_mm8_workspace_bytes).
+ * bias [O] / residual [rows,O] may be NULL. */
+int rwkv7mi_mm8_matmul(const void* x, const uint8_t* w_u8, const void* mx,
+                       const void* rx, const void* my, const void* ry,
+                       const void* bias, const void* residual, void* y,
+                       int64_t rows, int64_t I, int64_t O, int epilogue,
+                       int act_dtype, int meta_dtype, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------- W4 group-128 */
+
+/* Device packer of the symmetric group W4 format of
+ * rwkv7_hf/sm70_quant.py:502-519: weight [O,I] -> packed [O,I/2],
+ * scales [O,I/group] (w_dtype).  group in {128, 256}. */
+int rwkv7mi_w4g_pack(const void* weight, int64_t O, int64_t I, int64_t group,
+                     int w_dtype, uint8_t* packed, void* scales, void* stream);
+
+/* y[rows,O] = epilogue(x @ W^T), W[o,i] = (nib - 8) * scales[o, i/group].
+ * Replaces w4_groupwise_linear (rwkv7_hf/sm70_quant.py:579). */
+int rwkv7mi_w4g_matmul(const void* x, const uint8_t* packed,
+                       const void* scales, const void* bias,
+                       const void* residual, void* y, int64_t rows, int64_t O,
+                       int64_t I, int64_t group, int epilogue, int act_dtype,
+                       int scale_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKV7MI_H */

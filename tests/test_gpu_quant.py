@@ -1,0 +1,127 @@
+"""GPU parity: MM8 / W4-group packers (bit-exact) and fused dequant GEMV/GEMM
+(fp64 oracle, relative tolerance) including epilogues and ragged batches."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _cuda(x, dtype):
+    return torch.tensor(np.asarray(x), dtype=dtype, device="cuda")
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _rel_err(got, ref):
+    return np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+
+
+@pytest.mark.parametrize("shape", [(256, 128), (128, 256), (512, 512), (3, 8), (9, 16)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_mm8_pack_bit_exact(oracle, shape, dtype):
+    from rwkv7mi import quantize_mm8
+
+    rng = np.random.default_rng(sum(shape))
+    W = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    Wt = _cuda(W, dtype)
+    w_u8, mx, rx, my, ry = quantize_mm8(Wt)
+    torch.cuda.synchronize()
+    npdt = np.float16 if dtype == torch.float16 else np.float32
+    q, omx, orx, omy, ory = oracle.mm8_pack(_np(Wt.float()), out_dtype=npdt)
+    np.testing.assert_array_equal(_np(w_u8), q)
+    for got, ref in ((mx, omx), (rx, orx), (my, omy), (ry, ory)):
+        np.testing.assert_array_equal(_np(got).view(np.uint16 if npdt == np.float16 else np.uint32),
+                                      np.asarray(ref).view(np.uint16 if npdt == np.float16 else np.uint32))
+    assert my.shape == (shape[0], 1) and ry.shape == (shape[0], 1)
+
+
+SHAPES_MM8 = [(2048, 2048), (2048, 8192), (8192, 2048), (1000, 1032), (128, 64)]
+
+
+@pytest.mark.parametrize("IO", SHAPES_MM8)
+@pytest.mark.parametrize("rows", [1, 8, 32, 64, 65, 3])
+def test_mm8_matmul(oracle, IO, rows):
+    from rwkv7mi.native_quant_mm8 import mm8_matmul, quantize_mm8
+
+    I, O = IO
+    rng = np.random.default_rng(I + O + rows)
+    W = (rng.standard_normal((I, O)) * 0.02).astype(np.float16)
+    x = rng.standard_normal((rows, I)).astype(np.float16)
+    packed = quantize_mm8(_cuda(W, torch.float16))
+    xt = _cuda(x, torch.float16)
+    y = mm8_matmul(xt, *packed)
+    y2 = mm8_matmul(xt, *packed)  # second call exercises the counter reset
+    torch.cuda.synchronize()
+    ref = oracle.mm8_matmul(x.astype(np.float64), *(_np(p) for p in packed))
+    err = _rel_err(_np(y).astype(np.float64), ref)
+    assert err <= 2e-3, err
+    assert torch.equal(y, y2), "repeated calls must be bit-identical"
+
+
+def test_mm8_epilogues_and_module(oracle):
+    from rwkv7mi import MM8Linear
+
+    rng = np.random.default_rng(5)
+    I, O, rows = 1024, 4096, 4
+    lin = torch.nn.Linear(I, O, bias=True).to(device="cuda", dtype=torch.float16)
+    with torch.no_grad():
+        lin.weight.copy_(_cuda(rng.standard_normal((O, I)) * 0.02, torch.float16))
+        lin.bias.copy_(_cuda(rng.standard_normal(O) * 0.1, torch.float16))
+    mod = MM8Linear(lin)
+    assert mod.w_u8.shape == (I, O) and mod.my.shape == (I, 1)
+    x = _cuda(rng.standard_normal((rows, I)), torch.float16)
+    res = _cuda(rng.standard_normal((rows, O)), torch.float16)
+    packed = [_np(b) for b in (mod.w_u8, mod.mx, mod.rx, mod.my, mod.ry)]
+    base = oracle.mm8_matmul(_np(x).astype(np.float64), *packed) + _np(lin.bias).astype(np.float64)
+    y = mod(x)
+    out = torch.empty_like(y)
+    mod.rwkv7_forward_into(x, out)
+    y_relu2 = mod.rwkv7_forward_relu2(x)
+    y_add = mod.rwkv7_forward_add(x, res)
+    y3 = mod(x.reshape(2, 2, I))
+    torch.cuda.synchronize()
+    scale = np.abs(base).max()
+    assert np.abs(_np(y) - base).max() <= 2e-3 * scale
+    assert torch.equal(out, y)
+    assert torch.equal(y3.reshape(rows, O), y)
+    relu2 = np.maximum(base, 0) ** 2
+    assert np.abs(_np(y_relu2) - relu2).max() <= 4e-3 * np.abs(relu2).max()
+    add = base + _np(res).astype(np.float64)
+    assert np.abs(_np(y_add) - add).max() <= 2e-3 * np.abs(add).max()
+
+
+@pytest.mark.parametrize("group", [128, 256])
+@pytest.mark.parametrize("shape", [(24, 256), (4096, 4096), (64, 1024)])
+def test_w4g_pack_bit_exact(oracle, group, shape):
+    from rwkv7mi import quantize_w4_groupwise
+
+    rng = np.random.default_rng(shape[0] + group)
+    W = (rng.standard_normal(shape) * 0.02).astype(np.float16)
+    packed, scales, k = quantize_w4_groupwise(_cuda(W, torch.float16), group_size=group)
+    torch.cuda.synchronize()
+    op, osc, ok = oracle.w4g_pack(W.astype(np.float32), group)
+    assert k == ok
+    np.testing.assert_array_equal(_np(packed), op)
+    np.testing.assert_array_equal(_np(scales).view(np.uint16), osc.view(np.uint16))
+
+
+@pytest.mark.parametrize("OI", [(4096, 4096), (16384, 4096), (4096, 16384), (256, 512)])
+@pytest.mark.parametrize("rows", [1, 4, 16, 40])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_w4g_linear(oracle, OI, rows, dtype):
+    from rwkv7mi import quantize_w4_groupwise, w4_groupwise_linear
+
+    O, I = OI
+    rng = np.random.default_rng(O + I + rows)
+    W = (rng.standard_normal((O, I)) * 0.02).astype(np.float16)
+    packed, scales, k = quantize_w4_groupwise(_cuda(W, torch.float16))
+    x = _cuda(rng.standard_normal((rows, I)), dtype)
+    y = w4_groupwise_linear(x, packed, scales.to(dtype), O, I)
+    torch.cuda.synchronize()
+    ref = oracle.w4g_linear(_np(x).astype(np.float64), _np(packed), _np(scales.to(dtype)).astype(np.float64))
+    assert _rel_err(_np(y).astype(np.float64), ref) <= 2e-3

@@ -1,0 +1,112 @@
+"""Pins of the CPU packers / dequant oracles (CPU only).
+
+Bit-exactness of the packers rests on the restatement using the reference's
+fp32 op sequence (rwkv7_hf/native_quant_mm8.py:62-97,
+rwkv7_hf/sm70_quant.py:502-519, rwkv7_hf/native_quant_mm4.py:77-105).  The
+invariants below are consequences of that algorithm that a wrong branch order,
+a missing /16 or a wrong rounding mode would break.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+
+@pytest.mark.parametrize("shape", [(40, 24), (24, 40), (33, 33), (3, 5), (5, 3)])
+def test_mm8_every_row_and_column_hits_0_and_255(oracle, shape):
+    rng = np.random.default_rng(1)
+    W = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    q, *_ = oracle.mm8_pack(W)
+    assert q.dtype == np.uint8
+    assert (q.min(axis=0) == 0).all() and (q.min(axis=1) == 0).all()
+    assert (q.max(axis=0) == 255).all() and (q.max(axis=1) == 255).all()
+
+
+def test_mm8_branch_order_tall_vs_wide(oracle):
+    rng = np.random.default_rng(2)
+    tall = (rng.standard_normal((50, 20)) * 0.02).astype(np.float32)
+    _, mx, rx, my, ry = oracle.mm8_pack(tall, out_dtype=np.float32)
+    np.testing.assert_array_equal(my.reshape(-1), tall.min(axis=1))  # rows first when N > M
+    wide = (rng.standard_normal((20, 50)) * 0.02).astype(np.float32)
+    _, mx, rx, my, ry = oracle.mm8_pack(wide, out_dtype=np.float32)
+    np.testing.assert_array_equal(mx, wide.min(axis=0))  # columns first when N <= M
+
+
+@pytest.mark.parametrize("shape", [(64, 48), (48, 64)])
+def test_mm8_reconstruction_bound(oracle, shape):
+    rng = np.random.default_rng(3)
+    W = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    q, mx, rx16, my, ry16 = oracle.mm8_pack(W, out_dtype=np.float32)
+    deq = oracle.mm8_dequant(q, mx, rx16, my, ry16)
+    bound = (np.asarray(ry16, np.float64).reshape(-1, 1) * 16) * (np.asarray(rx16, np.float64).reshape(1, -1) * 16) / 512
+    assert (np.abs(deq - W) <= bound * (1 + 1e-5) + 1e-7).all()
+
+
+def test_mm8_constant_matrix(oracle):
+    W = np.full((6, 4), 0.25, np.float32)
+    q, mx, rx16, my, ry16 = oracle.mm8_pack(W, out_dtype=np.float32)
+    assert (q == 0).all()
+    np.testing.assert_array_equal(my.reshape(-1), np.full(6, 0.25, np.float32))
+    np.testing.assert_array_equal(mx, np.zeros(4, np.float32))
+    np.testing.assert_array_equal(rx16, np.full(4, np.float32(1e-8) / np.float32(16), np.float32))
+
+
+def test_mm8_gemv_two_forms_agree(oracle):
+    rng = np.random.default_rng(4)
+    W = (rng.standard_normal((96, 80)) * 0.02).astype(np.float32)
+    packed = oracle.mm8_pack(W)
+    x = rng.standard_normal((5, 96))
+    np.testing.assert_allclose(oracle.mm8_matmul(x, *packed), oracle.mm8_matmul_split(x, *packed),
+                               rtol=1e-11, atol=1e-11)
+
+
+
+
+@pytest.mark.parametrize("group", [128, 256])
+def test_w4g_kat_shapes_and_invariants(oracle, group):
+    # tests/test_sm70_quant.py:118-125: [24, 256] -> packed [24, 128], scales [24, 256/group]
+    rng = np.random.default_rng(5)
+    W = (rng.standard_normal((24, 256)) * 0.02).astype(np.float32)
+    packed, scales, k = oracle.w4g_pack(W, group, out_dtype=np.float32)
+    assert packed.shape == (24, 128) and scales.shape == (24, 256 // group) and k == 256
+    lo, hi = packed & 15, packed >> 4
+    assert lo.min() >= 1 and hi.min() >= 1 and lo.max() <= 15 and hi.max() <= 15
+    g = W.reshape(24, 256 // group, group)
+    np.testing.assert_array_equal(scales, np.maximum(np.abs(g).max(-1) / np.float32(7), np.float32(1e-6)))
+    deq = oracle.w4g_dequant(packed, scales, group)
+    s_full = np.repeat(scales.astype(np.float64), group, axis=1)
+    assert (np.abs(deq - W) <= s_full / 2 * (1 + 1e-6)).all()
+    # the largest-magnitude element of every group lands on +-7
+    q = np.empty((24, 256), np.int64)
+    q[:, 0::2] = lo.astype(np.int64) - 8
+    q[:, 1::2] = hi.astype(np.int64) - 8
+    idx = np.abs(g).argmax(-1)
+    qg = q.reshape(24, 256 // group, group)
+    assert (np.abs(np.take_along_axis(qg, idx[..., None], -1)) == 7).all()
+
+
+def test_w4g_rounds_half_to_even(oracle):
+    # scale = 7/7 = 1 exactly, so w/s is exact and ties are visible
+    W = np.zeros((1, 128), np.float32)
+    W[0, 0] = 7.0
+    W[0, 1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 4.5]
+    packed, scales, _ = oracle.w4g_pack(W, 128, out_dtype=np.float32)
+    assert scales[0, 0] == 1.0
+    q = np.empty(128, np.int64)
+    q[0::2] = (packed[0] & 15).astype(np.int64) - 8
+    q[1::2] = (packed[0] >> 4).astype(np.int64) - 8
+    np.testing.assert_array_equal(q[:9], [7, 0, 2, 2, 0, -2, -2, 4, 4])
+
+
+def test_mm4_invariants(oracle):
+    rng = np.random.default_rng(6)
+    W = (rng.standard_normal((40, 31)) * 0.02).astype(np.float32)  # odd M is padded to 32
+    packed, mx, rx4, my, ry4, m_orig, m_pad = oracle.mm4_pack(W, out_dtype=np.float32)
+    assert packed.shape == (40, 16) and m_orig == 31 and m_pad == 32
+    u = np.empty((40, 32), np.int64)
+    u[:, 0::2] = packed & 15
+    u[:, 1::2] = packed >> 4
+    assert (u.min(0) == 0).all() and (u.max(1) == 15).all()
+    deq = oracle.mm4_dequant(packed, mx, rx4, my, ry4, m_orig)
+    bound = (np.asarray(ry4, np.float64).reshape(-1, 1) * 4) * (np.asarray(rx4, np.float64).reshape(1, -1)[:, :31] * 4) / 32
+    assert (np.abs(deq - W) <= bound * (1 + 1e-5) + 1e-7).all()
