@@ -13,6 +13,7 @@ from .fused_recurrent_update import (
     fused_recurrent_scan,
     fused_recurrent_update,
 )
+from .self_chunk_rwkv7 import dplr_chunk_scan, self_chunk_rwkv7
 from .native_quant_mm8 import MM8Linear, mm8_matmul, mm8_matmul_triton, quantize_mm8, quantize_model_mm8
 from .sm70_quant import quantize_w4_groupwise, w4_groupwise_linear
 
@@ -21,6 +22,8 @@ __all__ = [
     "fused_recurrent_output_prepare",
     "fused_recurrent_output_prepare_raw",
     "fused_recurrent_scan",
+    "self_chunk_rwkv7",
+    "dplr_chunk_scan",
     "quantize_mm8",
     "mm8_matmul",
     "mm8_matmul_triton",

@@ -111,6 +111,18 @@ int rwkv7mi_wkv7_scan(const void* r, const void* w, const void* k,
                       int64_t B, int64_t T, int64_t H, int64_t N,
                       int act_dtype, int w_dtype, void* stream);
 
+/* Chunked DPLR prefill (chunk C = 16): same result as the sequential scan.
+ * w is the per-step decay (w_is_log = 0) or its natural log (w_is_log = 1).
+ * Any T >= 0 (a ragged tail chunk is handled).  Replaces self_chunk_rwkv7
+ * (rwkv7_hf/self_chunk_rwkv7.py:33) and dplr_chunk_scan
+ * (rwkv7_hf/dplr_prefill.py:505). */
+int rwkv7mi_wkv7_chunk_prefill(const void* r, const void* w, const void* k,
+                               const void* v, const void* kk, const void* a,
+                               const float* state_in, float* state_out,
+                               void* y, int64_t B, int64_t T, int64_t H,
+                               int64_t N, int64_t chunk, int w_is_log,
+                               int act_dtype, int w_dtype, void* stream);
+
 /* ------------------------------------------------------------------- MM8 */
 
 /* Device packer of the uint8 affine format.  weight [I,O] (= Linear.weight.T)
