@@ -52,7 +52,7 @@ template <int MT, bool SPLIT, typename TA, typename TM>
 __global__ __launch_bounds__(256) void mm8_kernel(
     const TA* __restrict__ x, const uint8_t* __restrict__ w, const TM* __restrict__ mx,
     const TM* __restrict__ rx, const TM* __restrict__ my, const TM* __restrict__ ry,
-    const TM* __restrict__ bias, const TA* __restrict__ residual, TA* __restrict__ y, int rows,
+    const TM* __restrict__ bias, const TA* residual, TA* y, int rows,
     int I, int O, int KR, int ksplit, int epilogue, float* part, unsigned* cnt) {
   constexpr int R = 16 * MT;
   extern __shared__ __align__(16) char smem[];
@@ -414,5 +414,43 @@ extern "C" int rwkv7mi_mm8_pack(const void* weight, int64_t I, int64_t O, int w_
     hipLaunchKernelGGL((mm8_quantize<TW>), dim3(4096), dim3(256), 0, s, wt, (int)I, (int)O, workspace, w_u8,
                        (TW*)mx, (TW*)rx, (TW*)my, (TW*)ry);
     return check_launch("mm8_pack");
+  });
+}
+
+namespace rwkv7mi {
+// out[i, o] = (w_u8[i, o] + 0.5) * ry[i] * rx[o] + my[i] + mx[o], fp32 math, one rounding.
+template <typename TM, typename TO>
+__global__ __launch_bounds__(256) void mm8_dequant_kernel(const uint8_t* __restrict__ w, const TM* __restrict__ mx,
+                                                          const TM* __restrict__ rx, const TM* __restrict__ my,
+                                                          const TM* __restrict__ ry, TO* __restrict__ out, int I,
+                                                          int O) {
+  const int i = blockIdx.y;
+  const float ryi = to_f32(ry[i]), myi = to_f32(my[i]);
+  for (int o = (blockIdx.x * 256 + threadIdx.x) * 4; o < O; o += gridDim.x * 256 * 4) {
+    const uint32_t q = *reinterpret_cast<const uint32_t*>(w + (int64_t)i * O + o);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float wq = (float)((q >> (8 * e)) & 0xffu) + 0.5f;
+      out[(int64_t)i * O + o + e] = from_f32<TO>(wq * ryi * to_f32(rx[o + e]) + myi + to_f32(mx[o + e]));
+    }
+  }
+}
+}  // namespace rwkv7mi
+
+extern "C" int rwkv7mi_mm8_dequant(const uint8_t* w_u8, const void* mx, const void* rx, const void* my,
+                                   const void* ry, void* out, int64_t I, int64_t O, int meta_dtype, int out_dtype,
+                                   void* stream) {
+  if (I <= 0 || O <= 0 || O % 4 || I > 65535 || O > INT32_MAX) return fail(RWKV7MI_EINVAL, "mm8_dequant: bad shape");
+  if (!w_u8 || !mx || !rx || !my || !ry || !out) return fail(RWKV7MI_EINVAL, "mm8_dequant: null pointer");
+  if (reinterpret_cast<uintptr_t>(w_u8) & 3) return fail(RWKV7MI_EINVAL, "mm8_dequant: w_u8 must be 4-byte aligned");
+  return dispatch_dtype(meta_dtype, [&](auto tm) {
+    using TM = decltype(tm);
+    return dispatch_dtype(out_dtype, [&](auto to) {
+      using TO = decltype(to);
+      const int gx = (int)std::min<int64_t>((O / 4 + 255) / 256, 64);
+      hipLaunchKernelGGL((mm8_dequant_kernel<TM, TO>), dim3(gx, (unsigned)I), dim3(256), 0, as_stream(stream),
+                         w_u8, (const TM*)mx, (const TM*)rx, (const TM*)my, (const TM*)ry, (TO*)out, (int)I, (int)O);
+      return check_launch("mm8_dequant_kernel");
+    });
   });
 }

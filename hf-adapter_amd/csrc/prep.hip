@@ -1,0 +1,119 @@
+// Sequence-form elementwise preparation around the wkv7 scan (gfx950).
+//
+// state prep (rwkv7_hf/fused_prefill.py:43-150, torch form native_jit_prefill.py:779-790):
+//   kk = normalize(k_raw * k_k) per head,  k = k_raw * (1 + (a - 1) * k_a),
+//   v: mode 1 -> v_first = v;  mode 2 -> v = v + (v_first - v) * v_gate,
+//   log_w = -0.606531 * sigmoid(w_raw)  (natural log of the decay, fp32)
+// output prep (rwkv7_hf/fused_output.py:39-84, torch form native_jit_decode.py:862-866):
+//   out = (GroupNorm_H(y) + (sum_head r * k * r_k) * v) * g
+// One 64-lane wave per (row, head): lane = channel.
+#include "common.h"
+
+namespace rwkv7mi {
+
+constexpr int PHD = 64;
+
+template <typename TA, typename TP>
+__global__ __launch_bounds__(256) void state_prep_kernel(const TA* __restrict__ k_raw, const TA* __restrict__ a,
+                                                         const TA* __restrict__ w_raw, TA* v, TA* v_first,
+                                                         const TA* __restrict__ v_gate, const TP* __restrict__ k_k,
+                                                         const TP* __restrict__ k_a, TA* __restrict__ kk_out,
+                                                         TA* __restrict__ k_out, float* __restrict__ logw_out,
+                                                         int64_t rows, int H, int v_mode) {
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= rows * H) return;
+  const int h = (int)(unit % H);
+  const int c = threadIdx.x & 63;
+  const int64_t off = unit * PHD + c;
+  const int pc = h * PHD + c;
+  const float kr = to_f32(k_raw[off]);
+  const float av = to_f32(a[off]);
+  const float ku = kr * to_f32(k_k[pc]);
+  const float nrm = sqrtf(wave_sum(ku * ku));
+  kk_out[off] = from_f32<TA>(ku / fmaxf(nrm, 1.0e-12f));
+  k_out[off] = from_f32<TA>(kr * (1.0f + (av - 1.0f) * to_f32(k_a[pc])));
+  const float wr = to_f32(w_raw[off]);
+  logw_out[off] = -0.606531f / (1.0f + expf(-wr));
+  if (v_mode == 1) {
+    v_first[off] = v[off];
+  } else if (v_mode == 2) {
+    const float vv = to_f32(v[off]);
+    v[off] = from_f32<TA>(vv + (to_f32(v_first[off]) - vv) * to_f32(v_gate[off]));
+  }
+}
+
+template <typename TA, typename TP>
+__global__ __launch_bounds__(256) void output_prep_kernel(const TA* __restrict__ y, const TA* __restrict__ r,
+                                                          const TA* __restrict__ k, const TA* __restrict__ v,
+                                                          const TA* __restrict__ g, const TP* __restrict__ r_k,
+                                                          const TP* __restrict__ gn_w, const TP* __restrict__ gn_b,
+                                                          TA* __restrict__ out, int64_t rows, int H, float eps) {
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= rows * H) return;
+  const int h = (int)(unit % H);
+  const int c = threadIdx.x & 63;
+  const int64_t off = unit * PHD + c;
+  const int pc = h * PHD + c;
+  const float yv = to_f32(y[off]);
+  const float mean = wave_sum(yv) * (1.0f / PHD);
+  const float cen = yv - mean;
+  const float var = wave_sum(cen * cen) * (1.0f / PHD);
+  const float vv = to_f32(v[off]);
+  const float corr = wave_sum(to_f32(r[off]) * to_f32(k[off]) * to_f32(r_k[pc]));
+  const float o = (cen * rsqrtf(var + eps) * to_f32(gn_w[pc]) + to_f32(gn_b[pc]) + corr * vv) * to_f32(g[off]);
+  out[off] = from_f32<TA>(o);
+}
+
+}  // namespace rwkv7mi
+
+using namespace rwkv7mi;
+
+extern "C" int rwkv7mi_state_prep(const void* k_raw, const void* a, const void* w_raw, void* v, void* v_first,
+                                  const void* v_gate, const void* k_k, const void* k_a, void* kk_out, void* k_out,
+                                  float* logw_out, int64_t rows, int64_t H, int64_t N, int v_mode, int act_dtype,
+                                  int param_dtype, void* stream) {
+  if (N != PHD) return fail(RWKV7MI_EINVAL, "state_prep: head size must be 64");
+  if (rows < 0 || H <= 0) return fail(RWKV7MI_EINVAL, "state_prep: bad shape");
+  if (v_mode < 0 || v_mode > 2) return fail(RWKV7MI_EINVAL, "state_prep: bad v_mode");
+  if (rows == 0) return RWKV7MI_OK;
+  if (!k_raw || !a || !w_raw || !v || !k_k || !k_a || !kk_out || !k_out || !logw_out)
+    return fail(RWKV7MI_EINVAL, "state_prep: null pointer");
+  if (v_mode && !v_first) return fail(RWKV7MI_EINVAL, "state_prep: v_mode needs v_first");
+  if (v_mode == 2 && !v_gate) return fail(RWKV7MI_EINVAL, "state_prep: v_mode 2 needs v_gate");
+  const int64_t units = rows * H;
+  if ((units + 3) / 4 > INT32_MAX) return fail(RWKV7MI_EINVAL, "state_prep: too large");
+  return dispatch_dtype(act_dtype, [&](auto ta) {
+    using TA = decltype(ta);
+    return dispatch_dtype(param_dtype, [&](auto tp) {
+      using TP = decltype(tp);
+      hipLaunchKernelGGL((state_prep_kernel<TA, TP>), dim3((unsigned)((units + 3) / 4)), dim3(256), 0,
+                         as_stream(stream), (const TA*)k_raw, (const TA*)a, (const TA*)w_raw, (TA*)v, (TA*)v_first,
+                         (const TA*)v_gate, (const TP*)k_k, (const TP*)k_a, (TA*)kk_out, (TA*)k_out, logw_out,
+                         rows, (int)H, v_mode);
+      return check_launch("state_prep_kernel");
+    });
+  });
+}
+
+extern "C" int rwkv7mi_output_prepare(const void* y, const void* r, const void* k, const void* v, const void* g,
+                                      const void* r_k, const void* gn_w, const void* gn_b, void* out, int64_t rows,
+                                      int64_t H, int64_t N, float eps, int act_dtype, int param_dtype,
+                                      void* stream) {
+  if (N != PHD) return fail(RWKV7MI_EINVAL, "output_prepare: head size must be 64");
+  if (rows < 0 || H <= 0) return fail(RWKV7MI_EINVAL, "output_prepare: bad shape");
+  if (rows == 0) return RWKV7MI_OK;
+  if (!y || !r || !k || !v || !g || !r_k || !gn_w || !gn_b || !out)
+    return fail(RWKV7MI_EINVAL, "output_prepare: null pointer");
+  const int64_t units = rows * H;
+  if ((units + 3) / 4 > INT32_MAX) return fail(RWKV7MI_EINVAL, "output_prepare: too large");
+  return dispatch_dtype(act_dtype, [&](auto ta) {
+    using TA = decltype(ta);
+    return dispatch_dtype(param_dtype, [&](auto tp) {
+      using TP = decltype(tp);
+      hipLaunchKernelGGL((output_prep_kernel<TA, TP>), dim3((unsigned)((units + 3) / 4)), dim3(256), 0,
+                         as_stream(stream), (const TA*)y, (const TA*)r, (const TA*)k, (const TA*)v, (const TA*)g,
+                         (const TP*)r_k, (const TP*)gn_w, (const TP*)gn_b, (TA*)out, rows, (int)H, eps);
+      return check_launch("output_prep_kernel");
+    });
+  });
+}

@@ -65,7 +65,7 @@ __device__ __forceinline__ f16x8 w4_nibbles_to_f16(uint32_t d) {
 template <int MT, typename TA, typename TS>
 __global__ __launch_bounds__(256) void w4g_kernel(const TA* __restrict__ x, const uint8_t* __restrict__ packed,
                                                   const TS* __restrict__ scales, const TS* __restrict__ bias,
-                                                  const TA* __restrict__ residual, TA* __restrict__ y, int rows,
+                                                  const TA* residual, TA* y, int rows,
                                                   int O, int I, int group, int epilogue) {
   constexpr bool SPLIT = sizeof(TA) != 2 || !std::is_same<TA, __half>::value;
   __shared__ float s_red[16 * MT][16];

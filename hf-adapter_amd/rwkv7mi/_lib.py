@@ -50,11 +50,21 @@ SIGNATURES = {
         _i32,
         [_c_p] * 9 + [_i64, _i64, _i64, _i32, _i32, _i32, _c_p, _sz, _c_p],
     ),
+    "rwkv7mi_mm8_dequant": (_i32, [_c_p] * 6 + [_i64, _i64, _i32, _i32, _c_p]),
     "rwkv7mi_w4g_pack": (_i32, [_c_p, _i64, _i64, _i64, _i32, _c_p, _c_p, _c_p]),
     "rwkv7mi_w4g_matmul": (
         _i32,
         [_c_p] * 6 + [_i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_p],
     ),
+    "rwkv7mi_attn_norm_mix6": (
+        _i32, [_c_p] * 8 + [_i64, _i64, _i64, _f32, _i32, _i32, _c_p],
+    ),
+    "rwkv7mi_ffn_add_norm_mix": (_i32, [_c_p] * 8 + [_i64, _i64, _f32, _i32, _i32, _c_p]),
+    "rwkv7mi_seq_norm_mix": (_i32, [_c_p] * 7 + [_i64, _i64, _i64, _i64, _f32, _i32, _i32, _c_p]),
+    "rwkv7mi_layer_norm": (_i32, [_c_p] * 4 + [_i64, _i64, _f32, _i32, _i32, _c_p]),
+    "rwkv7mi_dense_multi": (_i32, [_c_p] * 7 + [_i64, _i64, _i32, _c_p]),
+    "rwkv7mi_state_prep": (_i32, [_c_p] * 11 + [_i64, _i64, _i64, _i32, _i32, _i32, _c_p]),
+    "rwkv7mi_output_prepare": (_i32, [_c_p] * 9 + [_i64, _i64, _i64, _f32, _i32, _i32, _c_p]),
 }
 
 _lock = threading.Lock()
@@ -102,6 +112,11 @@ def call(name: str, *args):
         if rc == -1:
             raise ValueError(f"{name}: {msg}")
         raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr_array(tensors) -> ctypes.Array:
+    """A C array of device pointers (NULL for None)."""
+    return (ctypes.c_void_p * len(tensors))(*[None if t is None else t.data_ptr() for t in tensors])
 
 
 def dtype_code(t: torch.Tensor) -> int:

@@ -1,0 +1,119 @@
+"""Decode LayerNorm + token-shift mixes with the reference's API.
+
+Mirrors ``fused_attn_norm_mix6_decode`` (rwkv7_hf/fused_decode_norm_mix.py:161)
+and ``fused_ffn_add_norm_mix_decode`` (:296): ``previous`` is updated in place
+with the normalised row; outputs are new tensors (or caller buffers via
+``out=``).  The ``stack_*`` options return views into one stacked allocation as
+the reference does.  Runs the gfx950 kernel; GPU tensors only.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _rows(x, name):
+    if x.dim() < 1:
+        raise ValueError(f"{name} must have a hidden dimension")
+    D = int(x.shape[-1])
+    return x.reshape(-1, D), D
+
+
+def _vec(t, D, name):
+    t = t.reshape(-1)
+    if int(t.numel()) != D:
+        raise ValueError(f"{name} must contain {D} values, got {int(t.numel())}")
+    return t.contiguous()
+
+
+def fused_attn_norm_mix6_decode(x, previous, norm_weight, norm_bias, mix_r, mix_w, mix_k, mix_v, mix_a, mix_g,
+                                *, eps: float = 1e-5, num_warps: int = 4, stack_rkv: bool = False,
+                                stack_wav: bool = False, stack_rkv_wagv: bool = False,
+                                force_fallback: bool = False, pre_norm_weight=None, pre_norm_bias=None,
+                                out=None):
+    """LayerNorm ``x``, update ``previous`` in place and return the six mixes (r,w,k,v,a,g).
+
+    ``pre_norm_*`` (extension): layer-0 pre-norm applied to ``x`` first, written back into ``x``.
+    ``out`` (extension): a ``[6, rows, D]`` buffer (order r,w,k,v,a,g) to write into.
+    """
+    x2, D = _rows(x, "x")
+    p2, Dp = _rows(previous, "previous")
+    if Dp != D or p2.shape[0] != x2.shape[0]:
+        raise ValueError("x and previous must have identical shapes")
+    if not p2.is_contiguous() or p2.data_ptr() != previous.data_ptr():
+        raise ValueError("previous must be contiguous (it is updated in place)")
+    if x2.data_ptr() == p2.data_ptr():
+        raise ValueError("x and previous must not alias")
+    params = [_vec(t, D, n) for t, n in ((norm_weight, "norm_weight"), (norm_bias, "norm_bias"))]
+    mixes = [_vec(t, D, n).to(params[0].dtype) for t, n in ((mix_r, "mix_r"), (mix_w, "mix_w"), (mix_k, "mix_k"),
+                                                           (mix_v, "mix_v"), (mix_a, "mix_a"), (mix_g, "mix_g"))]
+    pre = None
+    if pre_norm_weight is not None:
+        pre = (_vec(pre_norm_weight, D, "pre_norm_weight").to(params[0].dtype),
+               _vec(pre_norm_bias, D, "pre_norm_bias").to(params[0].dtype))
+        if x2.data_ptr() != x.data_ptr() or not x2.is_contiguous():
+            raise ValueError("x must be contiguous when the pre-norm is written back")
+    else:
+        x2 = x2.contiguous()
+    rows = int(x2.shape[0])
+    _lib.require_gpu(x2, p2, *params, name="fused_attn_norm_mix6_decode")
+    if out is None:
+        stacked = torch.empty((6, rows, D), device=x2.device, dtype=x2.dtype)
+    else:
+        stacked = out.reshape(6, rows, D)
+    outs = [stacked[i] for i in range(6)]
+    _lib.call("rwkv7mi_attn_norm_mix6", _lib.ptr(x2), _lib.ptr(p2), _lib.ptr(params[0]), _lib.ptr(params[1]),
+              _lib.ptr(pre[0] if pre else None), _lib.ptr(pre[1] if pre else None), _lib.ptr_array(mixes),
+              _lib.ptr_array(outs), 6, rows, D, float(eps), _lib.dtype_code(x2), _lib.dtype_code(params[0]),
+              _lib.stream_of(x2))
+    shape = tuple(x.shape)
+    return tuple(o.reshape(shape) for o in outs)
+
+
+def fused_ffn_add_norm_mix_decode(residual, attn_out, previous, norm_weight, norm_bias, mix, *, eps: float = 1e-5,
+                                  num_warps: int = 4, force_fallback: bool = False, residual_out=None, mixed=None):
+    """``x = residual + attn_out``; ``h = LN(x)``; returns ``(x, h + (previous - h) * mix)``; ``previous <- h``.
+
+    ``attn_out`` may be None (extension): then ``residual`` already holds the sum.
+    """
+    r2, D = _rows(residual, "residual")
+    p2, _ = _rows(previous, "previous")
+    if p2.data_ptr() != previous.data_ptr() or not p2.is_contiguous():
+        raise ValueError("previous must be contiguous (it is updated in place)")
+    a2 = None
+    if attn_out is not None:
+        a2, Da = _rows(attn_out, "attn_out")
+        if Da != D or a2.shape[0] != r2.shape[0]:
+            raise ValueError("residual, attn_out, and previous must have identical shapes")
+        a2 = a2.contiguous()
+    r2 = r2.contiguous()
+    w = _vec(norm_weight, D, "norm_weight")
+    b = _vec(norm_bias, D, "norm_bias").to(w.dtype)
+    m = _vec(mix, D, "mix").to(w.dtype)
+    rows = int(r2.shape[0])
+    _lib.require_gpu(r2, p2, w, name="fused_ffn_add_norm_mix_decode")
+    res_out = residual_out.reshape(rows, D) if residual_out is not None else (
+        torch.empty_like(r2) if a2 is not None else r2)
+    mix_out = mixed.reshape(rows, D) if mixed is not None else torch.empty_like(r2)
+    _lib.call("rwkv7mi_ffn_add_norm_mix", _lib.ptr(r2), _lib.ptr(a2), _lib.ptr(p2), _lib.ptr(w), _lib.ptr(b),
+              _lib.ptr(m), _lib.ptr(res_out if a2 is not None else None), _lib.ptr(mix_out), rows, D, float(eps),
+              _lib.dtype_code(r2), _lib.dtype_code(w), _lib.stream_of(r2))
+    shape = tuple(residual.shape)
+    return res_out.reshape(shape), mix_out.reshape(shape)
+
+
+def layer_norm(x, weight, bias, eps: float = 1e-5, out=None):
+    """``F.layer_norm`` over the last dimension (HIP kernel)."""
+    x2, D = _rows(x, "x")
+    x2 = x2.contiguous()
+    w = _vec(weight, D, "weight")
+    b = _vec(bias, D, "bias").to(w.dtype)
+    y = out.reshape(x2.shape) if out is not None else torch.empty_like(x2)
+    _lib.require_gpu(x2, w, name="layer_norm")
+    _lib.call("rwkv7mi_layer_norm", _lib.ptr(x2), _lib.ptr(y), _lib.ptr(w), _lib.ptr(b), int(x2.shape[0]), D,
+              float(eps), _lib.dtype_code(x2), _lib.dtype_code(w), _lib.stream_of(x2))
+    return y.reshape(x.shape)
+
+
+__all__ = ["fused_attn_norm_mix6_decode", "fused_ffn_add_norm_mix_decode", "layer_norm"]

@@ -1,0 +1,102 @@
+"""W/A/G/V LoRA projections with the reference's API.
+
+Mirrors ``fused_wavg_lora`` (rwkv7_hf/fused_lora.py:706) and ``fused_wag_lora``
+(:559): two grouped launches of the gfx950 dense MFMA kernel — the four down
+projections (tanh for W, sigmoid for G fused) and the four up projections
+(bias, and the V-gate sigmoid fused).  Returns ``(w, a_pre, g, v_gate)``;
+the caller applies the outer sigmoid to ``a_pre`` as in the reference.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+ACT_NONE, ACT_TANH, ACT_SIGMOID, ACT_RELU2 = 0, 1, 2, 3
+
+
+def dense_multi(problems, rows: int):
+    """problems: list of (x2 [rows,K], W [N,K], bias or None, y [rows,N], act)."""
+    xs = [p[0] for p in problems]
+    Ws = [p[1] for p in problems]
+    bs = [p[2] for p in problems]
+    ys = [p[3] for p in problems]
+    Ns = (ctypes_i64 := __import__("ctypes").c_int64 * len(problems))(*[int(p[1].shape[0]) for p in problems])
+    Ks = (__import__("ctypes").c_int64 * len(problems))(*[int(p[1].shape[1]) for p in problems])
+    acts = (__import__("ctypes").c_int * len(problems))(*[int(p[4]) for p in problems])
+    _lib.require_gpu(*xs, *Ws, *ys, name="dense_multi")
+    _lib.call("rwkv7mi_dense_multi", _lib.ptr_array(xs), _lib.ptr_array(Ws), _lib.ptr_array(bs), _lib.ptr_array(ys),
+              Ns, Ks, acts, len(problems), int(rows), _lib.dtype_code(xs[0]), _lib.stream_of(xs[0]))
+
+
+def _flat(x, name):
+    had_seq = x.dim() == 3
+    x2 = x.reshape(-1, int(x.shape[-1]))
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    return x2, had_seq
+
+
+def _lin(w, dtype):
+    w = w.to(dtype) if w.dtype != dtype else w
+    return w.contiguous()
+
+
+def fused_wavg_lora(xw, xa, xg, xv, w_down_weight, a_down_weight, g_down_weight, v_down_weight,
+                    w_up_weight, a_up_weight, g_up_weight, v_up_weight, w_up_bias=None, a_up_bias=None,
+                    g_up_bias=None, v_up_bias=None, *, block_m: int = 16, block_r: int = 64, block_k: int = 64,
+                    num_warps: int = 4, force_fallback: bool = False, mids=None, outs=None):
+    """W: tanh(xw W1^T) W2^T + b;  A: (xa A1^T) A2^T + b (pre-sigmoid);
+    G: sigmoid(xg G1^T) G2^T;  V gate: sigmoid((xv V1^T) V2^T + b)."""
+    x2s = [_flat(x, n) for x, n in ((xw, "xw"), (xa, "xa"), (xg, "xg"), (xv, "xv"))]
+    had_seq = x2s[0][1]
+    xs = [t[0] for t in x2s]
+    rows, D = (int(s) for s in xs[0].shape)
+    for x in xs[1:]:
+        if tuple(x.shape) != (rows, D):
+            raise ValueError("xw, xa, xg and xv must have identical flattened shapes")
+    dt = xs[0].dtype
+    downs = [_lin(w, dt) for w in (w_down_weight, a_down_weight, g_down_weight, v_down_weight)]
+    ups = [_lin(w, dt) for w in (w_up_weight, a_up_weight, g_up_weight, v_up_weight)]
+    biases = [None if b is None else _lin(b, dt) for b in (w_up_bias, a_up_bias, g_up_bias, v_up_bias)]
+    out_dim = int(ups[0].shape[0])
+    for d, u in zip(downs, ups):
+        if int(d.shape[1]) != D or int(u.shape[1]) != int(d.shape[0]) or int(u.shape[0]) != out_dim:
+            raise ValueError("LoRA weights do not match: down [R, D], up [out, R]")
+    dev = xs[0].device
+    if mids is None:
+        mids = [torch.empty((rows, int(d.shape[0])), device=dev, dtype=dt) for d in downs]
+    if outs is None:
+        outs = [torch.empty((rows, out_dim), device=dev, dtype=dt) for _ in range(4)]
+    dense_multi([(xs[0], downs[0], None, mids[0], ACT_TANH), (xs[1], downs[1], None, mids[1], ACT_NONE),
+                 (xs[2], downs[2], None, mids[2], ACT_SIGMOID), (xs[3], downs[3], None, mids[3], ACT_NONE)], rows)
+    dense_multi([(mids[0], ups[0], biases[0], outs[0], ACT_NONE), (mids[1], ups[1], biases[1], outs[1], ACT_NONE),
+                 (mids[2], ups[2], biases[2], outs[2], ACT_NONE), (mids[3], ups[3], biases[3], outs[3], ACT_SIGMOID)],
+                rows)
+    if had_seq:
+        return tuple(o.reshape(int(xw.shape[0]), int(xw.shape[1]), out_dim) for o in outs)
+    return tuple(outs)
+
+
+def fused_wag_lora(xw, xa, xg, w_down_weight, a_down_weight, g_down_weight, w_up_weight, a_up_weight, g_up_weight,
+                   w_up_bias=None, a_up_bias=None, g_up_bias=None, **kwargs):
+    """Layer-0 variant without the V gate; returns ``(w, a_pre, g)``."""
+    x2s = [_flat(x, n)[0] for x, n in ((xw, "xw"), (xa, "xa"), (xg, "xg"))]
+    rows = int(x2s[0].shape[0])
+    dt = x2s[0].dtype
+    downs = [_lin(w, dt) for w in (w_down_weight, a_down_weight, g_down_weight)]
+    ups = [_lin(w, dt) for w in (w_up_weight, a_up_weight, g_up_weight)]
+    biases = [None if b is None else _lin(b, dt) for b in (w_up_bias, a_up_bias, g_up_bias)]
+    out_dim = int(ups[0].shape[0])
+    dev = x2s[0].device
+    mids = [torch.empty((rows, int(d.shape[0])), device=dev, dtype=dt) for d in downs]
+    outs = [torch.empty((rows, out_dim), device=dev, dtype=dt) for _ in range(3)]
+    dense_multi([(x2s[0], downs[0], None, mids[0], ACT_TANH), (x2s[1], downs[1], None, mids[1], ACT_NONE),
+                 (x2s[2], downs[2], None, mids[2], ACT_SIGMOID)], rows)
+    dense_multi([(mids[i], ups[i], biases[i], outs[i], ACT_NONE) for i in range(3)], rows)
+    if xw.dim() == 3:
+        return tuple(o.reshape(int(xw.shape[0]), int(xw.shape[1]), out_dim) for o in outs)
+    return tuple(outs)
+
+
+__all__ = ["fused_wavg_lora", "fused_wag_lora", "dense_multi"]

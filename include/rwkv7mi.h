@@ -150,6 +150,14 @@ int rwkv7mi_mm8_matmul(const void* x, const uint8_t* w_u8, const void* mx,
                        int act_dtype, int meta_dtype, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* Materialise the dequantized weight out [I,O] = (w+0.5)*ry*rx + my + mx
+ * (fp32 math, one rounding to out_dtype), the reference's dequantize_mm8
+ * (rwkv7_hf/native_quant_mm8.py:100-108); used before a library GEMM when a
+ * prefill has many rows.  O % 4 == 0, I <= 65535. */
+int rwkv7mi_mm8_dequant(const uint8_t* w_u8, const void* mx, const void* rx,
+                        const void* my, const void* ry, void* out, int64_t I,
+                        int64_t O, int meta_dtype, int out_dtype, void* stream);
+
 /* ---------------------------------------------------------- W4 group-128 */
 
 /* Device packer of the symmetric group W4 format of
@@ -165,6 +173,79 @@ int rwkv7mi_w4g_matmul(const void* x, const uint8_t* packed,
                        const void* residual, void* y, int64_t rows, int64_t O,
                        int64_t I, int64_t group, int epilogue, int act_dtype,
                        int scale_dtype, void* stream);
+
+/* ------------------------------------------------ LayerNorm + token shift */
+
+/* Decode LN + six token-shift mixes per row (D <= 8192):
+ *   [x = LN_pre(x) written back when pre_w != NULL]  h = LN(x; ln_w, ln_b, eps);
+ *   outs[i] = h + (prev - h) * mixes[i] (i < nmix);  prev <- h.
+ * Replaces fused_attn_norm_mix6_decode (rwkv7_hf/fused_decode_norm_mix.py:161).
+ * x and prev must not alias.  mixes / outs are arrays of nmix pointers. */
+int rwkv7mi_attn_norm_mix6(void* x, void* prev, const void* ln_w,
+                           const void* ln_b, const void* pre_w,
+                           const void* pre_b, const void* const* mixes,
+                           void* const* outs, int64_t nmix, int64_t rows,
+                           int64_t D, float eps, int act_dtype,
+                           int param_dtype, void* stream);
+
+/* x = residual (+ attn_out -> residual_out); h = LN(x);
+ * mixed = h + (prev - h) * mix; prev <- h.
+ * Replaces fused_ffn_add_norm_mix_decode (rwkv7_hf/fused_decode_norm_mix.py:296). */
+int rwkv7mi_ffn_add_norm_mix(const void* residual, const void* attn_out,
+                             void* prev, const void* ln_w, const void* ln_b,
+                             const void* mix, void* residual_out, void* mixed,
+                             int64_t rows, int64_t D, float eps, int act_dtype,
+                             int param_dtype, void* stream);
+
+/* Sequence form over x [B,T,D]: h_t = LN(x_t), prev_t = h_{t-1} (prev_in for
+ * t = 0), outs[i] = h + (prev - h) * mixes[i]; prev_out <- h_{T-1}.
+ * Replaces fused_attn_sequence_shift_mix / fused_ffn_sequence_shift_mix
+ * (rwkv7_hf/fused_time_mix.py:413, :470).  prev_in != prev_out. */
+int rwkv7mi_seq_norm_mix(const void* x, const void* prev_in, void* prev_out,
+                         const void* ln_w, const void* ln_b,
+                         const void* const* mixes, void* const* outs,
+                         int64_t nmix, int64_t B, int64_t T, int64_t D,
+                         float eps, int act_dtype, int param_dtype,
+                         void* stream);
+
+/* y = LN(x) over rows of D (F.layer_norm; used for the pre-norm and the final
+ * norm before the LM head, rwkv7_hf/native_jit_prefill.py:1024-1036). */
+int rwkv7mi_layer_norm(const void* x, void* y, const void* w, const void* b,
+                       int64_t rows, int64_t D, float eps, int act_dtype,
+                       int param_dtype, void* stream);
+
+/* ------------------------------------------------ dense LoRA projections */
+
+/* Up to 4 independent y_i = act_i(x_i @ W_i^T + bias_i) in one launch,
+ * W_i [N_i, K_i] (nn.Linear layout), K_i % 8 == 0, act in
+ * {0 none, 1 tanh, 2 sigmoid, 3 relu^2}.  Replaces the W/A/G/V LoRA down and
+ * up projections of fused_wavg_lora (rwkv7_hf/fused_lora.py:706). */
+int rwkv7mi_dense_multi(const void* const* xs, const void* const* Ws,
+                        const void* const* biases, void* const* ys,
+                        const int64_t* Ns, const int64_t* Ks, const int* acts,
+                        int64_t nprob, int64_t rows, int act_dtype,
+                        void* stream);
+
+/* ------------------------------------------- scan input / output prep */
+
+/* Per (row, head): kk = normalize(k_raw * k_k), k_out = k_raw*(1+(a-1)*k_a),
+ * logw_out = -0.606531*sigmoid(w_raw) (fp32 natural-log decay), and the V
+ * interpolation (v_mode 1: v_first = v; 2: v += (v_first - v) * v_gate).
+ * Replaces fused_prefill_state_prep (rwkv7_hf/fused_prefill.py:184). */
+int rwkv7mi_state_prep(const void* k_raw, const void* a, const void* w_raw,
+                       void* v, void* v_first, const void* v_gate,
+                       const void* k_k, const void* k_a, void* kk_out,
+                       void* k_out, float* logw_out, int64_t rows, int64_t H,
+                       int64_t N, int v_mode, int act_dtype, int param_dtype,
+                       void* stream);
+
+/* out = (GroupNorm_H(y) + (sum_head r*k*r_k) * v) * g per (row, head).
+ * Replaces fused_attn_output_prepare (rwkv7_hf/fused_output.py:190). */
+int rwkv7mi_output_prepare(const void* y, const void* r, const void* k,
+                           const void* v, const void* g, const void* r_k,
+                           const void* gn_w, const void* gn_b, void* out,
+                           int64_t rows, int64_t H, int64_t N, float eps,
+                           int act_dtype, int param_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -212,3 +212,66 @@ def mm4_dequant(packed, mx, rx, my, ry, m_orig):
     deq = ((u + 0.5) * np.asarray(ry, np.float64).reshape(-1, 1) * np.asarray(rx, np.float64).reshape(1, -1)
            + np.asarray(my, np.float64).reshape(-1, 1) + np.asarray(mx, np.float64).reshape(1, -1))
     return deq[:, :m_orig]
+
+
+# ------------------------------------------------- elementwise / small ops
+def layer_norm(x, w, b, eps=1e-5):
+    """F.layer_norm over the last dim, fp64."""
+    x = np.asarray(x, np.float64)
+    m = x.mean(-1, keepdims=True)
+    v = ((x - m) ** 2).mean(-1, keepdims=True)
+    return (x - m) / np.sqrt(v + eps) * np.asarray(w, np.float64) + np.asarray(b, np.float64)
+
+
+def attn_norm_mix6(x, prev, w, b, mixes, eps=1e-5):
+    """rwkv7_hf/fused_decode_norm_mix.py:203-241: h = LN(x); out_i = h + (prev - h) mix_i; returns (outs, h)."""
+    h = layer_norm(x, w, b, eps)
+    return [h + (np.asarray(prev, np.float64) - h) * np.asarray(m, np.float64) for m in mixes], h
+
+
+def seq_norm_mix(x, prev0, w, b, mixes, eps=1e-5):
+    """rwkv7_hf/native_jit_prefill.py:533-540: shift of LN(x) over T with carried prev0; returns (outs, h[:, -1])."""
+    h = layer_norm(x, w, b, eps)
+    prev = np.concatenate([np.asarray(prev0, np.float64)[:, None], h[:, :-1]], 1)
+    return [h + (prev - h) * np.asarray(m, np.float64) for m in mixes], h[:, -1]
+
+
+def _sig(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def wavg_lora(xw, xa, xg, xv, W1, A1, G1, V1, W2, A2, G2, V2, w0, a0, g0, v0):
+    """rwkv7_hf/fused_lora.py:795-803 (fp64): returns (w, a_pre, g, v_gate)."""
+    f = lambda t: np.asarray(t, np.float64)
+    bias = lambda t: 0.0 if t is None else f(t)
+    w = np.tanh(f(xw) @ f(W1).T) @ f(W2).T + bias(w0)
+    a = (f(xa) @ f(A1).T) @ f(A2).T + bias(a0)
+    g = _sig(f(xg) @ f(G1).T) @ f(G2).T + bias(g0)
+    v = _sig((f(xv) @ f(V1).T) @ f(V2).T + bias(v0))
+    return w, a, g, v
+
+
+def output_prepare(y, r, k, v, g, r_k, gn_w, gn_b, H, eps):
+    """rwkv7_hf/fused_output.py:39-84 (fp64) over rows of H*N."""
+    f = lambda t: np.asarray(t, np.float64)
+    y, r, k, v, g = map(f, (y, r, k, v, g))
+    rows = y.shape[0]
+    N = y.shape[1] // H
+    n = group_norm_heads(y, gn_w, gn_b, H, eps)
+    corr = (r.reshape(rows, H, N) * k.reshape(rows, H, N) * f(r_k).reshape(1, H, N)).sum(-1, keepdims=True)
+    return (n + (corr * v.reshape(rows, H, N)).reshape(rows, H * N)) * g
+
+
+def state_prep(k_raw, a, w_raw, v, v_first, v_gate, k_k, k_a, H):
+    """rwkv7_hf/native_jit_prefill.py:779-790 (fp64): returns (kk, k, v, log_w)."""
+    f = lambda t: np.asarray(t, np.float64)
+    k_raw, a, w_raw, v = map(f, (k_raw, a, w_raw, v))
+    rows = k_raw.shape[0]
+    N = k_raw.shape[1] // H
+    kk = (k_raw * f(k_k).reshape(1, -1)).reshape(rows, H, N)
+    kk = (kk / np.maximum(np.linalg.norm(kk, axis=-1, keepdims=True), 1e-12)).reshape(rows, H * N)
+    k = k_raw * (1 + (a - 1) * f(k_a).reshape(1, -1))
+    if v_gate is not None:
+        v = v + (f(v_first) - v) * f(v_gate)
+    logw = -0.606531 * _sig(w_raw)
+    return kk, k, v, logw

@@ -1,0 +1,139 @@
+"""GPU parity of the end-to-end RWKV-7 model (prefill, eager decode, graph decode)
+against the fp64 per-token oracle (oracle/model_oracle.py), with and without MM8.
+
+Tolerance: logits max-abs error <= 2e-2 x max|logit| (fp16 activations through
+the whole stack); greedy ids must agree wherever the oracle's top-2 margin
+exceeds that tolerance.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_REL = 2e-2
+
+
+def _cfg(mm8: bool, layers=2):
+    from rwkv7mi.model import NativeRWKV7Config
+
+    return NativeRWKV7Config(vocab_size=512, hidden_size=128, num_hidden_layers=layers, intermediate_size=256,
+                             decay_low_rank_dim=32, a_low_rank_dim=32, gate_low_rank_dim=64, v_low_rank_dim=32,
+                             use_native_mm8=mm8, native_mm8_min_params=0)
+
+
+def _build(mm8: bool, layers=2, seed=0):
+    from oracle.model_oracle import ModelOracle
+    from oracle import oracle as o
+    from rwkv7mi.model import NativeRWKV7ForCausalLM, QuantLinear, random_weights
+
+    cfg = _cfg(mm8, layers)
+    w = random_weights(cfg, seed=seed, device="cpu", dtype=torch.float16)
+    model = NativeRWKV7ForCausalLM(cfg, w, device="cuda", dtype=torch.float16)
+    override = {}
+    if mm8:
+        named = {"lm_head": model.lm_head}
+        for L in model.layers:
+            p = f"model.layers.{L.idx}."
+            named.update({p + "attn.r_proj": L.r_proj, p + "attn.k_proj": L.k_proj, p + "attn.v_proj": L.v_proj,
+                          p + "attn.o_proj": L.o_proj, p + "ffn.key": L.key, p + "ffn.value": L.value})
+        for name, lin in named.items():
+            assert isinstance(lin, QuantLinear), name
+            m = lin.m
+            override[name] = o.mm8_dequant(*(t.cpu().numpy() for t in (m.w_u8, m.mx, m.rx, m.my, m.ry)))
+    ref = ModelOracle(cfg, {k: v.float().numpy() for k, v in w.items()}, override)
+    return cfg, model, ref
+
+
+def _close(got, ref):
+    got = got.float().cpu().numpy().astype(np.float64)
+    scale = np.abs(ref).max()
+    err = np.abs(got - ref).max()
+    assert err <= LOGIT_REL * scale, (err, scale)
+    top2 = np.sort(ref, -1)[:, -2:]
+    margin = top2[:, 1] - top2[:, 0]
+    sure = margin > 2 * LOGIT_REL * scale
+    np.testing.assert_array_equal(got.argmax(-1)[sure], ref.argmax(-1)[sure])
+
+
+@pytest.mark.parametrize("mm8", [False, True])
+def test_prefill_then_decode_matches_oracle(mm8):
+    cfg, model, ref = _build(mm8)
+    rng = np.random.default_rng(1)
+    B, T = 2, 37
+    ids = rng.integers(0, cfg.vocab_size, (B, T))
+    ref_logits, st = ref.run(ids)
+    logits, cache = model(torch.tensor(ids, device="cuda"))
+    torch.cuda.synchronize()
+    _close(logits[:, -1], ref_logits[:, -1])
+    # the cache matches the oracle's recurrent state after the prompt
+    for i in range(cfg.num_hidden_layers):
+        s = cache._state[i].double().cpu().numpy()
+        assert np.abs(s - st["state"][i]).max() <= 2e-2 * np.abs(st["state"][i]).max()
+    nxt = ids[:, -1]
+    for step in range(4):
+        nxt = rng.integers(0, cfg.vocab_size, (B,))
+        r = ref.step(nxt, st)
+        lg, cache = model(torch.tensor(nxt[:, None], device="cuda"), cache)
+        torch.cuda.synchronize()
+        _close(lg[:, -1], r)
+    assert cache.seen_tokens == T + 4
+
+
+@pytest.mark.parametrize("mm8", [False, True])
+def test_graph_decode_equals_eager_decode(mm8):
+    cfg, model, _ = _build(mm8)
+    rng = np.random.default_rng(2)
+    B = 3
+    ids = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 9)), device="cuda")
+    _, c1 = model(ids)
+    c2 = c1.clone()
+    runner = model.graph_runner(B)
+    for step in range(5):
+        tok = torch.tensor(rng.integers(0, cfg.vocab_size, (B,)), device="cuda")
+        eager, c1 = model(tok[:, None], c1)
+        lg = runner.replay(tok, c2).clone()
+        _ = torch.randn(64, device="cuda").sum()  # unrelated eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(lg, eager[:, -1]), step
+    for a, b in zip(c1._state, c2._state):
+        assert torch.equal(a, b)
+
+
+def test_generate_greedy_matches_oracle():
+    cfg, model, ref = _build(True)
+    rng = np.random.default_rng(3)
+    ids = rng.integers(0, cfg.vocab_size, (2, 12))
+    out = model.generate(torch.tensor(ids, device="cuda"), 6).cpu().numpy()
+    st = ref.new_state(2)
+    lg, st = ref.run(ids, st)
+    seq = [ids]
+    nxt = lg[:, -1].argmax(-1)
+    margins = []
+    for _ in range(6):
+        seq.append(nxt[:, None])
+        top2 = np.sort(lg[:, -1] if len(seq) == 2 else r, -1)[:, -2:]
+        margins.append(top2[:, 1] - top2[:, 0])
+        r = ref.step(nxt, st)
+        nxt = r.argmax(-1)
+    ref_ids = np.concatenate(seq, 1)
+    scale = np.abs(lg).max()
+    # compare up to the first near-tie of the oracle
+    for t in range(6):
+        if (margins[t] <= 2 * LOGIT_REL * scale).any():
+            break
+        np.testing.assert_array_equal(out[:, 12 + t], ref_ids[:, 12 + t])
+
+
+def test_cache_select_and_repeat():
+    cfg, model, _ = _build(False)
+    ids = torch.randint(0, cfg.vocab_size, (3, 5), device="cuda")
+    _, cache = model(ids)
+    sel = cache.clone().select_batch(torch.tensor([2, 0], device="cuda"))
+    assert sel.get_batch_size() == 2
+    assert torch.equal(sel._state[1][0], cache._state[1][2])
+    rep = cache.clone()
+    rep.batch_repeat_interleave(2)
+    assert rep.get_batch_size() == 6 and torch.equal(rep._state[0][1], cache._state[0][0])

@@ -1,0 +1,133 @@
+"""GPU parity of the elementwise / small-GEMM kernels around the scan
+(LN + token-shift mixes, W/A/G/V LoRA, output prep, state prep) against the
+fp64 oracle.  Tolerance: max-abs <= 1e-2 x max(1, max|ref|) for fp16 outputs."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(x, dt=torch.float16):
+    return torch.tensor(np.asarray(x), dtype=dt, device="cuda")
+
+
+def _f(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _ok(got, ref, tol=1e-2):
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(_f(got) - ref).max()
+    assert err <= tol * max(1.0, np.abs(ref).max()), (err, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("rows,D,pre", [(1, 4096, False), (8, 768, True), (3, 2560, False)])
+def test_attn_norm_mix6(oracle, rows, D, pre):
+    from rwkv7mi.fused_decode_norm_mix import fused_attn_norm_mix6_decode
+
+    rng = np.random.default_rng(D + rows)
+    x = _t(rng.standard_normal((rows, D)))
+    prev = _t(rng.standard_normal((rows, D)))
+    w, b = _t(1 + 0.1 * rng.standard_normal(D)), _t(0.1 * rng.standard_normal(D))
+    mixes = [_t(rng.random(D)) for _ in range(6)]
+    pw, pb = (_t(1 + 0.1 * rng.standard_normal(D)), _t(0.1 * rng.standard_normal(D))) if pre else (None, None)
+    x_np, prev_np = _f(x), _f(prev)
+    outs = fused_attn_norm_mix6_decode(x, prev, w, b, *mixes, pre_norm_weight=pw, pre_norm_bias=pb)
+    torch.cuda.synchronize()
+    if pre:
+        x_np = oracle.layer_norm(x_np, _f(pw), _f(pb))
+        _ok(x, x_np)
+    ref, h = oracle.attn_norm_mix6(x_np, prev_np, _f(w), _f(b), [_f(m) for m in mixes])
+    for got, r in zip(outs, ref):
+        _ok(got, r)
+    _ok(prev, h)
+
+
+def test_ffn_add_norm_mix(oracle):
+    from rwkv7mi.fused_decode_norm_mix import fused_ffn_add_norm_mix_decode
+
+    rng = np.random.default_rng(3)
+    rows, D = 4, 4096
+    res, att, prev = (_t(rng.standard_normal((rows, D))) for _ in range(3))
+    w, b, m = _t(1 + 0.1 * rng.standard_normal(D)), _t(0.1 * rng.standard_normal(D)), _t(rng.random(D))
+    prev_np = _f(prev)
+    x, mixed = fused_ffn_add_norm_mix_decode(res, att, prev, w, b, m)
+    torch.cuda.synchronize()
+    xs = _f(res) + _f(att)
+    _ok(x, xs)
+    (ref,), h = oracle.attn_norm_mix6(_f(x), prev_np, _f(w), _f(b), [_f(m)])
+    _ok(mixed, ref)
+    _ok(prev, h)
+
+
+@pytest.mark.parametrize("B,T,D", [(2, 33, 768), (1, 1, 4096), (3, 5, 256)])
+def test_sequence_shift_mix(oracle, B, T, D):
+    from rwkv7mi.fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
+
+    rng = np.random.default_rng(B * T)
+    x = _t(rng.standard_normal((B, T, D)))
+    prev = _t(rng.standard_normal((B, D)))
+    w, b = _t(1 + 0.1 * rng.standard_normal(D)), _t(0.1 * rng.standard_normal(D))
+    mixes = [_t(rng.random(D)) for _ in range(6)]
+    *outs, last = fused_attn_sequence_shift_mix(x, prev, *mixes, norm_weight=w, norm_bias=b)
+    fk, last_f = fused_ffn_sequence_shift_mix(x, prev, mixes[0], norm_weight=w, norm_bias=b)
+    torch.cuda.synchronize()
+    ref, ref_last = oracle.seq_norm_mix(_f(x), _f(prev), _f(w), _f(b), [_f(m) for m in mixes])
+    for got, r in zip(outs, ref):
+        _ok(got, r)
+    _ok(last, ref_last)
+    _ok(fk, ref[0])
+    _ok(last_f, ref_last)
+
+
+@pytest.mark.parametrize("rows,D", [(1, 4096), (8, 2048), (40, 768), (300, 256)])
+def test_wavg_lora(oracle, rows, D):
+    from rwkv7mi.fused_lora import fused_wavg_lora
+
+    rng = np.random.default_rng(rows + D)
+    A = D
+    xs = [_t(rng.standard_normal((rows, D))) for _ in range(4)]
+    ranks = (64, 64, 128, 32)
+    downs = [_t(rng.standard_normal((r, D)) * 0.02) for r in ranks]
+    ups = [_t(rng.standard_normal((A, r)) * 0.1) for r in ranks]
+    biases = [_t(rng.standard_normal(A) * 0.01), _t(rng.standard_normal(A) * 0.01), None,
+              _t(rng.standard_normal(A) * 0.01)]
+    got = fused_wavg_lora(*xs, *downs, *ups, *biases)
+    torch.cuda.synchronize()
+    ref = oracle.wavg_lora(*map(_f, xs), *map(_f, downs), *map(_f, ups),
+                           *[None if b is None else _f(b) for b in biases])
+    for g, r in zip(got, ref):
+        _ok(g, r)
+
+
+def test_output_prepare_and_state_prep(oracle):
+    from rwkv7mi.fused_output import fused_attn_output_prepare
+    from rwkv7mi.fused_prefill import fused_prefill_state_prep
+
+    rng = np.random.default_rng(5)
+    rows, H, N = 70, 12, 64
+    A = H * N
+    y, r, k, v, g = (_t(rng.standard_normal((rows, A))) for _ in range(5))
+    r_k, gw, gb = _t(0.1 * rng.standard_normal((H, N))), _t(1 + rng.standard_normal(A) * 0.1), _t(rng.standard_normal(A) * 0.1)
+    out = fused_attn_output_prepare(y, r, k, v, g, r_k, gw, gb, num_heads=H, head_dim=N, head_v_dim=N, eps=N * 1e-5)
+    torch.cuda.synchronize()
+    _ok(out, oracle.output_prepare(_f(y), _f(r), _f(k), _f(v), _f(g), _f(r_k), _f(gw), _f(gb), H, N * 1e-5))
+    k_raw, w_raw, vv = (_t(rng.standard_normal((rows, A))) for _ in range(3))
+    a = _t(1 / (1 + np.exp(-rng.standard_normal((rows, A)))))
+    k_k, k_a = _t(0.85 + 0.1 * rng.standard_normal(A)), _t(1 + 0.1 * rng.standard_normal(A))
+    vfirst = _t(rng.standard_normal((rows, A)))
+    vgate = _t(1 / (1 + np.exp(-rng.standard_normal((rows, A)))))
+    w_log, k_out, v_out, kk = fused_prefill_state_prep(w_raw, k_raw, vv, a, k_k, k_a, v_first=vfirst, v_gate=vgate,
+                                                       num_heads=H, head_dim=N, w_transform="log")
+    w_dec, *_ = fused_prefill_state_prep(w_raw, k_raw, vv, a, k_k, k_a, num_heads=H, head_dim=N)
+    torch.cuda.synchronize()
+    rkk, rk, rv, rlog = oracle.state_prep(_f(k_raw), _f(a), _f(w_raw), _f(vv), _f(vfirst), _f(vgate), _f(k_k),
+                                          _f(k_a), H)
+    _ok(kk, rkk)
+    _ok(k_out, rk)
+    _ok(v_out, rv)
+    _ok(w_log, rlog, 1e-5)
+    _ok(w_dec, np.exp(rlog), 1e-5)
