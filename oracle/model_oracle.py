@@ -26,12 +26,13 @@ def _sigmoid(x):
 
 
 class ModelOracle:
-    def __init__(self, cfg, weights: dict, linear_override: dict | None = None):
+    def __init__(self, cfg, weights: dict, linear_override: dict | None = None, dtype=np.float64):
         """weights: name -> array; linear_override: linear name (without .weight)
-        -> W_hat [in, out] fp64 used as x @ W_hat."""
+        -> W_hat [in, out] used as x @ W_hat.  dtype: fp64 (checker) or fp32 (CPU baseline)."""
         self.cfg = cfg
-        self.w = {k: np.asarray(v, dtype=np.float64) for k, v in weights.items()}
-        self.lin = {k: np.asarray(v, dtype=np.float64) for k, v in (linear_override or {}).items()}
+        self.dtype = dtype
+        self.w = {k: np.asarray(v, dtype=dtype) for k, v in weights.items()}
+        self.lin = {k: np.asarray(v, dtype=dtype) for k, v in (linear_override or {}).items()}
 
     def _linear(self, name, x):
         if name in self.lin:
@@ -41,12 +42,18 @@ class ModelOracle:
     def new_state(self, B):
         c = self.cfg
         H, N, D, A, L = c.num_heads, c.head_dim, c.hidden_size, c.attention_hidden_size, c.num_hidden_layers
+        dt = self.dtype
         return {
-            "state": [np.zeros((B, H, N, N)) for _ in range(L)],
-            "xpa": [np.zeros((B, D)) for _ in range(L)],
-            "xpf": [np.zeros((B, D)) for _ in range(L)],
-            "v_first": np.zeros((B, A)),
+            "state": [np.zeros((B, H, N, N), dt) for _ in range(L)],
+            "xpa": [np.zeros((B, D), dt) for _ in range(L)],
+            "xpf": [np.zeros((B, D), dt) for _ in range(L)],
+            "v_first": np.zeros((B, A), dt),
         }
+
+    def head(self, x):
+        """Final norm + LM head of one hidden row batch (used to time the head alone)."""
+        w = self.w
+        return self._linear("lm_head", _ln(x, w["model.norm.weight"], w["model.norm.bias"], self.cfg.norm_eps))
 
     def step(self, tokens, st):
         """One token per row (tokens [B]); updates st in place; returns logits [B, V]."""
