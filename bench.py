@@ -193,7 +193,9 @@ def run_decode(batches=(1, 8), steps=64, warmup=5, log=print):
         res[B] = {"tok_s": B / (ms / 1e3), "ms": ms, "wall_s": wall, "bytes": nbytes, "gbs": gbs,
                   "frac": gbs / HBM_PEAK_GBS}
         log(f"bench: decode bsz {B}: {ms:.3f} ms/step, {B / (ms / 1e3):.1f} tok/s, {gbs:.0f} GB/s")
-    # MM8 GEMV roofline: events around every MM8 launch of one eager bsz-1 step
+    # MM8 GEMV roofline: events around every MM8 launch of eager bsz-1 steps.  A
+    # spin kernel queued first keeps the GPU busy while Python enqueues the step,
+    # so the kernels run back to back and each event pair brackets GPU time only.
     B = 1
     cache = model.new_cache(B)
     toks = torch.zeros(B, dtype=torch.long, device="cuda")
@@ -201,25 +203,37 @@ def run_decode(batches=(1, 8), steps=64, warmup=5, log=print):
     bufs = model._decode_buffers(B)
     model.decode_step_(toks, cache, logits, bufs)
     records = []
-    orig = QuantLinear.apply
+    orig_apply, orig_group = QuantLinear.apply, QuantLinear.apply_group
 
-    def timed_apply(self, x2, out, **kw):
+    def mm8_bytes(lin, rows):
+        i, o = lin.in_features, lin.out_features
+        return o * i + 2 * (i + o) * 2 + rows * (i + o) * 2
+
+    def bracket(nbytes, call):
         s = torch.cuda.current_stream()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(s)
-        r = orig(self, x2, out, **kw)
+        r = call()
         e1.record(s)
-        i, o = self.in_features, self.out_features
-        records.append((e0, e1, o * i + 2 * (i + o) * 2 + int(x2.shape[0]) * (i + o) * 2))
+        records.append((e0, e1, nbytes))
         return r
 
+    def timed_apply(self, x2, out, **kw):
+        return bracket(mm8_bytes(self, int(x2.shape[0])), lambda: orig_apply(self, x2, out, **kw))
+
+    def timed_group(lins, xs, outs):
+        nb = sum(mm8_bytes(l, int(x.shape[0])) for l, x in zip(lins, xs))
+        return bracket(nb, lambda: orig_group(lins, xs, outs))
+
     QuantLinear.apply = timed_apply
+    QuantLinear.apply_group = staticmethod(timed_group)
     try:
         for _ in range(3):
+            torch.cuda._sleep(50_000_000)
             model.decode_step_(toks, cache, logits, bufs)
         torch.cuda.synchronize()
     finally:
-        QuantLinear.apply = orig
+        QuantLinear.apply, QuantLinear.apply_group = orig_apply, staticmethod(orig_group)
     tot_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in records)
     tot_b = sum(b for _, _, b in records)
     res["mm8_kernel"] = {"launches": len(records), "avg_us": 1e3 * tot_ms / len(records),
@@ -272,6 +286,7 @@ def main(argv=None):
     ap.add_argument("--workload", choices=["all", "decode", "scan"], default="all")
     ap.add_argument("--heads", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--batches", default="1,8", help="decode batch sizes (the first is the headline)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -289,7 +304,8 @@ def main(argv=None):
         log(f"bench: scan {scan['config']}: {scan['ms']:.3f} ms, {scan['tok_s'] / 1e6:.1f} M tok/s, "
             f"{100 * scan['frac']:.1f}% of HBM roofline")
     if args.workload in ("all", "decode"):
-        dec = run_decode(steps=args.steps, warmup=args.warmup, log=log)
+        dec = run_decode(batches=tuple(int(b) for b in args.batches.split(",")), steps=args.steps,
+                         warmup=args.warmup, log=log)
     if dec is not None:
         d1 = dec[1]
         mk = dec["mm8_kernel"]
@@ -303,12 +319,13 @@ def main(argv=None):
                        "hidden": 4096, "heads": 64, "ffn": 16384, "vocab": 65536, "global_batch": 1,
                        "parallelism": "single-gpu"},
             "roofline": {"bound": "hbm", "achieved": round(mk["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(mk["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "mm8_kernel",
+                         "frac": round(mk["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "mm8t_kernel",
                          "avg_launch_us": round(mk["avg_us"], 3),
                          "bytes_per_launch": round(mk["bytes_per_launch"]), "launches_per_step": mk["launches"] // 3},
             "decode": {str(b): {"tok_s": round(dec[b]["tok_s"], 2), "ms_per_step": round(dec[b]["ms"], 4),
                                 "step_bytes": dec[b]["bytes"], "step_gbs": round(dec[b]["gbs"], 1),
-                                "step_roofline_frac": round(dec[b]["frac"], 4)} for b in (1, 8)},
+                                "step_roofline_frac": round(dec[b]["frac"], 4)}
+                       for b in dec if isinstance(b, int)},
         }
     if scan is not None:
         s = {"tok_s": round(scan["tok_s"], 1), "ms_per_call": round(scan["ms"], 4), "config": scan["config"],

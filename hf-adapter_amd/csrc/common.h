@@ -63,6 +63,106 @@ inline int dispatch_dtype(int code, F&& f) {
   }
 }
 
+// ------------------------------------------------- 8-element vector I/O
+// p must be 16-byte aligned (32-byte for float); values convert to/from fp32.
+__device__ __forceinline__ void ld8(const float* p, float (&o)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+// two packed fp16 -> fp32.  (Decoded from a plain uint32_t: hipcc has been seen
+// to read element 0 for __builtin_bit_cast applied to a vector subscript.)
+__device__ __forceinline__ void f16x2_to_f32(uint32_t w, float& lo, float& hi) {
+  lo = __half2float(__ushort_as_half((unsigned short)(w & 0xffffu)));
+  hi = __half2float(__ushort_as_half((unsigned short)(w >> 16)));
+}
+
+__device__ __forceinline__ void ld8(const __half* p, float (&o)[8]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t d[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) f16x2_to_f32(d[q], o[2 * q], o[2 * q + 1]);
+}
+__device__ __forceinline__ void ld8(const __hip_bfloat16* p, float (&o)[8]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t d[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    o[2 * q] = __uint_as_float(d[q] << 16);
+    o[2 * q + 1] = __uint_as_float(d[q] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void st8(float* p, const float (&v)[8]) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+template <typename T>
+__device__ __forceinline__ void st8(T* p, const float (&v)[8]) {
+  uint32_t d[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const T lo = from_f32<T>(v[2 * q]), hi = from_f32<T>(v[2 * q + 1]);
+    d[q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+  }
+  *reinterpret_cast<uint4*>(p) = make_uint4(d[0], d[1], d[2], d[3]);
+}
+// ------------------------------------------------------ raw buffer loads
+// An offset at or beyond the descriptor's byte count returns zeros without a
+// memory access, so bounds checks become offset selects and loads stay
+// unconditional: a straight run of loads is issued back to back and waited on
+// once, instead of one branch and one full wait per load.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t BUF_OOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ float buf_ldf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+// 8 consecutive T elements from element index e (zeros when !valid) -> fp32
+__device__ __forceinline__ void buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t e, bool valid, const float*,
+                                        float (&o)[8]) {
+  const u32x4 a = buf_ld16(r, valid ? e * 4u : BUF_OOB);
+  const u32x4 b = buf_ld16(r, valid ? e * 4u + 16u : BUF_OOB);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    o[q] = __uint_as_float(a[q]);
+    o[4 + q] = __uint_as_float(b[q]);
+  }
+}
+__device__ __forceinline__ void buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t e, bool valid, const __half*,
+                                        float (&o)[8]) {
+  const u32x4 a = buf_ld16(r, valid ? e * 2u : BUF_OOB);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t w = a[q];
+    f16x2_to_f32(w, o[2 * q], o[2 * q + 1]);
+  }
+}
+__device__ __forceinline__ void buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t e, bool valid, const __hip_bfloat16*,
+                                        float (&o)[8]) {
+  const u32x4 a = buf_ld16(r, valid ? e * 2u : BUF_OOB);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    o[2 * q] = __uint_as_float(a[q] << 16);
+    o[2 * q + 1] = __uint_as_float(a[q] & 0xffff0000u);
+  }
+}
+
+// round each value to T and back (the value a T tensor would hold)
+template <typename T>
+__device__ __forceinline__ void round8(float (&v)[8]) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) v[q] = to_f32(from_f32<T>(v[q]));
+}
+
 }  // namespace rwkv7mi
 
 namespace rwkv7mi {

@@ -1,0 +1,313 @@
+// RWKV-7 W/A/G/V LoRA projections (rwkv7_hf/fused_lora.py:559 fused_wag_lora,
+// :706 fused_wavg_lora; torch form :795-803) as two grouped launches.
+//
+//   mid_p = act_down_p(x_p @ Wd_p^T)          Wd_p [r_p, D]   (no bias)
+//   y_p   = act_up_p(mid_p @ Wu_p^T + b_p)    Wu_p [A, r_p]
+//
+// The down projections are tall and thin (r_p = 32..128 features over
+// D = 4096 inputs): one workgroup per 16-feature tile would put only ~18
+// workgroups on the chip, so K is split into `ks` ranges and each workgroup
+// writes an fp32 partial tile.  The up kernel sums the partials of its inputs
+// in fixed order, applies act_down and rounds to the activation dtype (the
+// value the reference's mid tensor holds), stages them in LDS, and runs the
+// up projection on v_mfma_f32_16x16x32_f16 — so the split costs no extra
+// launch and the result is deterministic.  fp32 / bf16 operands are split
+// into fp16 hi + lo as in the dense kernel.
+#include "common.h"
+
+namespace rwkv7mi {
+
+enum { LORA_ACT_NONE = 0, LORA_ACT_TANH = 1, LORA_ACT_SIGMOID = 2 };
+constexpr int LORA_MAXR = 256;   // largest rank
+constexpr int LORA_ROWS = 32;    // rows per launch pair
+
+struct LoraProb {
+  const void* x;
+  const void* wd;
+  const void* wu;
+  const void* bu;
+  void* y;
+  int r, act_d, act_u, tile_d0, tile_u0;
+  int64_t part_off;  // floats
+};
+struct LoraBatch {
+  LoraProb p[4];
+  int nprob, D, A, ks, kr;
+};
+
+__device__ __forceinline__ float lora_act(float v, int act) {
+  if (act == LORA_ACT_TANH) return tanhf(v);
+  if (act == LORA_ACT_SIGMOID) return 1.0f / (1.0f + expf(-v));
+  return v;
+}
+
+// 8 consecutive elements at element index e of a buffer (zeros when !ok) as
+// fp16 hi (+ lo for fp32 / bf16 sources); unconditional raw buffer loads.
+template <typename T>
+__device__ __forceinline__ void lora_load8(__amdgpu_buffer_rsrc_t r, uint32_t e, bool ok, f16x8& hi, f16x8& lo) {
+  if constexpr (std::is_same<T, __half>::value) {
+    hi = __builtin_bit_cast(f16x8, buf_ld16(r, ok ? e * 2u : BUF_OOB));
+    lo = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+  } else {
+    float f[8];
+    buf_ld8(r, e, ok, (const T*)nullptr, f);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const _Float16 h = (_Float16)f[q];
+      hi[q] = h;
+      lo[q] = (_Float16)(f[q] - (float)h);
+    }
+  }
+}
+
+__device__ __forceinline__ int lora_find(const LoraBatch& B, int tile, bool up) {
+  int pi = 0;
+#pragma unroll
+  for (int q = 1; q < 4; ++q)
+    if (q < B.nprob && tile >= (up ? B.p[q].tile_u0 : B.p[q].tile_d0)) pi = q;
+  return pi;
+}
+
+// grid (down tiles, ks): partial[p][z][row][n] = sum_{k in range z} x[row,k] Wd[n,k]
+template <int MT, typename TA>
+__global__ __launch_bounds__(256) void lora_down_kernel(const LoraBatch B, int rows, float* __restrict__ part) {
+  constexpr bool SPLIT = !std::is_same<TA, __half>::value;
+  __shared__ float s_red[4][16 * MT][17];
+  const int tile = blockIdx.x;
+  const int z = blockIdx.y;
+  const LoraProb& P = B.p[lora_find(B, tile, false)];
+  const int D = B.D;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.x, (uint32_t)((int64_t)rows * D * sizeof(TA)));
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(P.wd, (uint32_t)((int64_t)P.r * D * sizeof(TA)));
+  const int n0 = (tile - P.tile_d0) * 16;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l16 = lane & 15, kg = lane >> 4;
+  const int k0 = z * B.kr;
+  const int k1 = min(D, k0 + B.kr);
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // 512-input blocks, each a fully unrolled run of four 32-wide wave steps whose
+  // loads are all issued before the MFMAs (steps past the range load zeros)
+  for (int c0 = k0; c0 < k1; c0 += 512) {
+    f16x8 bh[4], bl[4], ah[4][MT], al[4][MT];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int kk = c0 + 128 * it + wave * 32 + 8 * kg;
+      const bool kok = kk < k1;  // D % 8 == 0
+      lora_load8<TA>(wr, (uint32_t)((n0 + l16) * D + kk), kok && n0 + l16 < P.r, bh[it], bl[it]);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int row = 16 * t + l16;
+        lora_load8<TA>(xr, (uint32_t)(row * D + kk), kok && row < rows, ah[it][t], al[it][t]);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        acc[t] = mfma16x16x32(ah[it][t], bh[it], acc[t]);
+        if constexpr (SPLIT) {
+          acc[t] = mfma16x16x32(ah[it][t], bl[it], acc[t]);
+          acc[t] = mfma16x16x32(al[it][t], bh[it], acc[t]);
+        }
+      }
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_red[wave][16 * t + 4 * kg + e][l16] = acc[t][e];
+  __syncthreads();
+  float* dst = part + P.part_off + (int64_t)z * rows * P.r;
+  for (int idx = tid; idx < rows * 16; idx += 256) {
+    const int row = idx >> 4, nn = idx & 15;
+    if (n0 + nn < P.r)
+      dst[(int64_t)row * P.r + n0 + nn] =
+          ((s_red[0][row][nn] + s_red[1][row][nn]) + s_red[2][row][nn]) + s_red[3][row][nn];
+  }
+}
+
+// grid (up tiles): y[row, o] = act_up(sum_k mid[row,k] Wu[o,k] + b[o]),
+// mid = round_TA(act_down(sum_z partial[z])) staged in LDS.
+template <int MT, typename TA>
+__global__ __launch_bounds__(256) void lora_up_kernel(const LoraBatch B, int rows, const float* __restrict__ part) {
+  constexpr bool SPLIT = !std::is_same<TA, __half>::value;
+  constexpr int RS = LORA_MAXR + 8;  // LDS row stride (halfs)
+  __shared__ __align__(16) _Float16 mh[16 * MT][RS];
+  __shared__ __align__(16) _Float16 ml[SPLIT ? 16 * MT : 1][SPLIT ? RS : 8];
+  __shared__ float s_red[4][16 * MT][17];
+  const int tile = blockIdx.x;
+  const LoraProb& P = B.p[lora_find(B, tile, true)];
+  const int r = P.r;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(P.wu, (uint32_t)((int64_t)B.A * r * sizeof(TA)));
+  const int o0 = (tile - P.tile_u0) * 16;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l16 = lane & 15, kg = lane >> 4;
+
+  // this wave's up-weight operands (k steps wave*32 and wave*32 + 128; rank <= 256),
+  // loaded before staging so their latency overlaps it
+  f16x8 bh[2], bl[2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int kk = wave * 32 + 128 * it + 8 * kg;
+    lora_load8<TA>(wr, (uint32_t)((o0 + l16) * r + kk), kk < r && o0 + l16 < B.A, bh[it], bl[it]);
+  }
+
+  // stage mid: fixed-order sum over the K splits, eight loads in flight at a time
+  const int zstride = rows * r;
+  const __amdgpu_buffer_rsrc_t pr = make_rsrc(part + P.part_off, (uint32_t)(B.ks * zstride * 4));
+  for (int idx = tid; idx < rows * r; idx += 256) {
+    float s = 0.f;
+    for (int z0 = 0; z0 < B.ks; z0 += 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        t[u] = buf_ldf(pr, z0 + u < B.ks ? (uint32_t)(((z0 + u) * zstride + idx) * 4) : BUF_OOB);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += t[u];  // z order; past-the-end terms are +0
+    }
+    const float v = to_f32(from_f32<TA>(lora_act(s, P.act_d)));
+    const int row = idx / r, k = idx % r;
+    const _Float16 h = (_Float16)v;
+    mh[row][k] = h;
+    if constexpr (SPLIT) ml[row][k] = (_Float16)(v - (float)h);
+  }
+  __syncthreads();
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const f16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int kk = wave * 32 + 128 * it + 8 * kg;
+    const bool kok = kk < r;  // r % 8 == 0
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int row = 16 * t + l16;  // rows past `rows` only feed discarded D rows
+      const f16x8 ah = kok ? *reinterpret_cast<const f16x8*>(&mh[row][kk]) : zero8;
+      acc[t] = mfma16x16x32(ah, bh[it], acc[t]);
+      if constexpr (SPLIT) {
+        const f16x8 al = kok ? *reinterpret_cast<const f16x8*>(&ml[row][kk]) : zero8;
+        acc[t] = mfma16x16x32(ah, bl[it], acc[t]);
+        acc[t] = mfma16x16x32(al, bh[it], acc[t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_red[wave][16 * t + 4 * kg + e][l16] = acc[t][e];
+  __syncthreads();
+  TA* y = reinterpret_cast<TA*>(P.y);
+  const TA* bias = reinterpret_cast<const TA*>(P.bu);
+  for (int idx = tid; idx < rows * 16; idx += 256) {
+    const int row = idx >> 4, nn = idx & 15;
+    const int o = o0 + nn;
+    if (o >= B.A) continue;
+    float v = ((s_red[0][row][nn] + s_red[1][row][nn]) + s_red[2][row][nn]) + s_red[3][row][nn];
+    if (bias) v += to_f32(bias[o]);
+    y[(int64_t)row * B.A + o] = from_f32<TA>(lora_act(v, P.act_u));
+  }
+}
+
+static int lora_splits(int64_t tiles, int64_t D) {
+  // aim for 256-512 down workgroups, each split covering at least 128 inputs
+  int64_t ks = 1;
+  while (tiles * ks * 2 <= 512 && D / (ks * 2) >= 128) ks *= 2;
+  return (int)ks;
+}
+
+}  // namespace rwkv7mi
+
+using namespace rwkv7mi;
+
+static int64_t lora_tiles(int64_t nprob, const int64_t* ranks) {
+  int64_t t = 0;
+  for (int64_t i = 0; i < nprob; ++i) t += (ranks[i] + 15) / 16;
+  return t;
+}
+
+extern "C" size_t rwkv7mi_lora_workspace_bytes(int64_t nprob, const int64_t* ranks, int64_t rows, int64_t D) {
+  if (nprob < 1 || nprob > 4 || !ranks || rows <= 0 || D <= 0) return 0;
+  const int64_t ks = lora_splits(lora_tiles(nprob, ranks), D);
+  int64_t sr = 0;
+  for (int64_t i = 0; i < nprob; ++i) sr += ranks[i];
+  const int64_t nr = rows < LORA_ROWS ? rows : LORA_ROWS;
+  return (size_t)(ks * nr * sr) * sizeof(float);
+}
+
+extern "C" int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs, const void* const* w_down,
+                                  const void* const* w_up, const void* const* b_up, void* const* ys,
+                                  const int64_t* ranks, const int* act_down, const int* act_up, int64_t rows,
+                                  int64_t D, int64_t A, int act_dtype, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (nprob < 1 || nprob > 4) return fail(RWKV7MI_EINVAL, "lora_multi: 1..4 problems");
+  if (!xs || !w_down || !w_up || !ys || !ranks || !act_down || !act_up)
+    return fail(RWKV7MI_EINVAL, "lora_multi: null array");
+  if (rows < 0 || D <= 0 || A <= 0 || D % 8 || D > (1 << 20) || A > (1 << 20))
+    return fail(RWKV7MI_EINVAL, "lora_multi: bad shape (D a positive multiple of 8)");
+  if (rows == 0) return RWKV7MI_OK;
+  if (!valid_dtype(act_dtype)) return fail(RWKV7MI_EINVAL, "lora_multi: bad dtype");
+  LoraBatch batch{};
+  int td = 0, tu = 0;
+  int64_t off = 0;
+  const int64_t nr_max = rows < LORA_ROWS ? rows : LORA_ROWS;
+  const int tiles_d = (int)lora_tiles(nprob, ranks);
+  const int ks = lora_splits(tiles_d, D);
+  for (int i = 0; i < nprob; ++i) {
+    if (!xs[i] || !w_down[i] || !w_up[i] || !ys[i]) return fail(RWKV7MI_EINVAL, "lora_multi: null pointer");
+    if (ranks[i] <= 0 || ranks[i] % 8 || ranks[i] > LORA_MAXR)
+      return fail(RWKV7MI_EINVAL, "lora_multi: rank must be a positive multiple of 8, at most 256");
+    if (act_down[i] < 0 || act_down[i] > 2 || act_up[i] < 0 || act_up[i] > 2)
+      return fail(RWKV7MI_EINVAL, "lora_multi: activation must be 0 none, 1 tanh or 2 sigmoid");
+    if ((reinterpret_cast<uintptr_t>(xs[i]) | reinterpret_cast<uintptr_t>(w_down[i]) |
+         reinterpret_cast<uintptr_t>(w_up[i])) & 15)
+      return fail(RWKV7MI_EINVAL, "lora_multi: x and weights must be 16-byte aligned");
+    batch.p[i] = LoraProb{xs[i], w_down[i], w_up[i], b_up ? b_up[i] : nullptr, ys[i], (int)ranks[i],
+                          act_down[i], act_up[i], td, tu, off};
+    td += (int)((ranks[i] + 15) / 16);
+    tu += (int)((A + 15) / 16);
+    off += (int64_t)ks * nr_max * ranks[i];
+  }
+  if (!workspace || workspace_bytes < (size_t)off * sizeof(float))
+    return fail(RWKV7MI_ESIZE, "lora_multi: workspace too small");
+  batch.nprob = (int)nprob;
+  batch.D = (int)D;
+  batch.A = (int)A;
+  batch.ks = ks;
+  batch.kr = (int)((D + ks - 1) / ks);
+  batch.kr = (batch.kr + 7) / 8 * 8;
+  const size_t esz = act_dtype == RWKV7MI_F32 ? 4 : 2;
+  float* part = reinterpret_cast<float*>(workspace);
+  for (int64_t r0 = 0; r0 < rows; r0 += LORA_ROWS) {
+    const int64_t nr = rows - r0 > LORA_ROWS ? LORA_ROWS : rows - r0;
+    LoraBatch bb = batch;
+    for (int i = 0; i < nprob; ++i) {
+      bb.p[i].x = reinterpret_cast<const char*>(batch.p[i].x) + r0 * D * esz;
+      bb.p[i].y = reinterpret_cast<char*>(batch.p[i].y) + r0 * A * esz;
+      // partial tiles are packed [ks][nr][r] for this chunk's row count
+      int64_t o2 = 0;
+      for (int j = 0; j < i; ++j) o2 += (int64_t)ks * nr * ranks[j];
+      bb.p[i].part_off = o2;
+    }
+    const int mt = nr <= 16 ? 1 : 2;
+    int rc = dispatch_dtype(act_dtype, [&](auto ta) {
+      using TA = decltype(ta);
+      hipStream_t s = as_stream(stream);
+#define LORA_GO(MT_)                                                                                  \
+  hipLaunchKernelGGL((lora_down_kernel<MT_, TA>), dim3(td, ks), dim3(256), 0, s, bb, (int)nr, part); \
+  hipLaunchKernelGGL((lora_up_kernel<MT_, TA>), dim3(tu), dim3(256), 0, s, bb, (int)nr, (const float*)part)
+      if (mt == 1) {
+        LORA_GO(1);
+      } else {
+        LORA_GO(2);
+      }
+#undef LORA_GO
+      return check_launch("lora_multi");
+    });
+    if (rc) return rc;
+  }
+  return RWKV7MI_OK;
+}

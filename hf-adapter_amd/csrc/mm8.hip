@@ -235,57 +235,51 @@ static Mm8Plan mm8_plan(int64_t rows, int64_t I, int64_t O) {
 // Exact restatement of quantize_mm8 (rwkv7_hf/native_quant_mm8.py:62-97) as a
 // sequence of IEEE fp32 ops; every reduction is a min/max (order-independent),
 // every division is correctly rounded, so the result is bit-exact.
-template <typename TW>
-__global__ void mm8_colreduce(const TW* __restrict__ wt, int I, int O, int phase, float* ws) {
-  // phase 0: mx = colmin(w); 1: mx = colmin(w - my); 2: rx = max(colmax(w2), 1e-8)
-  float* my = ws;
-  float* mx = ws + I;
-  float* rx = ws + I + O;
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= O) return;
-  const bool rows_first = I > O;
-  float m = phase == 2 ? -INFINITY : INFINITY;
-  for (int i = 0; i < I; ++i) {
-    float v = to_f32(wt[(int64_t)i * O + j]);
-    if (phase == 0) {
-      m = fminf(m, v);
-    } else if (phase == 1) {
-      m = fminf(m, v - my[i]);
-    } else {
-      float w2 = rows_first ? (v - my[i]) - mx[j] : (v - mx[j]) - my[i];
-      m = fmaxf(m, w2);
-    }
-  }
-  if (phase == 2) rx[j] = fmaxf(m, 1.0e-8f);
-  else mx[j] = m;
+//
+// Element (i, j) of the [I, O] matrix W = weight.T lives at i*O + j (row-major,
+// OM = false) or at j*I + i (out-major, OM = true: nn.Linear.weight itself).
+// Per-out statistics (mx, rx) reduce over i, per-in ones (my, ry) over j.
+template <typename TW, bool OM>
+__device__ __forceinline__ float mm8_w(const TW* w, int i, int j, int I, int O) {
+  return to_f32(OM ? w[(int64_t)j * I + i] : w[(int64_t)i * O + j]);
 }
 
-template <typename TW>
-__global__ __launch_bounds__(256) void mm8_rowreduce(const TW* __restrict__ wt, int I, int O,
-                                                    int phase, float* ws) {
-  // phase 0: my = rowmin(w); 1: my = rowmin(w - mx); 2: ry = max(rowmax(w2 / rx), 1e-8)
-  float* my = ws;
-  float* mx = ws + I;
-  float* rx = ws + I + O;
-  float* ry = ws + I + 2 * O;
+// One reduction term.  phase 0: min w; 1: min (w - other offset);
+// 2: max of the offset-removed value (per-in: divided by rx[j]).
+template <bool PER_OUT>
+__device__ __forceinline__ float mm8_term(float v, int i, int j, int phase, bool rows_first, const float* my,
+                                          const float* mx, const float* rx) {
+  if (phase == 0) return v;
+  if (phase == 1) return PER_OUT ? v - my[i] : v - mx[j];
+  const float w2 = rows_first ? (v - my[i]) - mx[j] : (v - mx[j]) - my[i];
+  return PER_OUT ? w2 : __fdiv_rn(w2, rx[j]);
+}
+
+template <bool PER_OUT>
+__device__ __forceinline__ void mm8_stat_store(float m, int line, int phase, float* ws, int I, int O) {
+  float* dst = PER_OUT ? (phase == 2 ? ws + I + O : ws + I) : (phase == 2 ? ws + I + 2 * O : ws);
+  dst[line] = phase == 2 ? fmaxf(m, 1.0e-8f) : m;
+}
+
+// One workgroup per line; coalesced when the line is contiguous (PER_OUT == OM).
+template <typename TW, bool OM, bool PER_OUT>
+__global__ __launch_bounds__(256) void mm8_stat_line(const TW* __restrict__ w, int I, int O, int phase, float* ws) {
+  const float* my = ws;
+  const float* mx = ws + I;
+  const float* rx = ws + I + O;
   __shared__ float red[4];
-  const int i = blockIdx.x;
+  const int line = blockIdx.x;
+  const int len = PER_OUT ? I : O;
   const bool rows_first = I > O;
   float m = phase == 2 ? -INFINITY : INFINITY;
-  for (int j = threadIdx.x; j < O; j += 256) {
-    float v = to_f32(wt[(int64_t)i * O + j]);
-    if (phase == 0) {
-      m = fminf(m, v);
-    } else if (phase == 1) {
-      m = fminf(m, v - mx[j]);
-    } else {
-      float w2 = rows_first ? (v - my[i]) - mx[j] : (v - mx[j]) - my[i];
-      m = fmaxf(m, __fdiv_rn(w2, rx[j]));
-    }
+  for (int t = threadIdx.x; t < len; t += 256) {
+    const int i = PER_OUT ? t : line, j = PER_OUT ? line : t;
+    const float v = mm8_term<PER_OUT>(mm8_w<TW, OM>(w, i, j, I, O), i, j, phase, rows_first, my, mx, rx);
+    m = phase == 2 ? fmaxf(m, v) : fminf(m, v);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    float t = __shfl_xor(m, o, 64);
+    const float t = __shfl_xor(m, o, 64);
     m = phase == 2 ? fmaxf(m, t) : fminf(m, t);
   }
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
@@ -293,12 +287,32 @@ __global__ __launch_bounds__(256) void mm8_rowreduce(const TW* __restrict__ wt, 
   if (threadIdx.x == 0) {
     float r = red[0];
     for (int q = 1; q < 4; ++q) r = phase == 2 ? fmaxf(r, red[q]) : fminf(r, red[q]);
-    if (phase == 2) ry[i] = fmaxf(r, 1.0e-8f);
-    else my[i] = r;
+    mm8_stat_store<PER_OUT>(r, line, phase, ws, I, O);
   }
 }
 
-template <typename TW>
+// One thread per line; coalesced across threads when the line is strided (PER_OUT != OM).
+template <typename TW, bool OM, bool PER_OUT>
+__global__ __launch_bounds__(256) void mm8_stat_thread(const TW* __restrict__ w, int I, int O, int phase,
+                                                       float* ws) {
+  const float* my = ws;
+  const float* mx = ws + I;
+  const float* rx = ws + I + O;
+  const int line = blockIdx.x * 256 + threadIdx.x;
+  const int nlines = PER_OUT ? O : I;
+  if (line >= nlines) return;
+  const int len = PER_OUT ? I : O;
+  const bool rows_first = I > O;
+  float m = phase == 2 ? -INFINITY : INFINITY;
+  for (int t = 0; t < len; ++t) {
+    const int i = PER_OUT ? t : line, j = PER_OUT ? line : t;
+    const float v = mm8_term<PER_OUT>(mm8_w<TW, OM>(w, i, j, I, O), i, j, phase, rows_first, my, mx, rx);
+    m = phase == 2 ? fmaxf(m, v) : fminf(m, v);
+  }
+  mm8_stat_store<PER_OUT>(m, line, phase, ws, I, O);
+}
+
+template <typename TW, bool OM>
 __global__ void mm8_quantize(const TW* __restrict__ wt, int I, int O, const float* ws,
                              uint8_t* __restrict__ wu8, TW* mx_o, TW* rx_o, TW* my_o, TW* ry_o) {
   const float* my = ws;
@@ -309,7 +323,8 @@ __global__ void mm8_quantize(const TW* __restrict__ wt, int I, int O, const floa
   const int64_t total = (int64_t)I * O;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
-    const int i = (int)(e / O), j = (int)(e % O);
+    const int i = OM ? (int)(e % I) : (int)(e / O);
+    const int j = OM ? (int)(e / I) : (int)(e % O);
     float v = to_f32(wt[e]);
     float w2 = rows_first ? (v - my[i]) - mx[j] : (v - mx[j]) - my[i];
     float w4 = __fdiv_rn(__fdiv_rn(w2, rx[j]), ry[i]);
@@ -325,6 +340,33 @@ __global__ void mm8_quantize(const TW* __restrict__ wt, int I, int O, const floa
       ry_o[i] = from_f32<TW>(ry[i] / 16.0f);
     }
   }
+}
+
+template <typename TW, bool OM, bool PER_OUT>
+static void mm8_stat(const TW* w, int I, int O, int phase, float* ws, hipStream_t s) {
+  const int nlines = PER_OUT ? O : I;
+  if (PER_OUT == OM)
+    hipLaunchKernelGGL((mm8_stat_line<TW, OM, PER_OUT>), dim3((unsigned)nlines), dim3(256), 0, s, w, I, O, phase, ws);
+  else
+    hipLaunchKernelGGL((mm8_stat_thread<TW, OM, PER_OUT>), dim3((unsigned)((nlines + 255) / 256)), dim3(256), 0, s,
+                       w, I, O, phase, ws);
+}
+
+template <typename TW, bool OM>
+static int mm8_pack_run(const TW* w, int I, int O, uint8_t* w_u8, void* mx, void* rx, void* my, void* ry,
+                        float* ws, hipStream_t s) {
+  if (I > O) {  // rows first (rwkv7_hf/native_quant_mm8.py:66-71)
+    mm8_stat<TW, OM, false>(w, I, O, 0, ws, s);
+    mm8_stat<TW, OM, true>(w, I, O, 1, ws, s);
+  } else {
+    mm8_stat<TW, OM, true>(w, I, O, 0, ws, s);
+    mm8_stat<TW, OM, false>(w, I, O, 1, ws, s);
+  }
+  mm8_stat<TW, OM, true>(w, I, O, 2, ws, s);
+  mm8_stat<TW, OM, false>(w, I, O, 2, ws, s);
+  hipLaunchKernelGGL((mm8_quantize<TW, OM>), dim3(4096), dim3(256), 0, s, w, I, O, ws, w_u8, (TW*)mx, (TW*)rx,
+                     (TW*)my, (TW*)ry);
+  return check_launch("mm8_pack");
 }
 
 }  // namespace rwkv7mi
@@ -391,30 +433,28 @@ extern "C" int rwkv7mi_mm8_matmul(const void* x, const uint8_t* w_u8, const void
   return RWKV7MI_OK;
 }
 
-extern "C" int rwkv7mi_mm8_pack(const void* weight, int64_t I, int64_t O, int w_dtype, uint8_t* w_u8,
-                                void* mx, void* rx, void* my, void* ry, float* workspace, void* stream) {
+static int mm8_pack_entry(const void* weight, int64_t I, int64_t O, int w_dtype, uint8_t* w_u8, void* mx,
+                          void* rx, void* my, void* ry, float* workspace, void* stream, bool out_major) {
   if (I <= 0 || O <= 0 || I > INT32_MAX || O > INT32_MAX) return fail(RWKV7MI_EINVAL, "mm8_pack: bad shape");
   if (!weight || !w_u8 || !mx || !rx || !my || !ry || !workspace)
     return fail(RWKV7MI_EINVAL, "mm8_pack: null pointer");
   hipStream_t s = as_stream(stream);
   return dispatch_dtype(w_dtype, [&](auto tw) {
     using TW = decltype(tw);
-    const TW* wt = (const TW*)weight;
-    const int cb = (int)((O + 255) / 256);
-    const bool rows_first = I > O;
-    if (rows_first) {
-      hipLaunchKernelGGL((mm8_rowreduce<TW>), dim3((unsigned)I), dim3(256), 0, s, wt, (int)I, (int)O, 0, workspace);
-      hipLaunchKernelGGL((mm8_colreduce<TW>), dim3(cb), dim3(256), 0, s, wt, (int)I, (int)O, 1, workspace);
-    } else {
-      hipLaunchKernelGGL((mm8_colreduce<TW>), dim3(cb), dim3(256), 0, s, wt, (int)I, (int)O, 0, workspace);
-      hipLaunchKernelGGL((mm8_rowreduce<TW>), dim3((unsigned)I), dim3(256), 0, s, wt, (int)I, (int)O, 1, workspace);
-    }
-    hipLaunchKernelGGL((mm8_colreduce<TW>), dim3(cb), dim3(256), 0, s, wt, (int)I, (int)O, 2, workspace);
-    hipLaunchKernelGGL((mm8_rowreduce<TW>), dim3((unsigned)I), dim3(256), 0, s, wt, (int)I, (int)O, 2, workspace);
-    hipLaunchKernelGGL((mm8_quantize<TW>), dim3(4096), dim3(256), 0, s, wt, (int)I, (int)O, workspace, w_u8,
-                       (TW*)mx, (TW*)rx, (TW*)my, (TW*)ry);
-    return check_launch("mm8_pack");
+    const TW* w = (const TW*)weight;
+    return out_major ? mm8_pack_run<TW, true>(w, (int)I, (int)O, w_u8, mx, rx, my, ry, workspace, s)
+                     : mm8_pack_run<TW, false>(w, (int)I, (int)O, w_u8, mx, rx, my, ry, workspace, s);
   });
+}
+
+extern "C" int rwkv7mi_mm8_pack(const void* weight, int64_t I, int64_t O, int w_dtype, uint8_t* w_u8,
+                                void* mx, void* rx, void* my, void* ry, float* workspace, void* stream) {
+  return mm8_pack_entry(weight, I, O, w_dtype, w_u8, mx, rx, my, ry, workspace, stream, false);
+}
+
+extern "C" int rwkv7mi_mm8_pack_t(const void* weight, int64_t I, int64_t O, int w_dtype, uint8_t* w_t,
+                                  void* mx, void* rx, void* my, void* ry, float* workspace, void* stream) {
+  return mm8_pack_entry(weight, I, O, w_dtype, w_t, mx, rx, my, ry, workspace, stream, true);
 }
 
 namespace rwkv7mi {

@@ -1,0 +1,445 @@
+// MM8 dequant GEMV / small-batch GEMM over OUT-MAJOR weights, for gfx950.
+//
+// Same format as mm8.hip (rwkv7_hf/native_quant_mm8.py:62-126):
+//   W_hat[i,o] = (w[i,o] + 0.5) * ry[i] * rx[o] + my[i] + mx[o]
+//   y[b,o] = rx[o] * sum_i x'[b,i] (w[i,o] + 0.5) + sum_i x[b,i] my[i] + mx[o] sum_i x[b,i],
+//   x' = x * ry,
+// but the bytes are stored out-major: wt[o * I + i] == w[i, o] (the layout of
+// nn.Linear.weight; the [in, out] tensor the reference exposes is wt.t()).
+//
+// Out-major makes the whole K range of an output column one contiguous run,
+// so a workgroup owns 16 output columns and ALL of K: no split-K partials, no
+// cross-workgroup ordering, deterministic fixed-order sums.
+//
+// Workgroup = 4 waves, 16 columns, up to 16 batch rows (one MFMA M tile).
+// K is walked in 128-row steps; wave w takes steps w, w+4, ...  In a step,
+// lane (n = l%16, kg = l/16) loads two 16-byte runs of column n, rows
+// 16kg..16kg+15 and 64+16kg..64+16kg+15 — a wave reads 16 full 128-byte lines.
+// Each 8-byte half is one B operand of v_mfma_f32_16x16x32_f16 (the MFMA's
+// logical k = 8kg+e maps to physical row 64h + 16kg + 8q + e; the A operand
+// uses the same map), converted to fp16 (w + 0.5) by v_perm + one packed add.
+// Weight loads run DEPTH steps ahead of use, across LDS re-staging barriers
+// (__syncthreads waits on LDS traffic only).  All global loads are raw buffer
+// loads whose out-of-range lanes get an offset past the descriptor's size, so
+// the loop is branch-free and the load counter waits stay exact.
+//
+// x' is staged per K-chunk in LDS as fp16 hi + lo (x' = hi + lo to ~22 bits),
+// so each product is two MFMAs with fp32 accumulation.  A rows beyond the
+// batch read a duplicate row: MFMA row m of D depends only on A row m, and
+// those D rows are never stored.  The per-row sums (sum x, sum x*my) are
+// accumulated in fixed thread order during staging.
+//
+// Up to four problems with the same (rows, I, O) run in one launch
+// (blockIdx.y), e.g. the R/K/V projections of one layer.
+#include "common.h"
+
+namespace rwkv7mi {
+
+constexpr int MM8T_COLS = 16;
+constexpr int MM8T_MAXPROB = 4;
+constexpr int MM8T_SB = 4;  // x' staging groups per load batch
+constexpr int MM8T_LDS_X = 72 * 1024;      // x' staging bytes per workgroup (2 workgroups per CU)
+constexpr int MM8T_LDS_X_ONE = 144 * 1024; // when the grid is at most one workgroup per CU
+
+struct Mm8tProb {
+  const void* x;
+  const uint8_t* w;
+  const void* mx;
+  const void* rx;
+  const void* my;
+  const void* ry;
+  const void* bias;
+  const void* residual;
+  void* y;
+  int epilogue;
+};
+
+struct Mm8tBatch {
+  Mm8tProb p[MM8T_MAXPROB];
+  int rows, I, O, KC;
+};
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer loads: an offset at or beyond the descriptor's byte count returns
+// zeros without touching memory, so every load below is unconditional.
+constexpr uint32_t MM8T_OOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t mm8t_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 mm8t_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// 8 consecutive elements of type T starting at element e, raw (zeros when
+// !valid); loads are issued here and converted later so a batch of them is in
+// flight together.
+template <typename T>
+struct Raw8 {
+  u32x4 v[sizeof(T) == 4 ? 2 : 1];
+};
+
+template <typename T>
+__device__ __forceinline__ Raw8<T> mm8t_ld8(__amdgpu_buffer_rsrc_t r, uint32_t e, bool valid) {
+  Raw8<T> o;
+  const uint32_t off = valid ? e * (uint32_t)sizeof(T) : MM8T_OOB;
+  o.v[0] = mm8t_ld16(r, off);
+  if constexpr (sizeof(T) == 4) o.v[1] = mm8t_ld16(r, valid ? off + 16u : MM8T_OOB);
+  return o;
+}
+
+__device__ __forceinline__ void mm8t_cvt8(const Raw8<float>& a, float (&o)[8]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    o[q] = __uint_as_float(a.v[0][q]);
+    o[4 + q] = __uint_as_float(a.v[1][q]);
+  }
+}
+__device__ __forceinline__ void mm8t_cvt8(const Raw8<__half>& a, float (&o)[8]) {
+  const f16x8 v = __builtin_bit_cast(f16x8, a.v[0]);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o[q] = (float)v[q];
+}
+__device__ __forceinline__ void mm8t_cvt8(const Raw8<__hip_bfloat16>& a, float (&o)[8]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    o[2 * q] = __uint_as_float(a.v[0][q] << 16);
+    o[2 * q + 1] = __uint_as_float(a.v[0][q] & 0xffff0000u);
+  }
+}
+
+// bytes of (d0, d1) = rows r..r+7 of one column -> fp16 [w + 0.5] x 8
+__device__ __forceinline__ f16x8 mm8t_b_operand(uint32_t d0, uint32_t d1) {
+  const f16x2 half_off = {(_Float16)-1023.5f, (_Float16)-1023.5f};
+  f16x2 p0 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, d0, 0x04010400u)) + half_off;
+  f16x2 p1 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, d0, 0x04030402u)) + half_off;
+  f16x2 p2 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, d1, 0x04010400u)) + half_off;
+  f16x2 p3 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, d1, 0x04030402u)) + half_off;
+  return (f16x8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+template <typename TA, typename TM, int DEPTH>
+__global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
+  const Mm8tProb& P = B.p[blockIdx.y];
+  const int I = B.I, O = B.O, KC = B.KC;
+  const int row0 = blockIdx.z * 16;
+  const int nrows = min(16, B.rows - row0);
+  const int col0 = blockIdx.x * MM8T_COLS;
+  const int XS = KC + 8;  // LDS row stride (halfs)
+  extern __shared__ __align__(16) char smem[];
+  _Float16* xh = reinterpret_cast<_Float16*>(smem);
+  _Float16* xl = xh + nrows * XS;
+  __shared__ float red[4][16][17];
+  __shared__ float wsum[4][2];
+  __shared__ float rsum[16][2];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar step logic
+  const int lane = tid & 63;
+  const int n = lane & 15;
+  const int kg = lane >> 4;
+
+  // this workgroup's 16 columns are one contiguous run of ncols * I bytes
+  const int ncols = min(MM8T_COLS, O - col0);
+  const __amdgpu_buffer_rsrc_t wr = mm8t_rsrc(P.w + (int64_t)col0 * I, (uint32_t)ncols * (uint32_t)I);
+  const __amdgpu_buffer_rsrc_t xr =
+      mm8t_rsrc(reinterpret_cast<const TA*>(P.x) + (int64_t)row0 * I, (uint32_t)(nrows * I * sizeof(TA)));
+  const __amdgpu_buffer_rsrc_t ryr = mm8t_rsrc(P.ry, (uint32_t)(I * sizeof(TM)));
+  const __amdgpu_buffer_rsrc_t myr = mm8t_rsrc(P.my, (uint32_t)(I * sizeof(TM)));
+  const uint32_t lane_off = (uint32_t)n * (uint32_t)I + 16u * kg;
+
+  const int CSW = KC >> 9;  // steps per wave per chunk (a multiple of DEPTH)
+  const int nchunks = (I + KC - 1) / KC;
+
+  // staging: TPR threads per batch row, fixed for the whole kernel
+  int rp2 = 1;
+  while (rp2 < nrows) rp2 <<= 1;
+  const int TPR = 256 / rp2;
+  const int sr = tid / TPR;
+  const int su = tid % TPR;
+  const int NQ = KC >> 3;                  // 8-element groups per chunk row
+  const int QIT = (NQ + TPR - 1) / TPR;    // uniform trip count
+  float sx = 0.f, sxmy = 0.f;
+
+  // Step j of this wave covers K rows 128 (wave + 4j) .. +127.  Segments at or
+  // beyond I (the tail step, prefetches past the end) read as zeros.
+  u32x4 buf[DEPTH][2];
+  auto load_step = [&](int j, u32x4 (&b)[2]) {
+    const int k = 128 * (wave + 4 * j) + 16 * kg;
+    const uint32_t off = lane_off + 128u * (uint32_t)(wave + 4 * j);
+    b[0] = mm8t_ld16(wr, k < I ? off : MM8T_OOB);
+    b[1] = mm8t_ld16(wr, k + 64 < I ? off + 64u : MM8T_OOB);
+  };
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) load_step(d, buf[d]);
+
+  const int arow = n < nrows ? n : nrows - 1;
+  const _Float16* ah = xh + arow * XS + 16 * kg;
+  const _Float16* al = xl + arow * XS + 16 * kg;
+  f32x4 acc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc[q] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  for (int c = 0; c < nchunks; ++c) {
+    // ---- stage chunk c of x' into LDS (rows past I stage as zeros), in
+    // batches of MM8T_SB groups whose loads are all in flight together
+    const int kc0 = c * KC;
+    __syncthreads();
+    for (int it0 = 0; it0 < QIT; it0 += MM8T_SB) {
+      Raw8<TA> rxv[MM8T_SB];
+      Raw8<TM> rrv[MM8T_SB], rmv[MM8T_SB];
+#pragma unroll
+      for (int u = 0; u < MM8T_SB; ++u) {
+        const int q = su + (it0 + u) * TPR;
+        const int k = kc0 + 8 * q;
+        const bool valid = sr < nrows && q < NQ && k < I;
+        rxv[u] = mm8t_ld8<TA>(xr, (uint32_t)(sr * I + k), valid);
+        rrv[u] = mm8t_ld8<TM>(ryr, (uint32_t)k, valid);
+        rmv[u] = mm8t_ld8<TM>(myr, (uint32_t)k, valid);
+      }
+#pragma unroll
+      for (int u = 0; u < MM8T_SB; ++u) {
+        const int q = su + (it0 + u) * TPR;
+        float xv[8], rv[8], mv[8];
+        mm8t_cvt8(rxv[u], xv);
+        mm8t_cvt8(rrv[u], rv);
+        mm8t_cvt8(rmv[u], mv);
+        f16x8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float xp = xv[e] * rv[e];
+          const _Float16 h = (_Float16)xp;
+          hi[e] = h;
+          lo[e] = (_Float16)(xp - (float)h);
+          sx += xv[e];
+          sxmy += xv[e] * mv[e];
+        }
+        if (sr < nrows && q < NQ) {
+          *reinterpret_cast<f16x8*>(xh + sr * XS + 8 * q) = hi;
+          *reinterpret_cast<f16x8*>(xl + sr * XS + 8 * q) = lo;
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- this wave's steps of the chunk; the load ring runs DEPTH steps ahead
+    for (int jb = 0; jb < CSW; jb += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int jl = jb + d;
+        // convert this step's bytes first, then refill the same ring slot: the
+        // slot is dead once converted, so it keeps its registers across the loop
+        f16x8 bv[4];
+        bv[0] = mm8t_b_operand(buf[d][0][0], buf[d][0][1]);
+        bv[1] = mm8t_b_operand(buf[d][0][2], buf[d][0][3]);
+        bv[2] = mm8t_b_operand(buf[d][1][0], buf[d][1][1]);
+        bv[3] = mm8t_b_operand(buf[d][1][2], buf[d][1][3]);
+        load_step(c * CSW + jl + DEPTH, buf[d]);
+        const int kl = 128 * (wave + 4 * jl);
+#pragma unroll
+        for (int hq = 0; hq < 4; ++hq) {
+          const int off = kl + 64 * (hq >> 1) + 8 * (hq & 1);
+          const f16x8 a_hi = *reinterpret_cast<const f16x8*>(ah + off);
+          const f16x8 a_lo = *reinterpret_cast<const f16x8*>(al + off);
+          acc[hq] = mfma16x16x32(a_hi, bv[hq], acc[hq]);
+          acc[hq] = mfma16x16x32(a_lo, bv[hq], acc[hq]);
+        }
+      }
+    }
+  }
+  const f32x4 accs = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+
+  // ---- per-row sums: fixed-order butterfly inside each row's lanes, then waves
+  const int width = TPR < 64 ? TPR : 64;
+  for (int o = width >> 1; o > 0; o >>= 1) {
+    sx += __shfl_xor(sx, o, 64);
+    sxmy += __shfl_xor(sxmy, o, 64);
+  }
+  if (TPR >= 64) {
+    if (lane == 0) {
+      wsum[wave][0] = sx;
+      wsum[wave][1] = sxmy;
+    }
+  }
+  // ---- wave partial tiles: lane holds col n, rows 4kg + e
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red[wave][4 * kg + e][n] = accs[e];
+  __syncthreads();
+  if (TPR >= 64) {
+    if (tid < nrows) {
+      const int wpr = TPR >> 6;  // waves per row
+      float a = 0.f, b = 0.f;
+      for (int q = 0; q < wpr; ++q) {
+        a += wsum[tid * wpr + q][0];
+        b += wsum[tid * wpr + q][1];
+      }
+      rsum[tid][0] = a;
+      rsum[tid][1] = b;
+    }
+  } else if (su == 0 && sr < nrows) {
+    rsum[sr][0] = sx;
+    rsum[sr][1] = sxmy;
+  }
+  __syncthreads();
+
+  // ---- epilogue: one thread per (row, column)
+  if (tid < nrows * MM8T_COLS) {
+    const int m = tid >> 4;
+    const int cn = tid & 15;
+    const int o = col0 + cn;
+    if (o < O) {
+      const float s = ((red[0][m][cn] + red[1][m][cn]) + red[2][m][cn]) + red[3][m][cn];
+      float v = ld(reinterpret_cast<const TM*>(P.rx), o) * s + rsum[m][1] +
+                ld(reinterpret_cast<const TM*>(P.mx), o) * rsum[m][0];
+      if (P.bias) v += ld(reinterpret_cast<const TM*>(P.bias), o);
+      const int64_t oi = (int64_t)(row0 + m) * O + o;
+      if (P.epilogue == RWKV7MI_EPI_RELU2) {
+        v = fmaxf(v, 0.f);
+        v = v * v;
+      } else if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
+        v += ld(reinterpret_cast<const TA*>(P.residual), oi);
+      }
+      reinterpret_cast<TA*>(P.y)[oi] = from_f32<TA>(v);
+    }
+  }
+}
+
+// x' staging chunk: the largest power-of-two multiple of 1024 rows whose
+// hi/lo copy for the tile's rows fits the LDS budget, and no longer than I
+// needs.  A grid of at most one workgroup per CU, or a tile of more than four
+// rows (whose staging would otherwise repeat per chunk), uses most of the CU's
+// LDS; the DEPTH-step weight ring keeps 64 KB per CU in flight even then.
+static int mm8t_chunk(int64_t rows, int64_t I, int64_t nwg) {
+  const int64_t nr = rows < 16 ? rows : 16;
+  const int64_t budget = (nwg <= 256 || nr > 4) ? MM8T_LDS_X_ONE : MM8T_LDS_X;
+  int64_t kc = 1024;
+  while (kc < I && nr * (2 * kc + 8) * 4 <= budget) kc *= 2;
+  return (int)kc;
+}
+
+static size_t mm8t_lds(int64_t rows, int KC) {
+  const int64_t nr = rows < 16 ? rows : 16;
+  return (size_t)nr * (KC + 8) * 4;
+}
+
+}  // namespace rwkv7mi
+
+using namespace rwkv7mi;
+
+template <typename TA, typename TM, int DEPTH>
+static int mm8t_go(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
+  static bool lds_raised = false;  // dynamic LDS above 64 KB must be enabled once per instance
+  if (!lds_raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, DEPTH>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, MM8T_LDS_X_ONE + 1024) != hipSuccess)
+      return fail(RWKV7MI_ELAUNCH, "mm8t_kernel: cannot raise the dynamic LDS limit");
+    lds_raised = true;
+  }
+  hipLaunchKernelGGL((mm8t_kernel<TA, TM, DEPTH>), grid, dim3(256), lds, as_stream(stream), b);
+  return check_launch("mm8t_kernel");
+}
+
+static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I, int64_t O, int act_dtype,
+                       int meta_dtype, void* stream, const char* who) {
+  const std::string w(who);
+  if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
+  if (rows < 0 || I <= 0 || O <= 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
+  if (rows == 0) return RWKV7MI_OK;
+  if (I % 16) return fail(RWKV7MI_EINVAL, w + ": in_features must be a multiple of 16");
+  // buffer descriptors cover 16 columns x I bytes and 16 rows x I activations
+  if (I > (1 << 24) || O > INT32_MAX || rows > 65535 * 16) return fail(RWKV7MI_EINVAL, w + ": too large");
+  if (!valid_dtype(act_dtype) || !valid_dtype(meta_dtype)) return fail(RWKV7MI_EINVAL, w + ": bad dtype");
+  for (int p = 0; p < nprob; ++p) {
+    const Mm8tProb& q = probs[p];
+    if (!q.x || !q.w || !q.mx || !q.rx || !q.my || !q.ry || !q.y) return fail(RWKV7MI_EINVAL, w + ": null pointer");
+    if ((reinterpret_cast<uintptr_t>(q.x) | reinterpret_cast<uintptr_t>(q.w) | reinterpret_cast<uintptr_t>(q.my) |
+         reinterpret_cast<uintptr_t>(q.ry)) & 15)
+      return fail(RWKV7MI_EINVAL, w + ": x, w_t, my and ry must be 16-byte aligned");
+    if (q.epilogue < 0 || q.epilogue > 2) return fail(RWKV7MI_EINVAL, w + ": bad epilogue");
+    if (q.epilogue == RWKV7MI_EPI_RESIDUAL && !q.residual) return fail(RWKV7MI_EINVAL, w + ": residual missing");
+  }
+  Mm8tBatch b{};
+  for (int p = 0; p < nprob; ++p) b.p[p] = probs[p];
+  b.rows = (int)rows;
+  b.I = (int)I;
+  b.O = (int)O;
+  dim3 grid((unsigned)((O + MM8T_COLS - 1) / MM8T_COLS), (unsigned)nprob, (unsigned)((rows + 15) / 16));
+  b.KC = mm8t_chunk(rows, I, (int64_t)grid.x * grid.y * grid.z);
+  const size_t lds = mm8t_lds(rows, b.KC);
+  return dispatch_dtype(act_dtype, [&](auto ta) {
+    using TA = decltype(ta);
+    return dispatch_dtype(meta_dtype, [&](auto tm) {
+      using TM = decltype(tm);
+      const int csw = b.KC >> 9;
+      if (csw >= 8) return mm8t_go<TA, TM, 8>(grid, lds, stream, b);
+      if (csw >= 4) return mm8t_go<TA, TM, 4>(grid, lds, stream, b);
+      return mm8t_go<TA, TM, 2>(grid, lds, stream, b);
+    });
+  });
+}
+
+extern "C" int rwkv7mi_mm8t_matmul(const void* x, const uint8_t* w_t, const void* mx, const void* rx,
+                                   const void* my, const void* ry, const void* bias, const void* residual,
+                                   void* y, int64_t rows, int64_t I, int64_t O, int epilogue, int act_dtype,
+                                   int meta_dtype, void* stream) {
+  Mm8tProb p{x, w_t, mx, rx, my, ry, bias, residual, y, epilogue};
+  return mm8t_launch(1, &p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul");
+}
+
+extern "C" int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x, const uint8_t* const* w_t,
+                                         const void* const* mx, const void* const* rx, const void* const* my,
+                                         const void* const* ry, const void* const* bias,
+                                         const void* const* residual, void* const* y, const int* epilogue,
+                                         int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype,
+                                         void* stream) {
+  if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, "mm8t_matmul_multi: 1..4 problems per launch");
+  if (!x || !w_t || !mx || !rx || !my || !ry || !y || !epilogue)
+    return fail(RWKV7MI_EINVAL, "mm8t_matmul_multi: null array");
+  Mm8tProb p[MM8T_MAXPROB];
+  for (int i = 0; i < nprob; ++i)
+    p[i] = Mm8tProb{x[i], w_t[i], mx[i], rx[i], my[i], ry[i], bias ? bias[i] : nullptr,
+                    residual ? residual[i] : nullptr, y[i], epilogue[i]};
+  return mm8t_launch(nprob, p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul_multi");
+}
+
+namespace rwkv7mi {
+// out[o, i] = (wt[o, i] + 0.5) * ry[i] * rx[o] + my[i] + mx[o], fp32 math, one rounding
+// (the same expression as mm8_dequant_kernel, transposed storage).
+template <typename TM, typename TO>
+__global__ __launch_bounds__(256) void mm8t_dequant_kernel(const uint8_t* __restrict__ w, const TM* __restrict__ mx,
+                                                           const TM* __restrict__ rx, const TM* __restrict__ my,
+                                                           const TM* __restrict__ ry, TO* __restrict__ out, int I,
+                                                           int O) {
+  for (int o = blockIdx.y; o < O; o += gridDim.y) {
+    const float rxo = to_f32(rx[o]), mxo = to_f32(mx[o]);
+    for (int i = (blockIdx.x * 256 + threadIdx.x) * 4; i < I; i += gridDim.x * 256 * 4) {
+      const uint32_t q = *reinterpret_cast<const uint32_t*>(w + (int64_t)o * I + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float wq = (float)((q >> (8 * e)) & 0xffu) + 0.5f;
+        out[(int64_t)o * I + i + e] = from_f32<TO>(wq * to_f32(ry[i + e]) * rxo + to_f32(my[i + e]) + mxo);
+      }
+    }
+  }
+}
+}  // namespace rwkv7mi
+
+extern "C" int rwkv7mi_mm8t_dequant(const uint8_t* w_t, const void* mx, const void* rx, const void* my,
+                                    const void* ry, void* out, int64_t I, int64_t O, int meta_dtype, int out_dtype,
+                                    void* stream) {
+  if (I <= 0 || O <= 0 || I % 4 || I > INT32_MAX || O > INT32_MAX) return fail(RWKV7MI_EINVAL, "mm8t_dequant: bad shape");
+  if (!w_t || !mx || !rx || !my || !ry || !out) return fail(RWKV7MI_EINVAL, "mm8t_dequant: null pointer");
+  if (reinterpret_cast<uintptr_t>(w_t) & 3) return fail(RWKV7MI_EINVAL, "mm8t_dequant: w_t must be 4-byte aligned");
+  return dispatch_dtype(meta_dtype, [&](auto tm) {
+    using TM = decltype(tm);
+    return dispatch_dtype(out_dtype, [&](auto to) {
+      using TO = decltype(to);
+      const int gx = (int)std::min<int64_t>((I / 4 + 255) / 256, 64);
+      hipLaunchKernelGGL((mm8t_dequant_kernel<TM, TO>), dim3(gx, (unsigned)std::min<int64_t>(O, 32768)), dim3(256), 0, as_stream(stream),
+                         w_t, (const TM*)mx, (const TM*)rx, (const TM*)my, (const TM*)ry, (TO*)out, (int)I, (int)O);
+      return check_launch("mm8t_dequant_kernel");
+    });
+  });
+}

@@ -36,6 +36,28 @@ __global__ __launch_bounds__(256) void wkv7_decode_kernel(
   const int tid = threadIdx.x;
   const int64_t vec = (int64_t)bh * HEAD;
 
+  // Issue the state rows (the bulk of the bytes) and the per-row output
+  // parameters first, so they are in flight while the vectors are staged.
+  const int i = tid >> 2;
+  const int j0 = (tid & 3) * 16;
+  const int64_t soff = ((int64_t)bh * HEAD + i) * HEAD + j0;
+  float s[16];
+  {
+    const float4* src = reinterpret_cast<const float4*>(state_in + soff);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float4 t4 = src[q];
+      s[4 * q + 0] = t4.x; s[4 * q + 1] = t4.y; s[4 * q + 2] = t4.z; s[4 * q + 3] = t4.w;
+    }
+  }
+  float g_i = 0.f, gnw_i = 0.f, gnb_i = 0.f;
+  if constexpr (MODE != MODE_UPDATE) {
+    const int64_t pi = (int64_t)h * HEAD + i;
+    g_i = ld(g, vec + i);
+    gnw_i = ld(gn_w, pi);
+    gnb_i = ld(gn_b, pi);
+  }
+
   if (tid < HEAD) {
     const int c = tid;
     float rv = ld(r, vec + c);
@@ -78,18 +100,6 @@ __global__ __launch_bounds__(256) void wkv7_decode_kernel(
   }
   __syncthreads();
 
-  const int i = tid >> 2;
-  const int j0 = (tid & 3) * 16;
-  const int64_t soff = ((int64_t)bh * HEAD + i) * HEAD + j0;
-  float s[16];
-  {
-    const float4* src = reinterpret_cast<const float4*>(state_in + soff);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float4 t4 = src[q];
-      s[4 * q + 0] = t4.x; s[4 * q + 1] = t4.y; s[4 * q + 2] = t4.z; s[4 * q + 3] = t4.w;
-    }
-  }
   float dot = 0.f;
 #pragma unroll
   for (int j = 0; j < 16; ++j) dot += s[j] * s_kk[j0 + j];
@@ -124,9 +134,8 @@ __global__ __launch_bounds__(256) void wkv7_decode_kernel(
     __syncthreads();
     const float var = (s_red[4] + s_red[5] + s_red[6] + s_red[7]) * (1.0f / HEAD);
     if ((tid & 3) == 0) {
-      const int64_t pi = (int64_t)h * HEAD + i;
       float normed = cen * rsqrtf(var + eps);
-      float o = (normed * ld(gn_w, pi) + ld(gn_b, pi) + s_corr * vi) * ld(g, vec + i);
+      float o = (normed * gnw_i + gnb_i + s_corr * vi) * g_i;
       out[vec + i] = from_f32<TA>(o);
     }
   }

@@ -1,16 +1,19 @@
 """W/A/G/V LoRA projections with the reference's API.
 
 Mirrors ``fused_wavg_lora`` (rwkv7_hf/fused_lora.py:706) and ``fused_wag_lora``
-(:559): two grouped launches of the gfx950 dense MFMA kernel — the four down
-projections (tanh for W, sigmoid for G fused) and the four up projections
-(bias, and the V-gate sigmoid fused).  Returns ``(w, a_pre, g, v_gate)``;
+(:559): two grouped launches of the gfx950 LoRA kernels — the four down
+projections split over K (tanh for W, sigmoid for G applied when the partials
+are reduced) and the four up projections (bias, and the V-gate sigmoid fused).  Returns ``(w, a_pre, g, v_gate)``;
 the caller applies the outer sigmoid to ``a_pre`` as in the reference.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
+from . import workspace as _ws
 
 ACT_NONE, ACT_TANH, ACT_SIGMOID, ACT_RELU2 = 0, 1, 2, 3
 
@@ -21,12 +24,37 @@ def dense_multi(problems, rows: int):
     Ws = [p[1] for p in problems]
     bs = [p[2] for p in problems]
     ys = [p[3] for p in problems]
-    Ns = (ctypes_i64 := __import__("ctypes").c_int64 * len(problems))(*[int(p[1].shape[0]) for p in problems])
-    Ks = (__import__("ctypes").c_int64 * len(problems))(*[int(p[1].shape[1]) for p in problems])
-    acts = (__import__("ctypes").c_int * len(problems))(*[int(p[4]) for p in problems])
+    k = len(problems)
+    Ns = (ctypes.c_int64 * k)(*[int(p[1].shape[0]) for p in problems])
+    Ks = (ctypes.c_int64 * k)(*[int(p[1].shape[1]) for p in problems])
+    acts = (ctypes.c_int * k)(*[int(p[4]) for p in problems])
     _lib.require_gpu(*xs, *Ws, *ys, name="dense_multi")
     _lib.call("rwkv7mi_dense_multi", _lib.ptr_array(xs), _lib.ptr_array(Ws), _lib.ptr_array(bs), _lib.ptr_array(ys),
               Ns, Ks, acts, len(problems), int(rows), _lib.dtype_code(xs[0]), _lib.stream_of(xs[0]))
+
+
+def lora_workspace_bytes(ranks, rows: int, D: int) -> int:
+    arr = (ctypes.c_int64 * len(ranks))(*[int(r) for r in ranks])
+    return int(_lib.load().rwkv7mi_lora_workspace_bytes(len(ranks), arr, int(rows), int(D)))
+
+
+def lora_multi(xs, downs, ups, biases, outs, acts_down, acts_up):
+    """Grouped LoRA: ``outs[i] = act_up(act_down(xs[i] @ downs[i].T) @ ups[i].T + biases[i])``.
+
+    Two launches for up to four projections (split-K down kernel, up kernel that
+    reduces the partials); the fp32 partials live in the per-device workspace.
+    """
+    k = len(xs)
+    rows, D = (int(s) for s in xs[0].shape)
+    A = int(ups[0].shape[0])
+    ranks = [int(d.shape[0]) for d in downs]
+    _lib.require_gpu(*xs, *downs, *ups, *outs, name="lora_multi")
+    ws = _ws.reserve(xs[0].device, lora_workspace_bytes(ranks, rows, D), slot="lora")
+    _lib.call("rwkv7mi_lora_multi", k, _lib.ptr_array(xs), _lib.ptr_array(downs), _lib.ptr_array(ups),
+              _lib.ptr_array(biases), _lib.ptr_array(outs), (ctypes.c_int64 * k)(*ranks),
+              (ctypes.c_int * k)(*[int(a) for a in acts_down]), (ctypes.c_int * k)(*[int(a) for a in acts_up]),
+              rows, D, A, _lib.dtype_code(xs[0]), _lib.ptr(ws), int(ws.numel()), _lib.stream_of(xs[0]))
+    return outs
 
 
 def _flat(x, name):
@@ -64,15 +92,10 @@ def fused_wavg_lora(xw, xa, xg, xv, w_down_weight, a_down_weight, g_down_weight,
         if int(d.shape[1]) != D or int(u.shape[1]) != int(d.shape[0]) or int(u.shape[0]) != out_dim:
             raise ValueError("LoRA weights do not match: down [R, D], up [out, R]")
     dev = xs[0].device
-    if mids is None:
-        mids = [torch.empty((rows, int(d.shape[0])), device=dev, dtype=dt) for d in downs]
     if outs is None:
         outs = [torch.empty((rows, out_dim), device=dev, dtype=dt) for _ in range(4)]
-    dense_multi([(xs[0], downs[0], None, mids[0], ACT_TANH), (xs[1], downs[1], None, mids[1], ACT_NONE),
-                 (xs[2], downs[2], None, mids[2], ACT_SIGMOID), (xs[3], downs[3], None, mids[3], ACT_NONE)], rows)
-    dense_multi([(mids[0], ups[0], biases[0], outs[0], ACT_NONE), (mids[1], ups[1], biases[1], outs[1], ACT_NONE),
-                 (mids[2], ups[2], biases[2], outs[2], ACT_NONE), (mids[3], ups[3], biases[3], outs[3], ACT_SIGMOID)],
-                rows)
+    lora_multi(xs, downs, ups, biases, outs, [ACT_TANH, ACT_NONE, ACT_SIGMOID, ACT_NONE],
+               [ACT_NONE, ACT_NONE, ACT_NONE, ACT_SIGMOID])
     if had_seq:
         return tuple(o.reshape(int(xw.shape[0]), int(xw.shape[1]), out_dim) for o in outs)
     return tuple(outs)
@@ -89,14 +112,14 @@ def fused_wag_lora(xw, xa, xg, w_down_weight, a_down_weight, g_down_weight, w_up
     biases = [None if b is None else _lin(b, dt) for b in (w_up_bias, a_up_bias, g_up_bias)]
     out_dim = int(ups[0].shape[0])
     dev = x2s[0].device
-    mids = [torch.empty((rows, int(d.shape[0])), device=dev, dtype=dt) for d in downs]
+    for d, u in zip(downs, ups):
+        if int(d.shape[1]) != int(x2s[0].shape[1]) or int(u.shape[1]) != int(d.shape[0]) or int(u.shape[0]) != out_dim:
+            raise ValueError("LoRA weights do not match: down [R, D], up [out, R]")
     outs = [torch.empty((rows, out_dim), device=dev, dtype=dt) for _ in range(3)]
-    dense_multi([(x2s[0], downs[0], None, mids[0], ACT_TANH), (x2s[1], downs[1], None, mids[1], ACT_NONE),
-                 (x2s[2], downs[2], None, mids[2], ACT_SIGMOID)], rows)
-    dense_multi([(mids[i], ups[i], biases[i], outs[i], ACT_NONE) for i in range(3)], rows)
+    lora_multi(x2s, downs, ups, biases, outs, [ACT_TANH, ACT_NONE, ACT_SIGMOID], [ACT_NONE] * 3)
     if xw.dim() == 3:
         return tuple(o.reshape(int(xw.shape[0]), int(xw.shape[1]), out_dim) for o in outs)
     return tuple(outs)
 
 
-__all__ = ["fused_wavg_lora", "fused_wag_lora", "dense_multi"]
+__all__ = ["fused_wavg_lora", "fused_wag_lora", "dense_multi", "lora_multi", "lora_workspace_bytes"]

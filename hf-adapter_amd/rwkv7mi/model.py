@@ -11,7 +11,7 @@ the per-layer decode body of ``_block_ip_batched``
 (rwkv7_hf/native_jit_prefill.py:223-1057) and the graph-captured decode
 runner (rwkv7_hf/native_graph_runtime.py:212-711, ``torch.cuda.graph`` =
 hipGraph on ROCm).  Every operator is a HIP kernel from librwkv7mi.so except
-the embedding row gather and, for prefills with more than 256 rows, the dense
+the embedding row gather and, for prefills with more than 64 rows, the dense
 library GEMM that follows an MM8 dequantisation (rocBLAS through torch).
 """
 from __future__ import annotations
@@ -24,12 +24,12 @@ import torch
 from . import _lib
 from . import workspace as _ws
 from .fused_decode_norm_mix import fused_attn_norm_mix6_decode, fused_ffn_add_norm_mix_decode, layer_norm
-from .fused_lora import ACT_NONE, ACT_SIGMOID, ACT_TANH, dense_multi
+from .fused_lora import ACT_NONE, ACT_SIGMOID, ACT_TANH, dense_multi, lora_multi, lora_workspace_bytes
 from .fused_output import fused_attn_output_prepare
 from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
-from .native_quant_mm8 import MM8Linear
+from .native_quant_mm8 import MM8Linear, is_out_major, mm8_matmul_multi_into
 from .native_quant_policy import should_quantize_linear
 from .self_chunk_rwkv7 import _run_chunk
 
@@ -176,8 +176,10 @@ class DenseLinear:
 
 
 class QuantLinear:
-    """MM8 Linear (HIP fused dequant GEMV) with a dequantise + library GEMM route
-    for prefills of more than 256 rows."""
+    """MM8 Linear: the fused out-major dequant GEMV/GEMM for up to ``GEMV_ROWS``
+    rows, and a dequantise + library GEMM route for longer prefills."""
+
+    GEMV_ROWS = 64
 
     def __init__(self, mm8: MM8Linear):
         self.m = mm8
@@ -185,13 +187,22 @@ class QuantLinear:
 
     def apply(self, x2, out, *, act=ACT_NONE, residual=None):
         rows = int(x2.shape[0])
-        if rows > 256:
+        if rows > self.GEMV_ROWS:
             m = self.m
-            W = torch.empty((m.in_features, m.out_features), device=x2.device, dtype=x2.dtype)
-            _lib.call("rwkv7mi_mm8_dequant", _lib.ptr(m.w_u8), _lib.ptr(m.mx), _lib.ptr(m.rx), _lib.ptr(m.my),
-                      _lib.ptr(m.ry), _lib.ptr(W), m.in_features, m.out_features, _lib.dtype_code(m.mx),
-                      _lib.dtype_code(W), _lib.stream_of(x2))
-            y = x2 @ W
+            if is_out_major(m.w_u8):
+                W = torch.empty((m.out_features, m.in_features), device=x2.device, dtype=x2.dtype)
+                _lib.call("rwkv7mi_mm8t_dequant", _lib.ptr(m.w_u8), _lib.ptr(m.mx), _lib.ptr(m.rx), _lib.ptr(m.my),
+                          _lib.ptr(m.ry), _lib.ptr(W), m.in_features, m.out_features, _lib.dtype_code(m.mx),
+                          _lib.dtype_code(W), _lib.stream_of(x2))
+                y = torch.nn.functional.linear(x2, W)
+            else:
+                W = torch.empty((m.in_features, m.out_features), device=x2.device, dtype=x2.dtype)
+                _lib.call("rwkv7mi_mm8_dequant", _lib.ptr(m.w_u8), _lib.ptr(m.mx), _lib.ptr(m.rx), _lib.ptr(m.my),
+                          _lib.ptr(m.ry), _lib.ptr(W), m.in_features, m.out_features, _lib.dtype_code(m.mx),
+                          _lib.dtype_code(W), _lib.stream_of(x2))
+                y = x2 @ W
+            if m.bias is not None:
+                y = y + m.bias
             if act == 3:
                 y = torch.relu(y).square()
             if residual is not None:
@@ -200,6 +211,20 @@ class QuantLinear:
             return out
         epi = _lib.EPI_RELU2 if act == 3 else (_lib.EPI_RESIDUAL if residual is not None else _lib.EPI_NONE)
         return self.m._run(x2, out=out, residual=residual, epilogue=epi)
+
+    @staticmethod
+    def apply_group(lins, xs, outs):
+        """The same as ``[l.apply(x, o) for ...]``; out-major MM8 modules of one
+        shape run as one launch."""
+        rows = int(xs[0].shape[0])
+        if (all(isinstance(l, QuantLinear) for l in lins) and rows <= QuantLinear.GEMV_ROWS
+                and len({(l.in_features, l.out_features) for l in lins}) == 1
+                and all(is_out_major(l.m.w_u8) for l in lins)):
+            mm8_matmul_multi_into(list(xs), [l.m for l in lins], list(outs))
+            return outs
+        for l, x2, o in zip(lins, xs, outs):
+            l.apply(x2, o)
+        return outs
 
 
 # ------------------------------------------------------------------ cache
@@ -370,12 +395,16 @@ class NativeRWKV7ForCausalLM:
         return NativeRWKV7Cache.zeros(self.config, batch, self.device, self.dtype)
 
     def reserve_workspace(self, rows: int) -> None:
+        """Grow the per-device scratch slots for ``rows``-row decode steps (before capture)."""
         need = 0
         for lin in self._linears():
             if isinstance(lin, QuantLinear):
                 need = max(need, lin.m.rwkv7_workspace_bytes(min(rows, 64)))
         if need:
             _ws.reserve(self.device, need)
+        cfg = self.config
+        ranks = [cfg.decay_low_rank_dim, cfg.a_low_rank_dim, cfg.gate_low_rank_dim, cfg.v_low_rank_dim]
+        _ws.reserve(self.device, lora_workspace_bytes(ranks, rows, cfg.hidden_size), slot="lora")
 
     def _linears(self):
         for L in self.layers:
@@ -383,7 +412,7 @@ class NativeRWKV7ForCausalLM:
         yield self.lm_head
 
     def _lora(self, L, xw, xa, xg, xv, rows, outs, mids):
-        """W, A (sigmoid applied), G, V-gate projections on the dense HIP kernel."""
+        """W, A (sigmoid applied), G, V-gate projections on the LoRA HIP kernels."""
         n = len(L.lora_down)
         xin = [xw, xa, xg, xv][:n]
         acts_down = [ACT_TANH, ACT_NONE, ACT_SIGMOID, ACT_NONE][:n]
@@ -400,8 +429,7 @@ class NativeRWKV7ForCausalLM:
                     y = torch.sigmoid(y)
                 outs[q].copy_(y)
             return
-        dense_multi([(xin[q], L.lora_down[q], None, mids[q], acts_down[q]) for q in range(n)], rows)
-        dense_multi([(mids[q], L.lora_up[q], L.lora_bias[q], outs[q], acts_up[q]) for q in range(n)], rows)
+        lora_multi(xin, L.lora_down, L.lora_up, L.lora_bias, outs[:n], acts_down, acts_up)
 
     # ------------------------------------------------------------- decode
     def _decode_buffers(self, B):
@@ -442,9 +470,7 @@ class NativeRWKV7ForCausalLM:
                                         pre_norm_weight=L.pre[0] if L.pre else None,
                                         pre_norm_bias=L.pre[1] if L.pre else None)
             xr, xw, xk, xv, xa, xg = (mixb[q] for q in range(6))
-            L.r_proj.apply(xr, rkv[0])
-            L.k_proj.apply(xk, rkv[1])
-            L.v_proj.apply(xv, rkv[2])
+            QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
             self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
             fused_recurrent_output_prepare_raw(
                 rkv[0], lora[0], rkv[1], rkv[2], lora[1], state[i], lora[2], L.k_k, L.k_a, L.r_k, L.gn[0],

@@ -10,6 +10,8 @@ tensors: there is no CPU path.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -42,32 +44,113 @@ def quantize_mm8(weight: torch.Tensor):
     return w_u8, mx, rx, my, ry
 
 
+def quantize_mm8_outmajor(weight: torch.Tensor):
+    """Quantize ``nn.Linear.weight: [M, N]`` (out, in) to the same format as
+    ``quantize_mm8(weight.t())`` but with out-major byte storage.
+
+    Returns ``(w_u8, mx, rx, my, ry)`` where ``w_u8`` is the ``[N, M]`` (in, out)
+    transposed view of a contiguous ``[M, N]`` uint8 tensor; its values equal
+    the reference packer's bit for bit.  This layout feeds the fused decode
+    GEMV (``rwkv7mi_mm8t_matmul``).
+    """
+    if weight.dim() != 2:
+        raise ValueError("quantize_mm8_outmajor expects a 2-D weight")
+    _lib.require_gpu(weight, name="quantize_mm8_outmajor")
+    w = weight.contiguous()
+    m, n = (int(s) for s in w.shape)
+    dev, dt = w.device, w.dtype
+    w_t = torch.empty((m, n), device=dev, dtype=torch.uint8)
+    mx = torch.empty(m, device=dev, dtype=dt)
+    rx = torch.empty(m, device=dev, dtype=dt)
+    my = torch.empty((n, 1), device=dev, dtype=dt)
+    ry = torch.empty((n, 1), device=dev, dtype=dt)
+    ws = torch.empty(2 * n + 2 * m, device=dev, dtype=torch.float32)
+    _lib.call(
+        "rwkv7mi_mm8_pack_t", _lib.ptr(w), n, m, _lib.dtype_code(w), _lib.ptr(w_t), _lib.ptr(mx),
+        _lib.ptr(rx), _lib.ptr(my), _lib.ptr(ry), _lib.ptr(ws), _lib.stream_of(w),
+    )
+    return w_t.t(), mx, rx, my, ry
+
+
+def is_out_major(w_u8: torch.Tensor) -> bool:
+    """True when ``w_u8 [N, M]`` is the transposed view of contiguous ``[M, N]`` bytes."""
+    return (w_u8.dim() == 2 and not w_u8.is_contiguous() and w_u8.t().is_contiguous())
+
+
 def mm8_workspace_bytes(rows: int, n: int, m: int) -> int:
+    """Workspace of the row-major kernel; the out-major kernel needs none."""
     return int(_lib.load().rwkv7mi_mm8_workspace_bytes(int(rows), int(n), int(m)))
 
 
-def mm8_matmul_into(x2, w_u8, mx, rx, my, ry, out, *, bias=None, residual=None, epilogue=_lib.EPI_NONE):
-    """``out[rows, M] = epilogue(x2[rows, N] @ dequant(W))`` with no allocation."""
-    rows, n = (int(s) for s in x2.shape)
-    m = int(w_u8.shape[1])
-    if int(w_u8.shape[0]) != n:
-        raise ValueError(f"mm8: x has {n} features but w_u8 is {tuple(w_u8.shape)}")
+def _check_out(x2, m, out, residual):
+    rows = int(x2.shape[0])
     if tuple(out.shape) != (rows, m) or not out.is_contiguous() or out.dtype != x2.dtype:
         raise ValueError("mm8: out must be a contiguous [rows, M] tensor of x's dtype")
-    _lib.require_gpu(x2, w_u8, out, name="mm8_matmul")
-    need = mm8_workspace_bytes(rows, n, m)
-    ws = _ws.reserve(x2.device, need)
-    meta = mx
     if residual is not None:
         residual = residual.reshape(rows, m)
         if not residual.is_contiguous() or residual.dtype != x2.dtype:
             raise ValueError("mm8: residual must be contiguous with x's dtype")
+    return residual
+
+
+def mm8_matmul_into(x2, w_u8, mx, rx, my, ry, out, *, bias=None, residual=None, epilogue=_lib.EPI_NONE):
+    """``out[rows, M] = epilogue(x2[rows, N] @ dequant(W))`` with no allocation.
+
+    ``w_u8`` is either contiguous ``[N, M]`` (the reference's storage) or the
+    out-major view made by :func:`quantize_mm8_outmajor`; each has its kernel.
+    """
+    rows, n = (int(s) for s in x2.shape)
+    m = int(w_u8.shape[1])
+    if int(w_u8.shape[0]) != n:
+        raise ValueError(f"mm8: x has {n} features but w_u8 is {tuple(w_u8.shape)}")
+    _lib.require_gpu(x2, w_u8, out, name="mm8_matmul")
+    residual = _check_out(x2, m, out, residual)
+    if is_out_major(w_u8):
+        _lib.call(
+            "rwkv7mi_mm8t_matmul", _lib.ptr(x2), _lib.ptr(w_u8), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my),
+            _lib.ptr(ry), _lib.ptr(bias), _lib.ptr(residual), _lib.ptr(out), rows, n, m, int(epilogue),
+            _lib.dtype_code(x2), _lib.dtype_code(mx), _lib.stream_of(x2),
+        )
+        return out
+    if not w_u8.is_contiguous():
+        raise ValueError("mm8: w_u8 must be contiguous [N, M] or the out-major view")
+    ws = _ws.reserve(x2.device, mm8_workspace_bytes(rows, n, m))
     _lib.call(
         "rwkv7mi_mm8_matmul", _lib.ptr(x2), _lib.ptr(w_u8), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my),
         _lib.ptr(ry), _lib.ptr(bias), _lib.ptr(residual), _lib.ptr(out), rows, n, m, int(epilogue),
-        _lib.dtype_code(x2), _lib.dtype_code(meta), _lib.ptr(ws), int(ws.numel()), _lib.stream_of(x2),
+        _lib.dtype_code(x2), _lib.dtype_code(mx), _lib.ptr(ws), int(ws.numel()), _lib.stream_of(x2),
     )
     return out
+
+
+def mm8_matmul_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
+    """Up to four out-major ``MM8Linear`` products of one shape in a single launch.
+
+    ``xs[p] [rows, N]`` -> ``outs[p] [rows, M]`` through ``mods[p]``.
+    """
+    k = len(mods)
+    if not 1 <= k <= 4 or len(xs) != k or len(outs) != k:
+        raise ValueError("mm8_matmul_multi_into: 1..4 problems")
+    rows, n = (int(s) for s in xs[0].shape)
+    m = int(mods[0].out_features)
+    residuals = list(residuals) if residuals is not None else [None] * k
+    epilogues = list(epilogues) if epilogues is not None else [_lib.EPI_NONE] * k
+    for x2, mod, out, r in zip(xs, mods, outs, residuals):
+        if tuple(x2.shape) != (rows, n) or not x2.is_contiguous() or x2.dtype != xs[0].dtype:
+            raise ValueError("mm8_matmul_multi_into: inputs must share one contiguous shape and dtype")
+        if mod.in_features != n or mod.out_features != m or not is_out_major(mod.w_u8):
+            raise ValueError("mm8_matmul_multi_into: modules must be out-major and share one shape")
+        _check_out(x2, m, out, r)
+    _lib.require_gpu(*xs, *outs, name="mm8_matmul_multi")
+    arr = lambda ts: _lib.ptr_array(ts)
+    eps = (ctypes.c_int * k)(*[int(e) for e in epilogues])
+    _lib.call(
+        "rwkv7mi_mm8t_matmul_multi", k, arr(xs), arr([md.w_u8 for md in mods]), arr([md.mx for md in mods]),
+        arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),
+        arr([md.bias for md in mods]), arr(residuals), arr(outs), eps,
+        rows, n, m, _lib.dtype_code(xs[0]), _lib.dtype_code(mods[0].mx), _lib.stream_of(xs[0]),
+    )
+    return outs
 
 
 def _meta_1d(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
@@ -104,14 +187,17 @@ def mm8_matmul_triton(x, w_u8, mx, rx, my, ry, *, max_gemv_rows: int | None = No
 class MM8Linear(torch.nn.Module):
     """Drop-in for ``nn.Linear`` storing int8 (mm8) weights, dequantized on the fly.
 
-    Buffers match the reference module: ``w_u8 [in, out]``, ``mx, rx [out]``,
-    ``my, ry [in, 1]`` and optional ``bias``.
+    Buffers match the reference module (rwkv7_hf/native_quant_mm8.py:583-589):
+    ``w_u8 [in, out]``, ``mx, rx [out]``, ``my, ry [in, 1]`` and optional
+    ``bias``, with the same values.  ``w_u8`` is stored out-major (it is the
+    transposed view of ``[out, in]`` bytes), the layout the decode GEMV
+    streams; ``load_state_dict`` copies a reference ``w_u8`` into it.
     """
 
     def __init__(self, linear, *, fused=True):
         super().__init__()
         self.in_features, self.out_features = int(linear.weight.shape[1]), int(linear.weight.shape[0])
-        wu8, mx, rx, my, ry = quantize_mm8(linear.weight.data.t().contiguous())
+        wu8, mx, rx, my, ry = quantize_mm8_outmajor(linear.weight.data)
         self.register_buffer("w_u8", wu8)
         self.register_buffer("mx", mx)
         self.register_buffer("rx", rx)
@@ -151,6 +237,8 @@ class MM8Linear(torch.nn.Module):
         return self._run(x, residual=residual.contiguous(), epilogue=_lib.EPI_RESIDUAL)
 
     def rwkv7_workspace_bytes(self, rows: int) -> int:
+        if is_out_major(self.w_u8):
+            return 0
         return mm8_workspace_bytes(rows, self.in_features, self.out_features)
 
     def extra_repr(self):
@@ -176,6 +264,7 @@ def quantize_model_mm8(model, *, min_params: int = 8_000_000, fused: bool = True
 
 
 __all__ = [
-    "quantize_mm8", "mm8_matmul", "mm8_linear", "mm8_matmul_into", "mm8_gemv_triton",
+    "quantize_mm8", "quantize_mm8_outmajor", "is_out_major", "mm8_matmul", "mm8_linear", "mm8_matmul_into",
+    "mm8_matmul_multi_into", "mm8_gemv_triton",
     "mm8_matmul_triton", "mm8_workspace_bytes", "MM8Linear", "quantize_model_mm8",
 ]

@@ -158,6 +158,68 @@ int rwkv7mi_mm8_dequant(const uint8_t* w_u8, const void* mx, const void* rx,
                         const void* my, const void* ry, void* out, int64_t I,
                         int64_t O, int meta_dtype, int out_dtype, void* stream);
 
+/* Out-major MM8 (the decode path).  Same values as the [I,O] format, stored
+ * as w_t[o*I + i] == w_u8[i, o], i.e. in nn.Linear.weight's [O,I] layout; the
+ * reference's w_u8 buffer (rwkv7_hf/native_quant_mm8.py:583, uint8 [in, out])
+ * is the transposed view of w_t.  The reference picks its own per-device
+ * buffer layout the same way (q_row [out, in] at :578-580). */
+
+/* Packer from Linear.weight [O,I] itself: same outputs as rwkv7mi_mm8_pack on
+ * weight.T, with w_t [O,I].  Workspace as for rwkv7mi_mm8_pack. */
+int rwkv7mi_mm8_pack_t(const void* weight, int64_t I, int64_t O, int w_dtype,
+                       uint8_t* w_t, void* mx, void* rx, void* my, void* ry,
+                       float* workspace, void* stream);
+
+/* y[rows,O] = epilogue(x[rows,I] @ dequant(W)) over out-major w_t; no
+ * workspace, deterministic.  Replaces mm8_gemv_triton / mm8_matmul_triton /
+ * MM8Linear.forward (rwkv7_hf/native_quant_mm8.py:383, :468, :594) when the
+ * module stores out-major bytes.  I % 16 == 0; x, w_t, my, ry 16-byte
+ * aligned; y may alias residual. */
+int rwkv7mi_mm8t_matmul(const void* x, const uint8_t* w_t, const void* mx,
+                        const void* rx, const void* my, const void* ry,
+                        const void* bias, const void* residual, void* y,
+                        int64_t rows, int64_t I, int64_t O, int epilogue,
+                        int act_dtype, int meta_dtype, void* stream);
+
+/* Up to 4 rwkv7mi_mm8t_matmul problems of one shape in one launch (the
+ * r/k/v projections of rwkv7_hf/native.py:193-195).  Arrays have nprob
+ * entries; bias and residual arrays may be NULL. */
+int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x,
+                              const uint8_t* const* w_t, const void* const* mx,
+                              const void* const* rx, const void* const* my,
+                              const void* const* ry, const void* const* bias,
+                              const void* const* residual, void* const* y,
+                              const int* epilogue, int64_t rows, int64_t I,
+                              int64_t O, int act_dtype, int meta_dtype,
+                              void* stream);
+
+/* dequantize_mm8 (rwkv7_hf/native_quant_mm8.py:100-108) into out [O,I]
+ * (Linear.weight layout) for a library GEMM on long prefills.  I % 4 == 0. */
+int rwkv7mi_mm8t_dequant(const uint8_t* w_t, const void* mx, const void* rx,
+                         const void* my, const void* ry, void* out, int64_t I,
+                         int64_t O, int meta_dtype, int out_dtype, void* stream);
+
+/* ------------------------------------------------------------------ LoRA */
+
+/* Bytes of workspace rwkv7mi_lora_multi needs (fp32 split-K partials). */
+size_t rwkv7mi_lora_workspace_bytes(int64_t nprob, const int64_t* ranks,
+                                    int64_t rows, int64_t D);
+
+/* Up to four LoRA projections sharing x's shape, as in fused_wavg_lora /
+ * fused_wag_lora (rwkv7_hf/fused_lora.py:706, :559; torch form :795-803):
+ *   y_i = act_up_i(act_down_i(x_i @ w_down_i^T) @ w_up_i^T + b_up_i)
+ * x_i [rows,D], w_down_i [rank_i,D], w_up_i [A,rank_i], b_up_i [A] or NULL
+ * (b_up may be NULL), y_i [rows,A]; activations 0 none, 1 tanh, 2 sigmoid.
+ * The intermediate is rounded to act_dtype as the reference's tensor is.
+ * rank_i a multiple of 8, at most 256; D a multiple of 8. */
+int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs,
+                       const void* const* w_down, const void* const* w_up,
+                       const void* const* b_up, void* const* ys,
+                       const int64_t* ranks, const int* act_down,
+                       const int* act_up, int64_t rows, int64_t D, int64_t A,
+                       int act_dtype, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
 /* ---------------------------------------------------------- W4 group-128 */
 
 /* Device packer of the symmetric group W4 format of

@@ -1,0 +1,177 @@
+"""GPU parity of the out-major MM8 path: the packer from Linear.weight is
+bit-identical to the row-major packer (and so to the oracle), the fused GEMV /
+small-batch GEMM matches the fp64 oracle, the grouped launch equals single
+launches bit for bit, and the out-major dequantisation equals the row-major one."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _cuda(x, dtype):
+    return torch.tensor(np.asarray(x), dtype=dtype, device="cuda")
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _rel_err(got, ref):
+    return np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+
+
+@pytest.mark.parametrize("OI", [(256, 128), (128, 256), (1024, 4096), (40, 48), (3, 16)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.bfloat16])
+def test_pack_outmajor_equals_rowmajor(oracle, OI, dtype):
+    from rwkv7mi.native_quant_mm8 import is_out_major, quantize_mm8, quantize_mm8_outmajor
+
+    O, I = OI
+    rng = np.random.default_rng(O * 7 + I)
+    Wl = _cuda(rng.standard_normal((O, I)) * 0.02, dtype)  # Linear.weight [out, in]
+    a = quantize_mm8(Wl.t().contiguous())
+    b = quantize_mm8_outmajor(Wl)
+    torch.cuda.synchronize()
+    assert is_out_major(b[0]) and b[0].shape == (I, O)
+    for x, y in zip(a, b):
+        assert x.shape == y.shape
+        assert torch.equal(x, y)
+    if dtype == torch.float32:
+        q, *_ = oracle.mm8_pack(_np(Wl.t().contiguous()), out_dtype=np.float32)
+        np.testing.assert_array_equal(_np(b[0]), q)
+
+
+SHAPES = [(4096, 4096), (4096, 1024), (16384, 512), (144, 40), (1024, 65), (16, 16)]
+
+
+@pytest.mark.parametrize("IO", SHAPES)
+@pytest.mark.parametrize("rows", [1, 2, 5, 8, 16, 17, 40, 64])
+def test_mm8t_matmul_matches_oracle(oracle, IO, rows):
+    from rwkv7mi.native_quant_mm8 import mm8_matmul, quantize_mm8_outmajor
+
+    I, O = IO
+    rng = np.random.default_rng(I * 3 + O + rows)
+    Wl = _cuda(rng.standard_normal((O, I)) * 0.02, torch.float16)
+    packed = quantize_mm8_outmajor(Wl)
+    x = rng.standard_normal((rows, I)).astype(np.float16)
+    xt = _cuda(x, torch.float16)
+    y = mm8_matmul(xt, *packed)
+    y2 = mm8_matmul(xt, *packed)
+    torch.cuda.synchronize()
+    ref = oracle.mm8_matmul(x.astype(np.float64), *(_np(p) for p in packed))
+    err = _rel_err(_np(y).astype(np.float64), ref)
+    assert err <= 2e-3, err
+    assert torch.equal(y, y2), "repeated calls must be bit-identical"
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("meta", [torch.float32, torch.float16])
+def test_mm8t_dtypes(oracle, act, meta):
+    from rwkv7mi.native_quant_mm8 import mm8_matmul, quantize_mm8_outmajor
+
+    I, O, rows = 2048, 768, 6
+    rng = np.random.default_rng(11)
+    Wl = _cuda(rng.standard_normal((O, I)) * 0.02, meta)
+    packed = quantize_mm8_outmajor(Wl)
+    x = _cuda(rng.standard_normal((rows, I)), act)
+    y = mm8_matmul(x, *packed)
+    torch.cuda.synchronize()
+    ref = oracle.mm8_matmul(_np(x.float()).astype(np.float64), *(_np(p.float()) if p.is_floating_point() else _np(p)
+                                                                   for p in packed))
+    tol = 2e-3 if act != torch.bfloat16 else 8e-3
+    assert _rel_err(_np(y.float()).astype(np.float64), ref) <= tol
+
+
+def test_mm8t_epilogues_in_place_and_module(oracle):
+    from rwkv7mi import MM8Linear
+    from rwkv7mi.native_quant_mm8 import is_out_major
+
+    rng = np.random.default_rng(5)
+    I, O, rows = 1024, 4096, 3
+    lin = torch.nn.Linear(I, O, bias=True).to(device="cuda", dtype=torch.float16)
+    with torch.no_grad():
+        lin.weight.copy_(_cuda(rng.standard_normal((O, I)) * 0.02, torch.float16))
+        lin.bias.copy_(_cuda(rng.standard_normal(O) * 0.1, torch.float16))
+    mod = MM8Linear(lin)
+    assert is_out_major(mod.w_u8) and mod.rwkv7_workspace_bytes(rows) == 0
+    x = _cuda(rng.standard_normal((rows, I)), torch.float16)
+    res = _cuda(rng.standard_normal((rows, O)), torch.float16)
+    packed = [_np(b) for b in (mod.w_u8, mod.mx, mod.rx, mod.my, mod.ry)]
+    base = oracle.mm8_matmul(_np(x).astype(np.float64), *packed) + _np(lin.bias).astype(np.float64)
+    y = mod(x)
+    relu2 = mod.rwkv7_forward_relu2(x)
+    acc = res.clone()
+    mod._run(x, out=acc, residual=acc, epilogue=2)  # y aliases the residual
+    torch.cuda.synchronize()
+    scale = np.abs(base).max()
+    assert np.abs(_np(y) - base).max() <= 2e-3 * scale
+    r2 = np.maximum(base, 0) ** 2
+    assert np.abs(_np(relu2) - r2).max() <= 4e-3 * np.abs(r2).max()
+    add = base + _np(res).astype(np.float64)
+    assert np.abs(_np(acc) - add).max() <= 2e-3 * np.abs(add).max()
+    # a reference-layout state dict loads into the out-major buffer
+    sd = {k: v.clone() for k, v in mod.state_dict().items()}
+    sd["w_u8"] = sd["w_u8"].contiguous()
+    mod2 = MM8Linear(lin)
+    with torch.no_grad():
+        mod2.w_u8.zero_()
+    mod2.load_state_dict(sd)
+    assert is_out_major(mod2.w_u8) and torch.equal(mod2.w_u8, mod.w_u8)
+
+
+@pytest.mark.parametrize("rows", [1, 8, 20])
+def test_mm8t_multi_equals_single(rows):
+    from rwkv7mi import MM8Linear
+    from rwkv7mi.native_quant_mm8 import mm8_matmul_multi_into
+
+    rng = np.random.default_rng(rows)
+    I, O = 512, 384
+    mods, xs = [], []
+    for p in range(3):
+        lin = torch.nn.Linear(I, O, bias=(p == 1)).to(device="cuda", dtype=torch.float16)
+        with torch.no_grad():
+            lin.weight.copy_(_cuda(rng.standard_normal((O, I)) * 0.02, torch.float16))
+        mods.append(MM8Linear(lin))
+        xs.append(_cuda(rng.standard_normal((rows, I)), torch.float16))
+    outs = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(3)]
+    mm8_matmul_multi_into(xs, mods, outs)
+    single = [m(x) for m, x in zip(mods, xs)]
+    torch.cuda.synchronize()
+    for a, b in zip(outs, single):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("IO", [(256, 512), (4096, 1024)])
+def test_mm8t_dequant_equals_rowmajor(IO):
+    from rwkv7mi import _lib
+    from rwkv7mi.native_quant_mm8 import quantize_mm8_outmajor
+
+    I, O = IO
+    rng = np.random.default_rng(I)
+    Wl = _cuda(rng.standard_normal((O, I)) * 0.02, torch.float16)
+    w, mx, rx, my, ry = quantize_mm8_outmajor(Wl)
+    a = torch.empty(O, I, device="cuda", dtype=torch.float16)
+    b = torch.empty(I, O, device="cuda", dtype=torch.float16)
+    s = _lib.stream_of(a)
+    _lib.call("rwkv7mi_mm8t_dequant", _lib.ptr(w), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my), _lib.ptr(ry),
+              _lib.ptr(a), I, O, _lib.F16, _lib.F16, s)
+    wc = w.contiguous()
+    _lib.call("rwkv7mi_mm8_dequant", _lib.ptr(wc), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my), _lib.ptr(ry),
+              _lib.ptr(b), I, O, _lib.F16, _lib.F16, s)
+    torch.cuda.synchronize()
+    assert torch.equal(a.t(), b)
+
+
+def test_mm8t_rejects_bad_shapes():
+    from rwkv7mi import _lib
+
+    x = torch.zeros(1, 24, device="cuda", dtype=torch.float16)
+    w = torch.zeros(8, 24, device="cuda", dtype=torch.uint8)
+    m8 = torch.zeros(8, device="cuda", dtype=torch.float16)
+    m24 = torch.zeros(24, device="cuda", dtype=torch.float16)
+    y = torch.zeros(1, 8, device="cuda", dtype=torch.float16)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        _lib.call("rwkv7mi_mm8t_matmul", _lib.ptr(x), _lib.ptr(w), _lib.ptr(m8), _lib.ptr(m8), _lib.ptr(m24),
+                  _lib.ptr(m24), None, None, _lib.ptr(y), 1, 24, 8, 0, _lib.F16, _lib.F16, _lib.stream_of(x))

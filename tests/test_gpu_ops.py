@@ -103,6 +103,29 @@ def test_wavg_lora(oracle, rows, D):
         _ok(g, r)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,D", [(2, 1024), (33, 200)])
+def test_wag_lora_dtypes(oracle, dt, rows, D):
+    from rwkv7mi.fused_lora import fused_wag_lora
+
+    rng = np.random.default_rng(rows * 7 + D)
+    A = 512
+    xs = [_t(rng.standard_normal((rows, D)), dt) for _ in range(3)]
+    ranks = (32, 48, 96)
+    downs = [_t(rng.standard_normal((r, D)) * 0.02, dt) for r in ranks]
+    ups = [_t(rng.standard_normal((A, r)) * 0.1, dt) for r in ranks]
+    biases = [_t(rng.standard_normal(A) * 0.01, dt), None, _t(rng.standard_normal(A) * 0.01, dt)]
+    got = fused_wag_lora(*xs, *downs, *ups, *biases)
+    torch.cuda.synchronize()
+    # the intermediate is rounded to the activation dtype, as the reference's tensor is
+    rnd = (lambda a: _f(torch.tensor(a, dtype=dt))) if dt != torch.float32 else (lambda a: a)
+    acts = (np.tanh, lambda v: v, lambda v: 1 / (1 + np.exp(-v)))
+    for q in range(3):
+        mid = rnd(acts[q](_f(xs[q]) @ _f(downs[q]).T))
+        ref = mid @ _f(ups[q]).T + (0 if biases[q] is None else _f(biases[q]))
+        _ok(got[q], ref, tol=1e-2 if dt == torch.bfloat16 else 1e-4)
+
+
 def test_output_prepare_and_state_prep(oracle):
     from rwkv7mi.fused_output import fused_attn_output_prepare
     from rwkv7mi.fused_prefill import fused_prefill_state_prep
