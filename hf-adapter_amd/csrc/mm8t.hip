@@ -120,14 +120,19 @@ __device__ __forceinline__ f16x8 mm8t_b_operand(uint32_t d0, uint32_t d1) {
   return (f16x8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
-template <typename TA, typename TM, int DEPTH>
+template <typename TA, typename TM, int CSW>
 __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
+  // CSW: 128-row steps per wave per K-chunk (KC = 512 CSW); the chunk body is
+  // fully unrolled so the load ring needs no loop-carried waits.
+  constexpr int DEPTH = CSW < 8 ? CSW : 8;
   const Mm8tProb& P = B.p[blockIdx.y];
-  const int I = B.I, O = B.O, KC = B.KC;
+  const int I = B.I, O = B.O;
+  constexpr int KC = 512 * CSW;
   const int row0 = blockIdx.z * 16;
   const int nrows = min(16, B.rows - row0);
-  const int col0 = blockIdx.x * MM8T_COLS;
-  const int XS = KC + 8;  // LDS row stride (halfs)
+  const int ngroups = (O + MM8T_COLS - 1) / MM8T_COLS;
+  const int gstride = gridDim.x;
+  constexpr int XS = KC + 8;  // LDS row stride (halfs)
   extern __shared__ __align__(16) char smem[];
   _Float16* xh = reinterpret_cast<_Float16*>(smem);
   _Float16* xl = xh + nrows * XS;
@@ -141,17 +146,20 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
   const int n = lane & 15;
   const int kg = lane >> 4;
 
-  // this workgroup's 16 columns are one contiguous run of ncols * I bytes
-  const int ncols = min(MM8T_COLS, O - col0);
-  const __amdgpu_buffer_rsrc_t wr = mm8t_rsrc(P.w + (int64_t)col0 * I, (uint32_t)ncols * (uint32_t)I);
+  // A column group's 16 columns are one contiguous run of ncols * I bytes;
+  // groups past the end get an empty descriptor (all loads read zeros).
+  auto group_rsrc = [&](int g) {
+    const int c0 = g * MM8T_COLS;
+    const int nc = g < ngroups ? min(MM8T_COLS, O - c0) : 0;
+    return mm8t_rsrc(P.w + (int64_t)(g < ngroups ? c0 : 0) * I, (uint32_t)nc * (uint32_t)I);
+  };
   const __amdgpu_buffer_rsrc_t xr =
       mm8t_rsrc(reinterpret_cast<const TA*>(P.x) + (int64_t)row0 * I, (uint32_t)(nrows * I * sizeof(TA)));
   const __amdgpu_buffer_rsrc_t ryr = mm8t_rsrc(P.ry, (uint32_t)(I * sizeof(TM)));
   const __amdgpu_buffer_rsrc_t myr = mm8t_rsrc(P.my, (uint32_t)(I * sizeof(TM)));
   const uint32_t lane_off = (uint32_t)n * (uint32_t)I + 16u * kg;
-
-  const int CSW = KC >> 9;  // steps per wave per chunk (a multiple of DEPTH)
   const int nchunks = (I + KC - 1) / KC;
+  const int J = nchunks * CSW;  // steps per wave per column group
 
   // staging: TPR threads per batch row, fixed for the whole kernel
   int rp2 = 1;
@@ -159,84 +167,124 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
   const int TPR = 256 / rp2;
   const int sr = tid / TPR;
   const int su = tid % TPR;
-  const int NQ = KC >> 3;                  // 8-element groups per chunk row
+  constexpr int NQ = KC >> 3;              // 8-element groups per chunk row
   const int QIT = (NQ + TPR - 1) / TPR;    // uniform trip count
   float sx = 0.f, sxmy = 0.f;
 
-  // Step j of this wave covers K rows 128 (wave + 4j) .. +127.  Segments at or
-  // beyond I (the tail step, prefetches past the end) read as zeros.
+  // x' staging in batches of MM8T_SB groups: issue (loads in flight together),
+  // then finish (x' = x ry as fp16 hi + lo into LDS, row sums).  Rows past I
+  // stage as zeros.
+  Raw8<TA> rxv[MM8T_SB];
+  Raw8<TM> rrv[MM8T_SB], rmv[MM8T_SB];
+  auto stage_issue = [&](int kc0, int it0) {
+#pragma unroll
+    for (int u = 0; u < MM8T_SB; ++u) {
+      const int q = su + (it0 + u) * TPR;
+      const int k = kc0 + 8 * q;
+      const bool valid = sr < nrows && q < NQ && k < I;
+      rxv[u] = mm8t_ld8<TA>(xr, (uint32_t)(sr * I + k), valid);
+      rrv[u] = mm8t_ld8<TM>(ryr, (uint32_t)k, valid);
+      rmv[u] = mm8t_ld8<TM>(myr, (uint32_t)k, valid);
+    }
+  };
+  auto stage_finish = [&](int it0) {
+#pragma unroll
+    for (int u = 0; u < MM8T_SB; ++u) {
+      const int q = su + (it0 + u) * TPR;
+      float xv[8], rv[8], mv[8];
+      mm8t_cvt8(rxv[u], xv);
+      mm8t_cvt8(rrv[u], rv);
+      mm8t_cvt8(rmv[u], mv);
+      f16x8 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xp = xv[e] * rv[e];
+        const _Float16 h = (_Float16)xp;
+        hi[e] = h;
+        lo[e] = (_Float16)(xp - (float)h);
+        sx += xv[e];
+        sxmy += xv[e] * mv[e];
+      }
+      if (sr < nrows && q < NQ) {
+        *reinterpret_cast<f16x8*>(xh + sr * XS + 8 * q) = hi;
+        *reinterpret_cast<f16x8*>(xl + sr * XS + 8 * q) = lo;
+      }
+    }
+  };
+
+  // Step j of this wave covers K rows 128 (wave + 4j) .. +127 of a group.
+  // Segments at or beyond I (the tail step) read as zeros.
   u32x4 buf[DEPTH][2];
-  auto load_step = [&](int j, u32x4 (&b)[2]) {
+  auto load_step = [&](__amdgpu_buffer_rsrc_t r, int j, u32x4 (&b)[2]) {
     const int k = 128 * (wave + 4 * j) + 16 * kg;
     const uint32_t off = lane_off + 128u * (uint32_t)(wave + 4 * j);
-    b[0] = mm8t_ld16(wr, k < I ? off : MM8T_OOB);
-    b[1] = mm8t_ld16(wr, k + 64 < I ? off + 64u : MM8T_OOB);
+    b[0] = mm8t_ld16(r, k < I ? off : MM8T_OOB);
+    b[1] = mm8t_ld16(r, k + 64 < I ? off + 64u : MM8T_OOB);
   };
+  int g = blockIdx.x;
+  __amdgpu_buffer_rsrc_t wr = group_rsrc(g);             // this group
+  __amdgpu_buffer_rsrc_t wn = group_rsrc(g + gstride);   // the next one
+
+  // chunk 0: the first staging batch goes out before the weight ring fill, so
+  // the x' math waits only for those loads while the weights stream in
+  stage_issue(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) load_step(d, buf[d]);
+  for (int d = 0; d < DEPTH; ++d) load_step(wr, d, buf[d]);  // DEPTH <= CSW <= J
+  __builtin_amdgcn_sched_barrier(0);
+  stage_finish(0);
+  for (int it0 = MM8T_SB; it0 < QIT; it0 += MM8T_SB) {
+    stage_issue(0, it0);
+    stage_finish(it0);
+  }
+  __syncthreads();
 
   const int arow = n < nrows ? n : nrows - 1;
   const _Float16* ah = xh + arow * XS + 16 * kg;
   const _Float16* al = xl + arow * XS + 16 * kg;
-  f32x4 acc[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) acc[q] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const TM* rx = reinterpret_cast<const TM*>(P.rx);
+  const TM* mx = reinterpret_cast<const TM*>(P.mx);
+  const TM* bias = reinterpret_cast<const TM*>(P.bias);
 
-  for (int c = 0; c < nchunks; ++c) {
-    // ---- stage chunk c of x' into LDS (rows past I stage as zeros), in
-    // batches of MM8T_SB groups whose loads are all in flight together
-    const int kc0 = c * KC;
-    __syncthreads();
-    for (int it0 = 0; it0 < QIT; it0 += MM8T_SB) {
-      Raw8<TA> rxv[MM8T_SB];
-      Raw8<TM> rrv[MM8T_SB], rmv[MM8T_SB];
+  // Column groups g = blockIdx.x, + gridDim.x, ...  With one K-chunk, x' stays
+  // in LDS for all of them and the ring prefetches the next group's first
+  // steps while this one finishes; with several chunks the host launches one
+  // group per workgroup.
+  for (bool first = true; g < ngroups; g += gstride, first = false) {
+    f32x4 acc[4];
 #pragma unroll
-      for (int u = 0; u < MM8T_SB; ++u) {
-        const int q = su + (it0 + u) * TPR;
-        const int k = kc0 + 8 * q;
-        const bool valid = sr < nrows && q < NQ && k < I;
-        rxv[u] = mm8t_ld8<TA>(xr, (uint32_t)(sr * I + k), valid);
-        rrv[u] = mm8t_ld8<TM>(ryr, (uint32_t)k, valid);
-        rmv[u] = mm8t_ld8<TM>(myr, (uint32_t)k, valid);
-      }
-#pragma unroll
-      for (int u = 0; u < MM8T_SB; ++u) {
-        const int q = su + (it0 + u) * TPR;
-        float xv[8], rv[8], mv[8];
-        mm8t_cvt8(rxv[u], xv);
-        mm8t_cvt8(rrv[u], rv);
-        mm8t_cvt8(rmv[u], mv);
-        f16x8 hi, lo;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float xp = xv[e] * rv[e];
-          const _Float16 h = (_Float16)xp;
-          hi[e] = h;
-          lo[e] = (_Float16)(xp - (float)h);
-          sx += xv[e];
-          sxmy += xv[e] * mv[e];
-        }
-        if (sr < nrows && q < NQ) {
-          *reinterpret_cast<f16x8*>(xh + sr * XS + 8 * q) = hi;
-          *reinterpret_cast<f16x8*>(xl + sr * XS + 8 * q) = lo;
-        }
-      }
-    }
-    __syncthreads();
+    for (int q = 0; q < 4; ++q) acc[q] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    // ---- this wave's steps of the chunk; the load ring runs DEPTH steps ahead
-    for (int jb = 0; jb < CSW; jb += DEPTH) {
+    for (int c = 0; c < nchunks; ++c) {
+      if (c > 0) {
+        __syncthreads();
+        for (int it0 = 0; it0 < QIT; it0 += MM8T_SB) {
+          stage_issue(c * KC, it0);
+          stage_finish(it0);
+        }
+        __syncthreads();
+      }
+      // ---- this wave's CSW steps of the chunk; the load ring runs DEPTH steps ahead
+      const bool last_chunk = c == nchunks - 1;
 #pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        const int jl = jb + d;
+      for (int jl = 0; jl < CSW; ++jl) {
+        const int d = jl % DEPTH;
         // convert this step's bytes first, then refill the same ring slot: the
-        // slot is dead once converted, so it keeps its registers across the loop
+        // slot is dead once converted, so it keeps its registers
         f16x8 bv[4];
         bv[0] = mm8t_b_operand(buf[d][0][0], buf[d][0][1]);
         bv[1] = mm8t_b_operand(buf[d][0][2], buf[d][0][3]);
         bv[2] = mm8t_b_operand(buf[d][1][0], buf[d][1][1]);
         bv[3] = mm8t_b_operand(buf[d][1][2], buf[d][1][3]);
-        load_step(c * CSW + jl + DEPTH, buf[d]);
+        if (jl + DEPTH < CSW) {
+          load_step(wr, c * CSW + jl + DEPTH, buf[d]);
+        } else {  // may wrap into the next group's first steps (uniform select)
+          const int t = c * CSW + jl + DEPTH;
+          load_step(last_chunk ? wn : wr, last_chunk ? t - J : t, buf[d]);
+        }
+        // keep the refill here: sunk to the end of the body it would leave the
+        // ring empty while the body computes
+        __builtin_amdgcn_sched_barrier(0);
         const int kl = 128 * (wave + 4 * jl);
 #pragma unroll
         for (int hq = 0; hq < 4; ++hq) {
@@ -248,74 +296,77 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
         }
       }
     }
-  }
-  const f32x4 accs = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    const f32x4 accs = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 
-  // ---- per-row sums: fixed-order butterfly inside each row's lanes, then waves
-  const int width = TPR < 64 ? TPR : 64;
-  for (int o = width >> 1; o > 0; o >>= 1) {
-    sx += __shfl_xor(sx, o, 64);
-    sxmy += __shfl_xor(sxmy, o, 64);
-  }
-  if (TPR >= 64) {
-    if (lane == 0) {
-      wsum[wave][0] = sx;
-      wsum[wave][1] = sxmy;
+    if (first) {
+      // ---- per-row sums (staging is complete): fixed-order butterfly inside
+      // each row's lanes, then across waves
+      const int width = TPR < 64 ? TPR : 64;
+      for (int o = width >> 1; o > 0; o >>= 1) {
+        sx += __shfl_xor(sx, o, 64);
+        sxmy += __shfl_xor(sxmy, o, 64);
+      }
+      if (TPR >= 64 && lane == 0) {
+        wsum[wave][0] = sx;
+        wsum[wave][1] = sxmy;
+      }
+      __syncthreads();
+      if (TPR >= 64) {
+        if (tid < nrows) {
+          const int wpr = TPR >> 6;  // waves per row
+          float a = 0.f, b = 0.f;
+          for (int q = 0; q < wpr; ++q) {
+            a += wsum[tid * wpr + q][0];
+            b += wsum[tid * wpr + q][1];
+          }
+          rsum[tid][0] = a;
+          rsum[tid][1] = b;
+        }
+      } else if (su == 0 && sr < nrows) {
+        rsum[sr][0] = sx;
+        rsum[sr][1] = sxmy;
+      }
     }
-  }
-  // ---- wave partial tiles: lane holds col n, rows 4kg + e
+    // ---- wave partial tiles (lane holds col n, rows 4kg + e), then one thread
+    // per (row, column) finishes; the barrier pair also fences the previous
+    // group's reads of red[]
+    __syncthreads();
 #pragma unroll
-  for (int e = 0; e < 4; ++e) red[wave][4 * kg + e][n] = accs[e];
-  __syncthreads();
-  if (TPR >= 64) {
-    if (tid < nrows) {
-      const int wpr = TPR >> 6;  // waves per row
-      float a = 0.f, b = 0.f;
-      for (int q = 0; q < wpr; ++q) {
-        a += wsum[tid * wpr + q][0];
-        b += wsum[tid * wpr + q][1];
+    for (int e = 0; e < 4; ++e) red[wave][4 * kg + e][n] = accs[e];
+    __syncthreads();
+    if (tid < nrows * MM8T_COLS) {
+      const int m = tid >> 4;
+      const int cn = tid & 15;
+      const int o = g * MM8T_COLS + cn;
+      if (o < O) {
+        const float s = ((red[0][m][cn] + red[1][m][cn]) + red[2][m][cn]) + red[3][m][cn];
+        float v = ld(rx, o) * s + rsum[m][1] + ld(mx, o) * rsum[m][0];
+        if (bias) v += ld(bias, o);
+        const int64_t oi = (int64_t)(row0 + m) * O + o;
+        if (P.epilogue == RWKV7MI_EPI_RELU2) {
+          v = fmaxf(v, 0.f);
+          v = v * v;
+        } else if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
+          v += ld(reinterpret_cast<const TA*>(P.residual), oi);
+        }
+        reinterpret_cast<TA*>(P.y)[oi] = from_f32<TA>(v);
       }
-      rsum[tid][0] = a;
-      rsum[tid][1] = b;
     }
-  } else if (su == 0 && sr < nrows) {
-    rsum[sr][0] = sx;
-    rsum[sr][1] = sxmy;
-  }
-  __syncthreads();
-
-  // ---- epilogue: one thread per (row, column)
-  if (tid < nrows * MM8T_COLS) {
-    const int m = tid >> 4;
-    const int cn = tid & 15;
-    const int o = col0 + cn;
-    if (o < O) {
-      const float s = ((red[0][m][cn] + red[1][m][cn]) + red[2][m][cn]) + red[3][m][cn];
-      float v = ld(reinterpret_cast<const TM*>(P.rx), o) * s + rsum[m][1] +
-                ld(reinterpret_cast<const TM*>(P.mx), o) * rsum[m][0];
-      if (P.bias) v += ld(reinterpret_cast<const TM*>(P.bias), o);
-      const int64_t oi = (int64_t)(row0 + m) * O + o;
-      if (P.epilogue == RWKV7MI_EPI_RELU2) {
-        v = fmaxf(v, 0.f);
-        v = v * v;
-      } else if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
-        v += ld(reinterpret_cast<const TA*>(P.residual), oi);
-      }
-      reinterpret_cast<TA*>(P.y)[oi] = from_f32<TA>(v);
-    }
+    wr = wn;
+    wn = group_rsrc(g + 2 * gstride);
   }
 }
 
-// x' staging chunk: the largest power-of-two multiple of 1024 rows whose
-// hi/lo copy for the tile's rows fits the LDS budget, and no longer than I
-// needs.  A grid of at most one workgroup per CU, or a tile of more than four
-// rows (whose staging would otherwise repeat per chunk), uses most of the CU's
-// LDS; the DEPTH-step weight ring keeps 64 KB per CU in flight even then.
+// x' staging chunk: the largest power-of-two multiple of 1024 rows (at most
+// 16384) whose hi/lo copy for the tile's rows fits the LDS budget, and no
+// longer than I needs.  A grid of at most one workgroup per CU, or a tile of
+// more than four rows (whose staging would otherwise repeat per chunk), uses
+// most of the CU's LDS; the weight ring keeps 64 KB per CU in flight even then.
 static int mm8t_chunk(int64_t rows, int64_t I, int64_t nwg) {
   const int64_t nr = rows < 16 ? rows : 16;
   const int64_t budget = (nwg <= 256 || nr > 4) ? MM8T_LDS_X_ONE : MM8T_LDS_X;
   int64_t kc = 1024;
-  while (kc < I && nr * (2 * kc + 8) * 4 <= budget) kc *= 2;
+  while (kc < I && kc < 16384 && nr * (2 * kc + 8) * 4 <= budget) kc *= 2;
   return (int)kc;
 }
 
@@ -328,17 +379,29 @@ static size_t mm8t_lds(int64_t rows, int KC) {
 
 using namespace rwkv7mi;
 
-template <typename TA, typename TM, int DEPTH>
+template <typename TA, typename TM, int CSW>
 static int mm8t_go(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
   static bool lds_raised = false;  // dynamic LDS above 64 KB must be enabled once per instance
   if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, DEPTH>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, CSW>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, MM8T_LDS_X_ONE + 1024) != hipSuccess)
       return fail(RWKV7MI_ELAUNCH, "mm8t_kernel: cannot raise the dynamic LDS limit");
     lds_raised = true;
   }
-  hipLaunchKernelGGL((mm8t_kernel<TA, TM, DEPTH>), grid, dim3(256), lds, as_stream(stream), b);
+  hipLaunchKernelGGL((mm8t_kernel<TA, TM, CSW>), grid, dim3(256), lds, as_stream(stream), b);
   return check_launch("mm8t_kernel");
+}
+
+// compute units of the current device (cached per device)
+static int64_t mm8t_cus() {
+  static int64_t cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
 }
 
 static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I, int64_t O, int act_dtype,
@@ -365,17 +428,31 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
   b.rows = (int)rows;
   b.I = (int)I;
   b.O = (int)O;
-  dim3 grid((unsigned)((O + MM8T_COLS - 1) / MM8T_COLS), (unsigned)nprob, (unsigned)((rows + 15) / 16));
-  b.KC = mm8t_chunk(rows, I, (int64_t)grid.x * grid.y * grid.z);
+  const int64_t ngroups = (O + MM8T_COLS - 1) / MM8T_COLS;
+  const int64_t rtiles = (rows + 15) / 16;
+  b.KC = mm8t_chunk(rows, I, ngroups * nprob * rtiles);
   const size_t lds = mm8t_lds(rows, b.KC);
+  // With x' in one LDS chunk, workgroups loop over column groups: as many as
+  // stay resident (two per CU at this kernel's register use and LDS size),
+  // split between the problems and row tiles.
+  int64_t gx = ngroups;
+  if (b.KC >= I) {
+    const int64_t per_cu = lds <= MM8T_LDS_X ? 2 : 1;
+    const int64_t slots = mm8t_cus() * per_cu / (nprob * rtiles);
+    if (slots >= 1 && slots < gx) gx = slots;
+  }
+  dim3 grid((unsigned)gx, (unsigned)nprob, (unsigned)rtiles);
   return dispatch_dtype(act_dtype, [&](auto ta) {
     using TA = decltype(ta);
     return dispatch_dtype(meta_dtype, [&](auto tm) {
       using TM = decltype(tm);
-      const int csw = b.KC >> 9;
-      if (csw >= 8) return mm8t_go<TA, TM, 8>(grid, lds, stream, b);
-      if (csw >= 4) return mm8t_go<TA, TM, 4>(grid, lds, stream, b);
-      return mm8t_go<TA, TM, 2>(grid, lds, stream, b);
+      switch (b.KC >> 9) {
+        case 2: return mm8t_go<TA, TM, 2>(grid, lds, stream, b);
+        case 4: return mm8t_go<TA, TM, 4>(grid, lds, stream, b);
+        case 8: return mm8t_go<TA, TM, 8>(grid, lds, stream, b);
+        case 16: return mm8t_go<TA, TM, 16>(grid, lds, stream, b);
+        default: return mm8t_go<TA, TM, 32>(grid, lds, stream, b);
+      }
     });
   });
 }
