@@ -239,9 +239,12 @@ static Mm8Plan mm8_plan(int64_t rows, int64_t I, int64_t O) {
 // Element (i, j) of the [I, O] matrix W = weight.T lives at i*O + j (row-major,
 // OM = false) or at j*I + i (out-major, OM = true: nn.Linear.weight itself).
 // Per-out statistics (mx, rx) reduce over i, per-in ones (my, ry) over j.
+// Or real output columns are stored; columns Or.. of a padded matrix read as 0
+// (the zero pad column rwkv7_hf/native_quant_mm4.py:89-92 appends).
 template <typename TW, bool OM>
-__device__ __forceinline__ float mm8_w(const TW* w, int i, int j, int I, int O) {
-  return to_f32(OM ? w[(int64_t)j * I + i] : w[(int64_t)i * O + j]);
+__device__ __forceinline__ float mm8_w(const TW* w, int i, int j, int I, int Or) {
+  if (j >= Or) return 0.f;
+  return to_f32(OM ? w[(int64_t)j * I + i] : w[(int64_t)i * Or + j]);
 }
 
 // One reduction term.  phase 0: min w; 1: min (w - other offset);
@@ -263,7 +266,8 @@ __device__ __forceinline__ void mm8_stat_store(float m, int line, int phase, flo
 
 // One workgroup per line; coalesced when the line is contiguous (PER_OUT == OM).
 template <typename TW, bool OM, bool PER_OUT>
-__global__ __launch_bounds__(256) void mm8_stat_line(const TW* __restrict__ w, int I, int O, int phase, float* ws) {
+__global__ __launch_bounds__(256) void mm8_stat_line(const TW* __restrict__ w, int I, int O, int Or, int phase,
+                                                    float* ws) {
   const float* my = ws;
   const float* mx = ws + I;
   const float* rx = ws + I + O;
@@ -274,7 +278,7 @@ __global__ __launch_bounds__(256) void mm8_stat_line(const TW* __restrict__ w, i
   float m = phase == 2 ? -INFINITY : INFINITY;
   for (int t = threadIdx.x; t < len; t += 256) {
     const int i = PER_OUT ? t : line, j = PER_OUT ? line : t;
-    const float v = mm8_term<PER_OUT>(mm8_w<TW, OM>(w, i, j, I, O), i, j, phase, rows_first, my, mx, rx);
+    const float v = mm8_term<PER_OUT>(mm8_w<TW, OM>(w, i, j, I, Or), i, j, phase, rows_first, my, mx, rx);
     m = phase == 2 ? fmaxf(m, v) : fminf(m, v);
   }
 #pragma unroll
@@ -293,7 +297,7 @@ __global__ __launch_bounds__(256) void mm8_stat_line(const TW* __restrict__ w, i
 
 // One thread per line; coalesced across threads when the line is strided (PER_OUT != OM).
 template <typename TW, bool OM, bool PER_OUT>
-__global__ __launch_bounds__(256) void mm8_stat_thread(const TW* __restrict__ w, int I, int O, int phase,
+__global__ __launch_bounds__(256) void mm8_stat_thread(const TW* __restrict__ w, int I, int O, int Or, int phase,
                                                        float* ws) {
   const float* my = ws;
   const float* mx = ws + I;
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(256) void mm8_stat_thread(const TW* __restrict__ w,
   float m = phase == 2 ? -INFINITY : INFINITY;
   for (int t = 0; t < len; ++t) {
     const int i = PER_OUT ? t : line, j = PER_OUT ? line : t;
-    const float v = mm8_term<PER_OUT>(mm8_w<TW, OM>(w, i, j, I, O), i, j, phase, rows_first, my, mx, rx);
+    const float v = mm8_term<PER_OUT>(mm8_w<TW, OM>(w, i, j, I, Or), i, j, phase, rows_first, my, mx, rx);
     m = phase == 2 ? fmaxf(m, v) : fminf(m, v);
   }
   mm8_stat_store<PER_OUT>(m, line, phase, ws, I, O);
@@ -343,30 +347,105 @@ __global__ void mm8_quantize(const TW* __restrict__ wt, int I, int O, const floa
 }
 
 template <typename TW, bool OM, bool PER_OUT>
-static void mm8_stat(const TW* w, int I, int O, int phase, float* ws, hipStream_t s) {
+static void mm8_stat(const TW* w, int I, int O, int Or, int phase, float* ws, hipStream_t s) {
   const int nlines = PER_OUT ? O : I;
   if (PER_OUT == OM)
-    hipLaunchKernelGGL((mm8_stat_line<TW, OM, PER_OUT>), dim3((unsigned)nlines), dim3(256), 0, s, w, I, O, phase, ws);
+    hipLaunchKernelGGL((mm8_stat_line<TW, OM, PER_OUT>), dim3((unsigned)nlines), dim3(256), 0, s, w, I, O, Or, phase,
+                       ws);
   else
     hipLaunchKernelGGL((mm8_stat_thread<TW, OM, PER_OUT>), dim3((unsigned)((nlines + 255) / 256)), dim3(256), 0, s,
-                       w, I, O, phase, ws);
+                       w, I, O, Or, phase, ws);
+}
+
+// the statistics passes of the reference (rwkv7_hf/native_quant_mm8.py:66-80,
+// rwkv7_hf/native_quant_mm4.py:93-100) over O logical columns, Or of them stored
+template <typename TW, bool OM>
+static void mm8_stats(const TW* w, int I, int O, int Or, float* ws, hipStream_t s) {
+  if (I > O) {  // rows first
+    mm8_stat<TW, OM, false>(w, I, O, Or, 0, ws, s);
+    mm8_stat<TW, OM, true>(w, I, O, Or, 1, ws, s);
+  } else {
+    mm8_stat<TW, OM, true>(w, I, O, Or, 0, ws, s);
+    mm8_stat<TW, OM, false>(w, I, O, Or, 1, ws, s);
+  }
+  mm8_stat<TW, OM, true>(w, I, O, Or, 2, ws, s);
+  mm8_stat<TW, OM, false>(w, I, O, Or, 2, ws, s);
 }
 
 template <typename TW, bool OM>
 static int mm8_pack_run(const TW* w, int I, int O, uint8_t* w_u8, void* mx, void* rx, void* my, void* ry,
                         float* ws, hipStream_t s) {
-  if (I > O) {  // rows first (rwkv7_hf/native_quant_mm8.py:66-71)
-    mm8_stat<TW, OM, false>(w, I, O, 0, ws, s);
-    mm8_stat<TW, OM, true>(w, I, O, 1, ws, s);
-  } else {
-    mm8_stat<TW, OM, true>(w, I, O, 0, ws, s);
-    mm8_stat<TW, OM, false>(w, I, O, 1, ws, s);
-  }
-  mm8_stat<TW, OM, true>(w, I, O, 2, ws, s);
-  mm8_stat<TW, OM, false>(w, I, O, 2, ws, s);
+  mm8_stats<TW, OM>(w, I, O, O, ws, s);
   hipLaunchKernelGGL((mm8_quantize<TW, OM>), dim3(4096), dim3(256), 0, s, w, I, O, ws, w_u8, (TW*)mx, (TW*)rx,
                      (TW*)my, (TW*)ry);
   return check_launch("mm8_pack");
+}
+
+// MM4 affine (rwkv7_hf/native_quant_mm4.py:77-105): 16 levels over the O = Mp
+// (even) logical columns.  OM = false: packed [I, O/2], byte (i, b) =
+// q(i, 2b) | q(i, 2b+1) << 4 (the reference layout); OM = true: packed
+// [O, I/2], byte (j, a) = q(2a, j) | q(2a+1, j) << 4 (pairs along the inputs,
+// the fused GEMV's layout; the pad column's nibbles are kept as a last row).
+template <typename TW, bool OM>
+__device__ __forceinline__ uint32_t mm4_q(const TW* w, int i, int j, int I, int Or, bool rows_first,
+                                          const float* my, const float* mx, const float* rx, const float* ry) {
+  const float v = mm8_w<TW, OM>(w, i, j, I, Or);
+  const float w2 = rows_first ? (v - my[i]) - mx[j] : (v - mx[j]) - my[i];
+  const float w4 = __fdiv_rn(__fdiv_rn(w2, rx[j]), ry[i]);
+  float q = floorf(w4 * 16.0f);
+  q = fminf(fmaxf(q, 0.0f), 15.0f);
+  return (uint32_t)q;
+}
+
+template <typename TW, bool OM>
+__global__ void mm4_quantize(const TW* __restrict__ w, int I, int O, int Or, const float* ws,
+                             uint8_t* __restrict__ packed) {
+  const float* my = ws;
+  const float* mx = ws + I;
+  const float* rx = ws + I + O;
+  const float* ry = ws + I + 2 * O;
+  const bool rows_first = I > O;
+  const int64_t total = OM ? (int64_t)O * (I / 2) : (int64_t)I * (O / 2);
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    uint32_t lo, hi;
+    if (OM) {
+      const int j = (int)(e / (I / 2)), a = (int)(e % (I / 2));
+      lo = mm4_q<TW, OM>(w, 2 * a, j, I, Or, rows_first, my, mx, rx, ry);
+      hi = mm4_q<TW, OM>(w, 2 * a + 1, j, I, Or, rows_first, my, mx, rx, ry);
+    } else {
+      const int i = (int)(e / (O / 2)), b = (int)(e % (O / 2));
+      lo = mm4_q<TW, OM>(w, i, 2 * b, I, Or, rows_first, my, mx, rx, ry);
+      hi = mm4_q<TW, OM>(w, i, 2 * b + 1, I, Or, rows_first, my, mx, rx, ry);
+    }
+    packed[e] = (uint8_t)(lo | (hi << 4));
+  }
+}
+
+// mx, rx/4 over the O padded columns; my, ry/4 over the I rows
+template <typename TW>
+__global__ void mm4_meta(int I, int O, const float* ws, TW* mx_o, TW* rx_o, TW* my_o, TW* ry_o) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < O) {
+    mx_o[t] = from_f32<TW>(ws[I + t]);
+    rx_o[t] = from_f32<TW>(ws[I + O + t] / 4.0f);
+  }
+  if (t < I) {
+    my_o[t] = from_f32<TW>(ws[t]);
+    ry_o[t] = from_f32<TW>(ws[I + 2 * O + t] / 4.0f);
+  }
+}
+
+template <typename TW, bool OM>
+static int mm4_pack_run(const TW* w, int I, int Or, uint8_t* packed, void* mx, void* rx, void* my, void* ry,
+                        float* ws, hipStream_t s) {
+  const int Mp = Or + (Or & 1);
+  mm8_stats<TW, OM>(w, I, Mp, Or, ws, s);
+  hipLaunchKernelGGL((mm4_quantize<TW, OM>), dim3(4096), dim3(256), 0, s, w, I, Mp, Or, ws, packed);
+  const int n = I > Mp ? I : Mp;
+  hipLaunchKernelGGL((mm4_meta<TW>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, I, Mp, ws, (TW*)mx, (TW*)rx,
+                     (TW*)my, (TW*)ry);
+  return check_launch("mm4_pack");
 }
 
 }  // namespace rwkv7mi
@@ -455,6 +534,69 @@ extern "C" int rwkv7mi_mm8_pack(const void* weight, int64_t I, int64_t O, int w_
 extern "C" int rwkv7mi_mm8_pack_t(const void* weight, int64_t I, int64_t O, int w_dtype, uint8_t* w_t,
                                   void* mx, void* rx, void* my, void* ry, float* workspace, void* stream) {
   return mm8_pack_entry(weight, I, O, w_dtype, w_t, mx, rx, my, ry, workspace, stream, true);
+}
+
+static int mm4_pack_entry(const void* weight, int64_t I, int64_t O, int w_dtype, uint8_t* packed, void* mx,
+                          void* rx, void* my, void* ry, float* workspace, void* stream, bool out_major) {
+  if (I <= 0 || O <= 0 || I > INT32_MAX / 2 || O > INT32_MAX / 2) return fail(RWKV7MI_EINVAL, "mm4_pack: bad shape");
+  if (out_major && (I & 1)) return fail(RWKV7MI_EINVAL, "mm4_pack_t: in_features must be even");
+  if (!weight || !packed || !mx || !rx || !my || !ry || !workspace)
+    return fail(RWKV7MI_EINVAL, "mm4_pack: null pointer");
+  hipStream_t s = as_stream(stream);
+  return dispatch_dtype(w_dtype, [&](auto tw) {
+    using TW = decltype(tw);
+    const TW* w = (const TW*)weight;
+    return out_major ? mm4_pack_run<TW, true>(w, (int)I, (int)O, packed, mx, rx, my, ry, workspace, s)
+                     : mm4_pack_run<TW, false>(w, (int)I, (int)O, packed, mx, rx, my, ry, workspace, s);
+  });
+}
+
+extern "C" int rwkv7mi_mm4_pack(const void* weight, int64_t I, int64_t O, int w_dtype, uint8_t* packed, void* mx,
+                                void* rx_s, void* my, void* ry_s, float* workspace, void* stream) {
+  return mm4_pack_entry(weight, I, O, w_dtype, packed, mx, rx_s, my, ry_s, workspace, stream, false);
+}
+
+extern "C" int rwkv7mi_mm4_pack_t(const void* weight, int64_t I, int64_t O, int w_dtype, uint8_t* packed_t,
+                                  void* mx, void* rx_s, void* my, void* ry_s, float* workspace, void* stream) {
+  return mm4_pack_entry(weight, I, O, w_dtype, packed_t, mx, rx_s, my, ry_s, workspace, stream, true);
+}
+
+namespace rwkv7mi {
+// out[i, o] = (u4[i, o] + 0.5) * ry[i] * rx[o] + my[i] + mx[o] from the reference
+// layout [I, Mp/2], fp32 math, one rounding
+template <typename TM, typename TO>
+__global__ __launch_bounds__(256) void mm4_dequant_kernel(const uint8_t* __restrict__ p, const TM* __restrict__ mx,
+                                                          const TM* __restrict__ rx, const TM* __restrict__ my,
+                                                          const TM* __restrict__ ry, TO* __restrict__ out, int I,
+                                                          int O) {
+  const int Mh = (O + 1) / 2;
+  for (int i = blockIdx.y; i < I; i += gridDim.y) {
+    const float ryi = to_f32(ry[i]), myi = to_f32(my[i]);
+    for (int o = blockIdx.x * 256 + threadIdx.x; o < O; o += gridDim.x * 256) {
+      const uint32_t b = p[(int64_t)i * Mh + o / 2];
+      const float u = (float)((o & 1) ? (b >> 4) : (b & 15u)) + 0.5f;
+      out[(int64_t)i * O + o] = from_f32<TO>(u * ryi * to_f32(rx[o]) + myi + to_f32(mx[o]));
+    }
+  }
+}
+}  // namespace rwkv7mi
+
+extern "C" int rwkv7mi_mm4_dequant(const uint8_t* packed, const void* mx, const void* rx_s, const void* my,
+                                   const void* ry_s, void* out, int64_t I, int64_t O, int meta_dtype, int out_dtype,
+                                   void* stream) {
+  if (I <= 0 || O <= 0 || I > INT32_MAX || O > INT32_MAX) return fail(RWKV7MI_EINVAL, "mm4_dequant: bad shape");
+  if (!packed || !mx || !rx_s || !my || !ry_s || !out) return fail(RWKV7MI_EINVAL, "mm4_dequant: null pointer");
+  return dispatch_dtype(meta_dtype, [&](auto tm) {
+    using TM = decltype(tm);
+    return dispatch_dtype(out_dtype, [&](auto to) {
+      using TO = decltype(to);
+      const int gx = (int)std::min<int64_t>((O + 255) / 256, 64);
+      hipLaunchKernelGGL((mm4_dequant_kernel<TM, TO>), dim3(gx, (unsigned)std::min<int64_t>(I, 32768)), dim3(256), 0,
+                         as_stream(stream), packed, (const TM*)mx, (const TM*)rx_s, (const TM*)my, (const TM*)ry_s,
+                         (TO*)out, (int)I, (int)O);
+      return check_launch("mm4_dequant_kernel");
+    });
+  });
 }
 
 namespace rwkv7mi {

@@ -11,8 +11,8 @@
 // so a workgroup owns 16 output columns and ALL of K: no split-K partials, no
 // cross-workgroup ordering, deterministic fixed-order sums.
 //
-// Workgroup = 4 waves, 16 columns, up to 16 batch rows (one MFMA M tile).
-// K is walked in 128-row steps; wave w takes steps w, w+4, ...  In a step,
+// Workgroup = NW (4 or 8) waves, 16 columns, up to 16 batch rows (one MFMA M
+// tile).  K is walked in 128-row steps; wave w takes steps w, w+NW, ...  In a step,
 // lane (n = l%16, kg = l/16) loads two 16-byte runs of column n, rows
 // 16kg..16kg+15 and 64+16kg..64+16kg+15 — a wave reads 16 full 128-byte lines.
 // Each 8-byte half is one B operand of v_mfma_f32_16x16x32_f16 (the MFMA's
@@ -120,14 +120,34 @@ __device__ __forceinline__ f16x8 mm8t_b_operand(uint32_t d0, uint32_t d1) {
   return (f16x8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
-template <typename TA, typename TM, int CSW>
-__global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
-  // CSW: 128-row steps per wave per K-chunk (KC = 512 CSW); the chunk body is
-  // fully unrolled so the load ring needs no loop-carried waits.
+// nibbles of dword d = rows r..r+7 of one column (low nibble first) -> fp16
+// [u + 0.5] x 8 in the order [0,4,1,5,2,6,3,7] (the x' staging for 4-bit
+// weights stores each 8-group in the same order)
+__device__ __forceinline__ f16x8 mm4t_b_operand(uint32_t d) {
+  const f16x2 half_off = {(_Float16)-1023.5f, (_Float16)-1023.5f};
+  f16x2 p0 = __builtin_bit_cast(f16x2, (d & 0x000f000fu) | 0x64006400u) + half_off;
+  f16x2 p1 = __builtin_bit_cast(f16x2, ((d >> 4) & 0x000f000fu) | 0x64006400u) + half_off;
+  f16x2 p2 = __builtin_bit_cast(f16x2, ((d >> 8) & 0x000f000fu) | 0x64006400u) + half_off;
+  f16x2 p3 = __builtin_bit_cast(f16x2, ((d >> 12) & 0x000f000fu) | 0x64006400u) + half_off;
+  return (f16x8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// BITS = 8: MM8 bytes, a step is 128 K rows; BITS = 4: MM4 nibbles packed in
+// pairs along K (low nibble = even row), a step is 256 K rows.  Either way a
+// step is two 16-byte loads per lane, 128 bytes of each of the 16 columns.
+template <typename TA, typename TM, int NW, int CSW, int BITS>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B) {
+  // NW waves per workgroup; CSW: steps per wave per K-chunk (KC = RS NW CSW
+  // rows).  The chunk body is fully unrolled so the load ring needs no
+  // loop-carried waits.
+  constexpr int NT = 64 * NW;
   constexpr int DEPTH = CSW < 8 ? CSW : 8;
+  constexpr int RS = BITS == 8 ? 128 : 256;  // K rows per step
+  constexpr int NB = BITS == 8 ? 4 : 8;      // B operands (8 rows each) per step
   const Mm8tProb& P = B.p[blockIdx.y];
   const int I = B.I, O = B.O;
-  constexpr int KC = 512 * CSW;
+  const int bcol = BITS == 8 ? I : I / 2;  // bytes per column
+  constexpr int KC = RS * NW * CSW;
   const int row0 = blockIdx.z * 16;
   const int nrows = min(16, B.rows - row0);
   const int ngroups = (O + MM8T_COLS - 1) / MM8T_COLS;
@@ -136,8 +156,8 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
   extern __shared__ __align__(16) char smem[];
   _Float16* xh = reinterpret_cast<_Float16*>(smem);
   _Float16* xl = xh + nrows * XS;
-  __shared__ float red[4][16][17];
-  __shared__ float wsum[4][2];
+  __shared__ float red[NW][16][17];
+  __shared__ float wsum[NW][2];
   __shared__ float rsum[16][2];
 
   const int tid = threadIdx.x;
@@ -151,20 +171,20 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
   auto group_rsrc = [&](int g) {
     const int c0 = g * MM8T_COLS;
     const int nc = g < ngroups ? min(MM8T_COLS, O - c0) : 0;
-    return mm8t_rsrc(P.w + (int64_t)(g < ngroups ? c0 : 0) * I, (uint32_t)nc * (uint32_t)I);
+    return mm8t_rsrc(P.w + (int64_t)(g < ngroups ? c0 : 0) * bcol, (uint32_t)nc * (uint32_t)bcol);
   };
   const __amdgpu_buffer_rsrc_t xr =
       mm8t_rsrc(reinterpret_cast<const TA*>(P.x) + (int64_t)row0 * I, (uint32_t)(nrows * I * sizeof(TA)));
   const __amdgpu_buffer_rsrc_t ryr = mm8t_rsrc(P.ry, (uint32_t)(I * sizeof(TM)));
   const __amdgpu_buffer_rsrc_t myr = mm8t_rsrc(P.my, (uint32_t)(I * sizeof(TM)));
-  const uint32_t lane_off = (uint32_t)n * (uint32_t)I + 16u * kg;
+  const uint32_t lane_off = (uint32_t)n * (uint32_t)bcol + 16u * kg;
   const int nchunks = (I + KC - 1) / KC;
   const int J = nchunks * CSW;  // steps per wave per column group
 
   // staging: TPR threads per batch row, fixed for the whole kernel
   int rp2 = 1;
   while (rp2 < nrows) rp2 <<= 1;
-  const int TPR = 256 / rp2;
+  const int TPR = NT / rp2;
   const int sr = tid / TPR;
   const int su = tid % TPR;
   constexpr int NQ = KC >> 3;              // 8-element groups per chunk row
@@ -198,7 +218,10 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
       f16x8 hi, lo;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float xp = xv[e] * rv[e];
+        // 4-bit weights pair rows (e, e+4) in their B operands: store x' as
+        // [0,4,1,5,2,6,3,7] so one 16-byte LDS read matches
+        const int src = BITS == 8 ? e : (e >> 1) + 4 * (e & 1);
+        const float xp = xv[src] * rv[src];
         const _Float16 h = (_Float16)xp;
         hi[e] = h;
         lo[e] = (_Float16)(xp - (float)h);
@@ -212,14 +235,15 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
     }
   };
 
-  // Step j of this wave covers K rows 128 (wave + 4j) .. +127 of a group.
-  // Segments at or beyond I (the tail step) read as zeros.
+  // Step j of this wave covers K rows RS (wave + NW j) .. +RS-1 of a group,
+  // bytes 128 (wave + NW j) .. +127 of each column.  Segments at or beyond the
+  // column's bytes (the tail step) read as zeros.
   u32x4 buf[DEPTH][2];
   auto load_step = [&](__amdgpu_buffer_rsrc_t r, int j, u32x4 (&b)[2]) {
-    const int k = 128 * (wave + 4 * j) + 16 * kg;
-    const uint32_t off = lane_off + 128u * (uint32_t)(wave + 4 * j);
-    b[0] = mm8t_ld16(r, k < I ? off : MM8T_OOB);
-    b[1] = mm8t_ld16(r, k + 64 < I ? off + 64u : MM8T_OOB);
+    const int kb = 128 * (wave + NW * j) + 16 * kg;
+    const uint32_t off = lane_off + 128u * (uint32_t)(wave + NW * j);
+    b[0] = mm8t_ld16(r, kb < bcol ? off : MM8T_OOB);
+    b[1] = mm8t_ld16(r, kb + 64 < bcol ? off + 64u : MM8T_OOB);
   };
   int g = blockIdx.x;
   __amdgpu_buffer_rsrc_t wr = group_rsrc(g);             // this group
@@ -240,8 +264,9 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
   __syncthreads();
 
   const int arow = n < nrows ? n : nrows - 1;
-  const _Float16* ah = xh + arow * XS + 16 * kg;
-  const _Float16* al = xl + arow * XS + 16 * kg;
+  // lane kg's 16-byte runs hold rows 16kg.. (8-bit) or 32kg.. (4-bit) of each half step
+  const _Float16* ah = xh + arow * XS + (BITS == 8 ? 16 : 32) * kg;
+  const _Float16* al = xl + arow * XS + (BITS == 8 ? 16 : 32) * kg;
   const TM* rx = reinterpret_cast<const TM*>(P.rx);
   const TM* mx = reinterpret_cast<const TM*>(P.mx);
   const TM* bias = reinterpret_cast<const TM*>(P.bias);
@@ -271,11 +296,19 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
         const int d = jl % DEPTH;
         // convert this step's bytes first, then refill the same ring slot: the
         // slot is dead once converted, so it keeps its registers
-        f16x8 bv[4];
-        bv[0] = mm8t_b_operand(buf[d][0][0], buf[d][0][1]);
-        bv[1] = mm8t_b_operand(buf[d][0][2], buf[d][0][3]);
-        bv[2] = mm8t_b_operand(buf[d][1][0], buf[d][1][1]);
-        bv[3] = mm8t_b_operand(buf[d][1][2], buf[d][1][3]);
+        f16x8 bv[NB];
+        if constexpr (BITS == 8) {
+          bv[0] = mm8t_b_operand(buf[d][0][0], buf[d][0][1]);
+          bv[1] = mm8t_b_operand(buf[d][0][2], buf[d][0][3]);
+          bv[2] = mm8t_b_operand(buf[d][1][0], buf[d][1][1]);
+          bv[3] = mm8t_b_operand(buf[d][1][2], buf[d][1][3]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            bv[q] = mm4t_b_operand(buf[d][0][q]);
+            bv[4 + q] = mm4t_b_operand(buf[d][1][q]);
+          }
+        }
         if (jl + DEPTH < CSW) {
           load_step(wr, c * CSW + jl + DEPTH, buf[d]);
         } else {  // may wrap into the next group's first steps (uniform select)
@@ -285,14 +318,16 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
         // keep the refill here: sunk to the end of the body it would leave the
         // ring empty while the body computes
         __builtin_amdgcn_sched_barrier(0);
-        const int kl = 128 * (wave + 4 * jl);
+        const int kl = RS * (wave + NW * jl);
 #pragma unroll
-        for (int hq = 0; hq < 4; ++hq) {
-          const int off = kl + 64 * (hq >> 1) + 8 * (hq & 1);
+        for (int hq = 0; hq < NB; ++hq) {
+          // 8-bit: operand hq = rows 64(hq/2) + 16kg + 8(hq%2);
+          // 4-bit: operand hq = rows 128(hq/4) + 32kg + 8(hq%4)
+          const int off = BITS == 8 ? kl + 64 * (hq >> 1) + 8 * (hq & 1) : kl + 128 * (hq >> 2) + 8 * (hq & 3);
           const f16x8 a_hi = *reinterpret_cast<const f16x8*>(ah + off);
           const f16x8 a_lo = *reinterpret_cast<const f16x8*>(al + off);
-          acc[hq] = mfma16x16x32(a_hi, bv[hq], acc[hq]);
-          acc[hq] = mfma16x16x32(a_lo, bv[hq], acc[hq]);
+          acc[hq & 3] = mfma16x16x32(a_hi, bv[hq], acc[hq & 3]);
+          acc[hq & 3] = mfma16x16x32(a_lo, bv[hq], acc[hq & 3]);
         }
       }
     }
@@ -339,7 +374,9 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
       const int cn = tid & 15;
       const int o = g * MM8T_COLS + cn;
       if (o < O) {
-        const float s = ((red[0][m][cn] + red[1][m][cn]) + red[2][m][cn]) + red[3][m][cn];
+        float s = red[0][m][cn];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) s += red[q][m][cn];
         float v = ld(rx, o) * s + rsum[m][1] + ld(mx, o) * rsum[m][0];
         if (bias) v += ld(bias, o);
         const int64_t oi = (int64_t)(row0 + m) * O + o;
@@ -357,16 +394,20 @@ __global__ __launch_bounds__(256, 2) void mm8t_kernel(const Mm8tBatch B) {
   }
 }
 
-// x' staging chunk: the largest power-of-two multiple of 1024 rows (at most
-// 16384) whose hi/lo copy for the tile's rows fits the LDS budget, and no
-// longer than I needs.  A grid of at most one workgroup per CU, or a tile of
-// more than four rows (whose staging would otherwise repeat per chunk), uses
-// most of the CU's LDS; the weight ring keeps 64 KB per CU in flight even then.
-static int mm8t_chunk(int64_t rows, int64_t I, int64_t nwg) {
+
+// x' staging chunk: the largest power-of-two multiple of 2 RS NW rows (at
+// most 32 RS NW; RS = K rows per step) whose hi/lo copy for the tile's rows
+// fits the LDS budget, and no longer than I needs.  A grid of at most one
+// workgroup per CU, or a tile of more than four rows (whose staging would
+// otherwise repeat per chunk), uses most of the CU's LDS; the weight ring
+// keeps 64 KB per CU in flight even then.
+static int mm8t_chunk(int64_t rows, int64_t I, int64_t nwg, int nw, int bits) {
   const int64_t nr = rows < 16 ? rows : 16;
+  const int64_t rs = bits == 8 ? 128 : 256;
   const int64_t budget = (nwg <= 256 || nr > 4) ? MM8T_LDS_X_ONE : MM8T_LDS_X;
-  int64_t kc = 1024;
-  while (kc < I && kc < 16384 && nr * (2 * kc + 8) * 4 <= budget) kc *= 2;
+  int64_t kc = 2 * rs * nw;
+  if (nr * (kc + 8) * 4 > budget) return 0;  // not even the smallest chunk fits
+  while (kc < I && kc < rs * nw * 32 && nr * (2 * kc + 8) * 4 <= budget) kc *= 2;
   return (int)kc;
 }
 
@@ -379,17 +420,28 @@ static size_t mm8t_lds(int64_t rows, int KC) {
 
 using namespace rwkv7mi;
 
-template <typename TA, typename TM, int CSW>
+template <typename TA, typename TM, int NW, int CSW, int BITS>
 static int mm8t_go(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
   static bool lds_raised = false;  // dynamic LDS above 64 KB must be enabled once per instance
   if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, CSW>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, NW, CSW, BITS>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, MM8T_LDS_X_ONE + 1024) != hipSuccess)
       return fail(RWKV7MI_ELAUNCH, "mm8t_kernel: cannot raise the dynamic LDS limit");
     lds_raised = true;
   }
-  hipLaunchKernelGGL((mm8t_kernel<TA, TM, CSW>), grid, dim3(256), lds, as_stream(stream), b);
+  hipLaunchKernelGGL((mm8t_kernel<TA, TM, NW, CSW, BITS>), grid, dim3(64 * NW), lds, as_stream(stream), b);
   return check_launch("mm8t_kernel");
+}
+
+template <typename TA, typename TM, int NW, int BITS>
+static int mm8t_go_csw(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
+  switch (b.KC / ((BITS == 8 ? 128 : 256) * NW)) {
+    case 2: return mm8t_go<TA, TM, NW, 2, BITS>(grid, lds, stream, b);
+    case 4: return mm8t_go<TA, TM, NW, 4, BITS>(grid, lds, stream, b);
+    case 8: return mm8t_go<TA, TM, NW, 8, BITS>(grid, lds, stream, b);
+    case 16: return mm8t_go<TA, TM, NW, 16, BITS>(grid, lds, stream, b);
+    default: return mm8t_go<TA, TM, NW, 32, BITS>(grid, lds, stream, b);
+  }
 }
 
 // compute units of the current device (cached per device)
@@ -405,12 +457,14 @@ static int64_t mm8t_cus() {
 }
 
 static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I, int64_t O, int act_dtype,
-                       int meta_dtype, void* stream, const char* who) {
+                       int meta_dtype, void* stream, const char* who, int bits = 8) {
   const std::string w(who);
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
   if (rows < 0 || I <= 0 || O <= 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
   if (rows == 0) return RWKV7MI_OK;
-  if (I % 16) return fail(RWKV7MI_EINVAL, w + ": in_features must be a multiple of 16");
+  if (I % (bits == 8 ? 16 : 32))
+    return fail(RWKV7MI_EINVAL, w + (bits == 8 ? ": in_features must be a multiple of 16"
+                                               : ": in_features must be a multiple of 32"));
   // buffer descriptors cover 16 columns x I bytes and 16 rows x I activations
   if (I > (1 << 24) || O > INT32_MAX || rows > 65535 * 16) return fail(RWKV7MI_EINVAL, w + ": too large");
   if (!valid_dtype(act_dtype) || !valid_dtype(meta_dtype)) return fail(RWKV7MI_EINVAL, w + ": bad dtype");
@@ -430,15 +484,23 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
   b.O = (int)O;
   const int64_t ngroups = (O + MM8T_COLS - 1) / MM8T_COLS;
   const int64_t rtiles = (rows + 15) / 16;
-  b.KC = mm8t_chunk(rows, I, ngroups * nprob * rtiles);
+  const int64_t cus = mm8t_cus();
+  // At most one workgroup per CU: eight waves each, so twice the weight bytes
+  // are in flight per CU.  Otherwise four-wave workgroups, two per CU.
+  int nw = ngroups * nprob * rtiles <= cus ? 8 : 4;
+  b.KC = mm8t_chunk(rows, I, ngroups * nprob * rtiles, nw, bits);
+  if (!b.KC && nw == 8) {
+    nw = 4;
+    b.KC = mm8t_chunk(rows, I, ngroups * nprob * rtiles, nw, bits);
+  }
+  if (!b.KC) return fail(RWKV7MI_EINVAL, w + ": x' staging does not fit in LDS");
   const size_t lds = mm8t_lds(rows, b.KC);
   // With x' in one LDS chunk, workgroups loop over column groups: as many as
-  // stay resident (two per CU at this kernel's register use and LDS size),
-  // split between the problems and row tiles.
+  // stay resident, split between the problems and row tiles.
   int64_t gx = ngroups;
-  if (b.KC >= I) {
+  if (b.KC >= I && nw == 4) {
     const int64_t per_cu = lds <= MM8T_LDS_X ? 2 : 1;
-    const int64_t slots = mm8t_cus() * per_cu / (nprob * rtiles);
+    const int64_t slots = cus * per_cu / (nprob * rtiles);
     if (slots >= 1 && slots < gx) gx = slots;
   }
   dim3 grid((unsigned)gx, (unsigned)nprob, (unsigned)rtiles);
@@ -446,13 +508,9 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
     using TA = decltype(ta);
     return dispatch_dtype(meta_dtype, [&](auto tm) {
       using TM = decltype(tm);
-      switch (b.KC >> 9) {
-        case 2: return mm8t_go<TA, TM, 2>(grid, lds, stream, b);
-        case 4: return mm8t_go<TA, TM, 4>(grid, lds, stream, b);
-        case 8: return mm8t_go<TA, TM, 8>(grid, lds, stream, b);
-        case 16: return mm8t_go<TA, TM, 16>(grid, lds, stream, b);
-        default: return mm8t_go<TA, TM, 32>(grid, lds, stream, b);
-      }
+      if (bits == 4)
+        return nw == 8 ? mm8t_go_csw<TA, TM, 8, 4>(grid, lds, stream, b) : mm8t_go_csw<TA, TM, 4, 4>(grid, lds, stream, b);
+      return nw == 8 ? mm8t_go_csw<TA, TM, 8, 8>(grid, lds, stream, b) : mm8t_go_csw<TA, TM, 4, 8>(grid, lds, stream, b);
     });
   });
 }
@@ -479,6 +537,14 @@ extern "C" int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x, const 
     p[i] = Mm8tProb{x[i], w_t[i], mx[i], rx[i], my[i], ry[i], bias ? bias[i] : nullptr,
                     residual ? residual[i] : nullptr, y[i], epilogue[i]};
   return mm8t_launch(nprob, p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul_multi");
+}
+
+extern "C" int rwkv7mi_mm4t_matmul(const void* x, const uint8_t* w_t, const void* mx, const void* rx_s,
+                                   const void* my, const void* ry_s, const void* bias, const void* residual,
+                                   void* y, int64_t rows, int64_t I, int64_t O, int epilogue, int act_dtype,
+                                   int meta_dtype, void* stream) {
+  Mm8tProb p{x, w_t, mx, rx_s, my, ry_s, bias, residual, y, epilogue};
+  return mm8t_launch(1, &p, rows, I, O, act_dtype, meta_dtype, stream, "mm4t_matmul", 4);
 }
 
 namespace rwkv7mi {

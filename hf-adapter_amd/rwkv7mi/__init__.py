@@ -15,6 +15,7 @@ from .fused_recurrent_update import (
 )
 from .self_chunk_rwkv7 import dplr_chunk_scan, self_chunk_rwkv7
 from .native_quant_mm8 import MM8Linear, mm8_matmul, mm8_matmul_triton, quantize_mm8, quantize_model_mm8
+from .native_quant_mm4 import MM4Linear, dequantize_mm4, mm4_matmul, quantize_mm4, quantize_model_mm4
 from .sm70_quant import quantize_w4_groupwise, w4_groupwise_linear
 
 __all__ = [
@@ -29,6 +30,11 @@ __all__ = [
     "mm8_matmul_triton",
     "MM8Linear",
     "quantize_model_mm8",
+    "quantize_mm4",
+    "dequantize_mm4",
+    "mm4_matmul",
+    "MM4Linear",
+    "quantize_model_mm4",
     "quantize_w4_groupwise",
     "w4_groupwise_linear",
 ]

@@ -330,6 +330,8 @@ class NativeRWKV7ForCausalLM:
         self.config = cfg = config
         self.device = torch.device(device)
         self.dtype = dtype
+        # run the decode LoRA projections on a second stream beside R/K/V
+        self.lora_side_stream = False
         dev = self.device
 
         def get(name):
@@ -464,14 +466,27 @@ class NativeRWKV7ForCausalLM:
         state, xpa, xpf, v_first = cache
         H, N, eps = cfg.num_heads, cfg.head_dim, cfg.norm_eps
         mixb, rkv, lora, prep = bufs["mix"], bufs["rkv"], bufs["lora"], bufs["prep"]
+        main = torch.cuda.current_stream(x.device)
+        side, ev_in, ev_out = self._side(x.device) if self.lora_side_stream else (None, None, None)
         for L in self.layers:
             i = L.idx
             fused_attn_norm_mix6_decode(x, xpa[i], L.ln1[0], L.ln1[1], *L.mix, eps=eps, out=mixb,
                                         pre_norm_weight=L.pre[0] if L.pre else None,
                                         pre_norm_bias=L.pre[1] if L.pre else None)
             xr, xw, xk, xv, xa, xg = (mixb[q] for q in range(6))
-            QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
-            self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
+            if self.lora_side_stream:
+                # the LoRA projections depend only on the mixes: a second stream
+                # (a parallel branch of the captured graph) runs them beside R/K/V
+                ev_in.record(main)
+                side.wait_event(ev_in)
+                with torch.cuda.stream(side):
+                    self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
+                    ev_out.record(side)
+                QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
+                main.wait_event(ev_out)
+            else:
+                QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
+                self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
             fused_recurrent_output_prepare_raw(
                 rkv[0], lora[0], rkv[1], rkv[2], lora[1], state[i], lora[2], L.k_k, L.k_a, L.r_k, L.gn[0],
                 L.gn[1], eps=N * 1e-5, state_out=state[i], out=prep.view(B, H, N),
@@ -483,6 +498,15 @@ class NativeRWKV7ForCausalLM:
         layer_norm(x, self.norm[0], self.norm[1], eps, out=bufs["h"])
         self.lm_head.apply(bufs["h"], logits)
         return logits
+
+    def _side(self, device):
+        """Second stream (default priority) and its two fork/join events, per device."""
+        key = torch.device(device).index
+        if not hasattr(self, "_side_streams"):
+            self._side_streams = {}
+        if key not in self._side_streams:
+            self._side_streams[key] = (torch.cuda.Stream(device=device), torch.cuda.Event(), torch.cuda.Event())
+        return self._side_streams[key]
 
     # ------------------------------------------------------------- prefill
     def prefill_(self, input_ids: torch.Tensor, cache: NativeRWKV7Cache) -> torch.Tensor:

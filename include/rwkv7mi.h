@@ -199,6 +199,42 @@ int rwkv7mi_mm8t_dequant(const uint8_t* w_t, const void* mx, const void* rx,
                          const void* my, const void* ry, void* out, int64_t I,
                          int64_t O, int meta_dtype, int out_dtype, void* stream);
 
+/* ------------------------------------------------------------ MM4 affine */
+
+/* Device packer of the 4-bit affine format, quantize_mm4
+ * (rwkv7_hf/native_quant_mm4.py:77-105): weight [I,O] (= Linear.weight.T) in
+ * w_dtype; O is padded to even Mp with a zero column as the reference does;
+ * outputs packed [I, Mp/2] (byte = u4[i,2b] | u4[i,2b+1] << 4), mx, rx_s [Mp],
+ * my, ry_s [I] in w_dtype (rx/4, ry/4).  Workspace 2*I + 2*Mp floats. */
+int rwkv7mi_mm4_pack(const void* weight, int64_t I, int64_t O, int w_dtype,
+                     uint8_t* packed, void* mx, void* rx_s, void* my,
+                     void* ry_s, float* workspace, void* stream);
+
+/* Same values from Linear.weight [O,I], packed along the inputs for the fused
+ * GEMV: packed_t [Mp, I/2], byte (o, a) = u4[2a,o] | u4[2a+1,o] << 4 (I even;
+ * row O of an odd O holds the pad column's nibbles).
+ * The reference keeps its own per-device buffer layouts (MM4Linear,
+ * rwkv7_hf/native_quant_mm4.py:587-619). */
+int rwkv7mi_mm4_pack_t(const void* weight, int64_t I, int64_t O, int w_dtype,
+                       uint8_t* packed_t, void* mx, void* rx_s, void* my,
+                       void* ry_s, float* workspace, void* stream);
+
+/* y[rows,O] = epilogue(x @ dequant(W)), (u4+0.5)*ry_s*rx_s + my + mx with fp32
+ * accumulation, over packed_t.  Replaces mm4_gemv_triton / mm4_matmul_triton /
+ * MM4Linear.forward (rwkv7_hf/native_quant_mm4.py:545-578, :621-660).
+ * I % 32 == 0; x, packed_t, my, ry_s 16-byte aligned; y may alias residual. */
+int rwkv7mi_mm4t_matmul(const void* x, const uint8_t* packed_t, const void* mx,
+                        const void* rx_s, const void* my, const void* ry_s,
+                        const void* bias, const void* residual, void* y,
+                        int64_t rows, int64_t I, int64_t O, int epilogue,
+                        int act_dtype, int meta_dtype, void* stream);
+
+/* dequantize_mm4 (rwkv7_hf/native_quant_mm4.py:108-122) from the reference
+ * layout packed [I, ceil(O/2)] into out [I, O] (fp32 math, one rounding). */
+int rwkv7mi_mm4_dequant(const uint8_t* packed, const void* mx, const void* rx_s,
+                        const void* my, const void* ry_s, void* out, int64_t I,
+                        int64_t O, int meta_dtype, int out_dtype, void* stream);
+
 /* ------------------------------------------------------------------ LoRA */
 
 /* Bytes of workspace rwkv7mi_lora_multi needs (fp32 split-K partials). */
