@@ -1,0 +1,71 @@
+"""Write the model golden vectors tests/golden/model_<name>.npz.
+
+What they pin: the end-to-end composition of the RWKV-7 decode path (logits
+and greedy ids), which no closed form or component check fixes.  The vectors
+come from the reference implementation itself (rwkv-rs/hf-adapter 0.8.1,
+``rwkv7_hf.native_model.NativeRWKV7ForCausalLM``) run on the CPU in fp32 in
+the build container, where the reference is available read-only at
+/root/reference; it is imported here and nowhere else, and never shipped.
+
+Weights are this build's name-keyed random init (rwkv7mi.model.random_weights,
+seed 0), loaded into the reference model by parameter name; token ids are
+uniform with seed 0.  Each fixture holds the prompt ids, the reference's
+last-position logits after the prompt, and its greedy continuation.
+
+Run: python tests/golden/make_model_golden.py [names...]   (tiny, c1)
+"""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+REPO = HERE.parent.parent
+sys.path.insert(0, str(REPO / "hf-adapter_amd"))
+
+CONFIGS = {
+    # small enough for the CPU test suite
+    "tiny": dict(vocab_size=512, hidden_size=128, num_hidden_layers=2, intermediate_size=256,
+                 decay_low_rank_dim=32, a_low_rank_dim=32, gate_low_rank_dim=64, v_low_rank_dim=32,
+                 prompt=24, steps=8),
+    # the 0.1B architecture (short prompt, fp32)
+    "c1": dict(vocab_size=65536, hidden_size=768, num_hidden_layers=12, intermediate_size=3072,
+               decay_low_rank_dim=64, a_low_rank_dim=64, gate_low_rank_dim=128, v_low_rank_dim=32,
+               prompt=32, steps=8),
+}
+
+
+def main(names):
+    sys.path.insert(0, "/root/reference")
+    from rwkv7_hf.model_config import NativeRWKV7Config as RefConfig
+    from rwkv7_hf.native_model import NativeRWKV7ForCausalLM as RefModel
+    from rwkv7mi.model import NativeRWKV7Config, random_weights
+
+    torch.manual_seed(0)
+    for name in names:
+        c = dict(CONFIGS[name])
+        prompt, steps = c.pop("prompt"), c.pop("steps")
+        ours = NativeRWKV7Config(**c)
+        w = random_weights(ours, seed=0, device="cpu", dtype=torch.float32)
+        ref = RefModel(RefConfig(head_dim=64, **c)).eval().float()
+        missing, unexpected = ref.load_state_dict(w, strict=False)
+        missing = [k for k in missing if k in w or not k.endswith(("_buffer",))]
+        if unexpected or [k for k in missing if not k.startswith("model.layers") and "lora" not in k]:
+            print(f"{name}: missing {missing[:8]}, unexpected {unexpected[:8]}")
+        loaded = {k: v for k, v in ref.state_dict().items()}
+        for k, v in w.items():
+            assert torch.equal(loaded[k].float(), v.float()), k
+        ids = torch.tensor(np.random.default_rng(0).integers(0, c["vocab_size"], (1, prompt)), dtype=torch.long)
+        with torch.no_grad():
+            logits = ref(input_ids=ids).logits[0, -1].float().numpy()
+            gen = ref.generate(ids, max_new_tokens=steps, do_sample=False)
+        out = HERE / f"model_{name}.npz"
+        np.savez_compressed(out, ids=ids.numpy(), logits=logits, greedy=gen[0, prompt:].numpy())
+        print(f"wrote {out}: greedy {gen[0, prompt:].tolist()}")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:] or ["tiny", "c1"])

@@ -44,6 +44,8 @@ def test_pack_outmajor_equals_rowmajor(oracle, OI, dtype):
 
 
 SHAPES = [(4096, 4096), (4096, 1024), (16384, 512), (144, 40), (1024, 65), (16, 16)]
+# the RWKV-7 1.5B projection and head shapes at batch 1, 8, 32
+C3 = [(2048, 2048), (2048, 8192), (8192, 2048), (2048, 65536)]
 
 
 @pytest.mark.parametrize("IO", SHAPES)
@@ -64,6 +66,12 @@ def test_mm8t_matmul_matches_oracle(oracle, IO, rows):
     err = _rel_err(_np(y).astype(np.float64), ref)
     assert err <= 2e-3, err
     assert torch.equal(y, y2), "repeated calls must be bit-identical"
+
+
+@pytest.mark.parametrize("IO", C3)
+@pytest.mark.parametrize("rows", [1, 8, 32])
+def test_mm8t_c3_shapes(oracle, IO, rows):
+    test_mm8t_matmul_matches_oracle(oracle, IO, rows)
 
 
 @pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])

@@ -137,3 +137,30 @@ def test_cache_select_and_repeat():
     rep = cache.clone()
     rep.batch_repeat_interleave(2)
     assert rep.get_batch_size() == 6 and torch.equal(rep._state[0][1], cache._state[0][0])
+
+
+@pytest.mark.parametrize("name,dtype", [("tiny", torch.float32), ("tiny", torch.float16), ("c1", torch.float32)])
+def test_model_matches_reference_golden(name, dtype):
+    """Prefill + greedy decode against the reference model's own logits and
+    greedy ids (tests/golden/make_model_golden.py).  fp32: logits max-abs
+    <= 1e-3 x max|logit| and ids bit-exact; fp16: 2e-2 x max|logit| and ids
+    bit-exact wherever the reference's top-2 margin exceeds that tolerance."""
+    from rwkv7mi.model import NativeRWKV7ForCausalLM
+    from test_oracle_model import golden_case
+
+    cfg, w, g = golden_case(name)
+    model = NativeRWKV7ForCausalLM(cfg, w, device="cuda", dtype=dtype)
+    ids = torch.tensor(g["ids"], device="cuda")
+    logits, _ = model(ids)
+    out = model.generate(ids, len(g["greedy"])).cpu().numpy()[0, ids.shape[1]:]
+    torch.cuda.synchronize()
+    ref = g["logits"].astype(np.float64)
+    got = logits[0, -1].double().cpu().numpy()
+    tol = 1e-3 if dtype == torch.float32 else LOGIT_REL
+    assert np.abs(got - ref).max() <= tol * np.abs(ref).max()
+    if dtype == torch.float32:
+        np.testing.assert_array_equal(out, g["greedy"])
+    else:
+        top2 = np.sort(ref)[-2:]
+        if top2[1] - top2[0] > 2 * tol * np.abs(ref).max():
+            assert out[0] == g["greedy"][0]
