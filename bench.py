@@ -193,51 +193,64 @@ def run_decode(batches=(1, 8), steps=64, warmup=5, log=print):
         res[B] = {"tok_s": B / (ms / 1e3), "ms": ms, "wall_s": wall, "bytes": nbytes, "gbs": gbs,
                   "frac": gbs / HBM_PEAK_GBS}
         log(f"bench: decode bsz {B}: {ms:.3f} ms/step, {B / (ms / 1e3):.1f} tok/s, {gbs:.0f} GB/s")
-    # MM8 GEMV roofline: events around every MM8 launch of eager bsz-1 steps.  A
-    # spin kernel queued first keeps the GPU busy while Python enqueues the step,
-    # so the kernels run back to back and each event pair brackets GPU time only.
+    # MM8 GEMV roofline: the MM8 launches of one bsz-1 decode step (the same
+    # modules, shapes and buffers), captured alone in a hipGraph and replayed
+    # back to back between two HIP events on the launch stream; the average
+    # launch duration is the elapsed time over all launches.
     B = 1
     cache = model.new_cache(B)
     toks = torch.zeros(B, dtype=torch.long, device="cuda")
     logits = torch.empty(B, cfg.vocab_size, device="cuda", dtype=torch.float16)
     bufs = model._decode_buffers(B)
-    model.decode_step_(toks, cache, logits, bufs)
-    records = []
+    calls, nbytes = [], []
     orig_apply, orig_group = QuantLinear.apply, QuantLinear.apply_group
 
     def mm8_bytes(lin, rows):
         i, o = lin.in_features, lin.out_features
         return o * i + 2 * (i + o) * 2 + rows * (i + o) * 2
 
-    def bracket(nbytes, call):
-        s = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        r = call()
-        e1.record(s)
-        records.append((e0, e1, nbytes))
-        return r
+    def rec_apply(self, x2, out, **kw):
+        calls.append(lambda: orig_apply(self, x2, out, **kw))
+        nbytes.append(mm8_bytes(self, int(x2.shape[0])))
+        return orig_apply(self, x2, out, **kw)
 
-    def timed_apply(self, x2, out, **kw):
-        return bracket(mm8_bytes(self, int(x2.shape[0])), lambda: orig_apply(self, x2, out, **kw))
+    def rec_group(lins, xs, outs):
+        calls.append(lambda: orig_group(lins, xs, outs))
+        nbytes.append(sum(mm8_bytes(l, int(x.shape[0])) for l, x in zip(lins, xs)))
+        return orig_group(lins, xs, outs)
 
-    def timed_group(lins, xs, outs):
-        nb = sum(mm8_bytes(l, int(x.shape[0])) for l, x in zip(lins, xs))
-        return bracket(nb, lambda: orig_group(lins, xs, outs))
-
-    QuantLinear.apply = timed_apply
-    QuantLinear.apply_group = staticmethod(timed_group)
+    QuantLinear.apply = rec_apply
+    QuantLinear.apply_group = staticmethod(rec_group)
     try:
-        for _ in range(3):
-            torch.cuda._sleep(50_000_000)
-            model.decode_step_(toks, cache, logits, bufs)
-        torch.cuda.synchronize()
+        model.decode_step_(toks, cache, logits, bufs)
     finally:
         QuantLinear.apply, QuantLinear.apply_group = orig_apply, staticmethod(orig_group)
-    tot_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in records)
-    tot_b = sum(b for _, _, b in records)
-    res["mm8_kernel"] = {"launches": len(records), "avg_us": 1e3 * tot_ms / len(records),
-                         "bytes_per_launch": tot_b / len(records), "gbs": tot_b / (tot_ms / 1e3) / 1e9}
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for c in calls:
+            c()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in calls:
+            c()
+    reps = 20
+    graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    tot_ms = e0.elapsed_time(e1)
+    n = reps * len(calls)
+    tot_b = reps * sum(nbytes)
+    res["mm8_kernel"] = {"launches": len(calls), "avg_us": 1e3 * tot_ms / n,
+                         "bytes_per_launch": tot_b / n, "gbs": tot_b / (tot_ms / 1e3) / 1e9}
+    del graph
     return res
 
 
@@ -278,16 +291,88 @@ def cpu_decode_baseline(min_seconds=10.0):
                       f"per-layer time scaled to 32 layers"}
 
 
+TRAFFIC_JSON = Path(__file__).resolve().parent / "profiles" / "traffic.json"
+
+
+def _traffic():
+    """HBM bytes per MM8 launch measured by the counter runs (profiles/traffic.json), or None."""
+    try:
+        return json.loads(TRAFFIC_JSON.read_text())["traffic_bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        return None
+COPY_BYTES = 256 << 20
+
+
+def run_traffic():
+    """Kernels for the HBM-traffic counters: two eager bsz-1 decode steps of the
+    7.2B MM8 model (the second is the measured one) and one elementwise copy of
+    COPY_BYTES (read and written once) that calibrates FETCH_SIZE / WRITE_SIZE.
+    Run under ``rocprofv3 --pmc FETCH_SIZE`` and then ``--pmc WRITE_SIZE``."""
+    import torch
+    from rwkv7mi.model import NativeRWKV7ForCausalLM
+
+    cfg = config_7p2b()
+    model = NativeRWKV7ForCausalLM.from_random(cfg, seed=0, device="cuda", dtype=torch.float16)
+    cache = model.new_cache(1)
+    toks = torch.zeros(1, dtype=torch.long, device="cuda")
+    logits = torch.empty(1, cfg.vocab_size, device="cuda", dtype=torch.float16)
+    bufs = model._decode_buffers(1)
+    for _ in range(2):
+        model.decode_step_(toks, cache, logits, bufs)
+    src = torch.ones(COPY_BYTES // 2, device="cuda", dtype=torch.float16)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print("bench: traffic workload done (2 decode steps + calibration copy)", file=sys.stderr, flush=True)
+
+
+def _counter_rows(path):
+    import csv
+
+    with open(path) as f:
+        return list(csv.DictReader(f))
+
+
+def summarize_traffic(fetch_csv, write_csv, out=TRAFFIC_JSON):
+    """Per-launch HBM bytes of the decode step's MM8 GEMV launches from the two
+    counter runs, scaled by the copy kernel's known bytes; writes ``out``."""
+    def per_dispatch(path, counter):
+        rows = [r for r in _counter_rows(path) if r.get("Counter_Name") == counter]
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        mm8 = [float(r["Counter_Value"]) * 1024 for r in rows if "mm8t_kernel" in r["Kernel_Name"]]
+        copy = [float(r["Counter_Value"]) * 1024 for r in rows if "neg" in r["Kernel_Name"]]
+        half = len(mm8) // 2  # two decode steps: keep the second
+        return mm8[half:], copy[-1]
+    f_mm8, f_copy = per_dispatch(fetch_csv, "FETCH_SIZE")
+    w_mm8, w_copy = per_dispatch(write_csv, "WRITE_SIZE")
+    ff, fw = COPY_BYTES / f_copy, COPY_BYTES / w_copy
+    n = len(f_mm8)
+    traffic = (sum(f_mm8) * ff + sum(w_mm8) * fw) / n
+    res = {"kernel": "mm8t_kernel", "launches_per_step": n, "traffic_bytes_per_launch": round(traffic),
+           "fetch_bytes_per_launch": round(sum(f_mm8) * ff / n), "write_bytes_per_launch": round(sum(w_mm8) * fw / n),
+           "fetch_scale": ff, "write_scale": fw, "copy_bytes": COPY_BYTES,
+           "source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of bench.py --workload traffic"}
+    Path(out).parent.mkdir(parents=True, exist_ok=True)
+    Path(out).write_text(json.dumps(res, indent=1) + "\n")
+    print(json.dumps(res))
+    return res
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["all", "decode", "scan"], default="all")
+    ap.add_argument("--workload", choices=["all", "decode", "scan", "traffic"], default="all")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write profiles/traffic.json from two rocprofv3 --pmc counter CSVs and exit")
     ap.add_argument("--heads", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--batches", default="1,8", help="decode batch sizes (the first is the headline)")
     args = ap.parse_args(argv)
+    if args.summarize_traffic:
+        summarize_traffic(*args.summarize_traffic)
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is described in DESIGN.md and not run.", file=sys.stderr)
@@ -297,6 +382,9 @@ def main(argv=None):
 
     torch.cuda.set_device(0)
     log = lambda m: print(m, file=sys.stderr, flush=True)
+    if args.workload == "traffic":
+        run_traffic()
+        return 0
     out: dict = {}
     scan = dec = None
     if args.workload in ("all", "scan"):
@@ -319,9 +407,9 @@ def main(argv=None):
                        "hidden": 4096, "heads": 64, "ffn": 16384, "vocab": 65536, "global_batch": 1,
                        "parallelism": "single-gpu"},
             "roofline": {"bound": "hbm", "achieved": round(mk["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(mk["gbs"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "mm8t_kernel",
+                         "frac": round(mk["gbs"] / HBM_PEAK_GBS, 4), "traffic": _traffic(), "kernel": "mm8t_kernel",
                          "avg_launch_us": round(mk["avg_us"], 3),
-                         "bytes_per_launch": round(mk["bytes_per_launch"]), "launches_per_step": mk["launches"] // 3},
+                         "bytes_per_launch": round(mk["bytes_per_launch"]), "launches_per_step": mk["launches"]},
             "decode": {str(b): {"tok_s": round(dec[b]["tok_s"], 2), "ms_per_step": round(dec[b]["ms"], 4),
                                 "step_bytes": dec[b]["bytes"], "step_gbs": round(dec[b]["gbs"], 1),
                                 "step_roofline_frac": round(dec[b]["frac"], 4)}
