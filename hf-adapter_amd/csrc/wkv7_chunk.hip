@@ -3,108 +3,107 @@
 // Recurrence (native V x K state, rwkv7_hf/fused_recurrent_update.py:757-783):
 //   S_t = S_{t-1} (diag(w_t) + alpha_t beta_t^T) + v_t k_t^T,  y_t = S_t r_t,
 //   alpha = -kk, beta = kk * a.
-// Per chunk, with g_t = sum_{s<=t} log2 w_s (per key channel j, 0 at the chunk
-// start), centre c = g_8, p_t = 2^{g_t - c}, q_t = 1/p_t and the gated rows
-//   rc_t = r_t p_t, ac_t = alpha_t p_{t-1}, kc_t = k_t q_t, bc_t = beta_t q_t,
-// the 16x16 causal matrices are
-//   A_qk = tril(rc kc^T), A_qb = tril(rc bc^T), A_ak = tril(ac kc^T, -1), A_ab = tril(ac bc^T, -1)
-// (entry [t,s] = sum_j x_t y_s 2^{g_t - g_s}, every factor kept within 2^+-120),
-// and with S' = S0 diag(2^c), T = (I - A_ab)^{-1}:
-//   U   = (T ac) S'^T + (T A_ak) V              (u_t = S_{t-1} alpha_t)
-//   Y   = rc S'^T + A_qb U + A_qk V
-//   S_C = S0 diag(2^{g_C}) + diag(2^{g_C - c}) (bc^T U + kc^T V)   (as S^T)
-// — the WY form of the reference's chunk algebra (rwkv7_hf/self_chunk_rwkv7.py:85-134,
-// rwkv7_hf/dplr_prefill.py:221-311) arranged so that one set of gated rows
-// serves every product and the per-channel scales fold into the state.
+// Per chunk, with g_t = sum_{s<=t} log2 w_s per key channel (g_{-1} = 0, gC = g_15)
+// and the causal 16 x 16 matrices
+//   A_qk[t,s] = sum_j r_t k_s 2^{g_t - g_s}   (s <= t)     A_qb: beta_s in place of k_s
+//   A_ak[t,s] = sum_j alpha_t k_s 2^{g_{t-1} - g_s} (s < t) A_ab: beta_s in place of k_s
+// and T = (I - A_ab)^{-1}, the chunk is affine in its start state S:
+//   U   = Wa S^T + M V,   Wa = T as,  M = T A_ak,          (u_t = S_{t-1} alpha_t)
+//   Y   = Rq S^T + Qm V,  Rq = rs + A_qb Wa,  Qm = A_qb M + A_qk
+//   S^T <- diag(2^gC) S^T + Bd^T U + Kd^T V
+// with rs_t = r_t 2^{g_t}, as_t = alpha_t 2^{g_{t-1}}, bd_t = beta_t 2^{gC - g_t},
+// kd_t = k_t 2^{gC - g_t} — the WY form of the reference's chunk algebra
+// (rwkv7_hf/self_chunk_rwkv7.py:85-134, rwkv7_hf/dplr_prefill.py:221-311) with
+// everything that does not depend on S moved off the state's critical path.
+// The A matrices use rows centred on c = round(gC / 2):
+//   rc = r 2^{g-c}, kc = k 2^{c-g}, ac = alpha 2^{g_{t-1}-c}, bc = beta 2^{c-g},
+// exact while a chunk's log2-decay span -gC stays within 240 (per-token
+// w >= 2^-15 on average); beyond that the factors clamp at 2^+-126.
 //
-// Mapping: one 256-lane workgroup per (batch, head).  Wave q owns value rows
-// [16q, 16q+16) of the state, held transposed in MFMA accumulator layout
-// (4 key tiles x f32x4 per lane); the state never leaves registers.  Products
-// run on v_mfma_f32_16x16x{32,16}_bf16 with operands split into bf16 hi + lo
-// (hi*hi + hi*lo + lo*hi, ~1e-5 relative) and fp32 accumulation; K = 16
-// products are paired into one K = 32 MFMA ([U ; V] as a single operand).
-// Per chunk: (A) derive inputs, stage log-decay and V; (B) per-channel gate
-// cumsum and the gated rows (+ transposed copies); (C) the four causal
-// matrices, one per wave; (D) T by forward substitution on 16 lanes;
-// (E) per wave: T ac and T A_ak by MFMA straight into operand layout, then
-// U -> Y -> S.  The next chunk's raw inputs are in flight during (C)-(E).
-// Limitation: contributions below 2^-120 of a chunk's gate range are dropped.
+// Mapping: one workgroup of 8 waves per (batch, head), specialised:
+// * waves 0-3 ("chain") hold the fp32 state — wave q owns 16 value rows, as
+//   S^T tiles in MFMA accumulator layout — and per chunk run the products
+//   of U, Y and the state update (30 bf16x3 MFMAs per wave);
+// * waves 4-7 ("producers") each build whole chunks (chunks p, p+4, ...):
+//   loads, gate cumsum (DPP row scan), gated rows, the four A matrices, T by
+//   forward substitution, and Wa, Rq, M, Qm and the transposed Bd, Kd, V
+//   operands, all by MFMA, written into one of four LDS slots in exactly the
+//   per-lane register layout the chain waves consume.
+// Slots hand over through LDS flags (producer: ready = chunk id; chain waves:
+// done = chunk id); with five slots for four producers a producer never
+// waits for a slot in steady state, and no workgroup barrier sits in the
+// chunk loop.  All waits are bounded.
+//
+// Products run on v_mfma_f32_16x16x{32,16}_bf16 with operands split into bf16
+// hi + lo (hi*hi + hi*lo + lo*hi, ~1e-5 relative) and fp32 accumulation.
+// Layout changes (transposes) are MFMAs against the identity, which move
+// bf16 values exactly.
+//
+// Key channels are held in a permuted order sigma = 16 jt + 4 kg + e ->
+// channel 32 (jt >> 1) + 8 kg + 4 (jt & 1) + e, so that one lane's 16
+// channels of a token are two 16-byte runs; value rows use the same map.
 #include "common.h"
 
 namespace rwkv7mi {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int CH = 16;      // chunk length
-constexpr int HD = 64;      // head size
-constexpr int PR = HD + 8;  // padded bf16 row [t][j]
-constexpr int PT = CH + 4;  // padded bf16 row [j][t]
+constexpr int CH = 16;   // chunk length
+constexpr int HD = 64;   // head size
+constexpr int NSLOT = 6; // LDS slots: more than producer waves, so a producer
+                          // rarely waits for the chain to free one
+constexpr int WAIT_SPINS = 1 << 20;
 
-struct ChunkLDS {
-  float lw[CH][HD];                      // log2 decay
-  __bf16 vh[CH][PR], vl[CH][PR];         // V [s][i]
-  __bf16 rch[CH][PR], rcl[CH][PR];       // rc [t][j]
-  __bf16 ach[CH][PR], acl[CH][PR];       // ac [t][j]
-  __bf16 kch[CH][PR], kcl[CH][PR];       // kc [t][j]
-  __bf16 bch[CH][PR], bcl[CH][PR];       // bc [t][j]
-  __bf16 acth[HD][PT], actl[HD][PT];     // ac^T [j][t]
-  __bf16 kcth[HD][PT], kctl[HD][PT];     // kc^T
-  __bf16 bcth[HD][PT], bctl[HD][PT];     // bc^T
-  float amat[4][CH][CH];                 // [0] A_qk [t][s], [1] A_qb [t][s], [2] A_ak^T [s][t], [3] A_ab [t][s]
-  float tmat[CH][CH];                    // T [t][s]
-  float ecen[HD], pc[HD], ec[HD];        // 2^c, 2^{g_C - c}, 2^{g_C}
+// one chunk's operands for the chain waves, each array indexed [..][lane]
+struct ChunkSlot {
+  bf16x8 wa[2][2][64];  // [hi/lo][k-half cc] A(Wa): lane (t, kg)
+  bf16x8 rq[2][2][64];  // A(Rq)
+  bf16x8 bk[2][4][64];  // [hi/lo][jt] A([Bd^T | Kd^T]) rows of key tile jt
+  bf16x4 vt[2][4][64];  // [hi/lo][value tile] B(V)
+  bf16x4 am[2][64];     // [hi/lo] A(M)
+  bf16x4 aq[2][64];     // [hi/lo] A(Qm)
+  f32x4 ec[4][4];       // [jt][kg] 2^gC of channels 16jt + 4kg + e
 };
 
-// x = hi + lo with hi = x truncated to bf16 (exact) and lo = bf16(x - hi);
-// |x - hi - lo| <= 2^-17 |x|.
+struct ChunkShared {
+  ChunkSlot slot[NSLOT];
+  float nmat[4][CH][CH];  // per producer: A_ab [t][s]
+  float tcol[4][CH][CH];  // per producer: T column-major [s][t]
+  int ready[NSLOT];
+  int done[4][NSLOT];
+};
+
 __device__ __forceinline__ float trunc_bf16(float x) {
   return __uint_as_float(__float_as_uint(x) & 0xffff0000u);
 }
 __device__ __forceinline__ __bf16 hi_bits(float x) {
   return __builtin_bit_cast(__bf16, (unsigned short)(__float_as_uint(x) >> 16));
 }
-__device__ __forceinline__ void split2(float x, __bf16& hi, __bf16& lo) {
-  hi = hi_bits(x);
-  lo = (__bf16)(x - trunc_bf16(x));
-}
-__device__ __forceinline__ void split4(const float (&x)[4], bf16x4& hi, bf16x4& lo) {
+// x = hi + lo, hi = x truncated to bf16, lo = bf16(x - hi); |x - hi - lo| <= 2^-16 |x|
+__device__ __forceinline__ void split_f4(const f32x4& x, bf16x4& hi, bf16x4& lo) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     hi[e] = hi_bits(x[e]);
     lo[e] = (__bf16)(x[e] - trunc_bf16(x[e]));
   }
 }
-__device__ __forceinline__ void split_f4(const f32x4& x, bf16x4& hi, bf16x4& lo) {
-  const float a[4] = {x[0], x[1], x[2], x[3]};
-  split4(a, hi, lo);
+// f32x4 holding bf16 values -> bf16x4 (exact)
+__device__ __forceinline__ bf16x4 pack_exact(const f32x4& x) {
+  return (bf16x4){hi_bits(x[0]), hi_bits(x[1]), hi_bits(x[2]), hi_bits(x[3])};
 }
-__device__ __forceinline__ void split_pair(float x0, float x1, bf16x2& hi, bf16x2& lo) {
-  hi = (bf16x2){hi_bits(x0), hi_bits(x1)};
-  lo = (bf16x2){(__bf16)(x0 - trunc_bf16(x0)), (__bf16)(x1 - trunc_bf16(x1))};
+__device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
+  return (bf16x8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
 __device__ __forceinline__ f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
                                                    __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
 }
-__device__ __forceinline__ f32x4 mma3_16(bf16x4 ah, bf16x4 al, bf16x4 bh, bf16x4 bl, f32x4 c) {
-  c = mma16(ah, bh, c);
-  c = mma16(ah, bl, c);
-  return mma16(al, bh, c);
-}
-__device__ __forceinline__ f32x4 mma3_32(bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl, f32x4 c) {
-  c = mfma16x16x32(ah, bh, c);
-  c = mfma16x16x32(ah, bl, c);
-  return mfma16x16x32(al, bh, c);
-}
-// Split-term accumulators: the three products of a bf16x3 GEMM kept in
-// independent MFMA chains (summed once at the end) to shorten dependencies.
+constexpr f32x4 ZERO4 = {0.f, 0.f, 0.f, 0.f};
+
+// bf16x3 products with the three terms in independent accumulators
 struct Acc3 {
-  f32x4 hh, hl, lh;
-  __device__ __forceinline__ void zero() {
-    hh = hl = lh = (f32x4){0.f, 0.f, 0.f, 0.f};
-  }
+  f32x4 hh = ZERO4, hl = ZERO4, lh = ZERO4;
   __device__ __forceinline__ void add32(bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl) {
     hh = mfma16x16x32(ah, bh, hh);
     hl = mfma16x16x32(ah, bl, hl);
@@ -117,285 +116,400 @@ struct Acc3 {
   }
   __device__ __forceinline__ f32x4 sum() const { return hh + (hl + lh); }
 };
-__device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
-  return (bf16x8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
-__device__ __forceinline__ bf16x4 ld4(const __bf16* p) { return *reinterpret_cast<const bf16x4*>(p); }
-__device__ __forceinline__ bf16x8 ld8(const __bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
-__device__ __forceinline__ f32x4 ldf4(const float* p) {
-  const float4 q = *reinterpret_cast<const float4*>(p);
-  return (f32x4){q.x, q.y, q.z, q.w};
+// the same three products in one accumulator (fewer adds, longer chain)
+__device__ __forceinline__ f32x4 mma3_16(bf16x4 ah, bf16x4 al, bf16x4 bh, bf16x4 bl) {
+  return mma16(al, bh, mma16(ah, bl, mma16(ah, bh, ZERO4)));
 }
 
-__device__ __forceinline__ float clamp_exp(float e) { return fminf(fmaxf(e, -120.f), 120.f); }
+// ---- cross-lane helpers on 16-lane rows (lane = token within the chunk)
+template <int N>
+__device__ __forceinline__ float row_shr(float x) {  // lane t gets lane t-N (0 below the row)
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float row_scan(float x) {  // inclusive prefix sum over the row
+  x += row_shr<1>(x);
+  x += row_shr<2>(x);
+  x += row_shr<4>(x);
+  x += row_shr<8>(x);
+  return x;
+}
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {  // the row rotated by N lanes
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_sum(float x) {  // the row's total in every lane
+  x += row_ror<8>(x);
+  x += row_ror<4>(x);
+  x += row_ror<2>(x);
+  x += row_ror<1>(x);
+  return x;
+}
+
+// ---- LDS flags (workgroup scope)
+__device__ __forceinline__ void wait_geq(int* f, int v) {
+  for (int it = 0; it < WAIT_SPINS; ++it) {
+    if (__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+__device__ __forceinline__ void set_flag(int* f, int v) {
+  __hip_atomic_store(f, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// ---- one token's 16 channels of this lane: channels 8kg..8kg+7 and 32+8kg..32+8kg+7
+template <typename T>
+struct RawRow {
+  u32x4 v[sizeof(T) == 4 ? 4 : 2];
+};
+template <typename T>
+__device__ __forceinline__ void load_row(RawRow<T>& o, __amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  if constexpr (sizeof(T) == 4) {
+    o.v[0] = buf_ld16(rs, off);
+    o.v[1] = buf_ld16(rs, off + 16u);
+    o.v[2] = buf_ld16(rs, off + 128u);
+    o.v[3] = buf_ld16(rs, off + 144u);
+  } else {
+    o.v[0] = buf_ld16(rs, off);
+    o.v[1] = buf_ld16(rs, off + 64u);
+  }
+}
+// value of slot (jt, e): half jt >> 1, element 4 (jt & 1) + e of that half
+template <typename T>
+__device__ __forceinline__ float row_val(const RawRow<T>& o, int jt, int e) {
+  const int h = jt >> 1, idx = 4 * (jt & 1) + e;
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(o.v[2 * h + (idx >> 2)][idx & 3]);
+  } else {
+    const uint32_t w = o.v[h][idx >> 1];
+    if constexpr (std::is_same<T, __half>::value) {
+      float lo, hi;
+      f16x2_to_f32(w, lo, hi);
+      return (idx & 1) ? hi : lo;
+    } else {
+      return __uint_as_float((idx & 1) ? (w & 0xffff0000u) : (w << 16));
+    }
+  }
+}
+
+__device__ __forceinline__ float clamp126(float x) { return fminf(fmaxf(x, -126.f), 126.f); }
 
 template <typename TA, typename TW, bool WLOG>
-__global__ __launch_bounds__(256, 2) void wkv7_chunk_kernel(
+__global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
     const TA* __restrict__ r, const TW* __restrict__ w, const TA* __restrict__ k,
     const TA* __restrict__ v, const TA* __restrict__ kk, const TA* __restrict__ a,
     const float* state_in, float* state_out, TA* __restrict__ y, int T, int H) {
-  __shared__ ChunkLDS L;
+  extern __shared__ __align__(16) char smem_raw[];
+  ChunkShared& L = *reinterpret_cast<ChunkShared*>(smem_raw);
   const int bh = blockIdx.x;
   const int b = bh / H;
   const int h = bh % H;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int kg = lane >> 4;
-  const int64_t tok = (int64_t)H * HD;
-  const int64_t base = ((int64_t)b * T * H + h) * HD;
-
-  // state S[i][j], i = 16*wave + l16, j = 16*jt + 4*kg + e  (= S^T tile jt, D layout)
-  f32x4 S[4];
-  const int irow = 16 * wave + l16;
-  {
-    const float* src = state_in + ((int64_t)bh * HD + irow) * HD + 4 * kg;
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) S[jt] = ldf4(src + 16 * jt);
-  }
-
-  // raw inputs of this thread (channel j = lane, tokens 4*wave + tt), kept in
-  // their storage type until phase (A) so the prefetch never stalls on them
-  const int j = lane;
-  TA rr_[4], rk_[4], rv_[4], rkk_[4], ra_[4];
-  TW rw_[4];
-  auto load_raw = [&](int t0) {
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int tg = min(t0 + 4 * wave + tt, T - 1);  // clamped; masked in (A)
-      const int64_t off = base + (int64_t)tg * tok + j;
-      rr_[tt] = r[off];
-      rk_[tt] = k[off];
-      rv_[tt] = v[off];
-      rkk_[tt] = kk[off];
-      ra_[tt] = a[off];
-      rw_[tt] = w[off];
-    }
-  };
-  float xr[4], xk[4], xal[4], xbe[4];
-
   const int nchunks = (T + CH - 1) / CH;
-  if (nchunks > 0) load_raw(0);
-  for (int c = 0; c < nchunks; ++c) {
-    const int t0 = c * CH;
-    // ---------------- (A) derive inputs, stage log-decay and v
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int t = 4 * wave + tt;
-      const bool ok = t0 + t < T;  // padding tokens: zero vectors, decay 1
-      const float kkv = to_f32(rkk_[tt]);
-      xr[tt] = ok ? to_f32(rr_[tt]) : 0.f;
-      xk[tt] = ok ? to_f32(rk_[tt]) : 0.f;
-      xal[tt] = ok ? -kkv : 0.f;
-      xbe[tt] = ok ? kkv * to_f32(ra_[tt]) : 0.f;
-      const float wv = to_f32(rw_[tt]);
-      const float lw = WLOG ? wv * 1.4426950408889634f : log2f(wv);
-      L.lw[t][j] = ok ? fmaxf(lw, -126.f) : 0.f;
-      split2(ok ? to_f32(rv_[tt]) : 0.f, L.vh[t][j], L.vl[t][j]);
-    }
-    __syncthreads();
-    // ---------------- (B) gates and gated rows
+  const int64_t tok = (int64_t)H * HD;  // elements per token
+
+  if (tid < NSLOT) L.ready[tid] = -1;
+  if (tid < 4 * NSLOT) L.done[tid / NSLOT][tid % NSLOT] = -1;
+  __syncthreads();
+
+  if (wave < 4) {
+    // ===================== chain wave q: value rows i = phi(16q + l16)
+    const int q = wave;
+    const int ich = 32 * (q >> 1) + 8 * (l16 >> 2) + 4 * (q & 1) + (l16 & 3);
+    // S[jt] lane (l16, kg): S[ich][j], j = 32 (jt >> 1) + 8 kg + 4 (jt & 1) + e
+    f32x4 S[4];
     {
-      float g[CH];
-      float acc = 0.f;
+      const float* src = state_in + ((int64_t)bh * HD + ich) * HD + 8 * kg;
 #pragma unroll
-      for (int t = 0; t < CH; ++t) {
-        acc += L.lw[t][j];
-        g[t] = acc;
-      }
-      const float gC = g[CH - 1];
-      const float cen = g[CH / 2 - 1];
-      // g[4*wave - 1 .. 4*wave + 3] via a wave-uniform branch (compile-time indices)
-      float gprev = 0.f;
-      float gt4[4];
-      switch (wave) {
-        case 0: gt4[0] = g[0]; gt4[1] = g[1]; gt4[2] = g[2]; gt4[3] = g[3]; break;
-        case 1: gprev = g[3]; gt4[0] = g[4]; gt4[1] = g[5]; gt4[2] = g[6]; gt4[3] = g[7]; break;
-        case 2: gprev = g[7]; gt4[0] = g[8]; gt4[1] = g[9]; gt4[2] = g[10]; gt4[3] = g[11]; break;
-        default: gprev = g[11]; gt4[0] = g[12]; gt4[1] = g[13]; gt4[2] = g[14]; gt4[3] = g[15]; break;
-      }
-      float p[5], q[4];
-      p[0] = exp2f(clamp_exp(gprev - cen));
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        p[tt + 1] = exp2f(clamp_exp(gt4[tt] - cen));
-        q[tt] = exp2f(clamp_exp(cen - gt4[tt]));
-      }
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp) {
-        const int t = 4 * wave + 2 * pp;
-        const int a0 = 2 * pp, a1 = 2 * pp + 1;
-        bf16x2 hi, lo;
-        split_pair(xr[a0] * p[a0 + 1], xr[a1] * p[a1 + 1], hi, lo);
-        L.rch[t][j] = hi[0]; L.rch[t + 1][j] = hi[1]; L.rcl[t][j] = lo[0]; L.rcl[t + 1][j] = lo[1];
-        split_pair(xal[a0] * p[a0], xal[a1] * p[a1], hi, lo);
-        L.ach[t][j] = hi[0]; L.ach[t + 1][j] = hi[1]; L.acl[t][j] = lo[0]; L.acl[t + 1][j] = lo[1];
-        *reinterpret_cast<bf16x2*>(&L.acth[j][t]) = hi;
-        *reinterpret_cast<bf16x2*>(&L.actl[j][t]) = lo;
-        split_pair(xk[a0] * q[a0], xk[a1] * q[a1], hi, lo);
-        L.kch[t][j] = hi[0]; L.kch[t + 1][j] = hi[1]; L.kcl[t][j] = lo[0]; L.kcl[t + 1][j] = lo[1];
-        *reinterpret_cast<bf16x2*>(&L.kcth[j][t]) = hi;
-        *reinterpret_cast<bf16x2*>(&L.kctl[j][t]) = lo;
-        split_pair(xbe[a0] * q[a0], xbe[a1] * q[a1], hi, lo);
-        L.bch[t][j] = hi[0]; L.bch[t + 1][j] = hi[1]; L.bcl[t][j] = lo[0]; L.bcl[t + 1][j] = lo[1];
-        *reinterpret_cast<bf16x2*>(&L.bcth[j][t]) = hi;
-        *reinterpret_cast<bf16x2*>(&L.bctl[j][t]) = lo;
-      }
-      if (wave == 0) {
-        L.ecen[j] = exp2f(cen);
-        L.pc[j] = exp2f(clamp_exp(gC - cen));
-        L.ec[j] = exp2f(gC);
+      for (int jt = 0; jt < 4; ++jt) {
+        const float4 t4 = *reinterpret_cast<const float4*>(src + 32 * (jt >> 1) + 4 * (jt & 1));
+        S[jt] = (f32x4){t4.x, t4.y, t4.z, t4.w};
       }
     }
-    if (c + 1 < nchunks) load_raw(t0 + CH);  // in flight during (C)-(E)
-    __syncthreads();
-    // ---------------- (C) causal matrices: wave 0 A_qk, 1 A_qb, 2 A_ak, 3 A_ab
-    {
-      const bool use_k = (wave == 0 || wave == 2);
-      const bool use_r = (wave < 2);
-      const __bf16(*Xh)[PR] = use_k ? L.kch : L.bch;
-      const __bf16(*Xl)[PR] = use_k ? L.kcl : L.bcl;
-      const __bf16(*Yh)[PR] = use_r ? L.rch : L.ach;
-      const __bf16(*Yl)[PR] = use_r ? L.rcl : L.acl;
-      f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+    TA* ybase = y + ((int64_t)b * T * H + h) * HD + ich;
+    for (int x = 0; x < nchunks; ++x) {
+      const int s = x % NSLOT;
+      const ChunkSlot& Z = L.slot[s];
+      wait_geq(&L.ready[s], x);
+      bf16x8 waH[2], waL[2], rqH[2], rqL[2], bkH[4], bkL[4];
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
-        const int jo = 32 * cc + 8 * kg;
-        acc = mma3_32(ld8(&Xh[l16][jo]), ld8(&Xl[l16][jo]), ld8(&Yh[l16][jo]), ld8(&Yl[l16][jo]), acc);
+        waH[cc] = Z.wa[0][cc][lane];
+        waL[cc] = Z.wa[1][cc][lane];
+        rqH[cc] = Z.rq[0][cc][lane];
+        rqL[cc] = Z.rq[1][cc][lane];
       }
-      // D[m = s][n = t]: lane holds s = 4kg + e, t = l16
-      float o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int s = 4 * kg + e;
-        const bool keep = use_r ? (s <= l16) : (s < l16);
-        o[e] = keep ? acc[e] : 0.f;
-      }
-      if (wave == 2) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) L.amat[2][4 * kg + e][l16] = o[e];  // A_ak^T [s][t]
-      } else {
-        *reinterpret_cast<float4*>(&L.amat[wave][l16][4 * kg]) = make_float4(o[0], o[1], o[2], o[3]);
-      }
-    }
-    __syncthreads();
-    // ---------------- (D) T = (I - A_ab)^{-1}: column s = lane, forward substitution
-    if (wave == 0 && lane < CH) {
-      float Lm[CH][CH];
-#pragma unroll
-      for (int t = 1; t < CH; ++t)
-#pragma unroll
-        for (int qq = 0; qq < (t + 3) / 4; ++qq) {
-          const float4 v4 = *reinterpret_cast<const float4*>(&L.amat[3][t][4 * qq]);
-          Lm[t][4 * qq] = v4.x; Lm[t][4 * qq + 1] = v4.y; Lm[t][4 * qq + 2] = v4.z; Lm[t][4 * qq + 3] = v4.w;
-        }
-      float x[CH];
-#pragma unroll
-      for (int t = 0; t < CH; ++t) {
-        float accx = (t == lane) ? 1.f : 0.f;
-#pragma unroll
-        for (int u = 0; u < t; ++u) accx += Lm[t][u] * x[u];
-        x[t] = accx;
-        L.tmat[t][lane] = accx;
-      }
-    }
-    __syncthreads();
-    // ---------------- (E) state chain for value rows [16*wave, 16*wave + 16)
-    {
-      // T as B operand (K = s = 4kg + e, N = t = l16): T[t][s]
-      bf16x4 TBh, TBl;
-      split_f4(ldf4(&L.tmat[l16][4 * kg]), TBh, TBl);
-      // W' = T ac, in A layout: (T ac)^T = ac^T T^T, D lane (j = 16jt + 4kg + e, t = l16)
-      bf16x4 WAh[4], WAl[4];
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
-        const int jr = 16 * jt + l16;
-        f32x4 wt = mma3_16(ld4(&L.acth[jr][4 * kg]), ld4(&L.actl[jr][4 * kg]), TBh, TBl,
-                           (f32x4){0.f, 0.f, 0.f, 0.f});
-        split_f4(wt, WAh[jt], WAl[jt]);
+        bkH[jt] = Z.bk[0][jt][lane];
+        bkL[jt] = Z.bk[1][jt][lane];
       }
-      // M = T A_ak, in A layout: (T A_ak)^T = A_ak^T T^T, D lane (s = 4kg + e, t = l16)
-      bf16x4 MAh, MAl;
-      {
-        bf16x4 AkH, AkL;
-        split_f4(ldf4(&L.amat[2][l16][4 * kg]), AkH, AkL);
-        f32x4 mt = mma3_16(AkH, AkL, TBh, TBl, (f32x4){0.f, 0.f, 0.f, 0.f});
-        split_f4(mt, MAh, MAl);
-      }
-      // S' = S diag(2^c)
+      const bf16x4 vH = Z.vt[0][q][lane], vL = Z.vt[1][q][lane];
+      const bf16x4 amH = Z.am[0][lane], amL = Z.am[1][lane], aqH = Z.aq[0][lane], aqL = Z.aq[1][lane];
+      f32x4 ec[4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) ec[jt] = Z.ec[jt][kg];
+      set_flag(&L.done[q][s], x);  // the operands are in registers
+
       bf16x4 SH[4], SL[4];
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        const f32x4 sc = ldf4(&L.ecen[16 * jt + 4 * kg]);
-        split_f4(S[jt] * sc, SH[jt], SL[jt]);
-      }
-      bf16x4 VH, VL;
+      for (int jt = 0; jt < 4; ++jt) split_f4(S[jt], SH[jt], SL[jt]);
+      Acc3 accU, accY;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        VH[e] = L.vh[4 * kg + e][16 * wave + l16];
-        VL[e] = L.vl[4 * kg + e][16 * wave + l16];
+      for (int cc = 0; cc < 2; ++cc) {
+        const bf16x8 sh = cat(SH[2 * cc], SH[2 * cc + 1]), sl = cat(SL[2 * cc], SL[2 * cc + 1]);
+        accU.add32(waH[cc], waL[cc], sh, sl);
+        accY.add32(rqH[cc], rqL[cc], sh, sl);
       }
-      // U = W' S'^T + M V
-      Acc3 accU;
-      accU.zero();
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc)
-        accU.add32(cat(WAh[2 * cc], WAh[2 * cc + 1]), cat(WAl[2 * cc], WAl[2 * cc + 1]),
-                   cat(SH[2 * cc], SH[2 * cc + 1]), cat(SL[2 * cc], SL[2 * cc + 1]));
-      accU.add16(MAh, MAl, VH, VL);
+      accU.add16(amH, amL, vH, vL);  // + M V
       const f32x4 U = accU.sum();
       bf16x4 UH, UL;
       split_f4(U, UH, UL);
-      // [U ; V] as one K = 32 B operand: slots 0-3 = U[s][i], slots 4-7 = V[s][i], s = 4kg + e
-      const bf16x8 UVh = cat(UH, VH);
-      const bf16x8 UVl = cat(UL, VL);
-      // Y = rc S'^T + [A_qb | A_qk] [U ; V]
-      Acc3 accY;
-      accY.zero();
+      const bf16x8 uvH = cat(UH, vH), uvL = cat(UL, vL);
 #pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        const int jo = 32 * cc + 4 * kg;
-        accY.add32(cat(ld4(&L.rch[l16][jo]), ld4(&L.rch[l16][jo + 16])),
-                   cat(ld4(&L.rcl[l16][jo]), ld4(&L.rcl[l16][jo + 16])),
-                   cat(SH[2 * cc], SH[2 * cc + 1]), cat(SL[2 * cc], SL[2 * cc + 1]));
+      for (int jt = 0; jt < 4; ++jt) {
+        Acc3 acc;
+        acc.add32(bkH[jt], bkL[jt], uvH, uvL);
+        S[jt] = S[jt] * ec[jt] + acc.sum();
       }
-      {
-        bf16x4 QBH, QBL, QKH, QKL;
-        split_f4(ldf4(&L.amat[1][l16][4 * kg]), QBH, QBL);
-        split_f4(ldf4(&L.amat[0][l16][4 * kg]), QKH, QKL);
-        accY.add32(cat(QBH, QKH), cat(QBL, QKL), UVh, UVl);
-      }
+      accY.add16(aqH, aqL, vH, vL);  // + Qm V
       const f32x4 Yv = accY.sum();
+      const int t0 = x * CH;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int tg = t0 + 4 * kg + e;
-        if (tg < T) y[base + (int64_t)tg * tok + 16 * wave + l16] = from_f32<TA>(Yv[e]);
-      }
-      // S^T = diag(2^{g_C}) S^T + diag(2^{g_C - c}) [bc^T | kc^T] [U ; V]
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        const int jr = 16 * jt + l16;
-        const f32x4 X = mma3_32(cat(ld4(&L.bcth[jr][4 * kg]), ld4(&L.kcth[jr][4 * kg])),
-                                cat(ld4(&L.bctl[jr][4 * kg]), ld4(&L.kctl[jr][4 * kg])), UVh, UVl,
-                                (f32x4){0.f, 0.f, 0.f, 0.f});
-        S[jt] = S[jt] * ldf4(&L.ec[16 * jt + 4 * kg]) + X * ldf4(&L.pc[16 * jt + 4 * kg]);
+        if (tg < T) ybase[(int64_t)tg * tok] = from_f32<TA>(Yv[e]);
       }
     }
-    __syncthreads();
-  }
-
-  {
-    float* dst = state_out + ((int64_t)bh * HD + irow) * HD + 4 * kg;
+    float* dst = state_out + ((int64_t)bh * HD + ich) * HD + 8 * kg;
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
-      *reinterpret_cast<float4*>(dst + 16 * jt) = make_float4(S[jt][0], S[jt][1], S[jt][2], S[jt][3]);
+      *reinterpret_cast<float4*>(dst + 32 * (jt >> 1) + 4 * (jt & 1)) = make_float4(S[jt][0], S[jt][1], S[jt][2], S[jt][3]);
+    return;
+  }
+
+  // ===================== producer wave p: chunks p, p+4, ...; lane = (token t = l16, kg)
+  const int p = wave - 4;
+  const int t = l16;
+  // identity as a B operand: lane (n = l16, k = 4kg + e)
+  bf16x4 Ib;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) Ib[e] = (__bf16)((4 * kg + e == l16) ? 1.f : 0.f);
+  float(&N)[CH][CH] = L.nmat[p];
+  float(&Tc)[CH][CH] = L.tcol[p];
+
+  RawRow<TA> rr, rk, rv, rkk, ra;
+  RawRow<TW> rw;
+  auto issue = [&](int x) {
+    const int t0 = x * CH;
+    const int valid = min(CH, T - t0);
+    const int64_t base = (((int64_t)b * T + t0) * H + h) * HD;
+    const uint32_t nbA = (uint32_t)(valid * tok * (int64_t)sizeof(TA));
+    const uint32_t nbW = (uint32_t)(valid * tok * (int64_t)sizeof(TW));
+    const uint32_t offA = (uint32_t)(t * tok * (int64_t)sizeof(TA)) + 8u * kg * (uint32_t)sizeof(TA);
+    const uint32_t offW = (uint32_t)(t * tok * (int64_t)sizeof(TW)) + 8u * kg * (uint32_t)sizeof(TW);
+    load_row<TA>(rr, make_rsrc(r + base, nbA), offA);
+    load_row<TA>(rk, make_rsrc(k + base, nbA), offA);
+    load_row<TA>(rv, make_rsrc(v + base, nbA), offA);
+    load_row<TA>(rkk, make_rsrc(kk + base, nbA), offA);
+    load_row<TA>(ra, make_rsrc(a + base, nbA), offA);
+    load_row<TW>(rw, make_rsrc(w + base, nbW), offW);
+  };
+  if (p < nchunks) issue(p);
+
+  for (int x = p; x < nchunks; x += 4) {
+    const bool ok = x * CH + t < T;
+    // Wait until the chain waves have taken chunk x - NSLOT out of this slot;
+    // every result below is then stored as soon as it exists (Das and rs are
+    // parked in the Wa / Rq areas until Wa and Rq replace them).
+    const int s = x % NSLOT;
+    for (int qq = 0; qq < 4; ++qq) wait_geq(&L.done[qq][s], x - NSLOT);
+    ChunkSlot& Z = L.slot[s];
+
+    // ---- per K half cc (channel tiles 2cc, 2cc+1): gates, gated rows, their
+    // A-matrix products, and the transposed operands (identity MFMAs:
+    // D(x) tile jt = lane (sigma = 16jt + l16, t = 4kg + e))
+    f32x4 AqbA = ZERO4, AqkA = ZERO4, AakD = ZERO4, AabA = ZERO4;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      bf16x4 rcH[2], rcL[2], kcH[2], kcL[2], acH[2], acL[2], bcH[2], bcL[2];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int jt = 2 * cc + jj;
+        f32x4 rc, kc, ac, bc, as, bd, kd, xv, rs, ecv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // inputs of token t, channel slot (jt, e), read from the raw rows here
+          const float xr = row_val<TA>(rr, jt, e), xk = row_val<TA>(rk, jt, e);
+          const float xkk = row_val<TA>(rkk, jt, e), xa = row_val<TA>(ra, jt, e);
+          xv[e] = row_val<TA>(rv, jt, e);
+          const float wv = row_val<TW>(rw, jt, e);
+          const float l2 = WLOG ? wv * 1.4426950408889634f : __builtin_amdgcn_logf(wv);
+          const float lwv = ok ? fmaxf(l2, -126.f) : 0.f;
+          const float g = row_scan(lwv);
+          const float gC = row_sum(lwv);
+          const float cf = rintf(0.5f * gC);
+          const int ci = (int)cf;
+          const float pv = __builtin_amdgcn_exp2f(clamp126(g - cf));
+          const float qv = __builtin_amdgcn_exp2f(clamp126(cf - g));
+          const float pp = row_shr<1>(pv);  // 2^{g_{t-1} - c}; lane 0 unused
+          const float pC = __builtin_amdgcn_exp2f(clamp126(gC - cf));
+          const float al = -xkk;
+          const float be = xkk * xa;
+          rc[e] = xr * pv;
+          kc[e] = xk * qv;
+          ac[e] = al * pp;
+          bc[e] = be * qv;
+          rs[e] = __builtin_amdgcn_ldexpf(rc[e], ci);
+          as[e] = t == 0 ? al : __builtin_amdgcn_ldexpf(ac[e], ci);
+          const float dv = pC * qv;  // 2^{gC - g_t}
+          bd[e] = be * dv;
+          kd[e] = xk * dv;
+          ecv[e] = __builtin_amdgcn_ldexpf(pC, ci);
+        }
+        split_f4(rc, rcH[jj], rcL[jj]);
+        split_f4(kc, kcH[jj], kcL[jj]);
+        split_f4(ac, acH[jj], acL[jj]);
+        split_f4(bc, bcH[jj], bcL[jj]);
+        bf16x4 hi, lo, hi2, lo2;
+        split_f4(as, hi, lo);
+        reinterpret_cast<bf16x4*>(&Z.wa[0][cc][lane])[jj] = pack_exact(mma16(hi, Ib, ZERO4));  // Das
+        reinterpret_cast<bf16x4*>(&Z.wa[1][cc][lane])[jj] = pack_exact(mma16(lo, Ib, ZERO4));
+        split_f4(xv, hi, lo);
+        Z.vt[0][jt][lane] = pack_exact(mma16(hi, Ib, ZERO4));
+        Z.vt[1][jt][lane] = pack_exact(mma16(lo, Ib, ZERO4));
+        split_f4(bd, hi, lo);
+        split_f4(kd, hi2, lo2);
+        Z.bk[0][jt][lane] = cat(pack_exact(mma16(hi, Ib, ZERO4)), pack_exact(mma16(hi2, Ib, ZERO4)));
+        Z.bk[1][jt][lane] = cat(pack_exact(mma16(lo, Ib, ZERO4)), pack_exact(mma16(lo2, Ib, ZERO4)));
+        *reinterpret_cast<f32x4*>(&Z.rq[jj][cc][lane]) = rs;  // rs, until Rq
+        if (t == 0) Z.ec[jt][kg] = ecv;
+      }
+      const bf16x8 rH = cat(rcH[0], rcH[1]), rL = cat(rcL[0], rcL[1]);
+      const bf16x8 kH = cat(kcH[0], kcH[1]), kL = cat(kcL[0], kcL[1]);
+      const bf16x8 aH = cat(acH[0], acH[1]), aL = cat(acL[0], acL[1]);
+      const bf16x8 bH = cat(bcH[0], bcH[1]), bL = cat(bcL[0], bcL[1]);
+      // A(A_qb), A(A_qk): lane (t = l16, s = 4kg + e); D(A_ak): lane (s = l16, t = 4kg + e); A(A_ab)
+      AqbA = mfma16x16x32(bH, rH, AqbA);
+      AqkA = mfma16x16x32(kH, rH, AqkA);
+      AakD = mfma16x16x32(aH, kH, AakD);
+      AabA = mfma16x16x32(bH, aH, AabA);
+      AqbA = mfma16x16x32(bH, rL, AqbA);
+      AqkA = mfma16x16x32(kH, rL, AqkA);
+      AakD = mfma16x16x32(aH, kL, AakD);
+      AabA = mfma16x16x32(bH, aL, AabA);
+      AqbA = mfma16x16x32(bL, rH, AqbA);
+      AqkA = mfma16x16x32(kL, rH, AqkA);
+      AakD = mfma16x16x32(aL, kH, AakD);
+      AabA = mfma16x16x32(bL, aH, AabA);
+    }
+    if (x + 4 < nchunks) issue(x + 4);  // the raw rows are consumed; the next ones land meanwhile
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s4 = 4 * kg + e;
+      AqbA[e] = s4 <= l16 ? AqbA[e] : 0.f;
+      AqkA[e] = s4 <= l16 ? AqkA[e] : 0.f;
+      AakD[e] = s4 > l16 ? AakD[e] : 0.f;
+      AabA[e] = s4 < l16 ? AabA[e] : 0.f;
+    }
+    // ---- T = (I - A_ab)^{-1} by forward substitution, column s = lane (lanes 0-15)
+    *reinterpret_cast<float4*>(&N[l16][4 * kg]) = make_float4(AabA[0], AabA[1], AabA[2], AabA[3]);
+    if (lane < CH) {
+      float xc[CH];
+#pragma unroll
+      for (int tt = 0; tt < CH; ++tt) {
+        float acc = (tt == lane) ? 1.f : 0.f;
+#pragma unroll
+        for (int u4 = 0; u4 < (tt + 3) / 4; ++u4) {
+          const float4 n4 = *reinterpret_cast<const float4*>(&N[tt][4 * u4]);
+          if (4 * u4 + 0 < tt) acc += n4.x * xc[4 * u4 + 0];
+          if (4 * u4 + 1 < tt) acc += n4.y * xc[4 * u4 + 1];
+          if (4 * u4 + 2 < tt) acc += n4.z * xc[4 * u4 + 2];
+          if (4 * u4 + 3 < tt) acc += n4.w * xc[4 * u4 + 3];
+        }
+        xc[tt] = acc;
+      }
+#pragma unroll
+      for (int u4 = 0; u4 < 4; ++u4)
+        *reinterpret_cast<float4*>(&Tc[lane][4 * u4]) =
+            make_float4(xc[4 * u4], xc[4 * u4 + 1], xc[4 * u4 + 2], xc[4 * u4 + 3]);
+    }
+    // D(T): lane (s = l16, t = 4kg + e); A(T): lane (t = l16, s = 4kg + e)
+    f32x4 Dt, At;
+    {
+      const float4 d4 = *reinterpret_cast<const float4*>(&Tc[l16][4 * kg]);
+      Dt = (f32x4){d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) At[e] = Tc[4 * kg + e][l16];
+    }
+    bf16x4 AtH, AtL, DtH, DtL, AakH, AakL, AqbH, AqbL;
+    split_f4(At, AtH, AtL);
+    split_f4(Dt, DtH, DtL);
+    split_f4(AakD, AakH, AakL);
+    split_f4(AqbA, AqbH, AqbL);
+    // A(M), M = T A_ak;  A(Pm), Pm = A_qb T
+    bf16x4 AmH, AmL, ApH, ApL;
+    split_f4(mma3_16(AakH, AakL, AtH, AtL), AmH, AmL);
+    split_f4(mma3_16(DtH, DtL, AqbH, AqbL), ApH, ApL);
+
+    // ---- Wa = T as and Rq = rs + Pm as (lane (t, sigma) layout) replace Das and rs
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      const bf16x8 dH = Z.wa[0][cc][lane], dL = Z.wa[1][cc][lane];
+      const f32x4 rs0 = *reinterpret_cast<const f32x4*>(&Z.rq[0][cc][lane]);
+      const f32x4 rs1 = *reinterpret_cast<const f32x4*>(&Z.rq[1][cc][lane]);
+      bf16x4 waH[2], waL[2], rqH[2], rqL[2];
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const bf16x4 daH = {dH[4 * jj], dH[4 * jj + 1], dH[4 * jj + 2], dH[4 * jj + 3]};
+        const bf16x4 daL = {dL[4 * jj], dL[4 * jj + 1], dL[4 * jj + 2], dL[4 * jj + 3]};
+        split_f4(mma3_16(daH, daL, AtH, AtL), waH[jj], waL[jj]);
+        split_f4((jj ? rs1 : rs0) + mma3_16(daH, daL, ApH, ApL), rqH[jj], rqL[jj]);
+      }
+      Z.wa[0][cc][lane] = cat(waH[0], waH[1]);
+      Z.wa[1][cc][lane] = cat(waL[0], waL[1]);
+      Z.rq[0][cc][lane] = cat(rqH[0], rqH[1]);
+      Z.rq[1][cc][lane] = cat(rqL[0], rqL[1]);
+    }
+    // ---- M and Qm = A_qb M + A_qk for the chain's M V and Qm V
+    {
+      bf16x4 DmH, DmL;
+      split_f4(mma3_16(AtH, AtL, AakH, AakL), DmH, DmL);  // D(M) = A(T) x D(A_ak)
+      bf16x4 qH, qL;
+      split_f4(AqkA + mma3_16(DmH, DmL, AqbH, AqbL), qH, qL);  // A(A_qb M) = D(M) x A(A_qb)
+      Z.am[0][lane] = AmH;
+      Z.am[1][lane] = AmL;
+      Z.aq[0][lane] = qH;
+      Z.aq[1][lane] = qL;
+    }
+    set_flag(&L.ready[s], x);
   }
 }
 
 }  // namespace rwkv7mi
 
 using namespace rwkv7mi;
+
+template <typename TA, typename TW, bool WLOG>
+static int chunk_go(int64_t B, int64_t T, int64_t H, void* stream, const void* r, const void* w, const void* k,
+                    const void* v, const void* kk, const void* a, const float* state_in, float* state_out,
+                    void* y) {
+  static bool lds_raised = false;  // dynamic LDS above 64 KB must be enabled once per instance
+  const size_t lds = sizeof(ChunkShared);
+  if (!lds_raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&wkv7_chunk_kernel<TA, TW, WLOG>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+      return fail(RWKV7MI_ELAUNCH, "wkv7_chunk_kernel: cannot raise the dynamic LDS limit");
+    lds_raised = true;
+  }
+  hipLaunchKernelGGL((wkv7_chunk_kernel<TA, TW, WLOG>), dim3((unsigned)(B * H)), dim3(512), lds, as_stream(stream),
+                     (const TA*)r, (const TW*)w, (const TA*)k, (const TA*)v, (const TA*)kk, (const TA*)a, state_in,
+                     state_out, (TA*)y, (int)T, (int)H);
+  return check_launch("wkv7_chunk_kernel");
+}
 
 extern "C" int rwkv7mi_wkv7_chunk_prefill(const void* r, const void* w, const void* k, const void* v,
                                           const void* kk, const void* a, const float* state_in,
@@ -412,19 +526,19 @@ extern "C" int rwkv7mi_wkv7_chunk_prefill(const void* r, const void* w, const vo
   if ((reinterpret_cast<uintptr_t>(state_in) | reinterpret_cast<uintptr_t>(state_out)) & 15)
     return fail(RWKV7MI_EINVAL, "wkv7 chunk: state must be 16-byte aligned");
   if (B * H > INT32_MAX || T > INT32_MAX) return fail(RWKV7MI_EINVAL, "wkv7 chunk: too large");
+  // per-chunk buffer descriptors span 16 tokens of the [B, T, H, 64] inputs
+  if (16 * H * HD * 4 > (int64_t)UINT32_MAX) return fail(RWKV7MI_EINVAL, "wkv7 chunk: too many heads");
   return dispatch_dtype(act_dtype, [&](auto ta) {
     using TA = decltype(ta);
+    // 16-byte channel runs: every input row must start 16-byte aligned
+    const uintptr_t al = reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(k) |
+                         reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(kk) |
+                         reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(w);
+    if (al & 15) return fail(RWKV7MI_EINVAL, "wkv7 chunk: inputs must be 16-byte aligned");
     return dispatch_dtype(w_dtype, [&](auto tw) {
       using TW = decltype(tw);
-      if (w_is_log)
-        hipLaunchKernelGGL((wkv7_chunk_kernel<TA, TW, true>), dim3((unsigned)(B * H)), dim3(256), 0,
-                           as_stream(stream), (const TA*)r, (const TW*)w, (const TA*)k, (const TA*)v,
-                           (const TA*)kk, (const TA*)a, state_in, state_out, (TA*)y, (int)T, (int)H);
-      else
-        hipLaunchKernelGGL((wkv7_chunk_kernel<TA, TW, false>), dim3((unsigned)(B * H)), dim3(256), 0,
-                           as_stream(stream), (const TA*)r, (const TW*)w, (const TA*)k, (const TA*)v,
-                           (const TA*)kk, (const TA*)a, state_in, state_out, (TA*)y, (int)T, (int)H);
-      return check_launch("wkv7_chunk_kernel");
+      if (w_is_log) return chunk_go<TA, TW, true>(B, T, H, stream, r, w, k, v, kk, a, state_in, state_out, y);
+      return chunk_go<TA, TW, false>(B, T, H, stream, r, w, k, v, kk, a, state_in, state_out, y);
     });
   });
 }

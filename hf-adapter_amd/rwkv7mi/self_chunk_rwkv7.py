@@ -6,8 +6,9 @@ chunk kernel (chunk 16, bf16x3 MFMA products, fp32 state in registers).
 ``self_chunk_rwkv7`` keeps the reference's argument checks (N = 64, T
 divisible by chunk_size, chunk_size in {16, 32, 64}); ``dplr_chunk_scan``
 accepts any T like the reference's pure-torch oracle.  The kernel always uses
-16-token chunks internally; ``chunk_size`` does not change the result beyond
-rounding.
+16-token chunks internally (one workgroup of four state waves and four chunk
+producer waves per (batch, head)); ``chunk_size`` does not change the result
+beyond rounding.
 """
 from __future__ import annotations
 
@@ -27,9 +28,15 @@ def self_chunk_rwkv7_available() -> bool:
     return torch.cuda.is_available()
 
 
+def _aligned16(x: torch.Tensor) -> torch.Tensor:
+    """The kernel reads 16-byte channel runs; a view at an odd offset is copied."""
+    return x if x.data_ptr() % 16 == 0 else x.clone()
+
+
 def _run_chunk(r4, w4, k4, v4, kk4, a4, state, *, w_is_log: bool, chunk: int,
                state_out=None, out=None):
     B, T, H, N = (int(s) for s in r4.shape)
+    r4, w4, k4, v4, kk4, a4 = (_aligned16(x) for x in (r4, w4, k4, v4, kk4, a4))
     _lib.require_gpu(r4, w4, k4, v4, kk4, a4, state, name="wkv7 chunk prefill")
     st = state.contiguous()
     final = _state_dst(st, state_out)
