@@ -8,17 +8,17 @@
 //   A_qk[t,s] = sum_j r_t k_s 2^{g_t - g_s}   (s <= t)     A_qb: beta_s in place of k_s
 //   A_ak[t,s] = sum_j alpha_t k_s 2^{g_{t-1} - g_s} (s < t) A_ab: beta_s in place of k_s
 // and T = (I - A_ab)^{-1}, the chunk is affine in its start state S:
-//   U   = Wa S^T + M V,   Wa = T as,  M = T A_ak,          (u_t = S_{t-1} alpha_t)
-//   Y   = Rq S^T + Qm V,  Rq = rs + A_qb Wa,  Qm = A_qb M + A_qk
-//   S^T <- diag(2^gC) S^T + Bd^T U + Kd^T V
-// with rs_t = r_t 2^{g_t}, as_t = alpha_t 2^{g_{t-1}}, bd_t = beta_t 2^{gC - g_t},
-// kd_t = k_t 2^{gC - g_t} — the WY form of the reference's chunk algebra
-// (rwkv7_hf/self_chunk_rwkv7.py:85-134, rwkv7_hf/dplr_prefill.py:221-311) with
-// everything that does not depend on S moved off the state's critical path.
-// The A matrices use rows centred on c = round(gC / 2):
-//   rc = r 2^{g-c}, kc = k 2^{c-g}, ac = alpha 2^{g_{t-1}-c}, bc = beta 2^{c-g},
-// exact while a chunk's log2-decay span -gC stays within 240 (per-token
-// w >= 2^-15 on average); beyond that the factors clamp at 2^+-126.
+//   U   = Wa S'^T + M V,   Wa = T ac,  M = T A_ak,          (u_t = S_{t-1} alpha_t)
+//   Y   = Rq S'^T + Qm V,  Rq = rc + A_qb Wa,  Qm = A_qb M + A_qk
+//   S^T <- diag(2^gC) S^T + diag(2^{gC-c}) (Bc^T U + Kc^T V),   S' = S diag(2^c)
+// with the rows centred on c = round(gC / 2) (per key channel):
+//   rc = r 2^{g-c}, kc = k 2^{c-g}, ac = alpha 2^{g_{t-1}-c}, bc = beta 2^{c-g}
+// — the WY form of the reference's chunk algebra (rwkv7_hf/self_chunk_rwkv7.py:85-134,
+// rwkv7_hf/dplr_prefill.py:221-311) with everything that does not depend on S
+// moved off the state's critical path, and one set of gated rows serving every
+// product (the per-channel scales fold into the state).  Exact while a chunk's
+// log2-decay span -gC stays within 240 (per-token w >= 2^-15 on average);
+// beyond that the factors clamp at 2^+-126.
 //
 // Mapping: one workgroup of 8 waves per (batch, head), specialised:
 // * waves 0-3 ("chain") hold the fp32 state — wave q owns 16 value rows, as
@@ -63,6 +63,8 @@ struct ChunkSlot {
   bf16x4 am[2][64];     // [hi/lo] A(M)
   bf16x4 aq[2][64];     // [hi/lo] A(Qm)
   f32x4 ec[4][4];       // [jt][kg] 2^gC of channels 16jt + 4kg + e
+  f32x4 pc[4][4];       // [jt][kg] 2^{gC - c}
+  f32x4 cen[4][4];      // [jt][kg] 2^c
 };
 
 struct ChunkShared {
@@ -249,14 +251,18 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
       }
       const bf16x4 vH = Z.vt[0][q][lane], vL = Z.vt[1][q][lane];
       const bf16x4 amH = Z.am[0][lane], amL = Z.am[1][lane], aqH = Z.aq[0][lane], aqL = Z.aq[1][lane];
-      f32x4 ec[4];
+      f32x4 ec[4], pc[4], cen[4];
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) ec[jt] = Z.ec[jt][kg];
+      for (int jt = 0; jt < 4; ++jt) {
+        ec[jt] = Z.ec[jt][kg];
+        pc[jt] = Z.pc[jt][kg];
+        cen[jt] = Z.cen[jt][kg];
+      }
       set_flag(&L.done[q][s], x);  // the operands are in registers
 
       bf16x4 SH[4], SL[4];
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) split_f4(S[jt], SH[jt], SL[jt]);
+      for (int jt = 0; jt < 4; ++jt) split_f4(S[jt] * cen[jt], SH[jt], SL[jt]);  // S' = S diag(2^c)
       Acc3 accU, accY;
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
@@ -273,7 +279,7 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
       for (int jt = 0; jt < 4; ++jt) {
         Acc3 acc;
         acc.add32(bkH[jt], bkL[jt], uvH, uvL);
-        S[jt] = S[jt] * ec[jt] + acc.sum();
+        S[jt] = S[jt] * ec[jt] + pc[jt] * acc.sum();
       }
       accY.add16(aqH, aqL, vH, vL);  // + Qm V
       const f32x4 Yv = accY.sum();
@@ -323,7 +329,7 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
   for (int x = p; x < nchunks; x += 4) {
     const bool ok = x * CH + t < T;
     // Wait until the chain waves have taken chunk x - NSLOT out of this slot;
-    // every result below is then stored as soon as it exists (Das and rs are
+    // every result below is then stored as soon as it exists (D(ac) and rc are
     // parked in the Wa / Rq areas until Wa and Rq replace them).
     const int s = x % NSLOT;
     for (int qq = 0; qq < 4; ++qq) wait_geq(&L.done[qq][s], x - NSLOT);
@@ -339,7 +345,7 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         const int jt = 2 * cc + jj;
-        f32x4 rc, kc, ac, bc, as, bd, kd, xv, rs, ecv;
+        f32x4 rc, kc, ac, bc, xv, ecv, pcv, cenv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           // inputs of token t, channel slot (jt, e), read from the raw rows here
@@ -353,40 +359,39 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
           const float gC = row_sum(lwv);
           const float cf = rintf(0.5f * gC);
           const int ci = (int)cf;
-          const float pv = __builtin_amdgcn_exp2f(clamp126(g - cf));
-          const float qv = __builtin_amdgcn_exp2f(clamp126(cf - g));
-          const float pp = row_shr<1>(pv);  // 2^{g_{t-1} - c}; lane 0 unused
+          const float xd = clamp126(g - cf);
+          const float pv = __builtin_amdgcn_exp2f(xd);
+          const float qv = __builtin_amdgcn_exp2f(-xd);
+          const float sh = row_shr<1>(pv);
+          const float pp = t == 0 ? __builtin_amdgcn_ldexpf(1.f, -ci) : sh;  // 2^{g_{t-1} - c}, g_{-1} = 0
           const float pC = __builtin_amdgcn_exp2f(clamp126(gC - cf));
-          const float al = -xkk;
-          const float be = xkk * xa;
           rc[e] = xr * pv;
           kc[e] = xk * qv;
-          ac[e] = al * pp;
-          bc[e] = be * qv;
-          rs[e] = __builtin_amdgcn_ldexpf(rc[e], ci);
-          as[e] = t == 0 ? al : __builtin_amdgcn_ldexpf(ac[e], ci);
-          const float dv = pC * qv;  // 2^{gC - g_t}
-          bd[e] = be * dv;
-          kd[e] = xk * dv;
+          ac[e] = -xkk * pp;
+          bc[e] = xkk * xa * qv;
           ecv[e] = __builtin_amdgcn_ldexpf(pC, ci);
+          pcv[e] = pC;
+          cenv[e] = __builtin_amdgcn_ldexpf(1.f, ci);
         }
         split_f4(rc, rcH[jj], rcL[jj]);
         split_f4(kc, kcH[jj], kcL[jj]);
         split_f4(ac, acH[jj], acL[jj]);
         split_f4(bc, bcH[jj], bcL[jj]);
-        bf16x4 hi, lo, hi2, lo2;
-        split_f4(as, hi, lo);
-        reinterpret_cast<bf16x4*>(&Z.wa[0][cc][lane])[jj] = pack_exact(mma16(hi, Ib, ZERO4));  // Das
-        reinterpret_cast<bf16x4*>(&Z.wa[1][cc][lane])[jj] = pack_exact(mma16(lo, Ib, ZERO4));
+        // transposed operands: D(ac) (parked in the Wa area), [D(bc) | D(kc)], D(v)
+        reinterpret_cast<bf16x4*>(&Z.wa[0][cc][lane])[jj] = pack_exact(mma16(acH[jj], Ib, ZERO4));
+        reinterpret_cast<bf16x4*>(&Z.wa[1][cc][lane])[jj] = pack_exact(mma16(acL[jj], Ib, ZERO4));
+        Z.bk[0][jt][lane] = cat(pack_exact(mma16(bcH[jj], Ib, ZERO4)), pack_exact(mma16(kcH[jj], Ib, ZERO4)));
+        Z.bk[1][jt][lane] = cat(pack_exact(mma16(bcL[jj], Ib, ZERO4)), pack_exact(mma16(kcL[jj], Ib, ZERO4)));
+        bf16x4 hi, lo;
         split_f4(xv, hi, lo);
         Z.vt[0][jt][lane] = pack_exact(mma16(hi, Ib, ZERO4));
         Z.vt[1][jt][lane] = pack_exact(mma16(lo, Ib, ZERO4));
-        split_f4(bd, hi, lo);
-        split_f4(kd, hi2, lo2);
-        Z.bk[0][jt][lane] = cat(pack_exact(mma16(hi, Ib, ZERO4)), pack_exact(mma16(hi2, Ib, ZERO4)));
-        Z.bk[1][jt][lane] = cat(pack_exact(mma16(lo, Ib, ZERO4)), pack_exact(mma16(lo2, Ib, ZERO4)));
-        *reinterpret_cast<f32x4*>(&Z.rq[jj][cc][lane]) = rs;  // rs, until Rq
-        if (t == 0) Z.ec[jt][kg] = ecv;
+        *reinterpret_cast<f32x4*>(&Z.rq[jj][cc][lane]) = rc;  // rc, until Rq
+        if (t == 0) {
+          Z.ec[jt][kg] = ecv;
+          Z.pc[jt][kg] = pcv;
+          Z.cen[jt][kg] = cenv;
+        }
       }
       const bf16x8 rH = cat(rcH[0], rcH[1]), rL = cat(rcL[0], rcL[1]);
       const bf16x8 kH = cat(kcH[0], kcH[1]), kL = cat(kcL[0], kcL[1]);
@@ -455,19 +460,19 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
     split_f4(mma3_16(AakH, AakL, AtH, AtL), AmH, AmL);
     split_f4(mma3_16(DtH, DtL, AqbH, AqbL), ApH, ApL);
 
-    // ---- Wa = T as and Rq = rs + Pm as (lane (t, sigma) layout) replace Das and rs
+    // ---- Wa = T ac and Rq = rc + Pm ac (lane (t, sigma) layout) replace D(ac) and rc
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
       const bf16x8 dH = Z.wa[0][cc][lane], dL = Z.wa[1][cc][lane];
-      const f32x4 rs0 = *reinterpret_cast<const f32x4*>(&Z.rq[0][cc][lane]);
-      const f32x4 rs1 = *reinterpret_cast<const f32x4*>(&Z.rq[1][cc][lane]);
+      const f32x4 rc0 = *reinterpret_cast<const f32x4*>(&Z.rq[0][cc][lane]);
+      const f32x4 rc1 = *reinterpret_cast<const f32x4*>(&Z.rq[1][cc][lane]);
       bf16x4 waH[2], waL[2], rqH[2], rqL[2];
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         const bf16x4 daH = {dH[4 * jj], dH[4 * jj + 1], dH[4 * jj + 2], dH[4 * jj + 3]};
         const bf16x4 daL = {dL[4 * jj], dL[4 * jj + 1], dL[4 * jj + 2], dL[4 * jj + 3]};
         split_f4(mma3_16(daH, daL, AtH, AtL), waH[jj], waL[jj]);
-        split_f4((jj ? rs1 : rs0) + mma3_16(daH, daL, ApH, ApL), rqH[jj], rqL[jj]);
+        split_f4((jj ? rc1 : rc0) + mma3_16(daH, daL, ApH, ApL), rqH[jj], rqL[jj]);
       }
       Z.wa[0][cc][lane] = cat(waH[0], waH[1]);
       Z.wa[1][cc][lane] = cat(waL[0], waL[1]);
