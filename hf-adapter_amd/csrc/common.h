@@ -166,6 +166,26 @@ __device__ __forceinline__ void round8(float (&v)[8]) {
 }  // namespace rwkv7mi
 
 namespace rwkv7mi {
+// ------------------------------------------------------ LoRA partial layout
+// The LoRA down projections split K = D into `ks` ranges; partial sums are
+// stored fp32 [problem][ks][rows][rank] (problems packed back to back).  The
+// up projection (lora.hip) and the fused decode (wkv7_decode.hip) both read
+// this layout.
+constexpr int LORA_ROWS = 32;  // rows per launch pair
+inline int64_t lora_tiles(int64_t nprob, const int64_t* ranks) {
+  int64_t t = 0;
+  for (int64_t i = 0; i < nprob; ++i) t += (ranks[i] + 15) / 16;
+  return t;
+}
+inline int lora_splits(int64_t tiles, int64_t D) {
+  // aim for 256-512 down workgroups, each split covering at least 128 inputs
+  int64_t ks = 1;
+  while (tiles * ks * 2 <= 512 && D / (ks * 2) >= 128) ks *= 2;
+  return (int)ks;
+}
+}  // namespace rwkv7mi
+
+namespace rwkv7mi {
 // ------------------------------------------------------------ MFMA types
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));

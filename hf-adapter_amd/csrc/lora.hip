@@ -19,7 +19,6 @@ namespace rwkv7mi {
 
 enum { LORA_ACT_NONE = 0, LORA_ACT_TANH = 1, LORA_ACT_SIGMOID = 2 };
 constexpr int LORA_MAXR = 256;   // largest rank
-constexpr int LORA_ROWS = 32;    // rows per launch pair
 
 struct LoraProb {
   const void* x;
@@ -212,22 +211,9 @@ __global__ __launch_bounds__(256) void lora_up_kernel(const LoraBatch B, int row
   }
 }
 
-static int lora_splits(int64_t tiles, int64_t D) {
-  // aim for 256-512 down workgroups, each split covering at least 128 inputs
-  int64_t ks = 1;
-  while (tiles * ks * 2 <= 512 && D / (ks * 2) >= 128) ks *= 2;
-  return (int)ks;
-}
-
 }  // namespace rwkv7mi
 
 using namespace rwkv7mi;
-
-static int64_t lora_tiles(int64_t nprob, const int64_t* ranks) {
-  int64_t t = 0;
-  for (int64_t i = 0; i < nprob; ++i) t += (ranks[i] + 15) / 16;
-  return t;
-}
 
 extern "C" size_t rwkv7mi_lora_workspace_bytes(int64_t nprob, const int64_t* ranks, int64_t rows, int64_t D) {
   if (nprob < 1 || nprob > 4 || !ranks || rows <= 0 || D <= 0) return 0;
@@ -238,17 +224,17 @@ extern "C" size_t rwkv7mi_lora_workspace_bytes(int64_t nprob, const int64_t* ran
   return (size_t)(ks * nr * sr) * sizeof(float);
 }
 
-extern "C" int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs, const void* const* w_down,
-                                  const void* const* w_up, const void* const* b_up, void* const* ys,
-                                  const int64_t* ranks, const int* act_down, const int* act_up, int64_t rows,
-                                  int64_t D, int64_t A, int act_dtype, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* const* w_down,
+                    const void* const* w_up, const void* const* b_up, void* const* ys, const int64_t* ranks,
+                    const int* act_down, const int* act_up, int64_t rows, int64_t D, int64_t A, int act_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream) {
   if (nprob < 1 || nprob > 4) return fail(RWKV7MI_EINVAL, "lora_multi: 1..4 problems");
-  if (!xs || !w_down || !w_up || !ys || !ranks || !act_down || !act_up)
+  if (!xs || !w_down || (up && (!w_up || !ys)) || !ranks || !act_down || !act_up)
     return fail(RWKV7MI_EINVAL, "lora_multi: null array");
   if (rows < 0 || D <= 0 || A <= 0 || D % 8 || D > (1 << 20) || A > (1 << 20))
     return fail(RWKV7MI_EINVAL, "lora_multi: bad shape (D a positive multiple of 8)");
   if (rows == 0) return RWKV7MI_OK;
+  if (!up && rows > LORA_ROWS) return fail(RWKV7MI_EINVAL, "lora_down_multi: at most 32 rows");
   if (!valid_dtype(act_dtype)) return fail(RWKV7MI_EINVAL, "lora_multi: bad dtype");
   LoraBatch batch{};
   int td = 0, tu = 0;
@@ -257,15 +243,16 @@ extern "C" int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs, const vo
   const int tiles_d = (int)lora_tiles(nprob, ranks);
   const int ks = lora_splits(tiles_d, D);
   for (int i = 0; i < nprob; ++i) {
-    if (!xs[i] || !w_down[i] || !w_up[i] || !ys[i]) return fail(RWKV7MI_EINVAL, "lora_multi: null pointer");
+    if (!xs[i] || !w_down[i] || (up && (!w_up[i] || !ys[i]))) return fail(RWKV7MI_EINVAL, "lora_multi: null pointer");
     if (ranks[i] <= 0 || ranks[i] % 8 || ranks[i] > LORA_MAXR)
       return fail(RWKV7MI_EINVAL, "lora_multi: rank must be a positive multiple of 8, at most 256");
     if (act_down[i] < 0 || act_down[i] > 2 || act_up[i] < 0 || act_up[i] > 2)
       return fail(RWKV7MI_EINVAL, "lora_multi: activation must be 0 none, 1 tanh or 2 sigmoid");
     if ((reinterpret_cast<uintptr_t>(xs[i]) | reinterpret_cast<uintptr_t>(w_down[i]) |
-         reinterpret_cast<uintptr_t>(w_up[i])) & 15)
+         reinterpret_cast<uintptr_t>(up ? w_up[i] : nullptr)) & 15)
       return fail(RWKV7MI_EINVAL, "lora_multi: x and weights must be 16-byte aligned");
-    batch.p[i] = LoraProb{xs[i], w_down[i], w_up[i], b_up ? b_up[i] : nullptr, ys[i], (int)ranks[i],
+    batch.p[i] = LoraProb{xs[i], w_down[i], up ? w_up[i] : nullptr, up && b_up ? b_up[i] : nullptr,
+                          up ? ys[i] : nullptr, (int)ranks[i],
                           act_down[i], act_up[i], td, tu, off};
     td += (int)((ranks[i] + 15) / 16);
     tu += (int)((A + 15) / 16);
@@ -286,7 +273,7 @@ extern "C" int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs, const vo
     LoraBatch bb = batch;
     for (int i = 0; i < nprob; ++i) {
       bb.p[i].x = reinterpret_cast<const char*>(batch.p[i].x) + r0 * D * esz;
-      bb.p[i].y = reinterpret_cast<char*>(batch.p[i].y) + r0 * A * esz;
+      if (up) bb.p[i].y = reinterpret_cast<char*>(batch.p[i].y) + r0 * A * esz;
       // partial tiles are packed [ks][nr][r] for this chunk's row count
       int64_t o2 = 0;
       for (int j = 0; j < i; ++j) o2 += (int64_t)ks * nr * ranks[j];
@@ -296,8 +283,9 @@ extern "C" int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs, const vo
     int rc = dispatch_dtype(act_dtype, [&](auto ta) {
       using TA = decltype(ta);
       hipStream_t s = as_stream(stream);
-#define LORA_GO(MT_)                                                                                  \
-  hipLaunchKernelGGL((lora_down_kernel<MT_, TA>), dim3(td, ks), dim3(256), 0, s, bb, (int)nr, part); \
+#define LORA_GO(MT_)                                                                                    \
+  hipLaunchKernelGGL((lora_down_kernel<MT_, TA>), dim3(td, ks), dim3(256), 0, s, bb, (int)nr, part);   \
+  if (up)                                                                                               \
   hipLaunchKernelGGL((lora_up_kernel<MT_, TA>), dim3(tu), dim3(256), 0, s, bb, (int)nr, (const float*)part)
       if (mt == 1) {
         LORA_GO(1);
@@ -310,4 +298,21 @@ extern "C" int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs, const vo
     if (rc) return rc;
   }
   return RWKV7MI_OK;
+}
+
+extern "C" int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs, const void* const* w_down,
+                                  const void* const* w_up, const void* const* b_up, void* const* ys,
+                                  const int64_t* ranks, const int* act_down, const int* act_up, int64_t rows,
+                                  int64_t D, int64_t A, int act_dtype, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  return lora_run(true, nprob, xs, w_down, w_up, b_up, ys, ranks, act_down, act_up, rows, D, A, act_dtype,
+                  workspace, workspace_bytes, stream);
+}
+
+extern "C" int rwkv7mi_lora_down_multi(int64_t nprob, const void* const* xs, const void* const* w_down,
+                                       const int64_t* ranks, const int* act_down, int64_t rows, int64_t D,
+                                       int act_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  int act_up[4] = {0, 0, 0, 0};
+  return lora_run(false, nprob, xs, w_down, nullptr, nullptr, nullptr, ranks, act_down, act_up, rows, D, 1,
+                  act_dtype, workspace, workspace_bytes, stream);
 }

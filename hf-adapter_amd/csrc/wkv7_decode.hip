@@ -19,6 +19,89 @@ enum { MODE_UPDATE = 0, MODE_PREP = 1, MODE_RAW = 2 };
 
 constexpr int HEAD = 64;
 
+// After staging: the state row update, y = S' r, and (output-prep modes) the
+// per-head GroupNorm, bonus and gate.  Lane t owns row i = t/4, key columns
+// j0 .. j0+15 of the head; s[] holds them on entry.
+template <bool PREP, typename TA>
+__device__ __forceinline__ void decode_core(float (&s)[16], const float* s_r, const float* s_w, const float* s_k,
+                                            const float* s_kk, const float* s_ka, const float* s_v, float corr,
+                                            float* s_red, float g_i, float gnw_i, float gnb_i, float eps,
+                                            float* state_out, int64_t soff, TA* out, int64_t vec) {
+  const int tid = threadIdx.x;
+  const int i = tid >> 2;
+  const int j0 = (tid & 3) * 16;
+  float dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) dot += s[j] * s_kk[j0 + j];
+  dot = group_sum<4>(dot);
+  const float vi = s_v[i];
+  float y = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float ns = s[j] * s_w[j0 + j] - dot * s_ka[j0 + j] + vi * s_k[j0 + j];
+    s[j] = ns;
+    y += ns * s_r[j0 + j];
+  }
+  y = group_sum<4>(y);
+  {
+    float4* dst = reinterpret_cast<float4*>(state_out + soff);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dst[q] = make_float4(s[4 * q], s[4 * q + 1], s[4 * q + 2], s[4 * q + 3]);
+  }
+
+  if constexpr (!PREP) {
+    if ((tid & 3) == 0) out[vec + i] = from_f32<TA>(y);
+  } else {
+    // GroupNorm over the head's 64 outputs (each row is replicated in 4 lanes).
+    const int wave = tid >> 6;
+    float ws = wave_sum(y) * 0.25f;
+    if ((tid & 63) == 0) s_red[wave] = ws;
+    __syncthreads();
+    const float mean = (s_red[0] + s_red[1] + s_red[2] + s_red[3]) * (1.0f / HEAD);
+    const float cen = y - mean;
+    float wv2 = wave_sum(cen * cen) * 0.25f;
+    if ((tid & 63) == 0) s_red[4 + wave] = wv2;
+    __syncthreads();
+    const float var = (s_red[4] + s_red[5] + s_red[6] + s_red[7]) * (1.0f / HEAD);
+    if ((tid & 3) == 0) {
+      float normed = cen * rsqrtf(var + eps);
+      float o = (normed * gnw_i + gnb_i + corr * vi) * g_i;
+      out[vec + i] = from_f32<TA>(o);
+    }
+  }
+}
+
+// kk = normalize(k_raw * k_k), k = k_raw * (1 + (a - 1) * k_a),
+// w = exp(-0.606531 * sigmoid(w_raw))  (rwkv7_hf/fused_recurrent_update.py:198-204);
+// v_mode 1 stores v as v_first, 2 mixes v toward v_first by v_gate.  Called by
+// the first wave (lane = channel c).
+template <typename TA>
+__device__ __forceinline__ void stage_raw(int c, float rv, float wr, float kraw, float vv, float av, float kkw,
+                                          float kaw, float rkw, int v_mode, TA* v_first, float vgate,
+                                          int64_t vec, float* s_r, float* s_w, float* s_k, float* s_kk,
+                                          float* s_ka, float* s_v, float* s_corr) {
+  float kku = kraw * kkw;
+  float nrm = sqrtf(wave_sum(kku * kku));
+  const float kkv = kku / fmaxf(nrm, 1.0e-12f);
+  const float kv = kraw * (1.0f + (av - 1.0f) * kaw);
+  const float wv = expf(-0.606531f * (1.0f / (1.0f + expf(-wr))));
+  if (v_mode == 1) {
+    v_first[vec + c] = from_f32<TA>(vv);
+  } else if (v_mode == 2) {
+    float vf = to_f32(v_first[vec + c]);
+    vv = vv + (vf - vv) * vgate;
+  }
+  s_r[c] = rv;
+  s_w[c] = wv;
+  s_k[c] = kv;
+  s_kk[c] = kkv;
+  s_ka[c] = kkv * av;
+  s_v[c] = vv;
+  // bonus scale sum_c r*k*r_k (rwkv7_hf/fused_recurrent_update.py:911)
+  float corr = wave_sum(rv * kv * rkw);
+  if (c == 0) *s_corr = corr;
+}
+
 template <int MODE, typename TA, typename TW, typename TP>
 __global__ __launch_bounds__(256) void wkv7_decode_kernel(
     const TA* __restrict__ r, const TW* __restrict__ w, const TA* __restrict__ k,
@@ -63,82 +146,172 @@ __global__ __launch_bounds__(256) void wkv7_decode_kernel(
     float rv = ld(r, vec + c);
     float av = ld(a, vec + c);
     float vv = ld(v, vec + c);
-    float kv, kkv, wv;
     if constexpr (MODE == MODE_RAW) {
-      // kk = normalize(k_raw * k_k), k = k_raw * (1 + (a - 1) * k_a),
-      // w = exp(-0.606531 * sigmoid(w_raw))  (rwkv7_hf/fused_recurrent_update.py:198-204)
-      float kraw = ld(k, vec + c);
-      float kku = kraw * ld(k_k, (int64_t)h * HEAD + c);
-      float nrm = sqrtf(wave_sum(kku * kku));
-      kkv = kku / fmaxf(nrm, 1.0e-12f);
-      kv = kraw * (1.0f + (av - 1.0f) * ld(k_a, (int64_t)h * HEAD + c));
-      float wr = ld(w, vec + c);
-      wv = expf(-0.606531f * (1.0f / (1.0f + expf(-wr))));
-      if (v_mode == 1) {
-        v_first[vec + c] = from_f32<TA>(vv);
-      } else if (v_mode == 2) {
-        float vf = to_f32(v_first[vec + c]);
-        float gt = ld(v_gate, vec + c);
-        vv = vv + (vf - vv) * gt;
-      }
+      const int64_t pc = (int64_t)h * HEAD + c;
+      stage_raw<TA>(c, rv, ld(w, vec + c), ld(k, vec + c), vv, av, ld(k_k, pc), ld(k_a, pc), ld(r_k, pc), v_mode,
+                    v_first, v_mode == 2 ? ld(v_gate, vec + c) : 0.f, vec, s_r, s_w, s_k, s_kk, s_ka, s_v, &s_corr);
     } else {
+      float kv, kkv, wv;
       kv = ld(k, vec + c);
       kkv = ld(kk, vec + c);
       wv = ld(w, vec + c);
-    }
-    s_r[c] = rv;
-    s_w[c] = wv;
-    s_k[c] = kv;
-    s_kk[c] = kkv;
-    s_ka[c] = kkv * av;
-    s_v[c] = vv;
-    if constexpr (MODE != MODE_UPDATE) {
-      // bonus scale sum_c r*k*r_k (rwkv7_hf/fused_recurrent_update.py:911)
-      float corr = wave_sum(rv * kv * ld(r_k, (int64_t)h * HEAD + c));
-      if (c == 0) s_corr = corr;
+      s_r[c] = rv;
+      s_w[c] = wv;
+      s_k[c] = kv;
+      s_kk[c] = kkv;
+      s_ka[c] = kkv * av;
+      s_v[c] = vv;
+      if constexpr (MODE != MODE_UPDATE) {
+        // bonus scale sum_c r*k*r_k (rwkv7_hf/fused_recurrent_update.py:911)
+        float corr = wave_sum(rv * kv * ld(r_k, (int64_t)h * HEAD + c));
+        if (c == 0) s_corr = corr;
+      }
     }
   }
   __syncthreads();
+  decode_core<MODE != MODE_UPDATE, TA>(s, s_r, s_w, s_k, s_kk, s_ka, s_v, MODE != MODE_UPDATE ? s_corr : 0.f, s_red,
+                                       g_i, gnw_i, gnb_i, eps, state_out, soff, out, vec);
+}
 
-  float dot = 0.f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) dot += s[j] * s_kk[j0 + j];
-  dot = group_sum<4>(dot);
-  const float vi = s_v[i];
-  float y = 0.f;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    float ns = s[j] * s_w[j0 + j] - dot * s_ka[j0 + j] + vi * s_k[j0 + j];
-    s[j] = ns;
-    y += ns * s_r[j0 + j];
-  }
-  y = group_sum<4>(y);
+// ---------------------------------------------------------------------------
+// Decode with the W/A/G/V LoRA up projections fused in (rwkv7_hf/fused_lora.py
+// :706 fused_wavg_lora, then fused_recurrent_output_prepare_raw).  The down
+// projections' fp32 partials (lora.hip, [problem][ks][rows][rank]) are summed
+// in fixed order, act_down applied and rounded to the activation dtype (the
+// reference's mid tensor); each (batch, head) workgroup then computes only its
+// own 64 channels of every up projection, y_p = act_up_p(mid_p Wu_p^T + b_p),
+// rounded to the activation dtype as the reference's tensors are.
+// Problems: 0 w_raw, 1 a, 2 g, 3 v_gate (the last only with v_mode 2).
+// Wave p handles problem p end to end (lane c = output channel h*64 + c), so
+// its pointers and rank are wave-uniform and it needs no barrier until the
+// four results meet for the state update.
+constexpr int DL_MAXR = 128;  // largest rank on this route
+constexpr int DL_ZB = 16;     // K-split partials loaded per batch
+
+struct DecLora {
+  const float* part;
+  const void* wu[4];
+  const void* bu[4];
+  int64_t part_off[4];  // floats
+  int64_t part_total;   // floats of the whole partial buffer
+  int rank[4], act_d[4], act_u[4];
+  int nprob, ks, rows;
+};
+
+__device__ __forceinline__ float dl_act(float v, int act) {
+  if (act == 1) return tanhf(v);
+  if (act == 2) return 1.0f / (1.0f + expf(-v));
+  return v;
+}
+
+template <typename TA, typename TP>
+__global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
+    const TA* __restrict__ r, const TA* __restrict__ k, const TA* __restrict__ v, const DecLora LA,
+    const float* state_in, float* state_out, const TP* __restrict__ k_k, const TP* __restrict__ k_a,
+    const TP* __restrict__ r_k, const TP* __restrict__ gn_w, const TP* __restrict__ gn_b, TA* __restrict__ out,
+    TA* v_first, int v_mode, int H, float eps) {
+  __shared__ float s_r[HEAD], s_w[HEAD], s_k[HEAD], s_kk[HEAD], s_ka[HEAD], s_v[HEAD];
+  __shared__ float s_red[8];
+  __shared__ float s_corr;
+  __shared__ __align__(16) float s_mid[4][DL_MAXR];
+  __shared__ float s_lo[4][HEAD];
+
+  const int bh = blockIdx.x;
+  const int b = bh / H;
+  const int h = bh % H;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int64_t vec = (int64_t)bh * HEAD;
+  const int i = tid >> 2;
+  const int j0 = (tid & 3) * 16;
+  const int64_t soff = ((int64_t)bh * HEAD + i) * HEAD + j0;
+
+  // state rows, per-row output parameters and channel `lane` of this head's
+  // vectors (every wave loads them; only the first uses them) — no branches,
+  // so all of these loads are in flight together with the LoRA loads below
+  float s[16];
   {
-    float4* dst = reinterpret_cast<float4*>(state_out + soff);
+    const float4* src = reinterpret_cast<const float4*>(state_in + soff);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = make_float4(s[4 * q], s[4 * q + 1], s[4 * q + 2], s[4 * q + 3]);
-  }
-
-  if constexpr (MODE == MODE_UPDATE) {
-    if ((tid & 3) == 0) out[vec + i] = from_f32<TA>(y);
-  } else {
-    // GroupNorm over the head's 64 outputs (each row is replicated in 4 lanes).
-    const int wave = tid >> 6;
-    float ws = wave_sum(y) * 0.25f;
-    if ((tid & 63) == 0) s_red[wave] = ws;
-    __syncthreads();
-    const float mean = (s_red[0] + s_red[1] + s_red[2] + s_red[3]) * (1.0f / HEAD);
-    const float cen = y - mean;
-    float wv2 = wave_sum(cen * cen) * 0.25f;
-    if ((tid & 63) == 0) s_red[4 + wave] = wv2;
-    __syncthreads();
-    const float var = (s_red[4] + s_red[5] + s_red[6] + s_red[7]) * (1.0f / HEAD);
-    if ((tid & 3) == 0) {
-      float normed = cen * rsqrtf(var + eps);
-      float o = (normed * gnw_i + gnb_i + s_corr * vi) * g_i;
-      out[vec + i] = from_f32<TA>(o);
+    for (int q = 0; q < 4; ++q) {
+      float4 t4 = src[q];
+      s[4 * q + 0] = t4.x; s[4 * q + 1] = t4.y; s[4 * q + 2] = t4.z; s[4 * q + 3] = t4.w;
     }
   }
+  const int64_t pi = (int64_t)h * HEAD + i;
+  const float gnw_i = ld(gn_w, pi), gnb_i = ld(gn_b, pi);
+  const int64_t pc = (int64_t)h * HEAD + lane;
+  const float rv = ld(r, vec + lane), kraw = ld(k, vec + lane), vv = ld(v, vec + lane);
+  const float kkw = ld(k_k, pc), kaw = ld(k_a, pc), rkw = ld(r_k, pc);
+
+  const bool active = wave < LA.nprob;  // wave-uniform
+  const int rp = active ? LA.rank[wave] : 0;
+  // up-projection row h*64 + lane of Wu_p: rank elements in 8-element chunks
+  float wrow[DL_MAXR];
+  {
+    const __amdgpu_buffer_rsrc_t wr =
+        make_rsrc(active ? LA.wu[wave] : LA.wu[0], (uint32_t)((int64_t)H * HEAD * rp * (int64_t)sizeof(TA)));
+    const uint32_t e0 = (uint32_t)((int64_t)(h * HEAD + lane) * rp);
+#pragma unroll
+    for (int e = 0; e < DL_MAXR; e += 8) {
+      float f[8];
+      buf_ld8(wr, e0 + e, e < rp, (const TA*)nullptr, f);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) wrow[e + u] = f[u];
+    }
+  }
+  // mid_p[kk] for kk = lane, lane + 64: all K-split partials of this batch row,
+  // loaded at once (an out-of-range offset reads zero), summed in z order
+  {
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(LA.part, (uint32_t)LA.part_total * 4u);
+    const uint32_t zs = (uint32_t)(LA.rows * rp);
+    const uint32_t base = (uint32_t)((active ? LA.part_off[wave] : 0) + (int64_t)b * rp);
+    float acc[2] = {0.f, 0.f};
+    for (int z0 = 0; z0 < LA.ks; z0 += DL_ZB) {
+      float t[2][DL_ZB];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int zz = 0; zz < DL_ZB; ++zz) {
+          const bool ok = lane + 64 * u < rp && z0 + zz < LA.ks;
+          t[u][zz] = buf_ldf(pr, ok ? (base + (uint32_t)(z0 + zz) * zs + lane + 64u * u) * 4u : BUF_OOB);
+        }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int zz = 0; zz < DL_ZB; ++zz) acc[u] += t[u][zz];  // past-the-end terms are +0
+    }
+    if (active) {
+      const int ad = LA.act_d[wave];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        if (lane + 64 * u < rp) s_mid[wave][lane + 64 * u] = to_f32(from_f32<TA>(dl_act(acc[u], ad)));
+    }
+  }
+  // this wave's problem, channel `lane` (the wave reads its own s_mid row: LDS
+  // operations of one wave complete in order, so no barrier is needed)
+  if (active) {
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < DL_MAXR; e += 4) {
+      if (e < rp) {
+        const float4 m4 = *reinterpret_cast<const float4*>(&s_mid[wave][e]);  // broadcast
+        acc += m4.x * wrow[e] + m4.y * wrow[e + 1] + m4.z * wrow[e + 2] + m4.w * wrow[e + 3];
+      }
+    }
+    const TA* bias = reinterpret_cast<const TA*>(LA.bu[wave]);
+    if (bias) acc += to_f32(bias[(int64_t)h * HEAD + lane]);
+    s_lo[wave][lane] = to_f32(from_f32<TA>(dl_act(acc, LA.act_u[wave])));
+  }
+  __syncthreads();
+
+  if (tid < HEAD)
+    stage_raw<TA>(tid, rv, s_lo[0][tid], kraw, vv, s_lo[1][tid], kkw, kaw, rkw, v_mode, v_first,
+                  v_mode == 2 ? s_lo[3][tid] : 0.f, vec, s_r, s_w, s_k, s_kk, s_ka, s_v, &s_corr);
+  __syncthreads();
+  decode_core<true, TA>(s, s_r, s_w, s_k, s_kk, s_ka, s_v, s_corr, s_red, s_lo[2][i], gnw_i, gnb_i, eps,
+                        state_out, soff, out, vec);
 }
 
 template <int MODE>
@@ -221,4 +394,59 @@ extern "C" int rwkv7mi_wkv7_decode_output_prepare_raw(
   return launch_decode<MODE_RAW>(r, w_raw, k_raw, v, nullptr, a, state_in, state_out, g, r_k, k_k,
                                  k_a, gn_w, gn_b, out, v_first, v_gate, v_mode, B, H, N, eps,
                                  act_dtype, act_dtype, param_dtype, stream);
+}
+
+extern "C" int rwkv7mi_wkv7_decode_lora_output_prepare(
+    const void* r, const void* k_raw, const void* v, const float* lora_part, int64_t nprob,
+    const int64_t* ranks, const void* const* w_up, const void* const* b_up, const int* act_down,
+    const int* act_up, int64_t D, const float* state_in, float* state_out, const void* k_k, const void* k_a,
+    const void* r_k, const void* gn_w, const void* gn_b, void* out, void* v_first, int v_mode, int64_t B,
+    int64_t H, int64_t N, float eps, int act_dtype, int param_dtype, void* stream) {
+  if (N != HEAD) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: head size must be 64");
+  if (B < 0 || H <= 0 || D <= 0) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: bad B/H/D");
+  if (B == 0) return RWKV7MI_OK;
+  if (B > LORA_ROWS) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: at most 32 rows");
+  if (!r || !k_raw || !v || !lora_part || !ranks || !w_up || !act_down || !act_up || !state_in || !state_out ||
+      !k_k || !k_a || !r_k || !gn_w || !gn_b || !out)
+    return fail(RWKV7MI_EINVAL, "wkv7 decode lora: null pointer");
+  if (v_mode < 0 || v_mode > 2) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: bad v_mode");
+  if (nprob != 3 && nprob != 4) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: 3 or 4 LoRA problems");
+  if (v_mode == 2 && nprob != 4) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: v_mode 2 needs the v LoRA");
+  if (v_mode != 0 && !v_first) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: v_mode needs v_first");
+  if ((reinterpret_cast<uintptr_t>(state_in) | reinterpret_cast<uintptr_t>(state_out)) & 15)
+    return fail(RWKV7MI_EINVAL, "wkv7 decode lora: state must be 16-byte aligned");
+  if (B * H > INT32_MAX) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: B*H too large");
+  DecLora la{};
+  la.part = lora_part;
+  la.nprob = (int)nprob;
+  la.rows = (int)B;
+  la.ks = lora_splits(lora_tiles(nprob, ranks), D);
+  int64_t off = 0;
+  for (int p = 0; p < nprob; ++p) {
+    if (ranks[p] <= 0 || ranks[p] % 8 || ranks[p] > DL_MAXR || !w_up[p])
+      return fail(RWKV7MI_EINVAL, "wkv7 decode lora: ranks must be positive multiples of 8, at most 128");
+    if (act_down[p] < 0 || act_down[p] > 2 || act_up[p] < 0 || act_up[p] > 2)
+      return fail(RWKV7MI_EINVAL, "wkv7 decode lora: activation must be 0 none, 1 tanh or 2 sigmoid");
+    if (reinterpret_cast<uintptr_t>(w_up[p]) & 15)
+      return fail(RWKV7MI_EINVAL, "wkv7 decode lora: up weights must be 16-byte aligned");
+    la.wu[p] = w_up[p];
+    la.bu[p] = b_up ? b_up[p] : nullptr;
+    la.rank[p] = (int)ranks[p];
+    la.act_d[p] = act_down[p];
+    la.act_u[p] = act_up[p];
+    la.part_off[p] = off;
+    off += (int64_t)la.ks * B * ranks[p];
+  }
+  la.part_total = off;
+  return dispatch_dtype(act_dtype, [&](auto ta) {
+    using TA = decltype(ta);
+    return dispatch_dtype(param_dtype, [&](auto tp) {
+      using TP = decltype(tp);
+      hipLaunchKernelGGL((wkv7_decode_lora_kernel<TA, TP>), dim3((unsigned)(B * H)), dim3(256), 0,
+                         as_stream(stream), (const TA*)r, (const TA*)k_raw, (const TA*)v, la, state_in, state_out,
+                         (const TP*)k_k, (const TP*)k_a, (const TP*)r_k, (const TP*)gn_w, (const TP*)gn_b,
+                         (TA*)out, (TA*)v_first, v_mode, (int)H, eps);
+      return check_launch("wkv7_decode_lora_kernel");
+    });
+  });
 }

@@ -61,6 +61,11 @@ SIGNATURES = {
     "rwkv7mi_mm4_dequant": (_i32, [_c_p] * 6 + [_i64, _i64, _i32, _i32, _c_p]),
     "rwkv7mi_lora_workspace_bytes": (_sz, [_i64, _c_p, _i64, _i64]),
     "rwkv7mi_lora_multi": (_i32, [_i64] + [_c_p] * 8 + [_i64, _i64, _i64, _i32, _c_p, _sz, _c_p]),
+    "rwkv7mi_lora_down_multi": (_i32, [_i64] + [_c_p] * 4 + [_i64, _i64, _i32, _c_p, _sz, _c_p]),
+    "rwkv7mi_wkv7_decode_lora_output_prepare": (
+        _i32,
+        [_c_p] * 4 + [_i64] + [_c_p] * 5 + [_i64] + [_c_p] * 9 + [_i32, _i64, _i64, _i64, _f32, _i32, _i32, _c_p],
+    ),
     "rwkv7mi_w4g_pack": (_i32, [_c_p, _i64, _i64, _i64, _i32, _c_p, _c_p, _c_p]),
     "rwkv7mi_w4g_matmul": (
         _i32,

@@ -57,6 +57,52 @@ def lora_multi(xs, downs, ups, biases, outs, acts_down, acts_up):
     return outs
 
 
+def fused_lora_decode_supported(ranks, rows: int) -> bool:
+    """Whether ``fused_wavg_lora_output_prepare_raw`` takes these shapes."""
+    ranks = [int(r) for r in ranks]
+    return 0 < int(rows) <= 32 and len(ranks) in (3, 4) and all(0 < r <= 128 and r % 8 == 0 for r in ranks)
+
+
+def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, state, k_k, k_a, r_k,
+                                       group_norm_weight, group_norm_bias, *, eps: float, out, state_out=None,
+                                       v_first=None, v_mode: int = 0):
+    """``fused_wavg_lora`` (rwkv7_hf/fused_lora.py:706) followed by
+    ``fused_recurrent_output_prepare_raw`` (fused_recurrent_update.py:1089) in two
+    launches: the split-K down projections, then one decode kernel in which each
+    (batch, head) workgroup computes its 64 channels of the W/A/G/V up projections
+    before the state update.  ``xs``/``downs``/``ups``/``biases`` are in the order
+    W, A, G[, V]; activations are the reference's (tanh/none, none/sigmoid,
+    sigmoid/none, none/sigmoid).  Returns ``(out [B, H*N], new_state)``."""
+    k = len(xs)
+    rows, D = (int(s) for s in xs[0].shape)
+    ranks = [int(d.shape[0]) for d in downs]
+    if not fused_lora_decode_supported(ranks, rows):
+        raise ValueError("fused LoRA decode: rows <= 32, 3 or 4 ranks, multiples of 8 up to 128")
+    B, H, N = (int(x) for x in state.shape[:3])
+    if rows != B or int(r.numel()) != B * H * N:
+        raise ValueError("fused LoRA decode: rows must match the state batch")
+    acts_down = [ACT_TANH, ACT_NONE, ACT_SIGMOID, ACT_NONE][:k]
+    acts_up = [ACT_NONE, ACT_SIGMOID, ACT_NONE, ACT_SIGMOID][:k]
+    hidden = H * N
+    pdt = k_k.dtype
+    kk_s, ka, rk, gnw, gnb = (t.reshape(hidden).to(pdt).contiguous()
+                              for t in (k_k, k_a, r_k, group_norm_weight, group_norm_bias))
+    _lib.require_gpu(r, k_raw, v, *xs, *downs, *ups, state, out, name="fused_wavg_lora_output_prepare_raw")
+    ws = _ws.reserve(xs[0].device, lora_workspace_bytes(ranks, rows, D), slot="lora")
+    s = _lib.stream_of(xs[0])
+    rk_arr = (ctypes.c_int64 * k)(*ranks)
+    _lib.call("rwkv7mi_lora_down_multi", k, _lib.ptr_array(xs), _lib.ptr_array(downs), rk_arr,
+              (ctypes.c_int * k)(*acts_down), rows, D, _lib.dtype_code(xs[0]), _lib.ptr(ws), int(ws.numel()), s)
+    new_state = state if state_out is None else state_out
+    _lib.call("rwkv7mi_wkv7_decode_lora_output_prepare",
+              _lib.ptr(r), _lib.ptr(k_raw), _lib.ptr(v), _lib.ptr(ws), k, rk_arr, _lib.ptr_array(ups),
+              _lib.ptr_array(biases), (ctypes.c_int * k)(*acts_down), (ctypes.c_int * k)(*acts_up), D,
+              _lib.ptr(state), _lib.ptr(new_state), _lib.ptr(kk_s), _lib.ptr(ka), _lib.ptr(rk), _lib.ptr(gnw),
+              _lib.ptr(gnb), _lib.ptr(out), _lib.ptr(v_first), int(v_mode), B, H, N, float(eps),
+              _lib.dtype_code(r), _lib.dtype_code(kk_s), s)
+    return out, new_state
+
+
 def _flat(x, name):
     had_seq = x.dim() == 3
     x2 = x.reshape(-1, int(x.shape[-1]))

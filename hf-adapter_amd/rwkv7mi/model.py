@@ -24,7 +24,8 @@ import torch
 from . import _lib
 from . import workspace as _ws
 from .fused_decode_norm_mix import fused_attn_norm_mix6_decode, fused_ffn_add_norm_mix_decode, layer_norm
-from .fused_lora import ACT_NONE, ACT_SIGMOID, ACT_TANH, dense_multi, lora_multi, lora_workspace_bytes
+from .fused_lora import (ACT_NONE, ACT_SIGMOID, ACT_TANH, dense_multi, fused_lora_decode_supported,
+                         fused_wavg_lora_output_prepare_raw, lora_multi, lora_workspace_bytes)
 from .fused_output import fused_attn_output_prepare
 from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
@@ -332,6 +333,8 @@ class NativeRWKV7ForCausalLM:
         self.dtype = dtype
         # run the decode LoRA projections on a second stream beside R/K/V
         self.lora_side_stream = False
+        # decode: LoRA up projections inside the wkv kernel (when the shapes allow)
+        self.fused_lora_decode = True
         dev = self.device
 
         def get(name):
@@ -474,23 +477,33 @@ class NativeRWKV7ForCausalLM:
                                         pre_norm_weight=L.pre[0] if L.pre else None,
                                         pre_norm_bias=L.pre[1] if L.pre else None)
             xr, xw, xk, xv, xa, xg = (mixb[q] for q in range(6))
-            if self.lora_side_stream:
-                # the LoRA projections depend only on the mixes: a second stream
-                # (a parallel branch of the captured graph) runs them beside R/K/V
-                ev_in.record(main)
-                side.wait_event(ev_in)
-                with torch.cuda.stream(side):
-                    self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
-                    ev_out.record(side)
+            n = len(L.lora_down)
+            if (self.fused_lora_decode and not self.lora_side_stream
+                    and fused_lora_decode_supported([int(d.shape[0]) for d in L.lora_down], B)):
+                # LoRA down (split-K launch), then the up projections inside the wkv kernel
                 QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
-                main.wait_event(ev_out)
+                fused_wavg_lora_output_prepare_raw(
+                    rkv[0], rkv[1], rkv[2], [xw, xa, xg, xv][:n], L.lora_down, L.lora_up, L.lora_bias, state[i],
+                    L.k_k, L.k_a, L.r_k, L.gn[0], L.gn[1], eps=N * 1e-5, out=prep, state_out=state[i],
+                    v_first=v_first, v_mode=1 if i == 0 else 2)
             else:
-                QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
-                self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
-            fused_recurrent_output_prepare_raw(
-                rkv[0], lora[0], rkv[1], rkv[2], lora[1], state[i], lora[2], L.k_k, L.k_a, L.r_k, L.gn[0],
-                L.gn[1], eps=N * 1e-5, state_out=state[i], out=prep.view(B, H, N),
-                v_first=v_first, v_gate=lora[3] if i > 0 else None, v_mode=1 if i == 0 else 2)
+                if self.lora_side_stream:
+                    # the LoRA projections depend only on the mixes: a second stream
+                    # (a parallel branch of the captured graph) runs them beside R/K/V
+                    ev_in.record(main)
+                    side.wait_event(ev_in)
+                    with torch.cuda.stream(side):
+                        self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
+                        ev_out.record(side)
+                    QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
+                    main.wait_event(ev_out)
+                else:
+                    QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
+                    self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
+                fused_recurrent_output_prepare_raw(
+                    rkv[0], lora[0], rkv[1], rkv[2], lora[1], state[i], lora[2], L.k_k, L.k_a, L.r_k, L.gn[0],
+                    L.gn[1], eps=N * 1e-5, state_out=state[i], out=prep.view(B, H, N),
+                    v_first=v_first, v_gate=lora[3] if i > 0 else None, v_mode=1 if i == 0 else 2)
             L.o_proj.apply(prep, x, residual=x)
             fused_ffn_add_norm_mix_decode(x, None, xpf[i], L.ln2[0], L.ln2[1], L.fx_k, eps=eps, mixed=bufs["fk"])
             L.key.apply(bufs["fk"], bufs["kf"], act=3)

@@ -100,6 +100,25 @@ int rwkv7mi_wkv7_decode_output_prepare_raw(
     int v_mode, int64_t B, int64_t H, int64_t N, float eps, int act_dtype,
     int param_dtype, void* stream);
 
+/* rwkv7mi_wkv7_decode_output_prepare_raw with the W/A/G/V LoRA up projections
+ * fused in: the second half of fused_wavg_lora (rwkv7_hf/fused_lora.py:706)
+ * followed by fused_recurrent_output_prepare_raw (fused_recurrent_update.py
+ * :1089).  lora_part holds the partials of rwkv7mi_lora_down_multi over the
+ * same (nprob, ranks, rows = B, D); problems 0 w_raw, 1 a, 2 g, 3 v_gate with
+ * w_up[p] [H*N, rank_p], b_up[p] [H*N] or NULL, activations 0 none, 1 tanh,
+ * 2 sigmoid.  Each (batch, head) workgroup computes its own 64 channels of
+ * every up projection, rounded to act_dtype as the reference's tensors are.
+ * B <= 32; ranks multiples of 8, at most 128; nprob 3 or 4 (4 when
+ * v_mode == 2). */
+int rwkv7mi_wkv7_decode_lora_output_prepare(
+    const void* r, const void* k_raw, const void* v, const float* lora_part,
+    int64_t nprob, const int64_t* ranks, const void* const* w_up,
+    const void* const* b_up, const int* act_down, const int* act_up, int64_t D,
+    const float* state_in, float* state_out, const void* k_k, const void* k_a,
+    const void* r_k, const void* gn_w, const void* gn_b, void* out, void* v_first,
+    int v_mode, int64_t B, int64_t H, int64_t N, float eps, int act_dtype,
+    int param_dtype, void* stream);
+
 /* ----------------------------------------------------- wkv7 sequence scans */
 
 /* Sequential on-chip scan over T tokens (T x the decode update), y [B,T,H,N].
@@ -255,6 +274,16 @@ int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs,
                        const int* act_up, int64_t rows, int64_t D, int64_t A,
                        int act_dtype, void* workspace, size_t workspace_bytes,
                        void* stream);
+
+/* The down projections of rwkv7mi_lora_multi alone (the first half of
+ * fused_wavg_lora, rwkv7_hf/fused_lora.py:706): fp32 partial sums
+ * [problem][ks][rows][rank] in the workspace, for
+ * rwkv7mi_wkv7_decode_lora_output_prepare.  rows <= 32. */
+int rwkv7mi_lora_down_multi(int64_t nprob, const void* const* xs,
+                            const void* const* w_down, const int64_t* ranks,
+                            const int* act_down, int64_t rows, int64_t D,
+                            int act_dtype, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* ---------------------------------------------------------- W4 group-128 */
 

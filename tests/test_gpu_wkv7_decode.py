@@ -140,6 +140,85 @@ def test_decode_output_prepare_raw(oracle, v_mode):
         assert torch.equal(vf.reshape(B, H, N), T[3])
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,v_mode,nl", [(1, 2, 4), (3, 2, 4), (8, 1, 3), (32, 2, 4), (2, 0, 3)])
+@pytest.mark.parametrize("ranks", [(64, 64, 128, 32), (24, 128, 8, 96)])
+def test_decode_fused_lora(oracle, dt, B, v_mode, nl, ranks):
+    """LoRA up projections fused into the decode kernel == the fp64 oracle composition
+    (LoRA, then the raw decode prep) with the reference's roundings of the mid and
+    output tensors to the activation dtype, and == the unfused kernels."""
+    from rwkv7mi import fused_recurrent_output_prepare_raw
+    from rwkv7mi.fused_lora import fused_wavg_lora_output_prepare_raw, lora_multi
+
+    rng = np.random.default_rng(B * 11 + v_mode + nl)
+    H, N, D = 4, 64, 512
+    A = H * N
+    ranks = ranks[:nl]
+    xs = [_t(_vec(rng, (B, D), 1.0), dt) for _ in range(nl)]
+    downs = [_t(rng.standard_normal((r, D)) * 0.05, dt) for r in ranks]
+    ups = [_t(rng.standard_normal((A, r)) * 0.1, dt) for r in ranks]
+    biases = [_t(rng.standard_normal(A) * 0.1, dt), _t(rng.standard_normal(A) * 0.1, dt), None,
+              _t(rng.standard_normal(A) * 0.1, dt)][:nl]
+    r, k_raw, v = (_t(_vec(rng, (B, A)), dt) for _ in range(3))
+    state = rng.standard_normal((B, H, N, N)) * 0.1
+    k_k = _t(rng.standard_normal((H, N)), dt)
+    k_a = _t(rng.standard_normal((H, N)) * 0.1, dt)
+    r_k = _t(rng.standard_normal((H, N)) * 0.1, dt)
+    gn_w, gn_b = _t(rng.standard_normal(A), dt), _t(rng.standard_normal(A), dt)
+    v_first0 = _vec(rng, (B, A))
+    eps = N * 1e-5
+    vf = _t(v_first0, dt)
+    out = torch.empty(B, A, device="cuda", dtype=dt)
+    st = _t(state, torch.float32)
+    fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, st, k_k, k_a, r_k, gn_w, gn_b,
+                                       eps=eps, out=out, v_first=vf if v_mode else None, v_mode=v_mode)
+    # unfused kernels on the same inputs
+    lo = [torch.empty(B, A, device="cuda", dtype=dt) for _ in range(nl)]
+    acts_d, acts_u = [1, 0, 2, 0][:nl], [0, 2, 0, 2][:nl]
+    lora_multi(xs, downs, ups, biases, lo, acts_d, acts_u)
+    vf2 = _t(v_first0, dt)
+    out2, st2 = fused_recurrent_output_prepare_raw(
+        r.view(B, H, N), lo[0].view(B, H, N), k_raw.view(B, H, N), v.view(B, H, N), lo[1].view(B, H, N),
+        _t(state, torch.float32), lo[2].view(B, H, N), k_k, k_a, r_k, gn_w, gn_b, eps=eps,
+        v_first=vf2 if v_mode else None, v_gate=lo[3] if v_mode == 2 else None, v_mode=v_mode)
+    torch.cuda.synchronize()
+    # oracle: fp64 LoRA with the mid / output tensors rounded to dt, then the decode prep
+    rnd = lambda a: _f64(torch.tensor(a, dtype=dt))
+    sig = lambda z: 1 / (1 + np.exp(-z))
+    act = {0: lambda z: z, 1: np.tanh, 2: sig}
+    ys = []
+    for q in range(nl):
+        mid = rnd(act[acts_d[q]](_f64(xs[q]) @ _f64(downs[q]).T))
+        y = mid @ _f64(ups[q]).T + (0 if biases[q] is None else _f64(biases[q]))
+        ys.append(rnd(act[acts_u[q]](y)))
+    kk, k, w = oracle.decode_raw_prep(_f64(k_raw).reshape(B, H, N), ys[0].reshape(B, H, N),
+                                      ys[1].reshape(B, H, N), _f64(k_k), _f64(k_a))
+    vv = _f64(v).reshape(B, H, N)
+    if v_mode == 2:
+        vv = vv + (_f64(_t(v_first0, dt)).reshape(B, H, N) - vv) * ys[3].reshape(B, H, N)
+    ref, ref_s = oracle.wkv7_output_prepare(_f64(r).reshape(B, H, N), w, k, vv, kk, ys[1].reshape(B, H, N), state,
+                                            ys[2].reshape(B, H, N), _f64(r_k), _f64(gn_w), _f64(gn_b), eps)
+    # a one-ulp difference of a rounded LoRA output moves the state by ~2^-11 of a term
+    ssc = np.abs(ref_s).max()
+    assert np.abs(_f64(st) - ref_s).max() <= 1e-3 * ssc
+    tol = OUT_ABS if dt == torch.float16 else 4 * OUT_ABS
+    assert np.abs(_f64(out).reshape(B, H, N) - ref).max() <= tol * max(1.0, np.abs(ref).max() / 4)
+    assert np.abs(_f64(st) - _f64(st2)).max() <= 1e-3 * ssc
+    assert np.abs(_f64(out) - _f64(out2).reshape(B, A)).max() <= tol * max(1.0, np.abs(ref).max() / 4)
+    if v_mode == 1:
+        assert torch.equal(vf, v)
+
+
+def test_decode_fused_lora_rejects_unsupported():
+    from rwkv7mi.fused_lora import fused_lora_decode_supported
+
+    assert fused_lora_decode_supported((64, 64, 128, 32), 8)
+    assert not fused_lora_decode_supported((64, 64, 128, 32), 33)
+    assert fused_lora_decode_supported((64, 64, 120, 40), 1)
+    assert not fused_lora_decode_supported((64, 64, 124, 32), 1)
+    assert not fused_lora_decode_supported((64, 64, 256, 32), 1)
+
+
 @pytest.mark.parametrize("B,T,H", [(1, 1, 2), (2, 37, 4), (1, 256, 8), (2, 0, 2)])
 def test_sequential_scan(oracle, B, T, H):
     from rwkv7mi import fused_recurrent_scan
