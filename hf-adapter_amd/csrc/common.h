@@ -33,6 +33,13 @@ template <> __device__ __forceinline__ __hip_bfloat16 from_f32<__hip_bfloat16>(f
   return __float2bfloat16(x);
 }
 
+// ------------------------------------------------------- lane exchange
+// x from lane (i + N) mod 16 of this lane's 16-lane row (DPP row_ror:N)
+template <int N>
+__device__ __forceinline__ float dpp_row_ror(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xF, 0xF, false));
+}
+
 template <typename T>
 __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i]); }
 

@@ -43,6 +43,7 @@ constexpr int MM8T_LDS_X_ONE = 144 * 1024; // when the grid is at most one workg
 
 struct Mm8tProb {
   const void* x;
+  const void* mix;  // LN-mix prologue only: this problem's token-shift mix [I]
   const uint8_t* w;
   const void* mx;
   const void* rx;
@@ -54,8 +55,27 @@ struct Mm8tProb {
   int epilogue;
 };
 
+// Optional decode prologue (rwkv7_hf/fused_decode_norm_mix.py:39-86, 161-296):
+// the activations are built from the residual row x as
+//   h = LayerNorm(x),  x_p = h + (prev - h) * mix_p   (rounded to the act dtype)
+// inside the x' staging, so no separate mix kernel runs.  Every workgroup
+// computes the row statistics itself; the workgroups between them also write
+// h (the next token's `prev`) and up to four extra mixes of the same h for
+// other consumers, each workgroup a slice of the 8-element groups.
+struct Mm8tPro {
+  const void* prev;  // [rows, I] previous token's LN output
+  const void* ln_w;
+  const void* ln_b;  // [I]
+  void* h_out;       // [rows, I] or null
+  const void* aux_mix[4];
+  void* aux_out[4];  // [rows, I]
+  float eps;
+  int naux;
+};
+
 struct Mm8tBatch {
   Mm8tProb p[MM8T_MAXPROB];
+  Mm8tPro pro;
   int rows, I, O, KC;
 };
 
@@ -135,7 +155,7 @@ __device__ __forceinline__ f16x8 mm4t_b_operand(uint32_t d) {
 // BITS = 8: MM8 bytes, a step is 128 K rows; BITS = 4: MM4 nibbles packed in
 // pairs along K (low nibble = even row), a step is 256 K rows.  Either way a
 // step is two 16-byte loads per lane, 128 bytes of each of the 16 columns.
-template <typename TA, typename TM, int NW, int CSW, int BITS>
+template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B) {
   // NW waves per workgroup; CSW: steps per wave per K-chunk (KC = RS NW CSW
   // rows).  The chunk body is fully unrolled so the load ring needs no
@@ -159,6 +179,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   __shared__ float red[NW][16][17];
   __shared__ float wsum[NW][2];
   __shared__ float rsum[16][2];
+  __shared__ float wpart[PRO ? 2 : 1][PRO ? NW : 1];  // LN-mix prologue: per-wave partial sums
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar step logic
@@ -194,27 +215,89 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   // x' staging in batches of MM8T_SB groups: issue (loads in flight together),
   // then finish (x' = x ry as fp16 hi + lo into LDS, row sums).  Rows past I
   // stage as zeros.
-  Raw8<TA> rxv[MM8T_SB];
-  Raw8<TM> rrv[MM8T_SB], rmv[MM8T_SB];
+  constexpr int SB = PRO ? 2 : MM8T_SB;  // staging groups per load batch
+  Raw8<TA> rxv[SB];
+  Raw8<TM> rrv[SB], rmv[SB];
+  // LN-mix prologue operands (act dtype): prev row, this problem's mix, LN w / b
+  constexpr int SBP = PRO ? SB : 1;
+  float pro_mean = 0.f, pro_rstd = 0.f;  // this thread's row statistics
+  Raw8<TA> rpv[SBP], rcv[SBP], rwv[SBP], rbv[SBP], rav[SBP][4];
+  // h and the extra mixes of group q are written by workgroup q mod W of the
+  // W that share this row tile, from the registers that staged them
+  const int W = gridDim.x * gridDim.y;
+  const int wl = blockIdx.y * gridDim.x + blockIdx.x;
+  // (empty descriptors when the prologue is off: nothing reads them)
+  const __amdgpu_buffer_rsrc_t prr =
+      mm8t_rsrc(PRO ? reinterpret_cast<const TA*>(B.pro.prev) + (int64_t)row0 * I : nullptr,
+                PRO ? (uint32_t)(nrows * I * sizeof(TA)) : 0u);
+  const __amdgpu_buffer_rsrc_t mixr = mm8t_rsrc(PRO ? P.mix : nullptr, PRO ? (uint32_t)(I * sizeof(TA)) : 0u);
+  const __amdgpu_buffer_rsrc_t lnwr = mm8t_rsrc(PRO ? B.pro.ln_w : nullptr, PRO ? (uint32_t)(I * sizeof(TA)) : 0u);
+  const __amdgpu_buffer_rsrc_t lnbr = mm8t_rsrc(PRO ? B.pro.ln_b : nullptr, PRO ? (uint32_t)(I * sizeof(TA)) : 0u);
+  __amdgpu_buffer_rsrc_t auxr[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+    auxr[a] = mm8t_rsrc(PRO && a < B.pro.naux ? B.pro.aux_mix[a] : nullptr,
+                        PRO && a < B.pro.naux ? (uint32_t)(I * sizeof(TA)) : 0u);
   auto stage_issue = [&](int kc0, int it0) {
 #pragma unroll
-    for (int u = 0; u < MM8T_SB; ++u) {
+    for (int u = 0; u < SB; ++u) {
       const int q = su + (it0 + u) * TPR;
       const int k = kc0 + 8 * q;
       const bool valid = sr < nrows && q < NQ && k < I;
       rxv[u] = mm8t_ld8<TA>(xr, (uint32_t)(sr * I + k), valid);
       rrv[u] = mm8t_ld8<TM>(ryr, (uint32_t)k, valid);
       rmv[u] = mm8t_ld8<TM>(myr, (uint32_t)k, valid);
+      if constexpr (PRO) {
+        rpv[u] = mm8t_ld8<TA>(prr, (uint32_t)(sr * I + k), valid);
+        rcv[u] = mm8t_ld8<TA>(mixr, (uint32_t)k, valid);
+        rwv[u] = mm8t_ld8<TA>(lnwr, (uint32_t)k, valid);
+        rbv[u] = mm8t_ld8<TA>(lnbr, (uint32_t)k, valid);
+        const bool own = valid && q % W == wl;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) rav[u][a] = mm8t_ld8<TA>(auxr[a], (uint32_t)k, own && a < B.pro.naux);
+      }
     }
   };
   auto stage_finish = [&](int it0) {
 #pragma unroll
-    for (int u = 0; u < MM8T_SB; ++u) {
+    for (int u = 0; u < SB; ++u) {
       const int q = su + (it0 + u) * TPR;
       float xv[8], rv[8], mv[8];
       mm8t_cvt8(rxv[u], xv);
       mm8t_cvt8(rrv[u], rv);
       mm8t_cvt8(rmv[u], mv);
+      if constexpr (PRO) {
+        // x_p = round(h + (prev - h) mix), h = round((x - mean) / std * w + b)
+        float pv[8], cv[8], wv[8], bv[8];
+        mm8t_cvt8(rpv[u], pv);
+        mm8t_cvt8(rcv[u], cv);
+        mm8t_cvt8(rwv[u], wv);
+        mm8t_cvt8(rbv[u], bv);
+        const float mean = pro_mean, rstd = pro_rstd;
+        const bool valid = sr < nrows && q < NQ && 8 * q < I;  // one chunk: it starts at k = 0
+        float hv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          // h is rounded to the activation dtype before the mix, as the
+          // reference's normed tensor is
+          hv[e] = to_f32(from_f32<TA>((xv[e] - mean) * rstd * wv[e] + bv[e]));
+          xv[e] = valid ? to_f32(from_f32<TA>(hv[e] + (pv[e] - hv[e]) * cv[e])) : 0.f;
+        }
+        if (valid && q % W == wl) {
+          const int64_t off = (int64_t)(row0 + sr) * I + 8 * q;
+          if (B.pro.h_out) st8(reinterpret_cast<TA*>(B.pro.h_out) + off, hv);
+#pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            if (a < B.pro.naux) {
+              float av[8], ov[8];
+              mm8t_cvt8(rav[u][a], av);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) ov[e] = hv[e] + (pv[e] - hv[e]) * av[e];
+              st8(reinterpret_cast<TA*>(B.pro.aux_out[a]) + off, ov);
+            }
+          }
+        }
+      }
       f16x8 hi, lo;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -245,6 +328,61 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
     b[0] = mm8t_ld16(r, kb < bcol ? off : MM8T_OOB);
     b[1] = mm8t_ld16(r, kb + 64 < bcol ? off + 64u : MM8T_OOB);
   };
+  // LN-mix prologue: LayerNorm statistics of each staged row from the x
+  // registers of the first (only) staging batch, in two passes as the
+  // unfused kernel takes them (mean, then the mean squared deviation).  A
+  // row's TPR lanes sum with DPP rotations inside 16-lane rows, then across
+  // rows and waves; every lane of a row ends with the same value.
+  auto row_total = [&](float v, int pass) -> float {
+    if (TPR < 16) {
+      for (int o = TPR >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+      return __shfl(v, lane & ~(TPR - 1), 64);
+    }
+    v += dpp_row_ror<8>(v);
+    v += dpp_row_ror<4>(v);
+    v += dpp_row_ror<2>(v);
+    v += dpp_row_ror<1>(v);
+    if (TPR == 16) return __shfl(v, lane & ~15, 64);
+    if (TPR == 32) {
+      v += __shfl_xor(v, 16, 64);
+      return __shfl(v, lane & ~31, 64);
+    }
+    auto lane_v = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
+    v = (lane_v(v, 0) + lane_v(v, 16)) + (lane_v(v, 32) + lane_v(v, 48));
+    if (TPR == 64) return v;
+    if (lane == 0) wpart[pass][wave] = v;
+    __syncthreads();
+    const int wpr = TPR >> 6, w0 = (wave / wpr) * wpr;
+    float t = 0.f;
+    for (int q = 0; q < wpr; ++q) t += wpart[pass][w0 + q];
+    return t;
+  };
+  auto pro_stats = [&]() {
+    float xs[SB][8];
+    float s1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int q = su + u * TPR;
+      const bool valid = sr < nrows && q < NQ && 8 * q < I;
+      mm8t_cvt8(rxv[u], xs[u]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s1 += valid ? xs[u][e] : 0.f;
+    }
+    pro_mean = row_total(s1, 0) / (float)I;
+    float s2 = 0.f;
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int q = su + u * TPR;
+      const bool valid = sr < nrows && q < NQ && 8 * q < I;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float c = xs[u][e] - pro_mean;
+        s2 += valid ? c * c : 0.f;
+      }
+    }
+    pro_rstd = rsqrtf(row_total(s2, 1) / (float)I + B.pro.eps);  // biased variance, as F.layer_norm
+  };
+
   int g = blockIdx.x;
   __amdgpu_buffer_rsrc_t wr = group_rsrc(g);             // this group
   __amdgpu_buffer_rsrc_t wn = group_rsrc(g + gstride);   // the next one
@@ -258,12 +396,13 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   __builtin_amdgcn_sched_barrier(0);
   load_step(wr, 0, buf[0]);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (PRO) pro_stats();  // the whole row is in this batch (checked by the host)
   stage_finish(0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int d = 1; d < DEPTH; ++d) load_step(wr, d, buf[d]);  // DEPTH <= CSW <= J
   __builtin_amdgcn_sched_barrier(0);
-  for (int it0 = MM8T_SB; it0 < QIT; it0 += MM8T_SB) {
+  for (int it0 = SB; it0 < QIT; it0 += SB) {
     stage_issue(0, it0);
     stage_finish(it0);
   }
@@ -289,7 +428,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
     for (int c = 0; c < nchunks; ++c) {
       if (c > 0) {
         __syncthreads();
-        for (int it0 = 0; it0 < QIT; it0 += MM8T_SB) {
+        for (int it0 = 0; it0 < QIT; it0 += SB) {
           stage_issue(c * KC, it0);
           stage_finish(it0);
         }
@@ -426,27 +565,27 @@ static size_t mm8t_lds(int64_t rows, int KC) {
 
 using namespace rwkv7mi;
 
-template <typename TA, typename TM, int NW, int CSW, int BITS>
+template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO>
 static int mm8t_go(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
   static bool lds_raised = false;  // dynamic LDS above 64 KB must be enabled once per instance
   if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, NW, CSW, BITS>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, NW, CSW, BITS, PRO>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, MM8T_LDS_X_ONE + 1024) != hipSuccess)
       return fail(RWKV7MI_ELAUNCH, "mm8t_kernel: cannot raise the dynamic LDS limit");
     lds_raised = true;
   }
-  hipLaunchKernelGGL((mm8t_kernel<TA, TM, NW, CSW, BITS>), grid, dim3(64 * NW), lds, as_stream(stream), b);
+  hipLaunchKernelGGL((mm8t_kernel<TA, TM, NW, CSW, BITS, PRO>), grid, dim3(64 * NW), lds, as_stream(stream), b);
   return check_launch("mm8t_kernel");
 }
 
-template <typename TA, typename TM, int NW, int BITS>
+template <typename TA, typename TM, int NW, int BITS, bool PRO = false>
 static int mm8t_go_csw(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
   switch (b.KC / ((BITS == 8 ? 128 : 256) * NW)) {
-    case 2: return mm8t_go<TA, TM, NW, 2, BITS>(grid, lds, stream, b);
-    case 4: return mm8t_go<TA, TM, NW, 4, BITS>(grid, lds, stream, b);
-    case 8: return mm8t_go<TA, TM, NW, 8, BITS>(grid, lds, stream, b);
-    case 16: return mm8t_go<TA, TM, NW, 16, BITS>(grid, lds, stream, b);
-    default: return mm8t_go<TA, TM, NW, 32, BITS>(grid, lds, stream, b);
+    case 2: return mm8t_go<TA, TM, NW, 2, BITS, PRO>(grid, lds, stream, b);
+    case 4: return mm8t_go<TA, TM, NW, 4, BITS, PRO>(grid, lds, stream, b);
+    case 8: return mm8t_go<TA, TM, NW, 8, BITS, PRO>(grid, lds, stream, b);
+    case 16: return mm8t_go<TA, TM, NW, 16, BITS, PRO>(grid, lds, stream, b);
+    default: return mm8t_go<TA, TM, NW, 32, BITS, PRO>(grid, lds, stream, b);
   }
 }
 
@@ -463,7 +602,7 @@ static int64_t mm8t_cus() {
 }
 
 static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I, int64_t O, int act_dtype,
-                       int meta_dtype, void* stream, const char* who, int bits = 8) {
+                       int meta_dtype, void* stream, const char* who, int bits = 8, const Mm8tPro* pro = nullptr) {
   const std::string w(who);
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
   if (rows < 0 || I <= 0 || O <= 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
@@ -485,6 +624,7 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
   }
   Mm8tBatch b{};
   for (int p = 0; p < nprob; ++p) b.p[p] = probs[p];
+  if (pro) b.pro = *pro;
   b.rows = (int)rows;
   b.I = (int)I;
   b.O = (int)O;
@@ -500,12 +640,33 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
     b.KC = mm8t_chunk(rows, I, ngroups * nprob * rtiles, nw, bits);
   }
   if (!b.KC) return fail(RWKV7MI_EINVAL, w + ": x' staging does not fit in LDS");
+  if (pro) {
+    // the prologue takes the row statistics from one staging batch (two
+    // 8-element groups per thread): the whole row in one chunk, and
+    // 2 * 8 * (threads per row) >= chunk; eight waves double the threads
+    auto batches = [&](int nw_, int kc) {
+      int64_t rp2 = 1;
+      while (rp2 < std::min<int64_t>(rows, 16)) rp2 <<= 1;
+      const int64_t tpr = 64 * nw_ / rp2;
+      return tpr > 0 ? (kc / 8 + tpr - 1) / tpr : INT64_MAX;
+    };
+    if (nw == 4 && (b.KC < I || batches(4, b.KC) > 2)) {
+      const int kc8 = mm8t_chunk(rows, I, ngroups * nprob * rtiles, 8, bits);
+      if (kc8 >= I && batches(8, kc8) <= 2) {
+        nw = 8;
+        b.KC = kc8;
+      }
+    }
+    if (b.KC < I || batches(nw, b.KC) > 2 || bits != 8)
+      return fail(RWKV7MI_EINVAL, w + ": the LN-mix prologue needs the whole row in one staging batch "
+                                      "(rows <= 2 at in_features 4096)");
+  }
   const size_t lds = mm8t_lds(rows, b.KC);
   // With x' in one LDS chunk, workgroups loop over column groups: as many as
   // stay resident, split between the problems and row tiles.
   int64_t gx = ngroups;
-  if (b.KC >= I && nw == 4) {
-    const int64_t per_cu = lds <= MM8T_LDS_X ? 2 : 1;
+  if (b.KC >= I) {
+    const int64_t per_cu = nw == 4 && lds <= MM8T_LDS_X ? 2 : 1;
     const int64_t slots = cus * per_cu / (nprob * rtiles);
     if (slots >= 1 && slots < gx) gx = slots;
   }
@@ -516,6 +677,13 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
       using TM = decltype(tm);
       if (bits == 4)
         return nw == 8 ? mm8t_go_csw<TA, TM, 8, 4>(grid, lds, stream, b) : mm8t_go_csw<TA, TM, 4, 4>(grid, lds, stream, b);
+      if (pro) {
+        if constexpr (std::is_same<TA, TM>::value && !std::is_same<TA, float>::value)
+          return nw == 8 ? mm8t_go_csw<TA, TM, 8, 8, true>(grid, lds, stream, b)
+                         : mm8t_go_csw<TA, TM, 4, 8, true>(grid, lds, stream, b);
+        return fail(RWKV7MI_EINVAL, w + ": the LN-mix prologue takes fp16 or bf16 activations and metadata "
+                                        "of the same dtype");
+      }
       return nw == 8 ? mm8t_go_csw<TA, TM, 8, 8>(grid, lds, stream, b) : mm8t_go_csw<TA, TM, 4, 8>(grid, lds, stream, b);
     });
   });
@@ -525,7 +693,7 @@ extern "C" int rwkv7mi_mm8t_matmul(const void* x, const uint8_t* w_t, const void
                                    const void* my, const void* ry, const void* bias, const void* residual,
                                    void* y, int64_t rows, int64_t I, int64_t O, int epilogue, int act_dtype,
                                    int meta_dtype, void* stream) {
-  Mm8tProb p{x, w_t, mx, rx, my, ry, bias, residual, y, epilogue};
+  Mm8tProb p{x, nullptr, w_t, mx, rx, my, ry, bias, residual, y, epilogue};
   return mm8t_launch(1, &p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul");
 }
 
@@ -540,16 +708,58 @@ extern "C" int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x, const 
     return fail(RWKV7MI_EINVAL, "mm8t_matmul_multi: null array");
   Mm8tProb p[MM8T_MAXPROB];
   for (int i = 0; i < nprob; ++i)
-    p[i] = Mm8tProb{x[i], w_t[i], mx[i], rx[i], my[i], ry[i], bias ? bias[i] : nullptr,
+    p[i] = Mm8tProb{x[i], nullptr, w_t[i], mx[i], rx[i], my[i], ry[i], bias ? bias[i] : nullptr,
                     residual ? residual[i] : nullptr, y[i], epilogue[i]};
   return mm8t_launch(nprob, p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul_multi");
+}
+
+extern "C" int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* prev, const void* ln_w,
+                                        const void* ln_b, float eps, const void* const* mix,
+                                        const uint8_t* const* w_t, const void* const* mx, const void* const* rx,
+                                        const void* const* my, const void* const* ry, void* const* y,
+                                        const int* epilogue, void* h_out, int naux, const void* const* aux_mix,
+                                        void* const* aux_out, int64_t rows, int64_t I, int64_t O, int act_dtype,
+                                        void* stream) {
+  const char* who = "mm8t_lnmix_multi";
+  if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: 1..4 problems per launch");
+  if (!x || !prev || !ln_w || !ln_b || !mix || !w_t || !mx || !rx || !my || !ry || !y || !epilogue)
+    return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: null pointer");
+  if (naux < 0 || naux > 4 || (naux && (!aux_mix || !aux_out)))
+    return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: 0..4 extra mixes");
+  if (I % 8) return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: in_features must be a multiple of 8");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(prev) | reinterpret_cast<uintptr_t>(ln_w) |
+                       reinterpret_cast<uintptr_t>(ln_b) | reinterpret_cast<uintptr_t>(h_out);
+  if (al & 15) return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: prev, ln_w, ln_b, h_out must be 16-byte aligned");
+  Mm8tPro pro{};
+  pro.prev = prev;
+  pro.ln_w = ln_w;
+  pro.ln_b = ln_b;
+  pro.h_out = h_out;
+  pro.eps = eps;
+  pro.naux = naux;
+  for (int a = 0; a < naux; ++a) {
+    if (!aux_mix[a] || !aux_out[a] ||
+        ((reinterpret_cast<uintptr_t>(aux_mix[a]) | reinterpret_cast<uintptr_t>(aux_out[a])) & 15))
+      return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: extra mixes must be non-null and 16-byte aligned");
+    pro.aux_mix[a] = aux_mix[a];
+    pro.aux_out[a] = aux_out[a];
+  }
+  Mm8tProb p[MM8T_MAXPROB];
+  for (int i = 0; i < nprob; ++i) {
+    if (!mix[i] || (reinterpret_cast<uintptr_t>(mix[i]) & 15))
+      return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: mix vectors must be non-null and 16-byte aligned");
+    if (epilogue[i] == RWKV7MI_EPI_RESIDUAL)
+      return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: no residual epilogue on this route");
+    p[i] = Mm8tProb{x, mix[i], w_t[i], mx[i], rx[i], my[i], ry[i], nullptr, nullptr, y[i], epilogue[i]};
+  }
+  return mm8t_launch(nprob, p, rows, I, O, act_dtype, act_dtype, stream, who, 8, &pro);
 }
 
 extern "C" int rwkv7mi_mm4t_matmul(const void* x, const uint8_t* w_t, const void* mx, const void* rx_s,
                                    const void* my, const void* ry_s, const void* bias, const void* residual,
                                    void* y, int64_t rows, int64_t I, int64_t O, int epilogue, int act_dtype,
                                    int meta_dtype, void* stream) {
-  Mm8tProb p{x, w_t, mx, rx_s, my, ry_s, bias, residual, y, epilogue};
+  Mm8tProb p{x, nullptr, w_t, mx, rx_s, my, ry_s, bias, residual, y, epilogue};
   return mm8t_launch(1, &p, rows, I, O, act_dtype, meta_dtype, stream, "mm4t_matmul", 4);
 }
 

@@ -30,7 +30,7 @@ from .fused_output import fused_attn_output_prepare
 from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
-from .native_quant_mm8 import MM8Linear, is_out_major, mm8_matmul_multi_into
+from .native_quant_mm8 import MM8Linear, is_out_major, mm8_lnmix_multi_into, mm8_matmul_multi_into
 from .native_quant_policy import should_quantize_linear
 from .self_chunk_rwkv7 import _run_chunk
 
@@ -335,6 +335,8 @@ class NativeRWKV7ForCausalLM:
         self.lora_side_stream = False
         # decode: LoRA up projections inside the wkv kernel (when the shapes allow)
         self.fused_lora_decode = True
+        # decode: LayerNorm + token-shift mixes inside the R/K/V and FFN-key GEMVs
+        self.fused_mix_decode = True
         dev = self.device
 
         def get(name):
@@ -452,7 +454,24 @@ class NativeRWKV7ForCausalLM:
             "fk": torch.empty(B, D, device=dev, dtype=dt),
             "kf": torch.empty(B, cfg.intermediate_size, device=dev, dtype=dt),
             "h": torch.empty(B, D, device=dev, dtype=dt),
+            # this step's LayerNorm rows (the next token's shift inputs) on the fused-mix route
+            "hatt": torch.empty(cfg.num_hidden_layers, B, D, device=dev, dtype=dt),
+            "hffn": torch.empty(cfg.num_hidden_layers, B, D, device=dev, dtype=dt),
         }
+
+    def _mix_fusable(self, B) -> bool:
+        """True when every layer's R/K/V and FFN-key products can take the LN-mix prologue."""
+        if (not self.fused_mix_decode or B > 2 or self.config.hidden_size > 4096
+                or self.dtype not in (torch.float16, torch.bfloat16)):
+            return False
+        for L in self.layers:
+            for lin in (L.r_proj, L.k_proj, L.v_proj, L.key):
+                if (not isinstance(lin, QuantLinear) or not is_out_major(lin.m.w_u8) or lin.m.bias is not None
+                        or lin.m.mx.dtype != self.dtype):
+                    return False
+            if len({(l.in_features, l.out_features) for l in (L.r_proj, L.k_proj, L.v_proj)}) != 1:
+                return False
+        return True
 
     def decode_step_(self, tokens: torch.Tensor, cache: NativeRWKV7Cache, logits: torch.Tensor, bufs=None):
         """One token per row, cache updated in place; writes ``logits [B, V]``.
@@ -471,17 +490,29 @@ class NativeRWKV7ForCausalLM:
         mixb, rkv, lora, prep = bufs["mix"], bufs["rkv"], bufs["lora"], bufs["prep"]
         main = torch.cuda.current_stream(x.device)
         side, ev_in, ev_out = self._side(x.device) if self.lora_side_stream else (None, None, None)
+        fmix = self._mix_fusable(B) and not self.lora_side_stream
         for L in self.layers:
             i = L.idx
-            fused_attn_norm_mix6_decode(x, xpa[i], L.ln1[0], L.ln1[1], *L.mix, eps=eps, out=mixb,
-                                        pre_norm_weight=L.pre[0] if L.pre else None,
-                                        pre_norm_bias=L.pre[1] if L.pre else None)
             xr, xw, xk, xv, xa, xg = (mixb[q] for q in range(6))
             n = len(L.lora_down)
+            if fmix:
+                # LN + the six mixes inside the R/K/V GEMV: r/k/v mixes feed the
+                # products, w/a/g/v are written out for the LoRA kernels
+                if L.pre is not None:
+                    layer_norm(x, L.pre[0], L.pre[1], eps, out=x)
+                aux = [L.mix[1], L.mix[4], L.mix[5], L.mix[3]][:n]
+                mm8_lnmix_multi_into(x, xpa[i], L.ln1[0], L.ln1[1], eps, [L.mix[0], L.mix[2], L.mix[3]],
+                                     [L.r_proj.m, L.k_proj.m, L.v_proj.m], [rkv[0], rkv[1], rkv[2]],
+                                     h_out=bufs["hatt"][i], aux_mixes=aux, aux_outs=[xw, xa, xg, xv][:n])
+            else:
+                fused_attn_norm_mix6_decode(x, xpa[i], L.ln1[0], L.ln1[1], *L.mix, eps=eps, out=mixb,
+                                            pre_norm_weight=L.pre[0] if L.pre else None,
+                                            pre_norm_bias=L.pre[1] if L.pre else None)
             if (self.fused_lora_decode and not self.lora_side_stream
                     and fused_lora_decode_supported([int(d.shape[0]) for d in L.lora_down], B)):
                 # LoRA down (split-K launch), then the up projections inside the wkv kernel
-                QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
+                if not fmix:
+                    QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
                 fused_wavg_lora_output_prepare_raw(
                     rkv[0], rkv[1], rkv[2], [xw, xa, xg, xv][:n], L.lora_down, L.lora_up, L.lora_bias, state[i],
                     L.k_k, L.k_a, L.r_k, L.gn[0], L.gn[1], eps=N * 1e-5, out=prep, state_out=state[i],
@@ -498,16 +529,27 @@ class NativeRWKV7ForCausalLM:
                     QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
                     main.wait_event(ev_out)
                 else:
-                    QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
+                    if not fmix:
+                        QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv),
+                                                (rkv[0], rkv[1], rkv[2]))
                     self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
                 fused_recurrent_output_prepare_raw(
                     rkv[0], lora[0], rkv[1], rkv[2], lora[1], state[i], lora[2], L.k_k, L.k_a, L.r_k, L.gn[0],
                     L.gn[1], eps=N * 1e-5, state_out=state[i], out=prep.view(B, H, N),
                     v_first=v_first, v_gate=lora[3] if i > 0 else None, v_mode=1 if i == 0 else 2)
             L.o_proj.apply(prep, x, residual=x)
-            fused_ffn_add_norm_mix_decode(x, None, xpf[i], L.ln2[0], L.ln2[1], L.fx_k, eps=eps, mixed=bufs["fk"])
-            L.key.apply(bufs["fk"], bufs["kf"], act=3)
+            if fmix:
+                mm8_lnmix_multi_into(x, xpf[i], L.ln2[0], L.ln2[1], eps, [L.fx_k], [L.key.m], [bufs["kf"]],
+                                     epilogues=[_lib.EPI_RELU2], h_out=bufs["hffn"][i])
+            else:
+                fused_ffn_add_norm_mix_decode(x, None, xpf[i], L.ln2[0], L.ln2[1], L.fx_k, eps=eps,
+                                              mixed=bufs["fk"])
+                L.key.apply(bufs["fk"], bufs["kf"], act=3)
             L.value.apply(bufs["kf"], x, residual=x)
+        if fmix:
+            # the kernels read the shift inputs while writing this step's rows, so
+            # the rows go to separate buffers and replace the cache's here
+            torch._foreach_copy_(list(xpa) + list(xpf), list(bufs["hatt"].unbind(0)) + list(bufs["hffn"].unbind(0)))
         layer_norm(x, self.norm[0], self.norm[1], eps, out=bufs["h"])
         self.lm_head.apply(bufs["h"], logits)
         return logits

@@ -153,6 +153,59 @@ def mm8_matmul_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
     return outs
 
 
+def mm8_lnmix_multi_into(x, prev, ln_w, ln_b, eps: float, mixes, mods, outs, *, epilogues=None, h_out=None,
+                         aux_mixes=(), aux_outs=()):
+    """Decode form of ``fused_attn_norm_mix6_decode`` / ``fused_ffn_add_norm_mix_decode``
+    (rwkv7_hf/fused_decode_norm_mix.py:161, 296) followed by up to four out-major
+    ``MM8Linear`` products, in one launch: ``h = LayerNorm(x)``,
+    ``outs[p] = (h + (prev - h) * mixes[p]) @ W_p`` (the mixed input rounded to the
+    activation dtype as the reference's tensor is).  Also writes ``h`` to ``h_out``
+    (the next token's ``prev``; ``prev`` itself is only read) and
+    ``aux_outs[a] = h + (prev - h) * aux_mixes[a]`` for other consumers.
+    fp16 / bf16 only; rows <= 2 at in_features 4096 (the rows must fit one staging batch, which
+    the row statistics are taken from; the library rejects larger calls).
+    """
+    k = len(mods)
+    if not 1 <= k <= 4 or len(mixes) != k or len(outs) != k:
+        raise ValueError("mm8_lnmix_multi_into: 1..4 problems")
+    if len(aux_mixes) != len(aux_outs) or len(aux_mixes) > 4:
+        raise ValueError("mm8_lnmix_multi_into: 0..4 extra mixes")
+    rows, n = (int(s) for s in x.shape)
+    m = int(mods[0].out_features)
+    dt = x.dtype
+    vecs = [t.reshape(-1) for t in (ln_w, ln_b, *mixes, *aux_mixes)]
+    for t in (x, prev, *vecs, *outs, *aux_outs, *( [h_out] if h_out is not None else [])):
+        if not t.is_contiguous() or t.dtype != dt:
+            raise ValueError("mm8_lnmix_multi_into: tensors must be contiguous in the activation dtype")
+    for t in vecs:
+        if t.numel() != n:
+            raise ValueError("mm8_lnmix_multi_into: LN parameters and mixes must have in_features values")
+    for t in (prev, *aux_outs, *([h_out] if h_out is not None else [])):
+        if tuple(t.shape) != (rows, n):
+            raise ValueError("mm8_lnmix_multi_into: prev, h_out and extra outputs are [rows, in_features]")
+    reads = {t.data_ptr() for t in (x, prev)}
+    if any(t.data_ptr() in reads for t in (*outs, *aux_outs, *([h_out] if h_out is not None else []))):
+        raise ValueError("mm8_lnmix_multi_into: outputs must not alias x or prev (every workgroup reads them)")
+    for mod, out in zip(mods, outs):
+        if mod.in_features != n or mod.out_features != m or not is_out_major(mod.w_u8) or mod.bias is not None:
+            raise ValueError("mm8_lnmix_multi_into: out-major modules of one shape, without bias")
+        if mod.mx.dtype != dt:
+            raise ValueError("mm8_lnmix_multi_into: MM8 metadata must be in the activation dtype")
+        _check_out(x, m, out, None)
+    epilogues = list(epilogues) if epilogues is not None else [_lib.EPI_NONE] * k
+    _lib.require_gpu(x, prev, *outs, name="mm8_lnmix_multi")
+    arr = lambda ts: _lib.ptr_array(ts)
+    na = len(aux_mixes)
+    _lib.call(
+        "rwkv7mi_mm8t_lnmix_multi", k, _lib.ptr(x), _lib.ptr(prev), _lib.ptr(vecs[0]), _lib.ptr(vecs[1]),
+        float(eps), arr(vecs[2:2 + k]), arr([md.w_u8 for md in mods]), arr([md.mx for md in mods]),
+        arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]), arr(outs),
+        (ctypes.c_int * k)(*[int(e) for e in epilogues]), _lib.ptr(h_out), na, arr(vecs[2 + k:]), arr(list(aux_outs)),
+        rows, n, m, _lib.dtype_code(x), _lib.stream_of(x),
+    )
+    return outs
+
+
 def _meta_1d(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     t = t.reshape(-1)
     if t.dtype != dtype:

@@ -214,6 +214,27 @@ int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x,
 
 /* dequantize_mm8 (rwkv7_hf/native_quant_mm8.py:100-108) into out [O,I]
  * (Linear.weight layout) for a library GEMM on long prefills.  I % 4 == 0. */
+/* Decode LN + token-shift mix fused into the out-major MM8 GEMV: for up to
+ * four problems of one shape, h = LayerNorm(x) (x [rows, I] the residual
+ * rows, ln_w / ln_b [I]), x_p = round(h + (prev - h) * mix_p) and
+ * y_p = x_p @ W_p with epilogue_p (none or relu^2).  Writes h to h_out
+ * [rows, I] (may be NULL) and aux_out[a] = h + (prev - h) * aux_mix[a] for
+ * a < naux (<= 4).  prev is only read.  Replaces fused_attn_norm_mix6_decode /
+ * fused_ffn_add_norm_mix_decode (rwkv7_hf/fused_decode_norm_mix.py:161, 296)
+ * feeding MM8Linear (native_quant_mm8.py:564-628).  All activation-side
+ * tensors and the MM8 metadata in act_dtype (fp16 or bf16); rows <= 2 at
+ * I = 4096 (the rows must fit one x' staging batch).  Outputs must not alias
+ * x or prev. */
+int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* prev,
+                             const void* ln_w, const void* ln_b, float eps,
+                             const void* const* mix, const uint8_t* const* w_t,
+                             const void* const* mx, const void* const* rx,
+                             const void* const* my, const void* const* ry,
+                             void* const* y, const int* epilogue, void* h_out,
+                             int naux, const void* const* aux_mix, void* const* aux_out,
+                             int64_t rows, int64_t I, int64_t O, int act_dtype,
+                             void* stream);
+
 int rwkv7mi_mm8t_dequant(const uint8_t* w_t, const void* mx, const void* rx,
                          const void* my, const void* ry, void* out, int64_t I,
                          int64_t O, int meta_dtype, int out_dtype, void* stream);

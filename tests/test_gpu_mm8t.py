@@ -183,3 +183,110 @@ def test_mm8t_rejects_bad_shapes():
     with pytest.raises(ValueError, match="multiple of 16"):
         _lib.call("rwkv7mi_mm8t_matmul", _lib.ptr(x), _lib.ptr(w), _lib.ptr(m8), _lib.ptr(m8), _lib.ptr(m24),
                   _lib.ptr(m24), None, None, _lib.ptr(y), 1, 24, 8, 0, _lib.F16, _lib.F16, _lib.stream_of(x))
+
+
+def _round(a, dtype):
+    return _np(torch.tensor(a, dtype=torch.float64).to(dtype).to(torch.float64))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", [
+    # (rows, I, O, nprob, naux, epilogue): the 7.2B R/K/V and FFN-key shapes,
+    # the 1.5B ones, a ragged width
+    (1, 4096, 4096, 3, 4, 0), (2, 4096, 4096, 3, 3, 0), (1, 4096, 16384, 1, 0, 1), (2, 4096, 16384, 1, 0, 1),
+    (1, 2048, 2048, 3, 4, 0), (2, 2048, 8192, 1, 0, 1), (4, 2048, 2048, 2, 2, 0), (3, 1024, 200, 2, 1, 0),
+])
+def test_mm8t_lnmix_matches_oracle_and_unfused(oracle, dtype, case):
+    """LN + token-shift mix inside the GEMV (the decode form of
+    fused_decode_norm_mix.py:161 / :296 feeding MM8Linear) against the fp64
+    oracle (LN, h rounded, mix rounded, dequant product) and against the
+    unfused mix kernel + grouped GEMV."""
+    from rwkv7mi import MM8Linear, _lib
+    from rwkv7mi.fused_decode_norm_mix import fused_attn_norm_mix6_decode
+    from rwkv7mi.native_quant_mm8 import mm8_lnmix_multi_into, mm8_matmul_multi_into
+
+    rows, I, O, k, na, epi = case
+    rng = np.random.default_rng(rows * 131 + I + O + k)
+    # a residual stream with an offset and a few large channels
+    xr = rng.standard_normal((rows, I)) * 2.0 + 3.0
+    xr[:, :: max(I // 7, 1)] *= 20.0
+    x = _cuda(xr, dtype)
+    prev = _cuda(rng.standard_normal((rows, I)), dtype)
+    lnw = _cuda(1.0 + 0.2 * rng.standard_normal(I), dtype)
+    lnb = _cuda(0.1 * rng.standard_normal(I), dtype)
+    mixes = [_cuda(rng.uniform(0, 1, I), dtype) for _ in range(k + na)]
+    mods = []
+    for _ in range(k):
+        lin = torch.nn.Linear(I, O, bias=False).to(device="cuda", dtype=dtype)
+        with torch.no_grad():
+            lin.weight.copy_(_cuda(rng.standard_normal((O, I)) * 0.02, dtype))
+        mods.append(MM8Linear(lin))
+    outs = [torch.full((rows, O), float("nan"), device="cuda", dtype=dtype) for _ in range(k)]
+    h_out = torch.full((rows, I), float("nan"), device="cuda", dtype=dtype)
+    aux = [torch.full((rows, I), float("nan"), device="cuda", dtype=dtype) for _ in range(na)]
+    prev0 = prev.clone()
+    epis = [_lib.EPI_RELU2 if epi else _lib.EPI_NONE] * k
+    mm8_lnmix_multi_into(x, prev, lnw, lnb, 1e-5, mixes[:k], mods, outs, epilogues=epis, h_out=h_out,
+                         aux_mixes=mixes[k:], aux_outs=aux)
+    again = [torch.empty_like(o) for o in outs]
+    mm8_lnmix_multi_into(x, prev, lnw, lnb, 1e-5, mixes[:k], mods, again, epilogues=epis)
+    torch.cuda.synchronize()
+    assert torch.equal(prev, prev0), "prev is only read"
+    for a, b in zip(outs, again):
+        assert torch.equal(a, b), "repeated calls must be bit-identical"
+
+    # fp64 oracle
+    f = lambda t: _np(t.double())
+    outs_ref, h_ref = oracle.attn_norm_mix6(f(x), f(prev), f(lnw), f(lnb), [f(m) for m in mixes])
+    h_r = _round(h_ref, dtype)
+    mixed = [_round(h_r + (f(prev) - h_r) * f(m), dtype) for m in mixes]
+    tol_h = 1e-2 if dtype == torch.float16 else 4e-2
+    assert np.abs(f(h_out) - h_r).max() <= tol_h * max(np.abs(h_r).max(), 1.0)
+    for a in range(na):
+        assert np.abs(f(aux[a]) - mixed[k + a]).max() <= tol_h * max(np.abs(mixed[k + a]).max(), 1.0)
+    for p in range(k):
+        packed = [_np(b.float()) if b.is_floating_point() else _np(b)
+                  for b in (mods[p].w_u8, mods[p].mx, mods[p].rx, mods[p].my, mods[p].ry)]
+        ref = oracle.mm8_matmul(mixed[p], *packed)
+        if epi:
+            ref = np.maximum(ref, 0) ** 2
+        tol = (2e-3 if dtype == torch.float16 else 8e-3) * (2 if epi else 1)
+        assert _rel_err(f(outs[p]), ref) <= tol, p
+
+    # the unfused route: mix kernel (six slots), then the grouped GEMV
+    slots = torch.empty(6, rows, I, device="cuda", dtype=dtype)
+    pv = prev.clone()
+    six = (mixes + [mixes[0]] * 6)[:6]
+    fused_attn_norm_mix6_decode(x, pv, lnw, lnb, *six, eps=1e-5, out=slots)
+    ref_outs = [torch.empty_like(o) for o in outs]
+    mm8_matmul_multi_into([slots[p] for p in range(k)], mods, ref_outs, epilogues=epis)
+    torch.cuda.synchronize()
+    # the statistics are summed in another order: h may differ by one unit
+    # in the last place in a few elements, and the products by as little
+    assert (h_out != pv).float().mean().item() < 0.02
+    hd = (h_out.double() - pv.double()).abs().max().item()
+    assert hd <= tol_h * max(pv.double().abs().max().item(), 1.0)
+    for p in range(k):
+        d = (outs[p].double() - ref_outs[p].double()).abs().max().item()
+        assert d <= 4e-3 * max(ref_outs[p].double().abs().max().item(), 1.0), (p, d)
+
+
+def test_mm8t_lnmix_rejects_unsupported():
+    from rwkv7mi import MM8Linear, _lib
+    from rwkv7mi.native_quant_mm8 import mm8_lnmix_multi_into
+
+    I, O = 4096, 256
+    lin = torch.nn.Linear(I, O, bias=False).to(device="cuda", dtype=torch.float16)
+    mod = MM8Linear(lin)
+    v = torch.ones(I, device="cuda", dtype=torch.float16)
+    for rows in (4, 9, 16):  # the rows no longer fit one staging batch
+        x = torch.zeros(rows, I, device="cuda", dtype=torch.float16)
+        out = torch.empty(rows, O, device="cuda", dtype=torch.float16)
+        with pytest.raises(ValueError, match="staging batch"):
+            mm8_lnmix_multi_into(x, x.clone(), v, v, 1e-5, [v], [mod], [out])
+    x = torch.zeros(2, I, device="cuda", dtype=torch.float16)
+    out = torch.empty(2, O, device="cuda", dtype=torch.float16)
+    with pytest.raises(ValueError, match="residual"):
+        mm8_lnmix_multi_into(x, x.clone(), v, v, 1e-5, [v], [mod], [out], epilogues=[_lib.EPI_RESIDUAL])
+    with pytest.raises(ValueError):
+        mm8_lnmix_multi_into(x, x, v, v, 1e-5, [v], [mod], [out], h_out=x)

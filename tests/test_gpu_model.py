@@ -102,6 +102,31 @@ def test_graph_decode_equals_eager_decode(mm8):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("B", [1, 2, 3])
+def test_decode_fused_mix_equals_unfused(B):
+    """The LN + token-shift mixes inside the R/K/V and FFN-key GEMVs (rows <= 2)
+    against the separate mix kernels: the same logits and shift rows up to
+    the statistics' summation order."""
+    cfg, model, _ = _build(True, layers=3)
+    rng = np.random.default_rng(7 + B)
+    ids = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 5)), device="cuda")
+    _, c1 = model(ids)
+    c2 = c1.clone()
+    assert model._mix_fusable(B) == (B <= 2)
+    for step in range(3):
+        tok = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 1)), device="cuda")
+        model.fused_mix_decode = True
+        a, c1 = model(tok, c1)
+        model.fused_mix_decode = False
+        b, c2 = model(tok, c2)
+        model.fused_mix_decode = True
+        torch.cuda.synchronize()
+        scale = b.float().abs().max().item()
+        assert (a.float() - b.float()).abs().max().item() <= 5e-3 * scale, step
+        for x1, x2 in zip(c1._xpa + c1._xpf, c2._xpa + c2._xpf):
+            assert (x1.float() - x2.float()).abs().max().item() <= 1e-2 * max(x2.float().abs().max().item(), 1.0)
+
+
 def test_generate_greedy_matches_oracle():
     cfg, model, ref = _build(True)
     rng = np.random.default_rng(3)
