@@ -4,21 +4,30 @@
 //   W_hat[i,o] = (w[i,o] + 0.5) * ry[i] * rx[o] + my[i] + mx[o]
 //   y[b,o] = rx[o] * sum_i x'[b,i] (w[i,o] + 0.5) + sum_i x[b,i] my[i] + mx[o] sum_i x[b,i],
 //   x' = x * ry,
-// but the bytes are stored out-major: wt[o * I + i] == w[i, o] (the layout of
-// nn.Linear.weight; the [in, out] tensor the reference exposes is wt.t()).
+// but the MM8 bytes are stored BLOCKED by output-column group: for group g
+// (outputs 16g..16g+15) and K block b (inputs 128b..128b+127) one 2048-byte
+// tile at byte (g KB + b) 2048, KB = ceil(I / 128), holding at byte
+// 1024 h + 16 (16 q + c) + e the weight of output 16g + c, input
+// 128b + 64h + 16q + e (h < 2, q < 4, c < 16, e < 16); tails padded with
+// zeros.  A wave's step is then one contiguous 2 KB run (two 1 KB loads), the
+// access pattern HBM streams fastest; 16 columns x 64 bytes per load (the
+// plain [O, I] layout) measured ~25% slower on the 67 MB shapes.
+// rwkv7mi_mm8t_block / _unblock convert from and to the reference's [I, O].
+// MM4 (BITS = 4) keeps the out-major [O, I/2] layout.
 //
-// Out-major makes the whole K range of an output column one contiguous run,
-// so a workgroup owns 16 output columns and ALL of K: no split-K partials, no
+// A workgroup owns 16 output columns and ALL of K: no split-K partials, no
 // cross-workgroup ordering, deterministic fixed-order sums.
 //
 // Workgroup = NW (4 or 8) waves, 16 columns, up to 16 batch rows (one MFMA M
 // tile).  K is walked in 128-row steps; wave w takes steps w, w+NW, ...  In a step,
-// lane (n = l%16, kg = l/16) loads two 16-byte runs of column n, rows
-// 16kg..16kg+15 and 64+16kg..64+16kg+15 — a wave reads 16 full 128-byte lines.
+// lane (n = l%16, kg = l/16) holds two 16-byte runs of column n, rows
+// 16kg..16kg+15 and 64+16kg..64+16kg+15.
 // Each 8-byte half is one B operand of v_mfma_f32_16x16x32_f16 (the MFMA's
 // logical k = 8kg+e maps to physical row 64h + 16kg + 8q + e; the A operand
 // uses the same map), converted to fp16 (w + 0.5) by v_perm + one packed add.
-// Weight loads run DEPTH steps ahead of use, across LDS re-staging barriers
+// Weight loads run DEPTH steps ahead of use (DEPTH x 2 KB per wave; about
+// 32 KB in flight per CU streams fastest, deeper rings congest HBM), across
+// LDS re-staging barriers
 // (__syncthreads waits on LDS traffic only).  All global loads are raw buffer
 // loads whose out-of-range lanes get an offset past the descriptor's size, so
 // the loop is branch-free and the load counter waits stay exact.
@@ -155,13 +164,13 @@ __device__ __forceinline__ f16x8 mm4t_b_operand(uint32_t d) {
 // BITS = 8: MM8 bytes, a step is 128 K rows; BITS = 4: MM4 nibbles packed in
 // pairs along K (low nibble = even row), a step is 256 K rows.  Either way a
 // step is two 16-byte loads per lane, 128 bytes of each of the 16 columns.
-template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO>
+template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO, int RING>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B) {
   // NW waves per workgroup; CSW: steps per wave per K-chunk (KC = RS NW CSW
   // rows).  The chunk body is fully unrolled so the load ring needs no
   // loop-carried waits.
   constexpr int NT = 64 * NW;
-  constexpr int DEPTH = CSW < 8 ? CSW : 8;
+  constexpr int DEPTH = CSW < RING ? CSW : RING;
   constexpr int RS = BITS == 8 ? 128 : 256;  // K rows per step
   constexpr int NB = BITS == 8 ? 4 : 8;      // B operands (8 rows each) per step
   const Mm8tProb& P = B.p[blockIdx.y];
@@ -189,7 +198,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
 
   // A column group's 16 columns are one contiguous run of ncols * I bytes;
   // groups past the end get an empty descriptor (all loads read zeros).
+  const int KBLK = (I + 127) / 128;  // 8-bit: 2 KB tiles per column group
   auto group_rsrc = [&](int g) {
+    if constexpr (BITS == 8) {
+      const uint32_t gb = (uint32_t)KBLK * 2048u;
+      return mm8t_rsrc(P.w + (int64_t)(g < ngroups ? g : 0) * gb, g < ngroups ? gb : 0u);
+    }
     const int c0 = g * MM8T_COLS;
     const int nc = g < ngroups ? min(MM8T_COLS, O - c0) : 0;
     return mm8t_rsrc(P.w + (int64_t)(g < ngroups ? c0 : 0) * bcol, (uint32_t)nc * (uint32_t)bcol);
@@ -323,6 +337,13 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   // column's bytes (the tail step) read as zeros.
   u32x4 buf[DEPTH][2];
   auto load_step = [&](__amdgpu_buffer_rsrc_t r, int j, u32x4 (&b)[2]) {
+    if constexpr (BITS == 8) {
+      const int blk = wave + NW * j;
+      const uint32_t boff = (uint32_t)blk * 2048u + 16u * (uint32_t)lane;
+      b[0] = mm8t_ld16(r, blk < KBLK ? boff : MM8T_OOB);
+      b[1] = mm8t_ld16(r, blk < KBLK ? boff + 1024u : MM8T_OOB);
+      return;
+    }
     const int kb = 128 * (wave + NW * j) + 16 * kg;
     const uint32_t off = lane_off + 128u * (uint32_t)(wave + NW * j);
     b[0] = mm8t_ld16(r, kb < bcol ? off : MM8T_OOB);
@@ -541,18 +562,19 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
 
 
 // x' staging chunk: the largest power-of-two multiple of 2 RS NW rows (at
-// most 32 RS NW; RS = K rows per step) whose hi/lo copy for the tile's rows
-// fits the LDS budget, and no longer than I needs.  A grid of at most one
-// workgroup per CU, or a tile of more than four rows (whose staging would
-// otherwise repeat per chunk), uses most of the CU's LDS; the weight ring
-// keeps 64 KB per CU in flight even then.
+// most 32 RS NW, 16 RS NW for the 4-bit eight-wave kernel; RS = K rows per
+// step) whose hi/lo copy for the tile's rows fits the LDS budget, and no
+// longer than I needs.  A grid of at most one workgroup per CU, or a tile of
+// more than four rows (whose staging would otherwise repeat per chunk), uses
+// most of the CU's LDS.
 static int mm8t_chunk(int64_t rows, int64_t I, int64_t nwg, int nw, int bits) {
   const int64_t nr = rows < 16 ? rows : 16;
   const int64_t rs = bits == 8 ? 128 : 256;
   const int64_t budget = (nwg <= 256 || nr > 4) ? MM8T_LDS_X_ONE : MM8T_LDS_X;
   int64_t kc = 2 * rs * nw;
   if (nr * (kc + 8) * 4 > budget) return 0;  // not even the smallest chunk fits
-  while (kc < I && kc < rs * nw * 32 && nr * (2 * kc + 8) * 4 <= budget) kc *= 2;
+  const int64_t steps = bits == 4 && nw == 8 ? 16 : 32;  // steps per wave per chunk
+  while (kc < I && kc < rs * nw * steps && nr * (2 * kc + 8) * 4 <= budget) kc *= 2;
   return (int)kc;
 }
 
@@ -565,27 +587,46 @@ static size_t mm8t_lds(int64_t rows, int KC) {
 
 using namespace rwkv7mi;
 
-template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO>
+template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO, int RING>
 static int mm8t_go(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
   static bool lds_raised = false;  // dynamic LDS above 64 KB must be enabled once per instance
   if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, NW, CSW, BITS, PRO>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, NW, CSW, BITS, PRO, RING>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, MM8T_LDS_X_ONE + 1024) != hipSuccess)
       return fail(RWKV7MI_ELAUNCH, "mm8t_kernel: cannot raise the dynamic LDS limit");
     lds_raised = true;
   }
-  hipLaunchKernelGGL((mm8t_kernel<TA, TM, NW, CSW, BITS, PRO>), grid, dim3(64 * NW), lds, as_stream(stream), b);
+  hipLaunchKernelGGL((mm8t_kernel<TA, TM, NW, CSW, BITS, PRO, RING>), grid, dim3(64 * NW), lds, as_stream(stream), b);
   return check_launch("mm8t_kernel");
 }
 
-template <typename TA, typename TM, int NW, int BITS, bool PRO = false>
-static int mm8t_go_csw(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
+template <typename TA, typename TM, int NW, int BITS, bool PRO, int RING>
+static int mm8t_go_csw_ring(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
   switch (b.KC / ((BITS == 8 ? 128 : 256) * NW)) {
-    case 2: return mm8t_go<TA, TM, NW, 2, BITS, PRO>(grid, lds, stream, b);
-    case 4: return mm8t_go<TA, TM, NW, 4, BITS, PRO>(grid, lds, stream, b);
-    case 8: return mm8t_go<TA, TM, NW, 8, BITS, PRO>(grid, lds, stream, b);
-    case 16: return mm8t_go<TA, TM, NW, 16, BITS, PRO>(grid, lds, stream, b);
-    default: return mm8t_go<TA, TM, NW, 32, BITS, PRO>(grid, lds, stream, b);
+    case 2: return mm8t_go<TA, TM, NW, 2, BITS, PRO, RING>(grid, lds, stream, b);
+    case 4: return mm8t_go<TA, TM, NW, 4, BITS, PRO, RING>(grid, lds, stream, b);
+    case 8: return mm8t_go<TA, TM, NW, 8, BITS, PRO, RING>(grid, lds, stream, b);
+    case 16: return mm8t_go<TA, TM, NW, 16, BITS, PRO, RING>(grid, lds, stream, b);
+    default:
+      // the 4-bit eight-wave kernel at 32 steps per chunk runs out of
+      // registers; its chunks are capped at 16 steps
+      if constexpr (BITS == 4 && NW == 8)
+        return fail(RWKV7MI_EINVAL, "mm8t_kernel: chunk too long for the 4-bit eight-wave kernel");
+      else
+        return mm8t_go<TA, TM, NW, 32, BITS, PRO, RING>(grid, lds, stream, b);
+  }
+}
+
+// Ring depth: about 32 KB of weight loads in flight per CU (2 KB per wave and
+// step).  8-bit: depth 2 with eight resident waves per CU, 4 with four; the
+// 4-bit path keeps its depth of 8.
+template <typename TA, typename TM, int NW, int BITS, bool PRO = false>
+static int mm8t_go_csw(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b, int waves_per_cu) {
+  if constexpr (BITS == 4) {
+    return mm8t_go_csw_ring<TA, TM, NW, BITS, PRO, 8>(grid, lds, stream, b);
+  } else {
+    return waves_per_cu >= 8 ? mm8t_go_csw_ring<TA, TM, NW, BITS, PRO, 2>(grid, lds, stream, b)
+                             : mm8t_go_csw_ring<TA, TM, NW, BITS, PRO, 4>(grid, lds, stream, b);
   }
 }
 
@@ -618,7 +659,7 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
     if (!q.x || !q.w || !q.mx || !q.rx || !q.my || !q.ry || !q.y) return fail(RWKV7MI_EINVAL, w + ": null pointer");
     if ((reinterpret_cast<uintptr_t>(q.x) | reinterpret_cast<uintptr_t>(q.w) | reinterpret_cast<uintptr_t>(q.my) |
          reinterpret_cast<uintptr_t>(q.ry)) & 15)
-      return fail(RWKV7MI_EINVAL, w + ": x, w_t, my and ry must be 16-byte aligned");
+      return fail(RWKV7MI_EINVAL, w + ": x, the weights, my and ry must be 16-byte aligned");
     if (q.epilogue < 0 || q.epilogue > 2) return fail(RWKV7MI_EINVAL, w + ": bad epilogue");
     if (q.epilogue == RWKV7MI_EPI_RESIDUAL && !q.residual) return fail(RWKV7MI_EINVAL, w + ": residual missing");
   }
@@ -671,58 +712,61 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
     if (slots >= 1 && slots < gx) gx = slots;
   }
   dim3 grid((unsigned)gx, (unsigned)nprob, (unsigned)rtiles);
+  const int wpc = nw * (nw == 4 && lds <= MM8T_LDS_X ? 2 : 1);  // resident waves per CU
   return dispatch_dtype(act_dtype, [&](auto ta) {
     using TA = decltype(ta);
     return dispatch_dtype(meta_dtype, [&](auto tm) {
       using TM = decltype(tm);
       if (bits == 4)
-        return nw == 8 ? mm8t_go_csw<TA, TM, 8, 4>(grid, lds, stream, b) : mm8t_go_csw<TA, TM, 4, 4>(grid, lds, stream, b);
+        return nw == 8 ? mm8t_go_csw<TA, TM, 8, 4>(grid, lds, stream, b, wpc)
+                       : mm8t_go_csw<TA, TM, 4, 4>(grid, lds, stream, b, wpc);
       if (pro) {
         if constexpr (std::is_same<TA, TM>::value && !std::is_same<TA, float>::value)
-          return nw == 8 ? mm8t_go_csw<TA, TM, 8, 8, true>(grid, lds, stream, b)
-                         : mm8t_go_csw<TA, TM, 4, 8, true>(grid, lds, stream, b);
+          return nw == 8 ? mm8t_go_csw<TA, TM, 8, 8, true>(grid, lds, stream, b, wpc)
+                         : mm8t_go_csw<TA, TM, 4, 8, true>(grid, lds, stream, b, wpc);
         return fail(RWKV7MI_EINVAL, w + ": the LN-mix prologue takes fp16 or bf16 activations and metadata "
                                         "of the same dtype");
       }
-      return nw == 8 ? mm8t_go_csw<TA, TM, 8, 8>(grid, lds, stream, b) : mm8t_go_csw<TA, TM, 4, 8>(grid, lds, stream, b);
+      return nw == 8 ? mm8t_go_csw<TA, TM, 8, 8>(grid, lds, stream, b, wpc)
+                     : mm8t_go_csw<TA, TM, 4, 8>(grid, lds, stream, b, wpc);
     });
   });
 }
 
-extern "C" int rwkv7mi_mm8t_matmul(const void* x, const uint8_t* w_t, const void* mx, const void* rx,
+extern "C" int rwkv7mi_mm8t_matmul(const void* x, const uint8_t* w_blk, const void* mx, const void* rx,
                                    const void* my, const void* ry, const void* bias, const void* residual,
                                    void* y, int64_t rows, int64_t I, int64_t O, int epilogue, int act_dtype,
                                    int meta_dtype, void* stream) {
-  Mm8tProb p{x, nullptr, w_t, mx, rx, my, ry, bias, residual, y, epilogue};
+  Mm8tProb p{x, nullptr, w_blk, mx, rx, my, ry, bias, residual, y, epilogue};
   return mm8t_launch(1, &p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul");
 }
 
-extern "C" int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x, const uint8_t* const* w_t,
+extern "C" int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x, const uint8_t* const* w_blk,
                                          const void* const* mx, const void* const* rx, const void* const* my,
                                          const void* const* ry, const void* const* bias,
                                          const void* const* residual, void* const* y, const int* epilogue,
                                          int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype,
                                          void* stream) {
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, "mm8t_matmul_multi: 1..4 problems per launch");
-  if (!x || !w_t || !mx || !rx || !my || !ry || !y || !epilogue)
+  if (!x || !w_blk || !mx || !rx || !my || !ry || !y || !epilogue)
     return fail(RWKV7MI_EINVAL, "mm8t_matmul_multi: null array");
   Mm8tProb p[MM8T_MAXPROB];
   for (int i = 0; i < nprob; ++i)
-    p[i] = Mm8tProb{x[i], nullptr, w_t[i], mx[i], rx[i], my[i], ry[i], bias ? bias[i] : nullptr,
+    p[i] = Mm8tProb{x[i], nullptr, w_blk[i], mx[i], rx[i], my[i], ry[i], bias ? bias[i] : nullptr,
                     residual ? residual[i] : nullptr, y[i], epilogue[i]};
   return mm8t_launch(nprob, p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul_multi");
 }
 
 extern "C" int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* prev, const void* ln_w,
                                         const void* ln_b, float eps, const void* const* mix,
-                                        const uint8_t* const* w_t, const void* const* mx, const void* const* rx,
+                                        const uint8_t* const* w_blk, const void* const* mx, const void* const* rx,
                                         const void* const* my, const void* const* ry, void* const* y,
                                         const int* epilogue, void* h_out, int naux, const void* const* aux_mix,
                                         void* const* aux_out, int64_t rows, int64_t I, int64_t O, int act_dtype,
                                         void* stream) {
   const char* who = "mm8t_lnmix_multi";
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: 1..4 problems per launch");
-  if (!x || !prev || !ln_w || !ln_b || !mix || !w_t || !mx || !rx || !my || !ry || !y || !epilogue)
+  if (!x || !prev || !ln_w || !ln_b || !mix || !w_blk || !mx || !rx || !my || !ry || !y || !epilogue)
     return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: null pointer");
   if (naux < 0 || naux > 4 || (naux && (!aux_mix || !aux_out)))
     return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: 0..4 extra mixes");
@@ -750,7 +794,7 @@ extern "C" int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* pr
       return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: mix vectors must be non-null and 16-byte aligned");
     if (epilogue[i] == RWKV7MI_EPI_RESIDUAL)
       return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: no residual epilogue on this route");
-    p[i] = Mm8tProb{x, mix[i], w_t[i], mx[i], rx[i], my[i], ry[i], nullptr, nullptr, y[i], epilogue[i]};
+    p[i] = Mm8tProb{x, mix[i], w_blk[i], mx[i], rx[i], my[i], ry[i], nullptr, nullptr, y[i], epilogue[i]};
   }
   return mm8t_launch(nprob, p, rows, I, O, act_dtype, act_dtype, stream, who, 8, &pro);
 }
@@ -764,17 +808,24 @@ extern "C" int rwkv7mi_mm4t_matmul(const void* x, const uint8_t* w_t, const void
 }
 
 namespace rwkv7mi {
-// out[o, i] = (wt[o, i] + 0.5) * ry[i] * rx[o] + my[i] + mx[o], fp32 math, one rounding
-// (the same expression as mm8_dequant_kernel, transposed storage).
+// byte offset of weight (output o, input i) in the blocked 8-bit layout
+__host__ __device__ __forceinline__ int64_t mm8t_blk_off(int64_t o, int64_t i, int64_t KB) {
+  return ((o >> 4) * KB + (i >> 7)) * 2048 + ((i >> 6) & 1) * 1024 + 16 * (16 * ((i >> 4) & 3) + (o & 15)) + (i & 15);
+}
+
+// out[o, i] = (w[o, i] + 0.5) * ry[i] * rx[o] + my[i] + mx[o], fp32 math, one rounding
+// (the same expression as mm8_dequant_kernel), from the blocked layout.
 template <typename TM, typename TO>
 __global__ __launch_bounds__(256) void mm8t_dequant_kernel(const uint8_t* __restrict__ w, const TM* __restrict__ mx,
                                                            const TM* __restrict__ rx, const TM* __restrict__ my,
                                                            const TM* __restrict__ ry, TO* __restrict__ out, int I,
                                                            int O) {
+  const int64_t KB = (I + 127) / 128;
   for (int o = blockIdx.y; o < O; o += gridDim.y) {
     const float rxo = to_f32(rx[o]), mxo = to_f32(mx[o]);
     for (int i = (blockIdx.x * 256 + threadIdx.x) * 4; i < I; i += gridDim.x * 256 * 4) {
-      const uint32_t q = *reinterpret_cast<const uint32_t*>(w + (int64_t)o * I + i);
+      // four consecutive inputs (i % 4 == 0) share one 16-byte run
+      const uint32_t q = *reinterpret_cast<const uint32_t*>(w + mm8t_blk_off(o, i, KB));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float wq = (float)((q >> (8 * e)) & 0xffu) + 0.5f;
@@ -783,21 +834,87 @@ __global__ __launch_bounds__(256) void mm8t_dequant_kernel(const uint8_t* __rest
     }
   }
 }
+
+// blocked[tile, 16-byte run] <-> src[o, i] at src + o so + i si (zeros past the edges)
+__global__ __launch_bounds__(256) void mm8t_block_kernel(const uint8_t* __restrict__ src, int64_t so, int64_t si,
+                                                         int I, int O, uint8_t* __restrict__ blk, int64_t nruns) {
+  const int64_t KB = (I + 127) / 128;
+  for (int64_t t = blockIdx.x * 256 + threadIdx.x; t < nruns; t += (int64_t)gridDim.x * 256) {
+    const int64_t tile = t >> 7, w = t & 127;
+    const int64_t o = (tile / KB) * 16 + (w & 15);
+    const int64_t i0 = (tile % KB) * 128 + ((w >> 6) & 1) * 64 + ((w >> 4) & 3) * 16;
+    uint32_t v[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (o < O && i0 + e < I) v[e >> 2] |= (uint32_t)src[o * so + (i0 + e) * si] << (8 * (e & 3));
+    *reinterpret_cast<uint4*>(blk + t * 16) = make_uint4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+__global__ __launch_bounds__(256) void mm8t_unblock_kernel(const uint8_t* __restrict__ blk, int I, int O,
+                                                           uint8_t* __restrict__ dst, int64_t so, int64_t si,
+                                                           int64_t nruns) {
+  const int64_t KB = (I + 127) / 128;
+  for (int64_t t = blockIdx.x * 256 + threadIdx.x; t < nruns; t += (int64_t)gridDim.x * 256) {
+    const int64_t tile = t >> 7, w = t & 127;
+    const int64_t o = (tile / KB) * 16 + (w & 15);
+    const int64_t i0 = (tile % KB) * 128 + ((w >> 6) & 1) * 64 + ((w >> 4) & 3) * 16;
+    if (o >= O) continue;
+    const uint4 r = *reinterpret_cast<const uint4*>(blk + t * 16);
+    const uint32_t v[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (i0 + e < I) dst[o * so + (i0 + e) * si] = (uint8_t)(v[e >> 2] >> (8 * (e & 3)));
+  }
+}
 }  // namespace rwkv7mi
 
-extern "C" int rwkv7mi_mm8t_dequant(const uint8_t* w_t, const void* mx, const void* rx, const void* my,
+extern "C" size_t rwkv7mi_mm8t_blocked_bytes(int64_t I, int64_t O) {
+  if (I <= 0 || O <= 0) return 0;
+  return (size_t)((O + 15) / 16) * (size_t)((I + 127) / 128) * 2048u;
+}
+
+static int mm8t_relayout(bool to_blocked, const uint8_t* src, uint8_t* dst, int64_t I, int64_t O, int64_t so,
+                         int64_t si, void* stream, const char* who) {
+  if (I <= 0 || O <= 0 || I > INT32_MAX || O > INT32_MAX) return fail(RWKV7MI_EINVAL, std::string(who) + ": bad shape");
+  if (!src || !dst) return fail(RWKV7MI_EINVAL, std::string(who) + ": null pointer");
+  const uint8_t* blk = to_blocked ? dst : src;
+  if (reinterpret_cast<uintptr_t>(blk) & 15)
+    return fail(RWKV7MI_EINVAL, std::string(who) + ": the blocked buffer must be 16-byte aligned");
+  const int64_t nruns = (int64_t)(rwkv7mi_mm8t_blocked_bytes(I, O) / 16);
+  const unsigned gx = (unsigned)std::min<int64_t>((nruns + 255) / 256, 65536);
+  if (to_blocked)
+    hipLaunchKernelGGL(mm8t_block_kernel, dim3(gx), dim3(256), 0, as_stream(stream), src, so, si, (int)I, (int)O, dst,
+                       nruns);
+  else
+    hipLaunchKernelGGL(mm8t_unblock_kernel, dim3(gx), dim3(256), 0, as_stream(stream), src, (int)I, (int)O, dst, so,
+                       si, nruns);
+  return check_launch(who);
+}
+
+extern "C" int rwkv7mi_mm8t_block(const uint8_t* src, int64_t stride_o, int64_t stride_i, int64_t I, int64_t O,
+                                  uint8_t* w_blk, void* stream) {
+  return mm8t_relayout(true, src, w_blk, I, O, stride_o, stride_i, stream, "mm8t_block");
+}
+
+extern "C" int rwkv7mi_mm8t_unblock(const uint8_t* w_blk, int64_t I, int64_t O, uint8_t* dst, int64_t stride_o,
+                                    int64_t stride_i, void* stream) {
+  return mm8t_relayout(false, w_blk, dst, I, O, stride_o, stride_i, stream, "mm8t_unblock");
+}
+
+extern "C" int rwkv7mi_mm8t_dequant(const uint8_t* w_blk, const void* mx, const void* rx, const void* my,
                                     const void* ry, void* out, int64_t I, int64_t O, int meta_dtype, int out_dtype,
                                     void* stream) {
   if (I <= 0 || O <= 0 || I % 4 || I > INT32_MAX || O > INT32_MAX) return fail(RWKV7MI_EINVAL, "mm8t_dequant: bad shape");
-  if (!w_t || !mx || !rx || !my || !ry || !out) return fail(RWKV7MI_EINVAL, "mm8t_dequant: null pointer");
-  if (reinterpret_cast<uintptr_t>(w_t) & 3) return fail(RWKV7MI_EINVAL, "mm8t_dequant: w_t must be 4-byte aligned");
+  if (!w_blk || !mx || !rx || !my || !ry || !out) return fail(RWKV7MI_EINVAL, "mm8t_dequant: null pointer");
+  if (reinterpret_cast<uintptr_t>(w_blk) & 15) return fail(RWKV7MI_EINVAL, "mm8t_dequant: w_blk must be 16-byte aligned");
   return dispatch_dtype(meta_dtype, [&](auto tm) {
     using TM = decltype(tm);
     return dispatch_dtype(out_dtype, [&](auto to) {
       using TO = decltype(to);
       const int gx = (int)std::min<int64_t>((I / 4 + 255) / 256, 64);
       hipLaunchKernelGGL((mm8t_dequant_kernel<TM, TO>), dim3(gx, (unsigned)std::min<int64_t>(O, 32768)), dim3(256), 0, as_stream(stream),
-                         w_t, (const TM*)mx, (const TM*)rx, (const TM*)my, (const TM*)ry, (TO*)out, (int)I, (int)O);
+                         w_blk, (const TM*)mx, (const TM*)rx, (const TM*)my, (const TM*)ry, (TO*)out, (int)I, (int)O);
       return check_launch("mm8t_dequant_kernel");
     });
   });

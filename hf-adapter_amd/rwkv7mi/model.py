@@ -30,7 +30,7 @@ from .fused_output import fused_attn_output_prepare
 from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
-from .native_quant_mm8 import MM8Linear, is_out_major, mm8_lnmix_multi_into, mm8_matmul_multi_into
+from .native_quant_mm8 import MM8Linear, is_blocked, mm8_lnmix_multi_into, mm8_matmul_multi_into
 from .native_quant_policy import should_quantize_linear
 from .self_chunk_rwkv7 import _run_chunk
 
@@ -190,18 +190,11 @@ class QuantLinear:
         rows = int(x2.shape[0])
         if rows > self.GEMV_ROWS:
             m = self.m
-            if is_out_major(m.w_u8):
-                W = torch.empty((m.out_features, m.in_features), device=x2.device, dtype=x2.dtype)
-                _lib.call("rwkv7mi_mm8t_dequant", _lib.ptr(m.w_u8), _lib.ptr(m.mx), _lib.ptr(m.rx), _lib.ptr(m.my),
-                          _lib.ptr(m.ry), _lib.ptr(W), m.in_features, m.out_features, _lib.dtype_code(m.mx),
-                          _lib.dtype_code(W), _lib.stream_of(x2))
-                y = torch.nn.functional.linear(x2, W)
-            else:
-                W = torch.empty((m.in_features, m.out_features), device=x2.device, dtype=x2.dtype)
-                _lib.call("rwkv7mi_mm8_dequant", _lib.ptr(m.w_u8), _lib.ptr(m.mx), _lib.ptr(m.rx), _lib.ptr(m.my),
-                          _lib.ptr(m.ry), _lib.ptr(W), m.in_features, m.out_features, _lib.dtype_code(m.mx),
-                          _lib.dtype_code(W), _lib.stream_of(x2))
-                y = x2 @ W
+            W = torch.empty((m.out_features, m.in_features), device=x2.device, dtype=x2.dtype)
+            _lib.call("rwkv7mi_mm8t_dequant", _lib.ptr(m.w_blk), _lib.ptr(m.mx), _lib.ptr(m.rx), _lib.ptr(m.my),
+                      _lib.ptr(m.ry), _lib.ptr(W), m.in_features, m.out_features, _lib.dtype_code(m.mx),
+                      _lib.dtype_code(W), _lib.stream_of(x2))
+            y = torch.nn.functional.linear(x2, W)
             if m.bias is not None:
                 y = y + m.bias
             if act == 3:
@@ -220,7 +213,7 @@ class QuantLinear:
         rows = int(xs[0].shape[0])
         if (all(isinstance(l, QuantLinear) for l in lins) and rows <= QuantLinear.GEMV_ROWS
                 and len({(l.in_features, l.out_features) for l in lins}) == 1
-                and all(is_out_major(l.m.w_u8) for l in lins)):
+                and all(is_blocked(l.m.w_blk) for l in lins)):
             mm8_matmul_multi_into(list(xs), [l.m for l in lins], list(outs))
             return outs
         for l, x2, o in zip(lins, xs, outs):
@@ -466,7 +459,7 @@ class NativeRWKV7ForCausalLM:
             return False
         for L in self.layers:
             for lin in (L.r_proj, L.k_proj, L.v_proj, L.key):
-                if (not isinstance(lin, QuantLinear) or not is_out_major(lin.m.w_u8) or lin.m.bias is not None
+                if (not isinstance(lin, QuantLinear) or not is_blocked(lin.m.w_blk) or lin.m.bias is not None
                         or lin.m.mx.dtype != self.dtype):
                     return False
             if len({(l.in_features, l.out_features) for l in (L.r_proj, L.k_proj, L.v_proj)}) != 1:

@@ -72,6 +72,49 @@ def quantize_mm8_outmajor(weight: torch.Tensor):
     return w_t.t(), mx, rx, my, ry
 
 
+def mm8_block(w_u8: torch.Tensor) -> torch.Tensor:
+    """The decode GEMV's blocked copy of ``w_u8 [in, out]`` (any strides):
+    ``[ceil(out/16), ceil(in/128), 2048]`` uint8, tile ``(g, b)`` holding at
+    byte ``1024 h + 16 (16 q + c) + e`` the weight of output ``16 g + c`` and
+    input ``128 b + 64 h + 16 q + e``; edges padded with zeros.  A wave's
+    128-input step of 16 outputs is one contiguous 2 KB run."""
+    if w_u8.dim() != 2 or w_u8.dtype != torch.uint8:
+        raise ValueError("mm8_block expects a 2-D uint8 [in, out] tensor")
+    _lib.require_gpu(w_u8, name="mm8_block")
+    n, m = (int(s) for s in w_u8.shape)
+    out = torch.empty(((m + 15) // 16, (n + 127) // 128, 2048), device=w_u8.device, dtype=torch.uint8)
+    # element (i, o) sits at i * stride(0) + o * stride(1)
+    _lib.call("rwkv7mi_mm8t_block", _lib.ptr(w_u8), int(w_u8.stride(1)), int(w_u8.stride(0)), n, m, _lib.ptr(out),
+              _lib.stream_of(w_u8))
+    return out
+
+
+def mm8_unblock(w_blk: torch.Tensor, in_features: int, out_features: int) -> torch.Tensor:
+    """Inverse of :func:`mm8_block`: the reference's contiguous ``w_u8 [in, out]``."""
+    if not is_blocked(w_blk):
+        raise ValueError("mm8_unblock expects a blocked MM8 tensor")
+    n, m = int(in_features), int(out_features)
+    if tuple(w_blk.shape[:2]) != ((m + 15) // 16, (n + 127) // 128):
+        raise ValueError(f"mm8_unblock: blocked shape {tuple(w_blk.shape)} does not match [{n}, {m}]")
+    out = torch.empty((n, m), device=w_blk.device, dtype=torch.uint8)
+    _lib.call("rwkv7mi_mm8t_unblock", _lib.ptr(w_blk), n, m, _lib.ptr(out), 1, m, _lib.stream_of(w_blk))
+    return out
+
+
+def is_blocked(w: torch.Tensor) -> bool:
+    """True for the decode GEMV's blocked weight tensor (see :func:`mm8_block`)."""
+    return (w.dim() == 3 and int(w.shape[2]) == 2048 and w.dtype == torch.uint8 and w.is_contiguous())
+
+
+def quantize_mm8_blocked(weight: torch.Tensor):
+    """``quantize_mm8_outmajor`` with the bytes in the blocked decode layout:
+    ``(w_blk, mx, rx, my, ry)``."""
+    w_u8, mx, rx, my, ry = quantize_mm8_outmajor(weight)
+    w_blk = mm8_block(w_u8)
+    del w_u8
+    return w_blk, mx, rx, my, ry
+
+
 def is_out_major(w_u8: torch.Tensor) -> bool:
     """True when ``w_u8 [N, M]`` is the transposed view of contiguous ``[M, N]`` bytes."""
     return (w_u8.dim() == 2 and not w_u8.is_contiguous() and w_u8.t().is_contiguous())
@@ -94,26 +137,36 @@ def _check_out(x2, m, out, residual):
 
 
 def mm8_matmul_into(x2, w_u8, mx, rx, my, ry, out, *, bias=None, residual=None, epilogue=_lib.EPI_NONE):
-    """``out[rows, M] = epilogue(x2[rows, N] @ dequant(W))`` with no allocation.
+    """``out[rows, M] = epilogue(x2[rows, N] @ dequant(W))``.
 
-    ``w_u8`` is either contiguous ``[N, M]`` (the reference's storage) or the
-    out-major view made by :func:`quantize_mm8_outmajor`; each has its kernel.
+    ``w_u8`` is the blocked tensor of :func:`mm8_block` (the decode layout, no
+    allocation), contiguous ``[N, M]`` (the reference's storage; its own
+    kernel with a workspace slot) or the out-major view of
+    :func:`quantize_mm8_outmajor` (blocked into a temporary first).
     """
     rows, n = (int(s) for s in x2.shape)
-    m = int(w_u8.shape[1])
-    if int(w_u8.shape[0]) != n:
-        raise ValueError(f"mm8: x has {n} features but w_u8 is {tuple(w_u8.shape)}")
     _lib.require_gpu(x2, w_u8, out, name="mm8_matmul")
-    residual = _check_out(x2, m, out, residual)
     if is_out_major(w_u8):
+        if int(w_u8.shape[0]) != n:
+            raise ValueError(f"mm8: x has {n} features but w_u8 is {tuple(w_u8.shape)}")
+        w_u8 = mm8_block(w_u8)
+    if is_blocked(w_u8):
+        m = int(mx.numel())
+        if tuple(w_u8.shape[:2]) != ((m + 15) // 16, (n + 127) // 128) or int(ry.numel()) != n:
+            raise ValueError(f"mm8: blocked weights {tuple(w_u8.shape)} do not match [{n}, {m}]")
+        residual = _check_out(x2, m, out, residual)
         _lib.call(
             "rwkv7mi_mm8t_matmul", _lib.ptr(x2), _lib.ptr(w_u8), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my),
             _lib.ptr(ry), _lib.ptr(bias), _lib.ptr(residual), _lib.ptr(out), rows, n, m, int(epilogue),
             _lib.dtype_code(x2), _lib.dtype_code(mx), _lib.stream_of(x2),
         )
         return out
+    m = int(w_u8.shape[1])
+    if int(w_u8.shape[0]) != n:
+        raise ValueError(f"mm8: x has {n} features but w_u8 is {tuple(w_u8.shape)}")
+    residual = _check_out(x2, m, out, residual)
     if not w_u8.is_contiguous():
-        raise ValueError("mm8: w_u8 must be contiguous [N, M] or the out-major view")
+        raise ValueError("mm8: w_u8 must be blocked, contiguous [N, M] or the out-major view")
     ws = _ws.reserve(x2.device, mm8_workspace_bytes(rows, n, m))
     _lib.call(
         "rwkv7mi_mm8_matmul", _lib.ptr(x2), _lib.ptr(w_u8), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my),
@@ -138,14 +191,14 @@ def mm8_matmul_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
     for x2, mod, out, r in zip(xs, mods, outs, residuals):
         if tuple(x2.shape) != (rows, n) or not x2.is_contiguous() or x2.dtype != xs[0].dtype:
             raise ValueError("mm8_matmul_multi_into: inputs must share one contiguous shape and dtype")
-        if mod.in_features != n or mod.out_features != m or not is_out_major(mod.w_u8):
-            raise ValueError("mm8_matmul_multi_into: modules must be out-major and share one shape")
+        if mod.in_features != n or mod.out_features != m or not is_blocked(mod.w_blk):
+            raise ValueError("mm8_matmul_multi_into: modules must be blocked MM8Linear of one shape")
         _check_out(x2, m, out, r)
     _lib.require_gpu(*xs, *outs, name="mm8_matmul_multi")
     arr = lambda ts: _lib.ptr_array(ts)
     eps = (ctypes.c_int * k)(*[int(e) for e in epilogues])
     _lib.call(
-        "rwkv7mi_mm8t_matmul_multi", k, arr(xs), arr([md.w_u8 for md in mods]), arr([md.mx for md in mods]),
+        "rwkv7mi_mm8t_matmul_multi", k, arr(xs), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
         arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),
         arr([md.bias for md in mods]), arr(residuals), arr(outs), eps,
         rows, n, m, _lib.dtype_code(xs[0]), _lib.dtype_code(mods[0].mx), _lib.stream_of(xs[0]),
@@ -187,8 +240,8 @@ def mm8_lnmix_multi_into(x, prev, ln_w, ln_b, eps: float, mixes, mods, outs, *, 
     if any(t.data_ptr() in reads for t in (*outs, *aux_outs, *([h_out] if h_out is not None else []))):
         raise ValueError("mm8_lnmix_multi_into: outputs must not alias x or prev (every workgroup reads them)")
     for mod, out in zip(mods, outs):
-        if mod.in_features != n or mod.out_features != m or not is_out_major(mod.w_u8) or mod.bias is not None:
-            raise ValueError("mm8_lnmix_multi_into: out-major modules of one shape, without bias")
+        if mod.in_features != n or mod.out_features != m or not is_blocked(mod.w_blk) or mod.bias is not None:
+            raise ValueError("mm8_lnmix_multi_into: blocked MM8Linear modules of one shape, without bias")
         if mod.mx.dtype != dt:
             raise ValueError("mm8_lnmix_multi_into: MM8 metadata must be in the activation dtype")
         _check_out(x, m, out, None)
@@ -198,7 +251,7 @@ def mm8_lnmix_multi_into(x, prev, ln_w, ln_b, eps: float, mixes, mods, outs, *, 
     na = len(aux_mixes)
     _lib.call(
         "rwkv7mi_mm8t_lnmix_multi", k, _lib.ptr(x), _lib.ptr(prev), _lib.ptr(vecs[0]), _lib.ptr(vecs[1]),
-        float(eps), arr(vecs[2:2 + k]), arr([md.w_u8 for md in mods]), arr([md.mx for md in mods]),
+        float(eps), arr(vecs[2:2 + k]), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
         arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]), arr(outs),
         (ctypes.c_int * k)(*[int(e) for e in epilogues]), _lib.ptr(h_out), na, arr(vecs[2 + k:]), arr(list(aux_outs)),
         rows, n, m, _lib.dtype_code(x), _lib.stream_of(x),
@@ -215,7 +268,7 @@ def _meta_1d(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 
 def mm8_matmul(x, w_u8, mx, rx, my, ry):
     """``y = x @ dequant(W)`` for ``x: [..., N]`` -> ``[..., M]`` (fused HIP kernel)."""
-    n, m = (int(s) for s in w_u8.shape)
+    n, m = int(ry.numel()), int(mx.numel())
     lead = x.shape[:-1]
     x2 = x.reshape(-1, n).contiguous()
     mdt = mx.dtype
@@ -240,18 +293,20 @@ def mm8_matmul_triton(x, w_u8, mx, rx, my, ry, *, max_gemv_rows: int | None = No
 class MM8Linear(torch.nn.Module):
     """Drop-in for ``nn.Linear`` storing int8 (mm8) weights, dequantized on the fly.
 
-    Buffers match the reference module (rwkv7_hf/native_quant_mm8.py:583-589):
+    The state dict matches the reference module (rwkv7_hf/native_quant_mm8.py:583-589):
     ``w_u8 [in, out]``, ``mx, rx [out]``, ``my, ry [in, 1]`` and optional
-    ``bias``, with the same values.  ``w_u8`` is stored out-major (it is the
-    transposed view of ``[out, in]`` bytes), the layout the decode GEMV
-    streams; ``load_state_dict`` copies a reference ``w_u8`` into it.
+    ``bias``, with the same values.  The bytes live in the decode GEMV's
+    blocked layout (``w_blk``, see :func:`mm8_block`); ``state_dict`` writes
+    them back as the reference's ``w_u8`` and ``load_state_dict`` accepts a
+    reference ``w_u8`` (hooks below), and the ``w_u8`` attribute materialises
+    the reference tensor.
     """
 
     def __init__(self, linear, *, fused=True):
         super().__init__()
         self.in_features, self.out_features = int(linear.weight.shape[1]), int(linear.weight.shape[0])
-        wu8, mx, rx, my, ry = quantize_mm8_outmajor(linear.weight.data)
-        self.register_buffer("w_u8", wu8)
+        w_blk, mx, rx, my, ry = quantize_mm8_blocked(linear.weight.data)
+        self.register_buffer("w_blk", w_blk, persistent=False)
         self.register_buffer("mx", mx)
         self.register_buffer("rx", rx)
         self.register_buffer("my", my)
@@ -262,6 +317,32 @@ class MM8Linear(torch.nn.Module):
             self.bias = None
         self.fused = bool(fused)
         self.sm7x_rowwise = False
+        self.register_state_dict_post_hook(MM8Linear._export_w_u8)
+        self.register_load_state_dict_pre_hook(MM8Linear._import_w_u8)
+
+    @property
+    def w_u8(self) -> torch.Tensor:
+        """The reference's ``w_u8 [in, out]`` (a new contiguous tensor)."""
+        return mm8_unblock(self.w_blk, self.in_features, self.out_features)
+
+    @staticmethod
+    def _export_w_u8(module, state_dict, prefix, local_metadata):
+        state_dict[prefix + "w_u8"] = module.w_u8
+
+    @staticmethod
+    def _import_w_u8(module, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys, error_msgs):
+        key = prefix + "w_u8"
+        if key not in state_dict:
+            if strict:
+                missing_keys.append(key)
+            return
+        w = state_dict.pop(key)
+        if tuple(w.shape) != (module.in_features, module.out_features) or w.dtype != torch.uint8:
+            error_msgs.append(f"{key}: expected uint8 [{module.in_features}, {module.out_features}], "
+                              f"got {w.dtype} {tuple(w.shape)}")
+            return
+        with torch.no_grad():
+            module.w_blk.copy_(mm8_block(w.to(module.w_blk.device)))
 
     def _run(self, x, out=None, residual=None, epilogue=_lib.EPI_NONE):
         lead = x.shape[:-1]
@@ -273,7 +354,7 @@ class MM8Linear(torch.nn.Module):
             out2 = torch.empty((rows, self.out_features), device=x.device, dtype=x.dtype)
         else:
             out2 = out.reshape(rows, self.out_features)
-        mm8_matmul_into(x2, self.w_u8, self.mx, self.rx, self.my.reshape(-1), self.ry.reshape(-1), out2,
+        mm8_matmul_into(x2, self.w_blk, self.mx, self.rx, self.my.reshape(-1), self.ry.reshape(-1), out2,
                         bias=self.bias, residual=residual, epilogue=epilogue)
         return out2.reshape(*lead, self.out_features) if out is None else out
 
@@ -290,9 +371,7 @@ class MM8Linear(torch.nn.Module):
         return self._run(x, residual=residual.contiguous(), epilogue=_lib.EPI_RESIDUAL)
 
     def rwkv7_workspace_bytes(self, rows: int) -> int:
-        if is_out_major(self.w_u8):
-            return 0
-        return mm8_workspace_bytes(rows, self.in_features, self.out_features)
+        return 0  # the blocked GEMV needs none
 
     def extra_repr(self):
         return f"in={self.in_features}, out={self.out_features}, mm8(fused={self.fused}, hip=gfx950)"
@@ -317,7 +396,8 @@ def quantize_model_mm8(model, *, min_params: int = 8_000_000, fused: bool = True
 
 
 __all__ = [
-    "quantize_mm8", "quantize_mm8_outmajor", "is_out_major", "mm8_matmul", "mm8_linear", "mm8_matmul_into",
+    "quantize_mm8", "quantize_mm8_outmajor", "quantize_mm8_blocked", "mm8_block", "mm8_unblock", "is_blocked",
+    "is_out_major", "mm8_matmul", "mm8_linear", "mm8_matmul_into",
     "mm8_matmul_multi_into", "mm8_gemv_triton",
     "mm8_matmul_triton", "mm8_workspace_bytes", "MM8Linear", "quantize_model_mm8",
 ]

@@ -177,11 +177,27 @@ int rwkv7mi_mm8_dequant(const uint8_t* w_u8, const void* mx, const void* rx,
                         const void* my, const void* ry, void* out, int64_t I,
                         int64_t O, int meta_dtype, int out_dtype, void* stream);
 
-/* Out-major MM8 (the decode path).  Same values as the [I,O] format, stored
- * as w_t[o*I + i] == w_u8[i, o], i.e. in nn.Linear.weight's [O,I] layout; the
- * reference's w_u8 buffer (rwkv7_hf/native_quant_mm8.py:583, uint8 [in, out])
- * is the transposed view of w_t.  The reference picks its own per-device
+/* Blocked MM8 (the decode path).  Same values as the [I,O] format; the bytes
+ * are stored per output-column group g (16 outputs) and K block b (128
+ * inputs) as one 2048-byte tile at byte (g*KB + b)*2048, KB = ceil(I/128),
+ * holding at byte 1024*h + 16*(16*q + c) + e the weight of output 16*g + c
+ * and input 128*b + 64*h + 16*q + e (h<2, q<4, c<16, e<16), zero padded:
+ * rwkv7mi_mm8t_blocked_bytes(I, O) bytes.  A wave's 128-input step of 16
+ * outputs is one contiguous 2 KB run.  The reference's w_u8 buffer
+ * (rwkv7_hf/native_quant_mm8.py:583, uint8 [in, out]) converts with
+ * rwkv7mi_mm8t_block / _unblock; the reference picks its own per-device
  * buffer layout the same way (q_row [out, in] at :578-580). */
+
+size_t rwkv7mi_mm8t_blocked_bytes(int64_t I, int64_t O);
+
+/* src element (output o, input i) at src[o*stride_o + i*stride_i] (e.g. the
+ * reference w_u8 [I,O]: stride_o 1, stride_i O) -> w_blk; w_blk 16-byte
+ * aligned. */
+int rwkv7mi_mm8t_block(const uint8_t* src, int64_t stride_o, int64_t stride_i,
+                       int64_t I, int64_t O, uint8_t* w_blk, void* stream);
+/* w_blk -> dst[o*stride_o + i*stride_i]. */
+int rwkv7mi_mm8t_unblock(const uint8_t* w_blk, int64_t I, int64_t O, uint8_t* dst,
+                         int64_t stride_o, int64_t stride_i, void* stream);
 
 /* Packer from Linear.weight [O,I] itself: same outputs as rwkv7mi_mm8_pack on
  * weight.T, with w_t [O,I].  Workspace as for rwkv7mi_mm8_pack. */
@@ -189,12 +205,11 @@ int rwkv7mi_mm8_pack_t(const void* weight, int64_t I, int64_t O, int w_dtype,
                        uint8_t* w_t, void* mx, void* rx, void* my, void* ry,
                        float* workspace, void* stream);
 
-/* y[rows,O] = epilogue(x[rows,I] @ dequant(W)) over out-major w_t; no
+/* y[rows,O] = epilogue(x[rows,I] @ dequant(W)) over blocked w_blk; no
  * workspace, deterministic.  Replaces mm8_gemv_triton / mm8_matmul_triton /
- * MM8Linear.forward (rwkv7_hf/native_quant_mm8.py:383, :468, :594) when the
- * module stores out-major bytes.  I % 16 == 0; x, w_t, my, ry 16-byte
- * aligned; y may alias residual. */
-int rwkv7mi_mm8t_matmul(const void* x, const uint8_t* w_t, const void* mx,
+ * MM8Linear.forward (rwkv7_hf/native_quant_mm8.py:383, :468, :594).
+ * I % 16 == 0; x, w_blk, my, ry 16-byte aligned; y may alias residual. */
+int rwkv7mi_mm8t_matmul(const void* x, const uint8_t* w_blk, const void* mx,
                         const void* rx, const void* my, const void* ry,
                         const void* bias, const void* residual, void* y,
                         int64_t rows, int64_t I, int64_t O, int epilogue,
@@ -204,7 +219,7 @@ int rwkv7mi_mm8t_matmul(const void* x, const uint8_t* w_t, const void* mx,
  * r/k/v projections of rwkv7_hf/native.py:193-195).  Arrays have nprob
  * entries; bias and residual arrays may be NULL. */
 int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x,
-                              const uint8_t* const* w_t, const void* const* mx,
+                              const uint8_t* const* w_blk, const void* const* mx,
                               const void* const* rx, const void* const* my,
                               const void* const* ry, const void* const* bias,
                               const void* const* residual, void* const* y,
@@ -212,8 +227,6 @@ int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x,
                               int64_t O, int act_dtype, int meta_dtype,
                               void* stream);
 
-/* dequantize_mm8 (rwkv7_hf/native_quant_mm8.py:100-108) into out [O,I]
- * (Linear.weight layout) for a library GEMM on long prefills.  I % 4 == 0. */
 /* Decode LN + token-shift mix fused into the out-major MM8 GEMV: for up to
  * four problems of one shape, h = LayerNorm(x) (x [rows, I] the residual
  * rows, ln_w / ln_b [I]), x_p = round(h + (prev - h) * mix_p) and
@@ -227,7 +240,7 @@ int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x,
  * x or prev. */
 int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* prev,
                              const void* ln_w, const void* ln_b, float eps,
-                             const void* const* mix, const uint8_t* const* w_t,
+                             const void* const* mix, const uint8_t* const* w_blk,
                              const void* const* mx, const void* const* rx,
                              const void* const* my, const void* const* ry,
                              void* const* y, const int* epilogue, void* h_out,
@@ -235,7 +248,10 @@ int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* prev,
                              int64_t rows, int64_t I, int64_t O, int act_dtype,
                              void* stream);
 
-int rwkv7mi_mm8t_dequant(const uint8_t* w_t, const void* mx, const void* rx,
+/* dequantize_mm8 (rwkv7_hf/native_quant_mm8.py:100-108) from w_blk into out
+ * [O,I] (Linear.weight layout) for a library GEMM on long prefills.
+ * I % 4 == 0. */
+int rwkv7mi_mm8t_dequant(const uint8_t* w_blk, const void* mx, const void* rx,
                          const void* my, const void* ry, void* out, int64_t I,
                          int64_t O, int meta_dtype, int out_dtype, void* stream);
 

@@ -1,7 +1,9 @@
-"""GPU parity of the out-major MM8 path: the packer from Linear.weight is
-bit-identical to the row-major packer (and so to the oracle), the fused GEMV /
-small-batch GEMM matches the fp64 oracle, the grouped launch equals single
-launches bit for bit, and the out-major dequantisation equals the row-major one."""
+"""GPU parity of the blocked MM8 decode path: the packer from Linear.weight is
+bit-identical to the row-major packer (and so to the oracle), the blocked byte
+layout matches its numpy restatement and round-trips to the reference w_u8,
+the fused GEMV / small-batch GEMM matches the fp64 oracle, the grouped launch
+equals single launches bit for bit, and the blocked dequantisation equals the
+row-major one."""
 from __future__ import annotations
 
 import numpy as np
@@ -43,6 +45,36 @@ def test_pack_outmajor_equals_rowmajor(oracle, OI, dtype):
         np.testing.assert_array_equal(_np(b[0]), q)
 
 
+def _block_np(w_u8):
+    """numpy restatement of the blocked decode layout of w_u8 [I, O]."""
+    I, O = w_u8.shape
+    G, KB = (O + 15) // 16, (I + 127) // 128
+    P = np.zeros((G * 16, KB * 128), np.uint8)
+    P[:O, :I] = w_u8.T
+    # tile (g, b), byte 1024 h + 16 (16 q + c) + e  <-  output 16 g + c, input 128 b + 64 h + 16 q + e
+    return P.reshape(G, 16, KB, 2, 4, 16).transpose(0, 2, 3, 4, 1, 5).reshape(G, KB, 2048)
+
+
+@pytest.mark.parametrize("OI", [(256, 128), (128, 256), (1024, 4096), (40, 48), (3, 16), (200, 1040)])
+def test_block_layout_round_trip(OI):
+    from rwkv7mi.native_quant_mm8 import is_blocked, mm8_block, mm8_unblock, quantize_mm8_blocked, quantize_mm8_outmajor
+
+    O, I = OI
+    rng = np.random.default_rng(O + 3 * I)
+    Wl = _cuda(rng.standard_normal((O, I)) * 0.02, torch.float16)
+    w_om, *meta = quantize_mm8_outmajor(Wl)
+    w_blk, *meta2 = quantize_mm8_blocked(Wl)
+    torch.cuda.synchronize()
+    assert is_blocked(w_blk)
+    for a, b in zip(meta, meta2):
+        assert torch.equal(a, b)
+    ref = _block_np(_np(w_om))
+    np.testing.assert_array_equal(_np(w_blk), ref)
+    # from the reference's row-major [I, O] and back
+    np.testing.assert_array_equal(_np(mm8_block(w_om.contiguous())), ref)
+    np.testing.assert_array_equal(_np(mm8_unblock(w_blk, I, O)), _np(w_om))
+
+
 SHAPES = [(4096, 4096), (4096, 1024), (16384, 512), (144, 40), (1024, 65), (16, 16)]
 # BASELINE configs[2]: the RWKV-7 1.5B projection and head shapes at batch 1, 8, 32
 C3 = [(2048, 2048), (2048, 8192), (8192, 2048), (2048, 65536)]
@@ -51,18 +83,19 @@ C3 = [(2048, 2048), (2048, 8192), (8192, 2048), (2048, 65536)]
 @pytest.mark.parametrize("IO", SHAPES)
 @pytest.mark.parametrize("rows", [1, 2, 5, 8, 16, 17, 40, 64])
 def test_mm8t_matmul_matches_oracle(oracle, IO, rows):
-    from rwkv7mi.native_quant_mm8 import mm8_matmul, quantize_mm8_outmajor
+    from rwkv7mi.native_quant_mm8 import mm8_matmul, mm8_unblock, quantize_mm8_blocked
 
     I, O = IO
     rng = np.random.default_rng(I * 3 + O + rows)
     Wl = _cuda(rng.standard_normal((O, I)) * 0.02, torch.float16)
-    packed = quantize_mm8_outmajor(Wl)
+    packed = quantize_mm8_blocked(Wl)
     x = rng.standard_normal((rows, I)).astype(np.float16)
     xt = _cuda(x, torch.float16)
     y = mm8_matmul(xt, *packed)
     y2 = mm8_matmul(xt, *packed)
     torch.cuda.synchronize()
-    ref = oracle.mm8_matmul(x.astype(np.float64), *(_np(p) for p in packed))
+    w_u8 = mm8_unblock(packed[0], I, O)
+    ref = oracle.mm8_matmul(x.astype(np.float64), *(_np(p) for p in (w_u8, *packed[1:])))
     err = _rel_err(_np(y).astype(np.float64), ref)
     assert err <= 2e-3, err
     assert torch.equal(y, y2), "repeated calls must be bit-identical"
@@ -94,7 +127,7 @@ def test_mm8t_dtypes(oracle, act, meta):
 
 def test_mm8t_epilogues_in_place_and_module(oracle):
     from rwkv7mi import MM8Linear
-    from rwkv7mi.native_quant_mm8 import is_out_major
+    from rwkv7mi.native_quant_mm8 import is_blocked
 
     rng = np.random.default_rng(5)
     I, O, rows = 1024, 4096, 3
@@ -103,7 +136,8 @@ def test_mm8t_epilogues_in_place_and_module(oracle):
         lin.weight.copy_(_cuda(rng.standard_normal((O, I)) * 0.02, torch.float16))
         lin.bias.copy_(_cuda(rng.standard_normal(O) * 0.1, torch.float16))
     mod = MM8Linear(lin)
-    assert is_out_major(mod.w_u8) and mod.rwkv7_workspace_bytes(rows) == 0
+    assert is_blocked(mod.w_blk) and mod.rwkv7_workspace_bytes(rows) == 0
+    assert tuple(mod.w_u8.shape) == (I, O) and mod.w_u8.is_contiguous()
     x = _cuda(rng.standard_normal((rows, I)), torch.float16)
     res = _cuda(rng.standard_normal((rows, O)), torch.float16)
     packed = [_np(b) for b in (mod.w_u8, mod.mx, mod.rx, mod.my, mod.ry)]
@@ -119,14 +153,17 @@ def test_mm8t_epilogues_in_place_and_module(oracle):
     assert np.abs(_np(relu2) - r2).max() <= 4e-3 * np.abs(r2).max()
     add = base + _np(res).astype(np.float64)
     assert np.abs(_np(acc) - add).max() <= 2e-3 * np.abs(add).max()
-    # a reference-layout state dict loads into the out-major buffer
+    # the state dict holds the reference's keys and layout, and loads back
     sd = {k: v.clone() for k, v in mod.state_dict().items()}
-    sd["w_u8"] = sd["w_u8"].contiguous()
+    assert set(sd) == {"w_u8", "mx", "rx", "my", "ry", "bias"}
+    assert tuple(sd["w_u8"].shape) == (I, O) and torch.equal(sd["w_u8"], mod.w_u8)
     mod2 = MM8Linear(lin)
     with torch.no_grad():
-        mod2.w_u8.zero_()
+        mod2.w_blk.zero_()
     mod2.load_state_dict(sd)
-    assert is_out_major(mod2.w_u8) and torch.equal(mod2.w_u8, mod.w_u8)
+    assert torch.equal(mod2.w_blk, mod.w_blk)
+    with pytest.raises(RuntimeError):
+        mod2.load_state_dict({k: v for k, v in sd.items() if k != "w_u8"})
 
 
 @pytest.mark.parametrize("rows", [1, 8, 20])
@@ -154,18 +191,19 @@ def test_mm8t_multi_equals_single(rows):
 @pytest.mark.parametrize("IO", [(256, 512), (4096, 1024)])
 def test_mm8t_dequant_equals_rowmajor(IO):
     from rwkv7mi import _lib
-    from rwkv7mi.native_quant_mm8 import quantize_mm8_outmajor
+    from rwkv7mi.native_quant_mm8 import mm8_block, quantize_mm8_outmajor
 
     I, O = IO
     rng = np.random.default_rng(I)
     Wl = _cuda(rng.standard_normal((O, I)) * 0.02, torch.float16)
-    w, mx, rx, my, ry = quantize_mm8_outmajor(Wl)
+    w_om, mx, rx, my, ry = quantize_mm8_outmajor(Wl)
+    w = mm8_block(w_om)
     a = torch.empty(O, I, device="cuda", dtype=torch.float16)
     b = torch.empty(I, O, device="cuda", dtype=torch.float16)
     s = _lib.stream_of(a)
     _lib.call("rwkv7mi_mm8t_dequant", _lib.ptr(w), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my), _lib.ptr(ry),
               _lib.ptr(a), I, O, _lib.F16, _lib.F16, s)
-    wc = w.contiguous()
+    wc = w_om.contiguous()
     _lib.call("rwkv7mi_mm8_dequant", _lib.ptr(wc), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my), _lib.ptr(ry),
               _lib.ptr(b), I, O, _lib.F16, _lib.F16, s)
     torch.cuda.synchronize()
