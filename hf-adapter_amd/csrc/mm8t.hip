@@ -86,6 +86,7 @@ struct Mm8tBatch {
   Mm8tProb p[MM8T_MAXPROB];
   Mm8tPro pro;
   int rows, I, O, KC;
+  int gx;  // product workgroups along x; with the LN-mix prologue one more (x == gx) writes h and the extra mixes
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -180,7 +181,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   const int row0 = blockIdx.z * 16;
   const int nrows = min(16, B.rows - row0);
   const int ngroups = (O + MM8T_COLS - 1) / MM8T_COLS;
-  const int gstride = gridDim.x;
+  const int gstride = B.gx;
+  // LN-mix prologue: workgroup x == gx computes no product; it stages the row
+  // like the others and writes h and the extra mixes (its twins for the other
+  // problems exit at once)
+  const bool aux_wg = PRO && (int)blockIdx.x >= B.gx;
+  if (aux_wg && blockIdx.y != 0) return;
   constexpr int XS = KC + 8;  // LDS row stride (halfs)
   extern __shared__ __align__(16) char smem[];
   _Float16* xh = reinterpret_cast<_Float16*>(smem);
@@ -236,10 +242,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   constexpr int SBP = PRO ? SB : 1;
   float pro_mean = 0.f, pro_rstd = 0.f;  // this thread's row statistics
   Raw8<TA> rpv[SBP], rcv[SBP], rwv[SBP], rbv[SBP], rav[SBP][4];
-  // h and the extra mixes of group q are written by workgroup q mod W of the
-  // W that share this row tile, from the registers that staged them
-  const int W = gridDim.x * gridDim.y;
-  const int wl = blockIdx.y * gridDim.x + blockIdx.x;
   // (empty descriptors when the prologue is off: nothing reads them)
   const __amdgpu_buffer_rsrc_t prr =
       mm8t_rsrc(PRO ? reinterpret_cast<const TA*>(B.pro.prev) + (int64_t)row0 * I : nullptr,
@@ -253,12 +255,18 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
     auxr[a] = mm8t_rsrc(PRO && a < B.pro.naux ? B.pro.aux_mix[a] : nullptr,
                         PRO && a < B.pro.naux ? (uint32_t)(I * sizeof(TA)) : 0u);
   auto stage_issue = [&](int kc0, int it0) {
+    // x first: the prologue's row statistics wait on these loads only
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int q = su + (it0 + u) * TPR;
+      const int k = kc0 + 8 * q;
+      rxv[u] = mm8t_ld8<TA>(xr, (uint32_t)(sr * I + k), sr < nrows && q < NQ && k < I);
+    }
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
       const int q = su + (it0 + u) * TPR;
       const int k = kc0 + 8 * q;
       const bool valid = sr < nrows && q < NQ && k < I;
-      rxv[u] = mm8t_ld8<TA>(xr, (uint32_t)(sr * I + k), valid);
       rrv[u] = mm8t_ld8<TM>(ryr, (uint32_t)k, valid);
       rmv[u] = mm8t_ld8<TM>(myr, (uint32_t)k, valid);
       if constexpr (PRO) {
@@ -266,9 +274,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
         rcv[u] = mm8t_ld8<TA>(mixr, (uint32_t)k, valid);
         rwv[u] = mm8t_ld8<TA>(lnwr, (uint32_t)k, valid);
         rbv[u] = mm8t_ld8<TA>(lnbr, (uint32_t)k, valid);
-        const bool own = valid && q % W == wl;
+        if (aux_wg) {  // uniform: the product workgroups issue none of these
 #pragma unroll
-        for (int a = 0; a < 4; ++a) rav[u][a] = mm8t_ld8<TA>(auxr[a], (uint32_t)k, own && a < B.pro.naux);
+          for (int a = 0; a < 4; ++a) rav[u][a] = mm8t_ld8<TA>(auxr[a], (uint32_t)k, valid && a < B.pro.naux);
+        }
       }
     }
   };
@@ -297,7 +306,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
           hv[e] = to_f32(from_f32<TA>((xv[e] - mean) * rstd * wv[e] + bv[e]));
           xv[e] = valid ? to_f32(from_f32<TA>(hv[e] + (pv[e] - hv[e]) * cv[e])) : 0.f;
         }
-        if (valid && q % W == wl) {
+        if (aux_wg && valid) {
           const int64_t off = (int64_t)(row0 + sr) * I + 8 * q;
           if (B.pro.h_out) st8(reinterpret_cast<TA*>(B.pro.h_out) + off, hv);
 #pragma unroll
@@ -404,7 +413,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
     pro_rstd = rsqrtf(row_total(s2, 1) / (float)I + B.pro.eps);  // biased variance, as F.layer_norm
   };
 
-  int g = blockIdx.x;
+  int g = aux_wg ? ngroups : (int)blockIdx.x;           // (the prologue's own workgroup loads nothing)
   __amdgpu_buffer_rsrc_t wr = group_rsrc(g);             // this group
   __amdgpu_buffer_rsrc_t wn = group_rsrc(g + gstride);   // the next one
 
@@ -419,6 +428,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (PRO) pro_stats();  // the whole row is in this batch (checked by the host)
   stage_finish(0);
+  if (aux_wg) return;
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int d = 1; d < DEPTH; ++d) load_step(wr, d, buf[d]);  // DEPTH <= CSW <= J
@@ -711,7 +721,8 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
     const int64_t slots = cus * per_cu / (nprob * rtiles);
     if (slots >= 1 && slots < gx) gx = slots;
   }
-  dim3 grid((unsigned)gx, (unsigned)nprob, (unsigned)rtiles);
+  b.gx = (int)gx;
+  dim3 grid((unsigned)(gx + (pro ? 1 : 0)), (unsigned)nprob, (unsigned)rtiles);
   const int wpc = nw * (nw == 4 && lds <= MM8T_LDS_X ? 2 : 1);  // resident waves per CU
   return dispatch_dtype(act_dtype, [&](auto ta) {
     using TA = decltype(ta);

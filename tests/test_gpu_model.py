@@ -104,7 +104,7 @@ def test_graph_decode_equals_eager_decode(mm8):
 
 @pytest.mark.parametrize("B", [1, 2, 3])
 def test_decode_fused_mix_equals_unfused(B):
-    """The LN + token-shift mixes inside the R/K/V and FFN-key GEMVs (rows <= 2)
+    """The LN + token-shift mixes inside the R/K/V and FFN-key GEMVs (one row)
     against the separate mix kernels: the same logits and shift rows up to
     the statistics' summation order."""
     cfg, model, _ = _build(True, layers=3)
@@ -112,7 +112,7 @@ def test_decode_fused_mix_equals_unfused(B):
     ids = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 5)), device="cuda")
     _, c1 = model(ids)
     c2 = c1.clone()
-    assert model._mix_fusable(B) == (B <= 2)
+    assert model._mix_fusable(B) == (B == 1)
     for step in range(3):
         tok = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 1)), device="cuda")
         model.fused_mix_decode = True
