@@ -219,12 +219,29 @@ def run_decode(batches=(1, 8), steps=64, warmup=5, log=print):
         nbytes.append(sum(mm8_bytes(l, int(x.shape[0])) for l, x in zip(lins, xs)))
         return orig_group(lins, xs, outs)
 
+    import rwkv7mi.model as model_mod
+    orig_lnmix = model_mod.mm8_lnmix_multi_into
+
+    def rec_lnmix(x, prev, ln_w, ln_b, eps, mixes, mods, outs, **kw):
+        # the LN-mix prologue launches (R/K/V and FFN key at one row): weights and
+        # metadata as above, plus the prologue's vectors (x, prev, LN weight and
+        # bias, mixes) and its extra outputs (h, extra mixes)
+        calls.append(lambda: orig_lnmix(x, prev, ln_w, ln_b, eps, mixes, mods, outs, **kw))
+        rows, i = (int(v) for v in x.shape)
+        naux = len(kw.get("aux_outs", ()))
+        extra = (rows * i + 2 * i + len(mixes) * i + rows * i * (1 if kw.get("h_out") is not None else 0)
+                 + naux * (i + rows * i)) * 2
+        nbytes.append(sum(mm8_bytes(m, rows) for m in mods) + extra)
+        return orig_lnmix(x, prev, ln_w, ln_b, eps, mixes, mods, outs, **kw)
+
     QuantLinear.apply = rec_apply
     QuantLinear.apply_group = staticmethod(rec_group)
+    model_mod.mm8_lnmix_multi_into = rec_lnmix
     try:
         model.decode_step_(toks, cache, logits, bufs)
     finally:
         QuantLinear.apply, QuantLinear.apply_group = orig_apply, staticmethod(orig_group)
+        model_mod.mm8_lnmix_multi_into = orig_lnmix
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
