@@ -68,9 +68,11 @@ struct Mm8tProb {
 // the activations are built from the residual row x as
 //   h = LayerNorm(x),  x_p = h + (prev - h) * mix_p   (rounded to the act dtype)
 // inside the x' staging, so no separate mix kernel runs.  Every workgroup
-// computes the row statistics itself; the workgroups between them also write
-// h (the next token's `prev`) and up to four extra mixes of the same h for
-// other consumers, each workgroup a slice of the 8-element groups.
+// computes the row statistics itself.  Workgroups past the products (x >= gx,
+// y == 0) compute no product: the first writes h (the next token's `prev`) and
+// up to four extra mixes of the same h for other consumers; the next `lwgs`
+// ones take those extra mixes as inputs of low-rank down projections (the
+// decode LoRA), whole-K dot products written as fp32.
 struct Mm8tPro {
   const void* prev;  // [rows, I] previous token's LN output
   const void* ln_w;
@@ -80,6 +82,14 @@ struct Mm8tPro {
   void* aux_out[4];  // [rows, I]
   float eps;
   int naux;
+  // LoRA down projections of the extra mixes: lw[a] [lrank[a], I] (act dtype),
+  // lout[loff[a] + row * lrank[a] + j] = mix_a[row] . lw[a][j]
+  const void* lw[4];
+  int lrank[4];
+  int64_t loff[4];
+  float* lout;
+  int lwgs;   // workgroups for them (0: none)
+  int lrtot;  // sum of the ranks
 };
 
 struct Mm8tBatch {
@@ -186,6 +196,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   // like the others and writes h and the extra mixes (its twins for the other
   // problems exit at once)
   const bool aux_wg = PRO && (int)blockIdx.x >= B.gx;
+  const int lora_i = (int)blockIdx.x - B.gx - 1;  // >= 0: a LoRA-down workgroup
   if (aux_wg && blockIdx.y != 0) return;
   constexpr int XS = KC + 8;  // LDS row stride (halfs)
   extern __shared__ __align__(16) char smem[];
@@ -308,7 +319,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
         }
         if (aux_wg && valid) {
           const int64_t off = (int64_t)(row0 + sr) * I + 8 * q;
-          if (B.pro.h_out) st8(reinterpret_cast<TA*>(B.pro.h_out) + off, hv);
+          if (lora_i < 0 && B.pro.h_out) st8(reinterpret_cast<TA*>(B.pro.h_out) + off, hv);
 #pragma unroll
           for (int a = 0; a < 4; ++a) {
             if (a < B.pro.naux) {
@@ -316,7 +327,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
               mm8t_cvt8(rav[u][a], av);
 #pragma unroll
               for (int e = 0; e < 8; ++e) ov[e] = hv[e] + (pv[e] - hv[e]) * av[e];
-              st8(reinterpret_cast<TA*>(B.pro.aux_out[a]) + off, ov);
+              if (lora_i < 0)
+                st8(reinterpret_cast<TA*>(B.pro.aux_out[a]) + off, ov);
+              else  // the LoRA inputs, rounded as the mix tensors are, into LDS
+                st8(reinterpret_cast<TA*>(smem) + (int64_t)(a * nrows + sr) * (I + 8) + 8 * q, ov);
             }
           }
         }
@@ -334,7 +348,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
         sx += xv[e];
         sxmy += xv[e] * mv[e];
       }
-      if (sr < nrows && q < NQ) {
+      if (sr < nrows && q < NQ && !aux_wg) {  // (the LoRA workgroups keep their mixes there)
         *reinterpret_cast<f16x8*>(xh + sr * XS + 8 * q) = hi;
         *reinterpret_cast<f16x8*>(xl + sr * XS + 8 * q) = lo;
       }
@@ -413,6 +427,59 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
     pro_rstd = rsqrtf(row_total(s2, 1) / (float)I + B.pro.eps);  // biased variance, as F.layer_norm
   };
 
+  // LoRA-down workgroup i: outputs j = NW i + wave, + NW lwgs, ... of the
+  // concatenated ranks; each a whole-K dot product of one weight row (lanes
+  // split K in 8-element runs) with the mix staged in LDS, reduced across the
+  // wave in a fixed order
+  auto lora_down = [&](int li) {
+    __syncthreads();
+    const TA* lm = reinterpret_cast<const TA*>(smem);
+    for (int o = li * NW + wave; o < B.pro.lrtot; o += B.pro.lwgs * NW) {
+      int qa = 0, j = o;
+      while (qa < 3 && j >= B.pro.lrank[qa]) {
+        j -= B.pro.lrank[qa];
+        ++qa;
+      }
+      const __amdgpu_buffer_rsrc_t wrr =
+          mm8t_rsrc(reinterpret_cast<const TA*>(B.pro.lw[qa]) + (int64_t)j * I, (uint32_t)(I * sizeof(TA)));
+      float acc[2] = {0.f, 0.f};
+      for (int k0 = 0; k0 < I; k0 += 512 * 4) {
+        Raw8<TA> wv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int k = k0 + 8 * (lane + 64 * u);
+          wv[u] = mm8t_ld8<TA>(wrr, (uint32_t)k, k < I);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int k = k0 + 8 * (lane + 64 * u);
+          float w8[8];
+          mm8t_cvt8(wv[u], w8);
+#pragma unroll
+          for (int rr = 0; rr < 2; ++rr) {
+            if (rr < nrows && k < I) {
+              float x8[8];
+              ld8(lm + (int64_t)(qa * nrows + rr) * (I + 8) + k, x8);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) acc[rr] += w8[e] * x8[e];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        float v = acc[rr];
+        v += dpp_row_ror<8>(v);
+        v += dpp_row_ror<4>(v);
+        v += dpp_row_ror<2>(v);
+        v += dpp_row_ror<1>(v);
+        auto lane_v = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
+        v = (lane_v(v, 0) + lane_v(v, 16)) + (lane_v(v, 32) + lane_v(v, 48));
+        if (rr < nrows && lane == 0) B.pro.lout[B.pro.loff[qa] + (int64_t)(row0 + rr) * B.pro.lrank[qa] + j] = v;
+      }
+    }
+  };
+
   int g = aux_wg ? ngroups : (int)blockIdx.x;           // (the prologue's own workgroup loads nothing)
   __amdgpu_buffer_rsrc_t wr = group_rsrc(g);             // this group
   __amdgpu_buffer_rsrc_t wn = group_rsrc(g + gstride);   // the next one
@@ -428,7 +495,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (PRO) pro_stats();  // the whole row is in this batch (checked by the host)
   stage_finish(0);
-  if (aux_wg) return;
+  if (aux_wg) {
+    if constexpr (PRO) {
+      if (lora_i >= 0) lora_down(lora_i);
+    }
+    return;
+  }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int d = 1; d < DEPTH; ++d) load_step(wr, d, buf[d]);  // DEPTH <= CSW <= J
@@ -712,17 +784,28 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
       return fail(RWKV7MI_EINVAL, w + ": the LN-mix prologue needs the whole row in one staging batch "
                                       "(rows <= 2 at in_features 4096)");
   }
-  const size_t lds = mm8t_lds(rows, b.KC);
+  size_t lds = mm8t_lds(rows, b.KC);
+  int64_t extra = pro ? 1 : 0;  // the prologue's own workgroups (x >= gx, y == 0)
+  if (pro && pro->lrtot > 0) {
+    // LoRA-down workgroups: two outputs per wave (measured best at the 7.2B
+    // ranks: fewer workgroups stream their weights too slowly, more take
+    // product slots); their mixes sit in LDS
+    b.pro.lwgs = (int)((pro->lrtot + 2 * nw - 1) / (2 * nw));
+    extra += b.pro.lwgs;
+    lds = std::max<size_t>(lds, (size_t)pro->naux * (size_t)rows * (size_t)(I + 8) * 2u);
+    if (lds > (size_t)MM8T_LDS_X_ONE) return fail(RWKV7MI_EINVAL, w + ": the LoRA inputs do not fit in LDS");
+  }
   // With x' in one LDS chunk, workgroups loop over column groups: as many as
-  // stay resident, split between the problems and row tiles.
+  // stay resident (less the prologue's own), split between the problems and
+  // row tiles.
   int64_t gx = ngroups;
   if (b.KC >= I) {
     const int64_t per_cu = nw == 4 && lds <= MM8T_LDS_X ? 2 : 1;
-    const int64_t slots = cus * per_cu / (nprob * rtiles);
+    const int64_t slots = (cus * per_cu - extra) / (nprob * rtiles);
     if (slots >= 1 && slots < gx) gx = slots;
   }
   b.gx = (int)gx;
-  dim3 grid((unsigned)(gx + (pro ? 1 : 0)), (unsigned)nprob, (unsigned)rtiles);
+  dim3 grid((unsigned)(gx + extra), (unsigned)nprob, (unsigned)rtiles);
   const int wpc = nw * (nw == 4 && lds <= MM8T_LDS_X ? 2 : 1);  // resident waves per CU
   return dispatch_dtype(act_dtype, [&](auto ta) {
     using TA = decltype(ta);
@@ -773,7 +856,8 @@ extern "C" int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* pr
                                         const uint8_t* const* w_blk, const void* const* mx, const void* const* rx,
                                         const void* const* my, const void* const* ry, void* const* y,
                                         const int* epilogue, void* h_out, int naux, const void* const* aux_mix,
-                                        void* const* aux_out, int64_t rows, int64_t I, int64_t O, int act_dtype,
+                                        void* const* aux_out, const void* const* lora_w, const int64_t* lora_ranks,
+                                        float* lora_out, int64_t rows, int64_t I, int64_t O, int act_dtype,
                                         void* stream) {
   const char* who = "mm8t_lnmix_multi";
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: 1..4 problems per launch");
@@ -798,6 +882,23 @@ extern "C" int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* pr
       return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: extra mixes must be non-null and 16-byte aligned");
     pro.aux_mix[a] = aux_mix[a];
     pro.aux_out[a] = aux_out[a];
+  }
+  if (lora_w) {
+    if (!naux || !lora_ranks || !lora_out || rows > 2)
+      return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: the LoRA down projections need the extra mixes, their ranks, "
+                                  "an output and at most 2 rows");
+    int64_t off = 0;
+    for (int a = 0; a < naux; ++a) {
+      if (!lora_w[a] || (reinterpret_cast<uintptr_t>(lora_w[a]) & 15) || lora_ranks[a] <= 0 || lora_ranks[a] > 4096)
+        return fail(RWKV7MI_EINVAL, "mm8t_lnmix_multi: LoRA down weights must be non-null, 16-byte aligned, "
+                                    "with ranks in 1..4096");
+      pro.lw[a] = lora_w[a];
+      pro.lrank[a] = (int)lora_ranks[a];
+      pro.loff[a] = off;
+      off += rows * lora_ranks[a];
+      pro.lrtot += (int)lora_ranks[a];
+    }
+    pro.lout = lora_out;
   }
   Mm8tProb p[MM8T_MAXPROB];
   for (int i = 0; i < nprob; ++i) {

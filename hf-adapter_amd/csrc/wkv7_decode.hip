@@ -396,10 +396,15 @@ extern "C" int rwkv7mi_wkv7_decode_output_prepare_raw(
                                  act_dtype, act_dtype, param_dtype, stream);
 }
 
+static int lora_splits_for(int64_t nprob, const int64_t* ranks, int64_t D) {
+  return lora_splits(lora_tiles(nprob, ranks), D);
+}
+
 extern "C" int rwkv7mi_wkv7_decode_lora_output_prepare(
     const void* r, const void* k_raw, const void* v, const float* lora_part, int64_t nprob,
     const int64_t* ranks, const void* const* w_up, const void* const* b_up, const int* act_down,
-    const int* act_up, int64_t D, const float* state_in, float* state_out, const void* k_k, const void* k_a,
+    const int* act_up, int64_t D, int64_t lora_splits, const float* state_in, float* state_out, const void* k_k,
+    const void* k_a,
     const void* r_k, const void* gn_w, const void* gn_b, void* out, void* v_first, int v_mode, int64_t B,
     int64_t H, int64_t N, float eps, int act_dtype, int param_dtype, void* stream) {
   if (N != HEAD) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: head size must be 64");
@@ -420,7 +425,8 @@ extern "C" int rwkv7mi_wkv7_decode_lora_output_prepare(
   la.part = lora_part;
   la.nprob = (int)nprob;
   la.rows = (int)B;
-  la.ks = lora_splits(lora_tiles(nprob, ranks), D);
+  if (lora_splits < 0 || lora_splits > 4096) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: bad lora_splits");
+  la.ks = lora_splits ? (int)lora_splits : lora_splits_for(nprob, ranks, D);
   int64_t off = 0;
   for (int p = 0; p < nprob; ++p) {
     if (ranks[p] <= 0 || ranks[p] % 8 || ranks[p] > DL_MAXR || !w_up[p])

@@ -60,7 +60,8 @@ SIGNATURES = {
     "rwkv7mi_mm8t_unblock": (_i32, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p]),
     "rwkv7mi_mm8t_lnmix_multi": (
         _i32,
-        [_i32] + [_c_p] * 4 + [_f32] + [_c_p] * 8 + [_c_p, _i32, _c_p, _c_p, _i64, _i64, _i64, _i32, _c_p],
+        [_i32] + [_c_p] * 4 + [_f32] + [_c_p] * 8 + [_c_p, _i32, _c_p, _c_p, _c_p, _c_p, _c_p]
+        + [_i64, _i64, _i64, _i32, _c_p],
     ),
     "rwkv7mi_mm4_pack": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "rwkv7mi_mm4_pack_t": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
@@ -71,7 +72,7 @@ SIGNATURES = {
     "rwkv7mi_lora_down_multi": (_i32, [_i64] + [_c_p] * 4 + [_i64, _i64, _i32, _c_p, _sz, _c_p]),
     "rwkv7mi_wkv7_decode_lora_output_prepare": (
         _i32,
-        [_c_p] * 4 + [_i64] + [_c_p] * 5 + [_i64] + [_c_p] * 9 + [_i32, _i64, _i64, _i64, _f32, _i32, _i32, _c_p],
+        [_c_p] * 4 + [_i64] + [_c_p] * 5 + [_i64, _i64] + [_c_p] * 9 + [_i32, _i64, _i64, _i64, _f32, _i32, _i32, _c_p],
     ),
     "rwkv7mi_w4g_pack": (_i32, [_c_p, _i64, _i64, _i64, _i32, _c_p, _c_p, _c_p]),
     "rwkv7mi_w4g_matmul": (

@@ -65,14 +65,18 @@ def fused_lora_decode_supported(ranks, rows: int) -> bool:
 
 def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, state, k_k, k_a, r_k,
                                        group_norm_weight, group_norm_bias, *, eps: float, out, state_out=None,
-                                       v_first=None, v_mode: int = 0):
+                                       v_first=None, v_mode: int = 0, down_sums=None):
     """``fused_wavg_lora`` (rwkv7_hf/fused_lora.py:706) followed by
     ``fused_recurrent_output_prepare_raw`` (fused_recurrent_update.py:1089) in two
     launches: the split-K down projections, then one decode kernel in which each
     (batch, head) workgroup computes its 64 channels of the W/A/G/V up projections
     before the state update.  ``xs``/``downs``/``ups``/``biases`` are in the order
     W, A, G[, V]; activations are the reference's (tanh/none, none/sigmoid,
-    sigmoid/none, none/sigmoid).  Returns ``(out [B, H*N], new_state)``."""
+    sigmoid/none, none/sigmoid).  Returns ``(out [B, H*N], new_state)``.
+
+    ``down_sums`` (fp32, from :func:`native_quant_mm8.mm8_lnmix_multi_into` with
+    ``lora_downs``): the down projections already summed over K; ``xs`` and the
+    down launch are then skipped."""
     k = len(xs)
     rows, D = (int(s) for s in xs[0].shape)
     ranks = [int(d.shape[0]) for d in downs]
@@ -88,15 +92,22 @@ def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, stat
     kk_s, ka, rk, gnw, gnb = (t.reshape(hidden).to(pdt).contiguous()
                               for t in (k_k, k_a, r_k, group_norm_weight, group_norm_bias))
     _lib.require_gpu(r, k_raw, v, *xs, *downs, *ups, state, out, name="fused_wavg_lora_output_prepare_raw")
-    ws = _ws.reserve(xs[0].device, lora_workspace_bytes(ranks, rows, D), slot="lora")
-    s = _lib.stream_of(xs[0])
+    s = _lib.stream_of(r)
     rk_arr = (ctypes.c_int64 * k)(*ranks)
-    _lib.call("rwkv7mi_lora_down_multi", k, _lib.ptr_array(xs), _lib.ptr_array(downs), rk_arr,
-              (ctypes.c_int * k)(*acts_down), rows, D, _lib.dtype_code(xs[0]), _lib.ptr(ws), int(ws.numel()), s)
+    if down_sums is not None:
+        if (down_sums.dtype != torch.float32 or not down_sums.is_contiguous()
+                or int(down_sums.numel()) < rows * sum(ranks)):
+            raise ValueError("fused LoRA decode: down_sums must be contiguous fp32 with rows * sum(ranks) values")
+        ws, splits = down_sums, 1
+    else:
+        ws = _ws.reserve(xs[0].device, lora_workspace_bytes(ranks, rows, D), slot="lora")
+        splits = 0
+        _lib.call("rwkv7mi_lora_down_multi", k, _lib.ptr_array(xs), _lib.ptr_array(downs), rk_arr,
+                  (ctypes.c_int * k)(*acts_down), rows, D, _lib.dtype_code(xs[0]), _lib.ptr(ws), int(ws.numel()), s)
     new_state = state if state_out is None else state_out
     _lib.call("rwkv7mi_wkv7_decode_lora_output_prepare",
               _lib.ptr(r), _lib.ptr(k_raw), _lib.ptr(v), _lib.ptr(ws), k, rk_arr, _lib.ptr_array(ups),
-              _lib.ptr_array(biases), (ctypes.c_int * k)(*acts_down), (ctypes.c_int * k)(*acts_up), D,
+              _lib.ptr_array(biases), (ctypes.c_int * k)(*acts_down), (ctypes.c_int * k)(*acts_up), D, splits,
               _lib.ptr(state), _lib.ptr(new_state), _lib.ptr(kk_s), _lib.ptr(ka), _lib.ptr(rk), _lib.ptr(gnw),
               _lib.ptr(gnb), _lib.ptr(out), _lib.ptr(v_first), int(v_mode), B, H, N, float(eps),
               _lib.dtype_code(r), _lib.dtype_code(kk_s), s)

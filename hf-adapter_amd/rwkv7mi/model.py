@@ -450,6 +450,8 @@ class NativeRWKV7ForCausalLM:
             # this step's LayerNorm rows (the next token's shift inputs) on the fused-mix route
             "hatt": torch.empty(cfg.num_hidden_layers, B, D, device=dev, dtype=dt),
             "hffn": torch.empty(cfg.num_hidden_layers, B, D, device=dev, dtype=dt),
+            # the decode LoRA's down projections summed over K (fused-mix route)
+            "ldown": torch.empty(B * sum(ranks), device=dev, dtype=torch.float32),
         }
 
     def _mix_fusable(self, B) -> bool:
@@ -496,9 +498,13 @@ class NativeRWKV7ForCausalLM:
                 if L.pre is not None:
                     layer_norm(x, L.pre[0], L.pre[1], eps, out=x)
                 aux = [L.mix[1], L.mix[4], L.mix[5], L.mix[3]][:n]
+                flora = self.fused_lora_decode and fused_lora_decode_supported(
+                    [int(d.shape[0]) for d in L.lora_down], B)
                 mm8_lnmix_multi_into(x, xpa[i], L.ln1[0], L.ln1[1], eps, [L.mix[0], L.mix[2], L.mix[3]],
                                      [L.r_proj.m, L.k_proj.m, L.v_proj.m], [rkv[0], rkv[1], rkv[2]],
-                                     h_out=bufs["hatt"][i], aux_mixes=aux, aux_outs=[xw, xa, xg, xv][:n])
+                                     h_out=bufs["hatt"][i], aux_mixes=aux, aux_outs=[xw, xa, xg, xv][:n],
+                                     lora_downs=L.lora_down if flora else None,
+                                     lora_out=bufs["ldown"] if flora else None)
             else:
                 fused_attn_norm_mix6_decode(x, xpa[i], L.ln1[0], L.ln1[1], *L.mix, eps=eps, out=mixb,
                                             pre_norm_weight=L.pre[0] if L.pre else None,
@@ -511,7 +517,7 @@ class NativeRWKV7ForCausalLM:
                 fused_wavg_lora_output_prepare_raw(
                     rkv[0], rkv[1], rkv[2], [xw, xa, xg, xv][:n], L.lora_down, L.lora_up, L.lora_bias, state[i],
                     L.k_k, L.k_a, L.r_k, L.gn[0], L.gn[1], eps=N * 1e-5, out=prep, state_out=state[i],
-                    v_first=v_first, v_mode=1 if i == 0 else 2)
+                    v_first=v_first, v_mode=1 if i == 0 else 2, down_sums=bufs["ldown"] if fmix else None)
             else:
                 if self.lora_side_stream:
                     # the LoRA projections depend only on the mixes: a second stream

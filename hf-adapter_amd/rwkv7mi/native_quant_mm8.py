@@ -207,7 +207,7 @@ def mm8_matmul_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
 
 
 def mm8_lnmix_multi_into(x, prev, ln_w, ln_b, eps: float, mixes, mods, outs, *, epilogues=None, h_out=None,
-                         aux_mixes=(), aux_outs=()):
+                         aux_mixes=(), aux_outs=(), lora_downs=None, lora_out=None):
     """Decode form of ``fused_attn_norm_mix6_decode`` / ``fused_ffn_add_norm_mix_decode``
     (rwkv7_hf/fused_decode_norm_mix.py:161, 296) followed by up to four out-major
     ``MM8Linear`` products, in one launch: ``h = LayerNorm(x)``,
@@ -217,6 +217,12 @@ def mm8_lnmix_multi_into(x, prev, ln_w, ln_b, eps: float, mixes, mods, outs, *, 
     ``aux_outs[a] = h + (prev - h) * aux_mixes[a]`` for other consumers.
     fp16 / bf16 only; rows <= 2 at in_features 4096 (the rows must fit one staging batch, which
     the row statistics are taken from; the library rejects larger calls).
+
+    ``lora_downs`` (one ``[rank, in]`` weight per extra mix) adds the decode LoRA's
+    down projections of the extra mixes (the first half of ``fused_wavg_lora``,
+    rwkv7_hf/fused_lora.py:706), summed over K in fp32 into ``lora_out``
+    (``rows * sum(ranks)`` values, problem-major), for
+    :func:`fused_lora.fused_wavg_lora_output_prepare_raw`'s ``down_sums``.
     """
     k = len(mods)
     if not 1 <= k <= 4 or len(mixes) != k or len(outs) != k:
@@ -249,12 +255,24 @@ def mm8_lnmix_multi_into(x, prev, ln_w, ln_b, eps: float, mixes, mods, outs, *, 
     _lib.require_gpu(x, prev, *outs, name="mm8_lnmix_multi")
     arr = lambda ts: _lib.ptr_array(ts)
     na = len(aux_mixes)
+    lw = lr = None
+    if lora_downs is not None:
+        if len(lora_downs) != na or lora_out is None:
+            raise ValueError("mm8_lnmix_multi_into: one LoRA down weight per extra mix, and lora_out")
+        for d in lora_downs:
+            if d.dim() != 2 or int(d.shape[1]) != n or d.dtype != dt or not d.is_contiguous():
+                raise ValueError("mm8_lnmix_multi_into: LoRA down weights are contiguous [rank, in] in x's dtype")
+        ranks = [int(d.shape[0]) for d in lora_downs]
+        if lora_out.dtype != torch.float32 or not lora_out.is_contiguous() or int(lora_out.numel()) < rows * sum(ranks):
+            raise ValueError("mm8_lnmix_multi_into: lora_out must be contiguous fp32 with rows * sum(ranks) values")
+        lw, lr = arr(list(lora_downs)), (ctypes.c_int64 * na)(*ranks)
     _lib.call(
         "rwkv7mi_mm8t_lnmix_multi", k, _lib.ptr(x), _lib.ptr(prev), _lib.ptr(vecs[0]), _lib.ptr(vecs[1]),
         float(eps), arr(vecs[2:2 + k]), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
         arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]), arr(outs),
         (ctypes.c_int * k)(*[int(e) for e in epilogues]), _lib.ptr(h_out), na, arr(vecs[2 + k:]), arr(list(aux_outs)),
-        rows, n, m, _lib.dtype_code(x), _lib.stream_of(x),
+        lw, lr, _lib.ptr(lora_out if lora_downs is not None else None), rows, n, m, _lib.dtype_code(x),
+        _lib.stream_of(x),
     )
     return outs
 

@@ -109,12 +109,15 @@ int rwkv7mi_wkv7_decode_output_prepare_raw(
  * 2 sigmoid.  Each (batch, head) workgroup computes its own 64 channels of
  * every up projection, rounded to act_dtype as the reference's tensors are.
  * B <= 32; ranks multiples of 8, at most 128; nprob 3 or 4 (4 when
- * v_mode == 2). */
+ * v_mode == 2).  lora_splits: the number of K ranges in lora_part (0: the
+ * split rwkv7mi_lora_down_multi uses for these ranks and D; 1: the whole-K
+ * sums of rwkv7mi_mm8t_lnmix_multi). */
 int rwkv7mi_wkv7_decode_lora_output_prepare(
     const void* r, const void* k_raw, const void* v, const float* lora_part,
     int64_t nprob, const int64_t* ranks, const void* const* w_up,
     const void* const* b_up, const int* act_down, const int* act_up, int64_t D,
-    const float* state_in, float* state_out, const void* k_k, const void* k_a,
+    int64_t lora_splits, const float* state_in, float* state_out, const void* k_k,
+    const void* k_a,
     const void* r_k, const void* gn_w, const void* gn_b, void* out, void* v_first,
     int v_mode, int64_t B, int64_t H, int64_t N, float eps, int act_dtype,
     int param_dtype, void* stream);
@@ -237,7 +240,12 @@ int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x,
  * feeding MM8Linear (native_quant_mm8.py:564-628).  All activation-side
  * tensors and the MM8 metadata in act_dtype (fp16 or bf16); rows <= 2 at
  * I = 4096 (the rows must fit one x' staging batch).  Outputs must not alias
- * x or prev. */
+ * x or prev.  With lora_w (NULL for none; rows <= 2), also the first half of
+ * fused_wavg_lora (rwkv7_hf/fused_lora.py:706) on the extra mixes:
+ * lora_out[off_a + row*rank_a + j] = aux_out[a][row] . lora_w[a][j] in fp32
+ * (lora_w[a] [rank_a, I] in act_dtype, off_a = rows * sum of the earlier
+ * ranks) — the one-split layout rwkv7mi_wkv7_decode_lora_output_prepare
+ * reads with lora_splits = 1. */
 int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* prev,
                              const void* ln_w, const void* ln_b, float eps,
                              const void* const* mix, const uint8_t* const* w_blk,
@@ -245,8 +253,9 @@ int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* prev,
                              const void* const* my, const void* const* ry,
                              void* const* y, const int* epilogue, void* h_out,
                              int naux, const void* const* aux_mix, void* const* aux_out,
-                             int64_t rows, int64_t I, int64_t O, int act_dtype,
-                             void* stream);
+                             const void* const* lora_w, const int64_t* lora_ranks,
+                             float* lora_out, int64_t rows, int64_t I, int64_t O,
+                             int act_dtype, void* stream);
 
 /* dequantize_mm8 (rwkv7_hf/native_quant_mm8.py:100-108) from w_blk into out
  * [O,I] (Linear.weight layout) for a library GEMM on long prefills.

@@ -264,8 +264,13 @@ def test_mm8t_lnmix_matches_oracle_and_unfused(oracle, dtype, case):
     aux = [torch.full((rows, I), float("nan"), device="cuda", dtype=dtype) for _ in range(na)]
     prev0 = prev.clone()
     epis = [_lib.EPI_RELU2 if epi else _lib.EPI_NONE] * k
+    # the decode LoRA's down projections of the extra mixes (rows <= 2)
+    ranks = [64, 64, 128, 32][:na] if rows <= 2 else []
+    downs = [_cuda(rng.standard_normal((rr, I)) * 0.05, dtype) for rr in ranks]
+    lora_out = torch.full((rows * sum(ranks) + 7,), float("nan"), device="cuda", dtype=torch.float32)
     mm8_lnmix_multi_into(x, prev, lnw, lnb, 1e-5, mixes[:k], mods, outs, epilogues=epis, h_out=h_out,
-                         aux_mixes=mixes[k:], aux_outs=aux)
+                         aux_mixes=mixes[k:], aux_outs=aux, lora_downs=downs if ranks else None,
+                         lora_out=lora_out if ranks else None)
     again = [torch.empty_like(o) for o in outs]
     mm8_lnmix_multi_into(x, prev, lnw, lnb, 1e-5, mixes[:k], mods, again, epilogues=epis)
     torch.cuda.synchronize()
@@ -282,6 +287,15 @@ def test_mm8t_lnmix_matches_oracle_and_unfused(oracle, dtype, case):
     assert np.abs(f(h_out) - h_r).max() <= tol_h * max(np.abs(h_r).max(), 1.0)
     for a in range(na):
         assert np.abs(f(aux[a]) - mixed[k + a]).max() <= tol_h * max(np.abs(mixed[k + a]).max(), 1.0)
+    # LoRA down sums: [problem][row][j], fp32 over the mixes as written (rounded)
+    off = 0
+    for a, rr in enumerate(ranks):
+        got = _np(lora_out[off:off + rows * rr]).reshape(rows, rr).astype(np.float64)
+        ref = f(aux[a]) @ f(downs[a]).T
+        assert np.abs(got - ref).max() <= 1e-4 * max(np.abs(ref).max(), 1.0), (a, np.abs(got - ref).max())
+        off += rows * rr
+    if ranks:
+        assert torch.isnan(lora_out[off:]).all(), "nothing past the sums is written"
     for p in range(k):
         packed = [_np(b.float()) if b.is_floating_point() else _np(b)
                   for b in (mods[p].w_u8, mods[p].mx, mods[p].rx, mods[p].my, mods[p].ry)]

@@ -207,6 +207,17 @@ def test_decode_fused_lora(oracle, dt, B, v_mode, nl, ranks):
     assert np.abs(_f64(out) - _f64(out2).reshape(B, A)).max() <= tol * max(1.0, np.abs(ref).max() / 4)
     if v_mode == 1:
         assert torch.equal(vf, v)
+    # whole-K down sums handed in (the layout the LN-mix GEMV prologue writes)
+    sums = torch.cat([(xs[q].double() @ downs[q].double().T).float().reshape(-1) for q in range(nl)])
+    out3 = torch.empty_like(out)
+    st3 = _t(state, torch.float32)
+    vf3 = _t(v_first0, dt)
+    fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, st3, k_k, k_a, r_k, gn_w, gn_b,
+                                       eps=eps, out=out3, v_first=vf3 if v_mode else None, v_mode=v_mode,
+                                       down_sums=sums.contiguous())
+    torch.cuda.synchronize()
+    assert np.abs(_f64(st3) - ref_s).max() <= 1e-3 * ssc
+    assert np.abs(_f64(out3).reshape(B, H, N) - ref).max() <= tol * max(1.0, np.abs(ref).max() / 4)
 
 
 def test_decode_fused_lora_rejects_unsupported():
