@@ -44,17 +44,32 @@ template <typename T>
 __device__ __forceinline__ float ld(const T* p, int64_t i) { return to_f32(p[i]); }
 
 // -------------------------------------------------------- wave reductions
+// (the wave must be fully active: DPP and readlane read every lane)
+template <int CTRL>
+__device__ __forceinline__ float dpp_quad(float x) {  // quad_perm: lane i of each quad gets lane sel_i
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+// The wave's total, the same in every lane: DPP rotations inside the 16-lane
+// rows, then the four row totals read out in a fixed order (no LDS round trips).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_row_ror<8>(v);
+  v += dpp_row_ror<4>(v);
+  v += dpp_row_ror<2>(v);
+  v += dpp_row_ror<1>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
-// Sum over aligned groups of G consecutive lanes (G power of two <= 64).
+// Sum over aligned groups of G consecutive lanes (G power of two <= 64); every
+// lane of a group gets the same bits (pairwise butterfly).
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G >= 2) v += dpp_quad<0xB1>(v);  // lane i ^ 1
+  if constexpr (G >= 4) v += dpp_quad<0x4E>(v);  // lane i ^ 2
 #pragma unroll
-  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  for (int o = G / 2; o >= 4; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
 
@@ -131,6 +146,18 @@ __device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off
 
 __device__ __forceinline__ float buf_ldf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+// one T element at index e (zero when !valid or past the descriptor) -> fp32
+template <typename T>
+__device__ __forceinline__ float buf_ld1(__amdgpu_buffer_rsrc_t r, uint32_t e, bool valid) {
+  const int off = (int)(valid ? e * (uint32_t)sizeof(T) : BUF_OOB);
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  } else {
+    const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    return to_f32(__builtin_bit_cast(T, u));
+  }
 }
 
 // 8 consecutive T elements from element index e (zeros when !valid) -> fp32

@@ -391,8 +391,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
       v += __shfl_xor(v, 16, 64);
       return __shfl(v, lane & ~31, 64);
     }
-    auto lane_v = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
-    v = (lane_v(v, 0) + lane_v(v, 16)) + (lane_v(v, 32) + lane_v(v, 48));
+    v = (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
     if (TPR == 64) return v;
     if (lane == 0) wpart[pass][wave] = v;
     __syncthreads();
@@ -473,8 +472,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
         v += dpp_row_ror<4>(v);
         v += dpp_row_ror<2>(v);
         v += dpp_row_ror<1>(v);
-        auto lane_v = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
-        v = (lane_v(v, 0) + lane_v(v, 16)) + (lane_v(v, 32) + lane_v(v, 48));
+        v = (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
         if (rr < nrows && lane == 0) B.pro.lout[B.pro.loff[qa] + (int64_t)(row0 + rr) * B.pro.lrank[qa] + j] = v;
       }
     }

@@ -79,7 +79,8 @@ template <typename TA>
 __device__ __forceinline__ void stage_raw(int c, float rv, float wr, float kraw, float vv, float av, float kkw,
                                           float kaw, float rkw, int v_mode, TA* v_first, float vgate,
                                           int64_t vec, float* s_r, float* s_w, float* s_k, float* s_kk,
-                                          float* s_ka, float* s_v, float* s_corr) {
+                                          float* s_ka, float* s_v, float* s_corr, bool vf_given = false,
+                                          float vf_in = 0.f) {
   float kku = kraw * kkw;
   float nrm = sqrtf(wave_sum(kku * kku));
   const float kkv = kku / fmaxf(nrm, 1.0e-12f);
@@ -88,7 +89,7 @@ __device__ __forceinline__ void stage_raw(int c, float rv, float wr, float kraw,
   if (v_mode == 1) {
     v_first[vec + c] = from_f32<TA>(vv);
   } else if (v_mode == 2) {
-    float vf = to_f32(v_first[vec + c]);
+    const float vf = vf_given ? vf_in : to_f32(v_first[vec + c]);
     vv = vv + (vf - vv) * vgate;
   }
   s_r[c] = rv;
@@ -247,6 +248,14 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
 
   const bool active = wave < LA.nprob;  // wave-uniform
   const int rp = active ? LA.rank[wave] : 0;
+  // v_first (v_mode 2) and this wave's up-projection bias, issued with the rest
+  // rather than where they are used (each would add a memory round trip there)
+  const float vf_pre = buf_ld1<TA>(make_rsrc(v_first ? v_first + vec : nullptr, v_first ? HEAD * (uint32_t)sizeof(TA) : 0u),
+                                   (uint32_t)lane, v_mode == 2);
+  const void* bu_w = active ? LA.bu[wave] : nullptr;
+  const float bias_pre = buf_ld1<TA>(
+      make_rsrc(bu_w ? reinterpret_cast<const TA*>(bu_w) + (int64_t)h * HEAD : nullptr, bu_w ? HEAD * (uint32_t)sizeof(TA) : 0u),
+      (uint32_t)lane, bu_w != nullptr);
   // up-projection row h*64 + lane of Wu_p: rank elements in 8-element chunks
   float wrow[DL_MAXR];
   {
@@ -300,15 +309,14 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
         acc += m4.x * wrow[e] + m4.y * wrow[e + 1] + m4.z * wrow[e + 2] + m4.w * wrow[e + 3];
       }
     }
-    const TA* bias = reinterpret_cast<const TA*>(LA.bu[wave]);
-    if (bias) acc += to_f32(bias[(int64_t)h * HEAD + lane]);
+    if (bu_w) acc += bias_pre;
     s_lo[wave][lane] = to_f32(from_f32<TA>(dl_act(acc, LA.act_u[wave])));
   }
   __syncthreads();
 
   if (tid < HEAD)
     stage_raw<TA>(tid, rv, s_lo[0][tid], kraw, vv, s_lo[1][tid], kkw, kaw, rkw, v_mode, v_first,
-                  v_mode == 2 ? s_lo[3][tid] : 0.f, vec, s_r, s_w, s_k, s_kk, s_ka, s_v, &s_corr);
+                  v_mode == 2 ? s_lo[3][tid] : 0.f, vec, s_r, s_w, s_k, s_kk, s_ka, s_v, &s_corr, true, vf_pre);
   __syncthreads();
   decode_core<true, TA>(s, s_r, s_w, s_k, s_kk, s_ka, s_v, s_corr, s_red, s_lo[2][i], gnw_i, gnb_i, eps,
                         state_out, soff, out, vec);
