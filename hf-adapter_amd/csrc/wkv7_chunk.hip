@@ -135,16 +135,8 @@ __device__ __forceinline__ float row_scan(float x) {  // inclusive prefix sum ov
   x += row_shr<8>(x);
   return x;
 }
-template <int N>
-__device__ __forceinline__ float row_ror(float x) {  // the row rotated by N lanes
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float row_sum(float x) {  // the row's total in every lane
-  x += row_ror<8>(x);
-  x += row_ror<4>(x);
-  x += row_ror<2>(x);
-  x += row_ror<1>(x);
-  return x;
+__device__ __forceinline__ float row_last(float x) {  // lane 15 of the row in every lane (DPP row_newbcast)
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x15F, 0xF, 0xF, false));
 }
 
 // ---- LDS flags (workgroup scope)
@@ -339,13 +331,16 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
     // A-matrix products, and the transposed operands (identity MFMAs:
     // D(x) tile jt = lane (sigma = 16jt + l16, t = 4kg + e))
     f32x4 AqbA = ZERO4, AqkA = ZERO4, AakD = ZERO4, AabA = ZERO4;
+    // the chunk's total log-decay and centre of one channel per lane: lane
+    // (l16, kg) keeps those of channel slot (jt, e) = (l16 / 4, l16 % 4)
+    float myGC = 0.f, myCF = 0.f;
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
       bf16x4 rcH[2], rcL[2], kcH[2], kcL[2], acH[2], acL[2], bcH[2], bcL[2];
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         const int jt = 2 * cc + jj;
-        f32x4 rc, kc, ac, bc, xv, ecv, pcv, cenv;
+        f32x4 rc, kc, ac, bc, xv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           // inputs of token t, channel slot (jt, e), read from the raw rows here
@@ -356,7 +351,7 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
           const float l2 = WLOG ? wv * 1.4426950408889634f : __builtin_amdgcn_logf(wv);
           const float lwv = ok ? fmaxf(l2, -126.f) : 0.f;
           const float g = row_scan(lwv);
-          const float gC = row_sum(lwv);
+          const float gC = row_last(g);  // the scan's last token: the chunk total
           const float cf = rintf(0.5f * gC);
           const int ci = (int)cf;
           const float xd = clamp126(g - cf);
@@ -364,14 +359,14 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
           const float qv = __builtin_amdgcn_exp2f(-xd);
           const float sh = row_shr<1>(pv);
           const float pp = t == 0 ? __builtin_amdgcn_ldexpf(1.f, -ci) : sh;  // 2^{g_{t-1} - c}, g_{-1} = 0
-          const float pC = __builtin_amdgcn_exp2f(clamp126(gC - cf));
           rc[e] = xr * pv;
           kc[e] = xk * qv;
           ac[e] = -xkk * pp;
           bc[e] = xkk * xa * qv;
-          ecv[e] = __builtin_amdgcn_ldexpf(pC, ci);
-          pcv[e] = pC;
-          cenv[e] = __builtin_amdgcn_ldexpf(1.f, ci);
+          if (l16 == 4 * jt + e) {
+            myGC = gC;
+            myCF = cf;
+          }
         }
         split_f4(rc, rcH[jj], rcL[jj]);
         split_f4(kc, kcH[jj], kcL[jj]);
@@ -387,11 +382,6 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
         Z.vt[0][jt][lane] = pack_exact(mma16(hi, Ib, ZERO4));
         Z.vt[1][jt][lane] = pack_exact(mma16(lo, Ib, ZERO4));
         *reinterpret_cast<f32x4*>(&Z.rq[jj][cc][lane]) = rc;  // rc, until Rq
-        if (t == 0) {
-          Z.ec[jt][kg] = ecv;
-          Z.pc[jt][kg] = pcv;
-          Z.cen[jt][kg] = cenv;
-        }
       }
       const bf16x8 rH = cat(rcH[0], rcH[1]), rL = cat(rcL[0], rcL[1]);
       const bf16x8 kH = cat(kcH[0], kcH[1]), kL = cat(kcL[0], kcL[1]);
@@ -410,6 +400,15 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
       AqkA = mfma16x16x32(kL, rH, AqkA);
       AakD = mfma16x16x32(aL, kH, AakD);
       AabA = mfma16x16x32(bL, aH, AabA);
+    }
+    {
+      // per channel (one per lane): 2^gC, 2^{gC - c}, 2^c for the chain's state update
+      const int ci = (int)myCF;
+      const float pC = __builtin_amdgcn_exp2f(clamp126(myGC - myCF));
+      const int jt = l16 >> 2, e = l16 & 3;
+      reinterpret_cast<float*>(&Z.ec[jt][kg])[e] = __builtin_amdgcn_ldexpf(pC, ci);
+      reinterpret_cast<float*>(&Z.pc[jt][kg])[e] = pC;
+      reinterpret_cast<float*>(&Z.cen[jt][kg])[e] = __builtin_amdgcn_ldexpf(1.f, ci);
     }
     if (x + 4 < nchunks) issue(x + 4);  // the raw rows are consumed; the next ones land meanwhile
 #pragma unroll
