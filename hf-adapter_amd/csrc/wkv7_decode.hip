@@ -228,9 +228,26 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
   const int j0 = (tid & 3) * 16;
   const int64_t soff = ((int64_t)bh * HEAD + i) * HEAD + j0;
 
+  const bool active = wave < LA.nprob;  // wave-uniform
+  const int rp = active ? LA.rank[wave] : 0;
+  // the LoRA down partials first: the up projections wait on them, the state
+  // only at the update (loads complete in issue order)
+  float pt0[2][DL_ZB];
+  {
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(LA.part, (uint32_t)LA.part_total * 4u);
+    const uint32_t zs = (uint32_t)(LA.rows * rp);
+    const uint32_t base = (uint32_t)((active ? LA.part_off[wave] : 0) + (int64_t)b * rp);
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int zz = 0; zz < DL_ZB; ++zz) {
+        const bool ok = lane + 64 * u < rp && zz < LA.ks;
+        pt0[u][zz] = buf_ldf(pr, ok ? (base + (uint32_t)zz * zs + lane + 64u * u) * 4u : BUF_OOB);
+      }
+  }
   // state rows, per-row output parameters and channel `lane` of this head's
   // vectors (every wave loads them; only the first uses them) — no branches,
-  // so all of these loads are in flight together with the LoRA loads below
+  // so all of these loads are in flight together with the LoRA loads
   float s[16];
   {
     const float4* src = reinterpret_cast<const float4*>(state_in + soff);
@@ -246,8 +263,6 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
   const float rv = ld(r, vec + lane), kraw = ld(k, vec + lane), vv = ld(v, vec + lane);
   const float kkw = ld(k_k, pc), kaw = ld(k_a, pc), rkw = ld(r_k, pc);
 
-  const bool active = wave < LA.nprob;  // wave-uniform
-  const int rp = active ? LA.rank[wave] : 0;
   // v_first (v_mode 2) and this wave's up-projection bias, issued with the rest
   // rather than where they are used (each would add a memory round trip there)
   const float vf_pre = buf_ld1<TA>(make_rsrc(v_first ? v_first + vec : nullptr, v_first ? HEAD * (uint32_t)sizeof(TA) : 0u),
@@ -270,14 +285,18 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
       for (int u = 0; u < 8; ++u) wrow[e + u] = f[u];
     }
   }
-  // mid_p[kk] for kk = lane, lane + 64: all K-split partials of this batch row,
-  // loaded at once (an out-of-range offset reads zero), summed in z order
+  // mid_p[kk] for kk = lane, lane + 64: the rest of the K-split partials (the
+  // first DL_ZB splits are in flight since the kernel's start), summed in z order
   {
     const __amdgpu_buffer_rsrc_t pr = make_rsrc(LA.part, (uint32_t)LA.part_total * 4u);
     const uint32_t zs = (uint32_t)(LA.rows * rp);
     const uint32_t base = (uint32_t)((active ? LA.part_off[wave] : 0) + (int64_t)b * rp);
     float acc[2] = {0.f, 0.f};
-    for (int z0 = 0; z0 < LA.ks; z0 += DL_ZB) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int zz = 0; zz < DL_ZB; ++zz) acc[u] += pt0[u][zz];  // past-the-end terms are +0
+    for (int z0 = DL_ZB; z0 < LA.ks; z0 += DL_ZB) {
       float t[2][DL_ZB];
 #pragma unroll
       for (int u = 0; u < 2; ++u)
@@ -289,14 +308,14 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int zz = 0; zz < DL_ZB; ++zz) acc[u] += t[u][zz];  // past-the-end terms are +0
+        for (int zz = 0; zz < DL_ZB; ++zz) acc[u] += t[u][zz];
     }
-    if (active) {
-      const int ad = LA.act_d[wave];
+    // every entry of the wave's row is written (zeros past the rank), so the
+    // up-projection dot below runs unconditionally over DL_MAXR
+    const int ad = active ? LA.act_d[wave] : 0;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-        if (lane + 64 * u < rp) s_mid[wave][lane + 64 * u] = to_f32(from_f32<TA>(dl_act(acc[u], ad)));
-    }
+    for (int u = 0; u < 2; ++u)
+      s_mid[wave][lane + 64 * u] = lane + 64 * u < rp ? to_f32(from_f32<TA>(dl_act(acc[u], ad))) : 0.f;
   }
   // this wave's problem, channel `lane` (the wave reads its own s_mid row: LDS
   // operations of one wave complete in order, so no barrier is needed)
@@ -304,10 +323,8 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
     float acc = 0.f;
 #pragma unroll
     for (int e = 0; e < DL_MAXR; e += 4) {
-      if (e < rp) {
-        const float4 m4 = *reinterpret_cast<const float4*>(&s_mid[wave][e]);  // broadcast
-        acc += m4.x * wrow[e] + m4.y * wrow[e + 1] + m4.z * wrow[e + 2] + m4.w * wrow[e + 3];
-      }
+      const float4 m4 = *reinterpret_cast<const float4*>(&s_mid[wave][e]);  // broadcast
+      acc += m4.x * wrow[e] + m4.y * wrow[e + 1] + m4.z * wrow[e + 2] + m4.w * wrow[e + 3];
     }
     if (bu_w) acc += bias_pre;
     s_lo[wave][lane] = to_f32(from_f32<TA>(dl_act(acc, LA.act_u[wave])));
