@@ -204,6 +204,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   _Float16* xl = xh + nrows * XS;
   __shared__ float red[NW][16][17];
   __shared__ float wsum[NW][2];
+  __shared__ float wsum2[NW][2][2];  // per-wave staging: [wave][row][sum x, sum x my]
   __shared__ float rsum[16][2];
   __shared__ float wpart[PRO ? 2 : 1][PRO ? NW : 1];  // LN-mix prologue: per-wave partial sums
 
@@ -482,6 +483,66 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   __amdgpu_buffer_rsrc_t wr = group_rsrc(g);             // this group
   __amdgpu_buffer_rsrc_t wn = group_rsrc(g + gstride);   // the next one
 
+  // Per-wave staging (8-bit fp16 / bf16, one K chunk, at most two rows, no
+  // LN-mix prologue): wave w consumes only the K blocks w + NW j, so it stages
+  // just those (its own x' in LDS, its share of the row sums) and no workgroup
+  // barrier stands between a wave's loads and its first product.  (With the
+  // prologue every wave would need the whole row for the LN statistics; that
+  // measured slower than the shared staging.)
+  constexpr bool WSOK = BITS == 8 && sizeof(TA) == 2 && !PRO;
+  const bool ws = WSOK && nrows <= 2 && nchunks == 1;
+  float sxw[2] = {0.f, 0.f}, smw[2] = {0.f, 0.f};
+  if (ws) {
+    constexpr int NRND = (CSW + 3) / 4;  // 64 lanes cover four 128-input blocks per round
+    Raw8<TA> wx[NRND][2];
+    Raw8<TM> wry[NRND], wmy[NRND];
+#pragma unroll
+    for (int r = 0; r < NRND; ++r) {
+      const int j = 4 * r + (lane >> 4);
+      const int k = 128 * (wave + NW * j) + 8 * (lane & 15);
+      const bool valid = j < CSW && k < I;
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) wx[r][rr] = mm8t_ld8<TA>(xr, (uint32_t)(rr * I + k), valid && rr < nrows);
+      wry[r] = mm8t_ld8<TM>(ryr, (uint32_t)k, valid);
+      wmy[r] = mm8t_ld8<TM>(myr, (uint32_t)k, valid);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_step(wr, 0, buf[0]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < NRND; ++r) {
+      const int j = 4 * r + (lane >> 4);
+      const int k = 128 * (wave + NW * j) + 8 * (lane & 15);
+      float rv[8], mv[8];
+      mm8t_cvt8(wry[r], rv);
+      mm8t_cvt8(wmy[r], mv);
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        if (rr < nrows) {
+          float xv[8];
+          mm8t_cvt8(wx[r][rr], xv);  // blocks past I load as zeros
+          f16x8 hi, lo;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float xp = xv[e] * rv[e];
+            const _Float16 h = (_Float16)xp;
+            hi[e] = h;
+            lo[e] = (_Float16)(xp - (float)h);
+            sxw[rr] += xv[e];
+            smw[rr] += xv[e] * mv[e];
+          }
+          if (j < CSW) {
+            *reinterpret_cast<f16x8*>(xh + rr * XS + k) = hi;
+            *reinterpret_cast<f16x8*>(xl + rr * XS + k) = lo;
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 1; d < DEPTH; ++d) load_step(wr, d, buf[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
   // chunk 0: the first staging batch goes out first, then ONE ring step, and the
   // rest of the ring only once x' is staged.  Every workgroup reads the same
   // x / ry / my lines; issued behind the whole grid's ring fill they would
@@ -508,6 +569,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
     stage_finish(it0);
   }
   __syncthreads();
+  }
 
   const int arow = n < nrows ? n : nrows - 1;
   // lane kg's 16-byte runs hold rows 16kg.. (8-bit) or 32kg.. (4-bit) of each half step
@@ -579,7 +641,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
     }
     const f32x4 accs = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 
-    if (first) {
+    if (first && ws) {
+      // ---- per-row sums of the per-wave staging: each wave's total, then the
+      // waves in order
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const float a = wave_sum(sxw[rr]), b = wave_sum(smw[rr]);
+        if (lane == 0) {
+          wsum2[wave][rr][0] = a;
+          wsum2[wave][rr][1] = b;
+        }
+      }
+      __syncthreads();
+      if (tid < nrows) {
+        float a = 0.f, b = 0.f;
+        for (int q = 0; q < NW; ++q) {
+          a += wsum2[q][tid][0];
+          b += wsum2[q][tid][1];
+        }
+        rsum[tid][0] = a;
+        rsum[tid][1] = b;
+      }
+    } else if (first) {
       // ---- per-row sums (staging is complete): fixed-order butterfly inside
       // each row's lanes, then across waves
       const int width = TPR < 64 ? TPR : 64;
