@@ -62,8 +62,7 @@ struct ChunkSlot {
   bf16x4 vt[2][4][64];  // [hi/lo][value tile] B(V)
   bf16x4 am[2][64];     // [hi/lo] A(M)
   bf16x4 aq[2][64];     // [hi/lo] A(Qm)
-  f32x4 ec[4][4];       // [jt][kg] 2^gC of channels 16jt + 4kg + e
-  f32x4 pc[4][4];       // [jt][kg] 2^{gC - c}
+  f32x4 pc[4][4];       // [jt][kg] 2^{gC - c} of channels 16jt + 4kg + e
   f32x4 cen[4][4];      // [jt][kg] 2^c
 };
 
@@ -103,24 +102,13 @@ __device__ __forceinline__ f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
 }
 constexpr f32x4 ZERO4 = {0.f, 0.f, 0.f, 0.f};
 
-// bf16x3 products with the three terms in independent accumulators
-struct Acc3 {
-  f32x4 hh = ZERO4, hl = ZERO4, lh = ZERO4;
-  __device__ __forceinline__ void add32(bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl) {
-    hh = mfma16x16x32(ah, bh, hh);
-    hl = mfma16x16x32(ah, bl, hl);
-    lh = mfma16x16x32(al, bh, lh);
-  }
-  __device__ __forceinline__ void add16(bf16x4 ah, bf16x4 al, bf16x4 bh, bf16x4 bl) {
-    hh = mma16(ah, bh, hh);
-    hl = mma16(ah, bl, hl);
-    lh = mma16(al, bh, lh);
-  }
-  __device__ __forceinline__ f32x4 sum() const { return hh + (hl + lh); }
-};
-// the same three products in one accumulator (fewer adds, longer chain)
+// bf16x3 products (hi*hi + hi*lo + lo*hi) accumulated onto c in one chain:
+// each MFMA takes the previous one's result (same shape) as its C operand
 __device__ __forceinline__ f32x4 mma3_16(bf16x4 ah, bf16x4 al, bf16x4 bh, bf16x4 bl) {
   return mma16(al, bh, mma16(ah, bl, mma16(ah, bh, ZERO4)));
+}
+__device__ __forceinline__ f32x4 mma3_32(bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl, f32x4 c) {
+  return mfma16x16x32(al, bh, mfma16x16x32(ah, bl, mfma16x16x32(ah, bh, c)));
 }
 
 // ---- cross-lane helpers on 16-lane rows (lane = token within the chunk)
@@ -134,6 +122,10 @@ __device__ __forceinline__ float row_scan(float x) {  // inclusive prefix sum ov
   x += row_shr<4>(x);
   x += row_shr<8>(x);
   return x;
+}
+// lane t gets lane t-1; lane 0 of the row keeps `old` (DPP without bound control)
+__device__ __forceinline__ float row_shr1_or(float x, float old) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), 0x111, 0xF, 0xF, false));
 }
 __device__ __forceinline__ float row_last(float x) {  // lane 15 of the row in every lane (DPP row_newbcast)
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x15F, 0xF, 0xF, false));
@@ -168,6 +160,16 @@ __device__ __forceinline__ void load_row(RawRow<T>& o, __amdgpu_buffer_rsrc_t rs
   }
 }
 // value of slot (jt, e): half jt >> 1, element 4 (jt & 1) + e of that half
+// one element of y; an offset past the descriptor (a token beyond T) is dropped
+template <typename T>
+__device__ __forceinline__ void store_y(__amdgpu_buffer_rsrc_t rs, uint32_t off, float v) {
+  if constexpr (sizeof(T) == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rs, (int)off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, from_f32<T>(v)), rs, (int)off, 0, 0);
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ float row_val(const RawRow<T>& o, int jt, int e) {
   const int h = jt >> 1, idx = 4 * (jt & 1) + e;
@@ -223,7 +225,10 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
         S[jt] = (f32x4){t4.x, t4.y, t4.z, t4.w};
       }
     }
-    TA* ybase = y + ((int64_t)b * T * H + h) * HD + ich;
+    // byte offsets of this lane's y elements (tokens 4kg + e, value row ich) within a chunk
+    uint32_t yoff[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) yoff[e] = (uint32_t)(((4 * kg + e) * tok + ich) * (int64_t)sizeof(TA));
     for (int x = 0; x < nchunks; ++x) {
       const int s = x % NSLOT;
       const ChunkSlot& Z = L.slot[s];
@@ -243,44 +248,50 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
       }
       const bf16x4 vH = Z.vt[0][q][lane], vL = Z.vt[1][q][lane];
       const bf16x4 amH = Z.am[0][lane], amL = Z.am[1][lane], aqH = Z.aq[0][lane], aqL = Z.aq[1][lane];
-      f32x4 ec[4], pc[4], cen[4];
+      f32x4 pc[4], cen[4];
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
-        ec[jt] = Z.ec[jt][kg];
         pc[jt] = Z.pc[jt][kg];
         cen[jt] = Z.cen[jt][kg];
       }
       set_flag(&L.done[q][s], x);  // the operands are in registers
 
+      // S' = S diag(2^c): the bf16x3 operand of U and Y, and the seed of the
+      // update's product chain, so that S <- 2^{gC-c} (S' + Bc^T U + Kc^T V)
+      f32x4 Sp[4];
       bf16x4 SH[4], SL[4];
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) split_f4(S[jt] * cen[jt], SH[jt], SL[jt]);  // S' = S diag(2^c)
-      Acc3 accU, accY;
+      for (int jt = 0; jt < 4; ++jt) {
+        Sp[jt] = S[jt] * cen[jt];
+        split_f4(Sp[jt], SH[jt], SL[jt]);
+      }
+      f32x4 U = ZERO4, Yv = ZERO4;
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
         const bf16x8 sh = cat(SH[2 * cc], SH[2 * cc + 1]), sl = cat(SL[2 * cc], SL[2 * cc + 1]);
-        accU.add32(waH[cc], waL[cc], sh, sl);
-        accY.add32(rqH[cc], rqL[cc], sh, sl);
+        U = mma3_32(waH[cc], waL[cc], sh, sl, U);
+        Yv = mma3_32(rqH[cc], rqL[cc], sh, sl, Yv);
       }
-      accU.add16(amH, amL, vH, vL);  // + M V
-      const f32x4 U = accU.sum();
+      // + M V and, below, + Qm V, on 16x16x32 like the rest of each chain
+      // (A and B pair positionally: [mH | mH] x [vH | vL] gives hi*hi + hi*lo,
+      // [mL | 0] x [vH | 0] gives lo*hi).  A 16x16x16 MFMA that takes a
+      // 16x16x32 result as its C operand straight after it read a stale
+      // accumulator here, so the shapes are not mixed within a chain.
+      const bf16x8 vHL = cat(vH, vL), vH0 = cat(vH, (bf16x4){});
+      U = mfma16x16x32(cat(amH, amH), vHL, U);
+      U = mfma16x16x32(cat(amL, (bf16x4){}), vH0, U);
       bf16x4 UH, UL;
       split_f4(U, UH, UL);
       const bf16x8 uvH = cat(UH, vH), uvL = cat(UL, vL);
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        Acc3 acc;
-        acc.add32(bkH[jt], bkL[jt], uvH, uvL);
-        S[jt] = S[jt] * ec[jt] + pc[jt] * acc.sum();
-      }
-      accY.add16(aqH, aqL, vH, vL);  // + Qm V
-      const f32x4 Yv = accY.sum();
+      for (int jt = 0; jt < 4; ++jt) S[jt] = pc[jt] * mma3_32(bkH[jt], bkL[jt], uvH, uvL, Sp[jt]);
+      Yv = mfma16x16x32(cat(aqH, aqH), vHL, Yv);
+      Yv = mfma16x16x32(cat(aqL, (bf16x4){}), vH0, Yv);
       const int t0 = x * CH;
+      const __amdgpu_buffer_rsrc_t ys =
+          make_rsrc(y + (((int64_t)b * T + t0) * H + h) * HD, (uint32_t)(min(CH, T - t0) * tok * (int64_t)sizeof(TA)));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int tg = t0 + 4 * kg + e;
-        if (tg < T) ybase[(int64_t)tg * tok] = from_f32<TA>(Yv[e]);
-      }
+      for (int e = 0; e < 4; ++e) store_y<TA>(ys, yoff[e], Yv[e]);
     }
     float* dst = state_out + ((int64_t)bh * HD + ich) * HD + 8 * kg;
 #pragma unroll
@@ -319,7 +330,9 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
   if (p < nchunks) issue(p);
 
   for (int x = p; x < nchunks; x += 4) {
-    const bool ok = x * CH + t < T;
+    // A token past T loads w = 0 (log2 -> -inf, or 0 as a log) and must add
+    // nothing to the gate sums: its floor is 0 instead of -126.
+    const float lwlo = x * CH + t < T ? -126.f : 0.f;
     // Wait until the chain waves have taken chunk x - NSLOT out of this slot;
     // every result below is then stored as soon as it exists (D(ac) and rc are
     // parked in the Wa / Rq areas until Wa and Rq replace them).
@@ -331,43 +344,51 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
     // A-matrix products, and the transposed operands (identity MFMAs:
     // D(x) tile jt = lane (sigma = 16jt + l16, t = 4kg + e))
     f32x4 AqbA = ZERO4, AqkA = ZERO4, AakD = ZERO4, AabA = ZERO4;
-    // the chunk's total log-decay and centre of one channel per lane: lane
-    // (l16, kg) keeps those of channel slot (jt, e) = (l16 / 4, l16 % 4)
-    float myGC = 0.f, myCF = 0.f;
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
       bf16x4 rcH[2], rcL[2], kcH[2], kcL[2], acH[2], acL[2], bcH[2], bcL[2];
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         const int jt = 2 * cc + jj;
-        f32x4 rc, kc, ac, bc, xv;
+        // gate prefix sums of the four channels of slot (jt, .), the four
+        // scans stepped together so no DPP read waits on its own producer
+        float g[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float wv = row_val<TW>(rw, jt, e);
+          const float l2 = WLOG ? wv * 1.4426950408889634f : __builtin_amdgcn_logf(wv);
+          g[e] = fmaxf(l2, lwlo);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g[e] += row_shr<1>(g[e]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g[e] += row_shr<2>(g[e]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g[e] += row_shr<4>(g[e]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g[e] += row_shr<8>(g[e]);
+        f32x4 rc, kc, ac, bc, xv, gcv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           // inputs of token t, channel slot (jt, e), read from the raw rows here
           const float xr = row_val<TA>(rr, jt, e), xk = row_val<TA>(rk, jt, e);
           const float xkk = row_val<TA>(rkk, jt, e), xa = row_val<TA>(ra, jt, e);
           xv[e] = row_val<TA>(rv, jt, e);
-          const float wv = row_val<TW>(rw, jt, e);
-          const float l2 = WLOG ? wv * 1.4426950408889634f : __builtin_amdgcn_logf(wv);
-          const float lwv = ok ? fmaxf(l2, -126.f) : 0.f;
-          const float g = row_scan(lwv);
-          const float gC = row_last(g);  // the scan's last token: the chunk total
+          const float gC = row_last(g[e]);  // the scan's last token: the chunk total
+          gcv[e] = gC;
           const float cf = rintf(0.5f * gC);
           const int ci = (int)cf;
-          const float xd = clamp126(g - cf);
+          const float xd = clamp126(g[e] - cf);
           const float pv = __builtin_amdgcn_exp2f(xd);
           const float qv = __builtin_amdgcn_exp2f(-xd);
-          const float sh = row_shr<1>(pv);
-          const float pp = t == 0 ? __builtin_amdgcn_ldexpf(1.f, -ci) : sh;  // 2^{g_{t-1} - c}, g_{-1} = 0
+          const float pp = row_shr1_or(pv, __builtin_amdgcn_ldexpf(1.f, -ci));  // 2^{g_{t-1} - c}, g_{-1} = 0
           rc[e] = xr * pv;
           kc[e] = xk * qv;
           ac[e] = -xkk * pp;
           bc[e] = xkk * xa * qv;
-          if (l16 == 4 * jt + e) {
-            myGC = gC;
-            myCF = cf;
-          }
         }
+        // the row's last token parks the four chunk totals for the per-channel factors below
+        if (t == CH - 1) *reinterpret_cast<f32x4*>(&N[kg][4 * jt]) = gcv;
         split_f4(rc, rcH[jj], rcL[jj]);
         split_f4(kc, kcH[jj], kcL[jj]);
         split_f4(ac, acH[jj], acL[jj]);
@@ -402,12 +423,14 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
       AabA = mfma16x16x32(bL, aH, AabA);
     }
     {
-      // per channel (one per lane): 2^gC, 2^{gC - c}, 2^c for the chain's state update
+      // per channel (one per lane, slot (l16 / 4, l16 % 4) of row kg): 2^{gC - c}
+      // and 2^c for the chain's state update, from the totals parked in N
+      // (LDS accesses of one wave complete in order; A_ab overwrites N below)
+      const float myGC = N[kg][l16];
+      const float myCF = rintf(0.5f * myGC);
       const int ci = (int)myCF;
-      const float pC = __builtin_amdgcn_exp2f(clamp126(myGC - myCF));
       const int jt = l16 >> 2, e = l16 & 3;
-      reinterpret_cast<float*>(&Z.ec[jt][kg])[e] = __builtin_amdgcn_ldexpf(pC, ci);
-      reinterpret_cast<float*>(&Z.pc[jt][kg])[e] = pC;
+      reinterpret_cast<float*>(&Z.pc[jt][kg])[e] = __builtin_amdgcn_exp2f(clamp126(myGC - myCF));
       reinterpret_cast<float*>(&Z.cen[jt][kg])[e] = __builtin_amdgcn_ldexpf(1.f, ci);
     }
     if (x + 4 < nchunks) issue(x + 4);  // the raw rows are consumed; the next ones land meanwhile
