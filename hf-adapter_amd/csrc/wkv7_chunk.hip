@@ -302,6 +302,10 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
 
   // ===================== producer wave p: chunks p, p+4, ...; lane = (token t = l16, kg)
   const int p = wave - 4;
+  // The producers bound the chunk rate (the chain waves wait for a ready slot
+  // about half of the time), so where a producer and a chain wave can both
+  // issue on a SIMD, the producer goes first.
+  __builtin_amdgcn_s_setprio(1);
   const int t = l16;
   // identity as a B operand: lane (n = l16, k = 4kg + e)
   bf16x4 Ib;
