@@ -446,16 +446,22 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
       AakD[e] = s4 > l16 ? AakD[e] : 0.f;
       AabA[e] = s4 < l16 ? AabA[e] : 0.f;
     }
-    // ---- T = (I - A_ab)^{-1} by forward substitution, column s = lane (lanes 0-15)
+    // ---- T = (I - A_ab)^{-1} in 8 x 8 blocks, T = [[T11, 0], [T21, T22]]:
+    // T11 = (I - N11)^-1 and T22 = (I - N22)^-1 by forward substitution (lane
+    // o + c, o in {0, 8}, solves column c of the block at rows/columns o..o+7),
+    // then T21 = T22 (N21 T11) on all 64 lanes.  Scratch in N once its blocks
+    // are consumed: R = T22 row-major in N[0..7][8..15], X^T = (N21 T11)^T in
+    // N[8..15][8..15].  (LDS accesses of one wave complete in order.)
     *reinterpret_cast<float4*>(&N[l16][4 * kg]) = make_float4(AabA[0], AabA[1], AabA[2], AabA[3]);
     if (lane < CH) {
-      float xc[CH];
+      const int o = lane & 8, c = lane & 7;
+      float xc[8];
 #pragma unroll
-      for (int tt = 0; tt < CH; ++tt) {
-        float acc = (tt == lane) ? 1.f : 0.f;
+      for (int tt = 0; tt < 8; ++tt) {
+        float acc = (tt == c) ? 1.f : 0.f;
 #pragma unroll
         for (int u4 = 0; u4 < (tt + 3) / 4; ++u4) {
-          const float4 n4 = *reinterpret_cast<const float4*>(&N[tt][4 * u4]);
+          const float4 n4 = *reinterpret_cast<const float4*>(&N[o + tt][o + 4 * u4]);
           if (4 * u4 + 0 < tt) acc += n4.x * xc[4 * u4 + 0];
           if (4 * u4 + 1 < tt) acc += n4.y * xc[4 * u4 + 1];
           if (4 * u4 + 2 < tt) acc += n4.z * xc[4 * u4 + 2];
@@ -463,10 +469,33 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
         }
         xc[tt] = acc;
       }
+      *reinterpret_cast<float4*>(&Tc[o + c][o]) = make_float4(xc[0], xc[1], xc[2], xc[3]);
+      *reinterpret_cast<float4*>(&Tc[o + c][o + 4]) = make_float4(xc[4], xc[5], xc[6], xc[7]);
+      // the upper block is zero (for lanes 0-7 this is T21's place, written below)
+      *reinterpret_cast<float4*>(&Tc[o + c][8 - o]) = make_float4(0.f, 0.f, 0.f, 0.f);
+      *reinterpret_cast<float4*>(&Tc[o + c][12 - o]) = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (o) {
 #pragma unroll
-      for (int u4 = 0; u4 < 4; ++u4)
-        *reinterpret_cast<float4*>(&Tc[lane][4 * u4]) =
-            make_float4(xc[4 * u4], xc[4 * u4 + 1], xc[4 * u4 + 2], xc[4 * u4 + 3]);
+        for (int tt = 0; tt < 8; ++tt) N[tt][8 + c] = xc[tt];  // R[tt][c] = T22[tt][c]
+      }
+    }
+    {
+      const int i = lane >> 3, j = lane & 7;
+      // X[i][j] = sum_k N21[i][k] T11[k][j]  (T11[k][j] = Tc[j][k])
+      const float4 a0 = *reinterpret_cast<const float4*>(&N[8 + i][0]);
+      const float4 a1 = *reinterpret_cast<const float4*>(&N[8 + i][4]);
+      const float4 b0 = *reinterpret_cast<const float4*>(&Tc[j][0]);
+      const float4 b1 = *reinterpret_cast<const float4*>(&Tc[j][4]);
+      const float xij = a0.x * b0.x + a0.y * b0.y + a0.z * b0.z + a0.w * b0.w +
+                        a1.x * b1.x + a1.y * b1.y + a1.z * b1.z + a1.w * b1.w;
+      N[8 + j][8 + i] = xij;  // X^T
+      // T21[i][j] = sum_k T22[i][k] X[k][j] = sum_k R[i][k] X^T[j][k]
+      const float4 r0 = *reinterpret_cast<const float4*>(&N[i][8]);
+      const float4 r1 = *reinterpret_cast<const float4*>(&N[i][12]);
+      const float4 x0 = *reinterpret_cast<const float4*>(&N[8 + j][8]);
+      const float4 x1 = *reinterpret_cast<const float4*>(&N[8 + j][12]);
+      Tc[j][8 + i] = r0.x * x0.x + r0.y * x0.y + r0.z * x0.z + r0.w * x0.w +
+                     r1.x * x1.x + r1.y * x1.y + r1.z * x1.z + r1.w * x1.w;
     }
     // D(T): lane (s = l16, t = 4kg + e); A(T): lane (t = l16, s = 4kg + e)
     f32x4 Dt, At;
