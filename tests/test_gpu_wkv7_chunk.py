@@ -72,6 +72,27 @@ def test_chunk_real_model_decay_long(oracle):
     _check(oracle, args, st_np, y, s)
 
 
+def test_chunk_strong_decay_mixed_tiles(oracle):
+    """Channels 32-63 decay hard (about -7 log2 per token, chunk totals -110 to
+    -180, where the centring of the gated rows matters) and channels 0-31
+    weakly, in one chunk; then every channel decays hard.  Totals stay inside
+    the span the centred form keeps exact (-240)."""
+    from rwkv7mi import dplr_chunk_scan
+
+    rng = np.random.default_rng(27)
+    B, T, H, N = 2, 80, 3, 64
+    args, st, st_np = _inputs(rng, B, T, H, state_scale=0.1)
+    x = rng.normal(-0.5, 0.5, (B, T, H, N))
+    x[..., 32:] = rng.normal(1.6, 0.15, (B, T, H, N - 32))
+    args[1] = torch.tensor(np.exp(-np.exp(x)), dtype=torch.float32, device="cuda")
+    y, s = dplr_chunk_scan(*args, st)
+    _check(oracle, args, st_np, y, s)
+    args[1] = torch.tensor(np.exp(-np.exp(rng.normal(1.6, 0.15, (B, T, H, N)))), dtype=torch.float32,
+                           device="cuda")
+    y, s = dplr_chunk_scan(*args, st)
+    _check(oracle, args, st_np, y, s)
+
+
 def test_chunk_log_decay_input(oracle):
     from rwkv7mi import self_chunk_rwkv7
 
