@@ -7,12 +7,12 @@ Workloads (synthetic inputs, random-init weights; nothing is downloaded):
            H=64, N=64, F=16384, V=65536, LoRA 64/64/128/32) with MM8 weights
            (memory policy: every Linear >= 8M weights), fp16 activations, fp32
            state; a 16-token prefill, then hipGraph-replayed greedy decode steps
-           at bsz 1 and 8.  One step = one token for every row, the full model.
+           at bsz 1, 8 and 64.  One step = one token for every row, the full model.
   scan   : the wkv7 chunked prefill scan: B=8, T=4096, H=32, N=64,
            r,k,v ~ N(0,1) fp16, k L2-normalised, kk = k, a = sigmoid(N(0,1)),
            w = exp(-exp(x)), x ~ N(-0.5, 0.5), fp32 state from zero.
 The default run measures both and prints ONE JSON line whose ``value`` is the
-bsz-1 decode throughput; bsz 8 and the scan are reported alongside.
+bsz-1 decode throughput; bsz 8 and 64 and the scan are reported alongside.
 
     python bench.py [--steps K] [--warmup W] [--workload decode|scan|all] [--no-cpu]
 """
@@ -385,7 +385,7 @@ def main(argv=None):
                     help="write profiles/traffic.json from two rocprofv3 --pmc counter CSVs and exit")
     ap.add_argument("--heads", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--batches", default="1,8", help="decode batch sizes (the first is the headline)")
+    ap.add_argument("--batches", default="1,8,64", help="decode batch sizes (1 is the headline)")
     args = ap.parse_args(argv)
     if args.summarize_traffic:
         summarize_traffic(*args.summarize_traffic)
@@ -415,7 +415,7 @@ def main(argv=None):
         d1 = dec[1]
         mk = dec["mm8_kernel"]
         out = {
-            "metric": "decode tok/s 7.2B MM8 bsz1 (bsz8 and wkv7 prefill tok/s alongside)",
+            "metric": "decode tok/s 7.2B MM8 bsz1 (bsz 8 and 64 and wkv7 prefill tok/s alongside)",
             "value": round(d1["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(d1["ms"], 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "f16 activations / u8 MM8 weights / f32 state",
