@@ -411,6 +411,11 @@ def main(argv=None):
     if args.workload in ("all", "decode"):
         dec = run_decode(batches=tuple(int(b) for b in args.batches.split(",")), steps=args.steps,
                          warmup=args.warmup, log=log)
+    if dec is not None and 1 not in dec:  # a partial sweep without the headline batch size
+        print(json.dumps({"decode": {str(b): {"tok_s": round(dec[b]["tok_s"], 2), "ms_per_step": round(dec[b]["ms"], 4),
+                                              "step_roofline_frac": round(dec[b]["frac"], 4)}
+                                     for b in dec if isinstance(b, int)}}), flush=True)
+        return 0
     if dec is not None:
         d1 = dec[1]
         mk = dec["mm8_kernel"]

@@ -153,24 +153,41 @@ __global__ __launch_bounds__(256) void lora_up_kernel(const LoraBatch B, int row
     lora_load8<TA>(wr, (uint32_t)((o0 + l16) * r + kk), kk < r && o0 + l16 < B.A, bh[it], bl[it]);
   }
 
-  // stage mid: fixed-order sum over the K splits, eight loads in flight at a time
+  // stage mid: fixed-order sum over the K splits for four elements per pass,
+  // 32 loads in flight at a time (each element's sum runs in z order)
+  constexpr int IB = 4;  // elements per pass
   const int zstride = rows * r;
   const __amdgpu_buffer_rsrc_t pr = make_rsrc(part + P.part_off, (uint32_t)(B.ks * zstride * 4));
-  for (int idx = tid; idx < rows * r; idx += 256) {
-    float s = 0.f;
+  for (int idx0 = tid; idx0 < rows * r; idx0 += 256 * IB) {
+    float s[IB];
+#pragma unroll
+    for (int ib = 0; ib < IB; ++ib) s[ib] = 0.f;
     for (int z0 = 0; z0 < B.ks; z0 += 8) {
-      float t[8];
+      float t[IB][8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        t[u] = buf_ldf(pr, z0 + u < B.ks ? (uint32_t)(((z0 + u) * zstride + idx) * 4) : BUF_OOB);
+      for (int ib = 0; ib < IB; ++ib) {
+        const int idx = idx0 + 256 * ib;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) s += t[u];  // z order; past-the-end terms are +0
+        for (int u = 0; u < 8; ++u)
+          t[ib][u] = buf_ldf(pr, z0 + u < B.ks && idx < zstride ? (uint32_t)(((z0 + u) * zstride + idx) * 4)
+                                                                 : BUF_OOB);
+      }
+#pragma unroll
+      for (int ib = 0; ib < IB; ++ib)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s[ib] += t[ib][u];  // z order; past-the-end terms are +0
     }
-    const float v = to_f32(from_f32<TA>(lora_act(s, P.act_d)));
-    const int row = idx / r, k = idx % r;
-    const _Float16 h = (_Float16)v;
-    mh[row][k] = h;
-    if constexpr (SPLIT) ml[row][k] = (_Float16)(v - (float)h);
+#pragma unroll
+    for (int ib = 0; ib < IB; ++ib) {
+      const int idx = idx0 + 256 * ib;
+      if (idx < zstride) {
+        const float v = to_f32(from_f32<TA>(lora_act(s[ib], P.act_d)));
+        const int row = idx / r, k = idx % r;
+        const _Float16 h = (_Float16)v;
+        mh[row][k] = h;
+        if constexpr (SPLIT) ml[row][k] = (_Float16)(v - (float)h);
+      }
+    }
   }
   __syncthreads();
 

@@ -40,29 +40,13 @@
 //
 // Up to four problems with the same (rows, I, O) run in one launch
 // (blockIdx.y), e.g. the R/K/V projections of one layer.
-#include "common.h"
+#include "mm8t_common.h"
 
 namespace rwkv7mi {
 
-constexpr int MM8T_COLS = 16;
-constexpr int MM8T_MAXPROB = 4;
 constexpr int MM8T_SB = 4;  // x' staging groups per load batch
 constexpr int MM8T_LDS_X = 72 * 1024;      // x' staging bytes per workgroup (2 workgroups per CU)
 constexpr int MM8T_LDS_X_ONE = 144 * 1024; // when the grid is at most one workgroup per CU
-
-struct Mm8tProb {
-  const void* x;
-  const void* mix;  // LN-mix prologue only: this problem's token-shift mix [I]
-  const uint8_t* w;
-  const void* mx;
-  const void* rx;
-  const void* my;
-  const void* ry;
-  const void* bias;
-  const void* residual;
-  void* y;
-  int epilogue;
-};
 
 // Optional decode prologue (rwkv7_hf/fused_decode_norm_mix.py:39-86, 161-296):
 // the activations are built from the residual row x as
@@ -98,57 +82,6 @@ struct Mm8tBatch {
   int rows, I, O, KC;
   int gx;  // product workgroups along x; with the LN-mix prologue one more (x == gx) writes h and the extra mixes
 };
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer loads: an offset at or beyond the descriptor's byte count returns
-// zeros without touching memory, so every load below is unconditional.
-constexpr uint32_t MM8T_OOB = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t mm8t_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ u32x4 mm8t_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
-
-// 8 consecutive elements of type T starting at element e, raw (zeros when
-// !valid); loads are issued here and converted later so a batch of them is in
-// flight together.
-template <typename T>
-struct Raw8 {
-  u32x4 v[sizeof(T) == 4 ? 2 : 1];
-};
-
-template <typename T>
-__device__ __forceinline__ Raw8<T> mm8t_ld8(__amdgpu_buffer_rsrc_t r, uint32_t e, bool valid) {
-  Raw8<T> o;
-  const uint32_t off = valid ? e * (uint32_t)sizeof(T) : MM8T_OOB;
-  o.v[0] = mm8t_ld16(r, off);
-  if constexpr (sizeof(T) == 4) o.v[1] = mm8t_ld16(r, valid ? off + 16u : MM8T_OOB);
-  return o;
-}
-
-__device__ __forceinline__ void mm8t_cvt8(const Raw8<float>& a, float (&o)[8]) {
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    o[q] = __uint_as_float(a.v[0][q]);
-    o[4 + q] = __uint_as_float(a.v[1][q]);
-  }
-}
-__device__ __forceinline__ void mm8t_cvt8(const Raw8<__half>& a, float (&o)[8]) {
-  const f16x8 v = __builtin_bit_cast(f16x8, a.v[0]);
-#pragma unroll
-  for (int q = 0; q < 8; ++q) o[q] = (float)v[q];
-}
-__device__ __forceinline__ void mm8t_cvt8(const Raw8<__hip_bfloat16>& a, float (&o)[8]) {
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    o[2 * q] = __uint_as_float(a.v[0][q] << 16);
-    o[2 * q + 1] = __uint_as_float(a.v[0][q] & 0xffff0000u);
-  }
-}
 
 // bytes of (d0, d1) = rows r..r+7 of one column -> fp16 [w + 0.5] x 8
 __device__ __forceinline__ f16x8 mm8t_b_operand(uint32_t d0, uint32_t d1) {
@@ -794,7 +727,7 @@ static int mm8t_go_csw(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b, 
 }
 
 // compute units of the current device (cached per device)
-static int64_t mm8t_cus() {
+int64_t rwkv7mi::mm8t_cus() {
   static int64_t cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -1121,3 +1054,4 @@ extern "C" int rwkv7mi_mm8t_dequant(const uint8_t* w_blk, const void* mx, const 
     });
   });
 }
+

@@ -30,7 +30,8 @@ from .fused_output import fused_attn_output_prepare
 from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
-from .native_quant_mm8 import MM8Linear, is_blocked, mm8_lnmix_multi_into, mm8_matmul_multi_into
+from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_workspace_bytes,
+                               mm8_lnmix_multi_into, mm8_matmul_multi_into)
 from .native_quant_policy import should_quantize_linear
 from .self_chunk_rwkv7 import _run_chunk
 
@@ -177,13 +178,13 @@ class DenseLinear:
 
 
 class QuantLinear:
-    """MM8 Linear: the fused out-major dequant GEMV/GEMM for up to ``GEMV_ROWS``
-    rows, and a dequantise + library GEMM route above that.  The fused kernel
-    tiles 16 rows per workgroup, so each further 16 rows stream the weights
-    again and re-stage x' per K chunk; at 64 rows (bsz-64 decode) the
-    dequantise + GEMM route measured 15.1 ms per 7.2B step against 18.8 ms."""
+    """MM8 Linear: the fused out-major dequant GEMV for up to ``GEMV_ROWS``
+    rows, the 64-row MFMA tile GEMM (split K) up to ``GEMM_ROWS`` rows, and a
+    dequantise + library GEMM route above that (long prefills, where the
+    products are MFMA-bound and the library GEMM's tiling pays)."""
 
-    GEMV_ROWS = 16
+    GEMV_ROWS = GEMV_ROWS
+    GEMM_ROWS = GEMM_ROWS
 
     def __init__(self, mm8: MM8Linear):
         self.m = mm8
@@ -191,6 +192,12 @@ class QuantLinear:
 
     def apply(self, x2, out, *, act=ACT_NONE, residual=None):
         rows = int(x2.shape[0])
+        if self.GEMV_ROWS < rows <= self.GEMM_ROWS and is_blocked(self.m.w_blk):
+            epi = _lib.EPI_RELU2 if act == 3 else (_lib.EPI_RESIDUAL if residual is not None else _lib.EPI_NONE)
+            if act not in (0, 3) or (act == 3 and residual is not None):
+                raise ValueError("QuantLinear: unsupported activation / residual combination")
+            mm8_gemm_multi_into([x2], [self.m], [out], residuals=[residual], epilogues=[epi])
+            return out
         if rows > self.GEMV_ROWS:
             m = self.m
             W = torch.empty((m.out_features, m.in_features), device=x2.device, dtype=x2.dtype)
@@ -214,10 +221,13 @@ class QuantLinear:
         """The same as ``[l.apply(x, o) for ...]``; out-major MM8 modules of one
         shape run as one launch."""
         rows = int(xs[0].shape[0])
-        if (all(isinstance(l, QuantLinear) for l in lins) and rows <= QuantLinear.GEMV_ROWS
+        if (all(isinstance(l, QuantLinear) for l in lins) and rows <= QuantLinear.GEMM_ROWS
                 and len({(l.in_features, l.out_features) for l in lins}) == 1
                 and all(is_blocked(l.m.w_blk) for l in lins)):
-            mm8_matmul_multi_into(list(xs), [l.m for l in lins], list(outs))
+            if rows <= QuantLinear.GEMV_ROWS:
+                mm8_matmul_multi_into(list(xs), [l.m for l in lins], list(outs))
+            else:
+                mm8_gemm_multi_into(list(xs), [l.m for l in lins], list(outs))
             return outs
         for l, x2, o in zip(lins, xs, outs):
             l.apply(x2, o)
@@ -405,6 +415,15 @@ class NativeRWKV7ForCausalLM:
                 need = max(need, lin.m.rwkv7_workspace_bytes(min(rows, 64)))
         if need:
             _ws.reserve(self.device, need)
+        if QuantLinear.GEMV_ROWS < rows <= QuantLinear.GEMM_ROWS:
+            gneed = 0
+            for L in self.layers:
+                gneed = max(gneed, mm8_gemm_workspace_bytes(3, rows, L.r_proj.in_features, L.r_proj.out_features))
+            for lin in self._linears():
+                if isinstance(lin, QuantLinear):
+                    gneed = max(gneed, mm8_gemm_workspace_bytes(1, rows, lin.in_features, lin.out_features))
+            if gneed:
+                _ws.reserve(self.device, gneed, slot="mm8g")
         cfg = self.config
         ranks = [cfg.decay_low_rank_dim, cfg.a_low_rank_dim, cfg.gate_low_rank_dim, cfg.v_low_rank_dim]
         _ws.reserve(self.device, lora_workspace_bytes(ranks, rows, cfg.hidden_size), slot="lora")

@@ -11,6 +11,7 @@ tensors: there is no CPU path.
 from __future__ import annotations
 
 import ctypes
+import types
 
 import torch
 
@@ -136,6 +137,12 @@ def _check_out(x2, m, out, residual):
     return residual
 
 
+# Blocked-weight routes by row count: the fused GEMV up to GEMV_ROWS rows, the
+# 64-row MFMA tile GEMM up to GEMM_ROWS.
+GEMV_ROWS = 16
+GEMM_ROWS = 256
+
+
 def mm8_matmul_into(x2, w_u8, mx, rx, my, ry, out, *, bias=None, residual=None, epilogue=_lib.EPI_NONE):
     """``out[rows, M] = epilogue(x2[rows, N] @ dequant(W))``.
 
@@ -155,6 +162,11 @@ def mm8_matmul_into(x2, w_u8, mx, rx, my, ry, out, *, bias=None, residual=None, 
         if tuple(w_u8.shape[:2]) != ((m + 15) // 16, (n + 127) // 128) or int(ry.numel()) != n:
             raise ValueError(f"mm8: blocked weights {tuple(w_u8.shape)} do not match [{n}, {m}]")
         residual = _check_out(x2, m, out, residual)
+        if GEMV_ROWS < rows <= GEMM_ROWS:
+            mod = types.SimpleNamespace(w_blk=w_u8, mx=mx, rx=rx, my=my, ry=ry, bias=bias, in_features=n,
+                                        out_features=m)
+            mm8_gemm_multi_into([x2], [mod], [out], residuals=[residual], epilogues=[epilogue])
+            return out
         _lib.call(
             "rwkv7mi_mm8t_matmul", _lib.ptr(x2), _lib.ptr(w_u8), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my),
             _lib.ptr(ry), _lib.ptr(bias), _lib.ptr(residual), _lib.ptr(out), rows, n, m, int(epilogue),
@@ -202,6 +214,47 @@ def mm8_matmul_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
         arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),
         arr([md.bias for md in mods]), arr(residuals), arr(outs), eps,
         rows, n, m, _lib.dtype_code(xs[0]), _lib.dtype_code(mods[0].mx), _lib.stream_of(xs[0]),
+    )
+    return outs
+
+
+def mm8_gemm_workspace_bytes(nprob: int, rows: int, n: int, m: int, splits: int = 0) -> int:
+    """Scratch bytes :func:`mm8_gemm_multi_into` needs: x' and row sums, plus the
+    split-K partials when there is more than one split."""
+    return int(_lib.load().rwkv7mi_mm8t_gemm_workspace_bytes(int(nprob), int(rows), int(n), int(m), int(splits)))
+
+
+def mm8_gemm_multi_into(xs, mods, outs, *, residuals=None, epilogues=None, splits: int = 0):
+    """Many-row (17..256) form of :func:`mm8_matmul_multi_into`: up to four
+    blocked ``MM8Linear`` products of one shape on the MFMA tile kernel, the
+    route ``mm8_matmul_triton`` takes through dequantisation for rows above
+    ``fused_max_rows`` (rwkv7_hf/native_quant_mm8.py:468-507).  Split-K
+    partials use the device's ``"mm8g"`` workspace slot (reserve it before
+    graph capture)."""
+    k = len(mods)
+    if not 1 <= k <= 4 or len(xs) != k or len(outs) != k:
+        raise ValueError("mm8_gemm_multi_into: 1..4 problems")
+    rows, n = (int(s) for s in xs[0].shape)
+    m = int(mods[0].out_features)
+    residuals = list(residuals) if residuals is not None else [None] * k
+    epilogues = list(epilogues) if epilogues is not None else [_lib.EPI_NONE] * k
+    for x2, mod, out, r in zip(xs, mods, outs, residuals):
+        if tuple(x2.shape) != (rows, n) or not x2.is_contiguous() or x2.dtype != xs[0].dtype:
+            raise ValueError("mm8_gemm_multi_into: inputs must share one contiguous shape and dtype")
+        if mod.in_features != n or mod.out_features != m or not is_blocked(mod.w_blk):
+            raise ValueError("mm8_gemm_multi_into: modules must be blocked MM8Linear of one shape")
+        _check_out(x2, m, out, r)
+    _lib.require_gpu(*xs, *outs, name="mm8_gemm_multi")
+    need = mm8_gemm_workspace_bytes(k, rows, n, m, splits)
+    ws = _ws.reserve(xs[0].device, need, slot="mm8g")
+    arr = lambda ts: _lib.ptr_array(ts)
+    eps = (ctypes.c_int * k)(*[int(e) for e in epilogues])
+    _lib.call(
+        "rwkv7mi_mm8t_gemm_multi", k, arr(xs), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
+        arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),
+        arr([md.bias for md in mods]), arr(residuals), arr(outs), eps, rows, n, m, _lib.dtype_code(xs[0]),
+        _lib.dtype_code(mods[0].mx), int(splits), _lib.ptr(ws), int(ws.numel()),
+        _lib.stream_of(xs[0]),
     )
     return outs
 
@@ -416,6 +469,6 @@ def quantize_model_mm8(model, *, min_params: int = 8_000_000, fused: bool = True
 __all__ = [
     "quantize_mm8", "quantize_mm8_outmajor", "quantize_mm8_blocked", "mm8_block", "mm8_unblock", "is_blocked",
     "is_out_major", "mm8_matmul", "mm8_linear", "mm8_matmul_into",
-    "mm8_matmul_multi_into", "mm8_gemv_triton",
+    "mm8_matmul_multi_into", "mm8_gemm_multi_into", "mm8_gemm_workspace_bytes", "mm8_gemv_triton",
     "mm8_matmul_triton", "mm8_workspace_bytes", "MM8Linear", "quantize_model_mm8",
 ]

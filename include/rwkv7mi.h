@@ -230,6 +230,28 @@ int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x,
                               int64_t O, int act_dtype, int meta_dtype,
                               void* stream);
 
+/* Many-row form of rwkv7mi_mm8t_matmul_multi for 17..256 rows (bsz-64
+ * decode, short prefills): 64-row x 128-column MFMA tiles over split K, with
+ * x' = x * ry rounded once to fp16 and the weights centred (w - 128) so that
+ * the rounding touches only the centred term (relative error ~1e-4 of the
+ * result's scale).  With more than one split, fp32 partials go to
+ * `workspace` (>= rwkv7mi_mm8t_gemm_workspace_bytes, 256-byte aligned) and a
+ * second launch adds them in split order: deterministic, no atomics.
+ * splits = 0 picks the count.  Replaces mm8_matmul_triton's materialising
+ * route for rows > fused_max_rows (rwkv7_hf/native_quant_mm8.py:468-507,
+ * :100-126) and MM8Linear.forward (:594) at those row counts. */
+size_t rwkv7mi_mm8t_gemm_workspace_bytes(int nprob, int64_t rows, int64_t I,
+                                         int64_t O, int splits);
+int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x,
+                            const uint8_t* const* w_blk, const void* const* mx,
+                            const void* const* rx, const void* const* my,
+                            const void* const* ry, const void* const* bias,
+                            const void* const* residual, void* const* y,
+                            const int* epilogue, int64_t rows, int64_t I,
+                            int64_t O, int act_dtype, int meta_dtype,
+                            int splits, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* Decode LN + token-shift mix fused into the out-major MM8 GEMV: for up to
  * four problems of one shape, h = LayerNorm(x) (x [rows, I] the residual
  * rows, ln_w / ln_b [I]), x_p = round(h + (prev - h) * mix_p) and

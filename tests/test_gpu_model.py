@@ -58,11 +58,12 @@ def _close(got, ref):
     np.testing.assert_array_equal(got.argmax(-1)[sure], ref.argmax(-1)[sure])
 
 
-@pytest.mark.parametrize("mm8", [False, True])
-def test_prefill_then_decode_matches_oracle(mm8):
+@pytest.mark.parametrize("mm8,B", [(False, 2), (True, 2), (True, 20)])
+def test_prefill_then_decode_matches_oracle(mm8, B):
+    """B = 20 decodes through the many-row MM8 tile GEMM (more than 16 rows)."""
     cfg, model, ref = _build(mm8)
     rng = np.random.default_rng(1)
-    B, T = 2, 37
+    T = 37
     ids = rng.integers(0, cfg.vocab_size, (B, T))
     ref_logits, st = ref.run(ids)
     logits, cache = model(torch.tensor(ids, device="cuda"))
@@ -82,11 +83,10 @@ def test_prefill_then_decode_matches_oracle(mm8):
     assert cache.seen_tokens == T + 4
 
 
-@pytest.mark.parametrize("mm8", [False, True])
-def test_graph_decode_equals_eager_decode(mm8):
+@pytest.mark.parametrize("mm8,B", [(False, 3), (True, 3), (True, 24)])
+def test_graph_decode_equals_eager_decode(mm8, B):
     cfg, model, _ = _build(mm8)
     rng = np.random.default_rng(2)
-    B = 3
     ids = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 9)), device="cuda")
     _, c1 = model(ids)
     c2 = c1.clone()
