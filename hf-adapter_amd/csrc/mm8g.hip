@@ -273,24 +273,50 @@ __global__ __launch_bounds__(256, 2) void mm8g_kernel(const Mm8gBatch B) {
   }
 }
 
-// y[p][row][o] = epilogue of the splits' partials added in order 0..S-1
-template <typename TA, typename TM>
+// y[p][row][o..o+V-1] = epilogue of the splits' partials added in order
+// 0..S-1 (V = 4 when O % 4 == 0: float4 loads, four splits in flight)
+template <typename TA, typename TM, int V>
 __global__ __launch_bounds__(256) void mm8g_reduce_kernel(const Mm8gBatch B) {
   const int p = blockIdx.y;
   const Mm8tProb& P = B.p[p];
   const int O = B.O;
   const int64_t per = (int64_t)B.rows * O;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
   if (idx >= per) return;
   const int64_t row = idx / O;
   const int o = (int)(idx - row * O);
   const int64_t sstride = (int64_t)B.nprob * per;
   const float* part = B.part + (int64_t)p * per + idx;
+  float a[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) a[v] = 0.f;
+  constexpr int SB = 4;  // splits in flight
+  for (int s0 = 0; s0 < B.S; s0 += SB) {
+    float t[SB][V];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      if (s0 + u < B.S) {
+        if constexpr (V == 4) {
+          const float4 q = *reinterpret_cast<const float4*>(part + (s0 + u) * sstride);
+          t[u][0] = q.x, t[u][1] = q.y, t[u][2] = q.z, t[u][3] = q.w;
+        } else {
+          t[u][0] = part[(s0 + u) * sstride];
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v) t[u][v] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+#pragma unroll
+      for (int v = 0; v < V; ++v) a[v] += t[u][v];  // split order; past-the-end terms are +0
+  }
   const float* rsum = B.rsum + ((int64_t)p * B.rows + row) * 3;
-  float a = 0.f;
-  for (int s = 0; s < B.S; ++s) a += part[s * sstride];
   const float s0 = rsum[0], s1 = rsum[1], s2 = rsum[2];
-  reinterpret_cast<TA*>(P.y)[idx] = from_f32<TA>(mm8g_finish<TA, TM>(P, a, s0, s1, s2, row, o, O));
+#pragma unroll
+  for (int v = 0; v < V; ++v)
+    reinterpret_cast<TA*>(P.y)[idx + v] = from_f32<TA>(mm8g_finish<TA, TM>(P, a[v], s0, s1, s2, row, o + v, O));
 }
 
 // Split count: explicit, or the fewest (a power of two) that keep every
@@ -411,8 +437,13 @@ extern "C" int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x, const ui
         hipLaunchKernelGGL((mm8g_kernel<TA, TM, MM8G_DEPTH, MM8G_MAXKB>), grid, dim3(256), lds, as_stream(stream), b);
       rc = check_launch("mm8g_kernel");
       if (rc != RWKV7MI_OK || S == 1) return rc;
-      const dim3 rgrid((unsigned)((rows * O + 255) / 256), (unsigned)nprob);
-      hipLaunchKernelGGL((mm8g_reduce_kernel<TA, TM>), rgrid, dim3(256), 0, as_stream(stream), b);
+      if (O % 4 == 0) {
+        const dim3 rgrid((unsigned)((rows * O / 4 + 255) / 256), (unsigned)nprob);
+        hipLaunchKernelGGL((mm8g_reduce_kernel<TA, TM, 4>), rgrid, dim3(256), 0, as_stream(stream), b);
+      } else {
+        const dim3 rgrid((unsigned)((rows * O + 255) / 256), (unsigned)nprob);
+        hipLaunchKernelGGL((mm8g_reduce_kernel<TA, TM, 1>), rgrid, dim3(256), 0, as_stream(stream), b);
+      }
       return check_launch("mm8g_reduce_kernel");
     });
   });
