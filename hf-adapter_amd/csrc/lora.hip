@@ -258,7 +258,9 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
   int64_t off = 0;
   const int64_t nr_max = rows < LORA_ROWS ? rows : LORA_ROWS;
   const int tiles_d = (int)lora_tiles(nprob, ranks);
-  const int ks = lora_splits(tiles_d, D);
+  // more than 16 rows per chunk: a quarter of the K splits, so each up tile
+  // sums four times fewer partials (its staging is the up kernel's cost there)
+  const int ks = up && nr_max > 16 ? std::max(1, lora_splits(tiles_d, D) / 4) : lora_splits(tiles_d, D);
   for (int i = 0; i < nprob; ++i) {
     if (!xs[i] || !w_down[i] || (up && (!w_up[i] || !ys[i]))) return fail(RWKV7MI_EINVAL, "lora_multi: null pointer");
     if (ranks[i] <= 0 || ranks[i] % 8 || ranks[i] > LORA_MAXR)

@@ -86,22 +86,36 @@ __global__ __launch_bounds__(256) void mm8g_prep_kernel(const Mm8gBatch B) {
   const __amdgpu_buffer_rsrc_t myr = mm8t_rsrc(P.my, (uint32_t)(I * sizeof(TM)));
   _Float16* xo = B.xp + ((int64_t)p * B.rows + row) * KBK;
   float a = 0.f, b = 0.f, c = 0.f;
-  for (int k = 8 * tid; k < KBK; k += 8 * 256) {
-    const bool valid = k < I;
-    float x[8], rv[8], mv[8];
-    mm8t_cvt8(mm8t_ld8<TA>(xr, (uint32_t)k, valid), x);
-    mm8t_cvt8(mm8t_ld8<TM>(ryr, (uint32_t)k, valid), rv);
-    mm8t_cvt8(mm8t_ld8<TM>(myr, (uint32_t)k, valid), mv);
-    f16x8 h;
+  constexpr int PB = 4;  // passes whose loads are in flight together
+  for (int k0 = 8 * tid; k0 < KBK; k0 += 8 * 256 * PB) {
+    Raw8<TA> xv[PB];
+    Raw8<TM> rr[PB], mr[PB];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float xp = x[e] * rv[e];
-      h[e] = (_Float16)xp;
-      a += x[e];
-      b += x[e] * mv[e];
-      c += xp;
+    for (int u = 0; u < PB; ++u) {
+      const int k = k0 + 8 * 256 * u;
+      const bool valid = k < I;
+      xv[u] = mm8t_ld8<TA>(xr, (uint32_t)k, valid);
+      rr[u] = mm8t_ld8<TM>(ryr, (uint32_t)k, valid);
+      mr[u] = mm8t_ld8<TM>(myr, (uint32_t)k, valid);
     }
-    *reinterpret_cast<f16x8*>(xo + k) = h;
+#pragma unroll
+    for (int u = 0; u < PB; ++u) {
+      const int k = k0 + 8 * 256 * u;
+      float x[8], rv[8], mv[8];
+      mm8t_cvt8(xv[u], x);
+      mm8t_cvt8(rr[u], rv);
+      mm8t_cvt8(mr[u], mv);
+      f16x8 h;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xp = x[e] * rv[e];
+        h[e] = (_Float16)xp;
+        a += x[e];
+        b += x[e] * mv[e];
+        c += xp;
+      }
+      if (k < KBK) *reinterpret_cast<f16x8*>(xo + k) = h;
+    }
   }
   __shared__ float part[4][3];
   a = wave_sum(a);
