@@ -178,7 +178,8 @@ def run_decode(batches=(1, 8), steps=64, warmup=5, log=print):
     g.manual_seed(0)
     for B in batches:
         prompt = torch.randint(0, cfg.vocab_size, (B, 16), generator=g, device="cuda")
-        logits, cache = model(prompt)
+        out = model(prompt)
+        logits, cache = out.logits, out.past_key_values
         runner = model.graph_runner(B)
         tok = logits[:, -1].argmax(-1)
         state = {"tok": tok}
@@ -343,6 +344,22 @@ def run_traffic():
     print("bench: traffic workload done (2 decode steps + calibration copy)", file=sys.stderr, flush=True)
 
 
+def run_scan_traffic(H=32):
+    """Kernels for the scan's counter runs: two chunked-scan calls at B=8,
+    T=4096 (the second is the measured one) and the COPY_BYTES calibration copy."""
+    import torch
+    from rwkv7mi import self_chunk_rwkv7
+
+    inputs = make_scan_inputs(8, 4096, H, 64)
+    for _ in range(2):
+        self_chunk_rwkv7(*inputs, chunk_size=16)
+    src = torch.ones(COPY_BYTES // 2, device="cuda", dtype=torch.float16)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(f"bench: scan traffic workload done (H={H}: 2 scan calls + calibration copy)", file=sys.stderr, flush=True)
+
+
 def _counter_rows(path):
     import csv
 
@@ -380,7 +397,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["all", "decode", "scan", "traffic"], default="all")
+    ap.add_argument("--workload", choices=["all", "decode", "scan", "traffic", "scan_traffic"], default="all")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write profiles/traffic.json from two rocprofv3 --pmc counter CSVs and exit")
     ap.add_argument("--heads", type=int, default=32)
@@ -401,6 +418,9 @@ def main(argv=None):
     log = lambda m: print(m, file=sys.stderr, flush=True)
     if args.workload == "traffic":
         run_traffic()
+        return 0
+    if args.workload == "scan_traffic":
+        run_scan_traffic(args.heads)
         return 0
     out: dict = {}
     scan = dec = None

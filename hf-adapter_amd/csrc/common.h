@@ -5,6 +5,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_bf16.h>
 #include <stdint.h>
+#include <atomic>
 #include <string>
 
 #include "../../include/rwkv7mi.h"
@@ -18,6 +19,12 @@ int fail(int code, const std::string& msg);
 int check_launch(const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Raises a kernel's dynamic LDS limit on the current device once.  `done` is the
+// caller's per-kernel bitmask of devices already raised (bit = device index);
+// racing threads may both set the attribute, which is harmless.  Returns
+// RWKV7MI_OK or RWKV7MI_ELAUNCH.
+int raise_dynamic_lds(const void* kernel, int bytes, std::atomic<uint64_t>& done, const char* who);
 
 inline bool valid_dtype(int d) { return d == RWKV7MI_F32 || d == RWKV7MI_F16 || d == RWKV7MI_BF16; }
 

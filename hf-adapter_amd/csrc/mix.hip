@@ -173,17 +173,24 @@ __global__ __launch_bounds__(MIX_THREADS) void seq_norm_mix_kernel(
   const int64_t row = (int64_t)b * T + t;
   float v[MIX_SLOTS][MIX_VEC], pv[MIX_SLOTS][MIX_VEC], w[MIX_SLOTS][MIX_VEC], bb[MIX_SLOTS][MIX_VEC];
   float mx[6][MIX_SLOTS][MIX_VEC];
+  // ln_w == null: x is already normalised (the reference's calling convention,
+  // rwkv7_hf/fused_time_mix.py:413-515) and is mixed as given
+  const bool norm = ln_w != nullptr;
   ld_slots(x + row * D, D, v);
   ld_slots(t > 0 ? x + (row - 1) * D : prev_in + (int64_t)b * D, D, pv);
-  ld_slots(ln_w, D, w);
-  ld_slots(ln_b, D, bb);
+  if (norm) {
+    ld_slots(ln_w, D, w);
+    ld_slots(ln_b, D, bb);
+  }
 #pragma unroll
   for (int i = 0; i < 6; ++i) ld_slots(reinterpret_cast<const TP*>(m.mix[i]), D, mx[i], i < nmix);
-  ln_slots(v, D, w, bb, eps, red);
-  if (t > 0) {
-    ln_slots(pv, D, w, bb, eps, red);
+  if (norm) {
+    ln_slots(v, D, w, bb, eps, red);
+    if (t > 0) {
+      ln_slots(pv, D, w, bb, eps, red);
 #pragma unroll
-    for (int s = 0; s < MIX_SLOTS; ++s) round8<TA>(pv[s]);
+      for (int s = 0; s < MIX_SLOTS; ++s) round8<TA>(pv[s]);
+    }
   }
   if (t == T - 1) st_slots(prev_out + (int64_t)b * D, D, v);
 #pragma unroll
@@ -274,8 +281,8 @@ extern "C" int rwkv7mi_seq_norm_mix(const void* x, const void* prev_in, void* pr
     return fail(RWKV7MI_EINVAL, "seq_norm_mix: D must be a multiple of 8 and at most 8192");
   if (nmix < 1 || nmix > 6) return fail(RWKV7MI_EINVAL, "seq_norm_mix: nmix must be 1..6");
   if (B == 0 || T == 0) return RWKV7MI_OK;
-  if (!x || !prev_in || !prev_out || !ln_w || !ln_b || !mixes || !outs)
-    return fail(RWKV7MI_EINVAL, "seq_norm_mix: null pointer");
+  if (!x || !prev_in || !prev_out || !mixes || !outs || (!ln_w) != (!ln_b))
+    return fail(RWKV7MI_EINVAL, "seq_norm_mix: null pointer (ln_w and ln_b are both given or both null)");
   if (prev_in == prev_out) return fail(RWKV7MI_EINVAL, "seq_norm_mix: prev_in and prev_out must differ");
   if (!mix_aligned({x, prev_in, prev_out, ln_w, ln_b})) return fail(RWKV7MI_EINVAL, "seq_norm_mix: pointers must be 16-byte aligned");
   if (B * T > INT32_MAX) return fail(RWKV7MI_EINVAL, "seq_norm_mix: too many rows");

@@ -431,16 +431,14 @@ extern "C" int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x, const ui
     using TA = decltype(ta);
     return dispatch_dtype(meta_dtype, [&](auto tm) {
       using TM = decltype(tm);
-      static bool lds_raised = false;  // dynamic LDS above 64 KB is enabled once per instance
-      if (!lds_raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8g_kernel<TA, TM, MM8G_DEPTH, MM8G_MAXKB>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize,
-                                MM8G_ROWS * (128 * MM8G_MAXKB + 8) * 2) != hipSuccess ||
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8g_kernel<TA, TM, MM8G_DEPTH, 4>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, MM8G_ROWS * (128 * 4 + 8) * 2) != hipSuccess)
-          return fail(RWKV7MI_ELAUNCH, "mm8g_kernel: cannot raise the dynamic LDS limit");
-        lds_raised = true;
-      }
+      // devices whose dynamic LDS limit is raised for each instance
+      static std::atomic<uint64_t> raised_max{0}, raised_4{0};
+      if (int rc = raise_dynamic_lds(reinterpret_cast<const void*>(&mm8g_kernel<TA, TM, MM8G_DEPTH, MM8G_MAXKB>),
+                                     MM8G_ROWS * (128 * MM8G_MAXKB + 8) * 2, raised_max, "mm8g_kernel"))
+        return rc;
+      if (int rc = raise_dynamic_lds(reinterpret_cast<const void*>(&mm8g_kernel<TA, TM, MM8G_DEPTH, 4>),
+                                     MM8G_ROWS * (128 * 4 + 8) * 2, raised_4, "mm8g_kernel"))
+        return rc;
       hipLaunchKernelGGL((mm8g_prep_kernel<TA, TM>), dim3((unsigned)rows, (unsigned)nprob), dim3(256), 0,
                          as_stream(stream), b);
       int rc = check_launch("mm8g_prep_kernel");

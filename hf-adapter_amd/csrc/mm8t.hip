@@ -685,13 +685,10 @@ using namespace rwkv7mi;
 
 template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO, int RING>
 static int mm8t_go(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
-  static bool lds_raised = false;  // dynamic LDS above 64 KB must be enabled once per instance
-  if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, NW, CSW, BITS, PRO, RING>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, MM8T_LDS_X_ONE + 1024) != hipSuccess)
-      return fail(RWKV7MI_ELAUNCH, "mm8t_kernel: cannot raise the dynamic LDS limit");
-    lds_raised = true;
-  }
+  static std::atomic<uint64_t> lds_raised{0};  // devices whose dynamic LDS limit is raised for this instance
+  if (int rc = raise_dynamic_lds(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, NW, CSW, BITS, PRO, RING>),
+                                 MM8T_LDS_X_ONE + 1024, lds_raised, "mm8t_kernel"))
+    return rc;
   hipLaunchKernelGGL((mm8t_kernel<TA, TM, NW, CSW, BITS, PRO, RING>), grid, dim3(64 * NW), lds, as_stream(stream), b);
   return check_launch("mm8t_kernel");
 }

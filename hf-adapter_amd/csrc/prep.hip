@@ -3,7 +3,9 @@
 // state prep (rwkv7_hf/fused_prefill.py:43-150, torch form native_jit_prefill.py:779-790):
 //   kk = normalize(k_raw * k_k) per head,  k = k_raw * (1 + (a - 1) * k_a),
 //   v: mode 1 -> v_first = v;  mode 2 -> v = v + (v_first - v) * v_gate,
-//   log_w = -0.606531 * sigmoid(w_raw)  (natural log of the decay, fp32)
+//   log_w = -0.606531 * sigmoid(w_raw)  (natural log of the decay) or the decay
+//   exp(log_w), in fp32 or the activation dtype;  optionally a = sigmoid(a_raw)
+//   and v_gate = sigmoid(v_gate_raw) first (rounded to the activation dtype)
 // output prep (rwkv7_hf/fused_output.py:39-84, torch form native_jit_decode.py:862-866):
 //   out = (GroupNorm_H(y) + (sum_head r * k * r_k) * v) * g
 // One 64-lane wave per (row, head): lane = channel.
@@ -13,13 +15,14 @@ namespace rwkv7mi {
 
 constexpr int PHD = 64;
 
-template <typename TA, typename TP>
+template <typename TA, typename TP, typename TW>
 __global__ __launch_bounds__(256) void state_prep_kernel(const TA* __restrict__ k_raw, const TA* __restrict__ a,
-                                                         const TA* __restrict__ w_raw, TA* v, TA* v_first,
-                                                         const TA* __restrict__ v_gate, const TP* __restrict__ k_k,
-                                                         const TP* __restrict__ k_a, TA* __restrict__ kk_out,
-                                                         TA* __restrict__ k_out, float* __restrict__ logw_out,
-                                                         int64_t rows, int H, int v_mode) {
+                                                         const TA* __restrict__ w_raw, const TA* v_raw, TA* v_out,
+                                                         TA* v_first, const TA* __restrict__ v_gate,
+                                                         const TP* __restrict__ k_k, const TP* __restrict__ k_a,
+                                                         TA* __restrict__ kk_out, TA* __restrict__ k_out,
+                                                         TW* __restrict__ w_out, int64_t rows, int H, int v_mode,
+                                                         int flags) {
   const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (unit >= rows * H) return;
   const int h = (int)(unit % H);
@@ -27,18 +30,27 @@ __global__ __launch_bounds__(256) void state_prep_kernel(const TA* __restrict__ 
   const int64_t off = unit * PHD + c;
   const int pc = h * PHD + c;
   const float kr = to_f32(k_raw[off]);
-  const float av = to_f32(a[off]);
+  float av = to_f32(a[off]);
+  if (flags & RWKV7MI_PREP_A_RAW) av = to_f32(from_f32<TA>(1.0f / (1.0f + expf(-av))));  // sigmoid in the act dtype
   const float ku = kr * to_f32(k_k[pc]);
   const float nrm = sqrtf(wave_sum(ku * ku));
   kk_out[off] = from_f32<TA>(ku / fmaxf(nrm, 1.0e-12f));
   k_out[off] = from_f32<TA>(kr * (1.0f + (av - 1.0f) * to_f32(k_a[pc])));
   const float wr = to_f32(w_raw[off]);
-  logw_out[off] = -0.606531f / (1.0f + expf(-wr));
+  const float lw = -0.606531f / (1.0f + expf(-wr));
+  w_out[off] = from_f32<TW>((flags & RWKV7MI_PREP_W_DECAY) ? expf(lw) : lw);
+  // v_out may alias v_raw: each element is read, then written, by one lane
+  const TA vr = v_raw[off];
   if (v_mode == 1) {
-    v_first[off] = v[off];
+    v_first[off] = vr;
+    v_out[off] = vr;
   } else if (v_mode == 2) {
-    const float vv = to_f32(v[off]);
-    v[off] = from_f32<TA>(vv + (to_f32(v_first[off]) - vv) * to_f32(v_gate[off]));
+    const float vv = to_f32(vr);
+    float gv = to_f32(v_gate[off]);
+    if (flags & RWKV7MI_PREP_VGATE_RAW) gv = to_f32(from_f32<TA>(1.0f / (1.0f + expf(-gv))));
+    v_out[off] = from_f32<TA>(vv + (to_f32(v_first[off]) - vv) * gv);
+  } else {
+    v_out[off] = vr;
   }
 }
 
@@ -68,15 +80,19 @@ __global__ __launch_bounds__(256) void output_prep_kernel(const TA* __restrict__
 
 using namespace rwkv7mi;
 
-extern "C" int rwkv7mi_state_prep(const void* k_raw, const void* a, const void* w_raw, void* v, void* v_first,
-                                  const void* v_gate, const void* k_k, const void* k_a, void* kk_out, void* k_out,
-                                  float* logw_out, int64_t rows, int64_t H, int64_t N, int v_mode, int act_dtype,
-                                  int param_dtype, void* stream) {
+extern "C" int rwkv7mi_state_prep(const void* k_raw, const void* a, const void* w_raw, const void* v_raw,
+                                  void* v_out, void* v_first, const void* v_gate, const void* k_k, const void* k_a,
+                                  void* kk_out, void* k_out, void* w_out, int64_t rows, int64_t H, int64_t N,
+                                  int v_mode, int flags, int act_dtype, int param_dtype, int w_dtype, void* stream) {
   if (N != PHD) return fail(RWKV7MI_EINVAL, "state_prep: head size must be 64");
   if (rows < 0 || H <= 0) return fail(RWKV7MI_EINVAL, "state_prep: bad shape");
   if (v_mode < 0 || v_mode > 2) return fail(RWKV7MI_EINVAL, "state_prep: bad v_mode");
+  if (flags & ~(RWKV7MI_PREP_A_RAW | RWKV7MI_PREP_VGATE_RAW | RWKV7MI_PREP_W_DECAY))
+    return fail(RWKV7MI_EINVAL, "state_prep: unknown flags");
+  if (w_dtype != RWKV7MI_F32 && w_dtype != act_dtype)
+    return fail(RWKV7MI_EINVAL, "state_prep: w_out is fp32 or the activation dtype");
   if (rows == 0) return RWKV7MI_OK;
-  if (!k_raw || !a || !w_raw || !v || !k_k || !k_a || !kk_out || !k_out || !logw_out)
+  if (!k_raw || !a || !w_raw || !v_raw || !v_out || !k_k || !k_a || !kk_out || !k_out || !w_out)
     return fail(RWKV7MI_EINVAL, "state_prep: null pointer");
   if (v_mode && !v_first) return fail(RWKV7MI_EINVAL, "state_prep: v_mode needs v_first");
   if (v_mode == 2 && !v_gate) return fail(RWKV7MI_EINVAL, "state_prep: v_mode 2 needs v_gate");
@@ -86,11 +102,15 @@ extern "C" int rwkv7mi_state_prep(const void* k_raw, const void* a, const void* 
     using TA = decltype(ta);
     return dispatch_dtype(param_dtype, [&](auto tp) {
       using TP = decltype(tp);
-      hipLaunchKernelGGL((state_prep_kernel<TA, TP>), dim3((unsigned)((units + 3) / 4)), dim3(256), 0,
-                         as_stream(stream), (const TA*)k_raw, (const TA*)a, (const TA*)w_raw, (TA*)v, (TA*)v_first,
-                         (const TA*)v_gate, (const TP*)k_k, (const TP*)k_a, (TA*)kk_out, (TA*)k_out, logw_out,
-                         rows, (int)H, v_mode);
-      return check_launch("state_prep_kernel");
+      auto go = [&](auto tw) {
+        using TW = decltype(tw);
+        hipLaunchKernelGGL((state_prep_kernel<TA, TP, TW>), dim3((unsigned)((units + 3) / 4)), dim3(256), 0,
+                           as_stream(stream), (const TA*)k_raw, (const TA*)a, (const TA*)w_raw, (const TA*)v_raw,
+                           (TA*)v_out, (TA*)v_first, (const TA*)v_gate, (const TP*)k_k, (const TP*)k_a,
+                           (TA*)kk_out, (TA*)k_out, (TW*)w_out, rows, (int)H, v_mode, flags);
+        return check_launch("state_prep_kernel");
+      };
+      return w_dtype == RWKV7MI_F32 ? go(float{}) : go(TA{});
     });
   });
 }

@@ -17,8 +17,13 @@
 // rwkv7_hf/dplr_prefill.py:221-311) with everything that does not depend on S
 // moved off the state's critical path, and one set of gated rows serving every
 // product (the per-channel scales fold into the state).  Exact while a chunk's
-// log2-decay span -gC stays within 240 (per-token w >= 2^-15 on average);
-// beyond that the factors clamp at 2^+-126.
+// log2-decay span -gC stays within 252 (per-token w >= 2^-15.75 on average);
+// beyond that the factors clamp at 2^+-126 and the call's status word records
+// it (WKV7_STATUS_CLAMPED, read by rwkv7mi_wkv7_chunk_status).
+//
+// The decay w arrives as the decay itself (WMODE 0), its natural log (1) or
+// the raw pre-activation of the reference's clampw scan (2):
+// w = exp(-0.606531 sigmoid(w_raw)), so log2 w = -0.606531 log2(e) sigmoid(w_raw).
 //
 // Mapping: one workgroup of 8 waves per (batch, head), specialised:
 // * waves 0-3 ("chain") hold the fp32 state — wave q owns 16 value rows, as
@@ -32,7 +37,9 @@
 // Slots hand over through LDS flags (producer: ready = chunk id; chain waves:
 // done = chunk id); with five slots for four producers a producer never
 // waits for a slot in steady state, and no workgroup barrier sits in the
-// chunk loop.  All waits are bounded.
+// chunk loop.  All waits are bounded: a wait that gives up (the kernel then
+// goes on with whatever the slot holds) sets WKV7_STATUS_TIMEOUT in the
+// device's status word, so the host can tell that the call's output is void.
 //
 // Products run on v_mfma_f32_16x16x{32,16}_bf16 with operands split into bf16
 // hi + lo (hi*hi + hi*lo + lo*hi, ~1e-5 relative) and fp32 accumulation.
@@ -53,6 +60,12 @@ constexpr int HD = 64;   // head size
 constexpr int NSLOT = 6; // LDS slots: more than producer waves, so a producer
                           // rarely waits for the chain to free one
 constexpr int WAIT_SPINS = 1 << 20;
+
+// Sticky per-device status bits of the chunk kernel (this file's copy on each
+// GPU), read and cleared by rwkv7mi_wkv7_chunk_status.
+constexpr int WKV7_STATUS_TIMEOUT = 1;  // a bounded LDS-flag wait gave up
+constexpr int WKV7_STATUS_CLAMPED = 2;  // a chunk's gate span exceeded the exact range
+__device__ int wkv7_chunk_status_word;
 
 // one chunk's operands for the chain waves, each array indexed [..][lane]
 struct ChunkSlot {
@@ -132,11 +145,20 @@ __device__ __forceinline__ float row_last(float x) {  // lane 15 of the row in e
 }
 
 // ---- LDS flags (workgroup scope)
-__device__ __forceinline__ void wait_geq(int* f, int v) {
+// true once *f >= v; false when the wait gives up after WAIT_SPINS polls
+__device__ __forceinline__ bool wait_geq(int* f, int v) {
   for (int it = 0; it < WAIT_SPINS; ++it) {
-    if (__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) return;
+    if (__hip_atomic_load(f, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) return true;
     __builtin_amdgcn_s_sleep(1);
   }
+  return false;
+}
+// ORs this wave's status bits into the device's status word (one vector atomic
+// from lane 0; nothing when the bits are clear)
+__device__ __forceinline__ void post_status(int bits) {
+  bits = __builtin_amdgcn_readfirstlane(bits);
+  if (bits && (threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_or(&wkv7_chunk_status_word, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void set_flag(int* f, int v) {
   __hip_atomic_store(f, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -189,7 +211,7 @@ __device__ __forceinline__ float row_val(const RawRow<T>& o, int jt, int e) {
 
 __device__ __forceinline__ float clamp126(float x) { return fminf(fmaxf(x, -126.f), 126.f); }
 
-template <typename TA, typename TW, bool WLOG>
+template <typename TA, typename TW, int WMODE>
 __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
     const TA* __restrict__ r, const TW* __restrict__ w, const TA* __restrict__ k,
     const TA* __restrict__ v, const TA* __restrict__ kk, const TA* __restrict__ a,
@@ -229,10 +251,11 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
     uint32_t yoff[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) yoff[e] = (uint32_t)(((4 * kg + e) * tok + ich) * (int64_t)sizeof(TA));
+    int status = 0;
     for (int x = 0; x < nchunks; ++x) {
       const int s = x % NSLOT;
       const ChunkSlot& Z = L.slot[s];
-      wait_geq(&L.ready[s], x);
+      if (!wait_geq(&L.ready[s], x)) status |= WKV7_STATUS_TIMEOUT;
       bf16x8 waH[2], waL[2], rqH[2], rqL[2], bkH[4], bkL[4];
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
@@ -297,6 +320,7 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
       *reinterpret_cast<float4*>(dst + 32 * (jt >> 1) + 4 * (jt & 1)) = make_float4(S[jt][0], S[jt][1], S[jt][2], S[jt][3]);
+    post_status(status);
     return;
   }
 
@@ -333,6 +357,8 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
   };
   if (p < nchunks) issue(p);
 
+  bool waited_out = false;
+  float gmin = 0.f, gmax = 0.f;  // extremes of the chunk totals gC this lane saw
   for (int x = p; x < nchunks; x += 4) {
     // A token past T loads w = 0 (log2 -> -inf, or 0 as a log) and must add
     // nothing to the gate sums: its floor is 0 instead of -126.
@@ -341,7 +367,7 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
     // every result below is then stored as soon as it exists (D(ac) and rc are
     // parked in the Wa / Rq areas until Wa and Rq replace them).
     const int s = x % NSLOT;
-    for (int qq = 0; qq < 4; ++qq) wait_geq(&L.done[qq][s], x - NSLOT);
+    for (int qq = 0; qq < 4; ++qq) waited_out |= !wait_geq(&L.done[qq][s], x - NSLOT);
     ChunkSlot& Z = L.slot[s];
 
     // ---- per K half cc (channel tiles 2cc, 2cc+1): gates, gated rows, their
@@ -360,7 +386,14 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float wv = row_val<TW>(rw, jt, e);
-          const float l2 = WLOG ? wv * 1.4426950408889634f : __builtin_amdgcn_logf(wv);
+          float l2;
+          if constexpr (WMODE == 1) {
+            l2 = wv * 1.4426950408889634f;
+          } else if constexpr (WMODE == 2) {
+            l2 = -0.87503927f / (1.0f + __expf(-wv));  // -0.606531 log2(e) sigmoid(w_raw)
+          } else {
+            l2 = __builtin_amdgcn_logf(wv);
+          }
           g[e] = fmaxf(l2, lwlo);
         }
 #pragma unroll
@@ -380,6 +413,8 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
           xv[e] = row_val<TA>(rv, jt, e);
           const float gC = row_last(g[e]);  // the scan's last token: the chunk total
           gcv[e] = gC;
+          gmin = fminf(gmin, gC);
+          gmax = fmaxf(gmax, gC);
           const float cf = rintf(0.5f * gC);
           const int ci = (int)cf;
           const float xd = clamp126(g[e] - cf);
@@ -547,25 +582,25 @@ __global__ __launch_bounds__(512, 1) void wkv7_chunk_kernel(
     }
     set_flag(&L.ready[s], x);
   }
+  // |gC| <= 252 keeps every centred exponent (at most |gC| / 2 + 1/2) within +-126
+  const bool clamped = __builtin_amdgcn_ballot_w64(gmin < -252.f || gmax > 252.f) != 0;
+  post_status((waited_out ? WKV7_STATUS_TIMEOUT : 0) | (clamped ? WKV7_STATUS_CLAMPED : 0));
 }
 
 }  // namespace rwkv7mi
 
 using namespace rwkv7mi;
 
-template <typename TA, typename TW, bool WLOG>
+template <typename TA, typename TW, int WMODE>
 static int chunk_go(int64_t B, int64_t T, int64_t H, void* stream, const void* r, const void* w, const void* k,
                     const void* v, const void* kk, const void* a, const float* state_in, float* state_out,
                     void* y) {
-  static bool lds_raised = false;  // dynamic LDS above 64 KB must be enabled once per instance
+  static std::atomic<uint64_t> lds_raised{0};  // devices whose dynamic LDS limit is raised for this instance
   const size_t lds = sizeof(ChunkShared);
-  if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&wkv7_chunk_kernel<TA, TW, WLOG>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return fail(RWKV7MI_ELAUNCH, "wkv7_chunk_kernel: cannot raise the dynamic LDS limit");
-    lds_raised = true;
-  }
-  hipLaunchKernelGGL((wkv7_chunk_kernel<TA, TW, WLOG>), dim3((unsigned)(B * H)), dim3(512), lds, as_stream(stream),
+  if (int rc = raise_dynamic_lds(reinterpret_cast<const void*>(&wkv7_chunk_kernel<TA, TW, WMODE>), (int)lds,
+                                 lds_raised, "wkv7_chunk_kernel"))
+    return rc;
+  hipLaunchKernelGGL((wkv7_chunk_kernel<TA, TW, WMODE>), dim3((unsigned)(B * H)), dim3(512), lds, as_stream(stream),
                      (const TA*)r, (const TW*)w, (const TA*)k, (const TA*)v, (const TA*)kk, (const TA*)a, state_in,
                      state_out, (TA*)y, (int)T, (int)H);
   return check_launch("wkv7_chunk_kernel");
@@ -577,6 +612,7 @@ extern "C" int rwkv7mi_wkv7_chunk_prefill(const void* r, const void* w, const vo
                                           int64_t N, int64_t chunk, int w_is_log, int act_dtype,
                                           int w_dtype, void* stream) {
   if (N != HD) return fail(RWKV7MI_EINVAL, "wkv7 chunk: head size must be 64");
+  if (w_is_log < 0 || w_is_log > 2) return fail(RWKV7MI_EINVAL, "wkv7 chunk: w mode must be 0, 1 or 2");
   if (chunk != 16 && chunk != 32 && chunk != 64)
     return fail(RWKV7MI_EINVAL, "wkv7 chunk: chunk must be 16, 32 or 64");
   if (B < 0 || T < 0 || H <= 0) return fail(RWKV7MI_EINVAL, "wkv7 chunk: bad B/T/H");
@@ -597,8 +633,25 @@ extern "C" int rwkv7mi_wkv7_chunk_prefill(const void* r, const void* w, const vo
     if (al & 15) return fail(RWKV7MI_EINVAL, "wkv7 chunk: inputs must be 16-byte aligned");
     return dispatch_dtype(w_dtype, [&](auto tw) {
       using TW = decltype(tw);
-      if (w_is_log) return chunk_go<TA, TW, true>(B, T, H, stream, r, w, k, v, kk, a, state_in, state_out, y);
-      return chunk_go<TA, TW, false>(B, T, H, stream, r, w, k, v, kk, a, state_in, state_out, y);
+      if (w_is_log == 1) return chunk_go<TA, TW, 1>(B, T, H, stream, r, w, k, v, kk, a, state_in, state_out, y);
+      if (w_is_log == 2) return chunk_go<TA, TW, 2>(B, T, H, stream, r, w, k, v, kk, a, state_in, state_out, y);
+      return chunk_go<TA, TW, 0>(B, T, H, stream, r, w, k, v, kk, a, state_in, state_out, y);
     });
   });
+}
+
+extern "C" int rwkv7mi_wkv7_chunk_status(int clear, int* status) {
+  if (!status) return fail(RWKV7MI_EINVAL, "wkv7 chunk status: null output");
+  // every kernel issued so far on the device, on any stream, posts first
+  if (hipDeviceSynchronize() != hipSuccess) return fail(RWKV7MI_ELAUNCH, "wkv7 chunk status: device error");
+  if (hipMemcpyFromSymbol(status, HIP_SYMBOL(wkv7_chunk_status_word), sizeof(int), 0, hipMemcpyDeviceToHost) !=
+      hipSuccess)
+    return fail(RWKV7MI_ELAUNCH, "wkv7 chunk status: cannot read the status word");
+  if (clear) {
+    const int zero = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(wkv7_chunk_status_word), &zero, sizeof(int), 0, hipMemcpyHostToDevice) !=
+        hipSuccess)
+      return fail(RWKV7MI_ELAUNCH, "wkv7 chunk status: cannot clear the status word");
+  }
+  return RWKV7MI_OK;
 }

@@ -11,6 +11,9 @@ from .fused_recurrent_update import (
     fused_recurrent_output_prepare,
     fused_recurrent_output_prepare_raw,
     fused_recurrent_scan,
+    fused_recurrent_scan_clampw,
+    fused_recurrent_scan_output_prepare,
+    fused_recurrent_scan_state_prep,
     fused_recurrent_update,
 )
 from .self_chunk_rwkv7 import dplr_chunk_scan, self_chunk_rwkv7
@@ -23,6 +26,9 @@ __all__ = [
     "fused_recurrent_output_prepare",
     "fused_recurrent_output_prepare_raw",
     "fused_recurrent_scan",
+    "fused_recurrent_scan_clampw",
+    "fused_recurrent_scan_state_prep",
+    "fused_recurrent_scan_output_prepare",
     "self_chunk_rwkv7",
     "dplr_chunk_scan",
     "quantize_mm8",

@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "librwkv7mi.so"
 
 F32, F16, BF16 = 0, 1, 2
 EPI_NONE, EPI_RELU2, EPI_RESIDUAL = 0, 1, 2
+PREP_A_RAW, PREP_VGATE_RAW, PREP_W_DECAY = 1, 2, 4
 
 _DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -44,6 +45,7 @@ SIGNATURES = {
         _i32,
         [_c_p] * 9 + [_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_p],
     ),
+    "rwkv7mi_wkv7_chunk_status": (_i32, [_i32, ctypes.POINTER(_i32)]),
     "rwkv7mi_mm8_pack": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "rwkv7mi_mm8_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "rwkv7mi_mm8_matmul": (
@@ -88,7 +90,7 @@ SIGNATURES = {
     "rwkv7mi_seq_norm_mix": (_i32, [_c_p] * 7 + [_i64, _i64, _i64, _i64, _f32, _i32, _i32, _c_p]),
     "rwkv7mi_layer_norm": (_i32, [_c_p] * 4 + [_i64, _i64, _f32, _i32, _i32, _c_p]),
     "rwkv7mi_dense_multi": (_i32, [_c_p] * 7 + [_i64, _i64, _i32, _c_p]),
-    "rwkv7mi_state_prep": (_i32, [_c_p] * 11 + [_i64, _i64, _i64, _i32, _i32, _i32, _c_p]),
+    "rwkv7mi_state_prep": (_i32, [_c_p] * 12 + [_i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _c_p]),
     "rwkv7mi_output_prepare": (_i32, [_c_p] * 9 + [_i64, _i64, _i64, _f32, _i32, _i32, _c_p]),
 }
 

@@ -255,9 +255,134 @@ def fused_recurrent_scan(
     return y, final
 
 
+def _scan_checks(state, block_n, block_m, num_warps):
+    B, H, N = _check_state(state)
+    if int(block_n) < N:
+        raise ValueError(f"block_n must be >= head_dim={N}; got {block_n}")
+    if block_m is not None and not 0 < int(block_m) <= N:
+        raise ValueError(f"block_m must be in [1, head_dim={N}]; got {block_m}")
+    if num_warps is not None and int(num_warps) not in {1, 2, 4, 8}:
+        raise ValueError(f"num_warps must be one of 1, 2, 4, or 8; got {num_warps}")
+    return B, H, N
+
+
+def fused_recurrent_scan_clampw(
+    r: Any, w_raw: Any, k: Any, v: Any, kk: Any, a: Any, state: Any, *,
+    block_n: int = 64, block_m: int | None = None, num_warps: int | None = None,
+    force_fallback: bool = False, state_out: torch.Tensor | None = None,
+):
+    """Scan over ``[B,T,H,N]`` (or flat) inputs with the raw W pre-activation:
+    the decay ``exp(-0.606531 sigmoid(w_raw))`` is formed inside the chunk
+    kernel, so no decay tensor is written (rwkv7_hf/fused_recurrent_update.py:1420-1538).
+    Returns ``(out, final_state)``."""
+    from .self_chunk_rwkv7 import _run_chunk
+
+    B, H, N = _scan_checks(state, block_n, block_m, num_warps)
+    r4, flat = _as_bthn(r, H, N, name="r")
+    w4, _ = _as_bthn(w_raw, H, N, name="w_raw")
+    k4, _ = _as_bthn(k, H, N, name="k")
+    v4, _ = _as_bthn(v, H, N, name="v")
+    kk4, _ = _as_bthn(kk, H, N, name="kk")
+    a4, _ = _as_bthn(a, H, N, name="a")
+    if int(r4.shape[0]) != B:
+        raise ValueError("r/w/k/v/kk/a batch size must match state")
+    _same_dtype(r4, w4, k4, v4, kk4, a4, name="fused_recurrent_scan_clampw")
+    y, final = _run_chunk(r4, w4, k4, v4, kk4, a4, state, w_is_log=2, chunk=16, state_out=state_out)
+    if flat:
+        return y.reshape(B, int(r4.shape[1]), H * N), final
+    return y, final
+
+
+def fused_recurrent_scan_state_prep(
+    r: Any, w_raw: Any, k_raw: Any, v_raw: Any, a: Any, state: Any, k_k: Any, k_a: Any, *,
+    v_first: Any | None = None, v_gate: Any | None = None, block_n: int = 64,
+    block_m: int | None = None, num_warps: int | None = None, force_fallback: bool = False,
+    state_out: torch.Tensor | None = None,
+):
+    """State prep fused in front of the scan (rwkv7_hf/fused_recurrent_update.py:1541-1707):
+    ``kk = normalize(k_raw * k_k)``, ``k = k_raw (1 + (a - 1) k_a)``,
+    ``v = v_raw + (v_first - v_raw) v_gate`` when both are given, decay from
+    ``w_raw`` — ``a`` and ``v_gate`` already sigmoid'd.  Two launches: the prep
+    kernel (the log decay in fp32) and the chunk kernel.  Returns
+    ``(out, final_state, k_adjusted, v_interpolated)`` in the input layout."""
+    from .fused_prefill import fused_prefill_state_prep
+    from .self_chunk_rwkv7 import _run_chunk
+
+    B, H, N = _scan_checks(state, block_n, block_m, num_warps)
+    r4, flat = _as_bthn(r, H, N, name="r")
+    w4, _ = _as_bthn(w_raw, H, N, name="w_raw")
+    k4, _ = _as_bthn(k_raw, H, N, name="k_raw")
+    v4, _ = _as_bthn(v_raw, H, N, name="v_raw")
+    a4, _ = _as_bthn(a, H, N, name="a")
+    if int(r4.shape[0]) != B:
+        raise ValueError("r/w/k/v/a batch size must match state")
+    hidden = H * N
+    if int(k_k.numel()) != hidden or int(k_a.numel()) != hidden:
+        raise ValueError(f"k_k and k_a must have {hidden} elements")
+    has_v_gate = v_first is not None and v_gate is not None
+    vf = vg = None
+    if has_v_gate:
+        vf, _ = _as_bthn(v_first, H, N, name="v_first")
+        vg, _ = _as_bthn(v_gate, H, N, name="v_gate")
+    _same_dtype(r4, w4, k4, v4, a4, name="fused_recurrent_scan_state_prep")
+    T = int(r4.shape[1])
+    w_log, k_adj, v_adj, kk = fused_prefill_state_prep(
+        w4, k4, v4, a4, k_k, k_a, v_first=None if vf is None else vf.to(r4.dtype).contiguous(), v_gate=vg,
+        num_heads=H, head_dim=N, w_transform="log_decay", v_mode=2 if has_v_gate else 0)
+    y, final = _run_chunk(r4, w_log, k_adj, v_adj, kk, a4, state, w_is_log=1, chunk=16, state_out=state_out)
+    if flat:
+        return (y.reshape(B, T, hidden), final, k_adj.reshape(B, T, hidden), v_adj.reshape(B, T, hidden))
+    return y, final, k_adj, v_adj
+
+
+def fused_recurrent_scan_output_prepare(
+    r: Any, w: Any, k: Any, v: Any, kk: Any, a: Any, state: Any, g: Any, r_k: Any,
+    group_norm_weight: Any, group_norm_bias: Any, *, eps: float, block_n: int = 64,
+    force_fallback: bool = False, state_out: torch.Tensor | None = None,
+):
+    """Scan followed by the attention output prep (per-head GroupNorm, bonus
+    ``(sum r k r_k) v`` and gate ``g``; rwkv7_hf/fused_recurrent_update.py:1710-1833).
+    ``w`` is the decay in the activation dtype or fp32.  Two launches: the
+    chunk kernel and the output-prep kernel.  Returns ``(prepared, final_state)``
+    with ``prepared`` ready for ``o_proj``."""
+    from .fused_output import fused_attn_output_prepare
+    from .self_chunk_rwkv7 import _run_chunk
+
+    B, H, N = _scan_checks(state, block_n, None, None)
+    r4, flat = _as_bthn(r, H, N, name="r")
+    w4, _ = _as_bthn(w, H, N, name="w")
+    k4, _ = _as_bthn(k, H, N, name="k")
+    v4, _ = _as_bthn(v, H, N, name="v")
+    kk4, _ = _as_bthn(kk, H, N, name="kk")
+    a4, _ = _as_bthn(a, H, N, name="a")
+    g4, _ = _as_bthn(g, H, N, name="g")
+    if int(r4.shape[0]) != B:
+        raise ValueError("r/w/k/v/kk/a/g batch size must match state")
+    if r_k.dim() != 2 or int(r_k.shape[0]) != H or int(r_k.shape[1]) != N:
+        raise ValueError(f"r_k must be [{H}, {N}], got {tuple(r_k.shape)}")
+    if group_norm_weight.dim() != 1 or int(group_norm_weight.shape[0]) != H * N:
+        raise ValueError(f"group_norm_weight must be [{H * N}], got {tuple(group_norm_weight.shape)}")
+    if group_norm_bias.dim() != 1 or int(group_norm_bias.shape[0]) != H * N:
+        raise ValueError(f"group_norm_bias must be [{H * N}], got {tuple(group_norm_bias.shape)}")
+    _same_dtype(r4, k4, v4, kk4, a4, g4, name="fused_recurrent_scan_output_prepare")
+    if w4.dtype not in (r4.dtype, torch.float32):
+        raise ValueError("w must be in the activation dtype or float32")
+    T, A = int(r4.shape[1]), H * N
+    y, final = _run_chunk(r4, w4, k4, v4, kk4, a4, state, w_is_log=0, chunk=16, state_out=state_out)
+    prep = fused_attn_output_prepare(y.reshape(B * T, A), r4.reshape(B * T, A), k4.reshape(B * T, A),
+                                     v4.reshape(B * T, A), g4.reshape(B * T, A), r_k, group_norm_weight,
+                                     group_norm_bias, num_heads=H, head_dim=N, head_v_dim=N, eps=eps)
+    if flat:
+        return prep.reshape(B, T, A), final
+    return prep.reshape(B, T, H, N), final
+
+
 __all__ = [
     "fused_recurrent_update",
     "fused_recurrent_output_prepare",
     "fused_recurrent_output_prepare_raw",
     "fused_recurrent_scan",
+    "fused_recurrent_scan_clampw",
+    "fused_recurrent_scan_state_prep",
+    "fused_recurrent_scan_output_prepare",
 ]

@@ -16,6 +16,7 @@ library GEMM that follows an MM8 dequantisation (rocBLAS through torch).
 """
 from __future__ import annotations
 
+import weakref
 import zlib
 from dataclasses import dataclass, field
 
@@ -235,35 +236,145 @@ class QuantLinear:
 
 
 # ------------------------------------------------------------------ cache
-class NativeRWKV7Cache:
-    """Recurrent-state cache with the reference's contract (rwkv7_hf/model_cache.py:48).
+try:  # the HF Cache base lets GenerationMixin / Trainer accept the cache
+    from transformers.cache_utils import Cache as _HFCache
+except Exception:  # pragma: no cover - transformers absent
+    class _HFCache:  # type: ignore[no-redef]
+        pass
 
-    Iterable as ``(state, xpa, xpf, v_first)``; ``state[l]`` is ``[B,H,N,N]`` fp32.
+
+class _LegacyCache(tuple):
+    """Tuple ``(state, xpa, xpf, v_first)`` that remembers the sequence length
+    (the reference's legacy form, rwkv7_hf/model_cache.py:16-45)."""
+
+    def __new__(cls, state, xpa, xpf, v_first, seen_tokens: int = 0):
+        obj = super().__new__(cls, (state, xpa, xpf, v_first))
+        obj._seen_tokens = int(seen_tokens)
+        return obj
+
+    def get_seq_length(self, layer_idx: int | None = 0, cache_position=None) -> int:
+        n = 0 if self[0] is None else len(self[0])
+        if layer_idx is not None and (int(layer_idx) < 0 or (self[0] is not None and int(layer_idx) >= n)
+                                      or (self[0] is None and int(layer_idx) != 0)):
+            return 0
+        return self._seen_tokens
+
+    @property
+    def seen_tokens(self) -> int:
+        return self._seen_tokens
+
+    def to_legacy_cache(self):
+        return self
+
+
+_METRIC_KEYS = ("clones", "detaches", "device_moves", "select_batch_calls", "batch_select_calls",
+                "batch_select_indices_calls", "batch_repeat_interleave_calls", "reorder_calls", "crops", "resets",
+                "native_graph_bound_selects")
+
+
+class NativeRWKV7Cache(_HFCache):
+    """Recurrent-state cache with the reference's contract (rwkv7_hf/model_cache.py:48-466).
+
+    Holds ``(state, xpa, xpf, v_first)``: per-layer ``state[l] [B, H, N, N]``
+    fp32 (value x key), per-layer token-shift rows ``xpa[l]``, ``xpf[l]``
+    ``[B, D]`` and the cross-layer ``v_first [B, A]``, plus ``seen_tokens``.
+    Iterable as that 4-tuple.  Batch edits (select / reorder / repeat), device
+    moves, detach, crop-to-empty and legacy-tuple conversion follow the
+    reference.  A graph runner that replays the decode step binds the cache
+    (its tensors become the runner's buffers); any edit that replaces the
+    tensors bumps the cache version, which unbinds it, and a batch reorder of a
+    bound cache permutes the runner's buffers in place instead.
     """
 
+    is_compileable = True
+
     def __init__(self, state=None, xpa=None, xpf=None, v_first=None, seen_tokens: int = 0):
+        # (the HF base initialiser builds KV layer objects a recurrent cache does not use)
         self._state, self._xpa, self._xpf, self._v_first = state, xpa, xpf, v_first
         self._seen_tokens = int(seen_tokens)
+        self.layers = []
+        self._rwkv7_cache_metrics = {k: 0 for k in _METRIC_KEYS}
         self._rwkv7_cache_version = 0
-        self._bound_runner = None
+        self._bound_runner_ref = None
+        self._bound_version = None
 
     @classmethod
-    def zeros(cls, cfg: NativeRWKV7Config, batch: int, device, dtype=torch.float16):
+    def zeros(cls, cfg: "NativeRWKV7Config", batch: int, device, dtype=torch.float16):
         H, N, D, A, L = cfg.num_heads, cfg.head_dim, cfg.hidden_size, cfg.attention_hidden_size, cfg.num_hidden_layers
         return cls([torch.zeros(batch, H, N, N, device=device, dtype=torch.float32) for _ in range(L)],
                    [torch.zeros(batch, D, device=device, dtype=dtype) for _ in range(L)],
                    [torch.zeros(batch, D, device=device, dtype=dtype) for _ in range(L)],
                    torch.zeros(batch, A, device=device, dtype=dtype), 0)
 
+    # ---- graph binding / version protocol (rwkv7_hf/model_cache.py:89-114)
+    def _invalidate_native_graph_binding(self) -> None:
+        self._rwkv7_cache_version += 1
+        self._bound_runner_ref = None
+        self._bound_version = None
+
+    _invalidate = _invalidate_native_graph_binding
+
+    def _bind_native_graph_runner(self, runner) -> None:
+        self._bound_runner_ref = weakref.ref(runner)
+        self._bound_version = self._rwkv7_cache_version
+
+    def _native_graph_bound_runner(self):
+        if self._bound_version != self._rwkv7_cache_version or self._bound_runner_ref is None:
+            return None
+        return self._bound_runner_ref()
+
+    def _native_graph_bound_to(self, runner) -> bool:
+        return runner is not None and self._native_graph_bound_runner() is runner
+
+    @property
+    def _bound_runner(self):
+        return self._native_graph_bound_runner()
+
+    # ---- tuple view
+    def __repr__(self) -> str:
+        return (f"{type(self).__name__}(seen_tokens={self._seen_tokens}, batch_size={self.get_batch_size()}, "
+                f"layers={0 if self._state is None else len(self._state)})")
+
     def __iter__(self):
         return iter((self._state, self._xpa, self._xpf, self._v_first))
 
-    def __len__(self):
-        return 0 if self._state is None else len(self._state)
+    def __len__(self) -> int:
+        return 4
 
     def __getitem__(self, idx):
-        return (self._state[idx], self._xpa[idx], self._xpf[idx], self._v_first)
+        return self.to_legacy_cache()[idx]
 
+    def to_legacy_cache(self):
+        return _LegacyCache(self._state, self._xpa, self._xpf, self._v_first, seen_tokens=self._seen_tokens)
+
+    @classmethod
+    def from_legacy_cache(cls, legacy, seen_tokens: int = 0):
+        """A cache from None, an empty cache, a cache of this class or a 4-tuple."""
+        if legacy is None:
+            return cls(seen_tokens=seen_tokens)
+        if isinstance(legacy, NativeRWKV7Cache):
+            return legacy
+        seen = int(seen_tokens)
+        if hasattr(legacy, "get_seq_length"):
+            try:
+                n = int(legacy.get_seq_length())
+            except Exception:
+                n = None
+            if n == 0:
+                return cls(seen_tokens=seen_tokens)
+            if n is not None:
+                seen = n
+        if hasattr(legacy, "to_legacy_cache"):
+            legacy = legacy.to_legacy_cache()
+        if legacy is None or (isinstance(legacy, (list, tuple)) and len(legacy) == 0):
+            return cls(seen_tokens=seen_tokens)
+        if not isinstance(legacy, (list, tuple)) or len(legacy) != 4:
+            raise TypeError("NativeRWKV7Cache.from_legacy_cache expects None, an empty cache, or a 4-tuple "
+                            "recurrent cache")
+        state, xpa, xpf, v_first = legacy
+        return cls(state, xpa, xpf, v_first, seen_tokens=seen)
+
+    # ---- sizes
     @property
     def seen_tokens(self) -> int:
         return self._seen_tokens
@@ -272,56 +383,282 @@ class NativeRWKV7Cache:
     def seen_tokens(self, value: int) -> None:
         self._seen_tokens = int(value)
 
+    def _is_initialized(self, layer_idx: int | None = None) -> bool:
+        if any(t is None for t in (self._state, self._xpa, self._xpf, self._v_first)):
+            return False
+        return layer_idx is None or 0 <= int(layer_idx) < len(self._state)
+
+    @property
+    def is_initialized(self) -> bool:
+        return self._is_initialized()
+
+    @property
+    def is_sliding(self) -> bool:
+        return False
+
+    @property
+    def max_batch_size(self) -> int | None:
+        return self.get_batch_size()
+
+    @property
+    def max_cache_len(self) -> int:
+        return -1
+
+    @property
+    def states(self) -> list[dict]:
+        """Per-layer dict view (recurrent_state / attn_state / ffn_state)."""
+        if self._state is None:
+            return []
+        return [{"recurrent_state": s, "attn_state": a, "conv_state": None, "ffn_state": f}
+                for s, a, f in zip(self._state, self._xpa, self._xpf)]
+
     def get_seq_length(self, layer_idx: int | None = 0, cache_position=None) -> int:
+        if layer_idx is not None:
+            li = int(layer_idx)
+            if li < 0 or (self._state is not None and li >= len(self._state)) or (self._state is None and li != 0):
+                return 0
         return self._seen_tokens
 
+    def get_max_cache_shape(self, layer_idx: int = 0) -> int:
+        return -1
+
+    def get_mask_sizes(self, cache_position, layer_idx: int = 0) -> tuple[int, int]:
+        if cache_position is None:
+            q = 0
+        elif isinstance(cache_position, torch.Tensor):
+            q = int(cache_position.numel())
+        else:
+            q = int(cache_position)
+        return self.get_seq_length(layer_idx) + q, 0
+
     def get_batch_size(self) -> int | None:
+        for values in (self._state, self._xpa, self._xpf):
+            if values:
+                return int(values[0].shape[0])
         return None if self._v_first is None else int(self._v_first.shape[0])
 
-    def is_initialized(self) -> bool:
-        return self._state is not None
+    def has_previous_state(self, layer_idx: int | None = None) -> bool:
+        return self._is_initialized(layer_idx) and self._seen_tokens > 0
 
-    def _invalidate(self):
-        self._rwkv7_cache_version += 1
-        self._bound_runner = None
+    # ---- edits
+    def _map(self, fn):
+        self._state = None if self._state is None else [fn(t) for t in self._state]
+        self._xpa = None if self._xpa is None else [fn(t) for t in self._xpa]
+        self._xpf = None if self._xpf is None else [fn(t) for t in self._xpf]
+        self._v_first = None if self._v_first is None else fn(self._v_first)
 
     def clone(self) -> "NativeRWKV7Cache":
-        c = NativeRWKV7Cache([s.clone() for s in self._state], [x.clone() for x in self._xpa],
-                             [x.clone() for x in self._xpf], self._v_first.clone(), self._seen_tokens)
-        return c
+        out = type(self)(seen_tokens=self._seen_tokens)
+        out._state, out._xpa, out._xpf, out._v_first = self._state, self._xpa, self._xpf, self._v_first
+        out._map(lambda t: t.clone())
+        out._rwkv7_cache_metrics = dict(self._rwkv7_cache_metrics)
+        out._rwkv7_cache_metrics["clones"] += 1
+        return out
 
     def reset(self) -> None:
-        for t in (*self._state, *self._xpa, *self._xpf, self._v_first):
-            t.zero_()
+        """Drop the state (the reference's reset: the next forward starts fresh)."""
+        self._invalidate_native_graph_binding()
+        self._state = self._xpa = self._xpf = self._v_first = None
         self._seen_tokens = 0
-        self._invalidate()
+        self._rwkv7_cache_metrics["resets"] += 1
 
-    def to(self, device=None, dtype=None) -> "NativeRWKV7Cache":
-        self._state = [s.to(device) for s in self._state]
-        self._xpa = [x.to(device=device, dtype=dtype or x.dtype) for x in self._xpa]
-        self._xpf = [x.to(device=device, dtype=dtype or x.dtype) for x in self._xpf]
-        self._v_first = self._v_first.to(device=device, dtype=dtype or self._v_first.dtype)
-        self._invalidate()
+    def zero_(self) -> "NativeRWKV7Cache":
+        """Zero the state in place, keeping the tensors (and any graph binding)."""
+        for t in (*(self._state or ()), *(self._xpa or ()), *(self._xpf or ())):
+            t.zero_()
+        if self._v_first is not None:
+            self._v_first.zero_()
+        self._seen_tokens = 0
         return self
 
-    def select_batch(self, indices: torch.LongTensor, *, inplace: bool = True) -> "NativeRWKV7Cache":
-        idx = indices.to(self._v_first.device)
-        target = self if inplace else NativeRWKV7Cache(seen_tokens=self._seen_tokens)
-        target._state = [s.index_select(0, idx) for s in self._state]
-        target._xpa = [x.index_select(0, idx) for x in self._xpa]
-        target._xpf = [x.index_select(0, idx) for x in self._xpf]
-        target._v_first = self._v_first.index_select(0, idx)
-        target._invalidate()
+    def detach(self, *, inplace: bool = True) -> "NativeRWKV7Cache":
+        target = self if inplace else self.clone()
+        target._invalidate_native_graph_binding()
+        target._map(lambda t: t.detach())
+        target._rwkv7_cache_metrics["detaches"] += 1
         return target
 
-    reorder_cache = select_batch
+    def to(self, device=None, dtype=None, *, non_blocking: bool = False, copy: bool = False,
+           inplace: bool = True) -> "NativeRWKV7Cache":
+        """Move the cache; ``dtype`` applies to the token-shift rows and
+        ``v_first`` (the recurrent state stays fp32, as the kernels require)."""
+        target = self if inplace else self.clone()
+        target._invalidate_native_graph_binding()
+
+        def move(t, is_state=False):
+            kw = {"non_blocking": non_blocking, "copy": copy}
+            if device is not None:
+                kw["device"] = device
+            if dtype is not None and t.is_floating_point() and not is_state:
+                kw["dtype"] = dtype
+            if len(kw) == 2:
+                return t.clone() if copy else t
+            return t.to(**kw)
+
+        if target._state is not None:
+            target._state = [move(t, True) for t in target._state]
+        target._xpa = None if target._xpa is None else [move(t) for t in target._xpa]
+        target._xpf = None if target._xpf is None else [move(t) for t in target._xpf]
+        target._v_first = None if target._v_first is None else move(target._v_first)
+        target._rwkv7_cache_metrics["device_moves"] += 1
+        return target
+
+    def select_batch(self, indices, *, inplace: bool = True) -> "NativeRWKV7Cache":
+        idx = torch.as_tensor(indices).to(dtype=torch.long)
+        if inplace:
+            target = self
+        else:
+            target = type(self)(self._state, self._xpa, self._xpf, self._v_first, seen_tokens=self._seen_tokens)
+            target._rwkv7_cache_metrics = dict(self._rwkv7_cache_metrics)
+        runner = target._native_graph_bound_runner() if inplace else None
+        if runner is not None and target.get_batch_size() == int(idx.numel()) and runner.reorder_batch_inplace(idx):
+            target._rwkv7_cache_metrics["select_batch_calls"] += 1
+            target._rwkv7_cache_metrics["native_graph_bound_selects"] += 1
+            return target
+        target._invalidate_native_graph_binding()
+        target._map(lambda t: t.index_select(0, idx.to(t.device)))
+        target._rwkv7_cache_metrics["select_batch_calls"] += 1
+        return target
+
+    def batch_select(self, indices, *, inplace: bool = True) -> "NativeRWKV7Cache":
+        target = self.select_batch(indices, inplace=inplace)
+        target._rwkv7_cache_metrics["batch_select_calls"] += 1
+        return target
+
+    def compact(self, indices, *, inplace: bool = True) -> "NativeRWKV7Cache":
+        return self.batch_select(indices, inplace=inplace)
+
+    def batch_select_indices(self, indices):
+        target = self.select_batch(indices, inplace=True)
+        target._rwkv7_cache_metrics["batch_select_indices_calls"] += 1
+        return target
+
+    def reorder_cache(self, beam_idx):
+        target = self.select_batch(beam_idx, inplace=True)
+        target._rwkv7_cache_metrics["reorder_calls"] += 1
+        return target
 
     def batch_repeat_interleave(self, repeats: int):
-        self._state = [s.repeat_interleave(repeats, 0) for s in self._state]
-        self._xpa = [x.repeat_interleave(repeats, 0) for x in self._xpa]
-        self._xpf = [x.repeat_interleave(repeats, 0) for x in self._xpf]
-        self._v_first = self._v_first.repeat_interleave(repeats, 0)
-        self._invalidate()
+        repeats = int(repeats)
+        if repeats <= 0:
+            raise ValueError("NativeRWKV7Cache.batch_repeat_interleave requires repeats > 0")
+        self._invalidate_native_graph_binding()
+        self._map(lambda t: t.repeat_interleave(repeats, dim=0))
+        self._rwkv7_cache_metrics["batch_repeat_interleave_calls"] += 1
+        return self
+
+    def crop(self, max_length: int):
+        """Only a no-op crop or a crop to nothing is possible for a recurrent state."""
+        max_length = int(max_length)
+        target = self._seen_tokens + max_length if max_length < 0 else max_length
+        if target >= self._seen_tokens:
+            return self
+        if target <= 0:
+            self._rwkv7_cache_metrics["crops"] += 1
+            self.reset()
+            return self
+        raise NotImplementedError("NativeRWKV7Cache cannot crop recurrent state to a shorter positive prefix; "
+                                  "run a fresh prefill for that prefix instead.")
+
+    def rwkv7_cache_metrics(self) -> dict:
+        m = dict(self._rwkv7_cache_metrics)
+        m.update({"seen_tokens": self._seen_tokens, "batch_size": self.get_batch_size(),
+                  "layers": 0 if self._state is None else len(self._state)})
+        return m
+
+    # ---- KV-cache hooks a recurrent cache does not have
+    def update(self, *args, **kwargs):
+        raise NotImplementedError("NativeRWKV7Cache is not a Transformer KV cache; update it through "
+                                  "NativeRWKV7ForCausalLM.forward(..., past_key_values=...).")
+
+    def update_recurrent_state(self, *args, **kwargs):
+        raise NotImplementedError("NativeRWKV7Cache stores RWKV-7 state as (state, xpa, xpf, v_first); "
+                                  "update it through NativeRWKV7ForCausalLM.forward(..., past_key_values=...).")
+
+    def update_conv_state(self, *args, **kwargs):
+        raise NotImplementedError("NativeRWKV7Cache does not have convolution state.")
+
+    def update_indexer(self, *args, **kwargs):
+        raise NotImplementedError("NativeRWKV7Cache does not have an indexer key cache.")
+
+    def early_initialization(self, *args, **kwargs):
+        raise NotImplementedError("NativeRWKV7Cache cannot be early-initialized as a Transformer KV cache.")
+
+    def offload(self, *args, **kwargs):
+        raise NotImplementedError("Use NativeRWKV7Cache.to(device='cpu') to offload native recurrent state.")
+
+    def prefetch(self, *args, **kwargs):
+        raise NotImplementedError("Use NativeRWKV7Cache.to(device=...) to restore native recurrent state.")
+
+
+
+# ------------------------------------------------------------------ forward helpers
+try:
+    from transformers.modeling_outputs import CausalLMOutputWithPast as _CausalLMOutput
+except Exception:  # pragma: no cover - transformers absent
+    @dataclass
+    class _CausalLMOutput:  # type: ignore[no-redef]
+        loss: torch.Tensor | None = None
+        logits: torch.Tensor | None = None
+        past_key_values: object = None
+
+
+def _as_native_cache(past_key_values) -> NativeRWKV7Cache | None:
+    """The native cache behind ``past_key_values``; None for no (or an empty) cache
+    (rwkv7_hf/model_cache.py:480-504)."""
+    if past_key_values is None:
+        return None
+    if isinstance(past_key_values, NativeRWKV7Cache):
+        return past_key_values if (past_key_values.is_initialized or past_key_values.seen_tokens) else None
+    try:
+        values = tuple(past_key_values)
+    except Exception as exc:
+        seen = getattr(past_key_values, "get_seq_length", lambda: 0)()
+        if not seen:
+            return None
+        raise TypeError(f"Unsupported NativeRWKV7 cache type: {type(past_key_values)!r}") from exc
+    if len(values) == 4 and all(v is not None for v in values):
+        return NativeRWKV7Cache.from_legacy_cache(past_key_values)
+    if not getattr(past_key_values, "get_seq_length", lambda: 0)():
+        return None
+    raise TypeError(f"NativeRWKV7 expects a NativeRWKV7Cache or 4-tuple recurrent cache; got "
+                    f"{type(past_key_values)!r} with length {len(values)}")
+
+
+def _check_attention_mask(mask, B: int, T: int, *, allow_trailing: bool) -> None:
+    """All-ones masks are the same as none (rwkv7_hf/model_backbone.py:28-62);
+    a mask that drops tokens has no native route here."""
+    if mask is None:
+        return
+    if not isinstance(mask, torch.Tensor):
+        raise TypeError("NativeRWKV7 attention_mask must be a torch.Tensor when provided")
+    if mask.dim() == 1:
+        mask = mask.view(1, -1)
+    if mask.dim() != 2 or int(mask.shape[0]) != B:
+        raise ValueError("NativeRWKV7 attention_mask must be shaped [batch, seq]")
+    if int(mask.shape[1]) != T:
+        if not allow_trailing or int(mask.shape[1]) < T:
+            raise ValueError("NativeRWKV7 attention_mask must have the same [batch, seq] shape as inputs")
+        mask = mask[:, -T:]
+    if not bool((mask != 0).all()):
+        raise ValueError("rwkv7mi: attention masks that drop tokens are not supported on the native routes "
+                         "(RWKV state is order-sensitive; pass unpadded rows)")
+
+
+def _resolve_logits_to_keep(logits_to_keep, num_logits_to_keep):
+    if logits_to_keep is None:
+        return None if num_logits_to_keep is None else int(num_logits_to_keep)
+    if num_logits_to_keep is not None and int(num_logits_to_keep) != int(logits_to_keep):
+        raise ValueError("logits_to_keep and num_logits_to_keep must match when both are provided")
+    if isinstance(logits_to_keep, torch.Tensor) and logits_to_keep.dim() > 0:
+        raise ValueError("rwkv7mi: logits_to_keep must be an integer (position lists are not supported)")
+    return int(logits_to_keep)
+
+
+def _slice_logits(logits: torch.Tensor, keep):
+    if keep is None or int(keep) <= 0:
+        return logits
+    return logits[:, -min(int(keep), int(logits.shape[1])):, :]
 
 
 # ------------------------------------------------------------------ model
@@ -409,12 +746,6 @@ class NativeRWKV7ForCausalLM:
 
     def reserve_workspace(self, rows: int) -> None:
         """Grow the per-device scratch slots for ``rows``-row decode steps (before capture)."""
-        need = 0
-        for lin in self._linears():
-            if isinstance(lin, QuantLinear):
-                need = max(need, lin.m.rwkv7_workspace_bytes(min(rows, 64)))
-        if need:
-            _ws.reserve(self.device, need)
         if QuantLinear.GEMV_ROWS < rows <= QuantLinear.GEMM_ROWS:
             gneed = 0
             for L in self.layers:
@@ -587,17 +918,25 @@ class NativeRWKV7ForCausalLM:
         return self._side_streams[key]
 
     # ------------------------------------------------------------- prefill
-    def prefill_(self, input_ids: torch.Tensor, cache: NativeRWKV7Cache) -> torch.Tensor:
-        """Run ``input_ids [B, T]`` through every layer (chunked scan), update the cache,
-        return the last token's logits ``[B, V]``."""
+    def prefill_(self, input_ids: torch.Tensor | None, cache: NativeRWKV7Cache, *, logits_to_keep: int = 1,
+                 inputs_embeds: torch.Tensor | None = None) -> torch.Tensor:
+        """Run ``input_ids [B, T]`` (or ``inputs_embeds [B, T, D]``) through every
+        layer (chunked scan), update the cache in place, and return the logits of
+        the last ``logits_to_keep`` tokens ``[B, keep, V]`` (all T for
+        ``logits_to_keep <= 0``), as the reference's prefill tail
+        (rwkv7_hf/native_jit_prefill.py:1024-1036)."""
         cfg = self.config
-        B, T = (int(s) for s in input_ids.shape)
         dev, dt = self.device, self.dtype
         D, A, H, N, F, eps = (cfg.hidden_size, cfg.attention_hidden_size, cfg.num_heads, cfg.head_dim,
                               cfg.intermediate_size, cfg.norm_eps)
+        if inputs_embeds is not None:
+            B, T = (int(s) for s in inputs_embeds.shape[:2])
+            x = inputs_embeds.to(device=dev, dtype=dt).contiguous().clone()
+        else:
+            B, T = (int(s) for s in input_ids.shape)
+            x = torch.nn.functional.embedding(input_ids.reshape(-1), self.emb).reshape(B, T, D).contiguous()
         R = B * T
         state, xpa, xpf, v_first = cache
-        x = torch.nn.functional.embedding(input_ids.reshape(-1), self.emb).reshape(B, T, D).contiguous()
         mixb = torch.empty(6, B, T, D, device=dev, dtype=dt)
         rkv = torch.empty(3, R, A, device=dev, dtype=dt)
         lora = torch.empty(4, R, A, device=dev, dtype=dt)
@@ -613,17 +952,15 @@ class NativeRWKV7ForCausalLM:
                                                              norm_bias=L.ln1[1], eps=eps, workspace=mixb)
             xpa[i].copy_(new_prev)
             xr, xw, xk, xv, xa, xg = (m.reshape(R, D) for m in mixes)
-            L.r_proj.apply(xr, rkv[0])
-            L.k_proj.apply(xk, rkv[1])
-            L.v_proj.apply(xv, rkv[2])
+            QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
             self._lora(L, xw, xa, xg, xv, R, [lora[q] for q in range(4)], mids)
             w_log, k_adj, v_int, kk = fused_prefill_state_prep(
                 lora[0], rkv[1], rkv[2], lora[1], L.k_k, L.k_a, v_first=vfirst_seq,
-                v_gate=lora[3] if i > 0 else None, num_heads=H, head_dim=N, w_transform="log",
-                v_mode=1 if i == 0 else 2)
+                v_gate=lora[3] if i > 0 else None, num_heads=H, head_dim=N, w_transform="log_decay",
+                v_mode=1 if i == 0 else 2, v_out=rkv[2])
             shp = (B, T, H, N)
             y, _ = _run_chunk(rkv[0].view(shp), w_log.view(shp), k_adj.view(shp), v_int.view(shp), kk.view(shp),
-                              lora[1].view(shp), state[i], w_is_log=True, chunk=16, state_out=state[i])
+                              lora[1].view(shp), state[i], w_is_log=1, chunk=16, state_out=state[i])
             prep = fused_attn_output_prepare(y.view(R, A), rkv[0], k_adj, v_int, lora[2], L.r_k, L.gn[0], L.gn[1],
                                              num_heads=H, head_dim=N, head_v_dim=N, eps=N * 1e-5)
             x2 = x.reshape(R, D)
@@ -634,28 +971,118 @@ class NativeRWKV7ForCausalLM:
             L.key.apply(fk.reshape(R, D), kf, act=3)
             L.value.apply(kf, x2, residual=x2)
         v_first.copy_(vfirst_seq.view(B, T, A)[:, -1])
-        h = layer_norm(x[:, -1].contiguous(), self.norm[0], self.norm[1], eps)
-        logits = torch.empty(B, cfg.vocab_size, device=dev, dtype=dt)
+        keep = T if logits_to_keep is None or int(logits_to_keep) <= 0 else min(int(logits_to_keep), T)
+        h = layer_norm(x[:, T - keep:].reshape(B * keep, D).contiguous(), self.norm[0], self.norm[1], eps)
+        logits = torch.empty(B * keep, cfg.vocab_size, device=dev, dtype=dt)
         self.lm_head.apply(h, logits)
         cache.seen_tokens = cache.seen_tokens + T
-        cache._invalidate()
-        return logits
+        cache._invalidate_native_graph_binding()
+        return logits.view(B, keep, cfg.vocab_size)
 
     # ------------------------------------------------------------- API
     @torch.no_grad()
-    def forward(self, input_ids: torch.Tensor, past_key_values: NativeRWKV7Cache | None = None, use_cache=True):
-        """Returns ``(logits [B, 1, V], cache)``; prefill for T > 1, one decode step for T == 1."""
-        B, T = (int(s) for s in input_ids.shape)
-        cache = past_key_values if past_key_values is not None else self.new_cache(B)
-        if T == 1:
-            self.reserve_workspace(B)
-            logits = torch.empty(B, self.config.vocab_size, device=self.device, dtype=self.dtype)
-            self.decode_step_(input_ids[:, 0].contiguous(), cache, logits)
-            cache.seen_tokens = cache.seen_tokens + 1
-            cache._invalidate()
+    def forward(self, input_ids: torch.Tensor | None = None, attention_mask=None, inputs_embeds=None,
+                past_key_values=None, use_cache: bool | None = None, output_hidden_states: bool | None = None,
+                output_attentions: bool | None = None, return_dict: bool | None = None, labels=None,
+                logits_to_keep=None, num_logits_to_keep=None, return_legacy_cache: bool | None = None,
+                use_graph: bool = True, **kwargs):
+        """The reference's ``NativeRWKV7ForCausalLM.forward`` contract
+        (rwkv7_hf/native_model.py:618-853) on the native routes only.
+
+        * Prefill (no cache, or a cache plus T > 1 tokens): chunked-scan prefill;
+          logits of the last ``logits_to_keep`` tokens (all tokens when it is
+          0, or when ``labels`` are given).
+        * Decode (a cache and T == 1): the hipGraph-captured step of
+          :class:`NativeGraphRunner` (``use_graph=False``: the same step eagerly).
+        * ``labels``: shifted cross-entropy over all tokens, ignore index -100,
+          no cache input (as the reference).
+        * ``attention_mask``: all-ones masks are accepted (equivalent to none);
+          a mask that drops tokens is refused with ``ValueError``: the native
+          routes do not skip recurrent updates per row.
+        * ``output_attentions`` / ``output_hidden_states``: refused (RWKV-7 has
+          no attention maps; hidden states are not kept on the native route).
+
+        Returns ``CausalLMOutputWithPast(loss, logits [B, keep, V], past_key_values)``,
+        or the tuple form when ``return_dict`` is False.
+        """
+        if input_ids is not None and inputs_embeds is not None:
+            raise ValueError("NativeRWKV7ForCausalLM accepts either input_ids or inputs_embeds, not both")
+        if input_ids is None and inputs_embeds is None:
+            raise ValueError("NativeRWKV7ForCausalLM requires input_ids or inputs_embeds")
+        if input_ids is not None and input_ids.dim() == 1:
+            input_ids = input_ids.view(1, -1)
+        if input_ids is not None and input_ids.dim() != 2:
+            raise ValueError("NativeRWKV7ForCausalLM expects input_ids shaped [batch, seq]")
+        if inputs_embeds is not None and (inputs_embeds.dim() != 3
+                                          or int(inputs_embeds.shape[-1]) != self.config.hidden_size):
+            raise ValueError("NativeRWKV7ForCausalLM expects inputs_embeds shaped [batch, seq, hidden]")
+        src = input_ids if input_ids is not None else inputs_embeds
+        B, T = int(src.shape[0]), int(src.shape[1])
+        if B <= 0 or T <= 0:
+            raise ValueError("NativeRWKV7ForCausalLM requires a non-empty batch and sequence")
+        if output_attentions:
+            raise ValueError("RWKV-7 has no attention weights to output")
+        if output_hidden_states:
+            raise ValueError("rwkv7mi's native routes do not keep per-layer hidden states")
+        cache = _as_native_cache(past_key_values)
+        if cache is not None and cache.get_batch_size() not in (None, B):
+            raise ValueError(f"NativeRWKV7 cache batch size must match inputs (cache batch="
+                             f"{cache.get_batch_size()}, input batch={B})")
+        _check_attention_mask(attention_mask, B, T, allow_trailing=cache is not None)
+        use_cache = True if use_cache is None else bool(use_cache)
+        return_dict = True if return_dict is None else bool(return_dict)
+        keep = _resolve_logits_to_keep(logits_to_keep, num_logits_to_keep)
+        loss = None
+        if labels is not None:
+            if labels.dim() == 1:
+                labels = labels.view(1, -1)
+            if tuple(labels.shape[:2]) != (B, T):
+                raise ValueError("NativeRWKV7ForCausalLM labels must have the same shape as inputs")
+            if cache is not None:
+                raise ValueError("NativeRWKV7ForCausalLM does not support labels with past_key_values")
+            keep = 0
+        ids = None if input_ids is None else input_ids.to(self.device)
+        if cache is not None and T == 1 and ids is not None:
+            if use_graph:
+                runner = self.graph_runner(B)
+                logits = runner.replay(ids[:, 0], cache).clone().unsqueeze(1)
+            else:
+                self.reserve_workspace(B)
+                lg = torch.empty(B, self.config.vocab_size, device=self.device, dtype=self.dtype)
+                self.decode_step_(ids[:, 0].contiguous(), cache, lg)
+                cache.seen_tokens = cache.seen_tokens + 1
+                cache._invalidate_native_graph_binding()
+                logits = lg.unsqueeze(1)
         else:
-            logits = self.prefill_(input_ids, cache)
-        return logits.unsqueeze(1), cache
+            if cache is None:
+                cache = self.new_cache(B)
+            elif not cache.is_initialized:
+                seen = cache.seen_tokens
+                fresh = self.new_cache(B)
+                cache._state, cache._xpa, cache._xpf, cache._v_first = fresh._state, fresh._xpa, fresh._xpf, fresh._v_first
+                cache.seen_tokens = seen
+            else:
+                # the prefill updates the state in place; a cache bound to a
+                # graph runner keeps its tensors (they are the runner's buffers)
+                pass
+            logits = self.prefill_(ids, cache, logits_to_keep=1 if keep is None else keep,
+                                   inputs_embeds=None if ids is not None else inputs_embeds)
+        if loss is None and labels is not None:
+            lab = labels.to(logits.device)
+            shift_logits = logits[:, :-1].float()
+            shift_labels = lab[:, 1:]
+            if shift_logits.numel() == 0 or not bool((shift_labels != -100).any()):
+                loss = logits.float().sum() * 0.0
+            else:
+                loss = torch.nn.functional.cross_entropy(shift_logits.reshape(-1, shift_logits.shape[-1]),
+                                                         shift_labels.reshape(-1), ignore_index=-100)
+        logits = _slice_logits(logits, keep)
+        out_cache = cache if use_cache else None
+        if out_cache is not None and return_legacy_cache is True:
+            out_cache = out_cache.to_legacy_cache()
+        if not return_dict:
+            return tuple(v for v in (loss, logits, out_cache) if v is not None)
+        return _CausalLMOutput(loss=loss, logits=logits, past_key_values=out_cache)
 
     __call__ = forward
 
@@ -670,7 +1097,8 @@ class NativeRWKV7ForCausalLM:
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, *, use_graph: bool = True):
         """Greedy generation; returns ``[B, T + max_new_tokens]``."""
         B = int(input_ids.shape[0])
-        logits, cache = self.forward(input_ids)
+        out0 = self.forward(input_ids)
+        logits, cache = out0.logits, out0.past_key_values
         nxt = logits[:, -1].float().argmax(-1)
         out = [input_ids, nxt[:, None]]
         runner = self.graph_runner(B) if use_graph else None
@@ -678,8 +1106,7 @@ class NativeRWKV7ForCausalLM:
             if runner is not None:
                 lg = runner.replay(nxt, cache)
             else:
-                lg, cache = self.forward(nxt[:, None], cache)
-                lg = lg[:, -1]
+                lg = self.forward(nxt[:, None], past_key_values=cache, use_graph=False).logits[:, -1]
             nxt = lg.float().argmax(-1)
             out.append(nxt[:, None])
         return torch.cat(out, 1)
@@ -738,12 +1165,26 @@ class NativeGraphRunner:
             dst.copy_(src)
 
     def bind_cache(self, cache: NativeRWKV7Cache) -> None:
+        """The cache's tensors become this runner's buffers (no copies per step)."""
         cache._state, cache._xpa, cache._xpf, cache._v_first = (
             list(self.cache._state), list(self.cache._xpa), list(self.cache._xpf), self.cache._v_first)
-        cache._bound_runner = self
+        cache._invalidate_native_graph_binding()
+        cache._bind_native_graph_runner(self)
+
+    def reorder_batch_inplace(self, indices: torch.Tensor) -> bool:
+        """Permute the bound batch rows in place (beam search on a bound cache)."""
+        idx = indices.to(device=self.model.device, dtype=torch.long)
+        if int(idx.numel()) != self.batch:
+            return False
+        s, a, f, v = self.cache
+        for t in (*s, *a, *f, v):
+            t.copy_(t.index_select(0, idx))
+        return True
 
     def replay(self, tokens: torch.Tensor, cache: NativeRWKV7Cache) -> torch.Tensor:
-        if cache._bound_runner is not self:
+        if cache.get_batch_size() not in (None, self.batch):
+            raise ValueError(f"graph runner for batch {self.batch} got a cache of batch {cache.get_batch_size()}")
+        if not cache._native_graph_bound_to(self):
             self._copy_into(cache)
             self.bind_cache(cache)
         self.tokens.copy_(tokens.reshape(-1))

@@ -330,6 +330,32 @@ def mm8_lnmix_multi_into(x, prev, ln_w, ln_b, eps: float, mixes, mods, outs, *, 
     return outs
 
 
+def dequantize_mm8(w_u8, mx, rx, my, ry, out_dtype=None):
+    """The dequantised weight ``[N, M]``: ``(w + 0.5) ry rx + my + mx`` in
+    ``out_dtype`` (default: the metadata dtype), rwkv7_hf/native_quant_mm8.py:100-108.
+    One HIP pass in fp32 with a single rounding.  ``w_u8`` is the reference's
+    contiguous ``[N, M]`` bytes or the blocked decode layout (the result is then
+    the ``[N, M]`` view of an ``[M, N]`` tensor)."""
+    dt = out_dtype if out_dtype is not None else mx.dtype
+    _lib.require_gpu(w_u8, mx, name="dequantize_mm8")
+    if is_blocked(w_u8):
+        n, m = int(ry.numel()), int(mx.numel())
+        out = torch.empty((m, n), device=w_u8.device, dtype=dt)
+        _lib.call("rwkv7mi_mm8t_dequant", _lib.ptr(w_u8), _lib.ptr(mx.reshape(-1)), _lib.ptr(rx.reshape(-1)),
+                  _lib.ptr(my.reshape(-1).contiguous()), _lib.ptr(ry.reshape(-1).contiguous()), _lib.ptr(out), n, m,
+                  _lib.dtype_code(mx), _lib.dtype_code(out), _lib.stream_of(w_u8))
+        return out.t()
+    if w_u8.dim() != 2 or not w_u8.is_contiguous():
+        raise ValueError("dequantize_mm8 expects contiguous [N, M] bytes or the blocked layout")
+    n, m = (int(s) for s in w_u8.shape)
+    out = torch.empty((n, m), device=w_u8.device, dtype=dt)
+    _lib.call("rwkv7mi_mm8_dequant", _lib.ptr(w_u8), _lib.ptr(mx.reshape(-1).contiguous()),
+              _lib.ptr(rx.reshape(-1).contiguous()), _lib.ptr(my.reshape(-1).contiguous()),
+              _lib.ptr(ry.reshape(-1).contiguous()), _lib.ptr(out), n, m, _lib.dtype_code(mx), _lib.dtype_code(out),
+              _lib.stream_of(w_u8))
+    return out
+
+
 def _meta_1d(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     t = t.reshape(-1)
     if t.dtype != dtype:
@@ -441,8 +467,32 @@ class MM8Linear(torch.nn.Module):
     def rwkv7_forward_add(self, x, residual):
         return self._run(x, residual=residual.contiguous(), epilogue=_lib.EPI_RESIDUAL)
 
+    def rwkv7_forward_ffn(self, x, down, residual):
+        """The FFN pair ``residual + down(relu(self(x))^2)`` in two fused launches
+        (key with the relu^2 epilogue, value with the residual epilogue), the
+        optional quantized-module hook of rwkv7_hf/native_jit_graph_dispatch.py:594-598
+        and native_jit_prefill.py:964-973.  Returns a new tensor, or ``None`` (the
+        caller's fallback) when ``down`` is not an MM8Linear of the matching shape."""
+        if not isinstance(down, MM8Linear) or down.in_features != self.out_features:
+            return None
+        hidden = self._run(x, epilogue=_lib.EPI_RELU2)
+        res = residual.reshape(*hidden.shape[:-1], down.out_features).contiguous()
+        return down._run(hidden, residual=res, epilogue=_lib.EPI_RESIDUAL)
+
     def rwkv7_workspace_bytes(self, rows: int) -> int:
-        return 0  # the blocked GEMV needs none
+        """Scratch bytes a ``rows``-row call needs in the ``"mm8g"`` slot: none for
+        the fused GEMV (up to GEMV_ROWS rows), the tile GEMM's x', row sums and
+        split partials from GEMV_ROWS + 1 to GEMM_ROWS rows."""
+        rows = int(rows)
+        if GEMV_ROWS < rows <= GEMM_ROWS:
+            return mm8_gemm_workspace_bytes(1, rows, self.in_features, self.out_features)
+        return 0
+
+    def rwkv7_reserve_workspace(self, rows: int) -> None:
+        """Grow the ``"mm8g"`` slot for ``rows``-row calls (call before graph capture)."""
+        need = self.rwkv7_workspace_bytes(rows)
+        if need:
+            _ws.reserve(self.w_blk.device, need, slot="mm8g")
 
     def extra_repr(self):
         return f"in={self.in_features}, out={self.out_features}, mm8(fused={self.fused}, hip=gfx950)"
@@ -463,12 +513,36 @@ def quantize_model_mm8(model, *, min_params: int = 8_000_000, fused: bool = True
     setattr(model, "_rwkv7_native_mm_quantization", "mm8")
     setattr(model, "_rwkv7_native_mm_replaced_modules", len(targets))
     setattr(model, "_rwkv7_native_mm_block_replaced_modules", sum(n.startswith("model.layers.") for n in targets))
+    invalidate_model_caches(model)
     return len(targets)
 
 
+# Attributes under which the reference model keeps operand packs and graph
+# runners built from the modules being swapped (rwkv7_hf/native_quant_mm8.py:674-683,
+# native_quant_mm4.py:820-829), plus this build's runner cache.
+MODEL_CACHE_ATTRS = (
+    "_rwkv7_native_jit_pack_cache",
+    "_rwkv7_native_graph_pack_cache",
+    "_rwkv7_native_graph_runner_cache",
+    "_rwkv7_native_prefill_graph_runner_cache",
+    "_rwkv7_native_prefill_graph_hot_runner",
+    "_rwkv7_native_model_jit_pack_cache",
+)
+
+
+def invalidate_model_caches(model) -> None:
+    """Drop the packs and graph runners a model built from its old modules."""
+    for attr in MODEL_CACHE_ATTRS:
+        if hasattr(model, attr):
+            delattr(model, attr)
+    runners = getattr(model, "_graph_runners", None)
+    if isinstance(runners, dict):
+        runners.clear()
+
+
 __all__ = [
-    "quantize_mm8", "quantize_mm8_outmajor", "quantize_mm8_blocked", "mm8_block", "mm8_unblock", "is_blocked",
+    "quantize_mm8", "dequantize_mm8", "quantize_mm8_outmajor", "quantize_mm8_blocked", "mm8_block", "mm8_unblock", "is_blocked",
     "is_out_major", "mm8_matmul", "mm8_linear", "mm8_matmul_into",
     "mm8_matmul_multi_into", "mm8_gemm_multi_into", "mm8_gemm_workspace_bytes", "mm8_gemv_triton",
-    "mm8_matmul_triton", "mm8_workspace_bytes", "MM8Linear", "quantize_model_mm8",
+    "mm8_matmul_triton", "mm8_workspace_bytes", "MM8Linear", "quantize_model_mm8", "invalidate_model_caches",
 ]

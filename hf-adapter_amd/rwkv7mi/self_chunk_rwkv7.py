@@ -33,8 +33,10 @@ def _aligned16(x: torch.Tensor) -> torch.Tensor:
     return x if x.data_ptr() % 16 == 0 else x.clone()
 
 
-def _run_chunk(r4, w4, k4, v4, kk4, a4, state, *, w_is_log: bool, chunk: int,
+def _run_chunk(r4, w4, k4, v4, kk4, a4, state, *, w_is_log: int, chunk: int,
                state_out=None, out=None):
+    """The chunk kernel; ``w_is_log``: 0 decay, 1 natural-log decay, 2 raw
+    pre-activation (decay ``exp(-0.606531 sigmoid(w))`` formed in-kernel)."""
     B, T, H, N = (int(s) for s in r4.shape)
     r4, w4, k4, v4, kk4, a4 = (_aligned16(x) for x in (r4, w4, k4, v4, kk4, a4))
     _lib.require_gpu(r4, w4, k4, v4, kk4, a4, state, name="wkv7 chunk prefill")
@@ -44,7 +46,7 @@ def _run_chunk(r4, w4, k4, v4, kk4, a4, state, *, w_is_log: bool, chunk: int,
     _lib.call(
         "rwkv7mi_wkv7_chunk_prefill",
         _lib.ptr(r4), _lib.ptr(w4), _lib.ptr(k4), _lib.ptr(v4), _lib.ptr(kk4), _lib.ptr(a4),
-        _lib.ptr(st), _lib.ptr(final), _lib.ptr(y), B, T, H, N, int(chunk), int(bool(w_is_log)),
+        _lib.ptr(st), _lib.ptr(final), _lib.ptr(y), B, T, H, N, int(chunk), int(w_is_log),
         _lib.dtype_code(r4), _lib.dtype_code(w4), _lib.stream_of(r4),
     )
     return y, final
@@ -70,7 +72,7 @@ def self_chunk_rwkv7(r, w_decay, k, v, kk, a_gate, state_native, *, chunk_size: 
     _check_state(state_native)
     _same_dtype(r, k, v, kk, a_gate, name="self_chunk_rwkv7")
     return _run_chunk(r.contiguous(), w_decay.contiguous(), k.contiguous(), v.contiguous(), kk.contiguous(),
-                      a_gate.contiguous(), state_native, w_is_log=w_is_log, chunk=int(chunk_size),
+                      a_gate.contiguous(), state_native, w_is_log=int(bool(w_is_log)), chunk=int(chunk_size),
                       state_out=state_out)
 
 
@@ -90,10 +92,32 @@ def dplr_chunk_scan(r: Any, w: Any, k: Any, v: Any, kk: Any, a: Any, state: Any,
     if int(r4.shape[0]) != B:
         raise ValueError("r/w/k/v/kk/a batch size must match state")
     _same_dtype(r4, k4, v4, kk4, a4, name="dplr_chunk_scan")
-    y, final = _run_chunk(r4, w4, k4, v4, kk4, a4, state, w_is_log=False, chunk=16, state_out=state_out)
+    y, final = _run_chunk(r4, w4, k4, v4, kk4, a4, state, w_is_log=0, chunk=16, state_out=state_out)
     if flat:
         return y.reshape(B, int(r4.shape[1]), H * N), final
     return y, final
 
 
-__all__ = ["self_chunk_rwkv7", "self_chunk_rwkv7_available", "dplr_chunk_scan"]
+CHUNK_STATUS_TIMEOUT = 1  # a bounded wait between the kernel's waves gave up: that call's output is void
+CHUNK_STATUS_CLAMPED = 2  # a chunk's log2-decay span exceeded 252; gate factors were clamped
+
+
+def wkv7_chunk_status(clear: bool = True) -> int:
+    """The chunk kernel's sticky status bits on the current device since the
+    last clear (synchronises the device)."""
+    import ctypes
+
+    v = ctypes.c_int(0)
+    _lib.call("rwkv7mi_wkv7_chunk_status", int(bool(clear)), ctypes.byref(v))
+    return int(v.value)
+
+
+def check_wkv7_chunk_status() -> None:
+    """Raise RuntimeError if a chunk-kernel wait gave up since the last check."""
+    st = wkv7_chunk_status(clear=True)
+    if st & CHUNK_STATUS_TIMEOUT:
+        raise RuntimeError("wkv7 chunk kernel: a bounded wait between its waves timed out; outputs are void")
+
+
+__all__ = ["self_chunk_rwkv7", "self_chunk_rwkv7_available", "dplr_chunk_scan", "wkv7_chunk_status",
+           "check_wkv7_chunk_status", "CHUNK_STATUS_TIMEOUT", "CHUNK_STATUS_CLAMPED"]

@@ -134,16 +134,26 @@ int rwkv7mi_wkv7_scan(const void* r, const void* w, const void* k,
                       int act_dtype, int w_dtype, void* stream);
 
 /* Chunked DPLR prefill (chunk C = 16): same result as the sequential scan.
- * w is the per-step decay (w_is_log = 0) or its natural log (w_is_log = 1).
- * Any T >= 0 (a ragged tail chunk is handled).  Replaces self_chunk_rwkv7
- * (rwkv7_hf/self_chunk_rwkv7.py:33) and dplr_chunk_scan
- * (rwkv7_hf/dplr_prefill.py:505). */
+ * w is the per-step decay (w_is_log = 0), its natural log (w_is_log = 1) or
+ * the raw pre-activation w_raw of the clamp-w scan (w_is_log = 2: decay
+ * exp(-0.606531 sigmoid(w_raw)) formed in-kernel).  Any T >= 0 (a ragged tail
+ * chunk is handled).  Replaces self_chunk_rwkv7 (rwkv7_hf/self_chunk_rwkv7.py:33),
+ * dplr_chunk_scan (rwkv7_hf/dplr_prefill.py:505) and, with w_is_log = 2,
+ * fused_recurrent_scan_clampw (rwkv7_hf/fused_recurrent_update.py:1420). */
 int rwkv7mi_wkv7_chunk_prefill(const void* r, const void* w, const void* k,
                                const void* v, const void* kk, const void* a,
                                const float* state_in, float* state_out,
                                void* y, int64_t B, int64_t T, int64_t H,
                                int64_t N, int64_t chunk, int w_is_log,
                                int act_dtype, int w_dtype, void* stream);
+
+/* Sticky status bits of the chunk kernel on the current device since the last
+ * clear: 1 = a bounded wait between the kernel's waves gave up (that call's
+ * output is void), 2 = a chunk's log2-decay span exceeded 252 and the gate
+ * factors were clamped to 2^+-126.  Synchronises the device; clear != 0 resets
+ * the word.  This build's own diagnostic (no reference counterpart: the
+ * reference's Triton scans have no cross-wave waits). */
+int rwkv7mi_wkv7_chunk_status(int clear, int* status);
 
 /* ------------------------------------------------------------------- MM8 */
 
@@ -394,6 +404,7 @@ int rwkv7mi_ffn_add_norm_mix(const void* residual, const void* attn_out,
 
 /* Sequence form over x [B,T,D]: h_t = LN(x_t), prev_t = h_{t-1} (prev_in for
  * t = 0), outs[i] = h + (prev - h) * mixes[i]; prev_out <- h_{T-1}.
+ * ln_w = ln_b = NULL: h = x (x already normalised, the reference's convention).
  * Replaces fused_attn_sequence_shift_mix / fused_ffn_sequence_shift_mix
  * (rwkv7_hf/fused_time_mix.py:413, :470).  prev_in != prev_out. */
 int rwkv7mi_seq_norm_mix(const void* x, const void* prev_in, void* prev_out,
@@ -423,15 +434,23 @@ int rwkv7mi_dense_multi(const void* const* xs, const void* const* Ws,
 
 /* ------------------------------------------- scan input / output prep */
 
+/* state_prep flags */
+#define RWKV7MI_PREP_A_RAW 1     /* a is pre-sigmoid: a = sigmoid(a) first */
+#define RWKV7MI_PREP_VGATE_RAW 2 /* v_gate is pre-sigmoid */
+#define RWKV7MI_PREP_W_DECAY 4   /* w_out = exp(log decay), else the log decay */
+
 /* Per (row, head): kk = normalize(k_raw * k_k), k_out = k_raw*(1+(a-1)*k_a),
- * logw_out = -0.606531*sigmoid(w_raw) (fp32 natural-log decay), and the V
- * interpolation (v_mode 1: v_first = v; 2: v += (v_first - v) * v_gate).
+ * w_out = -0.606531*sigmoid(w_raw) (natural-log decay) or its exp (flag
+ * RWKV7MI_PREP_W_DECAY), in fp32 (w_dtype F32) or the activation dtype, and
+ * v_out = v_raw after the V interpolation (v_mode 0: as is; 1: v_first = v;
+ * 2: v += (v_first - v) * v_gate).  v_out may be v_raw.
  * Replaces fused_prefill_state_prep (rwkv7_hf/fused_prefill.py:184). */
 int rwkv7mi_state_prep(const void* k_raw, const void* a, const void* w_raw,
-                       void* v, void* v_first, const void* v_gate,
-                       const void* k_k, const void* k_a, void* kk_out,
-                       void* k_out, float* logw_out, int64_t rows, int64_t H,
-                       int64_t N, int v_mode, int act_dtype, int param_dtype,
+                       const void* v_raw, void* v_out, void* v_first,
+                       const void* v_gate, const void* k_k, const void* k_a,
+                       void* kk_out, void* k_out, void* w_out, int64_t rows,
+                       int64_t H, int64_t N, int v_mode, int flags,
+                       int act_dtype, int param_dtype, int w_dtype,
                        void* stream);
 
 /* out = (GroupNorm_H(y) + (sum_head r*k*r_k) * v) * g per (row, head).

@@ -236,6 +236,15 @@ def seq_norm_mix(x, prev0, w, b, mixes, eps=1e-5):
     return [h + (prev - h) * np.asarray(m, np.float64) for m in mixes], h[:, -1]
 
 
+def seq_shift_mix(x, prev0, mixes):
+    """rwkv7_hf/fused_time_mix.py:424-427, 480-483 (the sequence mixes' torch form,
+    fp64): x is already normalised; prev = [prev0, x[:, :-1]];
+    out_i = x + (prev - x) mix_i; returns (outs, x[:, -1])."""
+    x = np.asarray(x, np.float64)
+    prev = np.concatenate([np.asarray(prev0, np.float64)[:, None], x[:, :-1]], 1)
+    return [x + (prev - x) * np.asarray(m, np.float64) for m in mixes], x[:, -1]
+
+
 def _sig(x):
     return 1.0 / (1.0 + np.exp(-x))
 

@@ -66,7 +66,8 @@ def test_prefill_then_decode_matches_oracle(mm8, B):
     T = 37
     ids = rng.integers(0, cfg.vocab_size, (B, T))
     ref_logits, st = ref.run(ids)
-    logits, cache = model(torch.tensor(ids, device="cuda"))
+    out = model(torch.tensor(ids, device="cuda"))
+    logits, cache = out.logits, out.past_key_values
     torch.cuda.synchronize()
     _close(logits[:, -1], ref_logits[:, -1])
     # the cache matches the oracle's recurrent state after the prompt
@@ -77,7 +78,7 @@ def test_prefill_then_decode_matches_oracle(mm8, B):
     for step in range(4):
         nxt = rng.integers(0, cfg.vocab_size, (B,))
         r = ref.step(nxt, st)
-        lg, cache = model(torch.tensor(nxt[:, None], device="cuda"), cache)
+        lg = model(torch.tensor(nxt[:, None], device="cuda"), past_key_values=cache, use_graph=False).logits
         torch.cuda.synchronize()
         _close(lg[:, -1], r)
     assert cache.seen_tokens == T + 4
@@ -88,12 +89,12 @@ def test_graph_decode_equals_eager_decode(mm8, B):
     cfg, model, _ = _build(mm8)
     rng = np.random.default_rng(2)
     ids = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 9)), device="cuda")
-    _, c1 = model(ids)
+    c1 = model(ids).past_key_values
     c2 = c1.clone()
     runner = model.graph_runner(B)
     for step in range(5):
         tok = torch.tensor(rng.integers(0, cfg.vocab_size, (B,)), device="cuda")
-        eager, c1 = model(tok[:, None], c1)
+        eager = model(tok[:, None], past_key_values=c1, use_graph=False).logits
         lg = runner.replay(tok, c2).clone()
         _ = torch.randn(64, device="cuda").sum()  # unrelated eager work between replays
         torch.cuda.synchronize()
@@ -110,15 +111,15 @@ def test_decode_fused_mix_equals_unfused(B):
     cfg, model, _ = _build(True, layers=3)
     rng = np.random.default_rng(7 + B)
     ids = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 5)), device="cuda")
-    _, c1 = model(ids)
+    c1 = model(ids).past_key_values
     c2 = c1.clone()
     assert model._mix_fusable(B) == (B == 1)
     for step in range(3):
         tok = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 1)), device="cuda")
         model.fused_mix_decode = True
-        a, c1 = model(tok, c1)
+        a = model(tok, past_key_values=c1, use_graph=False).logits
         model.fused_mix_decode = False
-        b, c2 = model(tok, c2)
+        b = model(tok, past_key_values=c2, use_graph=False).logits
         model.fused_mix_decode = True
         torch.cuda.synchronize()
         scale = b.float().abs().max().item()
@@ -155,7 +156,7 @@ def test_generate_greedy_matches_oracle():
 def test_cache_select_and_repeat():
     cfg, model, _ = _build(False)
     ids = torch.randint(0, cfg.vocab_size, (3, 5), device="cuda")
-    _, cache = model(ids)
+    cache = model(ids).past_key_values
     sel = cache.clone().select_batch(torch.tensor([2, 0], device="cuda"))
     assert sel.get_batch_size() == 2
     assert torch.equal(sel._state[1][0], cache._state[1][2])
@@ -176,7 +177,7 @@ def test_model_matches_reference_golden(name, dtype):
     cfg, w, g = golden_case(name)
     model = NativeRWKV7ForCausalLM(cfg, w, device="cuda", dtype=dtype)
     ids = torch.tensor(g["ids"], device="cuda")
-    logits, _ = model(ids)
+    logits = model(ids).logits
     out = model.generate(ids, len(g["greedy"])).cpu().numpy()[0, ids.shape[1]:]
     torch.cuda.synchronize()
     ref = g["logits"].astype(np.float64)

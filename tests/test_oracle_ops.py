@@ -131,3 +131,27 @@ def test_output_prepare_matches_group_norm_and_decode_form(oracle):
     flat = oracle.output_prepare(y.reshape(B, -1), r.reshape(B, -1), k.reshape(B, -1), v.reshape(B, -1),
                                  g.reshape(B, -1), r_k, gn_w, gn_b, H, eps)
     np.testing.assert_allclose(flat, out.reshape(B, -1), rtol=1e-10, atol=1e-12)
+
+
+def test_seq_shift_mix_closed_forms(oracle):
+    """The reference-convention sequence mix (x already normalised): mix = 0
+    gives x, mix = 1 gives the one-token shift with the carried row first, and
+    it equals seq_norm_mix of an identity-normalised input (a planted
+    off-by-one shift would fail the mix = 1 case)."""
+    rng = _rng(31)
+    B, Tn, D = 2, 5, 16
+    x = rng.standard_normal((B, Tn, D))
+    prev0 = rng.standard_normal((B, D))
+    (o0, o1), last = oracle.seq_shift_mix(x, prev0, [np.zeros(D), np.ones(D)])
+    np.testing.assert_array_equal(o0, x)
+    np.testing.assert_allclose(o1[:, 0], prev0, rtol=0, atol=1e-14)
+    np.testing.assert_allclose(o1[:, 1:], x[:, :-1], rtol=0, atol=1e-14)
+    np.testing.assert_array_equal(last, x[:, -1])
+    # rows that are already LayerNorm outputs with unit affine: LN leaves them (almost) as they are
+    xn = oracle.layer_norm(x, np.ones(D), np.zeros(D), eps=0.0)
+    mixes = [rng.random(D) for _ in range(3)]
+    outs_a, _ = oracle.seq_shift_mix(xn, oracle.layer_norm(prev0, np.ones(D), np.zeros(D), eps=0.0), mixes)
+    outs_b, _ = oracle.seq_norm_mix(xn, oracle.layer_norm(prev0, np.ones(D), np.zeros(D), eps=0.0), np.ones(D),
+                                    np.zeros(D), mixes, eps=0.0)
+    for a, b in zip(outs_a, outs_b):
+        np.testing.assert_allclose(a[:, 1:], b[:, 1:], rtol=1e-9, atol=1e-9)
