@@ -2,6 +2,8 @@
 // layout and the per-launch problem record).
 #include <string>
 
+#include <mutex>
+
 #include "mm8t_common.h"
 
 // ---------------------------------------------------------------------------
@@ -370,13 +372,12 @@ extern "C" size_t rwkv7mi_mm8t_gemm_workspace_bytes(int nprob, int64_t rows, int
   return mm8g_ws_layout(mm8g_splits(rows, I, O, nprob, splits), nprob, rows, I, O).total;
 }
 
-extern "C" int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x, const uint8_t* const* w_blk,
-                                       const void* const* mx, const void* const* rx, const void* const* my,
-                                       const void* const* ry, const void* const* bias, const void* const* residual,
-                                       void* const* y, const int* epilogue, int64_t rows, int64_t I, int64_t O,
-                                       int act_dtype, int meta_dtype, int splits, void* workspace,
-                                       size_t workspace_bytes, void* stream) {
-  const std::string w("mm8t_gemm_multi");
+static int mm8g_run(const char* who, int nprob, const void* const* x, const uint8_t* const* w_blk,
+                    const void* const* mx, const void* const* rx, const void* const* my, const void* const* ry,
+                    const void* const* bias, const void* const* residual, void* const* y, const int* epilogue,
+                    int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype, int splits, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  const std::string w(who);
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
   if (!x || !w_blk || !mx || !rx || !my || !ry || !y || !epilogue) return fail(RWKV7MI_EINVAL, w + ": null array");
   if (rows < 0 || I <= 0 || O <= 0 || splits < 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
@@ -459,4 +460,61 @@ extern "C" int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x, const ui
       return check_launch("mm8g_reduce_kernel");
     });
   });
+}
+
+extern "C" int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x, const uint8_t* const* w_blk,
+                                       const void* const* mx, const void* const* rx, const void* const* my,
+                                       const void* const* ry, const void* const* bias, const void* const* residual,
+                                       void* const* y, const int* epilogue, int64_t rows, int64_t I, int64_t O,
+                                       int act_dtype, int meta_dtype, int splits, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  return mm8g_run("mm8t_gemm_multi", nprob, x, w_blk, mx, rx, my, ry, bias, residual, y, epilogue, rows, I, O,
+                  act_dtype, meta_dtype, splits, workspace, workspace_bytes, stream);
+}
+
+// ---- allocation-free form: the scratch lives in this file's device array
+// (one copy per GPU, held until the process ends).  Its host-side name is
+// only a stand-in; the device address of each GPU's copy comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+namespace {
+__device__ __align__(256) unsigned char scratch[RWKV7MI_MM8T_GEMM_SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+}  // namespace
+
+static int mm8g_scratch(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(RWKV7MI_ELAUNCH, "mm8t_gemm_multi_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(RWKV7MI_ELAUNCH, std::string("mm8t_gemm_multi_noalloc: hipGetSymbolAddress failed: ") +
+                                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return RWKV7MI_OK;
+}
+
+extern "C" int rwkv7mi_mm8t_gemm_multi_noalloc(int nprob, const void* const* x, const uint8_t* const* w_blk,
+                                               const void* const* mx, const void* const* rx, const void* const* my,
+                                               const void* const* ry, const void* const* bias,
+                                               const void* const* residual, void* const* y, const int* epilogue,
+                                               int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype,
+                                               int splits, void* stream) {
+  const size_t need = rwkv7mi_mm8t_gemm_workspace_bytes(nprob, rows, I, O, splits);
+  if (rows > 0 && need > (size_t)RWKV7MI_MM8T_GEMM_SCRATCH_BYTES)
+    return fail(RWKV7MI_ESIZE, "mm8t_gemm_multi_noalloc: the call needs " + std::to_string(need) +
+                                   " scratch bytes, more than the library's fixed " +
+                                   std::to_string((size_t)RWKV7MI_MM8T_GEMM_SCRATCH_BYTES) +
+                                   " (use rwkv7mi_mm8t_gemm_multi with a workspace)");
+  void* ws = nullptr;
+  if (rows > 0) {
+    if (int rc = mm8g_scratch(&ws)) return rc;
+  }
+  return mm8g_run("mm8t_gemm_multi_noalloc", nprob, x, w_blk, mx, rx, my, ry, bias, residual, y, epilogue, rows, I,
+                  O, act_dtype, meta_dtype, splits, ws, (size_t)RWKV7MI_MM8T_GEMM_SCRATCH_BYTES, stream);
 }

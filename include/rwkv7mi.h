@@ -262,6 +262,27 @@ int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x,
                             int splits, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* Allocation-free form of rwkv7mi_mm8t_gemm_multi (same arguments and results,
+ * no workspace argument).  No counterpart in the reference: it is for callers
+ * that cannot allocate (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Its scratch is a fixed per-GPU device
+ * array of RWKV7MI_MM8T_GEMM_SCRATCH_BYTES (80 MiB: every 7.2B projection
+ * at 64 rows, the 4096 x 65536 head included) held until the process ends;
+ * calls needing more (see rwkv7mi_mm8t_gemm_workspace_bytes) return
+ * RWKV7MI_ESIZE.  Every call on one GPU shares that array, so calls that
+ * overlap on one GPU (different streams or threads) race; the kernels write
+ * every scratch byte they read, so nothing needs clearing between calls. */
+#define RWKV7MI_MM8T_GEMM_SCRATCH_BYTES (80u << 20)
+int rwkv7mi_mm8t_gemm_multi_noalloc(int nprob, const void* const* x,
+                                    const uint8_t* const* w_blk,
+                                    const void* const* mx, const void* const* rx,
+                                    const void* const* my, const void* const* ry,
+                                    const void* const* bias,
+                                    const void* const* residual, void* const* y,
+                                    const int* epilogue, int64_t rows, int64_t I,
+                                    int64_t O, int act_dtype, int meta_dtype,
+                                    int splits, void* stream);
+
 /* Decode LN + token-shift mix fused into the out-major MM8 GEMV: for up to
  * four problems of one shape, h = LayerNorm(x) (x [rows, I] the residual
  * rows, ln_w / ln_b [I]), x_p = round(h + (prev - h) * mix_p) and
