@@ -42,14 +42,27 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> Path:
+def _stale(src: Path) -> bool:
+    obj = OUT_DIR / (src.stem + ".o")
+    if not obj.exists():
+        return True
+    newest = max([src.stat().st_mtime] + [h.stat().st_mtime for h in CSRC.glob("*.h")]
+                 + [(HERE.parent / "include" / "rwkv7mi.h").stat().st_mtime])
+    return newest > obj.stat().st_mtime
+
+
+def build(jobs: int | None = None, verbose: bool = True, incremental: bool = False) -> Path:
+    """Compile every source (``incremental``: only those older than their
+    sources or headers) and link the library."""
     OUT_DIR.mkdir(exist_ok=True)
     sources = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
     if not sources:
         raise RuntimeError("no sources under csrc/")
-    jobs = jobs or min(len(sources), max(1, min(8, os.cpu_count() or 1)))
+    todo = [s for s in sources if _stale(s)] if incremental else sources
+    jobs = jobs or min(max(len(todo), 1), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
+        list(ex.map(_compile, todo))
+    objs = [OUT_DIR / (s.stem + ".o") for s in sources]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -64,9 +77,10 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--incremental", action="store_true", help="recompile only stale objects")
     args = ap.parse_args()
     try:
-        build(args.jobs)
+        build(args.jobs, incremental=args.incremental)
     except RuntimeError as exc:
         print(exc, file=sys.stderr)
         sys.exit(1)
