@@ -669,9 +669,8 @@ class _Layer:
 class NativeRWKV7ForCausalLM:
     """RWKV-7 causal LM (inference) over the HIP kernels; see the module docstring."""
 
-    def __init__(self, config: NativeRWKV7Config, weights: dict[str, torch.Tensor], *, device="cuda",
-                 dtype=torch.float16):
-        self.config = cfg = config
+    def _init_common(self, config, device, dtype):
+        self.config = config
         self.device = torch.device(device)
         self.dtype = dtype
         # run the decode LoRA projections on a second stream beside R/K/V
@@ -680,6 +679,18 @@ class NativeRWKV7ForCausalLM:
         self.fused_lora_decode = True
         # decode: LayerNorm + token-shift mixes inside the R/K/V and FFN-key GEMVs
         self.fused_mix_decode = True
+        self._replaced = 0
+        self.layers = []
+
+    def _finish_init(self):
+        self._rwkv7_native_mm_quantization = "mm8" if self._replaced else None
+        self._rwkv7_native_mm_replaced_modules = self._replaced
+        self._graph_runners: dict[int, "NativeGraphRunner"] = {}
+
+    def __init__(self, config: NativeRWKV7Config, weights: dict[str, torch.Tensor], *, device="cuda",
+                 dtype=torch.float16):
+        self._init_common(config, device, dtype)
+        cfg = config
         dev = self.device
 
         def get(name):
@@ -699,9 +710,7 @@ class NativeRWKV7ForCausalLM:
                 return q
             return DenseLinear(w)
 
-        self._replaced = 0
         self.emb = get("model.embeddings.weight")
-        self.layers = []
         for i in range(cfg.num_hidden_layers):
             p = f"model.layers.{i}."
             L = _Layer()
@@ -731,9 +740,98 @@ class NativeRWKV7ForCausalLM:
             self.layers.append(L)
         self.norm = (get("model.norm.weight"), get("model.norm.bias"))
         self.lm_head = linear("lm_head")
-        self._rwkv7_native_mm_quantization = "mm8" if cfg.use_native_mm8 else None
-        self._rwkv7_native_mm_replaced_modules = self._replaced
-        self._graph_runners: dict[int, "NativeGraphRunner"] = {}
+        self._finish_init()
+
+    # ------------------------------------------------------------- packs
+    def extract_graph_packs(self):
+        """The per-layer 41-entry operand tuples of the reference's graph route
+        (rwkv7_hf/native_jit_packing.py:57-143), in its order:
+        ``(i, H, N, eps, has_pre, pre_w, pre_b, an_w, an_b, fn_w, fn_b, x_r, x_w,
+        x_k, x_v, x_a, x_g, k_k, k_a, r_k, Rw, Kw, Vw, Ow, w1, w2, w0, a1, a2, a0,
+        v1, v2, v0, g1, g2, gn_w, gn_b, fx_k, fK, fV, RKVw)``.  Quantized
+        projections stay callables (their ``MM8Linear`` modules), dense ones are
+        ``[out, in]`` weights; layer 0's missing V LoRA and pre-norm are zeros of
+        the reference's shapes, and the stacked-RKV slot is empty.  Returns
+        ``(packs, H, N, eps)``; the tensors are the model's own (no copies)."""
+        cfg = self.config
+        H, N, D, A = cfg.num_heads, cfg.head_dim, cfg.hidden_size, cfg.attention_hidden_size
+        eps = float(N * 1e-5)
+        dev, dt = self.device, self.dtype
+        op = lambda lin: lin.m if isinstance(lin, QuantLinear) else lin.weight
+        packs = []
+        for L in self.layers:
+            has_pre = 1 if L.pre is not None else 0
+            pre_w, pre_b = L.pre if has_pre else (torch.zeros(D, device=dev, dtype=dt),) * 2
+            lo = {n: q for q, n in enumerate(("w", "a", "g", "v")[:len(L.lora_down)])}
+            if "v" in lo:
+                v1, v2, v0 = L.lora_down[3], L.lora_up[3], L.lora_bias[3]
+            else:
+                v1 = torch.zeros(1, D, device=dev, dtype=dt)
+                v2 = torch.zeros(A, 1, device=dev, dtype=dt)
+                v0 = torch.zeros(A, device=dev, dtype=dt)
+            packs.append((
+                L.idx, H, N, eps, has_pre, pre_w, pre_b, L.ln1[0], L.ln1[1], L.ln2[0], L.ln2[1],
+                *L.mix, L.k_k, L.k_a, L.r_k,
+                op(L.r_proj), op(L.k_proj), op(L.v_proj), op(L.o_proj),
+                L.lora_down[0], L.lora_up[0], L.lora_bias[0],
+                L.lora_down[1], L.lora_up[1], L.lora_bias[1],
+                v1, v2, v0,
+                L.lora_down[2], L.lora_up[2],
+                L.gn[0], L.gn[1], L.fx_k, op(L.key), op(L.value),
+                self.emb.new_empty((0,)),
+            ))
+        return packs, H, N, eps
+
+    @classmethod
+    def from_graph_packs(cls, config: NativeRWKV7Config, packs, *, embeddings, norm_weight, norm_bias, lm_head,
+                         device="cuda", dtype=torch.float16):
+        """A model over operands in the reference's 41-entry pack layout (see
+        :meth:`extract_graph_packs`): the tensors are used as given (no copies
+        when they already have the device and dtype); a projection is an
+        ``MM8Linear`` module (fused MM8 route) or an ``[out, in]`` weight."""
+        if len(packs) != config.num_hidden_layers:
+            raise ValueError(f"{len(packs)} packs for {config.num_hidden_layers} layers")
+        self = cls.__new__(cls)
+        self._init_common(config, device, dtype)
+        dev = self.device
+        t = lambda x: None if x is None else x.to(device=dev, dtype=dtype).contiguous()
+
+        def lin(x):
+            if isinstance(x, MM8Linear):
+                self._replaced += 1
+                return QuantLinear(x)
+            if isinstance(x, torch.Tensor):
+                return DenseLinear(t(x))
+            raise TypeError(f"pack projection must be an MM8Linear or a weight tensor, got {type(x)!r}")
+
+        for pk in packs:
+            if len(pk) != 41:
+                raise ValueError(f"graph packs have 41 entries, got {len(pk)}")
+            (i, H, N, eps, has_pre, pre_w, pre_b, an_w, an_b, fn_w, fn_b, x_r, x_w, x_k, x_v, x_a, x_g, k_k, k_a,
+             r_k, Rw, Kw, Vw, Ow, w1, w2, w0, a1, a2, a0, v1, v2, v0, g1, g2, gn_w, gn_b, fx_k, fK, fV, _rkv) = pk
+            if int(H) != config.num_heads or int(N) != config.head_dim:
+                raise ValueError("pack head shape does not match the config")
+            L = _Layer()
+            L.idx = int(i)
+            L.pre = (t(pre_w), t(pre_b)) if has_pre else None
+            L.ln1, L.ln2 = (t(an_w), t(an_b)), (t(fn_w), t(fn_b))
+            L.mix = [t(m).reshape(-1) for m in (x_r, x_w, x_k, x_v, x_a, x_g)]
+            L.k_k, L.k_a, L.r_k = t(k_k), t(k_a), t(r_k)
+            L.r_proj, L.k_proj, L.v_proj, L.o_proj = lin(Rw), lin(Kw), lin(Vw), lin(Ow)
+            L.lora_down, L.lora_up, L.lora_bias = [t(w1), t(a1), t(g1)], [t(w2), t(a2), t(g2)], [t(w0), t(a0), None]
+            if L.idx > 0:  # layer 0 carries zero placeholders for the V LoRA
+                L.lora_down.append(t(v1))
+                L.lora_up.append(t(v2))
+                L.lora_bias.append(t(v0))
+            L.gn = (t(gn_w), t(gn_b))
+            L.fx_k = t(fx_k).reshape(-1)
+            L.key, L.value = lin(fK), lin(fV)
+            self.layers.append(L)
+        self.emb = t(embeddings)
+        self.norm = (t(norm_weight), t(norm_bias))
+        self.lm_head = lin(lm_head)
+        self._finish_init()
+        return self
 
     # ------------------------------------------------------------- helpers
     @classmethod

@@ -367,3 +367,90 @@ def test_mm8_dequant_matches_oracle(oracle, dtype):
     ref = oracle.mm8_dequant(*(t.cpu().numpy() for t in (w_u8, mx, rx, my, ry)))
     tol = 2.0 ** -10 if dtype == torch.float16 else 1e-6
     assert np.abs(_f(got) - ref).max() <= tol * np.abs(ref).max()
+
+
+def test_torch_ops_match_python_functions():
+    """torch.ops.rwkv7mi.* run the same kernels as the Python operators, and the
+    in-place forms update their marked arguments (also inside a captured graph)."""
+    import rwkv7mi
+    from rwkv7mi import dplr_chunk_scan, fused_recurrent_update, mm8_matmul, quantize_mm8
+
+    rng = np.random.default_rng(95)
+    B, T, H, N = 2, 32, 2, 64
+    r, k, v, a = _scan_inputs(rng, B, T, H)
+    w = np.exp(-np.exp(rng.normal(-0.5, 0.5, (B, T, H, N))))
+    args = [_t(r), _t(w, torch.float32), _t(k), _t(v), _t(k), _t(a)]
+    st = _t(0.1 * rng.standard_normal((B, H, N, N)), torch.float32)
+    y1, s1 = dplr_chunk_scan(*args, st)
+    y2, s2 = torch.ops.rwkv7mi.chunk_scan(*args, st, 0)
+    assert torch.equal(y1, y2) and torch.equal(s1, s2)
+    st_in = st.clone()
+    y3 = torch.empty_like(args[0])
+    torch.ops.rwkv7mi.chunk_scan_(*args, st_in, 0, y3)
+    assert torch.equal(y3, y1) and torch.equal(st_in, s1)
+    # captured: replays from the same start state give the same result each time
+    st_g, y_g = st.clone(), torch.empty_like(args[0])
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        torch.ops.rwkv7mi.chunk_scan_(*args, st_g, 0, y_g)
+    for _ in range(3):
+        st_g.copy_(st)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_g, y1) and torch.equal(st_g, s1)
+    # one-token update, out of place and in place
+    one = [x[:, 0] for x in args]
+    o1, n1 = fused_recurrent_update(*one, st)
+    o2, n2 = torch.ops.rwkv7mi.fused_recurrent_update(*one, st)
+    assert torch.equal(o1, o2) and torch.equal(n1, n2)
+    st2, o3 = st.clone(), torch.empty_like(o1)
+    torch.ops.rwkv7mi.fused_recurrent_update_(*one, st2, o3)
+    assert torch.equal(o3, o1) and torch.equal(st2, n1)
+    # MM8
+    W = _t(rng.standard_normal((256, 128)) * 0.02)
+    q = quantize_mm8(W)
+    q2 = torch.ops.rwkv7mi.quantize_mm8(W)
+    assert all(torch.equal(u, v2) for u, v2 in zip(q, q2))
+    x = _t(rng.standard_normal((3, 256)))
+    ym = mm8_matmul(x, *q)
+    assert torch.equal(torch.ops.rwkv7mi.mm8_matmul(x, *q), ym)
+    out = torch.empty_like(ym)
+    torch.ops.rwkv7mi.mm8_matmul_out(x, *q, out)
+    assert torch.equal(out, ym)
+    # sequence shift mix
+    xs = _t(rng.standard_normal((B, 5, 64)))
+    prev = _t(rng.standard_normal((B, 64)))
+    mixes = [_t(rng.random(64)) for _ in range(2)]
+    got = torch.ops.rwkv7mi.seq_shift_mix(xs, prev, mixes)
+    ref = rwkv7mi.fused_time_mix.fused_ffn_sequence_shift_mix(xs, prev, mixes[1])
+    assert len(got) == 3 and torch.equal(got[1], ref[0]) and torch.equal(got[2], ref[1])
+
+
+def test_graph_packs_round_trip():
+    """extract_graph_packs gives the reference's 41-entry tuples (quantized
+    projections as MM8Linear callables, layer 0's placeholders); a model built
+    from them decodes bit for bit like the original."""
+    from rwkv7mi import MM8Linear
+    from rwkv7mi.model import NativeRWKV7ForCausalLM
+
+    cfg, model = _tiny_mm8_model(layers=2)
+    packs, H, N, eps = model.extract_graph_packs()
+    assert len(packs) == 2 and all(len(p) == 41 for p in packs)
+    assert (H, N, eps) == (cfg.num_heads, 64, 64 * 1e-5)
+    p0, p1 = packs
+    assert p0[4] == 1 and p1[4] == 0 and float(p1[5].abs().sum()) == 0
+    assert isinstance(p0[20], MM8Linear) and isinstance(p0[38], MM8Linear) and p0[40].numel() == 0
+    assert tuple(p0[30].shape) == (1, cfg.hidden_size) and float(p0[31].abs().sum()) == 0  # no V LoRA on layer 0
+    assert tuple(p1[30].shape) == (cfg.v_low_rank_dim, cfg.hidden_size)
+    twin = NativeRWKV7ForCausalLM.from_graph_packs(cfg, packs, embeddings=model.emb, norm_weight=model.norm[0],
+                                                   norm_bias=model.norm[1], lm_head=model.lm_head.m)
+    assert twin._rwkv7_native_mm_replaced_modules == model._rwkv7_native_mm_replaced_modules
+    ids = torch.tensor(np.random.default_rng(96).integers(0, cfg.vocab_size, (2, 7)), device="cuda")
+    a = model(ids).logits
+    b = twin(ids).logits
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        NativeRWKV7ForCausalLM.from_graph_packs(cfg, packs[:1], embeddings=model.emb, norm_weight=model.norm[0],
+                                               norm_bias=model.norm[1], lm_head=model.lm_head.m)
