@@ -16,6 +16,13 @@
 // fp32/bf16 inputs are split hi + lo) is loaded in the same permuted order.
 // Each block's 4 MFMAs accumulate from zero, then the lane's per-(o, group)
 // scale is applied in fp32.  The 4 waves are reduced through LDS.
+//
+// Asymmetric (min/max affine) variant, AFF = true: q in [0, 15] with a scale
+// and a bias (the group minimum) per (o, group), W[o,i] = q s + b; stored in
+// the same packed layout.  With the kernel's centred nibbles (q - 8):
+//   sum_i W x = s sum (q - 8) x + (8 s + b) sum_i x,
+// and the group sums of x come from one more MFMA per step against a B
+// operand of ones, which lands them in the accumulator layout directly.
 #include "common.h"
 
 namespace rwkv7mi {
@@ -62,10 +69,10 @@ __device__ __forceinline__ f16x8 w4_nibbles_to_f16(uint32_t d) {
   return out;
 }
 
-template <int MT, typename TA, typename TS>
+template <int MT, typename TA, typename TS, bool AFF>
 __global__ __launch_bounds__(256) void w4g_kernel(const TA* __restrict__ x, const uint8_t* __restrict__ packed,
-                                                  const TS* __restrict__ scales, const TS* __restrict__ bias,
-                                                  const TA* residual, TA* y, int rows,
+                                                  const TS* __restrict__ scales, const TS* __restrict__ gbias,
+                                                  const TS* __restrict__ bias, const TA* residual, TA* y, int rows,
                                                   int O, int I, int group, int epilogue) {
   constexpr bool SPLIT = sizeof(TA) != 2 || !std::is_same<TA, __half>::value;
   __shared__ float s_red[16 * MT][16];
@@ -85,15 +92,21 @@ __global__ __launch_bounds__(256) void w4g_kernel(const TA* __restrict__ x, cons
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
+  f16x8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
   for (int blk = wave; blk < nblk; blk += 4) {
     uint4 wq = make_uint4(0u, 0u, 0u, 0u);
     if (ook) wq = *reinterpret_cast<const uint4*>(packed + (int64_t)o * rowbytes + blk * 64 + 16 * kg);
-    const float sc = ook ? ld(scales, (int64_t)o * ngroups + (blk * 128) / group) : 0.f;
+    const int64_t gi = (int64_t)o * ngroups + (blk * 128) / group;
+    const float sc = ook ? ld(scales, gi) : 0.f;
+    const float zc = AFF && ook ? 8.f * sc + ld(gbias, gi) : 0.f;  // weight of the group sum of x
     const uint32_t dw[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       const int b = 16 * t + n;  // A row of this lane
       f32x4 g = (f32x4){0.f, 0.f, 0.f, 0.f};
+      f32x4 gs = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         f16x8 ah, al;
@@ -101,8 +114,13 @@ __global__ __launch_bounds__(256) void w4g_kernel(const TA* __restrict__ x, cons
         const f16x8 bv = w4_nibbles_to_f16(dw[s]);
         g = mfma16x16x32(ah, bv, g);
         if constexpr (SPLIT) g = mfma16x16x32(al, bv, g);
+        if constexpr (AFF) {
+          gs = mfma16x16x32(ah, ones, gs);
+          if constexpr (SPLIT) gs = mfma16x16x32(al, ones, gs);
+        }
       }
       acc[t] += sc * g;
+      if constexpr (AFF) acc[t] += zc * gs;
     }
   }
 
@@ -161,9 +179,62 @@ __global__ __launch_bounds__(64) void w4g_pack_kernel(const TW* __restrict__ wt,
   if (lane == 0) scales[(int64_t)o * ngroups + g] = from_f32<TW>(s);
 }
 
+// Asymmetric group-wise W4 packer (min/max affine, fp32 ops):
+// s = max((max - min) / 15, 1e-8) (correctly rounded), b = min,
+// q = clamp(rint((w - b) / s), 0, 15); scales and biases stored in the weight
+// dtype (round to nearest even).  The group's minimum maps to 0, its maximum to 15.
+template <typename TW>
+__global__ __launch_bounds__(64) void w4a_pack_kernel(const TW* __restrict__ wt, int O, int I, int group,
+                                                      uint8_t* __restrict__ packed, TW* __restrict__ scales,
+                                                      TW* __restrict__ biases) {
+  const int ngroups = I / group;
+  const int og = blockIdx.x;
+  const int o = og / ngroups, g = og % ngroups;
+  const int lane = threadIdx.x;
+  const TW* src = wt + (int64_t)o * I + (int64_t)g * group;
+  float mn = INFINITY, mxv = -INFINITY;
+  for (int e = lane; e < group; e += 64) {
+    const float v = to_f32(src[e]);
+    mn = fminf(mn, v);
+    mxv = fmaxf(mxv, v);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    mn = fminf(mn, __shfl_xor(mn, off, 64));
+    mxv = fmaxf(mxv, __shfl_xor(mxv, off, 64));
+  }
+  const float s = fmaxf(__fdiv_rn(mxv - mn, 15.0f), 1.0e-8f);
+  uint8_t* dst = packed + (int64_t)o * (I / 2) + (int64_t)g * (group / 2);
+  for (int j = lane; j < group / 2; j += 64) {
+    float q0 = rintf(__fdiv_rn(to_f32(src[2 * j]) - mn, s));
+    float q1 = rintf(__fdiv_rn(to_f32(src[2 * j + 1]) - mn, s));
+    q0 = fminf(fmaxf(q0, 0.f), 15.f);
+    q1 = fminf(fmaxf(q1, 0.f), 15.f);
+    dst[j] = (uint8_t)((int)q0 | ((int)q1 << 4));
+  }
+  if (lane == 0) {
+    scales[(int64_t)o * ngroups + g] = from_f32<TW>(s);
+    biases[(int64_t)o * ngroups + g] = from_f32<TW>(mn);
+  }
+}
+
 }  // namespace rwkv7mi
 
 using namespace rwkv7mi;
+
+extern "C" int rwkv7mi_w4a_pack(const void* weight, int64_t O, int64_t I, int64_t group, int w_dtype,
+                                uint8_t* packed, void* scales, void* biases, void* stream) {
+  if (group != 128 && group != 256) return fail(RWKV7MI_EINVAL, "w4a_pack: group must be 128 or 256");
+  if (O <= 0 || I <= 0 || I % group) return fail(RWKV7MI_EINVAL, "w4a_pack: I must be a positive multiple of group");
+  if (O * (I / group) > INT32_MAX || I > INT32_MAX) return fail(RWKV7MI_EINVAL, "w4a_pack: too large");
+  if (!weight || !packed || !scales || !biases) return fail(RWKV7MI_EINVAL, "w4a_pack: null pointer");
+  return dispatch_dtype(w_dtype, [&](auto tw) {
+    using TW = decltype(tw);
+    hipLaunchKernelGGL((w4a_pack_kernel<TW>), dim3((unsigned)(O * (I / group))), dim3(64), 0, as_stream(stream),
+                       (const TW*)weight, (int)O, (int)I, (int)group, packed, (TW*)scales, (TW*)biases);
+    return check_launch("w4a_pack_kernel");
+  });
+}
 
 extern "C" int rwkv7mi_w4g_pack(const void* weight, int64_t O, int64_t I, int64_t group, int w_dtype,
                                 uint8_t* packed, void* scales, void* stream) {
@@ -179,19 +250,20 @@ extern "C" int rwkv7mi_w4g_pack(const void* weight, int64_t O, int64_t I, int64_
   });
 }
 
-extern "C" int rwkv7mi_w4g_matmul(const void* x, const uint8_t* packed, const void* scales, const void* bias,
-                                  const void* residual, void* y, int64_t rows, int64_t O, int64_t I,
-                                  int64_t group, int epilogue, int act_dtype, int scale_dtype, void* stream) {
-  if (group != 128 && group != 256) return fail(RWKV7MI_EINVAL, "w4g_matmul: group must be 128 or 256");
-  if (rows < 0 || O <= 0 || I <= 0 || I % group) return fail(RWKV7MI_EINVAL, "w4g_matmul: bad shape");
+static int w4_matmul(const char* who, const void* x, const uint8_t* packed, const void* scales, const void* gbias,
+                     const void* bias, const void* residual, void* y, int64_t rows, int64_t O, int64_t I,
+                     int64_t group, int epilogue, int act_dtype, int scale_dtype, void* stream) {
+  const std::string w(who);
+  if (group != 128 && group != 256) return fail(RWKV7MI_EINVAL, w + ": group must be 128 or 256");
+  if (rows < 0 || O <= 0 || I <= 0 || I % group) return fail(RWKV7MI_EINVAL, w + ": bad shape");
   if (rows == 0) return RWKV7MI_OK;
-  if (O > INT32_MAX || I > INT32_MAX) return fail(RWKV7MI_EINVAL, "w4g_matmul: too large");
-  if (!x || !packed || !scales || !y) return fail(RWKV7MI_EINVAL, "w4g_matmul: null pointer");
-  if (epilogue < 0 || epilogue > 2) return fail(RWKV7MI_EINVAL, "w4g_matmul: bad epilogue");
-  if (epilogue == RWKV7MI_EPI_RESIDUAL && !residual) return fail(RWKV7MI_EINVAL, "w4g_matmul: residual missing");
+  if (O > INT32_MAX || I > INT32_MAX) return fail(RWKV7MI_EINVAL, w + ": too large");
+  if (!x || !packed || !scales || !y) return fail(RWKV7MI_EINVAL, w + ": null pointer");
+  if (epilogue < 0 || epilogue > 2) return fail(RWKV7MI_EINVAL, w + ": bad epilogue");
+  if (epilogue == RWKV7MI_EPI_RESIDUAL && !residual) return fail(RWKV7MI_EINVAL, w + ": residual missing");
   if ((reinterpret_cast<uintptr_t>(packed) | reinterpret_cast<uintptr_t>(x)) & 15)
-    return fail(RWKV7MI_EINVAL, "w4g_matmul: x and packed must be 16-byte aligned");
-  if (!valid_dtype(act_dtype) || !valid_dtype(scale_dtype)) return fail(RWKV7MI_EINVAL, "w4g_matmul: bad dtype");
+    return fail(RWKV7MI_EINVAL, w + ": x and packed must be 16-byte aligned");
+  if (!valid_dtype(act_dtype) || !valid_dtype(scale_dtype)) return fail(RWKV7MI_EINVAL, w + ": bad dtype");
   const size_t esz = act_dtype == RWKV7MI_F32 ? 4 : 2;
   for (int64_t r0 = 0; r0 < rows; r0 += 64) {
     const int64_t nr = rows - r0 > 64 ? 64 : rows - r0;
@@ -204,13 +276,19 @@ extern "C" int rwkv7mi_w4g_matmul(const void* x, const uint8_t* packed, const vo
       return dispatch_dtype(scale_dtype, [&](auto ts) {
         using TS = decltype(ts);
         dim3 grid((unsigned)((O + 15) / 16));
-#define W4_LAUNCH(MT_)                                                                              \
-  hipLaunchKernelGGL((w4g_kernel<MT_, TA, TS>), grid, dim3(256), 0, as_stream(stream), (const TA*)xr, \
-                     packed, (const TS*)scales, (const TS*)bias, (const TA*)rr, (TA*)yr, (int)nr,     \
-                     (int)O, (int)I, (int)group, epilogue)
-        if (mt == 1) W4_LAUNCH(1);
-        else if (mt == 2) W4_LAUNCH(2);
-        else W4_LAUNCH(4);
+#define W4_LAUNCH(MT_, AFF_)                                                                              \
+  hipLaunchKernelGGL((w4g_kernel<MT_, TA, TS, AFF_>), grid, dim3(256), 0, as_stream(stream), (const TA*)xr, \
+                     packed, (const TS*)scales, (const TS*)gbias, (const TS*)bias, (const TA*)rr, (TA*)yr,   \
+                     (int)nr, (int)O, (int)I, (int)group, epilogue)
+        if (gbias) {
+          if (mt == 1) W4_LAUNCH(1, true);
+          else if (mt == 2) W4_LAUNCH(2, true);
+          else W4_LAUNCH(4, true);
+        } else {
+          if (mt == 1) W4_LAUNCH(1, false);
+          else if (mt == 2) W4_LAUNCH(2, false);
+          else W4_LAUNCH(4, false);
+        }
 #undef W4_LAUNCH
         return check_launch("w4g_kernel");
       });
@@ -218,4 +296,20 @@ extern "C" int rwkv7mi_w4g_matmul(const void* x, const uint8_t* packed, const vo
     if (rc) return rc;
   }
   return RWKV7MI_OK;
+}
+
+extern "C" int rwkv7mi_w4g_matmul(const void* x, const uint8_t* packed, const void* scales, const void* bias,
+                                  const void* residual, void* y, int64_t rows, int64_t O, int64_t I,
+                                  int64_t group, int epilogue, int act_dtype, int scale_dtype, void* stream) {
+  return w4_matmul("w4g_matmul", x, packed, scales, nullptr, bias, residual, y, rows, O, I, group, epilogue,
+                   act_dtype, scale_dtype, stream);
+}
+
+extern "C" int rwkv7mi_w4a_matmul(const void* x, const uint8_t* packed, const void* scales, const void* biases,
+                                  const void* bias, const void* residual, void* y, int64_t rows, int64_t O,
+                                  int64_t I, int64_t group, int epilogue, int act_dtype, int scale_dtype,
+                                  void* stream) {
+  if (!biases) return fail(RWKV7MI_EINVAL, "w4a_matmul: null group biases");
+  return w4_matmul("w4a_matmul", x, packed, scales, biases, bias, residual, y, rows, O, I, group, epilogue,
+                   act_dtype, scale_dtype, stream);
 }

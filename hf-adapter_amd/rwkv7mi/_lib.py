@@ -80,6 +80,8 @@ SIGNATURES = {
         [_c_p] * 4 + [_i64] + [_c_p] * 5 + [_i64, _i64] + [_c_p] * 9 + [_i32, _i64, _i64, _i64, _f32, _i32, _i32, _c_p],
     ),
     "rwkv7mi_w4g_pack": (_i32, [_c_p, _i64, _i64, _i64, _i32, _c_p, _c_p, _c_p]),
+    "rwkv7mi_w4a_pack": (_i32, [_c_p, _i64, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p]),
+    "rwkv7mi_w4a_matmul": (_i32, [_c_p] * 7 + [_i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_p]),
     "rwkv7mi_w4g_matmul": (
         _i32,
         [_c_p] * 6 + [_i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_p],

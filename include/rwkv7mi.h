@@ -400,6 +400,25 @@ int rwkv7mi_w4g_matmul(const void* x, const uint8_t* packed,
                        int64_t I, int64_t group, int epilogue, int act_dtype,
                        int scale_dtype, void* stream);
 
+/* Asymmetric group-wise W4 (min/max affine, group 128 / 256): per (row o,
+ * group g) s = max((max - min) / 15, 1e-8), b = min, q = clamp(rint((w - b)
+ * / s), 0, 15) in fp32; packed [O, I/2] as rwkv7mi_w4g_pack (low nibble =
+ * even input), scales and biases [O, I/group] in the weight dtype;
+ * W[o,i] = q s + b.  The reference's only asymmetric group format is MLX's
+ * affine mode (rwkv7_hf/mlx_quant.py:258-290, Apple only), which this format
+ * follows in form; its parity with MLX is unpinned (no MLX here). */
+int rwkv7mi_w4a_pack(const void* weight, int64_t O, int64_t I, int64_t group,
+                     int w_dtype, uint8_t* packed, void* scales, void* biases,
+                     void* stream);
+/* y = epilogue(x W^T + bias) with the affine W above; rows any, fp32
+ * accumulation, the same epilogues as rwkv7mi_w4g_matmul. */
+int rwkv7mi_w4a_matmul(const void* x, const uint8_t* packed,
+                       const void* scales, const void* biases,
+                       const void* bias, const void* residual, void* y,
+                       int64_t rows, int64_t O, int64_t I, int64_t group,
+                       int epilogue, int act_dtype, int scale_dtype,
+                       void* stream);
+
 /* ------------------------------------------------ LayerNorm + token shift */
 
 /* Decode LN + six token-shift mixes per row (D <= 8192):

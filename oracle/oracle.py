@@ -183,6 +183,40 @@ def w4g_linear(x, packed, scales, group: int = 128):
     return np.asarray(x, np.float64) @ w4g_dequant(packed, scales, group).T
 
 
+# ----------------------------------------------- W4 group, asymmetric (affine)
+def w4a_pack(W: np.ndarray, group: int = 128, out_dtype=np.float16):
+    """Min/max affine group W4 for W [O, I], in fp32 numpy arithmetic (IEEE
+    correctly rounded, round half to even): per (o, group) s = max((max - min)
+    / 15, 1e-8), b = min, q = clamp(rint((w - b) / s), 0, 15); returns
+    (packed [O, I/2] (low nibble = even input), scales, biases [O, I/group]).
+    This build's own asymmetric format: it follows the form of MLX's affine
+    mode (rwkv7_hf/mlx_quant.py:258-290, whose arithmetic lives in MLX, not in
+    the reference) — parity with MLX is unpinned."""
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    o, i = W.shape
+    g = W.reshape(o, i // group, group)
+    mn = g.min(-1)
+    mx = g.max(-1)
+    s = np.maximum((mx - mn) / np.float32(15.0), np.float32(1e-8)).astype(np.float32)
+    q = np.clip(np.rint((g - mn[..., None]) / s[..., None]), 0, 15).astype(np.uint8).reshape(o, i)
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    return packed, s.astype(out_dtype), mn.astype(out_dtype)
+
+
+def w4a_dequant(packed, scales, biases, group: int = 128):
+    """fp64 W[o, i] = q[o, i] * scales[o, i // group] + biases[o, i // group]."""
+    p = np.asarray(packed)
+    q = np.empty((p.shape[0], p.shape[1] * 2), np.float64)
+    q[:, 0::2] = (p & 15).astype(np.float64)
+    q[:, 1::2] = (p >> 4).astype(np.float64)
+    rep = lambda t: np.repeat(np.asarray(t, np.float64), group, axis=1)
+    return q * rep(scales) + rep(biases)
+
+
+def w4a_linear(x, packed, scales, biases, group: int = 128):
+    return np.asarray(x, np.float64) @ w4a_dequant(packed, scales, biases, group).T
+
+
 # ------------------------------------------------------------ MM4 affine
 def mm4_pack(W: np.ndarray, out_dtype=np.float16):
     """quantize_mm4 (rwkv7_hf/native_quant_mm4.py:77-105) for W [N_in, M_out]."""

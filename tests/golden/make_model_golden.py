@@ -10,7 +10,8 @@ the build container, where the reference is available read-only at
 Weights are this build's name-keyed random init (rwkv7mi.model.random_weights,
 seed 0), loaded into the reference model by parameter name; token ids are
 uniform with seed 0.  Each fixture holds the prompt ids, the reference's
-last-position logits after the prompt, and its greedy continuation.
+last-position logits after the prompt, its greedy continuation, and per
+greedy step the top-1 / top-2 logit margin and max |logit|.
 
 Run: python tests/golden/make_model_golden.py [names...]   (tiny, c1)
 """
@@ -31,10 +32,10 @@ CONFIGS = {
     "tiny": dict(vocab_size=512, hidden_size=128, num_hidden_layers=2, intermediate_size=256,
                  decay_low_rank_dim=32, a_low_rank_dim=32, gate_low_rank_dim=64, v_low_rank_dim=32,
                  prompt=24, steps=8),
-    # the 0.1B architecture (short prompt, fp32)
+    # the 0.1B architecture, a 512-token prompt and 64 greedy steps (fp32)
     "c1": dict(vocab_size=65536, hidden_size=768, num_hidden_layers=12, intermediate_size=3072,
                decay_low_rank_dim=64, a_low_rank_dim=64, gate_low_rank_dim=128, v_low_rank_dim=32,
-               prompt=32, steps=8),
+               prompt=512, steps=64),
 }
 
 
@@ -61,10 +62,16 @@ def main(names):
         ids = torch.tensor(np.random.default_rng(0).integers(0, c["vocab_size"], (1, prompt)), dtype=torch.long)
         with torch.no_grad():
             logits = ref(input_ids=ids).logits[0, -1].float().numpy()
-            gen = ref.generate(ids, max_new_tokens=steps, do_sample=False)
+            gen = ref.generate(ids, max_new_tokens=steps, do_sample=False, output_scores=True,
+                               return_dict_in_generate=True)
+        # per greedy step: the reference's top-1 minus top-2 logit and its max |logit|,
+        # so a lower-precision run can be held to the ids the margins decide
+        scores = torch.stack([sc[0].float() for sc in gen.scores])
+        top2 = scores.topk(2, dim=-1).values
         out = HERE / f"model_{name}.npz"
-        np.savez_compressed(out, ids=ids.numpy(), logits=logits, greedy=gen[0, prompt:].numpy())
-        print(f"wrote {out}: greedy {gen[0, prompt:].tolist()}")
+        np.savez_compressed(out, ids=ids.numpy(), logits=logits, greedy=gen.sequences[0, prompt:].numpy(),
+                            margins=(top2[:, 0] - top2[:, 1]).numpy(), scale=scores.abs().amax(-1).numpy())
+        print(f"wrote {out}: greedy {gen.sequences[0, prompt:].tolist()}")
 
 
 if __name__ == "__main__":

@@ -158,3 +158,23 @@ def test_quantize_model_mm4_group_policy():
     y = net(torch.randn(2, 512, device="cuda", dtype=torch.float16))
     torch.cuda.synchronize()
     assert y.shape == (2, 256) and torch.isfinite(y).all()
+
+
+@pytest.mark.parametrize("rows", [1, 4, 16])
+def test_mm4_head_shape_c4(oracle, rows):
+    """BASELINE configs[3]'s head shape, 4096 x 65536, on the MM4 affine GEMV."""
+    from rwkv7mi.native_quant_mm4 import mm4t_matmul_into, quantize_mm4, quantize_mm4_outmajor
+
+    I, O = 4096, 65536
+    rng = np.random.default_rng(7 + rows)
+    Wl = torch.randn(O, I, device="cuda", dtype=torch.float16, generator=torch.Generator("cuda").manual_seed(rows))
+    Wl *= 0.02
+    pt, mx, rx, my, ry, m_orig, _ = quantize_mm4_outmajor(Wl)
+    ref_layout = quantize_mm4(Wl.t().contiguous())
+    x = rng.standard_normal((rows, I)).astype(np.float16)
+    out = torch.empty(rows, O, device="cuda", dtype=torch.float16)
+    mm4t_matmul_into(_cuda(x, torch.float16), pt, mx, rx, my.reshape(-1), ry.reshape(-1), out)
+    torch.cuda.synchronize()
+    deq = oracle.mm4_dequant(*(_np(t) for t in ref_layout[:5]), m_orig)
+    ref = x.astype(np.float64) @ deq
+    assert _rel_err(_np(out).astype(np.float64), ref) <= 2e-3

@@ -125,3 +125,64 @@ def test_w4g_linear(oracle, OI, rows, dtype):
     torch.cuda.synchronize()
     ref = oracle.w4g_linear(_np(x).astype(np.float64), _np(packed), _np(scales.to(dtype)).astype(np.float64))
     assert _rel_err(_np(y).astype(np.float64), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("group", [128, 256])
+@pytest.mark.parametrize("shape", [(6, 512), (4096, 4096)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_w4a_pack_bit_exact(oracle, group, shape, dtype):
+    """Asymmetric (min/max affine) group W4: packed nibbles, scales and biases
+    bit-identical to the oracle's fp32 restatement."""
+    from rwkv7mi.sm70_quant import quantize_w4_affine_groupwise
+
+    rng = np.random.default_rng(shape[0] + group)
+    Wt = _cuda(rng.standard_normal(shape) * 0.02, dtype)
+    packed, scales, biases, k = quantize_w4_affine_groupwise(Wt, group_size=group)
+    torch.cuda.synchronize()
+    op, osc, obi = oracle.w4a_pack(_np(Wt.float()), group, out_dtype=np.float32)
+    assert k == shape[1]
+    np.testing.assert_array_equal(_np(packed), op)
+    cast = lambda a: _np(torch.tensor(a).to(dtype).float())
+    np.testing.assert_array_equal(_np(scales.float()), cast(osc))
+    np.testing.assert_array_equal(_np(biases.float()), cast(obi))
+
+
+@pytest.mark.parametrize("OI", [(4096, 4096), (16384, 4096), (4096, 16384), (256, 512)])
+@pytest.mark.parametrize("rows", [1, 4, 16, 40])
+def test_w4a_linear(oracle, OI, rows):
+    from rwkv7mi.sm70_quant import quantize_w4_affine_groupwise, w4_affine_groupwise_linear
+
+    O, I = OI
+    rng = np.random.default_rng(O + 3 * I + rows)
+    W = _cuda(rng.standard_normal((O, I)) * 0.02, torch.float16)
+    packed, scales, biases, _ = quantize_w4_affine_groupwise(W)
+    x = _cuda(rng.standard_normal((rows, I)), torch.float16)
+    y = w4_affine_groupwise_linear(x, packed, scales, biases, O, I)
+    torch.cuda.synchronize()
+    ref = oracle.w4a_linear(_np(x).astype(np.float64), _np(packed), _np(scales), _np(biases))
+    assert _rel_err(_np(y).astype(np.float64), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("rows", [1, 4, 16])
+def test_w4_head_shape_c4(oracle, rows):
+    """BASELINE configs[3]'s vocabulary head, 4096 x 65536, through the
+    symmetric group-128 W4 and the asymmetric (affine) form, at its batch
+    sizes 1 / 4 / 16."""
+    from rwkv7mi import quantize_w4_groupwise, w4_groupwise_linear
+    from rwkv7mi.sm70_quant import quantize_w4_affine_groupwise, w4_affine_groupwise_linear
+
+    O, I = 65536, 4096
+    rng = np.random.default_rng(65536 + rows)
+    W = torch.randn(O, I, device="cuda", dtype=torch.float16, generator=torch.Generator("cuda").manual_seed(rows))
+    W *= 0.02
+    x = _cuda(rng.standard_normal((rows, I)), torch.float16)
+    packed, scales, _ = quantize_w4_groupwise(W)
+    y = w4_groupwise_linear(x, packed, scales, O, I)
+    torch.cuda.synchronize()
+    ref = oracle.w4g_linear(_np(x).astype(np.float64), _np(packed), _np(scales))
+    assert _rel_err(_np(y).astype(np.float64), ref) <= 2e-3
+    pa, sa, ba, _ = quantize_w4_affine_groupwise(W)
+    ya = w4_affine_groupwise_linear(x, pa, sa, ba, O, I)
+    torch.cuda.synchronize()
+    refa = oracle.w4a_linear(_np(x).astype(np.float64), _np(pa), _np(sa), _np(ba))
+    assert _rel_err(_np(ya).astype(np.float64), refa) <= 2e-3

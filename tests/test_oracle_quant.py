@@ -110,3 +110,43 @@ def test_mm4_invariants(oracle):
     deq = oracle.mm4_dequant(packed, mx, rx4, my, ry4, m_orig)
     bound = (np.asarray(ry4, np.float64).reshape(-1, 1) * 4) * (np.asarray(rx4, np.float64).reshape(1, -1)[:, :31] * 4) / 32
     assert (np.abs(deq - W) <= bound * (1 + 1e-5) + 1e-7).all()
+
+
+def test_w4a_pack_closed_forms(oracle):
+    """The asymmetric (min/max affine) group W4 packer: in every non-constant
+    group the minimum maps to 0 and the maximum to 15; a constant group is
+    reproduced exactly by its bias; the reconstruction error is at most half a
+    step plus the fp16 rounding of scale and bias; a hand-computed known answer
+    (a ramp whose step is exactly representable) and a planted mistake (a
+    symmetric-style centring) that the bound catches."""
+    rng = np.random.default_rng(41)
+    O, I, G = 6, 512, 128
+    W = (rng.standard_normal((O, I)) * 0.02).astype(np.float32)
+    W[2, 128:256] = 0.0125  # a constant group
+    packed, sc, bi = oracle.w4a_pack(W, G)
+    q = np.empty((O, I), np.uint8)
+    q[:, 0::2], q[:, 1::2] = packed & 15, packed >> 4
+    qg = q.reshape(O, I // G, G)
+    for o in range(O):
+        for g in range(I // G):
+            grp = W[o, g * G:(g + 1) * G]
+            if grp.max() > grp.min():
+                assert qg[o, g][grp.argmin()] == 0 and qg[o, g][grp.argmax()] == 15
+            else:
+                assert (qg[o, g] == 0).all()
+    deq = oracle.w4a_dequant(packed, sc, bi, G)
+    assert deq[2, 128:256].tolist() == [float(np.float16(0.0125))] * 128
+    s32 = np.repeat(((W.reshape(O, -1, G).max(-1) - W.reshape(O, -1, G).min(-1)) / 15), G, axis=1)
+    bound = s32 / 2 + 15 * np.abs(s32) * 2.0 ** -11 + np.abs(W).max() * 2.0 ** -11
+    assert (np.abs(deq - W) <= bound + 1e-12).all()
+    # known answer: w = 0.25 * j - 1 over one group of 128 (j = 0..127 -> q = rint(j * 15 / 127))
+    ramp = (0.25 * np.arange(128, dtype=np.float32) - 1.0)[None]
+    p2, s2, b2 = oracle.w4a_pack(ramp, 128)
+    assert float(b2[0, 0]) == -1.0 and float(s2[0, 0]) == float(np.float16(np.float32(31.75) / np.float32(15)))
+    q2 = np.empty(128, np.uint8)
+    q2[0::2], q2[1::2] = p2[0] & 15, p2[0] >> 4
+    np.testing.assert_array_equal(q2, np.rint(np.arange(128) * (0.25 / np.float32(31.75 / 15))).clip(0, 15))
+    # planted: centring each group on 0 instead of its minimum breaks the bound
+    planted = (np.clip(np.rint(W.reshape(O, -1, G) / s32.reshape(O, -1, G)[..., :1]), -8, 7)
+               * s32.reshape(O, -1, G)[..., :1]).reshape(O, I)
+    assert (np.abs(planted - W) > bound).any()
