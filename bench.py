@@ -3,18 +3,24 @@
 "decode tok/s 7.2B MM8 bsz1/8; wkv7 prefill tok/s; % HBM roofline").
 
 Workloads (synthetic inputs, random-init weights; nothing is downloaded):
-  decode : RWKV-7 7.2B architecture (L=32, D=4096,
-           H=64, N=64, F=16384, V=65536, LoRA 64/64/128/32) with MM8 weights
-           (memory policy: every Linear >= 8M weights), fp16 activations, fp32
-           state; a 16-token prefill, then hipGraph-replayed greedy decode steps
-           at bsz 1, 8 and 64.  One step = one token for every row, the full model.
-  scan   : the wkv7 chunked prefill scan: B=8, T=4096, H=32, N=64,
-           r,k,v ~ N(0,1) fp16, k L2-normalised, kk = k, a = sigmoid(N(0,1)),
-           w = exp(-exp(x)), x ~ N(-0.5, 0.5), fp32 state from zero.
-The default run measures both and prints ONE JSON line whose ``value`` is the
-bsz-1 decode throughput; bsz 8 and 64 and the scan are reported alongside.
+  decode  : BASELINE configs[4], the RWKV-7 7.2B architecture (L=32, D=4096,
+            H=64, N=64, F=16384, V=65536, LoRA 64/64/128/32) with MM8 weights
+            (memory policy: every Linear with >= 8M weights, 193 modules), fp16
+            activations, fp32 state; a 16-token prefill, then hipGraph-replayed
+            greedy decode steps at bsz 1 (the headline ``value``), 8 and 64.
+            One step = one token for every row through the full model.
+  scan    : configs[1], the wkv7 chunked prefill scan B=8, T=4096, N=64 at
+            H=32 and H=64: r,k,v ~ N(0,1) fp16, k L2-normalised, kk = k,
+            a = sigmoid(N(0,1)), w = exp(-exp(x)), x ~ N(-0.5, 0.5), fp32 state;
+            and its decode form, one single-token update (B=8, H=32) with the
+            state in HBM.
+  gemv    : configs[2], MM8 GEMV/GEMM at the 1.5B shapes x batch 1/8/32, and
+            configs[3], group-128 W4 (asymmetric min/max affine, and the
+            reference's symmetric form) at the 7.2B shapes x batch 1/4/16.
+  prefill : configs[4]'s prefill, B=8 x T=4096 through the 7.2B model.
+The default run measures all of them and prints ONE JSON line.
 
-    python bench.py [--steps K] [--warmup W] [--workload decode|scan|all] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload all|decode|scan|gemv|prefill|...] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -30,6 +36,28 @@ sys.path.insert(0, str(ROOT / "hf-adapter_amd"))
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def host_cores() -> int:
+    """Host threads this process may use: its CPU affinity, capped by OMP_NUM_THREADS."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return min(n, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else n
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 # ------------------------------------------------------------------ byte models
@@ -45,7 +73,6 @@ def decode_step_bytes(cfg, B, quantized: set[str], shapes: dict):
     1 B/weight + fp16 row/col metadata; others fp16), the recurrent state read +
     written, shift states read + written, embedding rows and logits."""
     total = 0
-    mm8 = 0
     for name, shp in shapes.items():
         if name == "model.embeddings.weight":
             total += B * shp[1] * 2
@@ -56,37 +83,31 @@ def decode_step_bytes(cfg, B, quantized: set[str], shapes: dict):
         base = name[: -len(".weight")] if name.endswith(".weight") else None
         if base is not None and base in quantized:
             o, i = shp
-            b = o * i + 2 * (i + o) * 2
-            mm8 += b + B * (i + o) * 2
-            total += b
+            total += o * i + 2 * (i + o) * 2
         else:
             total += n * 2
     L, H, N, D = cfg.num_hidden_layers, cfg.num_heads, cfg.head_dim, cfg.hidden_size
     total += L * B * H * N * N * 4 * 2          # state read + write
     total += L * 2 * B * D * 2 * 2               # xpa / xpf read + write
     total += B * cfg.vocab_size * 2               # logits
-    return total, mm8
+    return total
 
 
-# ------------------------------------------------------------------ scan
-def make_scan_inputs(B, T, H, N, seed=0, device="cuda"):
-    import torch
-
-    g = torch.Generator(device=device)
-    g.manual_seed(seed)
-    r = torch.randn(B, T, H, N, generator=g, device=device).half()
-    k = torch.randn(B, T, H, N, generator=g, device=device)
-    k = (k / k.norm(dim=-1, keepdim=True).clamp_min(1e-12)).half()
-    v = torch.randn(B, T, H, N, generator=g, device=device).half()
-    kk = k.clone()
-    a = torch.sigmoid(torch.randn(B, T, H, N, generator=g, device=device)).half()
-    x = torch.randn(B, T, H, N, generator=g, device=device) * 0.5 - 0.5
-    w = torch.exp(-torch.exp(x)).float()
-    state = torch.zeros(B, H, N, N, device=device, dtype=torch.float32)
-    return r, w, k, v, kk, a, state
+def mm8_bytes(I, O, rows):
+    """One MM8 product: weights (1 B each), fp16 row/column metadata, activations in and out."""
+    return I * O + 2 * (I + O) * 2 + rows * (I + O) * 2
 
 
+def w4_bytes(I, O, rows, group=128, affine=True):
+    """One group W4 product: nibbles, fp16 scales (and biases), activations in and out."""
+    return I * O // 2 + (I * O // group) * 2 * (2 if affine else 1) + rows * (I + O) * 2
+
+
+# ------------------------------------------------------------------ timing
 def time_events(fn, steps, warmup):
+    """W untimed calls, then K timed ones between HIP events on the current
+    stream, with a device synchronisation on both sides; returns (mean ms per
+    call, wall seconds of the timed region)."""
     import torch
 
     for _ in range(warmup):
@@ -105,6 +126,54 @@ def time_events(fn, steps, warmup):
     return sum(per) / len(per), wall
 
 
+def time_graph(calls, reps=20):
+    """Capture ``calls`` (a list of launch closures) in one hipGraph, replay it
+    ``reps`` times back to back between two HIP events on the launch stream;
+    returns the mean ms per call."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for c in calls:
+            c()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in calls:
+            c()
+    graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * len(calls))
+    del graph
+    return ms
+
+
+# ------------------------------------------------------------------ scan (configs[1])
+def make_scan_inputs(B, T, H, N, seed=0, device="cuda"):
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    r = torch.randn(B, T, H, N, generator=g, device=device).half()
+    k = torch.randn(B, T, H, N, generator=g, device=device)
+    k = (k / k.norm(dim=-1, keepdim=True).clamp_min(1e-12)).half()
+    v = torch.randn(B, T, H, N, generator=g, device=device).half()
+    kk = k.clone()
+    a = torch.sigmoid(torch.randn(B, T, H, N, generator=g, device=device)).half()
+    x = torch.randn(B, T, H, N, generator=g, device=device) * 0.5 - 0.5
+    w = torch.exp(-torch.exp(x)).float()
+    state = torch.zeros(B, H, N, N, device=device, dtype=torch.float32)
+    return r, w, k, v, kk, a, state
+
+
 def run_scan(B=8, T=4096, H=32, steps=20, warmup=3):
     from rwkv7mi import self_chunk_rwkv7
 
@@ -115,6 +184,27 @@ def run_scan(B=8, T=4096, H=32, steps=20, warmup=3):
     gbs = nbytes / (ms / 1e3) / 1e9
     return {"tok_s": B * T / (ms / 1e3), "ms": ms, "wall_s": wall, "bytes": nbytes, "gbs": gbs,
             "frac": gbs / HBM_PEAK_GBS, "config": f"B={B} T={T} H={H} N={N} chunk=16"}
+
+
+def run_decode_form_step(B=8, H=32, reps=20):
+    """configs[1]'s decode form: one single-token DPLR update per launch with
+    the state read from and written to HBM (16 state buffers in rotation, 64 MB,
+    so the state is not cache-resident between launches)."""
+    import torch
+    from rwkv7mi import fused_recurrent_update
+
+    N = 64
+    r, w, k, v, kk, a, _ = make_scan_inputs(B, 1, H, N)
+    one = [t[:, 0].contiguous() for t in (r, w, k, v, kk, a)]
+    states = [torch.zeros(B, H, N, N, device="cuda") for _ in range(16)]
+    outs = [torch.empty(B, H, N, device="cuda", dtype=torch.float16) for _ in range(16)]
+    calls = [(lambda s=s, o=o: fused_recurrent_update(*one, s, state_out=s, out=o)) for s, o in zip(states, outs)]
+    ms = time_graph(calls, reps)
+    nbytes = B * H * (2 * N * N * 4 + N * 2 * 5 + N * 4 + N * 2)
+    gbs = nbytes / (ms / 1e3) / 1e9
+    return {"us_per_step": round(ms * 1e3, 3), "bytes": nbytes, "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "tok_s": round(B / (ms / 1e3), 1),
+            "config": f"B={B} H={H} N={N}, one token, fp32 state in HBM"}
 
 
 def cpu_scan_baseline(B=8, H=32, N=64, T_sample=1024, seed=0, min_seconds=10.0):
@@ -139,12 +229,13 @@ def cpu_scan_baseline(B=8, H=32, N=64, T_sample=1024, seed=0, min_seconds=10.0):
         dt = time.perf_counter() - t0
         if dt >= min_seconds:
             break
-    return {"value": B * T_sample * reps / dt, "unit": "tok/s", "cores": oracle.num_threads(), "kind": "port",
+    return {"value": round(B * T_sample * reps / dt, 1), "unit": "tok/s", "cores": oracle.num_threads(),
+            "kind": "port", "cpu": cpu_model(),
             "sample": f"wkv7 scan: fp32 C sequential restatement (OpenMP over heads), B={B} T={T_sample} H={H} "
                       f"N={N}, {reps} reps in {dt:.1f} s"}
 
 
-# ------------------------------------------------------------------ decode
+# ------------------------------------------------------------------ decode (configs[4])
 def config_7p2b():
     from rwkv7mi.model import NativeRWKV7Config
 
@@ -153,86 +244,96 @@ def config_7p2b():
                              use_native_mm8=True, native_mm8_min_params=8_000_000, native_mm8_policy="memory")
 
 
-def run_decode(batches=(1, 8), steps=64, warmup=5, log=print):
+def build_7p2b():
     import torch
-    from rwkv7mi.model import NativeRWKV7ForCausalLM, QuantLinear, parameter_shapes
+    from rwkv7mi.model import NativeRWKV7ForCausalLM, QuantLinear
 
     cfg = config_7p2b()
     t0 = time.perf_counter()
     model = NativeRWKV7ForCausalLM.from_random(cfg, seed=0, device="cuda", dtype=torch.float16)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
-    log(f"bench: 7.2B MM8 model built in {build_s:.1f} s ({model._rwkv7_native_mm_replaced_modules} MM8 modules)")
-    shapes = parameter_shapes(cfg)
-    quantized = set()
     named = {"lm_head": model.lm_head}
     for L in model.layers:
         p = f"model.layers.{L.idx}."
         named.update({p + "attn.r_proj": L.r_proj, p + "attn.k_proj": L.k_proj, p + "attn.v_proj": L.v_proj,
                       p + "attn.o_proj": L.o_proj, p + "ffn.key": L.key, p + "ffn.value": L.value})
-    for n, lin in named.items():
-        if isinstance(lin, QuantLinear):
-            quantized.add(n)
-    res = {"build_s": build_s, "mm8_modules": len(quantized)}
+    quantized = {n for n, lin in named.items() if isinstance(lin, QuantLinear)}
+    _log(f"bench: 7.2B MM8 model built in {build_s:.1f} s ({len(quantized)} MM8 modules)")
+    return cfg, model, quantized
+
+
+def run_decode(model, cfg, quantized, batches=(1, 8, 64), steps=64, warmup=5):
+    import torch
+    from rwkv7mi.model import parameter_shapes
+
+    shapes = parameter_shapes(cfg)
+    res = {}
     g = torch.Generator(device="cuda")
     g.manual_seed(0)
     for B in batches:
         prompt = torch.randint(0, cfg.vocab_size, (B, 16), generator=g, device="cuda")
         out = model(prompt)
-        logits, cache = out.logits, out.past_key_values
+        cache = out.past_key_values
         runner = model.graph_runner(B)
-        tok = logits[:, -1].argmax(-1)
-        state = {"tok": tok}
+        state = {"tok": out.logits[:, -1].argmax(-1)}
 
         def step():
             lg = runner.replay(state["tok"], cache)
             state["tok"] = lg.argmax(-1)
 
         ms, wall = time_events(step, steps, warmup)
-        nbytes, mm8b = decode_step_bytes(cfg, B, quantized, shapes)
+        nbytes = decode_step_bytes(cfg, B, quantized, shapes)
         gbs = nbytes / (ms / 1e3) / 1e9
         res[B] = {"tok_s": B / (ms / 1e3), "ms": ms, "wall_s": wall, "bytes": nbytes, "gbs": gbs,
                   "frac": gbs / HBM_PEAK_GBS}
-        log(f"bench: decode bsz {B}: {ms:.3f} ms/step, {B / (ms / 1e3):.1f} tok/s, {gbs:.0f} GB/s")
-    # MM8 GEMV roofline: the MM8 launches of one bsz-1 decode step (the same
-    # modules, shapes and buffers), captured alone in a hipGraph and replayed
-    # back to back between two HIP events on the launch stream; the average
-    # launch duration is the elapsed time over all launches.
+        _log(f"bench: decode bsz {B}: {ms:.3f} ms/step, {B / (ms / 1e3):.1f} tok/s, {gbs:.0f} GB/s "
+             f"({100 * gbs / HBM_PEAK_GBS:.1f}% of the step roofline)")
+        del model._graph_runners[B]
+    return res
+
+
+def run_mm8_roofline(model, cfg, reps=20):
+    """The MM8 launches of one bsz-1 decode step (the same modules, shapes and
+    buffers) recorded from an eager step, captured alone in a hipGraph and
+    replayed back to back between two HIP events on the launch stream: the
+    average launch duration and its algorithmic bytes."""
+    import torch
+    import rwkv7mi.model as model_mod
+    from rwkv7mi.model import QuantLinear
+
     B = 1
     cache = model.new_cache(B)
     toks = torch.zeros(B, dtype=torch.long, device="cuda")
     logits = torch.empty(B, cfg.vocab_size, device="cuda", dtype=torch.float16)
     bufs = model._decode_buffers(B)
     calls, nbytes = [], []
-    orig_apply, orig_group = QuantLinear.apply, QuantLinear.apply_group
-
-    def mm8_bytes(lin, rows):
-        i, o = lin.in_features, lin.out_features
-        return o * i + 2 * (i + o) * 2 + rows * (i + o) * 2
+    orig_apply, orig_group, orig_lnmix = QuantLinear.apply, QuantLinear.apply_group, model_mod.mm8_lnmix_multi_into
 
     def rec_apply(self, x2, out, **kw):
         calls.append(lambda: orig_apply(self, x2, out, **kw))
-        nbytes.append(mm8_bytes(self, int(x2.shape[0])))
+        nbytes.append(mm8_bytes(self.in_features, self.out_features, int(x2.shape[0])))
         return orig_apply(self, x2, out, **kw)
 
     def rec_group(lins, xs, outs):
         calls.append(lambda: orig_group(lins, xs, outs))
-        nbytes.append(sum(mm8_bytes(l, int(x.shape[0])) for l, x in zip(lins, xs)))
+        nbytes.append(sum(mm8_bytes(l.in_features, l.out_features, int(x.shape[0])) for l, x in zip(lins, xs)))
         return orig_group(lins, xs, outs)
-
-    import rwkv7mi.model as model_mod
-    orig_lnmix = model_mod.mm8_lnmix_multi_into
 
     def rec_lnmix(x, prev, ln_w, ln_b, eps, mixes, mods, outs, **kw):
         # the LN-mix prologue launches (R/K/V and FFN key at one row): weights and
-        # metadata as above, plus the prologue's vectors (x, prev, LN weight and
-        # bias, mixes) and its extra outputs (h, extra mixes)
+        # metadata, plus the prologue's vectors (x, prev, LN weight and bias,
+        # mixes), its extra outputs (h, extra mixes) and, on the R/K/V launch,
+        # the LoRA down-projection weights it reads and the fp32 sums it writes
         calls.append(lambda: orig_lnmix(x, prev, ln_w, ln_b, eps, mixes, mods, outs, **kw))
         rows, i = (int(v) for v in x.shape)
         naux = len(kw.get("aux_outs", ()))
         extra = (rows * i + 2 * i + len(mixes) * i + rows * i * (1 if kw.get("h_out") is not None else 0)
                  + naux * (i + rows * i)) * 2
-        nbytes.append(sum(mm8_bytes(m, rows) for m in mods) + extra)
+        if kw.get("lora_downs") is not None:
+            ranks = sum(int(d.shape[0]) for d in kw["lora_downs"])
+            extra += ranks * i * 2 + rows * ranks * 4
+        nbytes.append(sum(mm8_bytes(m.in_features, m.out_features, rows) for m in mods) + extra)
         return orig_lnmix(x, prev, ln_w, ln_b, eps, mixes, mods, outs, **kw)
 
     QuantLinear.apply = rec_apply
@@ -243,73 +344,145 @@ def run_decode(batches=(1, 8), steps=64, warmup=5, log=print):
     finally:
         QuantLinear.apply, QuantLinear.apply_group = orig_apply, staticmethod(orig_group)
         model_mod.mm8_lnmix_multi_into = orig_lnmix
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for c in calls:
-            c()
-    torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for c in calls:
-            c()
-    reps = 20
-    graph.replay()
-    torch.cuda.synchronize()
-    st = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for _ in range(reps):
-        graph.replay()
-    e1.record(st)
-    torch.cuda.synchronize()
-    tot_ms = e0.elapsed_time(e1)
-    n = reps * len(calls)
-    tot_b = reps * sum(nbytes)
-    res["mm8_kernel"] = {"launches": len(calls), "avg_us": 1e3 * tot_ms / n,
-                         "bytes_per_launch": tot_b / n, "gbs": tot_b / (tot_ms / 1e3) / 1e9}
-    del graph
-    return res
+    ms = time_graph(calls, reps)
+    per = sum(nbytes) / len(nbytes)
+    return {"launches": len(calls), "avg_us": 1e3 * ms, "bytes_per_launch": per, "gbs": per / (ms / 1e3) / 1e9}
 
 
-def cpu_decode_baseline(min_seconds=10.0):
-    """fp32 numpy restatement of the per-token model (oracle/model_oracle.py) on a
-    bounded slice of the 7.2B shapes: 2 of the 32 layers + head, bsz 1; the
-    per-token time is scaled to 32 layers."""
+def run_prefill(model, cfg, B=8, T=4096, steps=2, warmup=1):
+    """configs[4]'s prefill: B x T random tokens through the 7.2B model (the
+    chunked scan, the projections, the LoRA and the head on the last token)."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(3)
+    ids = torch.randint(0, cfg.vocab_size, (B, T), device="cuda", generator=g)
+    ms, wall = time_events(lambda: model(ids), steps, warmup)
+    # matmul flops per token: every projection's weights (MM8 and the fp16 LoRA), twice
+    D, A, F, L = cfg.hidden_size, cfg.attention_hidden_size, cfg.intermediate_size, cfg.num_hidden_layers
+    ranks = cfg.decay_low_rank_dim + cfg.a_low_rank_dim + cfg.gate_low_rank_dim + cfg.v_low_rank_dim
+    per_tok = L * (4 * D * A + 2 * D * F + 2 * D * ranks)
+    flops = 2 * per_tok * B * T + 2 * B * D * cfg.vocab_size
+    tflops = flops / (ms / 1e3) / 1e12
+    return {"tok_s": round(B * T / (ms / 1e3), 1), "ms": round(ms, 2), "config": f"B={B} T={T}",
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                         "flops_per_call": flops}}
+
+
+def cpu_decode_baseline(min_seconds=12.0, max_tokens=64):
+    """The fp32 numpy restatement of the per-token model (oracle/model_oracle.py)
+    over the whole 7.2B architecture (all 32 layers and the head; fp32 weights,
+    29 GB of host memory), bsz 1, timed over whole tokens for about
+    ``min_seconds`` after one warm-up token."""
     import numpy as np
     import torch
     from oracle.model_oracle import ModelOracle
-    from rwkv7mi.model import NativeRWKV7Config, random_weights
+    from rwkv7mi.model import parameter_shapes, random_weights
 
-    full = config_7p2b()
-    cfg = NativeRWKV7Config(vocab_size=full.vocab_size, hidden_size=full.hidden_size, num_hidden_layers=2,
-                            intermediate_size=full.intermediate_size)
-    w = random_weights(cfg, seed=0, device="cpu", dtype=torch.float32)
-    ora = ModelOracle(cfg, {k: v.numpy() for k, v in w.items()}, dtype=np.float32)
+    cfg = config_7p2b()
+    w = {}
+    for name in parameter_shapes(cfg):  # generated on the GPU one tensor at a time, kept on the host
+        w[name] = random_weights(cfg, seed=0, device="cuda", dtype=torch.float32, names=[name])[name].cpu().numpy()
+    ora = ModelOracle(cfg, w, dtype=np.float32)
     del w
     st = ora.new_state(1)
     ora.step(np.array([1]), st)
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < min_seconds:
-        ora.step(np.array([n % 1000]), st)
+    while n < max_tokens and (n < 3 or time.perf_counter() - t0 < min_seconds):
+        ora.step(np.array([(17 * n) % cfg.vocab_size]), st)
         n += 1
-    per_tok = (time.perf_counter() - t0) / n
-    xh = np.ones((1, cfg.hidden_size), np.float32)
-    m, t0 = 0, time.perf_counter()
-    while m < 3 or time.perf_counter() - t0 < 1.0:
-        ora.head(xh)
-        m += 1
-    t_head = (time.perf_counter() - t0) / m
-    t_layer = max(per_tok - t_head, 0.0) / cfg.num_hidden_layers
-    est = t_layer * full.num_hidden_layers + t_head
-    return {"value": 1.0 / est, "unit": "tok/s", "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
-            "kind": "port",
-            "sample": f"7.2B decode bsz 1: fp32 numpy per-token restatement (oracle/model_oracle.py) of 2 of 32 "
-                      f"layers + head, {n} tokens ({per_tok * 1e3:.0f} ms/token, head {t_head * 1e3:.0f} ms); "
-                      f"per-layer time scaled to 32 layers"}
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": host_cores(), "kind": "port", "cpu": cpu_model(),
+            "sample": f"7.2B decode bsz 1, all 32 layers + head: fp32 numpy per-token restatement "
+                      f"(oracle/model_oracle.py), {n} tokens in {dt:.1f} s"}
 
 
-TRAFFIC_JSON = Path(__file__).resolve().parent / "profiles" / "traffic.json"
+# ------------------------------------------------------------------ GEMV legs (configs[2], configs[3])
+def _mods_for(I, O, count, seed):
+    import torch
+    from rwkv7mi import MM8Linear
+
+    torch.manual_seed(seed)
+    mods = []
+    for _ in range(count):
+        lin = torch.nn.Linear(I, O, bias=False, device="cuda", dtype=torch.float16)
+        with torch.no_grad():
+            lin.weight.normal_(0.0, 0.02)
+        mods.append(MM8Linear(lin))
+        del lin
+    return mods
+
+
+def _distinct(nbytes_one):
+    """Copies of a weight that keep the rotation beyond the 256 MB last-level cache."""
+    return max(2, min(64, -(-(512 << 20) // nbytes_one)))
+
+
+def run_gemv_c3(reps=20):
+    """MM8 at the 1.5B shapes x batch 1 / 8 / 32: per shape and
+    batch, a hipGraph of launches over distinct weight copies (so no copy is
+    cache-resident), average launch time, algorithmic bytes and HBM fraction."""
+    import torch
+    from rwkv7mi import workspace as ws
+    from rwkv7mi.native_quant_mm8 import GEMV_ROWS, mm8_gemm_workspace_bytes
+
+    out = {}
+    for I, O in ((2048, 2048), (2048, 8192), (8192, 2048), (2048, 65536)):
+        mods = _mods_for(I, O, _distinct(I * O), seed=I + O)
+        for rows in (1, 8, 32):
+            if rows > GEMV_ROWS:
+                ws.reserve(torch.device("cuda", 0), mm8_gemm_workspace_bytes(1, rows, I, O), slot="mm8g")
+            x = torch.randn(rows, I, device="cuda", dtype=torch.float16)
+            ys = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in mods]
+            calls = [(lambda m=m, y=y: m.rwkv7_forward_into(x, y)) for m, y in zip(mods, ys)]
+            ms = time_graph(calls, reps)
+            nb = mm8_bytes(I, O, rows)
+            gbs = nb / (ms / 1e3) / 1e9
+            out[f"{I}x{O}/b{rows}"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                                       "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del mods
+        torch.cuda.empty_cache()
+    return out
+
+
+def run_gemv_c4(reps=20):
+    """Group-128 W4 at the 7.2B shapes x batch 1 / 4 / 16, the
+    asymmetric (min/max affine) form and the reference's symmetric form."""
+    import torch
+    from rwkv7mi.sm70_quant import (quantize_w4_affine_groupwise, quantize_w4_groupwise, w4_affine_groupwise_linear,
+                                    w4_groupwise_linear)
+
+    out = {}
+    for I, O in ((4096, 4096), (4096, 16384), (16384, 4096), (4096, 65536)):
+        n = _distinct(I * O // 2)
+        g = torch.Generator(device="cuda").manual_seed(I + O)
+        packs_a, packs_s = [], []
+        for _ in range(n):
+            W = torch.randn(O, I, device="cuda", dtype=torch.float16, generator=g) * 0.02
+            packs_a.append(quantize_w4_affine_groupwise(W))
+            packs_s.append(quantize_w4_groupwise(W))
+            del W
+        for rows in (1, 4, 16):
+            x = torch.randn(rows, I, device="cuda", dtype=torch.float16)
+            ys = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(n)]
+            calls = [(lambda p=p, y=y: w4_affine_groupwise_linear(x, p[0], p[1], p[2], O, I, out=y))
+                     for p, y in zip(packs_a, ys)]
+            ms = time_graph(calls, reps)
+            gbs = w4_bytes(I, O, rows, affine=True) / (ms / 1e3) / 1e9
+            calls_s = [(lambda p=p, y=y: w4_groupwise_linear(x, p[0], p[1], O, I, out=y)) for p, y in zip(packs_s, ys)]
+            ms_s = time_graph(calls_s, reps)
+            gbs_s = w4_bytes(I, O, rows, affine=False) / (ms_s / 1e3) / 1e9
+            out[f"{I}x{O}/b{rows}"] = {"asym_us": round(ms * 1e3, 2), "asym_gbs": round(gbs, 1),
+                                       "asym_frac": round(gbs / HBM_PEAK_GBS, 4), "sym_us": round(ms_s * 1e3, 2),
+                                       "sym_frac": round(gbs_s / HBM_PEAK_GBS, 4)}
+        del packs_a, packs_s
+        torch.cuda.empty_cache()
+    return out
+
+
+# ------------------------------------------------------------------ counter workloads
+TRAFFIC_JSON = ROOT / "profiles" / "traffic.json"
+COPY_BYTES = 256 << 20
 
 
 def _traffic():
@@ -318,7 +491,15 @@ def _traffic():
         return json.loads(TRAFFIC_JSON.read_text())["traffic_bytes_per_launch"]
     except (OSError, ValueError, KeyError):
         return None
-COPY_BYTES = 256 << 20
+
+
+def _calibration_copy():
+    import torch
+
+    src = torch.ones(COPY_BYTES // 2, device="cuda", dtype=torch.float16)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
 
 
 def run_traffic():
@@ -327,37 +508,28 @@ def run_traffic():
     COPY_BYTES (read and written once) that calibrates FETCH_SIZE / WRITE_SIZE.
     Run under ``rocprofv3 --pmc FETCH_SIZE`` and then ``--pmc WRITE_SIZE``."""
     import torch
-    from rwkv7mi.model import NativeRWKV7ForCausalLM
 
-    cfg = config_7p2b()
-    model = NativeRWKV7ForCausalLM.from_random(cfg, seed=0, device="cuda", dtype=torch.float16)
+    cfg, model, _ = build_7p2b()
     cache = model.new_cache(1)
     toks = torch.zeros(1, dtype=torch.long, device="cuda")
     logits = torch.empty(1, cfg.vocab_size, device="cuda", dtype=torch.float16)
     bufs = model._decode_buffers(1)
     for _ in range(2):
         model.decode_step_(toks, cache, logits, bufs)
-    src = torch.ones(COPY_BYTES // 2, device="cuda", dtype=torch.float16)
-    dst = torch.empty_like(src)
-    torch.neg(src, out=dst)
-    torch.cuda.synchronize()
-    print("bench: traffic workload done (2 decode steps + calibration copy)", file=sys.stderr, flush=True)
+    _calibration_copy()
+    _log("bench: traffic workload done (2 decode steps + calibration copy)")
 
 
 def run_scan_traffic(H=32):
     """Kernels for the scan's counter runs: two chunked-scan calls at B=8,
     T=4096 (the second is the measured one) and the COPY_BYTES calibration copy."""
-    import torch
     from rwkv7mi import self_chunk_rwkv7
 
     inputs = make_scan_inputs(8, 4096, H, 64)
     for _ in range(2):
         self_chunk_rwkv7(*inputs, chunk_size=16)
-    src = torch.ones(COPY_BYTES // 2, device="cuda", dtype=torch.float16)
-    dst = torch.empty_like(src)
-    torch.neg(src, out=dst)
-    torch.cuda.synchronize()
-    print(f"bench: scan traffic workload done (H={H}: 2 scan calls + calibration copy)", file=sys.stderr, flush=True)
+    _calibration_copy()
+    _log(f"bench: scan traffic workload done (H={H}: 2 scan calls + calibration copy)")
 
 
 def _counter_rows(path):
@@ -367,45 +539,49 @@ def _counter_rows(path):
         return list(csv.DictReader(f))
 
 
-def summarize_traffic(fetch_csv, write_csv, out=TRAFFIC_JSON):
-    """Per-launch HBM bytes of the decode step's MM8 GEMV launches from the two
-    counter runs, scaled by the copy kernel's known bytes; writes ``out``."""
+def summarize_traffic(fetch_csv, write_csv, out=TRAFFIC_JSON, kernel="mm8t_kernel"):
+    """Per-launch HBM bytes of ``kernel``'s launches in the second half of the
+    run (the second of its two identical passes) from the two counter runs,
+    scaled by what the counters read for the copy kernel of known size; writes ``out``."""
     def per_dispatch(path, counter):
         rows = [r for r in _counter_rows(path) if r.get("Counter_Name") == counter]
         rows.sort(key=lambda r: int(r["Dispatch_Id"]))
-        mm8 = [float(r["Counter_Value"]) * 1024 for r in rows if "mm8t_kernel" in r["Kernel_Name"]]
+        ks = [float(r["Counter_Value"]) * 1024 for r in rows if kernel in r["Kernel_Name"]]
         copy = [float(r["Counter_Value"]) * 1024 for r in rows if "neg" in r["Kernel_Name"]]
-        half = len(mm8) // 2  # two decode steps: keep the second
-        return mm8[half:], copy[-1]
-    f_mm8, f_copy = per_dispatch(fetch_csv, "FETCH_SIZE")
-    w_mm8, w_copy = per_dispatch(write_csv, "WRITE_SIZE")
+        return ks[len(ks) // 2:], copy[-1]
+    f_k, f_copy = per_dispatch(fetch_csv, "FETCH_SIZE")
+    w_k, w_copy = per_dispatch(write_csv, "WRITE_SIZE")
     ff, fw = COPY_BYTES / f_copy, COPY_BYTES / w_copy
-    n = len(f_mm8)
-    traffic = (sum(f_mm8) * ff + sum(w_mm8) * fw) / n
-    res = {"kernel": "mm8t_kernel", "launches_per_step": n, "traffic_bytes_per_launch": round(traffic),
-           "fetch_bytes_per_launch": round(sum(f_mm8) * ff / n), "write_bytes_per_launch": round(sum(w_mm8) * fw / n),
+    n = len(f_k)
+    res = {"kernel": kernel, "launches": n, "traffic_bytes_per_launch": round((sum(f_k) * ff + sum(w_k) * fw) / n),
+           "fetch_bytes_per_launch": round(sum(f_k) * ff / n), "write_bytes_per_launch": round(sum(w_k) * fw / n),
            "fetch_scale": ff, "write_scale": fw, "copy_bytes": COPY_BYTES,
-           "source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of bench.py --workload traffic"}
+           "source": f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs ({Path(fetch_csv).parent.name}, "
+                     f"{Path(write_csv).parent.name})"}
     Path(out).parent.mkdir(parents=True, exist_ok=True)
     Path(out).write_text(json.dumps(res, indent=1) + "\n")
     print(json.dumps(res))
     return res
 
 
+# ------------------------------------------------------------------ main
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=["all", "decode", "scan", "traffic", "scan_traffic"], default="all")
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "decode", "scan", "gemv", "prefill", "traffic", "scan_traffic"])
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="write profiles/traffic.json from two rocprofv3 --pmc counter CSVs and exit")
-    ap.add_argument("--heads", type=int, default=32)
+                    help="write a traffic summary from two rocprofv3 --pmc counter CSVs and exit")
+    ap.add_argument("--traffic-kernel", default="mm8t_kernel")
+    ap.add_argument("--traffic-out", default=str(TRAFFIC_JSON))
+    ap.add_argument("--heads", default="32,64", help="scan head counts (configs[1]: 32; north star: 64)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--batches", default="1,8,64", help="decode batch sizes (1 is the headline)")
     args = ap.parse_args(argv)
     if args.summarize_traffic:
-        summarize_traffic(*args.summarize_traffic)
+        summarize_traffic(*args.summarize_traffic, out=args.traffic_out, kernel=args.traffic_kernel)
         return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -415,32 +591,50 @@ def main(argv=None):
     import torch
 
     torch.cuda.set_device(0)
-    log = lambda m: print(m, file=sys.stderr, flush=True)
+    heads = [int(h) for h in args.heads.split(",")]
     if args.workload == "traffic":
         run_traffic()
         return 0
     if args.workload == "scan_traffic":
-        run_scan_traffic(args.heads)
+        run_scan_traffic(heads[0])
         return 0
+    wl = args.workload
+    scans = {}
+    step = None
+    if wl in ("all", "scan"):
+        for H in heads:
+            s = run_scan(H=H, steps=min(args.steps, 20), warmup=min(args.warmup, 3))
+            scans[H] = s
+            _log(f"bench: scan {s['config']}: {s['ms']:.3f} ms, {s['tok_s'] / 1e6:.1f} M tok/s, "
+                 f"{100 * s['frac']:.1f}% of HBM roofline")
+        step = run_decode_form_step()
+        _log(f"bench: decode-form step {step['config']}: {step['us_per_step']} us ({100 * step['frac']:.1f}%)")
+    dec = mk = pre = None
+    if wl in ("all", "decode", "prefill"):
+        cfg, model, quantized = build_7p2b()
+        if wl in ("all", "decode"):
+            dec = run_decode(model, cfg, quantized, tuple(int(b) for b in args.batches.split(",")), args.steps,
+                             args.warmup)
+            mk = run_mm8_roofline(model, cfg)
+            _log(f"bench: MM8 launches of a bsz-1 step: {mk['avg_us']:.2f} us avg, {mk['gbs']:.0f} GB/s")
+        if wl in ("all", "prefill"):
+            pre = run_prefill(model, cfg)
+            _log(f"bench: prefill {pre['config']}: {pre['ms']:.1f} ms, {pre['tok_s']:.0f} tok/s, "
+                 f"{pre['roofline']['achieved']} TFLOP/s")
+        del model
+        torch.cuda.empty_cache()
+    c3 = c4 = None
+    if wl in ("all", "gemv"):
+        c3 = run_gemv_c3()
+        _log("bench: configs[2] MM8: " + ", ".join(f"{k} {v['us']}us" for k, v in c3.items()))
+        c4 = run_gemv_c4()
+        _log("bench: configs[3] W4: " + ", ".join(f"{k} {v['asym_us']}us" for k, v in c4.items()))
+
     out: dict = {}
-    scan = dec = None
-    if args.workload in ("all", "scan"):
-        scan = run_scan(H=args.heads, steps=min(args.steps, 20), warmup=min(args.warmup, 3))
-        log(f"bench: scan {scan['config']}: {scan['ms']:.3f} ms, {scan['tok_s'] / 1e6:.1f} M tok/s, "
-            f"{100 * scan['frac']:.1f}% of HBM roofline")
-    if args.workload in ("all", "decode"):
-        dec = run_decode(batches=tuple(int(b) for b in args.batches.split(",")), steps=args.steps,
-                         warmup=args.warmup, log=log)
-    if dec is not None and 1 not in dec:  # a partial sweep without the headline batch size
-        print(json.dumps({"decode": {str(b): {"tok_s": round(dec[b]["tok_s"], 2), "ms_per_step": round(dec[b]["ms"], 4),
-                                              "step_roofline_frac": round(dec[b]["frac"], 4)}
-                                     for b in dec if isinstance(b, int)}}), flush=True)
-        return 0
-    if dec is not None:
+    if dec is not None and 1 in dec:
         d1 = dec[1]
-        mk = dec["mm8_kernel"]
         out = {
-            "metric": "decode tok/s 7.2B MM8 bsz1 (bsz 8 and 64 and wkv7 prefill tok/s alongside)",
+            "metric": "decode tok/s 7.2B MM8 bsz1 (bsz 8 and 64, wkv7 prefill tok/s and the other configs alongside)",
             "value": round(d1["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(d1["ms"], 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "f16 activations / u8 MM8 weights / f32 state",
@@ -450,35 +644,48 @@ def main(argv=None):
                        "parallelism": "single-gpu"},
             "roofline": {"bound": "hbm", "achieved": round(mk["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(mk["gbs"] / HBM_PEAK_GBS, 4), "traffic": _traffic(), "kernel": "mm8t_kernel",
-                         "avg_launch_us": round(mk["avg_us"], 3),
-                         "bytes_per_launch": round(mk["bytes_per_launch"]), "launches_per_step": mk["launches"]},
+                         "avg_launch_us": round(mk["avg_us"], 3), "bytes_per_launch": round(mk["bytes_per_launch"]),
+                         "launches_per_step": mk["launches"]},
             "decode": {str(b): {"tok_s": round(dec[b]["tok_s"], 2), "ms_per_step": round(dec[b]["ms"], 4),
                                 "step_bytes": dec[b]["bytes"], "step_gbs": round(dec[b]["gbs"], 1),
-                                "step_roofline_frac": round(dec[b]["frac"], 4)}
-                       for b in dec if isinstance(b, int)},
+                                "step_roofline_frac": round(dec[b]["frac"], 4)} for b in dec},
         }
-    if scan is not None:
-        s = {"tok_s": round(scan["tok_s"], 1), "ms_per_call": round(scan["ms"], 4), "config": scan["config"],
-             "roofline": {"bound": "hbm", "achieved": round(scan["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                          "frac": round(scan["frac"], 4), "algorithmic_bytes": scan["bytes"],
-                          "kernel": "wkv7_chunk_kernel"}}
+    elif dec is not None:
+        out = {"decode": {str(b): {"tok_s": round(dec[b]["tok_s"], 2), "ms_per_step": round(dec[b]["ms"], 4),
+                                   "step_roofline_frac": round(dec[b]["frac"], 4)} for b in dec}}
+    if scans:
+        scan_out = {f"H{H}": {"tok_s": round(s["tok_s"], 1), "ms_per_call": round(s["ms"], 4), "config": s["config"],
+                              "roofline": {"bound": "hbm", "achieved": round(s["gbs"], 1), "peak": HBM_PEAK_GBS,
+                                           "unit": "GB/s", "frac": round(s["frac"], 4),
+                                           "algorithmic_bytes": s["bytes"], "kernel": "wkv7_chunk_kernel"}}
+                    for H, s in scans.items()}
         if not out:
+            s = scans[heads[0]]
             out = {"metric": "wkv7 prefill tok/s (chunked DPLR scan, BASELINE.json configs[1])",
-                   "value": s["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": min(args.steps, 20),
-                   "warmup": min(args.warmup, 3), "ms_per_step": s["ms_per_call"], "higher_is_better": True,
+                   "value": round(s["tok_s"], 1), "unit": "tok/s", "n_gpus": 1, "steps": min(args.steps, 20),
+                   "warmup": min(args.warmup, 3), "ms_per_step": round(s["ms"], 4), "higher_is_better": True,
                    "scaling": "weak", "vs_baseline": None, "dtype": "f16 in / f32 state",
                    "data": "synthetic (configs[1] distribution, seed 0)",
-                   "config": {"workload": f"wkv7_scan_op {scan['config']}", "parallelism": "single-gpu"},
-                   "roofline": s["roofline"]}
-        else:
-            out["wkv7_prefill"] = s
-    if not args.no_cpu:
+                   "config": {"workload": f"wkv7_scan_op {s['config']}", "parallelism": "single-gpu"},
+                   "roofline": scan_out[f"H{heads[0]}"]["roofline"]}
+        out["wkv7_prefill"] = scan_out
+    if step:
+        out["wkv7_decode_form_step"] = step
+    if pre:
+        out["prefill_c5"] = pre
+    if c3:
+        out["mm8_c3"] = c3
+    if c4:
+        out["w4_c4"] = c4
+    if not args.no_cpu and out:
         if dec is not None:
             out["cpu_baseline"] = cpu_decode_baseline()
-            if scan is not None:
-                out["wkv7_prefill"]["cpu_baseline"] = cpu_scan_baseline()
-        else:
-            out["cpu_baseline"] = cpu_scan_baseline()
+        if scans:
+            cs = cpu_scan_baseline()
+            if dec is None:
+                out["cpu_baseline"] = cs
+            else:
+                out["wkv7_prefill"]["cpu_baseline"] = cs
     print(json.dumps(out), flush=True)
     return 0
 
