@@ -81,6 +81,12 @@ struct Mm8tBatch {
   Mm8tPro pro;
   int rows, I, O, KC;
   int gx;  // product workgroups along x; with the LN-mix prologue one more (x == gx) writes h and the extra mixes
+  // Split K (no prologue, 8-bit): S > 1 splits the inputs into S ranges of KC
+  // (one LDS chunk each); workgroup x takes range x % S, so its x' is staged
+  // once for all its column groups, and writes fp32 partials
+  // part[((s * nprob + p) * rows + row) * O + o] for mm8t_split_reduce_kernel.
+  int S;
+  float* part;
 };
 
 // bytes of (d0, d1) = rows r..r+7 of one column -> fp16 [w + 0.5] x 8
@@ -124,7 +130,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   const int row0 = blockIdx.z * 16;
   const int nrows = min(16, B.rows - row0);
   const int ngroups = (O + MM8T_COLS - 1) / MM8T_COLS;
-  const int gstride = B.gx;
+  const int S = B.S;
+  const int gstride = B.gx / S;
   // LN-mix prologue: workgroup x == gx computes no product; it stages the row
   // like the others and writes h and the extra mixes (its twins for the other
   // problems exit at once)
@@ -164,7 +171,10 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   const __amdgpu_buffer_rsrc_t ryr = mm8t_rsrc(P.ry, (uint32_t)(I * sizeof(TM)));
   const __amdgpu_buffer_rsrc_t myr = mm8t_rsrc(P.my, (uint32_t)(I * sizeof(TM)));
   const uint32_t lane_off = (uint32_t)n * (uint32_t)bcol + 16u * kg;
-  const int nchunks = (I + KC - 1) / KC;
+  // split K: this workgroup's range of inputs starts at kbase (one chunk)
+  const int sidx = (int)blockIdx.x % S;
+  const int kbase = S > 1 ? sidx * KC : 0;
+  const int nchunks = S > 1 ? 1 : (I + KC - 1) / KC;
   const int J = nchunks * CSW;  // steps per wave per column group
 
   // staging: TPR threads per batch row, fixed for the whole kernel
@@ -204,13 +214,13 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
       const int q = su + (it0 + u) * TPR;
-      const int k = kc0 + 8 * q;
+      const int k = kbase + kc0 + 8 * q;
       rxv[u] = mm8t_ld8<TA>(xr, (uint32_t)(sr * I + k), sr < nrows && q < NQ && k < I);
     }
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
       const int q = su + (it0 + u) * TPR;
-      const int k = kc0 + 8 * q;
+      const int k = kbase + kc0 + 8 * q;
       const bool valid = sr < nrows && q < NQ && k < I;
       rrv[u] = mm8t_ld8<TM>(ryr, (uint32_t)k, valid);
       rmv[u] = mm8t_ld8<TM>(myr, (uint32_t)k, valid);
@@ -295,7 +305,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   u32x4 buf[DEPTH][2];
   auto load_step = [&](__amdgpu_buffer_rsrc_t r, int j, u32x4 (&b)[2]) {
     if constexpr (BITS == 8) {
-      const int blk = wave + NW * j;
+      const int blk = kbase / 128 + wave + NW * j;
       const uint32_t boff = (uint32_t)blk * 2048u + 16u * (uint32_t)lane;
       b[0] = mm8t_ld16(r, blk < KBLK ? boff : MM8T_OOB);
       b[1] = mm8t_ld16(r, blk < KBLK ? boff + 1024u : MM8T_OOB);
@@ -412,7 +422,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
     }
   };
 
-  int g = aux_wg ? ngroups : (int)blockIdx.x;           // (the prologue's own workgroup loads nothing)
+  int g = aux_wg ? ngroups : (int)blockIdx.x / S;       // (the prologue's own workgroup loads nothing)
   __amdgpu_buffer_rsrc_t wr = group_rsrc(g);             // this group
   __amdgpu_buffer_rsrc_t wn = group_rsrc(g + gstride);   // the next one
 
@@ -432,7 +442,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
 #pragma unroll
     for (int r = 0; r < NRND; ++r) {
       const int j = 4 * r + (lane >> 4);
-      const int k = 128 * (wave + NW * j) + 8 * (lane & 15);
+      const int k = kbase + 128 * (wave + NW * j) + 8 * (lane & 15);  // global input index
       const bool valid = j < CSW && k < I;
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) wx[r][rr] = mm8t_ld8<TA>(xr, (uint32_t)(rr * I + k), valid && rr < nrows);
@@ -640,15 +650,19 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
 #pragma unroll
         for (int q = 1; q < NW; ++q) s += red[q][m][cn];
         float v = ld(rx, o) * s + rsum[m][1] + ld(mx, o) * rsum[m][0];
-        if (bias) v += ld(bias, o);
-        const int64_t oi = (int64_t)(row0 + m) * O + o;
-        if (P.epilogue == RWKV7MI_EPI_RELU2) {
-          v = fmaxf(v, 0.f);
-          v = v * v;
-        } else if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
-          v += ld(reinterpret_cast<const TA*>(P.residual), oi);
+        if (S > 1) {  // this range's share; the reduce kernel adds the ranges, bias and epilogue
+          B.part[(((int64_t)sidx * gridDim.y + blockIdx.y) * B.rows + row0 + m) * O + o] = v;
+        } else {
+          if (bias) v += ld(bias, o);
+          const int64_t oi = (int64_t)(row0 + m) * O + o;
+          if (P.epilogue == RWKV7MI_EPI_RELU2) {
+            v = fmaxf(v, 0.f);
+            v = v * v;
+          } else if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
+            v += ld(reinterpret_cast<const TA*>(P.residual), oi);
+          }
+          reinterpret_cast<TA*>(P.y)[oi] = from_f32<TA>(v);
         }
-        reinterpret_cast<TA*>(P.y)[oi] = from_f32<TA>(v);
       }
     }
     wr = wn;
@@ -656,6 +670,46 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   }
 }
 
+
+// Split-K finish: y[p][row][o] = epilogue(sum_s part[s][p][row][o] + bias[o]),
+// the ranges added in order 0..S-1 (deterministic).  V = 4 when O % 4 == 0.
+template <typename TA, typename TM, int V>
+__global__ __launch_bounds__(256) void mm8t_split_reduce_kernel(const Mm8tBatch B) {
+  const int p = blockIdx.y;
+  const Mm8tProb& P = B.p[p];
+  const int64_t n = (int64_t)B.rows * B.O;
+  const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+  if (idx >= n) return;
+  float a[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) a[v] = 0.f;
+  for (int sp = 0; sp < B.S; ++sp) {
+    const float* src = B.part + ((int64_t)sp * gridDim.y + p) * n + idx;
+    if constexpr (V == 4) {
+      const float4 t = *reinterpret_cast<const float4*>(src);
+      a[0] += t.x;
+      a[1] += t.y;
+      a[2] += t.z;
+      a[3] += t.w;
+    } else {
+      a[0] += src[0];
+    }
+  }
+  const int o0 = (int)(idx % B.O);
+  const TM* bias = reinterpret_cast<const TM*>(P.bias);
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    float x = a[v];
+    if (bias) x += ld(bias, o0 + v);
+    if (P.epilogue == RWKV7MI_EPI_RELU2) {
+      x = fmaxf(x, 0.f);
+      x = x * x;
+    } else if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
+      x += ld(reinterpret_cast<const TA*>(P.residual), idx + v);
+    }
+    reinterpret_cast<TA*>(P.y)[idx + v] = from_f32<TA>(x);
+  }
+}
 
 // x' staging chunk: the largest power-of-two multiple of 2 RS NW rows (at
 // most 32 RS NW, 16 RS NW for the 4-bit eight-wave kernel; RS = K rows per
@@ -735,8 +789,43 @@ int64_t rwkv7mi::mm8t_cus() {
   return cached[dev];
 }
 
+// Waves per workgroup and x' chunk of a call.  At most one workgroup per CU:
+// eight waves each, so twice the weight bytes are in flight per CU; otherwise
+// four-wave workgroups, two per CU.  Without the prologue, an x' too big for
+// two workgroups per CU (rows > 4) takes one eight-wave workgroup per CU
+// instead of one four-wave one (measured 8-16% faster at 8 rows).  Returns the
+// chunk (0: not even the smallest fits).
+static int mm8t_plan(int nprob, int64_t rows, int64_t I, int64_t O, int bits, bool pro, int* nw_out) {
+  const int64_t nwg = ((O + MM8T_COLS - 1) / MM8T_COLS) * nprob * ((rows + 15) / 16);
+  int nw = nwg <= mm8t_cus() ? 8 : 4;
+  int kc = mm8t_chunk(rows, I, nwg, nw, bits);
+  if (!kc && nw == 8) {
+    nw = 4;
+    kc = mm8t_chunk(rows, I, nwg, nw, bits);
+  }
+  if (kc && !pro && nw == 4 && bits == 8 && mm8t_lds(rows, kc) > (size_t)MM8T_LDS_X) {
+    const int kc8 = mm8t_chunk(rows, I, nwg, 8, bits);
+    if (kc8) {
+      nw = 8;
+      kc = kc8;
+    }
+  }
+  *nw_out = nw;
+  return kc;
+}
+
+// Bytes of split-K partials a call needs (0: no split).
+static size_t mm8t_part_bytes(int S, int nprob, int64_t rows, int64_t O) {
+  return S > 1 ? (size_t)S * (size_t)nprob * (size_t)rows * (size_t)O * 4u : 0;
+}
+
+// Split count for a call without the prologue: 1 when x' fits one LDS chunk,
+// else one split per chunk (the ranges' x' stays staged for all column groups).
+static int mm8t_auto_splits(int64_t I, int KC) { return KC >= I ? 1 : (int)((I + KC - 1) / KC); }
+
 static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I, int64_t O, int act_dtype,
-                       int meta_dtype, void* stream, const char* who, int bits = 8, const Mm8tPro* pro = nullptr) {
+                       int meta_dtype, void* stream, const char* who, int bits = 8, const Mm8tPro* pro = nullptr,
+                       void* workspace = nullptr, size_t workspace_bytes = 0, int* splits_out = nullptr) {
   const std::string w(who);
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
   if (rows < 0 || I <= 0 || O <= 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
@@ -765,24 +854,9 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
   const int64_t ngroups = (O + MM8T_COLS - 1) / MM8T_COLS;
   const int64_t rtiles = (rows + 15) / 16;
   const int64_t cus = mm8t_cus();
-  // At most one workgroup per CU: eight waves each, so twice the weight bytes
-  // are in flight per CU.  Otherwise four-wave workgroups, two per CU.
-  int nw = ngroups * nprob * rtiles <= cus ? 8 : 4;
-  b.KC = mm8t_chunk(rows, I, ngroups * nprob * rtiles, nw, bits);
-  if (!b.KC && nw == 8) {
-    nw = 4;
-    b.KC = mm8t_chunk(rows, I, ngroups * nprob * rtiles, nw, bits);
-  }
+  int nw = 8;
+  b.KC = mm8t_plan(nprob, rows, I, O, bits, pro != nullptr, &nw);
   if (!b.KC) return fail(RWKV7MI_EINVAL, w + ": x' staging does not fit in LDS");
-  // x' too big for two workgroups per CU (rows > 4): one eight-wave workgroup
-  // per CU instead of one four-wave one (measured 8-16% faster at 8 rows)
-  if (!pro && nw == 4 && bits == 8 && mm8t_lds(rows, b.KC) > (size_t)MM8T_LDS_X) {
-    const int kc8 = mm8t_chunk(rows, I, ngroups * nprob * rtiles, 8, bits);
-    if (kc8) {
-      nw = 8;
-      b.KC = kc8;
-    }
-  }
   if (pro) {
     // the prologue takes the row statistics from one staging batch (two
     // 8-element groups per thread): the whole row in one chunk, and
@@ -804,6 +878,20 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
       return fail(RWKV7MI_EINVAL, w + ": the LN-mix prologue needs the whole row in one staging batch "
                                       "(rows <= 2 at in_features 4096)");
   }
+  // split K when x' needs several chunks and the caller gave a workspace for
+  // the partials (8-bit, no prologue); otherwise the chunks are re-staged per
+  // column group
+  int S = 1;
+  if (!pro && bits == 8 && workspace) {
+    S = mm8t_auto_splits(I, b.KC);
+    if (S > 1 && (workspace_bytes < mm8t_part_bytes(S, nprob, rows, O) ||
+                  (reinterpret_cast<uintptr_t>(workspace) & 15)))
+      return fail(RWKV7MI_ESIZE, w + ": split-K workspace missing, unaligned or smaller than "
+                                     "rwkv7mi_mm8t_matmul_workspace_bytes");
+  }
+  if (splits_out) *splits_out = S;
+  b.S = S;
+  b.part = S > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
   size_t lds = mm8t_lds(rows, b.KC);
   int64_t extra = pro ? 1 : 0;  // the prologue's own workgroups (x >= gx, y == 0)
   if (pro && pro->lrtot > 0) {
@@ -818,16 +906,16 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
   // With x' in one LDS chunk, workgroups loop over column groups: as many as
   // stay resident (less the prologue's own), split between the problems and
   // row tiles.
-  int64_t gx = ngroups;
-  if (b.KC >= I) {
+  int64_t gx = ngroups;  // column-group workgroups per split
+  if (b.KC >= I || S > 1) {
     const int64_t per_cu = nw == 4 && lds <= MM8T_LDS_X ? 2 : 1;
-    const int64_t slots = (cus * per_cu - extra) / (nprob * rtiles);
+    const int64_t slots = (cus * per_cu - extra) / (nprob * rtiles * S);
     if (slots >= 1 && slots < gx) gx = slots;
   }
-  b.gx = (int)gx;
-  dim3 grid((unsigned)(gx + extra), (unsigned)nprob, (unsigned)rtiles);
+  b.gx = (int)(gx * S);
+  dim3 grid((unsigned)(b.gx + extra), (unsigned)nprob, (unsigned)rtiles);
   const int wpc = nw * (nw == 4 && lds <= MM8T_LDS_X ? 2 : 1);  // resident waves per CU
-  return dispatch_dtype(act_dtype, [&](auto ta) {
+  const int rc = dispatch_dtype(act_dtype, [&](auto ta) {
     using TA = decltype(ta);
     return dispatch_dtype(meta_dtype, [&](auto tm) {
       using TM = decltype(tm);
@@ -843,6 +931,21 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
       }
       return nw == 8 ? mm8t_go_csw<TA, TM, 8, 8>(grid, lds, stream, b, wpc)
                      : mm8t_go_csw<TA, TM, 4, 8>(grid, lds, stream, b, wpc);
+    });
+  });
+  if (rc != RWKV7MI_OK || S == 1) return rc;
+  return dispatch_dtype(act_dtype, [&](auto ta) {
+    using TA = decltype(ta);
+    return dispatch_dtype(meta_dtype, [&](auto tm) {
+      using TM = decltype(tm);
+      const int64_t n = rows * O;
+      if (O % 4 == 0)
+        hipLaunchKernelGGL((mm8t_split_reduce_kernel<TA, TM, 4>), dim3((unsigned)((n / 4 + 255) / 256), nprob),
+                           dim3(256), 0, as_stream(stream), b);
+      else
+        hipLaunchKernelGGL((mm8t_split_reduce_kernel<TA, TM, 1>), dim3((unsigned)((n + 255) / 256), nprob),
+                           dim3(256), 0, as_stream(stream), b);
+      return check_launch("mm8t_split_reduce_kernel");
     });
   });
 }
@@ -869,6 +972,31 @@ extern "C" int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x, const 
     p[i] = Mm8tProb{x[i], nullptr, w_blk[i], mx[i], rx[i], my[i], ry[i], bias ? bias[i] : nullptr,
                     residual ? residual[i] : nullptr, y[i], epilogue[i]};
   return mm8t_launch(nprob, p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul_multi");
+}
+
+extern "C" size_t rwkv7mi_mm8t_matmul_workspace_bytes(int nprob, int64_t rows, int64_t I, int64_t O) {
+  if (nprob < 1 || nprob > MM8T_MAXPROB || rows <= 0 || I <= 0 || O <= 0) return 0;
+  int nw = 8;
+  const int kc = mm8t_plan(nprob, rows, I, O, 8, false, &nw);
+  if (!kc) return 0;
+  return mm8t_part_bytes(mm8t_auto_splits(I, kc), nprob, rows, O);
+}
+
+extern "C" int rwkv7mi_mm8t_matmul_multi_ws(int nprob, const void* const* x, const uint8_t* const* w_blk,
+                                            const void* const* mx, const void* const* rx, const void* const* my,
+                                            const void* const* ry, const void* const* bias,
+                                            const void* const* residual, void* const* y, const int* epilogue,
+                                            int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, "mm8t_matmul_multi_ws: 1..4 problems per launch");
+  if (!x || !w_blk || !mx || !rx || !my || !ry || !y || !epilogue)
+    return fail(RWKV7MI_EINVAL, "mm8t_matmul_multi_ws: null array");
+  Mm8tProb p[MM8T_MAXPROB];
+  for (int i = 0; i < nprob; ++i)
+    p[i] = Mm8tProb{x[i], nullptr, w_blk[i], mx[i], rx[i], my[i], ry[i], bias ? bias[i] : nullptr,
+                    residual ? residual[i] : nullptr, y[i], epilogue[i]};
+  return mm8t_launch(nprob, p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul_multi_ws", 8, nullptr,
+                     workspace, workspace_bytes);
 }
 
 extern "C" int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* prev, const void* ln_w,

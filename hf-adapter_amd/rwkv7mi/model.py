@@ -32,7 +32,7 @@ from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
 from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_workspace_bytes,
-                               mm8_lnmix_multi_into, mm8_matmul_multi_into)
+                               mm8_lnmix_multi_into, mm8_matmul_multi_into, mm8t_workspace_bytes)
 from .native_quant_policy import should_quantize_linear
 from .self_chunk_rwkv7 import _run_chunk
 
@@ -844,6 +844,16 @@ class NativeRWKV7ForCausalLM:
 
     def reserve_workspace(self, rows: int) -> None:
         """Grow the per-device scratch slots for ``rows``-row decode steps (before capture)."""
+        if 0 < rows <= QuantLinear.GEMV_ROWS:
+            tneed = 0
+            for L in self.layers:
+                if isinstance(L.r_proj, QuantLinear):
+                    tneed = max(tneed, mm8t_workspace_bytes(3, rows, L.r_proj.in_features, L.r_proj.out_features))
+            for lin in self._linears():
+                if isinstance(lin, QuantLinear):
+                    tneed = max(tneed, mm8t_workspace_bytes(1, rows, lin.in_features, lin.out_features))
+            if tneed:
+                _ws.reserve(self.device, tneed, slot="mm8t")
         if QuantLinear.GEMV_ROWS < rows <= QuantLinear.GEMM_ROWS:
             gneed = 0
             for L in self.layers:

@@ -122,8 +122,14 @@ def is_out_major(w_u8: torch.Tensor) -> bool:
 
 
 def mm8_workspace_bytes(rows: int, n: int, m: int) -> int:
-    """Workspace of the row-major kernel; the out-major kernel needs none."""
+    """Workspace of the row-major kernel (the ``"mm8"`` slot)."""
     return int(_lib.load().rwkv7mi_mm8_workspace_bytes(int(rows), int(n), int(m)))
+
+
+def mm8t_workspace_bytes(nprob: int, rows: int, n: int, m: int) -> int:
+    """Split-K partials the blocked GEMV needs for ``rows`` rows (the ``"mm8t"``
+    slot); 0 when the rows' x' fits one LDS chunk."""
+    return int(_lib.load().rwkv7mi_mm8t_matmul_workspace_bytes(int(nprob), int(rows), int(n), int(m)))
 
 
 def _check_out(x2, m, out, residual):
@@ -167,11 +173,8 @@ def mm8_matmul_into(x2, w_u8, mx, rx, my, ry, out, *, bias=None, residual=None, 
                                         out_features=m)
             mm8_gemm_multi_into([x2], [mod], [out], residuals=[residual], epilogues=[epilogue])
             return out
-        _lib.call(
-            "rwkv7mi_mm8t_matmul", _lib.ptr(x2), _lib.ptr(w_u8), _lib.ptr(mx), _lib.ptr(rx), _lib.ptr(my),
-            _lib.ptr(ry), _lib.ptr(bias), _lib.ptr(residual), _lib.ptr(out), rows, n, m, int(epilogue),
-            _lib.dtype_code(x2), _lib.dtype_code(mx), _lib.stream_of(x2),
-        )
+        mod = types.SimpleNamespace(w_blk=w_u8, mx=mx, rx=rx, my=my, ry=ry, bias=bias, in_features=n, out_features=m)
+        mm8_matmul_multi_into([x2], [mod], [out], residuals=[residual], epilogues=[epilogue])
         return out
     m = int(w_u8.shape[1])
     if int(w_u8.shape[0]) != n:
@@ -209,11 +212,14 @@ def mm8_matmul_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
     _lib.require_gpu(*xs, *outs, name="mm8_matmul_multi")
     arr = lambda ts: _lib.ptr_array(ts)
     eps = (ctypes.c_int * k)(*[int(e) for e in epilogues])
+    need = mm8t_workspace_bytes(k, rows, n, m)
+    ws = _ws.reserve(xs[0].device, need, slot="mm8t") if need else None
     _lib.call(
-        "rwkv7mi_mm8t_matmul_multi", k, arr(xs), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
+        "rwkv7mi_mm8t_matmul_multi_ws", k, arr(xs), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
         arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),
         arr([md.bias for md in mods]), arr(residuals), arr(outs), eps,
-        rows, n, m, _lib.dtype_code(xs[0]), _lib.dtype_code(mods[0].mx), _lib.stream_of(xs[0]),
+        rows, n, m, _lib.dtype_code(xs[0]), _lib.dtype_code(mods[0].mx), _lib.ptr(ws),
+        0 if ws is None else int(ws.numel()), _lib.stream_of(xs[0]),
     )
     return outs
 
@@ -479,20 +485,26 @@ class MM8Linear(torch.nn.Module):
         res = residual.reshape(*hidden.shape[:-1], down.out_features).contiguous()
         return down._run(hidden, residual=res, epilogue=_lib.EPI_RESIDUAL)
 
-    def rwkv7_workspace_bytes(self, rows: int) -> int:
-        """Scratch bytes a ``rows``-row call needs in the ``"mm8g"`` slot: none for
-        the fused GEMV (up to GEMV_ROWS rows), the tile GEMM's x', row sums and
-        split partials from GEMV_ROWS + 1 to GEMM_ROWS rows."""
+    def _workspace_slot(self, rows: int):
         rows = int(rows)
         if GEMV_ROWS < rows <= GEMM_ROWS:
-            return mm8_gemm_workspace_bytes(1, rows, self.in_features, self.out_features)
-        return 0
+            return "mm8g", mm8_gemm_workspace_bytes(1, rows, self.in_features, self.out_features)
+        if 0 < rows <= GEMV_ROWS:
+            return "mm8t", mm8t_workspace_bytes(1, rows, self.in_features, self.out_features)
+        return None, 0
+
+    def rwkv7_workspace_bytes(self, rows: int) -> int:
+        """Scratch bytes a ``rows``-row call needs: the fused GEMV's split-K
+        partials (``"mm8t"`` slot, only when the rows' x' exceeds one LDS chunk)
+        up to GEMV_ROWS rows, the tile GEMM's x', row sums and split partials
+        (``"mm8g"`` slot) from GEMV_ROWS + 1 to GEMM_ROWS rows."""
+        return self._workspace_slot(rows)[1]
 
     def rwkv7_reserve_workspace(self, rows: int) -> None:
-        """Grow the ``"mm8g"`` slot for ``rows``-row calls (call before graph capture)."""
-        need = self.rwkv7_workspace_bytes(rows)
+        """Grow the slot a ``rows``-row call uses (call before graph capture)."""
+        slot, need = self._workspace_slot(rows)
         if need:
-            _ws.reserve(self.w_blk.device, need, slot="mm8g")
+            _ws.reserve(self.w_blk.device, need, slot=slot)
 
     def extra_repr(self):
         return f"in={self.in_features}, out={self.out_features}, mm8(fused={self.fused}, hip=gfx950)"
@@ -544,5 +556,5 @@ __all__ = [
     "quantize_mm8", "dequantize_mm8", "quantize_mm8_outmajor", "quantize_mm8_blocked", "mm8_block", "mm8_unblock", "is_blocked",
     "is_out_major", "mm8_matmul", "mm8_linear", "mm8_matmul_into",
     "mm8_matmul_multi_into", "mm8_gemm_multi_into", "mm8_gemm_workspace_bytes", "mm8_gemv_triton",
-    "mm8_matmul_triton", "mm8_workspace_bytes", "MM8Linear", "quantize_model_mm8", "invalidate_model_caches",
+    "mm8_matmul_triton", "mm8_workspace_bytes", "mm8t_workspace_bytes", "MM8Linear", "quantize_model_mm8", "invalidate_model_caches",
 ]

@@ -3,7 +3,8 @@
 Slot ``"mm8"`` holds the row-major MM8 kernel's split-K partials and
 completion counters; the kernel leaves its counters at zero after every call,
 so one zero-initialised buffer per device can be reused by every call issued
-on one stream.  Slot ``"mm8g"`` holds the many-row MM8 GEMM's x', row sums and
+on one stream.  Slot ``"mm8t"`` holds the blocked GEMV's split-K partials
+(written before they are read).  Slot ``"mm8g"`` holds the many-row MM8 GEMM's x', row sums and
 split partials (each call writes them before reading).  Slot ``"lora"`` holds
 the LoRA kernels' fp32 partials.  Slots never share memory, so one kernel
 family cannot disturb another's counters.  Calls that run concurrently on

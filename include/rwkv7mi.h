@@ -240,6 +240,26 @@ int rwkv7mi_mm8t_matmul_multi(int nprob, const void* const* x,
                               int64_t O, int act_dtype, int meta_dtype,
                               void* stream);
 
+/* rwkv7mi_mm8t_matmul_multi with a workspace for split K: when the rows' x'
+ * (rows x in_features x 4 bytes) exceeds one LDS chunk, the inputs split into
+ * ranges of one chunk each, every workgroup stages its range once for all its
+ * column groups, and a second launch adds the ranges' fp32 partials in order
+ * (deterministic) and applies bias and epilogue.  `workspace` (16-byte
+ * aligned) must hold rwkv7mi_mm8t_matmul_workspace_bytes (0 when the call
+ * does not split; the workspace may then be NULL). */
+size_t rwkv7mi_mm8t_matmul_workspace_bytes(int nprob, int64_t rows, int64_t I,
+                                           int64_t O);
+int rwkv7mi_mm8t_matmul_multi_ws(int nprob, const void* const* x,
+                                 const uint8_t* const* w_blk,
+                                 const void* const* mx, const void* const* rx,
+                                 const void* const* my, const void* const* ry,
+                                 const void* const* bias,
+                                 const void* const* residual, void* const* y,
+                                 const int* epilogue, int64_t rows, int64_t I,
+                                 int64_t O, int act_dtype, int meta_dtype,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
 /* Many-row form of rwkv7mi_mm8t_matmul_multi for 17..256 rows (bsz-64
  * decode, short prefills): 64-row x 128-column MFMA tiles over split K, with
  * x' = x * ry rounded once to fp16 and the weights centred (w - 128) so that

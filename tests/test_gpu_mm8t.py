@@ -346,3 +346,34 @@ def test_mm8t_lnmix_rejects_unsupported():
         mm8_lnmix_multi_into(x, x.clone(), v, v, 1e-5, [v], [mod], [out], epilogues=[_lib.EPI_RESIDUAL])
     with pytest.raises(ValueError):
         mm8_lnmix_multi_into(x, x, v, v, 1e-5, [v], [mod], [out], h_out=x)
+
+
+@pytest.mark.parametrize("IO,rows", [((16384, 1024), 8), ((4096, 2048), 16), ((16384, 4096), 3)])
+def test_mm8t_split_k_epilogues(oracle, IO, rows):
+    """Rows whose x' exceeds one LDS chunk take split K (ranges of one chunk,
+    fp32 partials added in order by a second launch): bias, relu^2 and residual
+    epilogues against the fp64 oracle, and repeated calls bit-identical."""
+    from rwkv7mi import MM8Linear
+    from rwkv7mi.native_quant_mm8 import mm8t_workspace_bytes
+
+    I, O = IO
+    assert mm8t_workspace_bytes(1, rows, I, O) > 0, "this shape must take the split-K route"
+    rng = np.random.default_rng(I + O + rows)
+    lin = torch.nn.Linear(I, O, bias=True).to(device="cuda", dtype=torch.float16)
+    with torch.no_grad():
+        lin.weight.copy_(_cuda(rng.standard_normal((O, I)) * 0.02, torch.float16))
+        lin.bias.copy_(_cuda(rng.standard_normal(O) * 0.1, torch.float16))
+    m = MM8Linear(lin)
+    x = _cuda(rng.standard_normal((rows, I)), torch.float16)
+    res = _cuda(rng.standard_normal((rows, O)), torch.float16)
+    y = m(x)
+    y2 = m(x)
+    r2 = m.rwkv7_forward_relu2(x)
+    ad = m.rwkv7_forward_add(x, res)
+    torch.cuda.synchronize()
+    wd = oracle.mm8_dequant(*(_np(t) for t in (m.w_u8, m.mx, m.rx, m.my, m.ry)))
+    ref = _np(x).astype(np.float64) @ wd + _np(m.bias).astype(np.float64)
+    assert _rel_err(_np(y).astype(np.float64), ref) <= 2e-3
+    assert torch.equal(y, y2)
+    assert _rel_err(_np(r2).astype(np.float64), np.maximum(ref, 0) ** 2) <= 4e-3
+    assert _rel_err(_np(ad).astype(np.float64), ref + _np(res).astype(np.float64)) <= 2e-3
