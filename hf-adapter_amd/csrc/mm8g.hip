@@ -25,11 +25,14 @@
 //     adds the splits in order 0..S-1 and applies the epilogue (deterministic,
 //     no atomics).
 //
-// Precision: x' is rounded once to fp16 and the weights enter the MFMA as the
+// Precision: x' is rounded to fp16 and the weights enter the MFMA as the
 // exact integers (w - 128), so the large common part 128.5 sum_i x' of
 // (w + 0.5) is added from the fp32 row sum instead:
 //   y = rx [sum_i x'_16 (w - 128) + 128.5 sum_i x ry] + sum_i x my + mx sum_i x.
-// The fp16 rounding of x' then only touches the centred term.
+// The fp16 rounding of x' then only touches the centred term.  fp32
+// activations keep x' as fp16 hi + lo (x' = hi + lo to ~22 bits, as the
+// GEMV stages it) and take two MFMAs per product, in 32-row tiles so the
+// doubled LDS copy keeps the 64-row tile's footprint.
 namespace rwkv7mi {
 
 constexpr int MM8G_ROWS = 64;   // rows per workgroup tile
@@ -41,6 +44,7 @@ constexpr int MM8G_DEPTH = 4;   // weight ring depth (steps): ~1.5 us of HBM lat
 struct Mm8gBatch {
   Mm8tProb p[MM8T_MAXPROB];
   _Float16* xp;  // [nprob][rows][KB 128] x' = fp16(x ry), zero past I
+  _Float16* xl;  // same shape: fp16(x ry - xp), written and read for fp32 activations only
   float* rsum;   // [nprob][rows][3] sum x, sum x my, sum x ry
   float* part;   // [S][nprob][rows][O] fp32 partial products (S > 1)
   int rows, I, O, KB, S, ctiles, nprob;
@@ -87,6 +91,7 @@ __global__ __launch_bounds__(256) void mm8g_prep_kernel(const Mm8gBatch B) {
   const __amdgpu_buffer_rsrc_t ryr = mm8t_rsrc(P.ry, (uint32_t)(I * sizeof(TM)));
   const __amdgpu_buffer_rsrc_t myr = mm8t_rsrc(P.my, (uint32_t)(I * sizeof(TM)));
   _Float16* xo = B.xp + ((int64_t)p * B.rows + row) * KBK;
+  _Float16* xlo = B.xl + ((int64_t)p * B.rows + row) * KBK;
   float a = 0.f, b = 0.f, c = 0.f;
   constexpr int PB = 4;  // passes whose loads are in flight together
   for (int k0 = 8 * tid; k0 < KBK; k0 += 8 * 256 * PB) {
@@ -107,16 +112,20 @@ __global__ __launch_bounds__(256) void mm8g_prep_kernel(const Mm8gBatch B) {
       mm8t_cvt8(xv[u], x);
       mm8t_cvt8(rr[u], rv);
       mm8t_cvt8(mr[u], mv);
-      f16x8 h;
+      f16x8 h, l;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float xp = x[e] * rv[e];
         h[e] = (_Float16)xp;
+        l[e] = (_Float16)(xp - (float)h[e]);
         a += x[e];
         b += x[e] * mv[e];
         c += xp;
       }
-      if (k < KBK) *reinterpret_cast<f16x8*>(xo + k) = h;
+      if (k < KBK) {
+        *reinterpret_cast<f16x8*>(xo + k) = h;
+        if constexpr (std::is_same<TA, float>::value) *reinterpret_cast<f16x8*>(xlo + k) = l;
+      }
     }
   }
   __shared__ float part[4][3];
@@ -143,6 +152,9 @@ __global__ __launch_bounds__(256, 2) void mm8g_kernel(const Mm8gBatch B) {
   // weights of all its tiles, the next tile's first steps loading during the
   // current tile's last ones.
   static_assert(NKP % DEPTH == 0 && NKP % 4 == 0, "whole ring turns, whole staging passes");
+  constexpr bool LO = std::is_same<TA, float>::value;  // x' as hi + lo
+  constexpr int MT = LO ? 2 : 4;                        // MFMA M tiles per workgroup
+  constexpr int TROWS = 16 * MT;
   const int p = blockIdx.y;
   const Mm8tProb& P = B.p[p];
   const int I = B.I, O = B.O, KB = B.KB;
@@ -150,8 +162,8 @@ __global__ __launch_bounds__(256, 2) void mm8g_kernel(const Mm8gBatch B) {
   const int c0 = (int)blockIdx.x / B.S;
   const int kb0 = s * KB / B.S, kb1 = (s + 1) * KB / B.S;
   const int nkb = kb1 - kb0;  // K blocks of this split (<= NKP)
-  const int row0 = blockIdx.z * MM8G_ROWS;
-  const int nrows = min(MM8G_ROWS, B.rows - row0);
+  const int row0 = blockIdx.z * TROWS;
+  const int nrows = min(TROWS, B.rows - row0);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -160,6 +172,7 @@ __global__ __launch_bounds__(256, 2) void mm8g_kernel(const Mm8gBatch B) {
   constexpr int XS = 128 * NKP + 8;  // LDS row stride (halfs): rows land 16 bytes apart in the banks
   extern __shared__ __align__(16) char smem[];
   _Float16* xs = reinterpret_cast<_Float16*>(smem);
+  _Float16* xsl = xs + TROWS * XS;  // the lo rows (LO only)
   (void)I;
 
   // ---- this wave's two column groups of tile ct (empty past the last tile)
@@ -187,41 +200,48 @@ __global__ __launch_bounds__(256, 2) void mm8g_kernel(const Mm8gBatch B) {
   // the split and rows past the batch stage as zeros.
   {
     const int KBK = KB * 128;
-    const __amdgpu_buffer_rsrc_t xr = mm8t_rsrc(B.xp + ((int64_t)p * B.rows + row0) * KBK,
-                                                (uint32_t)nrows * (uint32_t)KBK * 2u);
-    constexpr int RPW = MM8G_ROWS / 4;  // rows per wave
+    constexpr int NH = LO ? 2 : 1;      // hi (and lo) copies
+    constexpr int RPW = TROWS / 4;      // rows per wave
     constexpr int NIT = NKP / 4;        // passes: 64 lanes x 8 inputs = 4 blocks per pass
     const int kbase = kb0 * 128, kend = kb1 * 128;
-    u32x4 v[NIT][RPW];
+    u32x4 v[NH][NIT][RPW];
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int k = kbase + 8 * (lane + 64 * it);
+    for (int hl = 0; hl < NH; ++hl) {
+      const __amdgpu_buffer_rsrc_t xr = mm8t_rsrc((hl ? B.xl : B.xp) + ((int64_t)p * B.rows + row0) * KBK,
+                                                  (uint32_t)nrows * (uint32_t)KBK * 2u);
 #pragma unroll
-      for (int i = 0; i < RPW; ++i) {
-        const int r = wave + 4 * i;
-        v[it][i] = mm8t_ld16(xr, k < kend && r < nrows ? (uint32_t)(r * KBK + k) * 2u : MM8T_OOB);
+      for (int it = 0; it < NIT; ++it) {
+        const int k = kbase + 8 * (lane + 64 * it);
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+          const int r = wave + 4 * i;
+          v[hl][it][i] = mm8t_ld16(xr, k < kend && r < nrows ? (uint32_t)(r * KBK + k) * 2u : MM8T_OOB);
+        }
       }
     }
 #pragma unroll
-    for (int it = 0; it < NIT; ++it)
+    for (int hl = 0; hl < NH; ++hl)
 #pragma unroll
-      for (int i = 0; i < RPW; ++i)
-        *reinterpret_cast<u32x4*>(xs + (wave + 4 * i) * XS + 8 * (lane + 64 * it)) = v[it][i];
+      for (int it = 0; it < NIT; ++it)
+#pragma unroll
+        for (int i = 0; i < RPW; ++i)
+          *reinterpret_cast<u32x4*>((hl ? xsl : xs) + (wave + 4 * i) * XS + 8 * (lane + 64 * it)) = v[hl][it][i];
   }
   __syncthreads();
 
   const _Float16* abase = xs + n * XS + 16 * kg;
+  const _Float16* albase = xsl + n * XS + 16 * kg;
   for (int ct = c0; ct < B.ctiles; ct += B.cw) {
     const __amdgpu_buffer_rsrc_t nr0 = grsrc(ct + B.cw, 0), nr1 = grsrc(ct + B.cw, 1);
     // ---- per step (one K block) a lane converts its four B operands of each
     // group, refills the ring slot (from the next tile in the last DEPTH
     // steps), then 4 operands x 4 M tiles x 2 groups = 32 MFMAs (eight
     // independent accumulator chains, one shape)
-    f32x4 acc[2][4];
+    f32x4 acc[2][MT];
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi)
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) acc[gi][mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      for (int mt = 0; mt < MT; ++mt) acc[gi][mt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NKP; ++j) {
       const int d = j % DEPTH;
@@ -243,10 +263,15 @@ __global__ __launch_bounds__(256, 2) void mm8g_kernel(const Mm8gBatch B) {
         // operand hq = rows 64 (hq / 2) + 16 kg + 8 (hq % 2) of the block
         const int off = 128 * j + 64 * (hq >> 1) + 8 * (hq & 1);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
           const f16x8 a = *reinterpret_cast<const f16x8*>(abase + mt * 16 * XS + off);
           acc[0][mt] = mfma16x16x32(a, bv[0][hq], acc[0][mt]);
           acc[1][mt] = mfma16x16x32(a, bv[1][hq], acc[1][mt]);
+          if constexpr (LO) {
+            const f16x8 al = *reinterpret_cast<const f16x8*>(albase + mt * 16 * XS + off);
+            acc[0][mt] = mfma16x16x32(al, bv[0][hq], acc[0][mt]);
+            acc[1][mt] = mfma16x16x32(al, bv[1][hq], acc[1][mt]);
+          }
         }
       }
     }
@@ -258,7 +283,7 @@ __global__ __launch_bounds__(256, 2) void mm8g_kernel(const Mm8gBatch B) {
       for (int gi = 0; gi < 2; ++gi) {
         const int o = (g0 + gi) * MM8T_COLS + n;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 16 * mt + 4 * kg + e;
@@ -276,7 +301,7 @@ __global__ __launch_bounds__(256, 2) void mm8g_kernel(const Mm8gBatch B) {
       for (int gi = 0; gi < 2; ++gi) {
         const int o = (g0 + gi) * MM8T_COLS + n;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 16 * mt + 4 * kg + e;
@@ -348,16 +373,19 @@ static int mm8g_splits(int64_t rows, int64_t I, int64_t O, int nprob, int req) {
   return (int)std::min<int64_t>(S, KB);
 }
 
-// Workspace: x' [nprob][rows][KB 128] fp16 | row sums [nprob][rows][3] fp32 |
-// partials [S][nprob][rows][O] fp32 (S > 1), each part 256-byte aligned.
+// Workspace: x' [nprob][rows][KB 128] fp16 | its lo half, same shape (used by
+// fp32 activations; reserved for every dtype so the size does not depend on
+// it) | row sums [nprob][rows][3] fp32 | partials [S][nprob][rows][O] fp32
+// (S > 1), each part 256-byte aligned.
 struct Mm8gWs {
-  size_t xp, rsum, part, total;
+  size_t xp, xl, rsum, part, total;
 };
 static Mm8gWs mm8g_ws_layout(int S, int nprob, int64_t rows, int64_t I, int64_t O) {
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
   Mm8gWs w{};
   w.xp = 0;
-  w.rsum = up((size_t)nprob * rows * (size_t)((I + 127) / 128) * 128u * 2u);
+  w.xl = up((size_t)nprob * rows * (size_t)((I + 127) / 128) * 128u * 2u);
+  w.rsum = 2 * w.xl;
   w.part = w.rsum + up((size_t)nprob * rows * 3u * 4u);
   w.total = w.part + (S > 1 ? up((size_t)S * nprob * rows * O * 4u) : 0);
   return w;
@@ -383,7 +411,8 @@ static int mm8g_run(const char* who, int nprob, const void* const* x, const uint
   if (rows < 0 || I <= 0 || O <= 0 || splits < 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
   if (rows == 0) return RWKV7MI_OK;
   if (I % 16) return fail(RWKV7MI_EINVAL, w + ": in_features must be a multiple of 16");
-  if (I > (1 << 24) || O > (1 << 24) || rows > 65535LL * MM8G_ROWS || rows * std::max(I, O) > INT32_MAX)
+  const int trows = act_dtype == RWKV7MI_F32 ? MM8G_ROWS / 2 : MM8G_ROWS;  // rows per tile (fp32: hi + lo)
+  if (I > (1 << 24) || O > (1 << 24) || rows > 65535LL * trows || rows * std::max(I, O) > INT32_MAX)
     return fail(RWKV7MI_EINVAL, w + ": too large");
   if (!valid_dtype(act_dtype) || !valid_dtype(meta_dtype)) return fail(RWKV7MI_EINVAL, w + ": bad dtype");
   Mm8gBatch b{};
@@ -416,13 +445,14 @@ static int mm8g_run(const char* who, int nprob, const void* const* x, const uint
   b.ctiles = (int)((O + MM8G_COLS - 1) / MM8G_COLS);
   char* wsb = reinterpret_cast<char*>(workspace);
   b.xp = reinterpret_cast<_Float16*>(wsb + lay.xp);
+  b.xl = reinterpret_cast<_Float16*>(wsb + lay.xl);
   b.rsum = reinterpret_cast<float*>(wsb + lay.rsum);
   b.part = S > 1 ? reinterpret_cast<float*>(wsb + lay.part) : nullptr;
   const int nkp = (KB + S - 1) / S <= 4 ? 4 : MM8G_MAXKB;  // staged blocks: one of two kernel instances
-  const size_t lds = (size_t)MM8G_ROWS * (size_t)(128 * nkp + 8) * 2u;
+  const size_t lds = (size_t)MM8G_ROWS * (size_t)(128 * nkp + 8) * 2u;  // (fp32: half the rows, twice the copies)
   // persistent column tiles: as many workgroups as fit the CUs at once (one per
   // CU with 8 staged blocks, two with 4), the tiles shared out evenly
-  const int64_t rtiles = (rows + MM8G_ROWS - 1) / MM8G_ROWS;
+  const int64_t rtiles = (rows + trows - 1) / trows;
   const int64_t slots = mm8t_cus() * (nkp == 4 ? 2 : 1);
   const int64_t cwmax = std::max<int64_t>(1, slots / ((int64_t)S * nprob * rtiles));
   const int64_t per = (b.ctiles + cwmax - 1) / cwmax;  // tiles per workgroup

@@ -101,13 +101,22 @@ __device__ __forceinline__ f16x8 mm8t_b_operand(uint32_t d0, uint32_t d1) {
 
 // nibbles of dword d = rows r..r+7 of one column (low nibble first) -> fp16
 // [u + 0.5] x 8 in the order [0,4,1,5,2,6,3,7] (the x' staging for 4-bit
-// weights stores each 8-group in the same order)
+// weights stores each 8-group in the same order).  fp16 pairs with exponent
+// 0x64 hold 1024 + u (nibble in bits 0-3) or 1024 + 16 u (bits 4-7); one
+// packed add of -1023.5, or one packed fma by 1/16 with -63.5, gives u + 0.5
+// exactly.  9 VALU ops per dword.
 __device__ __forceinline__ f16x8 mm4t_b_operand(uint32_t d) {
+  const uint32_t d8 = d >> 8;
+  const f16x2 a = __builtin_bit_cast(f16x2, and_or(d, 0x000F000Fu, 0x64006400u));
+  const f16x2 b = __builtin_bit_cast(f16x2, and_or(d, 0x00F000F0u, 0x64006400u));
+  const f16x2 c = __builtin_bit_cast(f16x2, and_or(d8, 0x000F000Fu, 0x64006400u));
+  const f16x2 e = __builtin_bit_cast(f16x2, and_or(d8, 0x00F000F0u, 0x64006400u));
   const f16x2 half_off = {(_Float16)-1023.5f, (_Float16)-1023.5f};
-  f16x2 p0 = __builtin_bit_cast(f16x2, (d & 0x000f000fu) | 0x64006400u) + half_off;
-  f16x2 p1 = __builtin_bit_cast(f16x2, ((d >> 4) & 0x000f000fu) | 0x64006400u) + half_off;
-  f16x2 p2 = __builtin_bit_cast(f16x2, ((d >> 8) & 0x000f000fu) | 0x64006400u) + half_off;
-  f16x2 p3 = __builtin_bit_cast(f16x2, ((d >> 12) & 0x000f000fu) | 0x64006400u) + half_off;
+  const f16x2 sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const f16x2 off16 = {(_Float16)-63.5f, (_Float16)-63.5f};
+  const f16x2 p0 = a + half_off, p2 = c + half_off;
+  const f16x2 p1 = __builtin_elementwise_fma(b, sixteenth, off16);
+  const f16x2 p3 = __builtin_elementwise_fma(e, sixteenth, off16);
   return (f16x8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 

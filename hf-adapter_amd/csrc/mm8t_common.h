@@ -74,6 +74,16 @@ __device__ __forceinline__ void mm8t_cvt8(const Raw8<__hip_bfloat16>& a, float (
   }
 }
 
+// (a & mask) | bits in one v_and_or_b32 (the compiler otherwise emits a
+// separate and + or).  A VOP3 encoding on gfx950 takes no literal and reads
+// at most one SGPR: the mask comes from an SGPR, the bits from a VGPR (both
+// loop-invariant, materialised once).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(bits));
+  return r;
+}
+
 // Compute units of the current device (cached per device).
 int64_t mm8t_cus();
 

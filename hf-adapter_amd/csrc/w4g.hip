@@ -23,7 +23,7 @@
 //   sum_i W x = s sum (q - 8) x + (8 s + b) sum_i x,
 // and the group sums of x come from one more MFMA per step against a B
 // operand of ones, which lands them in the accumulator layout directly.
-#include "common.h"
+#include "mm8t_common.h"
 
 namespace rwkv7mi {
 
@@ -56,17 +56,22 @@ __device__ __forceinline__ void w4_load_a(const TA* __restrict__ xrow, bool ok, 
 }
 
 __device__ __forceinline__ f16x8 w4_nibbles_to_f16(uint32_t d) {
-  // d = 8 nibbles n0..n7 (n_{2j} low nibble of byte j); out = [n0,n4,n1,n5,n2,n6,n3,n7] - 8
-  f16x8 out;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const uint32_t hv = ((d >> (4 * s)) & 0x000F000Fu) | 0x64006400u;
-    f16x2 h = __builtin_bit_cast(f16x2, hv);
-    h = h + (f16x2){(_Float16)-1032.0f, (_Float16)-1032.0f};
-    out[2 * s] = h[0];
-    out[2 * s + 1] = h[1];
-  }
-  return out;
+  // d = 8 nibbles n0..n7 (n_{2j} low nibble of byte j); out = [n0,n4,n1,n5,n2,n6,n3,n7] - 8.
+  // fp16 pairs with exponent 0x64 hold 1024 + n (nibble in bits 0-3) or
+  // 1024 + 16 n (bits 4-7): one packed add of -1032 or one packed fma by
+  // 1/16 with -72 gives n - 8 exactly.  9 VALU ops per dword.
+  const uint32_t d8 = d >> 8;
+  const f16x2 a = __builtin_bit_cast(f16x2, and_or(d, 0x000F000Fu, 0x64006400u));
+  const f16x2 b = __builtin_bit_cast(f16x2, and_or(d, 0x00F000F0u, 0x64006400u));
+  const f16x2 c = __builtin_bit_cast(f16x2, and_or(d8, 0x000F000Fu, 0x64006400u));
+  const f16x2 e = __builtin_bit_cast(f16x2, and_or(d8, 0x00F000F0u, 0x64006400u));
+  const f16x2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const f16x2 sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const f16x2 off16 = {(_Float16)-72.0f, (_Float16)-72.0f};
+  const f16x2 p0 = a + off, p2 = c + off;
+  const f16x2 p1 = __builtin_elementwise_fma(b, sixteenth, off16);
+  const f16x2 p3 = __builtin_elementwise_fma(e, sixteenth, off16);
+  return (f16x8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
 template <int MT, typename TA, typename TS, bool AFF>
@@ -150,6 +155,252 @@ __global__ __launch_bounds__(256) void w4g_kernel(const TA* __restrict__ x, cons
       v += ld(residual, (int64_t)b * O + oo);
     }
     y[(int64_t)b * O + oo] = from_f32<TA>(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming GEMV for 1..16 rows (decode): the weights are read once, in long
+// coalesced runs with a load ring in flight, and x is staged in LDS once per
+// workgroup instead of re-read from L2 per MFMA.
+//
+// A workgroup (NW waves) owns 16 output columns at a time and loops over
+// column groups g = blockIdx.x, + gridDim.x, ... (persistent).  K is walked in
+// 256-input steps (128 bytes of each column): wave w takes steps w, w + NW,
+// ...; lane (n = l%16, kg = l/16) loads bytes 16kg.. and 64 + 16kg.. of
+// column n's step, two 16-byte loads whose dwords are the B operands of 8
+// MFMAs (nibbles widened to fp16 q - 8, exact).  Each 128-input half of a
+// step lies in one scale group (group 128: its own; group 256: half of one),
+// so a half's 4 MFMAs accumulate from zero and are scaled once:
+//   acc += s[o, grp] * sum_half (q - 8) x          (symmetric)
+//       +  (8 s + b)[o, grp] * sum_half x          (affine, the half's x sum
+//                                                   from the staging, in LDS)
+// x is staged as fp16 in the nibble order [0,4,1,5,2,6,3,7] of each 8-group,
+// split hi + lo for fp32 / bf16 activations (two MFMAs per product).  When
+// one chunk of KC inputs covers I, x stays staged for all of the workgroup's
+// column groups; otherwise each group re-stages its chunks.  Raw buffer loads
+// with out-of-range offsets make every load unconditional (tails read zeros).
+struct W4tArgs {
+  const void* x;        // [rows, I]
+  const uint8_t* w;     // [O, I/2]
+  const void* scales;   // [O, G]
+  const void* gbias;    // [O, G] (affine) or null
+  const void* bias;     // [O] or null
+  const void* residual; // [rows, O] or null
+  void* y;              // [rows, O]
+  int rows, I, O, G, gshift, epilogue;  // gshift: log2(group / 128)
+};
+
+template <typename TS>
+__device__ __forceinline__ uint32_t w4t_ld_raw(__amdgpu_buffer_rsrc_t r, uint32_t e, bool valid) {
+  const int off = valid ? (int)(e * (uint32_t)sizeof(TS)) : (int)BUF_OOB;
+  if constexpr (sizeof(TS) == 4)
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  else
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+template <typename TS>
+__device__ __forceinline__ float w4t_raw_f32(uint32_t v) {
+  if constexpr (sizeof(TS) == 4)
+    return __uint_as_float(v);
+  else if constexpr (std::is_same<TS, __half>::value)
+    return __half2float(__ushort_as_half((unsigned short)v));
+  else
+    return __uint_as_float(v << 16);
+}
+
+template <typename TA, typename TS, int NW, int CSW, bool AFF>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void w4t_kernel(const W4tArgs A) {
+  constexpr int NT = 64 * NW;
+  constexpr int DEPTH = 2;              // ring steps per wave (2 KB each)
+  constexpr int KC = 256 * NW * CSW;    // inputs per staged chunk
+  constexpr int XS = KC + 8;            // LDS row stride (halfs)
+  constexpr bool HL = !std::is_same<TA, __half>::value;
+  static_assert(CSW % DEPTH == 0, "the ring turns whole per chunk");
+  const int I = A.I, O = A.O, G = A.G, gshift = A.gshift;
+  const int nrows = A.rows;  // 1..16 (checked by the host)
+  const int bcol = I / 2;    // bytes per column
+  const int ngroups = (O + 15) / 16;
+  const int nchunks = (I + KC - 1) / KC;
+  const int J = nchunks * CSW;  // steps per wave per column group
+  extern __shared__ __align__(16) char smem[];
+  _Float16* xh = reinterpret_cast<_Float16*>(smem);
+  _Float16* xl = xh + nrows * XS;
+  float* gsum = reinterpret_cast<float*>(xh + (HL ? 2 : 1) * nrows * XS);  // [KC / 128][16]
+  __shared__ float red[NW][16][17];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n = lane & 15, kg = lane >> 4;
+  const uint32_t lane_off = (uint32_t)n * (uint32_t)bcol + 16u * (uint32_t)kg;
+
+  struct Res {
+    __amdgpu_buffer_rsrc_t w, s, b;
+  };
+  auto group_res = [&](int g) {
+    const int nc = g < ngroups ? min(16, O - 16 * g) : 0;
+    const int g0 = g < ngroups ? g : 0;
+    Res r;
+    r.w = make_rsrc(A.w + (int64_t)g0 * 16 * bcol, (uint32_t)nc * (uint32_t)bcol);
+    r.s = make_rsrc(reinterpret_cast<const TS*>(A.scales) + (int64_t)g0 * 16 * G, (uint32_t)(nc * G * sizeof(TS)));
+    r.b = make_rsrc(AFF ? reinterpret_cast<const TS*>(A.gbias) + (int64_t)g0 * 16 * G : nullptr,
+                    AFF ? (uint32_t)(nc * G * sizeof(TS)) : 0u);
+    return r;
+  };
+  // ring slot: weights, and the raw scale (and bias) bits of the step's halves
+  u32x4 buf[DEPTH][2];
+  uint32_t sraw[DEPTH][2], braw[DEPTH][2];
+  auto load_step = [&](const Res& r, int j, int d) {
+    const int c = j / CSW, jl = j % CSW;
+    const int gs = c * (NW * CSW) + wave + NW * jl;  // global step of this wave
+    const int b0 = 128 * gs + 16 * kg;
+    buf[d][0] = buf_ld16(r.w, b0 < bcol ? lane_off + 128u * (uint32_t)gs : BUF_OOB);
+    buf[d][1] = buf_ld16(r.w, b0 + 64 < bcol ? lane_off + 128u * (uint32_t)gs + 64u : BUF_OOB);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int blk = 2 * gs + h;  // 128-input block
+      const int grp = blk >> gshift;
+      const bool ok = 128 * blk < I;
+      sraw[d][h] = w4t_ld_raw<TS>(r.s, (uint32_t)(n * G + grp), ok);
+      if constexpr (AFF) braw[d][h] = w4t_ld_raw<TS>(r.b, (uint32_t)(n * G + grp), ok);
+    }
+  };
+
+  // staging of chunk c: 8-input items (row r, q), 64 consecutive items per
+  // wave and pass, so a 16-lane row of a wave covers one 128-input block of
+  // one row (its x sum for the affine form is a 16-lane reduction)
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(A.x, (uint32_t)(nrows * I * sizeof(TA)));
+  auto stage = [&](int c) {
+    constexpr int QPR = KC / 8;  // items per row
+    constexpr int SB = 2;        // passes whose loads are in flight together
+    const int nitems = nrows * QPR;
+    for (int it0 = tid; it0 < nitems; it0 += SB * NT) {
+      Raw8<TA> rv[SB];
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int it = it0 + u * NT;
+        const int r = it / QPR, q = it % QPR;
+        const int k = c * KC + 8 * q;
+        rv[u] = mm8t_ld8<TA>(xr, (uint32_t)(r * I + k), it < nitems && k < I);
+      }
+#pragma unroll
+      for (int u = 0; u < SB; ++u) {
+        const int it = it0 + u * NT;  // wave-uniform validity: nitems is a multiple of 64
+        if (it < nitems) {
+          const int r = it / QPR, q = it % QPR;
+          float v[8];
+          mm8t_cvt8(rv[u], v);
+          f16x8 hi, lo;
+          float sum = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float f = v[(e >> 1) + 4 * (e & 1)];
+            const _Float16 h = (_Float16)f;
+            hi[e] = h;
+            lo[e] = (_Float16)(f - (float)h);
+            sum += v[e];
+          }
+          *reinterpret_cast<f16x8*>(xh + r * XS + 8 * q) = hi;
+          if constexpr (HL) *reinterpret_cast<f16x8*>(xl + r * XS + 8 * q) = lo;
+          if constexpr (AFF) {
+            sum = group_sum<16>(sum);
+            if ((lane & 15) == 0) gsum[(q >> 4) * 16 + r] = sum;
+          }
+        }
+      }
+    }
+  };
+
+  const int arow = n < nrows ? n : nrows - 1;
+  const _Float16* ah = xh + arow * XS + 32 * kg;
+  const _Float16* al = xl + arow * XS + 32 * kg;
+
+  int g = blockIdx.x;
+  Res wr = group_res(g), wn = group_res(g + gridDim.x);
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) load_step(wr, d, d);  // DEPTH <= CSW <= J
+  if (nchunks == 1) {
+    stage(0);
+    __syncthreads();
+  }
+  const TS* bias = reinterpret_cast<const TS*>(A.bias);
+  for (; g < ngroups; g += gridDim.x) {
+    f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nchunks; ++c) {
+      if (nchunks > 1) {
+        __syncthreads();  // the previous chunk's (or group's) LDS reads are done
+        stage(c);
+        __syncthreads();
+      }
+      const bool last_chunk = c == nchunks - 1;
+#pragma unroll
+      for (int jl = 0; jl < CSW; ++jl) {
+        const int d = jl % DEPTH;
+        f16x8 bv[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bv[q] = w4_nibbles_to_f16(buf[d][0][q]);
+          bv[4 + q] = w4_nibbles_to_f16(buf[d][1][q]);
+        }
+        const uint32_t s0 = sraw[d][0], s1 = sraw[d][1];
+        const uint32_t z0 = AFF ? braw[d][0] : 0u, z1 = AFF ? braw[d][1] : 0u;
+        // refill the slot (from the next column group past the last step)
+        const int t = c * CSW + jl + DEPTH;
+        if (!last_chunk || jl + DEPTH < CSW)
+          load_step(wr, t, d);
+        else
+          load_step(wn, t - J, d);
+        __builtin_amdgcn_sched_barrier(0);
+        const int kl = 256 * (wave + NW * jl);  // chunk-local first input of the step
+        f32x4 gh[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          gh[h] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int off = kl + 128 * h + 8 * q;
+            gh[h] = mfma16x16x32(*reinterpret_cast<const f16x8*>(ah + off), bv[4 * h + q], gh[h]);
+            if constexpr (HL) gh[h] = mfma16x16x32(*reinterpret_cast<const f16x8*>(al + off), bv[4 * h + q], gh[h]);
+          }
+        }
+        const float sc0 = w4t_raw_f32<TS>(s0), sc1 = w4t_raw_f32<TS>(s1);
+        acc += sc0 * gh[0];
+        acc += sc1 * gh[1];
+        if constexpr (AFF) {
+          const int blk = kl / 128;  // chunk-local 128-input block of half 0
+          const f32x4 x0 = *reinterpret_cast<const f32x4*>(gsum + blk * 16 + 4 * kg);
+          const f32x4 x1 = *reinterpret_cast<const f32x4*>(gsum + (blk + 1) * 16 + 4 * kg);
+          acc += (8.f * sc0 + w4t_raw_f32<TS>(z0)) * x0;
+          acc += (8.f * sc1 + w4t_raw_f32<TS>(z1)) * x1;
+        }
+      }
+    }
+    // ---- waves' partial tiles (lane: column n, rows 4kg..4kg+3), then one
+    // thread per (row, column) adds them in wave order and finishes
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[wave][4 * kg + e][n] = acc[e];
+    __syncthreads();
+    if (tid < nrows * 16) {
+      const int m = tid >> 4, cn = tid & 15;
+      const int o = 16 * g + cn;
+      if (o < O) {
+        float v = red[0][m][cn];
+#pragma unroll
+        for (int q = 1; q < NW; ++q) v += red[q][m][cn];
+        if (bias) v += ld(bias, o);
+        const int64_t oi = (int64_t)m * O + o;
+        if (A.epilogue == RWKV7MI_EPI_RELU2) {
+          v = fmaxf(v, 0.f);
+          v = v * v;
+        } else if (A.epilogue == RWKV7MI_EPI_RESIDUAL) {
+          v += ld(reinterpret_cast<const TA*>(A.residual), oi);
+        }
+        reinterpret_cast<TA*>(A.y)[oi] = from_f32<TA>(v);
+      }
+    }
+    wr = wn;
+    wn = group_res(g + 2 * gridDim.x);
   }
 }
 
@@ -250,6 +501,66 @@ extern "C" int rwkv7mi_w4g_pack(const void* weight, int64_t O, int64_t I, int64_
   });
 }
 
+// Streaming GEMV plan (rows <= 16): waves per workgroup and steps per wave per
+// chunk.  Eight-wave workgroups (one per CU) when the column groups do not
+// fill two four-wave workgroups per CU; the smallest chunk that holds all of
+// I when its LDS fits (x then stays staged for every column group), else the
+// largest that fits (re-staged per group).  Returns the LDS bytes (0: none fits).
+static size_t w4t_lds(int64_t rows, int kc, bool hl, bool aff) {
+  return (size_t)rows * (size_t)(kc + 8) * 2u * (hl ? 2u : 1u) + (aff ? (size_t)(kc / 128) * 16u * 4u : 0u);
+}
+static size_t w4t_plan(int64_t rows, int64_t I, int64_t O, bool hl, bool aff, int* nw, int* csw) {
+  constexpr size_t TWO = 64 * 1024, ONE = 144 * 1024;  // per workgroup: two per CU / one per CU
+  struct C { int nw, csw; };
+  static const C cands[] = {{4, 2}, {4, 4}, {8, 2}, {4, 16}, {8, 8}};  // chunks 2K, 4K, 4K, 16K, 16K inputs
+  const int64_t ngroups = (O + 15) / 16;
+  const int want = ngroups <= mm8t_cus() ? 8 : 4;
+  for (int pass = 0; pass < 2; ++pass) {  // whole-I chunks: the preferred width, then the other
+    const int wnw = pass == 0 ? want : 12 - want;
+    for (const C& c : cands) {
+      const int kc = 256 * c.nw * c.csw;
+      const size_t lds = w4t_lds(rows, kc, hl, aff);
+      if (aff && c.nw == 4 && c.csw == 16) continue;  // (that instance runs out of registers)
+      if (c.nw == wnw && kc >= I && lds <= (c.nw == 4 ? TWO : ONE)) {
+        *nw = c.nw, *csw = c.csw;
+        return lds;
+      }
+    }
+  }
+  for (int i = 4; i >= 0; --i) {  // several chunks: the longest that fits one workgroup per CU
+    if (aff && cands[i].nw == 4 && cands[i].csw == 16) continue;
+    const int kc = 256 * cands[i].nw * cands[i].csw;
+    const size_t lds = w4t_lds(rows, kc, hl, aff);
+    if (kc < I && lds <= ONE) {
+      *nw = cands[i].nw, *csw = cands[i].csw;
+      return lds;
+    }
+  }
+  return 0;
+}
+
+template <typename TA, typename TS, int NW, int CSW, bool AFF>
+static int w4t_launch(dim3 grid, size_t lds, void* stream, const W4tArgs& a) {
+  static std::atomic<uint64_t> raised{0};  // devices whose dynamic LDS limit is raised for this instance
+  if (int rc = raise_dynamic_lds(reinterpret_cast<const void*>(&w4t_kernel<TA, TS, NW, CSW, AFF>), 144 * 1024 + 1024,
+                                 raised, "w4t_kernel"))
+    return rc;
+  hipLaunchKernelGGL((w4t_kernel<TA, TS, NW, CSW, AFF>), grid, dim3(64 * NW), lds, as_stream(stream), a);
+  return check_launch("w4t_kernel");
+}
+
+template <typename TA, typename TS, bool AFF>
+static int w4t_go(int nw, int csw, dim3 grid, size_t lds, void* stream, const W4tArgs& a) {
+  if (nw == 4) {
+    if (csw == 2) return w4t_launch<TA, TS, 4, 2, AFF>(grid, lds, stream, a);
+    if (csw == 4) return w4t_launch<TA, TS, 4, 4, AFF>(grid, lds, stream, a);
+    if constexpr (!AFF) return w4t_launch<TA, TS, 4, 16, AFF>(grid, lds, stream, a);
+    return fail(RWKV7MI_EINVAL, "w4t_kernel: no affine instance with that chunk");
+  }
+  if (csw == 2) return w4t_launch<TA, TS, 8, 2, AFF>(grid, lds, stream, a);
+  return w4t_launch<TA, TS, 8, 8, AFF>(grid, lds, stream, a);
+}
+
 static int w4_matmul(const char* who, const void* x, const uint8_t* packed, const void* scales, const void* gbias,
                      const void* bias, const void* residual, void* y, int64_t rows, int64_t O, int64_t I,
                      int64_t group, int epilogue, int act_dtype, int scale_dtype, void* stream) {
@@ -265,6 +576,28 @@ static int w4_matmul(const char* who, const void* x, const uint8_t* packed, cons
     return fail(RWKV7MI_EINVAL, w + ": x and packed must be 16-byte aligned");
   if (!valid_dtype(act_dtype) || !valid_dtype(scale_dtype)) return fail(RWKV7MI_EINVAL, w + ": bad dtype");
   const size_t esz = act_dtype == RWKV7MI_F32 ? 4 : 2;
+  if (rows <= 16 && I <= (1 << 22) && (int64_t)rows * I * (int64_t)esz <= INT32_MAX &&
+      16 * (I / 2) <= INT32_MAX) {
+    int nw = 4, csw = 4;
+    const bool hl = act_dtype != RWKV7MI_F16, aff = gbias != nullptr;
+    const size_t lds = w4t_plan(rows, I, O, hl, aff, &nw, &csw);
+    if (lds) {
+      W4tArgs a{x, packed, scales, gbias, bias, residual, y, (int)rows, (int)I, (int)O, (int)(I / group),
+                group == 256 ? 1 : 0, epilogue};
+      const int64_t ngroups = (O + 15) / 16;
+      const int64_t per_cu = nw == 4 && lds <= 64 * 1024 ? 2 : 1;
+      const int64_t gx = std::min<int64_t>(ngroups, mm8t_cus() * per_cu);
+      const dim3 grid((unsigned)gx);
+      return dispatch_dtype(act_dtype, [&](auto ta) {
+        using TA = decltype(ta);
+        return dispatch_dtype(scale_dtype, [&](auto ts) {
+          using TS = decltype(ts);
+          return aff ? w4t_go<TA, TS, true>(nw, csw, grid, lds, stream, a)
+                     : w4t_go<TA, TS, false>(nw, csw, grid, lds, stream, a);
+        });
+      });
+    }
+  }
   for (int64_t r0 = 0; r0 < rows; r0 += 64) {
     const int64_t nr = rows - r0 > 64 ? 64 : rows - r0;
     const int mt = nr <= 16 ? 1 : nr <= 32 ? 2 : 4;

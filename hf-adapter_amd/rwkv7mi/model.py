@@ -11,8 +11,8 @@ the per-layer decode body of ``_block_ip_batched``
 (rwkv7_hf/native_jit_prefill.py:223-1057) and the graph-captured decode
 runner (rwkv7_hf/native_graph_runtime.py:212-711, ``torch.cuda.graph`` =
 hipGraph on ROCm).  Every operator is a HIP kernel from librwkv7mi.so except
-the embedding row gather and, for prefills with more than 64 rows, the dense
-library GEMM that follows an MM8 dequantisation (rocBLAS through torch).
+the embedding row gather and, for prefills of more than 256 rows, the plain
+library GEMMs of dense (unquantised) projections (rocBLAS through torch).
 """
 from __future__ import annotations
 
@@ -31,7 +31,8 @@ from .fused_output import fused_attn_output_prepare
 from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
-from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_workspace_bytes,
+from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_prefill_multi_into,
+                               mm8_gemm_workspace_bytes,
                                mm8_lnmix_multi_into, mm8_matmul_multi_into, mm8t_workspace_bytes)
 from .native_quant_policy import should_quantize_linear
 from .self_chunk_rwkv7 import _run_chunk
@@ -199,22 +200,12 @@ class QuantLinear:
                 raise ValueError("QuantLinear: unsupported activation / residual combination")
             mm8_gemm_multi_into([x2], [self.m], [out], residuals=[residual], epilogues=[epi])
             return out
-        if rows > self.GEMV_ROWS:
-            m = self.m
-            W = torch.empty((m.out_features, m.in_features), device=x2.device, dtype=x2.dtype)
-            _lib.call("rwkv7mi_mm8t_dequant", _lib.ptr(m.w_blk), _lib.ptr(m.mx), _lib.ptr(m.rx), _lib.ptr(m.my),
-                      _lib.ptr(m.ry), _lib.ptr(W), m.in_features, m.out_features, _lib.dtype_code(m.mx),
-                      _lib.dtype_code(W), _lib.stream_of(x2))
-            y = torch.nn.functional.linear(x2, W)
-            if m.bias is not None:
-                y = y + m.bias
-            if act == 3:
-                y = torch.relu(y).square()
-            if residual is not None:
-                y = y + residual
-            out.copy_(y)
-            return out
+        if act not in (0, 3) or (act == 3 and residual is not None):
+            raise ValueError("QuantLinear: unsupported activation / residual combination")
         epi = _lib.EPI_RELU2 if act == 3 else (_lib.EPI_RESIDUAL if residual is not None else _lib.EPI_NONE)
+        if rows > self.GEMM_ROWS and is_blocked(self.m.w_blk):
+            mm8_gemm_prefill_multi_into([x2], [self.m], [out], residuals=[residual], epilogues=[epi])
+            return out
         return self.m._run(x2, out=out, residual=residual, epilogue=epi)
 
     @staticmethod
@@ -222,13 +213,15 @@ class QuantLinear:
         """The same as ``[l.apply(x, o) for ...]``; out-major MM8 modules of one
         shape run as one launch."""
         rows = int(xs[0].shape[0])
-        if (all(isinstance(l, QuantLinear) for l in lins) and rows <= QuantLinear.GEMM_ROWS
+        if (all(isinstance(l, QuantLinear) for l in lins)
                 and len({(l.in_features, l.out_features) for l in lins}) == 1
                 and all(is_blocked(l.m.w_blk) for l in lins)):
             if rows <= QuantLinear.GEMV_ROWS:
                 mm8_matmul_multi_into(list(xs), [l.m for l in lins], list(outs))
-            else:
+            elif rows <= QuantLinear.GEMM_ROWS:
                 mm8_gemm_multi_into(list(xs), [l.m for l in lins], list(outs))
+            else:
+                mm8_gemm_prefill_multi_into(list(xs), [l.m for l in lins], list(outs))
             return outs
         for l, x2, o in zip(lins, xs, outs):
             l.apply(x2, o)

@@ -144,7 +144,7 @@ def _check_out(x2, m, out, residual):
 
 
 # Blocked-weight routes by row count: the fused GEMV up to GEMV_ROWS rows, the
-# 64-row MFMA tile GEMM up to GEMM_ROWS.
+# 64-row MFMA tile GEMM up to GEMM_ROWS, the 256 x 256 prefill GEMM above.
 GEMV_ROWS = 16
 GEMM_ROWS = 256
 
@@ -168,13 +168,13 @@ def mm8_matmul_into(x2, w_u8, mx, rx, my, ry, out, *, bias=None, residual=None, 
         if tuple(w_u8.shape[:2]) != ((m + 15) // 16, (n + 127) // 128) or int(ry.numel()) != n:
             raise ValueError(f"mm8: blocked weights {tuple(w_u8.shape)} do not match [{n}, {m}]")
         residual = _check_out(x2, m, out, residual)
-        if GEMV_ROWS < rows <= GEMM_ROWS:
-            mod = types.SimpleNamespace(w_blk=w_u8, mx=mx, rx=rx, my=my, ry=ry, bias=bias, in_features=n,
-                                        out_features=m)
-            mm8_gemm_multi_into([x2], [mod], [out], residuals=[residual], epilogues=[epilogue])
-            return out
         mod = types.SimpleNamespace(w_blk=w_u8, mx=mx, rx=rx, my=my, ry=ry, bias=bias, in_features=n, out_features=m)
-        mm8_matmul_multi_into([x2], [mod], [out], residuals=[residual], epilogues=[epilogue])
+        if rows > GEMM_ROWS:
+            mm8_gemm_prefill_multi_into([x2], [mod], [out], residuals=[residual], epilogues=[epilogue])
+        elif rows > GEMV_ROWS:
+            mm8_gemm_multi_into([x2], [mod], [out], residuals=[residual], epilogues=[epilogue])
+        else:
+            mm8_matmul_multi_into([x2], [mod], [out], residuals=[residual], epilogues=[epilogue])
         return out
     m = int(w_u8.shape[1])
     if int(w_u8.shape[0]) != n:
@@ -262,6 +262,59 @@ def mm8_gemm_multi_into(xs, mods, outs, *, residuals=None, epilogues=None, split
         _lib.dtype_code(mods[0].mx), int(splits), _lib.ptr(ws), int(ws.numel()),
         _lib.stream_of(xs[0]),
     )
+    return outs
+
+
+# x's buffer descriptor in the prefill GEMM spans rows * in_features * 2 bytes,
+# below 2^31: longer inputs are split into row chunks
+_PREFILL_MAX_BYTES = (1 << 31) - 1
+
+
+def mm8_gemm_prefill_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
+    """Prefill form (more than ``GEMM_ROWS`` rows) of :func:`mm8_matmul_multi_into`:
+    up to four blocked ``MM8Linear`` products of one shape on the 256 x 256
+    MFMA GEMM that dequantises the MM8 bytes in registers, the route
+    ``mm8_matmul_triton`` takes by materialising the dequantised weight for
+    rows above ``fused_max_rows`` (rwkv7_hf/native_quant_mm8.py:468-507) and
+    the prefill projections of rwkv7_hf/native_jit_prefill.py:542-631,
+    955-1013.  fp16 activations with fp16 metadata; other dtypes run the
+    64-row tile GEMM over 256-row chunks (also without a dequantised weight).
+    No workspace."""
+    k = len(mods)
+    if not 1 <= k <= 4 or len(xs) != k or len(outs) != k:
+        raise ValueError("mm8_gemm_prefill_multi_into: 1..4 problems")
+    rows, n = (int(s) for s in xs[0].shape)
+    m = int(mods[0].out_features)
+    residuals = list(residuals) if residuals is not None else [None] * k
+    epilogues = list(epilogues) if epilogues is not None else [_lib.EPI_NONE] * k
+    for x2, mod, out, r in zip(xs, mods, outs, residuals):
+        if tuple(x2.shape) != (rows, n) or not x2.is_contiguous() or x2.dtype != xs[0].dtype:
+            raise ValueError("mm8_gemm_prefill_multi_into: inputs must share one contiguous shape and dtype")
+        if mod.in_features != n or mod.out_features != m or not is_blocked(mod.w_blk):
+            raise ValueError("mm8_gemm_prefill_multi_into: modules must be blocked MM8Linear of one shape")
+        _check_out(x2, m, out, r)
+    _lib.require_gpu(*xs, *outs, name="mm8_gemm_prefill_multi")
+    fast = xs[0].dtype == torch.float16 and all(md.mx.dtype == torch.float16 for md in mods)
+    chunk = max(1, _PREFILL_MAX_BYTES // (2 * n)) if fast else GEMM_ROWS
+    eps = (ctypes.c_int * k)(*[int(e) for e in epilogues])
+    arr = lambda ts: _lib.ptr_array(ts)
+    for r0 in range(0, rows, chunk):
+        r1 = min(rows, r0 + chunk)
+        xc = [x[r0:r1] for x in xs]
+        oc = [o[r0:r1] for o in outs]
+        rc = [None if r is None else r.reshape(rows, m)[r0:r1] for r in residuals]
+        if not fast:
+            if r1 - r0 > GEMV_ROWS:
+                mm8_gemm_multi_into(xc, mods, oc, residuals=rc, epilogues=epilogues)
+            else:
+                mm8_matmul_multi_into(xc, mods, oc, residuals=rc, epilogues=epilogues)
+            continue
+        _lib.call(
+            "rwkv7mi_mm8t_gemm_prefill", k, arr(xc), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
+            arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),
+            arr([md.bias for md in mods]), arr(rc), arr(oc), eps, r1 - r0, n, m, _lib.F16, _lib.F16,
+            _lib.stream_of(xs[0]),
+        )
     return outs
 
 
@@ -552,7 +605,7 @@ def invalidate_model_caches(model) -> None:
         runners.clear()
 
 
-__all__ = [
+__all__ = ["mm8_gemm_prefill_multi_into", 
     "quantize_mm8", "dequantize_mm8", "quantize_mm8_outmajor", "quantize_mm8_blocked", "mm8_block", "mm8_unblock", "is_blocked",
     "is_out_major", "mm8_matmul", "mm8_linear", "mm8_matmul_into",
     "mm8_matmul_multi_into", "mm8_gemm_multi_into", "mm8_gemm_workspace_bytes", "mm8_gemv_triton",

@@ -282,6 +282,24 @@ int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x,
                             int splits, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* Prefill GEMM over the blocked layout for many rows (long prompts): up to
+ * four problems of one shape, y = epilogue(x @ W_hat (+ bias)), on 256 x 256
+ * MFMA tiles that dequantise the MM8 bytes in registers -- the weight is
+ * never materialised -- with the per-row sums taken by the same MFMAs.  fp16
+ * activations and fp16 metadata; rows * I * 2 < 2^31 (callers split longer
+ * inputs); no workspace.  Replaces the materialising route of
+ * mm8_matmul_triton for rows > fused_max_rows
+ * (rwkv7_hf/native_quant_mm8.py:468-507, :100-126) used by the prefill
+ * projections (rwkv7_hf/native_jit_prefill.py:542-631, 955-1013). */
+int rwkv7mi_mm8t_gemm_prefill(int nprob, const void* const* x,
+                              const uint8_t* const* w_blk, const void* const* mx,
+                              const void* const* rx, const void* const* my,
+                              const void* const* ry, const void* const* bias,
+                              const void* const* residual, void* const* y,
+                              const int* epilogue, int64_t rows, int64_t I,
+                              int64_t O, int act_dtype, int meta_dtype,
+                              void* stream);
+
 /* Allocation-free form of rwkv7mi_mm8t_gemm_multi (same arguments and results,
  * no workspace argument).  No counterpart in the reference: it is for callers
  * that cannot allocate (code under hipGraph capture, tight serving loops,

@@ -146,8 +146,12 @@ def test_mm8g_dtypes(oracle, act, meta):
     y = torch.empty(rows, O, device="cuda", dtype=act)
     mm8_gemm_multi_into([x], [mod], [y])
     torch.cuda.synchronize()
-    tol = 2e-3 if act != torch.bfloat16 else 8e-3
-    assert _rel_err(_np(y.float()).astype(np.float64), _ref(oracle, x, mod)) <= tol
+    # fp32 activations stage x' as fp16 hi + lo (as the <= 16-row GEMV does):
+    # ~1e-6 typical, up to a few 1e-5 on rows whose lo parts sit just below
+    # the fp16 normal range (measured); fp16-rounded x' alone would be ~2e-4
+    tol = {torch.float16: 2e-3, torch.float32: 1e-4, torch.bfloat16: 8e-3}[act]
+    err = _rel_err(_np(y.float()).astype(np.float64), _ref(oracle, x, mod))
+    assert err <= tol, (act, meta, err)
 
 
 def test_mm8g_rkv_7p2b_bsz64(oracle):
@@ -175,9 +179,9 @@ def test_mm8g_workspace_contract():
     I, O, rows = 2048, 256, 32
     mod = _packed(rng, I, O)
     need = mm8_gemm_workspace_bytes(1, rows, I, O, 4)
-    assert need >= 4 * rows * O * 4 + rows * I * 2  # partials and x'
+    assert need >= 4 * rows * O * 4 + 2 * rows * I * 2  # partials and x' (hi and lo halves)
     one = mm8_gemm_workspace_bytes(1, rows, 1024, O, 1)  # x' and row sums only
-    assert rows * 1024 * 2 < one <= rows * 1024 * 2 + 1024
+    assert 2 * rows * 1024 * 2 < one <= 2 * rows * 1024 * 2 + 1024
     x = _cuda(rng.standard_normal((rows, I)), torch.float16)
     y = torch.empty(rows, O, device="cuda", dtype=torch.float16)
     ws = torch.empty(need - 256, device="cuda", dtype=torch.uint8)

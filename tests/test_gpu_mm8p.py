@@ -1,0 +1,138 @@
+"""GPU parity of the prefill MM8 GEMM (more than 256 rows over blocked
+weights, the weight never materialised): against the fp64 oracle on the
+dequantised weights for ragged rows / columns and in_features that end
+mid-tile, grouped launches, bias / relu^2 / residual epilogues, the
+non-fp16 chunked route, and the module routes that take it."""
+from __future__ import annotations
+
+import types
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _cuda(x, dtype):
+    return torch.tensor(np.asarray(x), dtype=dtype, device="cuda")
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _rel_err(got, ref):
+    return np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+
+
+def _packed(rng, I, O, dtype=torch.float16, bias=False):
+    from rwkv7mi.native_quant_mm8 import quantize_mm8_blocked
+
+    Wl = _cuda(rng.standard_normal((O, I)) * 0.02, dtype)
+    w_blk, mx, rx, my, ry = quantize_mm8_blocked(Wl)
+    b = _cuda(rng.standard_normal(O) * 0.1, dtype) if bias else None
+    return types.SimpleNamespace(w_blk=w_blk, mx=mx, rx=rx, my=my.reshape(-1), ry=ry.reshape(-1), bias=b,
+                                 in_features=I, out_features=O)
+
+
+def _ref(oracle, x, mod):
+    from rwkv7mi.native_quant_mm8 import mm8_unblock
+
+    w_u8 = mm8_unblock(mod.w_blk, mod.in_features, mod.out_features)
+    meta = [_np(t.float()) for t in (mod.mx, mod.rx, mod.my, mod.ry)]
+    y = oracle.mm8_matmul(_np(x.float()).astype(np.float64), _np(w_u8), *meta)
+    if mod.bias is not None:
+        y = y + _np(mod.bias.float()).astype(np.float64)
+    return y
+
+
+# fp16 output rounding (2^-11) plus the fp16 rounding of (w - 128) ry in the
+# B operand (the same rounding the reference's materialised fp16 weight has)
+TOL = 3e-3
+
+
+@pytest.mark.parametrize("IO", [(4096, 4096), (1024, 300), (144, 40), (2064, 520), (16384, 256), (80, 16)])
+@pytest.mark.parametrize("rows", [257, 600, 1024])
+def test_mm8p_matches_oracle(oracle, IO, rows):
+    from rwkv7mi.native_quant_mm8 import mm8_gemm_prefill_multi_into
+
+    I, O = IO
+    rng = np.random.default_rng(I + O + rows)
+    mod = _packed(rng, I, O)
+    x = _cuda(rng.standard_normal((rows, I)), torch.float16)
+    y = torch.full((rows, O), float("nan"), device="cuda", dtype=torch.float16)
+    print(f"mm8p: I={I} O={O} rows={rows}", flush=True)
+    mm8_gemm_prefill_multi_into([x], [mod], [y])
+    torch.cuda.synchronize()
+    err = _rel_err(_np(y).astype(np.float64), _ref(oracle, x, mod))
+    assert err <= TOL, (IO, rows, err)
+
+
+def test_mm8p_multi_and_epilogues(oracle):
+    from rwkv7mi import _lib
+    from rwkv7mi.native_quant_mm8 import mm8_gemm_prefill_multi_into
+
+    I, O, rows = 1024, 784, 700
+    rng = np.random.default_rng(7)
+    mods = [_packed(rng, I, O, bias=True) for _ in range(3)]
+    xs = [_cuda(rng.standard_normal((rows, I)), torch.float16) for _ in range(3)]
+    outs = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(3)]
+    res = _cuda(rng.standard_normal((rows, O)), torch.float16)
+    want_res = _np(res).astype(np.float64)
+    print("mm8p: three problems, none / relu^2 / residual in place", flush=True)
+    mm8_gemm_prefill_multi_into(xs, mods, [outs[0], outs[1], res], residuals=[None, None, res],
+                                epilogues=[_lib.EPI_NONE, _lib.EPI_RELU2, _lib.EPI_RESIDUAL])
+    torch.cuda.synchronize()
+    base = [_ref(oracle, x, m) for x, m in zip(xs, mods)]
+    assert _rel_err(_np(outs[0]).astype(np.float64), base[0]) <= TOL
+    rr = np.maximum(base[1], 0) ** 2
+    assert np.abs(_np(outs[1]) - rr).max() <= 2 * TOL * np.abs(rr).max()
+    add = base[2] + want_res
+    assert np.abs(_np(res) - add).max() <= TOL * np.abs(add).max()
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+def test_mm8p_other_dtypes_take_tile_chunks(oracle, act):
+    """Non-fp16 activations run the 64-row tile GEMM over 256-row chunks."""
+    from rwkv7mi.native_quant_mm8 import mm8_gemm_prefill_multi_into
+
+    I, O, rows = 1024, 256, 600
+    rng = np.random.default_rng(9)
+    mod = _packed(rng, I, O, dtype=act)
+    x = _cuda(rng.standard_normal((rows, I)), act)
+    y = torch.empty(rows, O, device="cuda", dtype=act)
+    mm8_gemm_prefill_multi_into([x], [mod], [y])
+    torch.cuda.synchronize()
+    tol = 1e-4 if act == torch.float32 else 8e-3
+    assert _rel_err(_np(y.float()).astype(np.float64), _ref(oracle, x, mod)) <= tol
+
+
+def test_mm8p_module_routes(oracle):
+    """MM8Linear.forward / the functional mm8_matmul and the model's
+    QuantLinear take the prefill GEMM above 256 rows, identical results."""
+    from rwkv7mi.model import QuantLinear
+    from rwkv7mi.native_quant_mm8 import MM8Linear
+
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(512, 384, bias=True).cuda().half()
+    m = MM8Linear(lin)
+    x = torch.randn(3, 200, 512, device="cuda", dtype=torch.float16)
+    y = m(x)
+    q = QuantLinear(m)
+    y2 = torch.empty(600, 384, device="cuda", dtype=torch.float16)
+    q.apply(x.reshape(600, 512), y2)
+    torch.cuda.synchronize()
+    assert torch.equal(y.reshape(600, 384), y2)
+    mod = types.SimpleNamespace(w_blk=m.w_blk, mx=m.mx, rx=m.rx, my=m.my.reshape(-1), ry=m.ry.reshape(-1),
+                                bias=m.bias, in_features=512, out_features=384)
+    err = _rel_err(_np(y.reshape(600, 384)).astype(np.float64), _ref(oracle, x.reshape(600, 512), mod))
+    assert err <= TOL
+
+
+def test_mm8p_rejects():
+    from rwkv7mi import _lib
+
+    with pytest.raises(ValueError):
+        _lib.call("rwkv7mi_mm8t_gemm_prefill", 0, None, None, None, None, None, None, None, None, None, None,
+                  300, 128, 16, _lib.F16, _lib.F16, None)

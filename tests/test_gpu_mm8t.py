@@ -121,8 +121,9 @@ def test_mm8t_dtypes(oracle, act, meta):
     torch.cuda.synchronize()
     ref = oracle.mm8_matmul(_np(x.float()).astype(np.float64), *(_np(p.float()) if p.is_floating_point() else _np(p)
                                                                    for p in packed))
-    tol = 2e-3 if act != torch.bfloat16 else 8e-3
-    assert _rel_err(_np(y.float()).astype(np.float64), ref) <= tol
+    tol = 1e-4 if act == torch.float32 else 8e-3  # x' staged as fp16 hi + lo (fp16 alone: ~2e-4)
+    err = _rel_err(_np(y.float()).astype(np.float64), ref)
+    assert err <= tol, (act, meta, err)
 
 
 def test_mm8t_epilogues_in_place_and_module(oracle):

@@ -186,3 +186,69 @@ def test_w4_head_shape_c4(oracle, rows):
     torch.cuda.synchronize()
     refa = oracle.w4a_linear(_np(x).astype(np.float64), _np(pa), _np(sa), _np(ba))
     assert _rel_err(_np(ya).astype(np.float64), refa) <= 2e-3
+
+
+@pytest.mark.parametrize("case", [
+    # (O, I, group, rows, act dtype, affine)
+    (200, 384, 128, 1, torch.float16, False),     # ragged columns, I not a multiple of 256
+    (200, 384, 128, 7, torch.float16, True),
+    (1040, 2048, 256, 2, torch.float16, False),   # group 256
+    (1040, 2048, 256, 16, torch.bfloat16, True),  # bf16 activations (hi + lo staging)
+    (520, 1536, 128, 5, torch.float32, True),     # fp32 activations
+    (4096, 16384, 128, 16, torch.float16, True),  # x re-staged per chunk (too big for LDS at once)
+    (48, 16384, 256, 3, torch.bfloat16, False),   # three column groups, bf16 x in four chunks
+])
+def test_w4_stream_gemv_edges(oracle, case):
+    """The streaming <= 16-row W4 GEMV on its edge shapes: ragged column
+    groups, a half step at the end of K, group 256, every activation dtype,
+    the chunked x staging, both the symmetric and the affine form."""
+    from rwkv7mi import quantize_w4_groupwise, w4_groupwise_linear
+    from rwkv7mi.sm70_quant import quantize_w4_affine_groupwise, w4_affine_groupwise_linear
+
+    O, I, group, rows, act, aff = case
+    rng = np.random.default_rng(O + I + rows + group)
+    W = _cuda(rng.standard_normal((O, I)) * 0.02, torch.float16)
+    x = _cuda(rng.standard_normal((rows, I)), act)
+    if aff:
+        q, s, b, _ = quantize_w4_affine_groupwise(W, group_size=group)
+        y = w4_affine_groupwise_linear(x, q, s, b, O, I, group_size=group)
+        ref = oracle.w4a_linear(_np(x.float()).astype(np.float64), _np(q), _np(s), _np(b), group)
+    else:
+        q, s, _ = quantize_w4_groupwise(W, group_size=group)
+        y = w4_groupwise_linear(x, q, s, O, I, group_size=group)
+        ref = oracle.w4g_linear(_np(x.float()).astype(np.float64), _np(q), _np(s), group)
+    torch.cuda.synchronize()
+    # fp16 / fp32: exact products, fp32 sums (the tolerance is the output
+    # rounding); bf16 outputs round to 8 bits
+    tol = {torch.float16: 2e-3, torch.float32: 1e-4, torch.bfloat16: 8e-3}[act]
+    err = _rel_err(_np(y.float()).astype(np.float64), ref)
+    assert err <= tol, (case, err)
+
+
+@pytest.mark.parametrize("rows", [1, 6])
+def test_w4_stream_gemv_epilogues(oracle, rows):
+    """Bias, residual (in place: out aliases the residual) and relu^2 epilogues
+    of the symmetric W4 GEMV against the oracle."""
+    from rwkv7mi import _lib
+    from rwkv7mi import quantize_w4_groupwise
+    from rwkv7mi.sm70_quant import w4_groupwise_linear_into
+
+    O, I = 784, 1024
+    rng = np.random.default_rng(rows)
+    W = _cuda(rng.standard_normal((O, I)) * 0.02, torch.float16)
+    q, s, _ = quantize_w4_groupwise(W)
+    x = _cuda(rng.standard_normal((rows, I)), torch.float16)
+    bias = _cuda(rng.standard_normal(O) * 0.1, torch.float16)
+    base = oracle.w4g_linear(_np(x).astype(np.float64), _np(q), _np(s)) + _np(bias).astype(np.float64)
+    y = torch.empty(rows, O, device="cuda", dtype=torch.float16)
+    w4_groupwise_linear_into(x, q, s, y, bias=bias)
+    r2 = torch.empty_like(y)
+    w4_groupwise_linear_into(x, q, s, r2, bias=bias, epilogue=_lib.EPI_RELU2)
+    res = _cuda(rng.standard_normal((rows, O)), torch.float16)
+    want_res = base + _np(res).astype(np.float64)
+    w4_groupwise_linear_into(x, q, s, res, bias=bias, residual=res, epilogue=_lib.EPI_RESIDUAL)
+    torch.cuda.synchronize()
+    assert np.abs(_np(y) - base).max() <= 2e-3 * np.abs(base).max()
+    rr = np.maximum(base, 0) ** 2
+    assert np.abs(_np(r2) - rr).max() <= 4e-3 * np.abs(rr).max()
+    assert np.abs(_np(res) - want_res).max() <= 2e-3 * np.abs(want_res).max()
