@@ -13,16 +13,25 @@
 // extra output columns (ry, my, 1), exact products with fp32 sums.
 //
 // Tile: a 512-lane workgroup computes 256 rows x 256 columns (16 column
-// groups of the blocked layout).  Eight waves in a 2 x 4 grid each own
-// 128 rows x 64 columns (8 x 4 MFMA tiles of v_mfma_f32_16x16x32_f16).  K
-// advances 64 inputs per step (one 1 KB half of each 2 KB blocked tile):
-//  * x rows go global -> registers -> LDS (double-buffered, one barrier per
-//    step; the next step's loads are in flight during this step's MFMAs);
-//  * each wave loads its own B bytes (16 bytes per lane and column group:
-//    one lane's 16 bytes are the B operands of two consecutive MFMAs) one
-//    step ahead, into registers;
-//  * ry and my of the step's inputs sit in LDS with the x tile.
-// Wave (wm, wn) also computes the extra columns for its M tiles 2wn, 2wn+1.
+// groups of the blocked layout).  Eight waves (two per SIMD) in a 2 x 4 grid
+// each own 128 rows x 64 columns: 8 x 4 MFMA tiles of
+// v_mfma_f32_16x16x32_f16 (128 fp32 accumulators per lane; 128 x 128 wave
+// tiles would need 256 and spill).  K advances 64 inputs per step (one 1 KB
+// half of each 2 KB blocked tile):
+//  * every operand of a step goes global -> LDS directly (buffer loads with
+//    the lds flag, no registers) into one of three stages, two steps ahead
+//    of the MFMAs, with one barrier per step;
+//  * x rows: a row is 128 bytes whose 16-byte chunk c sits at position
+//    c ^ (row % 8), so the 8 lanes of an MFMA A read phase hit 8 different
+//    chunk positions (all 32 banks once);
+//  * the MM8 bytes: the step's 1 KB half of each of the tile's 16 column
+//    groups, as stored (a lane's 16 bytes are the B operands of two
+//    consecutive MFMAs), loaded once per workgroup for both row halves;
+//  * ry and my of the step's inputs, followed by 64 ones and 64 zeros, so
+//    the extra columns' B operand is one LDS read per lane (column 0 reads
+//    ry, 1 my, 2 ones, the rest zeros).
+// Wave (wm, wn) also computes the extra columns for its M tiles 2wn, 2wn+1
+// (their A operands read again from LDS: no per-tile branch in the loop).
 // The tile order is XCD-aware: a workgroup's linear id L runs on XCD L % 8,
 // so tiles are numbered to give each XCD contiguous groups of 4 row tiles x
 // 8 column tiles (their x rows and weight columns stay in that XCD's L2).
@@ -33,10 +42,13 @@
 namespace rwkv7mi {
 
 constexpr int MM8P_M = 256, MM8P_N = 256, MM8P_KS = 64;
-constexpr int MM8P_XS = MM8P_KS + 8;                    // LDS row stride (halfs)
-constexpr int MM8P_ABYTES = MM8P_M * MM8P_XS * 2;       // one x buffer
-constexpr int MM8P_VBYTES = 2 * MM8P_KS * 2;            // ry, my of one step (fp16)
-constexpr int MM8P_LDS = 2 * (MM8P_ABYTES + MM8P_VBYTES);
+constexpr int MM8P_XS = MM8P_KS;                        // LDS row (halfs): 128 bytes, 16-byte chunks XOR-swizzled
+constexpr int MM8P_ABYTES = MM8P_M * MM8P_XS * 2;       // x rows of one step (32 KB)
+constexpr int MM8P_BBYTES = 16 * 1024;                  // MM8 bytes of one step: 16 column groups x 1 KB
+constexpr int MM8P_VBYTES = 4 * MM8P_KS * 2;            // ry, my of one step, then ones, zeros (fp16)
+constexpr int MM8P_STAGE = MM8P_ABYTES + MM8P_BBYTES + MM8P_VBYTES;
+constexpr int MM8P_NST = 3;                             // pipeline stages (two steps of loads in flight)
+constexpr int MM8P_LDS = MM8P_NST * MM8P_STAGE;
 
 struct Mm8pBatch {
   Mm8tProb p[MM8T_MAXPROB];
@@ -82,8 +94,6 @@ __global__ __launch_bounds__(512, 1) void mm8p_kernel(const Mm8pBatch B) {
   const int lane = tid & 63;
   const int n = lane & 15, kg = lane >> 4;
   const int wm = wave >> 2, wn = wave & 3;
-  auto xs = [&](int b) { return reinterpret_cast<_Float16*>(smem + b * (MM8P_ABYTES + MM8P_VBYTES)); };
-  auto vs = [&](int b) { return reinterpret_cast<_Float16*>(smem + b * (MM8P_ABYTES + MM8P_VBYTES) + MM8P_ABYTES); };
 
   // ---- global sources (raw buffer loads; out-of-range offsets read zeros)
   const __amdgpu_buffer_rsrc_t xr = mm8t_rsrc(P.x, (uint32_t)((int64_t)M * I * 2));
@@ -91,46 +101,56 @@ __global__ __launch_bounds__(512, 1) void mm8p_kernel(const Mm8pBatch B) {
   const __amdgpu_buffer_rsrc_t myr = mm8t_rsrc(P.my, (uint32_t)(I * 2));
   const int ngroups = (O + MM8T_COLS - 1) / MM8T_COLS;
   const uint32_t gbytes = (uint32_t)B.KB * 2048u;
-  __amdgpu_buffer_rsrc_t wr[4];
+  __amdgpu_buffer_rsrc_t wdma[2];  // the two column groups this wave loads for the workgroup
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int g = n0 / MM8T_COLS + 4 * wn + q;
-    wr[q] = mm8t_rsrc(P.w + (int64_t)(g < ngroups ? g : 0) * gbytes, g < ngroups ? gbytes : 0u);
+  for (int q = 0; q < 2; ++q) {
+    const int g = n0 / MM8T_COLS + 2 * wave + q;
+    wdma[q] = mm8t_rsrc(P.w + (int64_t)(g < ngroups ? g : 0) * gbytes, g < ngroups ? gbytes : 0u);
   }
   const int nsteps = (I + MM8P_KS - 1) / MM8P_KS;
+  auto xs = [&](int st) { return reinterpret_cast<_Float16*>(smem + st * MM8P_STAGE); };
+  auto bs = [&](int st) { return reinterpret_cast<const u32x4*>(smem + st * MM8P_STAGE + MM8P_ABYTES); };
+  auto vs = [&](int st) { return reinterpret_cast<_Float16*>(smem + st * MM8P_STAGE + MM8P_ABYTES + MM8P_BBYTES); };
+  typedef __attribute__((address_space(3))) void* lds_ptr;
 
-  // x staging: 256 rows x 64 inputs = 2048 runs of 16 bytes, four per thread
-  u32x4 xa[4];
-  auto x_issue = [&](int s) {
+  // loads of step s into stage s % 3 (the LDS writes complete with vmcnt):
+  //  * x: wave w, round u writes rows 64 u + 8 w .. +7 (1 KB; lane l lands
+  //    at row + l / 8, chunk position l % 8, so it fetches input chunk
+  //    (l % 8) ^ (l / 8) of that row); rows past M, inputs past I read zeros;
+  //  * B: wave w loads column groups 2w, 2w + 1 (1 KB each);
+  //  * ry (lanes 0..7) and my (lanes 8..15): wave 0.
+  // Per wave and step: 6 loads, 8 on wave 0.
+  auto issue = [&](int s) {
+    const int st = s % MM8P_NST;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int c = tid + 512 * u;
-      const int r = c >> 3, k = s * MM8P_KS + 8 * (c & 7);
+      const int r0 = 64 * u + 8 * wave;
+      const int r = r0 + (lane >> 3);
+      const int k = s * MM8P_KS + 8 * ((lane & 7) ^ (lane >> 3));
       const bool ok = m0 + r < M && k < I;
-      xa[u] = mm8t_ld16(xr, ok ? (uint32_t)(((int64_t)(m0 + r) * I + k) * 2) : MM8T_OOB);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(xs(st) + r0 * MM8P_XS), 16,
+                                               ok ? (int)(((int64_t)(m0 + r) * I + k) * 2) : (int)MM8T_OOB, 0, 0, 0);
     }
-  };
-  u32x4 va;  // threads 0..7: ry, 8..15: my (16 bytes each)
-  auto v_issue = [&](int s) {
-    if (tid < 16) {
-      const int k = s * MM8P_KS + 8 * (tid & 7);
-      va = mm8t_ld16(tid < 8 ? ryr : myr, k < I ? (uint32_t)(k * 2) : MM8T_OOB);
-    }
-  };
-  auto x_store = [&](int b) {
+    const int boff = s < nsteps ? (s >> 1) * 2048 + (s & 1) * 1024 + 16 * lane : (int)MM8T_OOB;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = tid + 512 * u;
-      *reinterpret_cast<u32x4*>(xs(b) + (c >> 3) * MM8P_XS + 8 * (c & 7)) = xa[u];
+    for (int q = 0; q < 2; ++q)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wdma[q], (lds_ptr)(bs(st) + 64 * (2 * wave + q)), 16, boff, 0, 0, 0);
+    if (wave == 0 && lane < 16) {
+      const int k = s * MM8P_KS + 8 * (lane & 7);
+      const int off = k < I ? k * 2 : (int)MM8T_OOB;
+      if (lane < 8)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ryr, (lds_ptr)vs(st), 16, off, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(myr, (lds_ptr)vs(st), 16, off, 0, 0, 0);
     }
-    if (tid < 16) *reinterpret_cast<u32x4*>(vs(b) + 8 * tid) = va;
   };
-  // this wave's B bytes of step s: column group q, lane's 16 bytes of half s%2 of tile s/2
-  u32x4 bq[2][4];
-  auto b_issue = [&](int s, u32x4 (&b)[4]) {
-    const uint32_t off = (uint32_t)(s >> 1) * 2048u + (uint32_t)(s & 1) * 1024u + 16u * (uint32_t)lane;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) b[q] = mm8t_ld16(wr[q], s < nsteps ? off : MM8T_OOB);
+  // wait until only the newest step's loads may be pending (s_waitcnt
+  // vmcnt(6) / vmcnt(8), no expcnt / lgkmcnt wait)
+  auto wait_one_step = [&]() {
+    if (wave == 0)
+      __builtin_amdgcn_s_waitcnt(0x0F78);
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F76);
   };
 
   f32x4 acc[8][4];
@@ -140,71 +160,69 @@ __global__ __launch_bounds__(512, 1) void mm8p_kernel(const Mm8pBatch B) {
     for (int q = 0; q < 4; ++q) acc[i][q] = (f32x4){0.f, 0.f, 0.f, 0.f};
   f32x4 ex[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
 
-  // prologue: step 0 into LDS buffer 0, step 1's loads in flight
-  x_issue(0);
-  v_issue(0);
-  b_issue(0, bq[0]);
-  x_store(0);
-  x_issue(1);
-  v_issue(1);
-  b_issue(1, bq[1]);
+  // constant tails of the v part of every stage: 64 ones, 64 zeros
+  if (tid < 16 * MM8P_NST) {  // stage tid / 16, 8-half run j = tid % 16 (runs 0..7 ones, 8..15 zeros)
+    const int j = tid & 15;
+    const _Float16 c = j < 8 ? (_Float16)1.0f : (_Float16)0.0f;
+    const f16x8 c8 = (f16x8){c, c, c, c, c, c, c, c};
+    *reinterpret_cast<f16x8*>(vs(tid >> 4) + 2 * MM8P_KS + 8 * j) = c8;
+  }
+  // prologue: steps 0 and 1 in flight, step 0 landed before the first barrier
+  issue(0);
+  issue(1);
+  wait_one_step();
   __syncthreads();
 
-  const _Float16 one = (_Float16)1.0f;
-  auto step = [&](int s, int b, u32x4 (&bc)[4]) {
-    const _Float16* xb = xs(b);
-    const _Float16* vb = vs(b);
+  const int xsel = 64 * (n < 3 ? n : 3);  // this lane's extra column: ry, my, ones or zeros
+  for (int s = 0; s < nsteps; ++s) {
+    issue(s + 2);  // into the stage step s - 1 used (every wave is past it: the last barrier)
+    const int st = s % MM8P_NST;
+    const _Float16* xb = xs(st);
+    const _Float16* vb = vs(st);
+    u32x4 braw[4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {  // two MFMA K sub-steps of 32 inputs
-      // the lane's 8 inputs: 16 kg + 8 h .. +7 of the step
-      const int kk = 16 * kg + 8 * h;
-      const f16x8 ry8 = *reinterpret_cast<const f16x8*>(vb + kk);
-      f16x8 bv[4];
+    for (int q = 0; q < 4; ++q) braw[q] = bs(st)[64 * (4 * wn + q) + lane];
+    // B operands of sub-step h (the lane's 8 inputs 16 kg + 8 h .. +7 of the
+    // step); sub-step 1's are converted while sub-step 0's MFMAs run
+    auto convert = [&](int h, f16x8 (&bv)[4]) {
+      const f16x8 ry8 = *reinterpret_cast<const f16x8*>(vb + 16 * kg + 8 * h);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) bv[q] = mm8p_b_operand(bc[q][2 * h], bc[q][2 * h + 1], ry8);
-      f16x8 bx;  // extra columns: 0 = ry, 1 = my, 2 = ones
-      {
-        const f16x8 my8 = *reinterpret_cast<const f16x8*>(vb + MM8P_KS + kk);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bx[e] = n == 0 ? ry8[e] : n == 1 ? my8[e] : n == 2 ? one : (_Float16)0.f;
-      }
+      for (int q = 0; q < 4; ++q) bv[q] = mm8p_b_operand(braw[q][2 * h], braw[q][2 * h + 1], ry8);
+    };
+    auto mfmas = [&](int h, const f16x8 (&bv)[4]) {
+      const int ka = 8 * ((2 * kg + h) ^ (n & 7));  // swizzled chunk of A row (... + n): row % 8 = n % 8
+      const f16x8 bx = *reinterpret_cast<const f16x8*>(vb + xsel + 16 * kg + 8 * h);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(xb + (128 * wm + 16 * i + n) * MM8P_XS + kk);
+        const f16x8 a = *reinterpret_cast<const f16x8*>(xb + (128 * wm + 16 * i + n) * MM8P_XS + ka);
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[i][q] = mfma16x16x32(a, bv[q], acc[i][q]);
-        if (i == 2 * wn) ex[0] = mfma16x16x32(a, bx, ex[0]);
-        if (i == 2 * wn + 1) ex[1] = mfma16x16x32(a, bx, ex[1]);
       }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const f16x8 a = *reinterpret_cast<const f16x8*>(xb + (128 * wm + 16 * (2 * wn + j) + n) * MM8P_XS + ka);
+        ex[j] = mfma16x16x32(a, bx, ex[j]);
+      }
+    };
+    f16x8 bv0[4], bv1[4];
+    convert(0, bv0);
+    mfmas(0, bv0);
+    convert(1, bv1);
+    // interleave: sub-step 1's conversions between sub-step 0's MFMA groups
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read (an A operand)
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // its MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU (conversions)
     }
-    (void)s;
-  };
-
-  // main loop, two steps per turn (the B ring slot is a compile-time index)
-  for (int s = 0; s < nsteps; s += 2) {
-    // step s from buffer 0 with bq[0]; step s+1 is in flight (x, v in xa/va, B in bq[1])
-    step(s, 0, bq[0]);
-    if (s + 2 < nsteps) b_issue(s + 2, bq[0]);
-    x_store(1);  // step s+1 (loaded during step s)
+    mfmas(1, bv1);
+    wait_one_step();  // step s + 1 has landed (step s + 2 may still be in flight)
     __syncthreads();
-    if (s + 2 < nsteps) {
-      x_issue(s + 2);
-      v_issue(s + 2);
-    }
-    if (s + 1 < nsteps) {
-      step(s + 1, 1, bq[1]);
-      if (s + 3 < nsteps) b_issue(s + 3, bq[1]);
-      x_store(0);  // step s+2
-      __syncthreads();
-      if (s + 3 < nsteps) {
-        x_issue(s + 3);
-        v_issue(s + 3);
-      }
-    }
   }
 
-  // ---- the extra columns -> LDS row sums (reusing x buffer 0)
+  // ---- the extra columns -> LDS row sums (reusing stage 0)
   float* rs = reinterpret_cast<float*>(smem);  // [256][3]: sum x ry, sum x my, sum x
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the trailing loads into LDS have landed
   __syncthreads();
   if (n < 3) {
 #pragma unroll
