@@ -19,6 +19,7 @@ namespace rwkv7mi {
 
 enum { LORA_ACT_NONE = 0, LORA_ACT_TANH = 1, LORA_ACT_SIGMOID = 2 };
 constexpr int LORA_MAXR = 256;   // largest rank
+constexpr int LORA_PREFILL_ROWS = 256;  // above: the fused many-row kernel (no workspace)
 
 struct LoraProb {
   const void* x;
@@ -228,6 +229,158 @@ __global__ __launch_bounds__(256) void lora_up_kernel(const LoraBatch B, int row
   }
 }
 
+// Many-row form (prefills): one launch, no workspace.  A workgroup owns
+// 64 MT rows of one problem; wave w owns rows 16 MT w .. + 16 MT - 1 (MT
+// MFMA row tiles, so every weight operand it loads feeds MT MFMAs) from start
+// to end:
+//  1. mid = act_down(x Wd^T) over the whole K, MFMA with the rank tiles as
+//     N (RT = ceil(r / 16) per row tile), x and Wd streamed from global with
+//     the next K step's loads issued before this step's MFMAs;
+//  2. mid rounded to the activation dtype (the reference's tensor) into the
+//     wave's own LDS rows (hi, and lo for fp32 / bf16);
+//  3. y = act_up(mid Wu^T + b) for every output tile of 16 columns, the up
+//     weights of the next tiles loaded ahead.
+// Waves never read each other's rows, so no workgroup barrier is needed.
+template <int RT, int MT, typename TA>
+__global__ __launch_bounds__(256) void lora_rows_kernel(const LoraBatch B, int rows) {
+  constexpr bool SPLIT = !std::is_same<TA, __half>::value;
+  constexpr int MS = 16 * RT + 8;  // LDS row stride of mid (halfs)
+  constexpr int WR = 16 * MT;      // rows per wave
+  extern __shared__ __align__(16) char lds[];
+  _Float16* mh = reinterpret_cast<_Float16*>(lds);  // [4][WR][MS]
+  _Float16* ml = mh + 4 * WR * MS;                   // (SPLIT) same shape
+  const LoraProb& P = B.p[blockIdx.y];
+  const int D = B.D, A = B.A, r = P.r;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n = lane & 15, kg = lane >> 4;
+  const int row0 = blockIdx.x * 4 * WR + WR * wave;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.x, (uint32_t)((int64_t)rows * D * sizeof(TA)));
+  const __amdgpu_buffer_rsrc_t dr = make_rsrc(P.wd, (uint32_t)((int64_t)r * D * sizeof(TA)));
+  const __amdgpu_buffer_rsrc_t ur = make_rsrc(P.wu, (uint32_t)((int64_t)A * r * sizeof(TA)));
+  _Float16* wmh = mh + wave * WR * MS;
+  _Float16* wml = ml + wave * WR * MS;
+
+  // ---- 1. down projection, K steps of 32 (lane: row n / rank n, inputs 8kg..)
+  f32x4 acc[MT][RT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[m][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  f16x8 ah[2][MT], al[2][MT], bh[2][RT], bl[2][RT];
+  auto load_k = [&](int k0, int sl) {
+    const int kk = k0 + 8 * kg;
+    const bool kok = kk < D;  // D % 8 == 0
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const int row = row0 + 16 * m + n;
+      lora_load8<TA>(xr, (uint32_t)(row * D + kk), kok && row < rows, ah[sl][m], al[sl][m]);
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+      lora_load8<TA>(dr, (uint32_t)((16 * t + n) * D + kk), kok && 16 * t + n < r, bh[sl][t], bl[sl][t]);
+  };
+  auto mfma_k = [&](int sl) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        acc[m][t] = mfma16x16x32(ah[sl][m], bh[sl][t], acc[m][t]);
+        if constexpr (SPLIT) {
+          acc[m][t] = mfma16x16x32(ah[sl][m], bl[sl][t], acc[m][t]);
+          acc[m][t] = mfma16x16x32(al[sl][m], bh[sl][t], acc[m][t]);
+        }
+      }
+  };
+  load_k(0, 0);
+  for (int k0 = 0; k0 < D; k0 += 64) {
+    load_k(k0 + 32, 1);
+    mfma_k(0);
+    load_k(k0 + 64, 0);
+    mfma_k(1);
+  }
+
+  // ---- 2. mid (lane holds rows 16m + 4kg + e of rank column 16t + n)
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = to_f32(from_f32<TA>(lora_act(acc[m][t][e], P.act_d)));
+        const _Float16 h = (_Float16)v;
+        const int idx = (16 * m + 4 * kg + e) * MS + 16 * t + n;
+        wmh[idx] = h;
+        if constexpr (SPLIT) wml[idx] = (_Float16)(v - (float)h);
+      }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's mid writes are done
+  __builtin_amdgcn_wave_barrier();
+
+  // ---- 3. up projection, output tiles of 16 columns, UT at a time
+  constexpr int KU = (16 * RT + 31) / 32;  // K steps of 32 over the rank
+  f16x8 mah[MT][KU], mal[MT][KU];
+  const f16x8 z8 = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int j = 0; j < KU; ++j) {
+      const int kk = 32 * j + 8 * kg;
+      const int idx = (16 * m + n) * MS + kk;
+      mah[m][j] = kk < r ? *reinterpret_cast<const f16x8*>(wmh + idx) : z8;
+      if constexpr (SPLIT) mal[m][j] = kk < r ? *reinterpret_cast<const f16x8*>(wml + idx) : z8;
+    }
+  TA* y = reinterpret_cast<TA*>(P.y);
+  const TA* bias = reinterpret_cast<const TA*>(P.bu);
+  const int ntiles = (A + 15) / 16;
+  constexpr int UT = 2;  // output tiles per turn
+  for (int ot0 = 0; ot0 < ntiles; ot0 += UT) {
+    f16x8 uh[UT][KU], ul[UT][KU];
+#pragma unroll
+    for (int u = 0; u < UT; ++u)
+#pragma unroll
+      for (int j = 0; j < KU; ++j) {
+        const int o = 16 * (ot0 + u) + n, kk = 32 * j + 8 * kg;
+        lora_load8<TA>(ur, (uint32_t)(o * r + kk), o < A && kk < r, uh[u][j], ul[u][j]);
+      }
+#pragma unroll
+    for (int u = 0; u < UT; ++u) {
+      const int o = 16 * (ot0 + u) + n;
+      const float bo = bias && o < A ? to_f32(bias[o]) : 0.f;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        f32x4 c = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < KU; ++j) {
+          c = mfma16x16x32(mah[m][j], uh[u][j], c);
+          if constexpr (SPLIT) {
+            c = mfma16x16x32(mah[m][j], ul[u][j], c);
+            c = mfma16x16x32(mal[m][j], uh[u][j], c);
+          }
+        }
+        if (o < A) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int row = row0 + 16 * m + 4 * kg + e;
+            if (row < rows) y[(int64_t)row * A + o] = from_f32<TA>(lora_act(c[e] + bo, P.act_u));
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int RT, int MT, typename TA>
+static int lora_rows_go(const LoraBatch& b, int64_t rows, void* stream) {
+  constexpr bool SPLIT = !std::is_same<TA, __half>::value;
+  constexpr int lds = 4 * 16 * MT * (16 * RT + 8) * 2 * (SPLIT ? 2 : 1);
+  static std::atomic<uint64_t> raised{0};
+  if (int rc = raise_dynamic_lds(reinterpret_cast<const void*>(&lora_rows_kernel<RT, MT, TA>), lds, raised,
+                                 "lora_rows_kernel"))
+    return rc;
+  const dim3 grid((unsigned)((rows + 64 * MT - 1) / (64 * MT)), (unsigned)b.nprob);
+  hipLaunchKernelGGL((lora_rows_kernel<RT, MT, TA>), grid, dim3(256), lds, as_stream(stream), b, (int)rows);
+  return check_launch("lora_rows_kernel");
+}
+
 }  // namespace rwkv7mi
 
 using namespace rwkv7mi;
@@ -277,7 +430,7 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
     tu += (int)((A + 15) / 16);
     off += (int64_t)ks * nr_max * ranks[i];
   }
-  if (!workspace || workspace_bytes < (size_t)off * sizeof(float))
+  if ((!up || rows <= LORA_PREFILL_ROWS) && (!workspace || workspace_bytes < (size_t)off * sizeof(float)))
     return fail(RWKV7MI_ESIZE, "lora_multi: workspace too small");
   batch.nprob = (int)nprob;
   batch.D = (int)D;
@@ -286,6 +439,24 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
   batch.kr = (int)((D + ks - 1) / ks);
   batch.kr = (batch.kr + 7) / 8 * 8;
   const size_t esz = act_dtype == RWKV7MI_F32 ? 4 : 2;
+  if (up && rows > LORA_PREFILL_ROWS) {
+    // many rows: the fused per-row-tile kernel, one launch, no partials
+    if (rows * std::max(D, A) * (int64_t)esz > INT32_MAX || A * LORA_MAXR * (int64_t)esz > INT32_MAX)
+      return fail(RWKV7MI_EINVAL, "lora_multi: too large");
+    int rmax = 0;
+    for (int i = 0; i < nprob; ++i) rmax = std::max(rmax, (int)ranks[i]);
+    const int rt = (rmax + 15) / 16;
+    return dispatch_dtype(act_dtype, [&](auto ta) {
+      using TA = decltype(ta);
+      // two row tiles per wave (each weight operand feeds two MFMAs); one for
+      // the largest ranks of the split (fp32 / bf16) form, which needs twice the registers
+      constexpr bool SPLIT = !std::is_same<TA, __half>::value;
+      if (rt <= 2) return lora_rows_go<2, 2, TA>(batch, rows, stream);
+      if (rt <= 4) return lora_rows_go<4, 2, TA>(batch, rows, stream);
+      if (rt <= 8) return lora_rows_go<8, SPLIT ? 1 : 2, TA>(batch, rows, stream);
+      return lora_rows_go<16, 1, TA>(batch, rows, stream);
+    });
+  }
   float* part = reinterpret_cast<float*>(workspace);
   for (int64_t r0 = 0; r0 < rows; r0 += LORA_ROWS) {
     const int64_t nr = rows - r0 > LORA_ROWS ? LORA_ROWS : rows - r0;

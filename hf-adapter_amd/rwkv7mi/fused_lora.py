@@ -41,15 +41,17 @@ def lora_workspace_bytes(ranks, rows: int, D: int) -> int:
 def lora_multi(xs, downs, ups, biases, outs, acts_down, acts_up):
     """Grouped LoRA: ``outs[i] = act_up(act_down(xs[i] @ downs[i].T) @ ups[i].T + biases[i])``.
 
-    Two launches for up to four projections (split-K down kernel, up kernel that
-    reduces the partials); the fp32 partials live in the per-device workspace.
+    Up to 256 rows: two launches for up to four projections (split-K down
+    kernel, up kernel that reduces the partials; the fp32 partials live in the
+    per-device workspace).  More rows (prefills): one launch of the fused
+    kernel, 64 rows per workgroup, no workspace.
     """
     k = len(xs)
     rows, D = (int(s) for s in xs[0].shape)
     A = int(ups[0].shape[0])
     ranks = [int(d.shape[0]) for d in downs]
     _lib.require_gpu(*xs, *downs, *ups, *outs, name="lora_multi")
-    ws = _ws.reserve(xs[0].device, lora_workspace_bytes(ranks, rows, D), slot="lora")
+    ws = _ws.reserve(xs[0].device, lora_workspace_bytes(ranks, min(rows, 32), D), slot="lora")
     _lib.call("rwkv7mi_lora_multi", k, _lib.ptr_array(xs), _lib.ptr_array(downs), _lib.ptr_array(ups),
               _lib.ptr_array(biases), _lib.ptr_array(outs), (ctypes.c_int64 * k)(*ranks),
               (ctypes.c_int * k)(*[int(a) for a in acts_down]), (ctypes.c_int * k)(*[int(a) for a in acts_up]),

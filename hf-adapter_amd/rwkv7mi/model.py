@@ -866,23 +866,12 @@ class NativeRWKV7ForCausalLM:
         yield self.lm_head
 
     def _lora(self, L, xw, xa, xg, xv, rows, outs, mids):
-        """W, A (sigmoid applied), G, V-gate projections on the LoRA HIP kernels."""
+        """W, A (sigmoid applied), G, V-gate projections on the LoRA HIP kernels
+        (split-K pair up to 256 rows, the fused many-row kernel above)."""
         n = len(L.lora_down)
         xin = [xw, xa, xg, xv][:n]
         acts_down = [ACT_TANH, ACT_NONE, ACT_SIGMOID, ACT_NONE][:n]
         acts_up = [ACT_NONE, ACT_SIGMOID, ACT_NONE, ACT_SIGMOID][:n]
-        if rows > 256:
-            for q in range(n):
-                h = xin[q] @ L.lora_down[q].t()
-                if acts_down[q] == ACT_TANH:
-                    h = torch.tanh(h)
-                elif acts_down[q] == ACT_SIGMOID:
-                    h = torch.sigmoid(h)
-                y = torch.nn.functional.linear(h, L.lora_up[q], L.lora_bias[q])
-                if acts_up[q] == ACT_SIGMOID:
-                    y = torch.sigmoid(y)
-                outs[q].copy_(y)
-            return
         lora_multi(xin, L.lora_down, L.lora_up, L.lora_bias, outs[:n], acts_down, acts_up)
 
     # ------------------------------------------------------------- decode

@@ -83,7 +83,8 @@ def test_sequence_shift_mix(oracle, B, T, D):
     _ok(last_f, ref_last)
 
 
-@pytest.mark.parametrize("rows,D", [(1, 4096), (8, 2048), (40, 768), (300, 256)])
+# rows above 256 take the fused many-row kernel (prefills)
+@pytest.mark.parametrize("rows,D", [(1, 4096), (8, 2048), (40, 768), (300, 256), (257, 512), (1000, 4096)])
 def test_wavg_lora(oracle, rows, D):
     from rwkv7mi.fused_lora import fused_wavg_lora
 
@@ -104,7 +105,7 @@ def test_wavg_lora(oracle, rows, D):
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("rows,D", [(2, 1024), (33, 200)])
+@pytest.mark.parametrize("rows,D", [(2, 1024), (33, 200), (300, 200)])
 def test_wag_lora_dtypes(oracle, dt, rows, D):
     from rwkv7mi.fused_lora import fused_wag_lora
 
