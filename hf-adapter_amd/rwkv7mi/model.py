@@ -293,10 +293,15 @@ class NativeRWKV7Cache(_HFCache):
 
     @classmethod
     def zeros(cls, cfg: "NativeRWKV7Config", batch: int, device, dtype=torch.float16):
+        """A zero cache whose per-layer tensors are views of layer-major
+        storage ([L, B, H, N, N] fp32 state, [L, B, D] shift rows): each layer
+        is contiguous and the layers are equally spaced, so one slot-copy
+        launch can move a batch row of every layer."""
         H, N, D, A, L = cfg.num_heads, cfg.head_dim, cfg.hidden_size, cfg.attention_hidden_size, cfg.num_hidden_layers
-        return cls([torch.zeros(batch, H, N, N, device=device, dtype=torch.float32) for _ in range(L)],
-                   [torch.zeros(batch, D, device=device, dtype=dtype) for _ in range(L)],
-                   [torch.zeros(batch, D, device=device, dtype=dtype) for _ in range(L)],
+        S = torch.zeros(L, batch, H, N, N, device=device, dtype=torch.float32)
+        xa = torch.zeros(L, batch, D, device=device, dtype=dtype)
+        xf = torch.zeros(L, batch, D, device=device, dtype=dtype)
+        return cls(list(S.unbind(0)), list(xa.unbind(0)), list(xf.unbind(0)),
                    torch.zeros(batch, A, device=device, dtype=dtype), 0)
 
     # ---- graph binding / version protocol (rwkv7_hf/model_cache.py:89-114)
@@ -681,7 +686,10 @@ class NativeRWKV7ForCausalLM:
         self._graph_runners: dict[int, "NativeGraphRunner"] = {}
 
     def __init__(self, config: NativeRWKV7Config, weights: dict[str, torch.Tensor], *, device="cuda",
-                 dtype=torch.float16):
+                 dtype=torch.float16, prepacked: dict | None = None):
+        """``weights``: HF-named parameters (see :func:`parameter_shapes`).
+        ``prepacked``: module name -> :class:`MM8Linear` built from a
+        prepacked checkpoint; those modules' ``.weight`` entries are not read."""
         self._init_common(config, device, dtype)
         cfg = config
         dev = self.device
@@ -690,6 +698,9 @@ class NativeRWKV7ForCausalLM:
             return weights[name].to(device=dev, dtype=dtype).contiguous()
 
         def linear(name):
+            if prepacked is not None and name in prepacked:
+                self._replaced += 1
+                return QuantLinear(prepacked[name])
             w = get(name + ".weight")
             if cfg.use_native_mm8 and should_quantize_linear(name, int(w.numel()),
                                                              min_params=cfg.native_mm8_min_params,
@@ -859,6 +870,41 @@ class NativeRWKV7ForCausalLM:
         cfg = self.config
         ranks = [cfg.decay_low_rank_dim, cfg.a_low_rank_dim, cfg.gate_low_rank_dim, cfg.v_low_rank_dim]
         _ws.reserve(self.device, lora_workspace_bytes(ranks, rows, cfg.hidden_size), slot="lora")
+
+    def named_linears(self):
+        """(HF module name, linear) for every projection and the head."""
+        for L in self.layers:
+            p = f"model.layers.{L.idx}."
+            yield from ((p + "attn.r_proj", L.r_proj), (p + "attn.k_proj", L.k_proj), (p + "attn.v_proj", L.v_proj),
+                        (p + "attn.o_proj", L.o_proj), (p + "ffn.key", L.key), (p + "ffn.value", L.value))
+        yield "lm_head", self.lm_head
+
+    def dense_state_dict(self) -> dict:
+        """HF-named tensors of every parameter the model holds unquantised
+        (the dense linears' ``.weight`` included, the MM8 modules' excluded)."""
+        sd = {"model.embeddings.weight": self.emb, "model.norm.weight": self.norm[0], "model.norm.bias": self.norm[1]}
+        for L in self.layers:
+            p = f"model.layers.{L.idx}."
+            if L.pre is not None:
+                sd[p + "pre_norm.weight"], sd[p + "pre_norm.bias"] = L.pre
+            sd[p + "attn_norm.weight"], sd[p + "attn_norm.bias"] = L.ln1
+            sd[p + "ffn_norm.weight"], sd[p + "ffn_norm.bias"] = L.ln2
+            D = self.config.hidden_size
+            for m, v in zip(("x_r", "x_w", "x_k", "x_v", "x_a", "x_g"), L.mix):
+                sd[p + "attn." + m] = v.reshape(1, 1, D)
+            sd[p + "attn.k_k"], sd[p + "attn.k_a"], sd[p + "attn.r_k"] = L.k_k, L.k_a, L.r_k
+            names = ["w_lora", "a_lora", "g_lora", "v_lora"][:len(L.lora_down)]
+            for n, d, u, b in zip(names, L.lora_down, L.lora_up, L.lora_bias):
+                sd[p + f"attn.{n}.lora.0.weight"] = d
+                sd[p + f"attn.{n}.lora.2.weight"] = u
+                if b is not None:
+                    sd[p + f"attn.{n}.lora.2.bias"] = b
+            sd[p + "attn.g_norm.weight"], sd[p + "attn.g_norm.bias"] = L.gn
+            sd[p + "ffn.x_k"] = L.fx_k
+        for name, lin in self.named_linears():
+            if isinstance(lin, DenseLinear):
+                sd[name + ".weight"] = lin.weight
+        return sd
 
     def _linears(self):
         for L in self.layers:

@@ -102,6 +102,11 @@ def mm8_unblock(w_blk: torch.Tensor, in_features: int, out_features: int) -> tor
     return out
 
 
+def mm8_block_shape(n: int, m: int) -> tuple:
+    """Shape of the blocked copy of ``w_u8 [n, m]`` (see :func:`mm8_block`)."""
+    return ((int(m) + 15) // 16, (int(n) + 127) // 128, 2048)
+
+
 def is_blocked(w: torch.Tensor) -> bool:
     """True for the decode GEMV's blocked weight tensor (see :func:`mm8_block`)."""
     return (w.dim() == 3 and int(w.shape[2]) == 2048 and w.dtype == torch.uint8 and w.is_contiguous())
@@ -476,6 +481,35 @@ class MM8Linear(torch.nn.Module):
         self.register_state_dict_post_hook(MM8Linear._export_w_u8)
         self.register_load_state_dict_pre_hook(MM8Linear._import_w_u8)
 
+    @classmethod
+    def from_packed(cls, w_blk, mx, rx, my, ry, in_features: int, out_features: int, bias=None, *, fused=True):
+        """A module from already packed tensors (a prepacked checkpoint): the
+        blocked bytes ``w_blk`` (:func:`mm8_block_shape`) and the four scale
+        vectors as :func:`quantize_mm8_blocked` returns them.  No quantisation."""
+        n, m = int(in_features), int(out_features)
+        if tuple(w_blk.shape) != mm8_block_shape(n, m) or w_blk.dtype != torch.uint8:
+            raise ValueError(f"MM8Linear.from_packed: w_blk {w_blk.dtype} {tuple(w_blk.shape)} is not the blocked "
+                             f"layout of [{n}, {m}]")
+        if mx.numel() != m or rx.numel() != m or my.numel() != n or ry.numel() != n:
+            raise ValueError("MM8Linear.from_packed: scale vectors do not match the features")
+        self = cls.__new__(cls)
+        torch.nn.Module.__init__(self)
+        self.in_features, self.out_features = n, m
+        self.register_buffer("w_blk", w_blk.contiguous(), persistent=False)
+        self.register_buffer("mx", mx)
+        self.register_buffer("rx", rx)
+        self.register_buffer("my", my)
+        self.register_buffer("ry", ry)
+        if bias is not None:
+            self.register_buffer("bias", bias)
+        else:
+            self.bias = None
+        self.fused = bool(fused)
+        self.sm7x_rowwise = False
+        self.register_state_dict_post_hook(MM8Linear._export_w_u8)
+        self.register_load_state_dict_pre_hook(MM8Linear._import_w_u8)
+        return self
+
     @property
     def w_u8(self) -> torch.Tensor:
         """The reference's ``w_u8 [in, out]`` (a new contiguous tensor)."""
@@ -605,7 +639,7 @@ def invalidate_model_caches(model) -> None:
         runners.clear()
 
 
-__all__ = ["mm8_gemm_prefill_multi_into", 
+__all__ = ["mm8_gemm_prefill_multi_into", "mm8_block_shape", 
     "quantize_mm8", "dequantize_mm8", "quantize_mm8_outmajor", "quantize_mm8_blocked", "mm8_block", "mm8_unblock", "is_blocked",
     "is_out_major", "mm8_matmul", "mm8_linear", "mm8_matmul_into",
     "mm8_matmul_multi_into", "mm8_gemm_multi_into", "mm8_gemm_workspace_bytes", "mm8_gemv_triton",

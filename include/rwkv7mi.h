@@ -391,6 +391,25 @@ int rwkv7mi_mm4_dequant(const uint8_t* packed, const void* mx, const void* rx_s,
                         const void* my, const void* ry_s, void* out, int64_t I,
                         int64_t O, int meta_dtype, int out_dtype, void* stream);
 
+/* ------------------------------------------------------------ state slots */
+
+/* Row copies between layer-major state pools and dense batches (the serving
+ * state-slot pool of docs/integrations/RWKV7_STATE_CACHE_ABI.md:52-133:
+ * gather / scatter / clone / reset of scheduled slots, NativeRWKV7Cache's
+ * select_batch / reorder semantics, rwkv7_hf/model_cache.py:335-343).  Row r
+ * of layer l is copied from src + l*src_layer_stride + src_rows[r]*
+ * src_row_stride to dst + l*dst_layer_stride + dst_rows[r]*dst_row_stride
+ * (byte strides; a NULL index array is the identity; src_rows / dst_rows /
+ * active are device arrays), rows with active[r] == 0 are left untouched, and
+ * src == NULL writes zeros.  row_bytes, pointers and strides 16-byte
+ * aligned; nrows, nlayers <= 65535. */
+int rwkv7mi_slot_copy(const void* src, int64_t src_layer_stride,
+                      int64_t src_row_stride, const int64_t* src_rows, void* dst,
+                      int64_t dst_layer_stride, int64_t dst_row_stride,
+                      const int64_t* dst_rows, const uint8_t* active,
+                      int64_t nrows, int64_t row_bytes, int64_t nlayers,
+                      void* stream);
+
 /* ------------------------------------------------------------------ LoRA */
 
 /* Bytes of workspace rwkv7mi_lora_multi needs (fp32 split-K partials). */
