@@ -1222,6 +1222,16 @@ class NativeRWKV7ForCausalLM:
 
     __call__ = forward
 
+    def prefill_graph_runner(self, batch: int, tokens: int, *, logits_to_keep: int = 1,
+                             carry_state: bool = False) -> "NativePrefillGraphRunner":
+        """The cached prefill graph for this shape (captured on first use)."""
+        key = (int(batch), int(tokens), int(logits_to_keep), bool(carry_state))
+        runners = self.__dict__.setdefault("_prefill_graph_runners", {})
+        if key not in runners:
+            runners[key] = NativePrefillGraphRunner(self, batch, tokens, logits_to_keep=logits_to_keep,
+                                                    carry_state=carry_state)
+        return runners[key]
+
     def graph_runner(self, batch: int) -> "NativeGraphRunner":
         r = self._graph_runners.get(batch)
         if r is None:
@@ -1330,5 +1340,83 @@ class NativeGraphRunner:
         return self.logits
 
 
+class NativePrefillGraphRunner:
+    """hipGraph-captured prefill for one shape ``(B, T, logits_to_keep)``
+    (rwkv7_hf/model_prefill_graph.py:38-381): the whole layer stack of
+    :meth:`NativeRWKV7ForCausalLM.prefill_` — embedding, mixes, MM8 GEMMs,
+    LoRA, state prep, chunked scan, output prep — replays as one graph for
+    repeated prompt shapes.
+
+    Static buffers: ``ids [B, T]`` and a layer-major cache; intermediates
+    live in the graph's private memory pool.  ``carry_state=False`` starts
+    every replay from zeros (the static cache is cleared by fill kernels
+    before the replay); ``carry_state=True`` copies ``initial_cache`` in
+    first (cache continuation).  ``replay`` returns ``(logits, cache)``: new
+    tensors by default (a later replay does not disturb them), or the
+    runner's static buffers with ``copy=False``."""
+
+    def __init__(self, model: "NativeRWKV7ForCausalLM", batch: int, tokens: int, *, logits_to_keep: int = 1,
+                 carry_state: bool = False, warmup: int = 1):
+        self.model = model
+        self.batch, self.tokens_n = int(batch), int(tokens)
+        self.logits_to_keep = int(logits_to_keep)
+        self.carry_state = bool(carry_state)
+        dev = model.device
+        model.reserve_workspace(min(self.batch * self.tokens_n, 256))
+        self.ids = torch.zeros(self.batch, self.tokens_n, dtype=torch.long, device=dev)
+        self.cache = model.new_cache(self.batch)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):  # grows every workspace slot the body uses, before capture
+                model.prefill_(self.ids, self.cache, logits_to_keep=self.logits_to_keep)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self._zero_state()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = model.prefill_(self.ids, self.cache, logits_to_keep=self.logits_to_keep)
+        self.replays = 0
+
+    def _zero_state(self) -> None:
+        s, a, f, v = self.cache
+        for t in (*s, *a, *f, v):
+            t.zero_()
+
+    def matches(self, batch: int, tokens: int, logits_to_keep: int, carry_state: bool) -> bool:
+        return (self.batch, self.tokens_n, self.logits_to_keep, self.carry_state) == (
+            int(batch), int(tokens), int(logits_to_keep), bool(carry_state))
+
+    def replay(self, input_ids: torch.Tensor, initial_cache: "NativeRWKV7Cache | None" = None, *, copy: bool = True):
+        if tuple(input_ids.shape) != (self.batch, self.tokens_n):
+            raise ValueError(f"prefill graph for [{self.batch}, {self.tokens_n}] got {tuple(input_ids.shape)}")
+        if initial_cache is not None and not self.carry_state:
+            raise ValueError("this prefill graph was captured without cache continuation (carry_state=False)")
+        seen = 0
+        if self.carry_state and initial_cache is not None and initial_cache.is_initialized:
+            if initial_cache.get_batch_size() != self.batch:
+                raise ValueError("initial cache batch differs from the captured batch")
+            s, a, f, v = self.cache
+            s2, a2, f2, v2 = initial_cache
+            for dst, src in zip((*s, *a, *f, v), (*s2, *a2, *f2, v2)):
+                dst.copy_(src)
+            seen = initial_cache.seen_tokens
+        else:
+            self._zero_state()
+        self.ids.copy_(input_ids)
+        self.graph.replay()
+        self.replays += 1
+        if not copy:
+            out = NativeRWKV7Cache(list(self.cache._state), list(self.cache._xpa), list(self.cache._xpf),
+                                   self.cache._v_first, seen + self.tokens_n)
+            return self.logits, out
+        out = self.model.new_cache(self.batch)
+        s, a, f, v = out
+        s2, a2, f2, v2 = self.cache
+        for dst, src in zip((*s, *a, *f, v), (*s2, *a2, *f2, v2)):
+            dst.copy_(src)
+        out.seen_tokens = seen + self.tokens_n
+        return self.logits.clone(), out
+
+
 __all__ = ["NativeRWKV7Config", "NativeRWKV7Cache", "NativeRWKV7ForCausalLM", "NativeGraphRunner",
-           "random_weights", "parameter_shapes"]
+           "NativePrefillGraphRunner", "random_weights", "parameter_shapes"]

@@ -634,12 +634,13 @@ def invalidate_model_caches(model) -> None:
     for attr in MODEL_CACHE_ATTRS:
         if hasattr(model, attr):
             delattr(model, attr)
-    runners = getattr(model, "_graph_runners", None)
-    if isinstance(runners, dict):
-        runners.clear()
+    for name in ("_graph_runners", "_prefill_graph_runners"):
+        runners = getattr(model, name, None)
+        if isinstance(runners, dict):
+            runners.clear()
 
 
-__all__ = ["mm8_gemm_prefill_multi_into", "mm8_block_shape", 
+__all__ = ["mm8_gemm_prefill_multi_into", "mm8_block_shape",
     "quantize_mm8", "dequantize_mm8", "quantize_mm8_outmajor", "quantize_mm8_blocked", "mm8_block", "mm8_unblock", "is_blocked",
     "is_out_major", "mm8_matmul", "mm8_linear", "mm8_matmul_into",
     "mm8_matmul_multi_into", "mm8_gemm_multi_into", "mm8_gemm_workspace_bytes", "mm8_gemv_triton",
