@@ -212,7 +212,7 @@ namespace rwkv7mi {
 // stored fp32 [problem][ks][rows][rank] (problems packed back to back).  The
 // up projection (lora.hip) and the fused decode (wkv7_decode.hip) both read
 // this layout.
-constexpr int LORA_ROWS = 32;  // rows per launch pair
+constexpr int LORA_ROWS = 64;  // rows per launch pair
 inline int64_t lora_tiles(int64_t nprob, const int64_t* ranks) {
   int64_t t = 0;
   for (int64_t i = 0; i < nprob; ++i) t += (ranks[i] + 15) / 16;

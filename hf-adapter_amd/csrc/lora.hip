@@ -27,17 +27,26 @@ struct LoraProb {
   const void* wu;
   const void* bu;
   void* y;
-  int r, act_d, act_u, tile_d0, tile_u0;
+  int r, act_d, act_u, tile_d0, tile_u0;  // tile_u0: first up workgroup (tpw output tiles each)
   int64_t part_off;  // floats
 };
 struct LoraBatch {
   LoraProb p[4];
   int nprob, D, A, ks, kr;
+  int tpw;  // up kernel: output tiles of 16 columns per workgroup
 };
 
 __device__ __forceinline__ float lora_act(float v, int act) {
   if (act == LORA_ACT_TANH) return tanhf(v);
   if (act == LORA_ACT_SIGMOID) return 1.0f / (1.0f + expf(-v));
+  return v;
+}
+// The same with the hardware exp2 / reciprocal for the sigmoid (a few ulp of
+// fp32, far below the activation dtype's rounding that follows); tanh keeps
+// the library routine (1 - e^-2|v| loses relative accuracy near 0).
+__device__ __forceinline__ float lora_act_fast(float v, int act) {
+  if (act == LORA_ACT_TANH) return tanhf(v);
+  if (act == LORA_ACT_SIGMOID) return __frcp_rn(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * v));
   return v;
 }
 
@@ -128,104 +137,146 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const LoraBatch B, int r
   }
 }
 
-// grid (up tiles): y[row, o] = act_up(sum_k mid[row,k] Wu[o,k] + b[o]),
-// mid = round_TA(act_down(sum_z partial[z])) staged in LDS.
+// grid (up workgroups): y[row, o] = act_up(sum_k mid[row,k] Wu[o,k] + b[o]),
+// mid = round_TA(act_down(sum_z partial[z])) staged in LDS once per workgroup,
+// then B.tpw output tiles of 16 columns, whole tiles per wave, each wave's next
+// tile's weights loaded before this tile's MFMAs.  MT = 4 (up to 64 rows)
+// takes ranks up to 128.
 template <int MT, typename TA>
 __global__ __launch_bounds__(256) void lora_up_kernel(const LoraBatch B, int rows, const float* __restrict__ part) {
   constexpr bool SPLIT = !std::is_same<TA, __half>::value;
-  constexpr int RS = LORA_MAXR + 8;  // LDS row stride (halfs)
+  constexpr int RMAX = MT == 4 ? 128 : LORA_MAXR;
+  constexpr int RS = RMAX + 8;  // LDS row stride (halfs)
   __shared__ __align__(16) _Float16 mh[16 * MT][RS];
   __shared__ __align__(16) _Float16 ml[SPLIT ? 16 * MT : 1][SPLIT ? RS : 8];
-  __shared__ float s_red[4][16 * MT][17];
-  const int tile = blockIdx.x;
-  const LoraProb& P = B.p[lora_find(B, tile, true)];
+  const int wgi = blockIdx.x;
+  const LoraProb& P = B.p[lora_find(B, wgi, true)];
   const int r = P.r;
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(P.wu, (uint32_t)((int64_t)B.A * r * sizeof(TA)));
-  const int o0 = (tile - P.tile_u0) * 16;
+  const int ntile = (B.A + 15) / 16;
+  const int t0 = (wgi - P.tile_u0) * B.tpw;
+  const int t1 = min(ntile, t0 + B.tpw);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, kg = lane >> 4;
 
-  // this wave's up-weight operands (k steps wave*32 and wave*32 + 128; rank <= 256),
-  // loaded before staging so their latency overlaps it
-  f16x8 bh[2], bl[2];
+  // a tile's up weights for this wave (lane: column 16 tl + l16, rank 32 j + 8 kg ..)
+  constexpr int KW = RMAX / 32;
+  f16x8 wh[KW], wl[KW];
+  auto load_w = [&](int tl) {
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int kk = wave * 32 + 128 * it + 8 * kg;
-    lora_load8<TA>(wr, (uint32_t)((o0 + l16) * r + kk), kk < r && o0 + l16 < B.A, bh[it], bl[it]);
-  }
+    for (int j = 0; j < KW; ++j) {
+      const int kk = 32 * j + 8 * kg;
+      const int o = 16 * tl + l16;
+      lora_load8<TA>(wr, (uint32_t)(o * r + kk), tl < t1 && kk < r && o < B.A, wh[j], wl[j]);
+    }
+  };
+  load_w(t0 + wave);  // the wave's first tile overlaps the staging
 
-  // stage mid: fixed-order sum over the K splits for four elements per pass,
-  // 32 loads in flight at a time (each element's sum runs in z order)
-  constexpr int IB = 4;  // elements per pass
+  // stage mid: fixed-order sum over the K splits, four consecutive elements per
+  // 16-byte load, IB groups x 4 splits = 32 loads in flight at a time (each
+  // element's sum runs in z order; rows * r is a multiple of 8)
+  constexpr int IB = 8;  // 4-element groups per thread and pass
   const int zstride = rows * r;
+  const int ngrp = zstride / 4;
+  const int r4 = r >> 2;  // 4-element groups per mid row
+  const float inv_r4 = 1.0f / (float)r4;
   const __amdgpu_buffer_rsrc_t pr = make_rsrc(part + P.part_off, (uint32_t)(B.ks * zstride * 4));
-  for (int idx0 = tid; idx0 < rows * r; idx0 += 256 * IB) {
-    float s[IB];
+  for (int g0 = tid; g0 < ngrp; g0 += 256 * IB) {
+    float s[IB][4];
 #pragma unroll
-    for (int ib = 0; ib < IB; ++ib) s[ib] = 0.f;
-    for (int z0 = 0; z0 < B.ks; z0 += 8) {
-      float t[IB][8];
+    for (int ib = 0; ib < IB; ++ib)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[ib][e] = 0.f;
+    for (int z0 = 0; z0 < B.ks; z0 += 4) {
+      u32x4 t[IB][4];
 #pragma unroll
       for (int ib = 0; ib < IB; ++ib) {
-        const int idx = idx0 + 256 * ib;
+        const int g = g0 + 256 * ib;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          t[ib][u] = buf_ldf(pr, z0 + u < B.ks && idx < zstride ? (uint32_t)(((z0 + u) * zstride + idx) * 4)
-                                                                 : BUF_OOB);
+        for (int u = 0; u < 4; ++u)
+          t[ib][u] = buf_ld16(pr, z0 + u < B.ks && g < ngrp ? (uint32_t)(((z0 + u) * zstride + 4 * g) * 4)
+                                                           : BUF_OOB);
       }
 #pragma unroll
       for (int ib = 0; ib < IB; ++ib)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) s[ib] += t[ib][u];  // z order; past-the-end terms are +0
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[ib][e] += __uint_as_float(t[ib][u][e]);  // z order; past-the-end terms are +0
     }
 #pragma unroll
     for (int ib = 0; ib < IB; ++ib) {
-      const int idx = idx0 + 256 * ib;
-      if (idx < zstride) {
-        const float v = to_f32(from_f32<TA>(lora_act(s[ib], P.act_d)));
-        const int row = idx / r, k = idx % r;
-        const _Float16 h = (_Float16)v;
-        mh[row][k] = h;
-        if constexpr (SPLIT) ml[row][k] = (_Float16)(v - (float)h);
+      const int g = g0 + 256 * ib;
+      if (g < ngrp) {
+        // row = g / r4 from a float reciprocal (g < 2^24) with a one-step fix-up
+        int row = (int)((float)g * inv_r4);
+        row -= row * r4 > g ? 1 : 0;
+        row += (row + 1) * r4 <= g ? 1 : 0;
+        const int k0 = 4 * (g - row * r4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float v = to_f32(from_f32<TA>(lora_act_fast(s[ib][e], P.act_d)));
+          const _Float16 h = (_Float16)v;
+          mh[row][k0 + e] = h;
+          if constexpr (SPLIT) ml[row][k0 + e] = (_Float16)(v - (float)h);
+        }
       }
     }
   }
   __syncthreads();
 
-  f32x4 acc[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // ---- each wave takes whole output tiles (every rank step), so no
+  // cross-wave reduction: tiles t0 + wave, t0 + wave + 4, ...; the wave's mid
+  // operands stay in registers for all of them
   const f16x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  constexpr int KU = RMAX / 32;  // rank steps of 32
+  f16x8 amh[MT][KU], aml[SPLIT ? MT : 1][SPLIT ? KU : 1];
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int kk = wave * 32 + 128 * it + 8 * kg;
-    const bool kok = kk < r;  // r % 8 == 0
+  for (int m = 0; m < MT; ++m)
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int row = 16 * t + l16;  // rows past `rows` only feed discarded D rows
-      const f16x8 ah = kok ? *reinterpret_cast<const f16x8*>(&mh[row][kk]) : zero8;
-      acc[t] = mfma16x16x32(ah, bh[it], acc[t]);
-      if constexpr (SPLIT) {
-        const f16x8 al = kok ? *reinterpret_cast<const f16x8*>(&ml[row][kk]) : zero8;
-        acc[t] = mfma16x16x32(ah, bl[it], acc[t]);
-        acc[t] = mfma16x16x32(al, bh[it], acc[t]);
-      }
+    for (int j = 0; j < KU; ++j) {
+      const int kk = 32 * j + 8 * kg;
+      const int row = 16 * m + l16;  // rows past `rows` only feed discarded D rows
+      amh[m][j] = kk < r ? *reinterpret_cast<const f16x8*>(&mh[row][kk]) : zero8;
+      if constexpr (SPLIT) aml[m][j] = kk < r ? *reinterpret_cast<const f16x8*>(&ml[row][kk]) : zero8;
     }
-  }
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s_red[wave][16 * t + 4 * kg + e][l16] = acc[t][e];
-  __syncthreads();
   TA* y = reinterpret_cast<TA*>(P.y);
   const TA* bias = reinterpret_cast<const TA*>(P.bu);
-  for (int idx = tid; idx < rows * 16; idx += 256) {
-    const int row = idx >> 4, nn = idx & 15;
-    const int o = o0 + nn;
-    if (o >= B.A) continue;
-    float v = ((s_red[0][row][nn] + s_red[1][row][nn]) + s_red[2][row][nn]) + s_red[3][row][nn];
-    if (bias) v += to_f32(bias[o]);
-    y[(int64_t)row * B.A + o] = from_f32<TA>(lora_act(v, P.act_u));
+  for (int tl = t0 + wave; tl < t1; tl += 4) {
+    f16x8 ch[KU], cl[KU];
+#pragma unroll
+    for (int j = 0; j < KU; ++j) {
+      ch[j] = wh[j];
+      cl[j] = wl[j];
+    }
+    load_w(tl + 4);  // the wave's next tile
+    f32x4 acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      acc[m] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KU; ++j) {
+        if (32 * j < r) {  // (uniform) rank steps past r hold zeros
+          acc[m] = mfma16x16x32(amh[m][j], ch[j], acc[m]);
+          if constexpr (SPLIT) {
+            acc[m] = mfma16x16x32(amh[m][j], cl[j], acc[m]);
+            acc[m] = mfma16x16x32(aml[m][j], ch[j], acc[m]);
+          }
+        }
+      }
+    }
+    // C: lane holds column 16 tl + l16, rows 16 m + 4 kg + e
+    const int o = 16 * tl + l16;
+    if (o < B.A) {
+      const float bo = bias ? to_f32(bias[o]) : 0.f;
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = 16 * m + 4 * kg + e;
+          if (row < rows) y[(int64_t)row * B.A + o] = from_f32<TA>(lora_act(acc[m][e] + bo, P.act_u));
+        }
+    }
   }
 }
 
@@ -404,13 +455,22 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
   if (rows < 0 || D <= 0 || A <= 0 || D % 8 || D > (1 << 20) || A > (1 << 20))
     return fail(RWKV7MI_EINVAL, "lora_multi: bad shape (D a positive multiple of 8)");
   if (rows == 0) return RWKV7MI_OK;
-  if (!up && rows > LORA_ROWS) return fail(RWKV7MI_EINVAL, "lora_down_multi: at most 32 rows");
+  if (!up && rows > LORA_ROWS) return fail(RWKV7MI_EINVAL, "lora_down_multi: at most 64 rows");
   if (!valid_dtype(act_dtype)) return fail(RWKV7MI_EINVAL, "lora_multi: bad dtype");
   LoraBatch batch{};
   int td = 0, tu = 0;
   int64_t off = 0;
-  const int64_t nr_max = rows < LORA_ROWS ? rows : LORA_ROWS;
+  int rmax = 0;
+  for (int i = 0; i < nprob; ++i) rmax = std::max(rmax, (int)ranks[i]);
+  // rows per launch pair: 64 (four MFMA row tiles) for ranks up to 128, else 32
+  const int64_t chunk = rmax > 128 ? 32 : LORA_ROWS;
+  const int64_t nr_max = rows < chunk ? rows : chunk;
   const int tiles_d = (int)lora_tiles(nprob, ranks);
+  // up workgroups: each stages its problem's mid once, so several output tiles
+  // share it; about one workgroup per compute unit over all problems
+  const int ntile_u = (int)((A + 15) / 16);
+  // about 128 up workgroups over all problems, at least one tile per wave
+  const int tpw = std::min(((ntile_u + 3) / 4) * 4, std::max(4, (int)((nprob * ntile_u / 128 + 3) / 4) * 4));
   // more than 16 rows per chunk: a quarter of the K splits, so each up tile
   // sums four times fewer partials (its staging is the up kernel's cost there)
   const int ks = up && nr_max > 16 ? std::max(1, lora_splits(tiles_d, D) / 4) : lora_splits(tiles_d, D);
@@ -427,7 +487,7 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
                           up ? ys[i] : nullptr, (int)ranks[i],
                           act_down[i], act_up[i], td, tu, off};
     td += (int)((ranks[i] + 15) / 16);
-    tu += (int)((A + 15) / 16);
+    tu += (ntile_u + tpw - 1) / tpw;
     off += (int64_t)ks * nr_max * ranks[i];
   }
   if ((!up || rows <= LORA_PREFILL_ROWS) && (!workspace || workspace_bytes < (size_t)off * sizeof(float)))
@@ -435,6 +495,7 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
   batch.nprob = (int)nprob;
   batch.D = (int)D;
   batch.A = (int)A;
+  batch.tpw = tpw;
   batch.ks = ks;
   batch.kr = (int)((D + ks - 1) / ks);
   batch.kr = (batch.kr + 7) / 8 * 8;
@@ -443,8 +504,6 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
     // many rows: the fused per-row-tile kernel, one launch, no partials
     if (rows * std::max(D, A) * (int64_t)esz > INT32_MAX || A * LORA_MAXR * (int64_t)esz > INT32_MAX)
       return fail(RWKV7MI_EINVAL, "lora_multi: too large");
-    int rmax = 0;
-    for (int i = 0; i < nprob; ++i) rmax = std::max(rmax, (int)ranks[i]);
     const int rt = (rmax + 15) / 16;
     return dispatch_dtype(act_dtype, [&](auto ta) {
       using TA = decltype(ta);
@@ -458,8 +517,8 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
     });
   }
   float* part = reinterpret_cast<float*>(workspace);
-  for (int64_t r0 = 0; r0 < rows; r0 += LORA_ROWS) {
-    const int64_t nr = rows - r0 > LORA_ROWS ? LORA_ROWS : rows - r0;
+  for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+    const int64_t nr = rows - r0 > chunk ? chunk : rows - r0;
     LoraBatch bb = batch;
     for (int i = 0; i < nprob; ++i) {
       bb.p[i].x = reinterpret_cast<const char*>(batch.p[i].x) + r0 * D * esz;
@@ -469,7 +528,7 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
       for (int j = 0; j < i; ++j) o2 += (int64_t)ks * nr * ranks[j];
       bb.p[i].part_off = o2;
     }
-    const int mt = nr <= 16 ? 1 : 2;
+    const int mt = nr <= 16 ? 1 : nr <= 32 ? 2 : 4;
     int rc = dispatch_dtype(act_dtype, [&](auto ta) {
       using TA = decltype(ta);
       hipStream_t s = as_stream(stream);
@@ -479,8 +538,10 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
   hipLaunchKernelGGL((lora_up_kernel<MT_, TA>), dim3(tu), dim3(256), 0, s, bb, (int)nr, (const float*)part)
       if (mt == 1) {
         LORA_GO(1);
-      } else {
+      } else if (mt == 2) {
         LORA_GO(2);
+      } else {
+        LORA_GO(4);
       }
 #undef LORA_GO
       return check_launch("lora_multi");

@@ -8,6 +8,8 @@ the reference does.  Runs the gfx950 kernel; GPU tensors only.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -103,6 +105,56 @@ def fused_ffn_add_norm_mix_decode(residual, attn_out, previous, norm_weight, nor
     return res_out.reshape(shape), mix_out.reshape(shape)
 
 
+def attn_mix_lora_chunks(D: int) -> int:
+    """K-chunks :func:`attn_mix_lora_decode` splits width ``D`` into (0: unsupported)."""
+    return int(_lib.load().rwkv7mi_attn_mix_lora_chunks(int(D)))
+
+
+def attn_mix_lora_decode(x, previous, norm_weight, norm_bias, mixes, outs, lora_downs, lora_mix, part, *,
+                         h_out, x_out=None, pre_norm_weight=None, pre_norm_bias=None, eps: float = 1e-5) -> int:
+    """Decode attention-side entry for 1..8 fp16/bf16 rows in one launch:
+    layer 0's pre-norm (the normalised row -> ``x_out``), ``h = LayerNorm``
+    (-> ``h_out``), the r / k / v mixed rows of ``mixes`` (x_r, x_w, x_k, x_v,
+    x_a, x_g) into ``outs``, and the LoRA down projections of the mixes
+    ``lora_mix[q]`` as K-chunk partial sums in ``part`` (fp32
+    ``[q][chunk][row][rank_q]``) -- fused_attn_norm_mix6_decode
+    (rwkv7_hf/fused_decode_norm_mix.py:161) plus the down half of
+    fused_wavg_lora (rwkv7_hf/fused_lora.py:706).  ``previous`` is read only.
+    Returns the chunk count (the wkv kernel's ``lora_splits``)."""
+    rows, D = int(_rows(x, "x")[0].shape[0]), int(x.shape[-1])
+    ranks = [int(w.shape[0]) for w in lora_downs]
+    chunks = attn_mix_lora_chunks(D)
+    if not chunks or not 1 <= rows <= 8 or x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("attn_mix_lora_decode: 1..8 fp16/bf16 rows, D a multiple of 128 up to 4096")
+    if len(mixes) != 6 or len(outs) != 3 or not 1 <= len(lora_downs) <= 4 or len(lora_mix) != len(lora_downs):
+        raise ValueError("attn_mix_lora_decode: six mixes, three outputs, 1..4 LoRA problems")
+    if (pre_norm_weight is None) != (x_out is None):
+        raise ValueError("attn_mix_lora_decode: x_out goes with the pre-norm")
+    for t in (x, h_out, previous, *outs) + ((x_out,) if x_out is not None else ()):
+        if tuple(t.shape) != (rows, D) or not t.is_contiguous() or t.dtype != x.dtype:
+            raise ValueError("attn_mix_lora_decode: rows must be contiguous [rows, D] in x's dtype")
+    for w in lora_downs:
+        if w.dim() != 2 or int(w.shape[1]) != D or w.dtype != x.dtype:
+            raise ValueError("attn_mix_lora_decode: LoRA down weights are [rank, D] in x's dtype")
+    if part.dtype != torch.float32 or not part.is_contiguous() or int(part.numel()) < chunks * rows * sum(ranks):
+        raise ValueError("attn_mix_lora_decode: part must be contiguous fp32 with chunks * rows * sum(ranks) values")
+    pdt = norm_weight.dtype
+    vecs = [_vec(m, D, "mix") for m in mixes]
+    if any(v.dtype != pdt for v in vecs) or norm_bias.dtype != pdt:
+        raise ValueError("attn_mix_lora_decode: the mixes and LN parameters must share one dtype")
+    _lib.require_gpu(x, previous, h_out, part, name="attn_mix_lora_decode")
+    _lib.call(
+        "rwkv7mi_attn_mix_lora", _lib.ptr(x), _lib.ptr(x_out), _lib.ptr(previous), _lib.ptr(h_out),
+        _lib.ptr(_vec(norm_weight, D, "norm_weight")), _lib.ptr(_vec(norm_bias, D, "norm_bias")),
+        _lib.ptr(None if pre_norm_weight is None else _vec(pre_norm_weight, D, "pre_norm_weight")),
+        _lib.ptr(None if pre_norm_bias is None else _vec(pre_norm_bias, D, "pre_norm_bias")),
+        _lib.ptr_array(vecs), _lib.ptr_array(list(outs)), len(lora_downs),
+        _lib.ptr_array([w.contiguous() for w in lora_downs]), (ctypes.c_int64 * len(ranks))(*ranks),
+        (ctypes.c_int * len(lora_mix))(*[int(i) for i in lora_mix]), _lib.ptr(part), rows, D, float(eps),
+        _lib.dtype_code(x), _lib.dtype_code(norm_weight), _lib.stream_of(x))
+    return chunks
+
+
 def layer_norm(x, weight, bias, eps: float = 1e-5, out=None):
     """``F.layer_norm`` over the last dimension (HIP kernel)."""
     x2, D = _rows(x, "x")
@@ -116,4 +168,4 @@ def layer_norm(x, weight, bias, eps: float = 1e-5, out=None):
     return y.reshape(x.shape)
 
 
-__all__ = ["fused_attn_norm_mix6_decode", "fused_ffn_add_norm_mix_decode", "layer_norm"]
+__all__ = ["attn_mix_lora_chunks", "attn_mix_lora_decode", "fused_attn_norm_mix6_decode", "fused_ffn_add_norm_mix_decode", "layer_norm"]

@@ -51,7 +51,7 @@ def lora_multi(xs, downs, ups, biases, outs, acts_down, acts_up):
     A = int(ups[0].shape[0])
     ranks = [int(d.shape[0]) for d in downs]
     _lib.require_gpu(*xs, *downs, *ups, *outs, name="lora_multi")
-    ws = _ws.reserve(xs[0].device, lora_workspace_bytes(ranks, min(rows, 32), D), slot="lora")
+    ws = _ws.reserve(xs[0].device, lora_workspace_bytes(ranks, rows, D), slot="lora")
     _lib.call("rwkv7mi_lora_multi", k, _lib.ptr_array(xs), _lib.ptr_array(downs), _lib.ptr_array(ups),
               _lib.ptr_array(biases), _lib.ptr_array(outs), (ctypes.c_int64 * k)(*ranks),
               (ctypes.c_int * k)(*[int(a) for a in acts_down]), (ctypes.c_int * k)(*[int(a) for a in acts_up]),
@@ -67,7 +67,7 @@ def fused_lora_decode_supported(ranks, rows: int) -> bool:
 
 def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, state, k_k, k_a, r_k,
                                        group_norm_weight, group_norm_bias, *, eps: float, out, state_out=None,
-                                       v_first=None, v_mode: int = 0, down_sums=None):
+                                       v_first=None, v_mode: int = 0, down_sums=None, down_splits: int = 1):
     """``fused_wavg_lora`` (rwkv7_hf/fused_lora.py:706) followed by
     ``fused_recurrent_output_prepare_raw`` (fused_recurrent_update.py:1089) in two
     launches: the split-K down projections, then one decode kernel in which each
@@ -77,8 +77,10 @@ def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, stat
     sigmoid/none, none/sigmoid).  Returns ``(out [B, H*N], new_state)``.
 
     ``down_sums`` (fp32, from :func:`native_quant_mm8.mm8_lnmix_multi_into` with
-    ``lora_downs``): the down projections already summed over K; ``xs`` and the
-    down launch are then skipped."""
+    ``lora_downs``, or :func:`fused_decode_norm_mix.attn_mix_lora_decode`): the
+    down projections already summed over K, or over ``down_splits`` K-chunks
+    (``[problem][split][row][rank]``); ``xs`` and the down launch are then
+    skipped."""
     k = len(xs)
     rows, D = (int(s) for s in xs[0].shape)
     ranks = [int(d.shape[0]) for d in downs]
@@ -98,9 +100,10 @@ def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, stat
     rk_arr = (ctypes.c_int64 * k)(*ranks)
     if down_sums is not None:
         if (down_sums.dtype != torch.float32 or not down_sums.is_contiguous()
-                or int(down_sums.numel()) < rows * sum(ranks)):
-            raise ValueError("fused LoRA decode: down_sums must be contiguous fp32 with rows * sum(ranks) values")
-        ws, splits = down_sums, 1
+                or int(down_splits) < 1 or int(down_sums.numel()) < int(down_splits) * rows * sum(ranks)):
+            raise ValueError("fused LoRA decode: down_sums must be contiguous fp32 with "
+                             "down_splits * rows * sum(ranks) values")
+        ws, splits = down_sums, int(down_splits)
     else:
         ws = _ws.reserve(xs[0].device, lora_workspace_bytes(ranks, rows, D), slot="lora")
         splits = 0

@@ -24,7 +24,8 @@ import torch
 
 from . import _lib
 from . import workspace as _ws
-from .fused_decode_norm_mix import fused_attn_norm_mix6_decode, fused_ffn_add_norm_mix_decode, layer_norm
+from .fused_decode_norm_mix import (attn_mix_lora_chunks, attn_mix_lora_decode, fused_attn_norm_mix6_decode,
+                                    fused_ffn_add_norm_mix_decode, layer_norm)
 from .fused_lora import (ACT_NONE, ACT_SIGMOID, ACT_TANH, dense_multi, fused_lora_decode_supported,
                          fused_wavg_lora_output_prepare_raw, lora_multi, lora_workspace_bytes)
 from .fused_output import fused_attn_output_prepare
@@ -32,8 +33,8 @@ from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
 from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_prefill_multi_into,
-                               mm8_gemm_workspace_bytes,
-                               mm8_lnmix_multi_into, mm8_matmul_multi_into, mm8t_workspace_bytes)
+                               mm8_gemm_workspace_bytes, mm8_lnmix_multi_into, mm8_matmul_multi_into,
+                               mm8t_workspace_bytes)
 from .native_quant_policy import should_quantize_linear
 from .self_chunk_rwkv7 import _run_chunk
 
@@ -677,6 +678,9 @@ class NativeRWKV7ForCausalLM:
         self.fused_lora_decode = True
         # decode: LayerNorm + token-shift mixes inside the R/K/V and FFN-key GEMVs
         self.fused_mix_decode = True
+        # decode, 2..8 rows: LN + mixes + LoRA down in one launch (off: at the
+        # 7.2B widths it measured slower than the mix kernel + the LoRA-down launch)
+        self.fused_mix_lora_decode = False
         self._replaced = 0
         self.layers = []
 
@@ -941,6 +945,8 @@ class NativeRWKV7ForCausalLM:
             "hffn": torch.empty(cfg.num_hidden_layers, B, D, device=dev, dtype=dt),
             # the decode LoRA's down projections summed over K (fused-mix route)
             "ldown": torch.empty(B * sum(ranks), device=dev, dtype=torch.float32),
+            # 2..8 rows: the fused attention-side launch's LoRA-down K-chunk sums
+            "lpart": torch.empty(4 * B * sum(ranks), device=dev, dtype=torch.float32),
         }
 
     def _mix_fusable(self, B) -> bool:
@@ -969,6 +975,8 @@ class NativeRWKV7ForCausalLM:
         B = int(tokens.shape[0])
         if bufs is None:
             bufs = self._decode_buffers(B)
+        if self._mix_lora_route(B):
+            return self._decode_mix_lora_(tokens, cache, logits, bufs)
         x = bufs["x"]
         torch.index_select(self.emb, 0, tokens, out=x)
         state, xpa, xpf, v_first = cache
@@ -1040,6 +1048,60 @@ class NativeRWKV7ForCausalLM:
             # the kernels read the shift inputs while writing this step's rows, so
             # the rows go to separate buffers and replace the cache's here
             torch._foreach_copy_(list(xpa) + list(xpf), list(bufs["hatt"].unbind(0)) + list(bufs["hffn"].unbind(0)))
+        layer_norm(x, self.norm[0], self.norm[1], eps, out=bufs["h"])
+        self.lm_head.apply(bufs["h"], logits)
+        return logits
+
+    def _mix_lora_route(self, B) -> bool:
+        """2..8 fp16/bf16 rows with fusable LoRA ranks: each layer's attention
+        side starts with one launch (LN + r/k/v mixes + LoRA down, MFMA)."""
+        cfg = self.config
+        if not (2 <= B <= 8 and self.fused_lora_decode and self.fused_mix_lora_decode and not self.lora_side_stream
+                and not self._mix_fusable(B) and self.dtype in (torch.float16, torch.bfloat16)
+                and attn_mix_lora_chunks(cfg.hidden_size)):
+            return False
+        return all(fused_lora_decode_supported([int(d.shape[0]) for d in L.lora_down], B)
+                   and all(d.dtype == self.dtype for d in L.lora_down) and L.mix[0].dtype == L.ln1[0].dtype
+                   for L in self.layers)
+
+    def _decode_mix_lora_(self, tokens, cache, logits, bufs):
+        """decode_step_ for 2..8 rows: per layer one launch of
+        attn_mix_lora_decode (LayerNorm, r/k/v mixes, the LoRA down projections
+        as K-chunk sums), the R/K/V GEMV, the wkv kernel with the LoRA up
+        projections, o_proj, the FFN mix, key and value."""
+        cfg = self.config
+        B = int(tokens.shape[0])
+        N, eps = cfg.head_dim, cfg.norm_eps
+        x = bufs["x"]
+        torch.index_select(self.emb, 0, tokens, out=x)
+        state, xpa, xpf, v_first = cache
+        mixb, rkv, prep = bufs["mix"], bufs["rkv"], bufs["prep"]
+        for L in self.layers:
+            i = L.idx
+            n = len(L.lora_down)
+            xr, xw, xk, xv, xa, xg = (mixb[q] for q in range(6))
+            if L.pre is not None:
+                # the pre-normed row goes to a second buffer, then back into x
+                splits = attn_mix_lora_decode(x, xpa[i], L.ln1[0], L.ln1[1], L.mix, (xr, xk, xv), L.lora_down,
+                                              [1, 4, 5, 3][:n], bufs["lpart"], h_out=bufs["hatt"][i],
+                                              x_out=bufs["h"], pre_norm_weight=L.pre[0], pre_norm_bias=L.pre[1],
+                                              eps=eps)
+                x.copy_(bufs["h"])
+            else:
+                splits = attn_mix_lora_decode(x, xpa[i], L.ln1[0], L.ln1[1], L.mix, (xr, xk, xv), L.lora_down,
+                                              [1, 4, 5, 3][:n], bufs["lpart"], h_out=bufs["hatt"][i], eps=eps)
+            QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
+            fused_wavg_lora_output_prepare_raw(
+                rkv[0], rkv[1], rkv[2], [xw, xa, xg, xv][:n], L.lora_down, L.lora_up, L.lora_bias, state[i],
+                L.k_k, L.k_a, L.r_k, L.gn[0], L.gn[1], eps=N * 1e-5, out=prep, state_out=state[i],
+                v_first=v_first, v_mode=1 if i == 0 else 2, down_sums=bufs["lpart"], down_splits=splits)
+            L.o_proj.apply(prep, x, residual=x)
+            fused_ffn_add_norm_mix_decode(x, None, xpf[i], L.ln2[0], L.ln2[1], L.fx_k, eps=eps, mixed=bufs["fk"])
+            L.key.apply(bufs["fk"], bufs["kf"], act=3)
+            L.value.apply(bufs["kf"], x, residual=x)
+        # the fused launch reads the shift rows while writing this step's, so
+        # they go to a separate buffer and replace the cache's here
+        torch._foreach_copy_(list(xpa), list(bufs["hatt"].unbind(0)))
         layer_norm(x, self.norm[0], self.norm[1], eps, out=bufs["h"])
         self.lm_head.apply(bufs["h"], logits)
         return logits

@@ -391,6 +391,29 @@ int rwkv7mi_mm4_dequant(const uint8_t* packed, const void* mx, const void* rx_s,
                         const void* my, const void* ry_s, void* out, int64_t I,
                         int64_t O, int meta_dtype, int out_dtype, void* stream);
 
+/* Decode attention-side entry for 1..8 rows, fp16 / bf16: layer 0's
+ * pre-norm (pre_w / pre_b; the normalised row goes to x_out), h = LayerNorm
+ * (h_out), the r / k / v mixed rows of mixes {r, w, k, v, a, g} (outs[3]),
+ * and the LoRA down projections of up to four problems as K-chunk partial
+ * sums part[q][c][row][j] = sum over chunk c of mix_{lora_mix[q]}(h) . W_q[j]
+ * (W_q [rank_q, D] in the activation dtype; problem q starts at float
+ * offset sum_{q'<q} chunks*rows*rank_q'), which the fused wkv decode kernel
+ * takes with lora_splits = chunks -- fused_attn_norm_mix6_decode
+ * (rwkv7_hf/fused_decode_norm_mix.py:161-293) plus the down half of
+ * fused_wavg_lora (rwkv7_hf/fused_lora.py:706).  D a multiple of 128, at
+ * most 4096; outputs must not alias x or prev. */
+int rwkv7mi_attn_mix_lora(const void* x, void* x_out, const void* prev,
+                          void* h_out, const void* ln_w, const void* ln_b,
+                          const void* pre_w, const void* pre_b,
+                          const void* const* mixes, void* const* outs,
+                          int64_t nlora, const void* const* lora_w,
+                          const int64_t* ranks, const int* lora_mix,
+                          float* part, int64_t rows, int64_t D, float eps,
+                          int act_dtype, int param_dtype, void* stream);
+
+/* K-chunks rwkv7mi_attn_mix_lora splits width D into (0: D unsupported). */
+int rwkv7mi_attn_mix_lora_chunks(int64_t D);
+
 /* ------------------------------------------------------------ state slots */
 
 /* Row copies between layer-major state pools and dense batches (the serving

@@ -16,20 +16,20 @@ pytestmark = pytest.mark.gpu
 LOGIT_REL = 2e-2
 
 
-def _cfg(mm8: bool, layers=2):
+def _cfg(mm8: bool, layers=2, D=128, F=256):
     from rwkv7mi.model import NativeRWKV7Config
 
-    return NativeRWKV7Config(vocab_size=512, hidden_size=128, num_hidden_layers=layers, intermediate_size=256,
+    return NativeRWKV7Config(vocab_size=512, hidden_size=D, num_hidden_layers=layers, intermediate_size=F,
                              decay_low_rank_dim=32, a_low_rank_dim=32, gate_low_rank_dim=64, v_low_rank_dim=32,
                              use_native_mm8=mm8, native_mm8_min_params=0)
 
 
-def _build(mm8: bool, layers=2, seed=0):
+def _build(mm8: bool, layers=2, seed=0, D=128, F=256):
     from oracle.model_oracle import ModelOracle
     from oracle import oracle as o
     from rwkv7mi.model import NativeRWKV7ForCausalLM, QuantLinear, random_weights
 
-    cfg = _cfg(mm8, layers)
+    cfg = _cfg(mm8, layers, D, F)
     w = random_weights(cfg, seed=seed, device="cpu", dtype=torch.float16)
     model = NativeRWKV7ForCausalLM(cfg, w, device="cuda", dtype=torch.float16)
     override = {}
@@ -126,6 +126,48 @@ def test_decode_fused_mix_equals_unfused(B):
         assert (a.float() - b.float()).abs().max().item() <= 5e-3 * scale, step
         for x1, x2 in zip(c1._xpa + c1._xpf, c2._xpa + c2._xpf):
             assert (x1.float() - x2.float()).abs().max().item() <= 1e-2 * max(x2.float().abs().max().item(), 1.0)
+
+
+@pytest.mark.parametrize("B,D,F,mm8", [(3, 128, 256, True), (8, 1024, 4096, True), (5, 256, 1024, True),
+                                       (2, 512, 1024, False)])
+def test_decode_mix_lora_route(B, D, F, mm8):
+    """Two to eight rows: each layer's LN + mixes + LoRA down in one launch
+    against the separate kernels and against the fp64 oracle, then the
+    graph-captured step against the eager one."""
+    cfg, model, ref = _build(mm8, layers=3, D=D, F=F)
+    model.fused_mix_lora_decode = True
+    assert model._mix_lora_route(B)
+    rng = np.random.default_rng(11 + B)
+    ids = rng.integers(0, cfg.vocab_size, (B, 6))
+    _, st = ref.run(ids)
+    c1 = model(torch.tensor(ids, device="cuda")).past_key_values
+    c2 = c1.clone()
+    for step in range(3):
+        nxt = rng.integers(0, cfg.vocab_size, (B,))
+        tok = torch.tensor(nxt[:, None], device="cuda")
+        r = ref.step(nxt, st)
+        model.fused_mix_lora_decode = True
+        a = model(tok, past_key_values=c1, use_graph=False).logits
+        model.fused_mix_lora_decode = False
+        b = model(tok, past_key_values=c2, use_graph=False).logits
+        model.fused_mix_lora_decode = True
+        torch.cuda.synchronize()
+        _close(a[:, -1], r)
+        scale = b.float().abs().max().item()
+        assert (a.float() - b.float()).abs().max().item() <= 5e-3 * scale, step
+        for x1, x2 in zip(c1._xpa + c1._xpf, c2._xpa + c2._xpf):
+            assert (x1.float() - x2.float()).abs().max().item() <= 1e-2 * max(x2.float().abs().max().item(), 1.0)
+    # the graph-captured step replays the same route bit for bit
+    c3 = c1.clone()
+    runner = model.graph_runner(B)
+    tok = torch.tensor(rng.integers(0, cfg.vocab_size, (B,)), device="cuda")
+    eager = model(tok[:, None], past_key_values=c1, use_graph=False).logits
+    for rep in range(2):
+        c4 = c3.clone()
+        lg = runner.replay(tok, c4).clone()
+        _ = torch.randn(64, device="cuda").sum()
+        torch.cuda.synchronize()
+        assert torch.equal(lg, eager[:, -1]), rep
 
 
 def test_generate_greedy_matches_oracle():

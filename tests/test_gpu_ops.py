@@ -46,6 +46,62 @@ def test_attn_norm_mix6(oracle, rows, D, pre):
     _ok(prev, h)
 
 
+@pytest.mark.parametrize("rows,D,pre,dt", [(3, 4096, False, torch.float16), (8, 1024, False, torch.float16),
+                                         (5, 768, True, torch.float16), (8, 2560, False, torch.bfloat16),
+                                         (2, 4096, True, torch.bfloat16), (1, 128, False, torch.float16)])
+def test_attn_mix_lora(oracle, rows, D, pre, dt):
+    """The fused decode attention-side launch against its parts: the pre-norm,
+    LN + r/k/v mixes (the fp64 oracle, as test_attn_norm_mix6) and the LoRA
+    down projections of the rounded w/a/g/v mixes per K-chunk (fp32 torch on
+    the kernel's own h; bound 2e-3 of the row's |m| . |W| sum)."""
+    from rwkv7mi.fused_decode_norm_mix import attn_mix_lora_chunks, attn_mix_lora_decode
+
+    rng = np.random.default_rng(D + rows)
+    x = _t(rng.standard_normal((rows, D)), dt)
+    prev = _t(rng.standard_normal((rows, D)), dt)
+    w, b = _t(1 + 0.1 * rng.standard_normal(D), dt), _t(0.1 * rng.standard_normal(D), dt)
+    mixes = [_t(rng.random(D), dt) for _ in range(6)]
+    pw, pb = (_t(1 + 0.1 * rng.standard_normal(D), dt), _t(0.1 * rng.standard_normal(D), dt)) if pre else (None, None)
+    ranks = [64, 64, 128, 32] if D >= 2048 else [16, 40, 48, 8]
+    downs = [_t(rng.standard_normal((r, D)) / np.sqrt(D), dt) for r in ranks]
+    lmix = [1, 4, 5, 3]
+    x0 = x.clone()
+    outs = [torch.full((rows, D), float("nan"), device="cuda", dtype=dt) for _ in range(3)]
+    h_out = torch.empty_like(x)
+    x_out = torch.empty_like(x) if pre else None
+    C = attn_mix_lora_chunks(D)
+    assert C >= 1
+    part = torch.full((C * rows * sum(ranks) + 5,), float("nan"), device="cuda", dtype=torch.float32)
+    got_c = attn_mix_lora_decode(x, prev, w, b, mixes, outs, downs, lmix, part, h_out=h_out, x_out=x_out,
+                                 pre_norm_weight=pw, pre_norm_bias=pb)
+    torch.cuda.synchronize()
+    assert got_c == C
+    assert torch.equal(x, x0), "x is read only"
+    x_np = _f(x)
+    if pre:
+        x_np = oracle.layer_norm(x_np, _f(pw), _f(pb))
+        _ok(x_out, x_np)
+        x_np = _f(x_out)
+    ref, h = oracle.attn_norm_mix6(x_np, _f(prev), _f(w), _f(b), [_f(m) for m in mixes])
+    for got, r in zip(outs, (ref[0], ref[2], ref[3])):
+        _ok(got, r)
+    _ok(h_out, h)
+    # LoRA down of the kernel's own rounded h: mixes from h_out, rounded to dt
+    hf, pf = h_out.float(), prev.float()
+    kc = D // C
+    off = 0
+    for q, (r, W) in enumerate(zip(ranks, downs)):
+        mk = (hf + (pf - hf) * mixes[lmix[q]].float()).to(dt).float()
+        got = part[off:off + C * rows * r].view(C, rows, r)
+        for c in range(C):
+            sl = slice(c * kc, (c + 1) * kc)
+            want = mk[:, sl] @ W.float()[:, sl].t()
+            bound = (mk[:, sl].abs() @ W.float()[:, sl].abs().t()) * 2e-3 + 1e-6
+            assert ((got[c] - want).abs() <= bound).all(), (q, c, (got[c] - want).abs().max().item())
+        off += C * rows * r
+    assert torch.isnan(part[off:]).all(), "nothing past the sums is written"
+
+
 def test_ffn_add_norm_mix(oracle):
     from rwkv7mi.fused_decode_norm_mix import fused_ffn_add_norm_mix_decode
 
@@ -84,7 +140,8 @@ def test_sequence_shift_mix(oracle, B, T, D):
 
 
 # rows above 256 take the fused many-row kernel (prefills)
-@pytest.mark.parametrize("rows,D", [(1, 4096), (8, 2048), (40, 768), (300, 256), (257, 512), (1000, 4096)])
+@pytest.mark.parametrize("rows,D", [(1, 4096), (8, 2048), (40, 768), (64, 4096), (100, 2048), (300, 256),
+                                    (257, 512), (1000, 4096)])
 def test_wavg_lora(oracle, rows, D):
     from rwkv7mi.fused_lora import fused_wavg_lora
 
@@ -105,7 +162,7 @@ def test_wavg_lora(oracle, rows, D):
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("rows,D", [(2, 1024), (33, 200), (300, 200)])
+@pytest.mark.parametrize("rows,D", [(2, 1024), (33, 200), (64, 200), (300, 200)])
 def test_wag_lora_dtypes(oracle, dt, rows, D):
     from rwkv7mi.fused_lora import fused_wag_lora
 
@@ -125,6 +182,28 @@ def test_wag_lora_dtypes(oracle, dt, rows, D):
         mid = rnd(acts[q](_f(xs[q]) @ _f(downs[q]).T))
         ref = mid @ _f(ups[q]).T + (0 if biases[q] is None else _f(biases[q]))
         _ok(got[q], ref, tol=1e-2 if dt == torch.bfloat16 else 1e-4)
+
+
+@pytest.mark.parametrize("rows", [20, 70])
+def test_lora_rank_above_128(oracle, rows):
+    """Ranks above 128 take 32-row launch pairs (64-row pairs hold ranks up to 128)."""
+    from rwkv7mi.fused_lora import fused_wag_lora
+
+    rng = np.random.default_rng(rows)
+    D, A = 512, 256
+    xs = [_t(rng.standard_normal((rows, D))) for _ in range(3)]
+    ranks = (32, 160, 256)
+    downs = [_t(rng.standard_normal((r, D)) * 0.02) for r in ranks]
+    ups = [_t(rng.standard_normal((A, r)) * 0.1) for r in ranks]
+    biases = [None, _t(rng.standard_normal(A) * 0.01), None]
+    got = fused_wag_lora(*xs, *downs, *ups, *biases)
+    torch.cuda.synchronize()
+    rnd = lambda a: _f(torch.tensor(a, dtype=torch.float16))
+    acts = (np.tanh, lambda v: v, lambda v: 1 / (1 + np.exp(-v)))
+    for q in range(3):
+        mid = rnd(acts[q](_f(xs[q]) @ _f(downs[q]).T))
+        ref = mid @ _f(ups[q]).T + (0 if biases[q] is None else _f(biases[q]))
+        _ok(got[q], ref)
 
 
 def test_output_prepare_and_state_prep(oracle):
