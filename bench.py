@@ -558,6 +558,13 @@ def summarize_traffic(fetch_csv, write_csv, out=TRAFFIC_JSON, kernel="mm8t_kerne
            "fetch_scale": ff, "write_scale": fw, "copy_bytes": COPY_BYTES,
            "source": f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs ({Path(fetch_csv).parent.name}, "
                      f"{Path(write_csv).parent.name})"}
+    try:  # the kernels' source revision, when summarised inside the git checkout
+        import subprocess
+
+        res["kernels_at_commit"] = subprocess.run(["git", "rev-parse", "--short", "HEAD"], cwd=ROOT, check=True,
+                                                  capture_output=True, text=True).stdout.strip()
+    except (OSError, subprocess.CalledProcessError):
+        pass
     Path(out).parent.mkdir(parents=True, exist_ok=True)
     Path(out).write_text(json.dumps(res, indent=1) + "\n")
     print(json.dumps(res))
