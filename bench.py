@@ -265,6 +265,7 @@ def build_7p2b():
 
 def run_decode(model, cfg, quantized, batches=(1, 8, 64), steps=64, warmup=5):
     import torch
+    from rwkv7mi import argmax_rows
     from rwkv7mi.model import parameter_shapes
 
     shapes = parameter_shapes(cfg)
@@ -276,11 +277,12 @@ def run_decode(model, cfg, quantized, batches=(1, 8, 64), steps=64, warmup=5):
         out = model(prompt)
         cache = out.past_key_values
         runner = model.graph_runner(B)
-        state = {"tok": out.logits[:, -1].argmax(-1)}
+        # the graph ends with the greedy tokens (argmax of the logits), which it
+        # feeds to its own next replay: a timed step is one whole greedy step
+        runner.replay_greedy(cache, argmax_rows(out.logits[:, -1]))
 
         def step():
-            lg = runner.replay(state["tok"], cache)
-            state["tok"] = lg.argmax(-1)
+            runner.replay_greedy(cache)
 
         ms, wall = time_events(step, steps, warmup)
         nbytes = decode_step_bytes(cfg, B, quantized, shapes)

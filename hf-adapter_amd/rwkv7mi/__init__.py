@@ -20,6 +20,7 @@ from .self_chunk_rwkv7 import dplr_chunk_scan, self_chunk_rwkv7
 from .native_quant_mm8 import MM8Linear, mm8_matmul, mm8_matmul_triton, quantize_mm8, quantize_model_mm8
 from .native_quant_mm4 import MM4Linear, dequantize_mm4, mm4_matmul, quantize_mm4, quantize_model_mm4
 from .sm70_quant import quantize_w4_groupwise, w4_groupwise_linear
+from .sampling import argmax_rows
 from . import ops as _ops
 
 _ops.register()  # torch.ops.rwkv7mi.*
@@ -46,4 +47,5 @@ __all__ = [
     "quantize_model_mm4",
     "quantize_w4_groupwise",
     "w4_groupwise_linear",
+    "argmax_rows",
 ]

@@ -32,6 +32,7 @@ from .fused_output import fused_attn_output_prepare
 from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
+from .sampling import argmax_rows
 from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_prefill_multi_into,
                                mm8_gemm_workspace_bytes, mm8_lnmix_multi_into, mm8_matmul_multi_into,
                                mm8t_workspace_bytes)
@@ -1307,15 +1308,15 @@ class NativeRWKV7ForCausalLM:
         B = int(input_ids.shape[0])
         out0 = self.forward(input_ids)
         logits, cache = out0.logits, out0.past_key_values
-        nxt = logits[:, -1].float().argmax(-1)
+        nxt = argmax_rows(logits[:, -1])
         out = [input_ids, nxt[:, None]]
         runner = self.graph_runner(B) if use_graph else None
-        for _ in range(max_new_tokens - 1):
+        for t in range(max_new_tokens - 1):
             if runner is not None:
-                lg = runner.replay(nxt, cache)
+                nxt = runner.replay_greedy(cache, nxt if t == 0 else None).clone()
             else:
                 lg = self.forward(nxt[:, None], past_key_values=cache, use_graph=False).logits[:, -1]
-            nxt = lg.float().argmax(-1)
+                nxt = argmax_rows(lg)
             out.append(nxt[:, None])
         return torch.cat(out, 1)
 
@@ -1341,7 +1342,10 @@ class NativeGraphRunner:
 
     The runner owns static cache tensors; ``replay`` copies a foreign cache in
     once, then binds it (the cache's tensors become the runner's buffers) so
-    later steps run with no copies.
+    later steps run with no copies.  The graph ends with the greedy token of
+    every row (``argmax_rows``), written both to ``next_tokens`` and to the
+    graph's own input buffer, so :meth:`replay_greedy` runs a greedy step with
+    no launch besides the graph.
     """
 
     def __init__(self, model: NativeRWKV7ForCausalLM, batch: int, *, warmup: int = 2):
@@ -1352,19 +1356,25 @@ class NativeGraphRunner:
         self.cache = model.new_cache(self.batch)
         self.tokens = torch.zeros(self.batch, dtype=torch.long, device=dev)
         self.logits = torch.empty(self.batch, model.config.vocab_size, device=dev, dtype=model.dtype)
+        self.next_tokens = torch.zeros(self.batch, dtype=torch.long, device=dev)
         self.bufs = model._decode_buffers(self.batch)
         snapshot = self.cache.clone()
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
             for _ in range(warmup):
-                model.decode_step_(self.tokens, self.cache, self.logits, self.bufs)
+                self._step()
         torch.cuda.current_stream(dev).wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            model.decode_step_(self.tokens, self.cache, self.logits, self.bufs)
+            self._step()
         self._copy_into(snapshot)
         self.replays = 0
+
+    def _step(self) -> None:
+        """The captured work: one decode step, then the greedy tokens."""
+        self.model.decode_step_(self.tokens, self.cache, self.logits, self.bufs)
+        argmax_rows(self.logits, out=self.next_tokens, out2=self.tokens)
 
     def _copy_into(self, cache: NativeRWKV7Cache) -> None:
         s, a, f, v = self.cache
@@ -1400,6 +1410,24 @@ class NativeGraphRunner:
         self.replays += 1
         cache.seen_tokens = cache.seen_tokens + 1
         return self.logits
+
+    def replay_greedy(self, cache: NativeRWKV7Cache, tokens: torch.Tensor | None = None) -> torch.Tensor:
+        """One greedy step: feed ``tokens`` (default: the previous replay's greedy
+        tokens, already in the graph's input buffer) and return the next greedy
+        tokens ``[B]``, the runner's ``next_tokens`` buffer (clone it to keep
+        it past the next replay).  ``self.logits`` holds the step's logits."""
+        if tokens is not None:
+            return self._greedy_from(tokens, cache)
+        if not cache._native_graph_bound_to(self):
+            raise ValueError("replay_greedy without tokens continues a cache bound to this runner")
+        self.graph.replay()
+        self.replays += 1
+        cache.seen_tokens = cache.seen_tokens + 1
+        return self.next_tokens
+
+    def _greedy_from(self, tokens: torch.Tensor, cache: NativeRWKV7Cache) -> torch.Tensor:
+        self.replay(tokens, cache)
+        return self.next_tokens
 
 
 class NativePrefillGraphRunner:

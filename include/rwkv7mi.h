@@ -433,6 +433,18 @@ int rwkv7mi_slot_copy(const void* src, int64_t src_layer_stride,
                       int64_t nrows, int64_t row_bytes, int64_t nlayers,
                       void* stream);
 
+/* ------------------------------------------------------- greedy selection */
+
+/* out[r] = argmax of row r of x [rows, n] (row stride ld elements, act dtype),
+ * as the reference's greedy decode loop takes it with torch
+ * (`out.logits[:, -1:].argmax(dim=-1)`, bench/bench_native_quant_e2e_decode.py:
+ * 424-437): ties go to the smaller index and NaN beats every number.  out2,
+ * when not NULL, receives the same indices (the decode graph writes its next
+ * input tokens and the caller's copy in one launch).  x 16-byte aligned,
+ * ld * element size a multiple of 16. */
+int rwkv7mi_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t ld,
+                        int dtype, int64_t* out, int64_t* out2, void* stream);
+
 /* ------------------------------------------------------------------ LoRA */
 
 /* Bytes of workspace rwkv7mi_lora_multi needs (fp32 split-K partials). */

@@ -258,3 +258,30 @@ def test_model_matches_reference_golden(name, dtype):
             checked += 1
     print(f"{name} fp16: {checked} of {len(greedy)} teacher-forced greedy ids decided by the margins", flush=True)
     assert checked >= len(greedy) // 2
+
+
+@pytest.mark.parametrize("mm8,B", [(False, 1), (True, 3)])
+def test_graph_greedy_equals_eager_greedy(mm8, B):
+    """The decode graph ends with the greedy tokens and feeds them to its own
+    next replay: replay_greedy's tokens equal torch's argmax of the eager
+    logits step by step, and the logits and state match eager decode bit for
+    bit."""
+    cfg, model, _ = _build(mm8)
+    rng = np.random.default_rng(5)
+    ids = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 7)), device="cuda")
+    c1 = model(ids).past_key_values
+    c2 = c1.clone()
+    runner = model.graph_runner(B)
+    tok = torch.tensor(rng.integers(0, cfg.vocab_size, (B,)), device="cuda")
+    nxt = runner.replay_greedy(c2, tok).clone()
+    for step in range(4):
+        eager = model(tok[:, None], past_key_values=c1, use_graph=False).logits[:, -1]
+        torch.cuda.synchronize()
+        assert torch.equal(runner.logits, eager), step
+        assert torch.equal(nxt, eager.argmax(-1)), step
+        if step < 3:
+            tok = nxt
+            nxt = runner.replay_greedy(c2).clone()
+            _ = torch.randn(64, device="cuda").sum()  # unrelated eager work between replays
+    for a, b in zip(c1._state, c2._state):
+        assert torch.equal(a, b)

@@ -234,3 +234,29 @@ def test_output_prepare_and_state_prep(oracle):
     _ok(v_out, rv)
     _ok(w_log, rlog, 1e-5)
     _ok(w_dec, np.exp(rlog), 1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows,n", [(1, 65536), (8, 65536), (64, 65536), (3, 1000), (2, 8)])
+def test_argmax_rows_matches_torch(dtype, rows, n):
+    """rwkv7mi_argmax_rows against torch.argmax: random rows, rows with
+    planted ties (the first index must win), a row whose maximum is the last
+    element, and rows holding NaN (the first NaN wins, as in torch)."""
+    from rwkv7mi import argmax_rows
+
+    g = torch.Generator(device="cuda").manual_seed(rows * 7 + n)
+    x = torch.randn(rows, n, device="cuda", generator=g).to(dtype)
+    if rows >= 3:
+        x[0, n // 3] = x[0, 2 * n // 3] = 50.0  # a tie
+        x[1, -1] = 60.0  # the last element
+        x[2, n // 4] = float("nan")
+        x[2, n // 2] = float("nan")
+    got = argmax_rows(x)
+    out2 = torch.full((rows,), -1, device="cuda", dtype=torch.int64)
+    got2 = argmax_rows(x, out2=out2)
+    torch.cuda.synchronize()
+    ref = x.argmax(-1)
+    assert torch.equal(got, ref)
+    assert torch.equal(got2, ref) and torch.equal(out2, ref)
+    if rows >= 3:
+        assert int(got[0]) == n // 3 and int(got[1]) == n - 1 and int(got[2]) == n // 4
