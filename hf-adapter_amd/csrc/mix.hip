@@ -84,22 +84,57 @@ struct Mix6 {
   void* out[6];
 };
 
+// Split-K partials of the product that feeds this row's residual add (the
+// previous layer's FFN value at 3..16 rows): x <- round(sum_s part[s] + x),
+// the sums in split order, exactly as mm8t_split_reduce_kernel would write x.
+struct MixParts {
+  const float* part;  // part[s * stride + row * D + i], or null
+  int64_t stride;     // floats between splits
+  int S;
+};
+constexpr int MIX_MAXS = 4;
+
 template <typename TA, typename TP>
 __global__ __launch_bounds__(MIX_THREADS) void attn_norm_mix6_kernel(
     TA* x, TA* prev, const TP* __restrict__ ln_w, const TP* __restrict__ ln_b, const TP* pre_w,
-    const TP* pre_b, Mix6 m, int D, int nmix, float eps) {
+    const TP* pre_b, Mix6 m, int D, int nmix, float eps, MixParts ps) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   TA* xr = x + row * D;
   TA* pr = prev + row * D;
   float v[MIX_SLOTS][MIX_VEC], pv[MIX_SLOTS][MIX_VEC], w[MIX_SLOTS][MIX_VEC], b[MIX_SLOTS][MIX_VEC];
   float mx[6][MIX_SLOTS][MIX_VEC];
+  float ps_acc[MIX_SLOTS][MIX_VEC];
+  if (ps.part) {  // uniform: every split's row first, so they are in flight with the rest
+#pragma unroll
+    for (int s = 0; s < MIX_SLOTS; ++s)
+#pragma unroll
+      for (int e = 0; e < MIX_VEC; ++e) ps_acc[s][e] = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < MIX_MAXS; ++sp) {
+      float t[MIX_SLOTS][MIX_VEC];
+      ld_slots(ps.part + sp * ps.stride + row * D, D, t, sp < ps.S);
+#pragma unroll
+      for (int s = 0; s < MIX_SLOTS; ++s)
+#pragma unroll
+        for (int e = 0; e < MIX_VEC; ++e) ps_acc[s][e] += t[s][e];  // split order; past-the-end terms are +0
+    }
+  }
   ld_slots(xr, D, v);
   ld_slots(pr, D, pv);
   ld_slots(ln_w, D, w);
   ld_slots(ln_b, D, b);
 #pragma unroll
   for (int i = 0; i < 6; ++i) ld_slots(reinterpret_cast<const TP*>(m.mix[i]), D, mx[i], i < nmix);
+  if (ps.part) {
+#pragma unroll
+    for (int s = 0; s < MIX_SLOTS; ++s) {
+#pragma unroll
+      for (int e = 0; e < MIX_VEC; ++e) v[s][e] = ps_acc[s][e] + v[s][e];
+      round8<TA>(v[s]);  // the residual stream stays in TA
+    }
+    st_slots(xr, D, v);
+  }
   if (pre_w) {
     float pw[MIX_SLOTS][MIX_VEC], pb[MIX_SLOTS][MIX_VEC];
     ld_slots(pre_w, D, pw);
@@ -546,10 +581,10 @@ static bool mix_aligned(std::initializer_list<const void*> ps) {
 
 using namespace rwkv7mi;
 
-extern "C" int rwkv7mi_attn_norm_mix6(void* x, void* prev, const void* ln_w, const void* ln_b,
-                                      const void* pre_w, const void* pre_b, const void* const* mixes,
-                                      void* const* outs, int64_t nmix, int64_t rows, int64_t D, float eps,
-                                      int act_dtype, int param_dtype, void* stream) {
+static int attn_norm_mix6_launch(void* x, void* prev, const void* ln_w, const void* ln_b, const void* pre_w,
+                                 const void* pre_b, const void* const* mixes, void* const* outs, int64_t nmix,
+                                 int64_t rows, int64_t D, float eps, int act_dtype, int param_dtype, MixParts ps,
+                                 void* stream) {
   if (rows < 0 || D <= 0 || D > MIX_MAXD || D % 8)
     return fail(RWKV7MI_EINVAL, "attn_norm_mix6: D must be a multiple of 8 and at most 8192");
   if (nmix < 1 || nmix > 6) return fail(RWKV7MI_EINVAL, "attn_norm_mix6: nmix must be 1..6");
@@ -571,10 +606,29 @@ extern "C" int rwkv7mi_attn_norm_mix6(void* x, void* prev, const void* ln_w, con
       using TP = decltype(tp);
       hipLaunchKernelGGL((attn_norm_mix6_kernel<TA, TP>), dim3((unsigned)rows), dim3(MIX_THREADS), 0,
                          as_stream(stream), (TA*)x, (TA*)prev, (const TP*)ln_w, (const TP*)ln_b,
-                         (const TP*)pre_w, (const TP*)pre_b, m, (int)D, (int)nmix, eps);
+                         (const TP*)pre_w, (const TP*)pre_b, m, (int)D, (int)nmix, eps, ps);
       return check_launch("attn_norm_mix6_kernel");
     });
   });
+}
+
+extern "C" int rwkv7mi_attn_norm_mix6(void* x, void* prev, const void* ln_w, const void* ln_b,
+                                      const void* pre_w, const void* pre_b, const void* const* mixes,
+                                      void* const* outs, int64_t nmix, int64_t rows, int64_t D, float eps,
+                                      int act_dtype, int param_dtype, void* stream) {
+  return attn_norm_mix6_launch(x, prev, ln_w, ln_b, pre_w, pre_b, mixes, outs, nmix, rows, D, eps, act_dtype,
+                               param_dtype, MixParts{nullptr, 0, 0}, stream);
+}
+
+extern "C" int rwkv7mi_attn_norm_mix6_parts(void* x, void* prev, const void* ln_w, const void* ln_b,
+                                            const void* const* mixes, void* const* outs, int64_t nmix,
+                                            const float* part, int64_t splits, int64_t part_stride, int64_t rows,
+                                            int64_t D, float eps, int act_dtype, int param_dtype, void* stream) {
+  if (!part || splits < 1 || splits > MIX_MAXS || part_stride < rows * D || (reinterpret_cast<uintptr_t>(part) & 15) ||
+      part_stride % 4)
+    return fail(RWKV7MI_EINVAL, "attn_norm_mix6_parts: 1..4 splits of 16-byte aligned [rows, D] fp32 partials");
+  return attn_norm_mix6_launch(x, prev, ln_w, ln_b, nullptr, nullptr, mixes, outs, nmix, rows, D, eps, act_dtype,
+                               param_dtype, MixParts{part, part_stride, (int)splits}, stream);
 }
 
 // K-chunks of the fused attention-side launch for width D (0: not supported):

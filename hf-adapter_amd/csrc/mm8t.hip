@@ -834,7 +834,8 @@ static int mm8t_auto_splits(int64_t I, int KC) { return KC >= I ? 1 : (int)((I +
 
 static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I, int64_t O, int act_dtype,
                        int meta_dtype, void* stream, const char* who, int bits = 8, const Mm8tPro* pro = nullptr,
-                       void* workspace = nullptr, size_t workspace_bytes = 0, int* splits_out = nullptr) {
+                       void* workspace = nullptr, size_t workspace_bytes = 0, int* splits_out = nullptr,
+                       bool defer_reduce = false) {
   const std::string w(who);
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
   if (rows < 0 || I <= 0 || O <= 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
@@ -942,7 +943,7 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
                      : mm8t_go_csw<TA, TM, 4, 8>(grid, lds, stream, b, wpc);
     });
   });
-  if (rc != RWKV7MI_OK || S == 1) return rc;
+  if (rc != RWKV7MI_OK || S == 1 || defer_reduce) return rc;
   return dispatch_dtype(act_dtype, [&](auto ta) {
     using TA = decltype(ta);
     return dispatch_dtype(meta_dtype, [&](auto tm) {
@@ -1006,6 +1007,19 @@ extern "C" int rwkv7mi_mm8t_matmul_multi_ws(int nprob, const void* const* x, con
                     residual ? residual[i] : nullptr, y[i], epilogue[i]};
   return mm8t_launch(nprob, p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul_multi_ws", 8, nullptr,
                      workspace, workspace_bytes);
+}
+
+extern "C" int rwkv7mi_mm8t_matmul_partials(const void* x, const uint8_t* w_blk, const void* mx, const void* rx,
+                                            const void* my, const void* ry, int64_t rows, int64_t I, int64_t O,
+                                            int act_dtype, int meta_dtype, void* workspace, size_t workspace_bytes,
+                                            int* splits, void* stream) {
+  if (!splits) return fail(RWKV7MI_EINVAL, "mm8t_matmul_partials: null splits");
+  if (rwkv7mi_mm8t_matmul_workspace_bytes(1, rows, I, O) == 0)
+    return fail(RWKV7MI_EINVAL, "mm8t_matmul_partials: this shape does not split K (use rwkv7mi_mm8t_matmul)");
+  // a placeholder output: the split kernels write partials only
+  Mm8tProb p{x, nullptr, w_blk, mx, rx, my, ry, nullptr, nullptr, workspace, RWKV7MI_EPI_NONE};
+  return mm8t_launch(1, &p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul_partials", 8, nullptr, workspace,
+                     workspace_bytes, splits, true);
 }
 
 extern "C" int rwkv7mi_mm8t_lnmix_multi(int nprob, const void* x, const void* prev, const void* ln_w,

@@ -33,11 +33,14 @@ def fused_attn_norm_mix6_decode(x, previous, norm_weight, norm_bias, mix_r, mix_
                                 *, eps: float = 1e-5, num_warps: int = 4, stack_rkv: bool = False,
                                 stack_wav: bool = False, stack_rkv_wagv: bool = False,
                                 force_fallback: bool = False, pre_norm_weight=None, pre_norm_bias=None,
-                                out=None):
+                                out=None, residual_parts=None):
     """LayerNorm ``x``, update ``previous`` in place and return the six mixes (r,w,k,v,a,g).
 
     ``pre_norm_*`` (extension): layer-0 pre-norm applied to ``x`` first, written back into ``x``.
     ``out`` (extension): a ``[6, rows, D]`` buffer (order r,w,k,v,a,g) to write into.
+    ``residual_parts`` (extension): ``[S, rows, D]`` fp32 split-K partials of the
+    previous layer's FFN value (:func:`mm8_matmul_partials`, S <= 4); ``x`` first
+    becomes ``round(sum_s part[s] + x)``, written back, as the split reduce would.
     """
     x2, D = _rows(x, "x")
     p2, Dp = _rows(previous, "previous")
@@ -65,6 +68,19 @@ def fused_attn_norm_mix6_decode(x, previous, norm_weight, norm_bias, mix_r, mix_
     else:
         stacked = out.reshape(6, rows, D)
     outs = [stacked[i] for i in range(6)]
+    if residual_parts is not None:
+        if pre is not None:
+            raise ValueError("residual_parts and the pre-norm do not combine")
+        parts = residual_parts
+        if (parts.dim() != 3 or tuple(parts.shape[1:]) != (rows, D) or parts.dtype != torch.float32
+                or not parts.is_contiguous() or x2.data_ptr() != x.data_ptr()):
+            raise ValueError("residual_parts: contiguous fp32 [S, rows, D] partials and a contiguous x")
+        _lib.call("rwkv7mi_attn_norm_mix6_parts", _lib.ptr(x2), _lib.ptr(p2), _lib.ptr(params[0]),
+                  _lib.ptr(params[1]), _lib.ptr_array(mixes), _lib.ptr_array(outs), 6, _lib.ptr(parts),
+                  int(parts.shape[0]), rows * D, rows, D, float(eps), _lib.dtype_code(x2),
+                  _lib.dtype_code(params[0]), _lib.stream_of(x2))
+        shape = tuple(x.shape)
+        return tuple(o.reshape(shape) for o in outs)
     _lib.call("rwkv7mi_attn_norm_mix6", _lib.ptr(x2), _lib.ptr(p2), _lib.ptr(params[0]), _lib.ptr(params[1]),
               _lib.ptr(pre[0] if pre else None), _lib.ptr(pre[1] if pre else None), _lib.ptr_array(mixes),
               _lib.ptr_array(outs), 6, rows, D, float(eps), _lib.dtype_code(x2), _lib.dtype_code(params[0]),

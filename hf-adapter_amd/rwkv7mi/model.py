@@ -35,7 +35,7 @@ from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_sh
 from .sampling import argmax_rows
 from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_prefill_multi_into,
                                mm8_gemm_workspace_bytes, mm8_lnmix_multi_into, mm8_matmul_multi_into,
-                               mm8t_workspace_bytes)
+                               mm8_matmul_partials, mm8t_workspace_bytes)
 from .native_quant_policy import should_quantize_linear
 from .self_chunk_rwkv7 import _run_chunk
 
@@ -682,6 +682,9 @@ class NativeRWKV7ForCausalLM:
         # decode, 2..8 rows: LN + mixes + LoRA down in one launch (off: at the
         # 7.2B widths it measured slower than the mix kernel + the LoRA-down launch)
         self.fused_mix_lora_decode = False
+        # 3..16 rows: the FFN value's split-K partials are added by the next
+        # layer's norm-mix kernel instead of a reduce launch of their own
+        self.defer_value_reduce = True
         self._replaced = 0
         self.layers = []
 
@@ -986,6 +989,7 @@ class NativeRWKV7ForCausalLM:
         main = torch.cuda.current_stream(x.device)
         side, ev_in, ev_out = self._side(x.device) if self.lora_side_stream else (None, None, None)
         fmix = self._mix_fusable(B) and not self.lora_side_stream
+        parts = None  # the previous layer's FFN value partials, not yet added to x
         for L in self.layers:
             i = L.idx
             xr, xw, xk, xv, xa, xg = (mixb[q] for q in range(6))
@@ -1006,7 +1010,8 @@ class NativeRWKV7ForCausalLM:
             else:
                 fused_attn_norm_mix6_decode(x, xpa[i], L.ln1[0], L.ln1[1], *L.mix, eps=eps, out=mixb,
                                             pre_norm_weight=L.pre[0] if L.pre else None,
-                                            pre_norm_bias=L.pre[1] if L.pre else None)
+                                            pre_norm_bias=L.pre[1] if L.pre else None, residual_parts=parts)
+                parts = None
             if (self.fused_lora_decode and not self.lora_side_stream
                     and fused_lora_decode_supported([int(d.shape[0]) for d in L.lora_down], B)):
                 # LoRA down (split-K launch), then the up projections inside the wkv kernel
@@ -1044,7 +1049,10 @@ class NativeRWKV7ForCausalLM:
                 fused_ffn_add_norm_mix_decode(x, None, xpf[i], L.ln2[0], L.ln2[1], L.fx_k, eps=eps,
                                               mixed=bufs["fk"])
                 L.key.apply(bufs["fk"], bufs["kf"], act=3)
-            L.value.apply(bufs["kf"], x, residual=x)
+            if not fmix and self._value_deferrable(L, B):
+                parts, _ = mm8_matmul_partials(bufs["kf"], L.value.m)
+            else:
+                L.value.apply(bufs["kf"], x, residual=x)
         if fmix:
             # the kernels read the shift inputs while writing this step's rows, so
             # the rows go to separate buffers and replace the cache's here
@@ -1052,6 +1060,19 @@ class NativeRWKV7ForCausalLM:
         layer_norm(x, self.norm[0], self.norm[1], eps, out=bufs["h"])
         self.lm_head.apply(bufs["h"], logits)
         return logits
+
+    def _value_deferrable(self, L, B) -> bool:
+        """The FFN value's split reduce can move into the next layer's norm-mix
+        launch: a next layer without a pre-norm, a blocked bias-free MM8 value
+        that splits K at these rows into at most four ranges."""
+        if not self.defer_value_reduce or L.idx + 1 >= len(self.layers) or self.layers[L.idx + 1].pre is not None:
+            return False
+        v = L.value
+        if (not isinstance(v, QuantLinear) or not 0 < B <= QuantLinear.GEMV_ROWS or not is_blocked(v.m.w_blk)
+                or v.m.bias is not None):
+            return False
+        need = mm8t_workspace_bytes(1, B, v.in_features, v.out_features)
+        return 0 < need <= 4 * B * v.out_features * 4
 
     def _mix_lora_route(self, B) -> bool:
         """2..8 fp16/bf16 rows with fusable LoRA ranks: each layer's attention

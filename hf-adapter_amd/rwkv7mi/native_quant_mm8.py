@@ -229,6 +229,29 @@ def mm8_matmul_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
     return outs
 
 
+def mm8_matmul_partials(x2, mod):
+    """The split-K products of ``x2 [rows, N] @ mod`` left as fp32 partials for the
+    consumer to add (no reduce launch): returns ``(part [S, rows, M], S)``, a view
+    of the ``"mm8t"`` workspace slot valid until the next call that uses that
+    slot; ``out = sum_s part[s] (+ bias)`` in split order.  Only for shapes the
+    blocked GEMV splits (:func:`mm8t_workspace_bytes` > 0)."""
+    rows, n = (int(s) for s in x2.shape)
+    m = int(mod.out_features)
+    if mod.in_features != n or not is_blocked(mod.w_blk) or not x2.is_contiguous():
+        raise ValueError("mm8_matmul_partials: a contiguous x and a blocked MM8Linear of matching width")
+    need = mm8t_workspace_bytes(1, rows, n, m)
+    if not need:
+        raise ValueError("mm8_matmul_partials: this shape does not split K")
+    _lib.require_gpu(x2, name="mm8_matmul_partials")
+    ws = _ws.reserve(x2.device, need, slot="mm8t")
+    splits = ctypes.c_int(0)
+    _lib.call("rwkv7mi_mm8t_matmul_partials", _lib.ptr(x2), _lib.ptr(mod.w_blk), _lib.ptr(mod.mx), _lib.ptr(mod.rx),
+              _lib.ptr(mod.my), _lib.ptr(mod.ry), rows, n, m, _lib.dtype_code(x2), _lib.dtype_code(mod.mx),
+              _lib.ptr(ws), int(ws.numel()), ctypes.byref(splits), _lib.stream_of(x2))
+    S = int(splits.value)
+    return ws[: S * rows * m * 4].view(torch.float32).view(S, rows, m), S
+
+
 def mm8_gemm_workspace_bytes(nprob: int, rows: int, n: int, m: int, splits: int = 0) -> int:
     """Scratch bytes :func:`mm8_gemm_multi_into` needs: x' and row sums, plus the
     split-K partials when there is more than one split."""

@@ -260,6 +260,21 @@ int rwkv7mi_mm8t_matmul_multi_ws(int nprob, const void* const* x,
                                  void* workspace, size_t workspace_bytes,
                                  void* stream);
 
+/* The split-K products of rwkv7mi_mm8t_matmul_multi_ws for one problem
+ * without the second launch: the ranges' fp32 partials stay in `workspace`
+ * as part[(s * rows + row) * O + o] (s < *splits), each already carrying its
+ * range's share of the row-sum terms, so y = sum_s part[s] (+ bias) in range
+ * order.  The consumer adds them, e.g. rwkv7mi_attn_norm_mix6_parts for the
+ * FFN value's residual.  Refuses shapes that do not split.  Replaces the
+ * value projection of the decode FFN (rwkv7_hf/native_jit_graph_dispatch.py:
+ * 594-598) at 3..16 rows, where x' exceeds one LDS chunk. */
+int rwkv7mi_mm8t_matmul_partials(const void* x, const uint8_t* w_blk,
+                                 const void* mx, const void* rx, const void* my,
+                                 const void* ry, int64_t rows, int64_t I,
+                                 int64_t O, int act_dtype, int meta_dtype,
+                                 void* workspace, size_t workspace_bytes,
+                                 int* splits, void* stream);
+
 /* Many-row form of rwkv7mi_mm8t_matmul_multi for 17..256 rows (bsz-64
  * decode, short prefills): 64-row x 128-column MFMA tiles over split K, with
  * x' = x * ry rounded once to fp16 and the weights centred (w - 128) so that
@@ -524,6 +539,20 @@ int rwkv7mi_attn_norm_mix6(void* x, void* prev, const void* ln_w,
                            void* const* outs, int64_t nmix, int64_t rows,
                            int64_t D, float eps, int act_dtype,
                            int param_dtype, void* stream);
+
+/* rwkv7mi_attn_norm_mix6 (no pre-norm) that first finishes the residual add
+ * of the previous layer's split FFN value: x = round(sum_s part[s *
+ * part_stride + row * D + i] + x), the splits (1..4) added in order as the
+ * split reduce would, written back to x, then the norm and mixes as above
+ * (rwkv7_hf/native_jit_graph_dispatch.py:594-598 then
+ * fused_decode_norm_mix.py:161). part 16-byte aligned fp32. */
+int rwkv7mi_attn_norm_mix6_parts(void* x, void* prev, const void* ln_w,
+                                 const void* ln_b, const void* const* mixes,
+                                 void* const* outs, int64_t nmix,
+                                 const float* part, int64_t splits,
+                                 int64_t part_stride, int64_t rows, int64_t D,
+                                 float eps, int act_dtype, int param_dtype,
+                                 void* stream);
 
 /* x = residual (+ attn_out -> residual_out); h = LN(x);
  * mixed = h + (prev - h) * mix; prev <- h.

@@ -285,3 +285,35 @@ def test_graph_greedy_equals_eager_greedy(mm8, B):
             _ = torch.randn(64, device="cuda").sum()  # unrelated eager work between replays
     for a, b in zip(c1._state, c2._state):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("B", [3, 8])
+def test_deferred_value_reduce_equals_reduce(B):
+    """At 3..16 rows the FFN value (16384 inputs here: K splits) leaves its
+    fp32 partials for the next layer's norm-mix launch to add; logits, state
+    and shift rows equal the path with the separate split reduce bit for bit,
+    eager and graph-replayed."""
+    cfg, model, _ = _build(True, layers=3, D=256, F=16384)
+    assert model._value_deferrable(model.layers[0], B) and not model._value_deferrable(model.layers[-1], B)
+    rng = np.random.default_rng(31 + B)
+    ids = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 4)), device="cuda")
+    c1 = model(ids).past_key_values
+    c2 = c1.clone()
+    for step in range(3):
+        tok = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 1)), device="cuda")
+        model.defer_value_reduce = False
+        a = model(tok, past_key_values=c1, use_graph=False).logits
+        model.defer_value_reduce = True
+        b = model(tok, past_key_values=c2, use_graph=False).logits
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), step
+    for s1, s2 in zip(c1._state + c1._xpa + c1._xpf, c2._state + c2._xpa + c2._xpf):
+        assert torch.equal(s1, s2)
+    runner = model.graph_runner(B)
+    tok = torch.tensor(rng.integers(0, cfg.vocab_size, (B,)), device="cuda")
+    model.defer_value_reduce = False
+    ref = model(tok[:, None], past_key_values=c1, use_graph=False).logits[:, -1]
+    model.defer_value_reduce = True
+    got = runner.replay(tok, c2).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
