@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void wkv7_decode_kernel(
 // its pointers and rank are wave-uniform and it needs no barrier until the
 // four results meet for the state update.
 constexpr int DL_MAXR = 128;  // largest rank on this route
-constexpr int DL_ZB = 16;     // K-split partials loaded per batch
+constexpr int DL_ZB = 16;     // K-split partials loaded per batch (1 when the sums arrive whole)
 
 struct DecLora {
   const float* part;
@@ -205,7 +205,7 @@ __device__ __forceinline__ float dl_act(float v, int act) {
   return v;
 }
 
-template <typename TA, typename TP>
+template <typename TA, typename TP, int ZB>
 __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
     const TA* __restrict__ r, const TA* __restrict__ k, const TA* __restrict__ v, const DecLora LA,
     const float* state_in, float* state_out, const TP* __restrict__ k_k, const TP* __restrict__ k_a,
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
   const int rp = active ? LA.rank[wave] : 0;
   // the LoRA down partials first: the up projections wait on them, the state
   // only at the update (loads complete in issue order)
-  float pt0[2][DL_ZB];
+  float pt0[2][ZB];
   {
     const __amdgpu_buffer_rsrc_t pr = make_rsrc(LA.part, (uint32_t)LA.part_total * 4u);
     const uint32_t zs = (uint32_t)(LA.rows * rp);
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int zz = 0; zz < DL_ZB; ++zz) {
+      for (int zz = 0; zz < ZB; ++zz) {
         const bool ok = lane + 64 * u < rp && zz < LA.ks;
         pt0[u][zz] = buf_ldf(pr, ok ? (base + (uint32_t)zz * zs + lane + 64u * u) * 4u : BUF_OOB);
       }
@@ -267,26 +267,33 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
   // rather than where they are used (each would add a memory round trip there)
   const float vf_pre = buf_ld1<TA>(make_rsrc(v_first ? v_first + vec : nullptr, v_first ? HEAD * (uint32_t)sizeof(TA) : 0u),
                                    (uint32_t)lane, v_mode == 2);
+  // Up projection of this wave's problem, loaded coalesced: a row of Wu_p
+  // (rank elements) is spread over L lanes, 8 elements each (L = rank / 8
+  // rounded up to a power of two), so load i reads the 64 / L consecutive
+  // rows i * 64 / L .. of the head as one contiguous run.  The lane's row
+  // segments are dotted with its 8 mid values and the L lanes of a row then
+  // reduce-scatter, which leaves channel c = lq * (64 / L) + lr in lane
+  // (lr, lq), lane = lr * L + lq.
+  const int r8 = rp >> 3;
+  const int L = r8 <= 1 ? 1 : r8 <= 2 ? 2 : r8 <= 4 ? 4 : r8 <= 8 ? 8 : 16;  // wave-uniform
+  const int lq = lane & (L - 1), lr = lane / L, rpi = HEAD / L;
+  const int cu = lq * rpi + lr;  // the channel this lane finishes
   const void* bu_w = active ? LA.bu[wave] : nullptr;
   const float bias_pre = buf_ld1<TA>(
       make_rsrc(bu_w ? reinterpret_cast<const TA*>(bu_w) + (int64_t)h * HEAD : nullptr, bu_w ? HEAD * (uint32_t)sizeof(TA) : 0u),
-      (uint32_t)lane, bu_w != nullptr);
-  // up-projection row h*64 + lane of Wu_p: rank elements in 8-element chunks
-  float wrow[DL_MAXR];
+      (uint32_t)cu, bu_w != nullptr);
+  float wseg[DL_MAXR / 8][8];
   {
     const __amdgpu_buffer_rsrc_t wr =
         make_rsrc(active ? LA.wu[wave] : LA.wu[0], (uint32_t)((int64_t)H * HEAD * rp * (int64_t)sizeof(TA)));
-    const uint32_t e0 = (uint32_t)((int64_t)(h * HEAD + lane) * rp);
 #pragma unroll
-    for (int e = 0; e < DL_MAXR; e += 8) {
-      float f[8];
-      buf_ld8(wr, e0 + e, e < rp, (const TA*)nullptr, f);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) wrow[e + u] = f[u];
+    for (int i = 0; i < DL_MAXR / 8; ++i) {
+      const uint32_t e0 = (uint32_t)((int64_t)(h * HEAD + i * rpi + lr) * rp + 8 * lq);
+      buf_ld8(wr, e0, i < L && lq < r8, (const TA*)nullptr, wseg[i]);
     }
   }
   // mid_p[kk] for kk = lane, lane + 64: the rest of the K-split partials (the
-  // first DL_ZB splits are in flight since the kernel's start), summed in z order
+  // first ZB splits are in flight since the kernel's start), summed in z order
   {
     const __amdgpu_buffer_rsrc_t pr = make_rsrc(LA.part, (uint32_t)LA.part_total * 4u);
     const uint32_t zs = (uint32_t)(LA.rows * rp);
@@ -295,39 +302,56 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int zz = 0; zz < DL_ZB; ++zz) acc[u] += pt0[u][zz];  // past-the-end terms are +0
-    for (int z0 = DL_ZB; z0 < LA.ks; z0 += DL_ZB) {
-      float t[2][DL_ZB];
+      for (int zz = 0; zz < ZB; ++zz) acc[u] += pt0[u][zz];  // past-the-end terms are +0
+    for (int z0 = ZB; z0 < LA.ks; z0 += ZB) {
+      float t[2][ZB];
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int zz = 0; zz < DL_ZB; ++zz) {
+        for (int zz = 0; zz < ZB; ++zz) {
           const bool ok = lane + 64 * u < rp && z0 + zz < LA.ks;
           t[u][zz] = buf_ldf(pr, ok ? (base + (uint32_t)(z0 + zz) * zs + lane + 64u * u) * 4u : BUF_OOB);
         }
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int zz = 0; zz < DL_ZB; ++zz) acc[u] += t[u][zz];
+        for (int zz = 0; zz < ZB; ++zz) acc[u] += t[u][zz];
     }
     // every entry of the wave's row is written (zeros past the rank), so the
-    // up-projection dot below runs unconditionally over DL_MAXR
+    // up projection's segments past the rank read zeros
     const int ad = active ? LA.act_d[wave] : 0;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
       s_mid[wave][lane + 64 * u] = lane + 64 * u < rp ? to_f32(from_f32<TA>(dl_act(acc[u], ad))) : 0.f;
   }
-  // this wave's problem, channel `lane` (the wave reads its own s_mid row: LDS
-  // operations of one wave complete in order, so no barrier is needed)
+  // this wave's problem (the wave reads its own s_mid row: LDS operations of
+  // one wave complete in order, so no barrier is needed)
   if (active) {
-    float acc = 0.f;
+    const float4 m0 = *reinterpret_cast<const float4*>(&s_mid[wave][8 * lq]);
+    const float4 m1 = *reinterpret_cast<const float4*>(&s_mid[wave][8 * lq + 4]);
+    float pt[DL_MAXR / 8];
 #pragma unroll
-    for (int e = 0; e < DL_MAXR; e += 4) {
-      const float4 m4 = *reinterpret_cast<const float4*>(&s_mid[wave][e]);  // broadcast
-      acc += m4.x * wrow[e] + m4.y * wrow[e + 1] + m4.z * wrow[e + 2] + m4.w * wrow[e + 3];
+    for (int i = 0; i < DL_MAXR / 8; ++i)
+      pt[i] = ((m0.x * wseg[i][0] + m0.y * wseg[i][1]) + (m0.z * wseg[i][2] + m0.w * wseg[i][3])) +
+              ((m1.x * wseg[i][4] + m1.y * wseg[i][5]) + (m1.z * wseg[i][6] + m1.w * wseg[i][7]));
+    // reduce-scatter over the row's L lanes: at distance d the lane with bit d
+    // of lq set keeps the upper half of its window; pt[0] ends as the total of
+    // load lq's row (loads past L read zeros)
+#pragma unroll
+    for (int d = DL_MAXR / 16; d >= 1; d >>= 1) {
+      if (d < L) {
+        const bool up = (lq & d) != 0;
+#pragma unroll
+        for (int j = 0; j < d; ++j) {
+          const float keep = up ? pt[j + d] : pt[j];
+          const float give = up ? pt[j] : pt[j + d];
+          pt[j] = keep + __shfl_xor(give, d, 64);
+        }
+      }
     }
+    float acc = pt[0];
     if (bu_w) acc += bias_pre;
-    s_lo[wave][lane] = to_f32(from_f32<TA>(dl_act(acc, LA.act_u[wave])));
+    s_lo[wave][cu] = to_f32(from_f32<TA>(dl_act(acc, LA.act_u[wave])));
   }
   __syncthreads();
 
@@ -473,10 +497,17 @@ extern "C" int rwkv7mi_wkv7_decode_lora_output_prepare(
     using TA = decltype(ta);
     return dispatch_dtype(param_dtype, [&](auto tp) {
       using TP = decltype(tp);
-      hipLaunchKernelGGL((wkv7_decode_lora_kernel<TA, TP>), dim3((unsigned)(B * H)), dim3(256), 0,
-                         as_stream(stream), (const TA*)r, (const TA*)k_raw, (const TA*)v, la, state_in, state_out,
-                         (const TP*)k_k, (const TP*)k_a, (const TP*)r_k, (const TP*)gn_w, (const TP*)gn_b,
-                         (TA*)out, (TA*)v_first, v_mode, (int)H, eps);
+      // sums that arrive whole (one split) need one partial load per lane, not a batch
+      if (la.ks == 1)
+        hipLaunchKernelGGL((wkv7_decode_lora_kernel<TA, TP, 1>), dim3((unsigned)(B * H)), dim3(256), 0,
+                           as_stream(stream), (const TA*)r, (const TA*)k_raw, (const TA*)v, la, state_in, state_out,
+                           (const TP*)k_k, (const TP*)k_a, (const TP*)r_k, (const TP*)gn_w, (const TP*)gn_b,
+                           (TA*)out, (TA*)v_first, v_mode, (int)H, eps);
+      else
+        hipLaunchKernelGGL((wkv7_decode_lora_kernel<TA, TP, DL_ZB>), dim3((unsigned)(B * H)), dim3(256), 0,
+                           as_stream(stream), (const TA*)r, (const TA*)k_raw, (const TA*)v, la, state_in, state_out,
+                           (const TP*)k_k, (const TP*)k_a, (const TP*)r_k, (const TP*)gn_w, (const TP*)gn_b,
+                           (TA*)out, (TA*)v_first, v_mode, (int)H, eps);
       return check_launch("wkv7_decode_lora_kernel");
     });
   });
