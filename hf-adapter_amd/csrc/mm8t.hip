@@ -914,13 +914,21 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
     if (lds > (size_t)MM8T_LDS_X_ONE) return fail(RWKV7MI_EINVAL, w + ": the LoRA inputs do not fit in LDS");
   }
   // With x' in one LDS chunk, workgroups loop over column groups: as many as
-  // stay resident (less the prologue's own), split between the problems and
-  // row tiles.
+  // stay resident, split between the problems and row tiles, and then as few
+  // as give every workgroup the same number of groups (a launch lasts as long
+  // as its busiest workgroup).  At two workgroups per CU the prologue's own
+  // workgroups are not counted: they run as a third workgroup on a CU where
+  // the kernel's registers allow it (the LN-mix instances do), else in the
+  // first free slot (measured faster than shrinking the product grid for
+  // them).  At one per CU they take product slots.
   int64_t gx = ngroups;  // column-group workgroups per split
   if (b.KC >= I || S > 1) {
     const int64_t per_cu = nw == 4 && lds <= MM8T_LDS_X ? 2 : 1;
-    const int64_t slots = (cus * per_cu - extra) / (nprob * rtiles * S);
-    if (slots >= 1 && slots < gx) gx = slots;
+    const int64_t slots = (cus * per_cu - (per_cu == 2 ? 0 : extra)) / (nprob * rtiles * S);
+    if (slots >= 1 && slots < gx) {
+      const int64_t k = (ngroups + slots - 1) / slots;  // groups per workgroup
+      gx = (ngroups + k - 1) / k;
+    }
   }
   b.gx = (int)(gx * S);
   dim3 grid((unsigned)(b.gx + extra), (unsigned)nprob, (unsigned)rtiles);
