@@ -123,7 +123,7 @@ __device__ __forceinline__ f16x8 mm4t_b_operand(uint32_t d) {
 // BITS = 8: MM8 bytes, a step is 128 K rows; BITS = 4: MM4 nibbles packed in
 // pairs along K (low nibble = even row), a step is 256 K rows.  Either way a
 // step is two 16-byte loads per lane, 128 bytes of each of the 16 columns.
-template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO, int RING>
+template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO, int RING, bool DEF = false>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B) {
   // NW waves per workgroup; CSW: steps per wave per K-chunk (KC = RS NW CSW
   // rows).  The chunk body is fully unrolled so the load ring needs no
@@ -443,6 +443,17 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   // measured slower than the shared staging.)
   constexpr bool WSOK = BITS == 8 && sizeof(TA) == 2 && !PRO;
   const bool ws = WSOK && nrows <= 2 && nchunks == 1;
+  // DEF (instances for 3..16 rows): shared staging of one chunk in two
+  // batches: the second batch's loads go out before the products start and
+  // it is finished only at step CSW / 2, the first whose K blocks lie in its
+  // inputs (it holds inputs [KC / 2, KC); steps jl >= CSW / 2 read blocks
+  // >= NW CSW / 2 = KC / (2 RS)), so its load latency overlaps the first
+  // steps.  The issue is unconditional (all-invalid loads read zeros when
+  // nothing is deferred) so the ring's load-counter waits stay exact.  (Its
+  // registers cost one wave per SIMD of occupancy, which the one- and
+  // two-row launches keep.)
+  const bool defer = DEF && !PRO && !ws && nchunks == 1 && CSW >= 2 && QIT == 2 * SB && NQ % TPR == 0;
+  const int last0 = defer ? SB : QIT;  // first iteration of the deferred batch
   float sxw[2] = {0.f, 0.f}, smw[2] = {0.f, 0.f};
   if (ws) {
     constexpr int NRND = (CSW + 3) / 4;  // 64 lanes cover four 128-input blocks per round
@@ -516,10 +527,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
 #pragma unroll
   for (int d = 1; d < DEPTH; ++d) load_step(wr, d, buf[d]);  // DEPTH <= CSW <= J
   __builtin_amdgcn_sched_barrier(0);
-  for (int it0 = SB; it0 < QIT; it0 += SB) {
+  for (int it0 = SB; it0 < last0; it0 += SB) {
     stage_issue(0, it0);
     stage_finish(it0);
   }
+  if constexpr (DEF) stage_issue(0, last0);
   __syncthreads();
   }
 
@@ -554,6 +566,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
 #pragma unroll
       for (int jl = 0; jl < CSW; ++jl) {
         const int d = jl % DEPTH;
+        if constexpr (DEF) {
+          if (jl == CSW / 2 && first && defer) {  // the deferred staging batch
+            stage_finish(last0);
+            __syncthreads();
+          }
+        }
         // convert this step's bytes first, then refill the same ring slot: the
         // slot is dead once converted, so it keeps its registers
         f16x8 bv[NB];
@@ -746,41 +764,55 @@ static size_t mm8t_lds(int64_t rows, int KC) {
 
 using namespace rwkv7mi;
 
-template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO, int RING>
+template <typename TA, typename TM, int NW, int CSW, int BITS, bool PRO, int RING, bool DEF>
 static int mm8t_go(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
   static std::atomic<uint64_t> lds_raised{0};  // devices whose dynamic LDS limit is raised for this instance
-  if (int rc = raise_dynamic_lds(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, NW, CSW, BITS, PRO, RING>),
+  if (int rc = raise_dynamic_lds(reinterpret_cast<const void*>(&mm8t_kernel<TA, TM, NW, CSW, BITS, PRO, RING, DEF>),
                                  MM8T_LDS_X_ONE + 1024, lds_raised, "mm8t_kernel"))
     return rc;
-  hipLaunchKernelGGL((mm8t_kernel<TA, TM, NW, CSW, BITS, PRO, RING>), grid, dim3(64 * NW), lds, as_stream(stream), b);
+  hipLaunchKernelGGL((mm8t_kernel<TA, TM, NW, CSW, BITS, PRO, RING, DEF>), grid, dim3(64 * NW), lds, as_stream(stream),
+                     b);
   return check_launch("mm8t_kernel");
 }
 
-template <typename TA, typename TM, int NW, int BITS, bool PRO, int RING>
+template <typename TA, typename TM, int NW, int BITS, bool PRO, int RING, bool DEF = false>
 static int mm8t_go_csw_ring(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b) {
   switch (b.KC / ((BITS == 8 ? 128 : 256) * NW)) {
-    case 2: return mm8t_go<TA, TM, NW, 2, BITS, PRO, RING>(grid, lds, stream, b);
-    case 4: return mm8t_go<TA, TM, NW, 4, BITS, PRO, RING>(grid, lds, stream, b);
-    case 8: return mm8t_go<TA, TM, NW, 8, BITS, PRO, RING>(grid, lds, stream, b);
-    case 16: return mm8t_go<TA, TM, NW, 16, BITS, PRO, RING>(grid, lds, stream, b);
+    case 2: return mm8t_go<TA, TM, NW, 2, BITS, PRO, RING, DEF>(grid, lds, stream, b);
+    case 4: return mm8t_go<TA, TM, NW, 4, BITS, PRO, RING, DEF>(grid, lds, stream, b);
+    case 8: return mm8t_go<TA, TM, NW, 8, BITS, PRO, RING, DEF>(grid, lds, stream, b);
+    case 16: return mm8t_go<TA, TM, NW, 16, BITS, PRO, RING, DEF>(grid, lds, stream, b);
     default:
       // the 4-bit eight-wave kernel at 32 steps per chunk runs out of
       // registers; its chunks are capped at 16 steps
       if constexpr (BITS == 4 && NW == 8)
         return fail(RWKV7MI_EINVAL, "mm8t_kernel: chunk too long for the 4-bit eight-wave kernel");
       else
-        return mm8t_go<TA, TM, NW, 32, BITS, PRO, RING>(grid, lds, stream, b);
+        return mm8t_go<TA, TM, NW, 32, BITS, PRO, RING, DEF>(grid, lds, stream, b);
   }
 }
 
 // Ring depth: about 32 KB of weight loads in flight per CU (2 KB per wave and
 // step).  8-bit: depth 2 with eight resident waves per CU, 4 with four; the
-// 4-bit path keeps its depth of 8.
+// 4-bit path keeps its depth of 8.  Three or more rows of fp16 / bf16 take
+// the instances that defer their second staging batch (DEF).
 template <typename TA, typename TM, int NW, int BITS, bool PRO = false>
 static int mm8t_go_csw(dim3 grid, size_t lds, void* stream, const Mm8tBatch& b, int waves_per_cu) {
   if constexpr (BITS == 4) {
     return mm8t_go_csw_ring<TA, TM, NW, BITS, PRO, 8>(grid, lds, stream, b);
   } else {
+    constexpr bool DEFOK = !PRO && std::is_same<TA, TM>::value && sizeof(TA) == 2;
+    if constexpr (DEFOK) {
+      // the kernel's staging split: rp2 threads' rows, TPR threads per row,
+      // QIT 8-element groups per thread, MM8T_SB per batch; deferral needs one
+      // chunk staged in exactly two batches
+      int rp2 = 1;
+      while (rp2 < std::min(b.rows, 16)) rp2 <<= 1;
+      const int tpr = 64 * NW / rp2, nq = b.KC / 8;
+      const bool one_chunk = b.KC >= b.I || b.S > 1;
+      if (waves_per_cu >= 8 && b.rows >= 3 && one_chunk && nq % tpr == 0 && nq / tpr == 2 * MM8T_SB)
+        return mm8t_go_csw_ring<TA, TM, NW, BITS, PRO, 2, true>(grid, lds, stream, b);
+    }
     return waves_per_cu >= 8 ? mm8t_go_csw_ring<TA, TM, NW, BITS, PRO, 2>(grid, lds, stream, b)
                              : mm8t_go_csw_ring<TA, TM, NW, BITS, PRO, 4>(grid, lds, stream, b);
   }
