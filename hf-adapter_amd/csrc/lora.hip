@@ -13,128 +13,15 @@
 // up projection on v_mfma_f32_16x16x32_f16 — so the split costs no extra
 // launch and the result is deterministic.  fp32 / bf16 operands are split
 // into fp16 hi + lo as in the dense kernel.
-#include "common.h"
+#include "lora_common.h"
 
 namespace rwkv7mi {
-
-enum { LORA_ACT_NONE = 0, LORA_ACT_TANH = 1, LORA_ACT_SIGMOID = 2 };
-constexpr int LORA_MAXR = 256;   // largest rank
-constexpr int LORA_PREFILL_ROWS = 256;  // above: the fused many-row kernel (no workspace)
-
-struct LoraProb {
-  const void* x;
-  const void* wd;
-  const void* wu;
-  const void* bu;
-  void* y;
-  int r, act_d, act_u, tile_d0, tile_u0;  // tile_u0: first up workgroup (tpw output tiles each)
-  int64_t part_off;  // floats
-};
-struct LoraBatch {
-  LoraProb p[4];
-  int nprob, D, A, ks, kr;
-  int tpw;  // up kernel: output tiles of 16 columns per workgroup
-};
-
-__device__ __forceinline__ float lora_act(float v, int act) {
-  if (act == LORA_ACT_TANH) return tanhf(v);
-  if (act == LORA_ACT_SIGMOID) return 1.0f / (1.0f + expf(-v));
-  return v;
-}
-// The same with the hardware exp2 / reciprocal for the sigmoid (a few ulp of
-// fp32, far below the activation dtype's rounding that follows); tanh keeps
-// the library routine (1 - e^-2|v| loses relative accuracy near 0).
-__device__ __forceinline__ float lora_act_fast(float v, int act) {
-  if (act == LORA_ACT_TANH) return tanhf(v);
-  if (act == LORA_ACT_SIGMOID) return __frcp_rn(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * v));
-  return v;
-}
-
-// 8 consecutive elements at element index e of a buffer (zeros when !ok) as
-// fp16 hi (+ lo for fp32 / bf16 sources); unconditional raw buffer loads.
-template <typename T>
-__device__ __forceinline__ void lora_load8(__amdgpu_buffer_rsrc_t r, uint32_t e, bool ok, f16x8& hi, f16x8& lo) {
-  if constexpr (std::is_same<T, __half>::value) {
-    hi = __builtin_bit_cast(f16x8, buf_ld16(r, ok ? e * 2u : BUF_OOB));
-    lo = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-  } else {
-    float f[8];
-    buf_ld8(r, e, ok, (const T*)nullptr, f);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const _Float16 h = (_Float16)f[q];
-      hi[q] = h;
-      lo[q] = (_Float16)(f[q] - (float)h);
-    }
-  }
-}
-
-__device__ __forceinline__ int lora_find(const LoraBatch& B, int tile, bool up) {
-  int pi = 0;
-#pragma unroll
-  for (int q = 1; q < 4; ++q)
-    if (q < B.nprob && tile >= (up ? B.p[q].tile_u0 : B.p[q].tile_d0)) pi = q;
-  return pi;
-}
 
 // grid (down tiles, ks): partial[p][z][row][n] = sum_{k in range z} x[row,k] Wd[n,k]
 template <int MT, typename TA>
 __global__ __launch_bounds__(256) void lora_down_kernel(const LoraBatch B, int rows, float* __restrict__ part) {
-  constexpr bool SPLIT = !std::is_same<TA, __half>::value;
   __shared__ float s_red[4][16 * MT][17];
-  const int tile = blockIdx.x;
-  const int z = blockIdx.y;
-  const LoraProb& P = B.p[lora_find(B, tile, false)];
-  const int D = B.D;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(P.x, (uint32_t)((int64_t)rows * D * sizeof(TA)));
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(P.wd, (uint32_t)((int64_t)P.r * D * sizeof(TA)));
-  const int n0 = (tile - P.tile_d0) * 16;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int l16 = lane & 15, kg = lane >> 4;
-  const int k0 = z * B.kr;
-  const int k1 = min(D, k0 + B.kr);
-
-  f32x4 acc[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  // 512-input blocks, each a fully unrolled run of four 32-wide wave steps whose
-  // loads are all issued before the MFMAs (steps past the range load zeros)
-  for (int c0 = k0; c0 < k1; c0 += 512) {
-    f16x8 bh[4], bl[4], ah[4][MT], al[4][MT];
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int kk = c0 + 128 * it + wave * 32 + 8 * kg;
-      const bool kok = kk < k1;  // D % 8 == 0
-      lora_load8<TA>(wr, (uint32_t)((n0 + l16) * D + kk), kok && n0 + l16 < P.r, bh[it], bl[it]);
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int row = 16 * t + l16;
-        lora_load8<TA>(xr, (uint32_t)(row * D + kk), kok && row < rows, ah[it][t], al[it][t]);
-      }
-    }
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        acc[t] = mfma16x16x32(ah[it][t], bh[it], acc[t]);
-        if constexpr (SPLIT) {
-          acc[t] = mfma16x16x32(ah[it][t], bl[it], acc[t]);
-          acc[t] = mfma16x16x32(al[it][t], bh[it], acc[t]);
-        }
-      }
-  }
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s_red[wave][16 * t + 4 * kg + e][l16] = acc[t][e];
-  __syncthreads();
-  float* dst = part + P.part_off + (int64_t)z * rows * P.r;
-  for (int idx = tid; idx < rows * 16; idx += 256) {
-    const int row = idx >> 4, nn = idx & 15;
-    if (n0 + nn < P.r)
-      dst[(int64_t)row * P.r + n0 + nn] =
-          ((s_red[0][row][nn] + s_red[1][row][nn]) + s_red[2][row][nn]) + s_red[3][row][nn];
-  }
+  lora_down_tile<MT, TA>(B, rows, part, blockIdx.x, blockIdx.y, threadIdx.x, true, s_red);
 }
 
 // grid (up workgroups): y[row, o] = act_up(sum_k mid[row,k] Wu[o,k] + b[o]),
@@ -548,6 +435,38 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
     });
     if (rc) return rc;
   }
+  return RWKV7MI_OK;
+}
+
+int rwkv7mi::lora_down_batch(int64_t nprob, const void* const* xs, const void* const* w_down, const int64_t* ranks,
+                             int64_t rows, int64_t D, int ks, int act_dtype, LoraBatch* out, int* tiles) {
+  if (nprob < 1 || nprob > 4) return fail(RWKV7MI_EINVAL, "lora down: 1..4 problems");
+  if (!xs || !w_down || !ranks || !out || !tiles) return fail(RWKV7MI_EINVAL, "lora down: null array");
+  if (rows < 1 || rows > 16 || D <= 0 || D % 8 || D > (1 << 20) || ks < 1 || ks > D / 8)
+    return fail(RWKV7MI_EINVAL, "lora down: 1..16 rows, D a positive multiple of 8, 1 <= ks <= D / 8");
+  if (!valid_dtype(act_dtype)) return fail(RWKV7MI_EINVAL, "lora down: bad dtype");
+  LoraBatch b{};
+  int td = 0;
+  int64_t off = 0;
+  for (int i = 0; i < nprob; ++i) {
+    if (!xs[i] || !w_down[i]) return fail(RWKV7MI_EINVAL, "lora down: null pointer");
+    if (ranks[i] <= 0 || ranks[i] % 8 || ranks[i] > LORA_MAXR)
+      return fail(RWKV7MI_EINVAL, "lora down: rank must be a positive multiple of 8, at most 256");
+    if ((reinterpret_cast<uintptr_t>(xs[i]) | reinterpret_cast<uintptr_t>(w_down[i])) & 15)
+      return fail(RWKV7MI_EINVAL, "lora down: x and weights must be 16-byte aligned");
+    b.p[i] = LoraProb{xs[i], w_down[i], nullptr, nullptr, nullptr, (int)ranks[i], 0, 0, td, 0, off};
+    td += (int)((ranks[i] + 15) / 16);
+    off += (int64_t)ks * rows * ranks[i];
+  }
+  b.nprob = (int)nprob;
+  b.D = (int)D;
+  b.A = 1;
+  b.tpw = 1;
+  b.ks = ks;
+  b.kr = (int)((D + ks - 1) / ks);
+  b.kr = (b.kr + 7) / 8 * 8;
+  *out = b;
+  *tiles = td;
   return RWKV7MI_OK;
 }
 

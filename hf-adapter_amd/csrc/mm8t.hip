@@ -41,6 +41,7 @@
 // Up to four problems with the same (rows, I, O) run in one launch
 // (blockIdx.y), e.g. the R/K/V projections of one layer.
 #include "mm8t_common.h"
+#include "lora_common.h"
 
 namespace rwkv7mi {
 
@@ -87,7 +88,32 @@ struct Mm8tBatch {
   // part[((s * nprob + p) * rows + row) * O + o] for mm8t_split_reduce_kernel.
   int S;
   float* part;
+  // Tail workgroups x >= gx (no prologue): the LoRA down projections of the
+  // decode step, whose inputs (the w/a/g/v mixes) are ready when this launch
+  // starts, on the CUs the products leave free (lora_down_tile; 0: none)
+  LoraBatch tl;
+  float* tl_part;
+  int tl_rows, tl_tiles, tl_wgs;
 };
+
+// The tail workgroups' share of the (down tile, K range) units, 256 lanes per
+// unit (two units at a time in an eight-wave workgroup); smem holds the units'
+// cross-wave sums.  Every lane runs the same trip count (one barrier each).
+template <typename TA, int NW>
+__device__ __forceinline__ void mm8t_lora_tail(const Mm8tBatch& B, char* smem) {
+  constexpr int HALVES = NW * 64 / 256;
+  const int h = (int)threadIdx.x >> 8;
+  const int tid = (int)threadIdx.x & 255;
+  float(*s_red)[16][17] = reinterpret_cast<float(*)[16][17]>(smem) + 4 * h;
+  const int nv = B.tl_tiles * B.tl.ks;
+  for (int v0 = ((int)blockIdx.x - B.gx) * HALVES; v0 < nv; v0 += B.tl_wgs * HALVES) {
+    const int v = v0 + h;
+    const bool valid = v < nv;
+    const int vv = valid ? v : 0;
+    lora_down_tile<1, TA>(B.tl, B.tl_rows, B.tl_part, vv % B.tl_tiles, vv / B.tl_tiles, tid, valid, s_red);
+    __syncthreads();  // the next unit reuses s_red
+  }
+}
 
 // bytes of (d0, d1) = rows r..r+7 of one column -> fp16 [w + 0.5] x 8
 __device__ __forceinline__ f16x8 mm8t_b_operand(uint32_t d0, uint32_t d1) {
@@ -149,6 +175,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void mm8t_kernel(const Mm8tBatch B
   if (aux_wg && blockIdx.y != 0) return;
   constexpr int XS = KC + 8;  // LDS row stride (halfs)
   extern __shared__ __align__(16) char smem[];
+  if constexpr (!PRO && BITS == 8) {
+    if (B.tl_wgs > 0 && (int)blockIdx.x >= B.gx) {  // a LoRA-down tail workgroup
+      if (blockIdx.y == 0 && blockIdx.z == 0) mm8t_lora_tail<TA, NW>(B, smem);
+      return;
+    }
+  }
   _Float16* xh = reinterpret_cast<_Float16*>(smem);
   _Float16* xl = xh + nrows * XS;
   __shared__ float red[NW][16][17];
@@ -867,7 +899,8 @@ static int mm8t_auto_splits(int64_t I, int KC) { return KC >= I ? 1 : (int)((I +
 static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I, int64_t O, int act_dtype,
                        int meta_dtype, void* stream, const char* who, int bits = 8, const Mm8tPro* pro = nullptr,
                        void* workspace = nullptr, size_t workspace_bytes = 0, int* splits_out = nullptr,
-                       bool defer_reduce = false) {
+                       bool defer_reduce = false, const LoraBatch* tl = nullptr, float* tl_part = nullptr,
+                       int tl_tiles = 0) {
   const std::string w(who);
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
   if (rows < 0 || I <= 0 || O <= 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
@@ -931,6 +964,9 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
       return fail(RWKV7MI_ESIZE, w + ": split-K workspace missing, unaligned or smaller than "
                                      "rwkv7mi_mm8t_matmul_workspace_bytes");
   }
+  if (tl && (pro || bits != 8 || S != 1 || rows > 16 || !tl_part || tl_tiles <= 0))
+    return fail(RWKV7MI_EINVAL, w + ": the LoRA-down tail runs with the 8-bit GEMV of at most 16 rows, "
+                                    "without the prologue or split K");
   if (splits_out) *splits_out = S;
   b.S = S;
   b.part = S > 1 ? reinterpret_cast<float*>(workspace) : nullptr;
@@ -963,6 +999,21 @@ static int mm8t_launch(int nprob, const Mm8tProb* probs, int64_t rows, int64_t I
     }
   }
   b.gx = (int)(gx * S);
+  if (tl) {
+    // the tail: as many workgroups as the products leave slots free (at least
+    // eight), two down units at a time in an eight-wave workgroup
+    const int64_t halves = nw * 64 / 256;
+    const int64_t units = (int64_t)tl_tiles * tl->ks;
+    const int64_t per_cu = nw == 4 && lds <= MM8T_LDS_X ? 2 : 1;
+    const int64_t free_slots = cus * per_cu - (int64_t)b.gx * nprob * rtiles;
+    extra = std::min<int64_t>((units + halves - 1) / halves, std::max<int64_t>(free_slots, 8));
+    b.tl = *tl;
+    b.tl_part = tl_part;
+    b.tl_rows = (int)rows;
+    b.tl_tiles = tl_tiles;
+    b.tl_wgs = (int)extra;
+    lds = std::max(lds, (size_t)halves * 4u * 16u * 17u * 4u);
+  }
   dim3 grid((unsigned)(b.gx + extra), (unsigned)nprob, (unsigned)rtiles);
   const int wpc = nw * (nw == 4 && lds <= MM8T_LDS_X ? 2 : 1);  // resident waves per CU
   const int rc = dispatch_dtype(act_dtype, [&](auto ta) {
@@ -1047,6 +1098,38 @@ extern "C" int rwkv7mi_mm8t_matmul_multi_ws(int nprob, const void* const* x, con
                     residual ? residual[i] : nullptr, y[i], epilogue[i]};
   return mm8t_launch(nprob, p, rows, I, O, act_dtype, meta_dtype, stream, "mm8t_matmul_multi_ws", 8, nullptr,
                      workspace, workspace_bytes);
+}
+
+extern "C" int rwkv7mi_mm8t_matmul_multi_lora(int nprob, const void* const* x, const uint8_t* const* w_blk,
+                                              const void* const* mx, const void* const* rx, const void* const* my,
+                                              const void* const* ry, const void* const* bias,
+                                              const void* const* residual, void* const* y, const int* epilogue,
+                                              int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype,
+                                              int64_t lora_nprob, const void* const* lora_x,
+                                              const void* const* lora_w_down, const int64_t* lora_ranks,
+                                              int64_t lora_splits, float* lora_part, size_t lora_part_bytes,
+                                              void* stream) {
+  const char* who = "mm8t_matmul_multi_lora";
+  if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, std::string(who) + ": 1..4 problems per launch");
+  if (!x || !w_blk || !mx || !rx || !my || !ry || !y || !epilogue)
+    return fail(RWKV7MI_EINVAL, std::string(who) + ": null array");
+  if (rows == 0) return RWKV7MI_OK;
+  if (lora_splits < 1 || lora_splits > 64) return fail(RWKV7MI_EINVAL, std::string(who) + ": lora_splits 1..64");
+  LoraBatch lb{};
+  int tiles = 0;
+  if (int rc = lora_down_batch(lora_nprob, lora_x, lora_w_down, lora_ranks, rows, I, (int)lora_splits, act_dtype,
+                               &lb, &tiles))
+    return rc;
+  size_t need = 0;
+  for (int64_t i = 0; i < lora_nprob; ++i) need += (size_t)lora_splits * (size_t)rows * (size_t)lora_ranks[i] * 4u;
+  if (!lora_part || lora_part_bytes < need || (reinterpret_cast<uintptr_t>(lora_part) & 15))
+    return fail(RWKV7MI_ESIZE, std::string(who) + ": LoRA partial buffer missing, unaligned or too small");
+  Mm8tProb p[MM8T_MAXPROB];
+  for (int i = 0; i < nprob; ++i)
+    p[i] = Mm8tProb{x[i], nullptr, w_blk[i], mx[i], rx[i], my[i], ry[i], bias ? bias[i] : nullptr,
+                    residual ? residual[i] : nullptr, y[i], epilogue[i]};
+  return mm8t_launch(nprob, p, rows, I, O, act_dtype, meta_dtype, stream, who, 8, nullptr, nullptr, 0, nullptr,
+                     false, &lb, lora_part, tiles);
 }
 
 extern "C" int rwkv7mi_mm8t_matmul_partials(const void* x, const uint8_t* w_blk, const void* mx, const void* rx,

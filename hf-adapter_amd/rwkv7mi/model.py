@@ -35,6 +35,7 @@ from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_sh
 from .sampling import argmax_rows
 from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_prefill_multi_into,
                                mm8_gemm_workspace_bytes, mm8_lnmix_multi_into, mm8_matmul_multi_into,
+                               mm8_matmul_multi_lora_into,
                                mm8_matmul_partials, mm8t_workspace_bytes)
 from .native_quant_policy import should_quantize_linear
 from .self_chunk_rwkv7 import _run_chunk
@@ -685,6 +686,9 @@ class NativeRWKV7ForCausalLM:
         # 3..16 rows: the FFN value's split-K partials are added by the next
         # layer's norm-mix kernel instead of a reduce launch of their own
         self.defer_value_reduce = True
+        # 2..16 rows: the LoRA down projections run as tail workgroups of the
+        # R/K/V launch instead of a launch of their own
+        self.rkv_lora_tail = True
         self._replaced = 0
         self.layers = []
 
@@ -949,9 +953,28 @@ class NativeRWKV7ForCausalLM:
             "hffn": torch.empty(cfg.num_hidden_layers, B, D, device=dev, dtype=dt),
             # the decode LoRA's down projections summed over K (fused-mix route)
             "ldown": torch.empty(B * sum(ranks), device=dev, dtype=torch.float32),
+            "ldown_tail": torch.empty(self.RKV_LORA_SPLITS * B * sum(ranks), device=dev, dtype=torch.float32),
             # 2..8 rows: the fused attention-side launch's LoRA-down K-chunk sums
             "lpart": torch.empty(4 * B * sum(ranks), device=dev, dtype=torch.float32),
         }
+
+    # K ranges of the LoRA down projections run in the R/K/V launch's tail
+    RKV_LORA_SPLITS = 8
+
+    def _rkv_lora_fusable(self, L, B: int) -> bool:
+        """2..16 rows: the LoRA down projections can run as tail workgroups of
+        the grouped R/K/V GEMV (blocked MM8 of one shape, LoRA inputs in the
+        activation dtype and of the model width)."""
+        if not self.rkv_lora_tail or not 1 <= B <= GEMV_ROWS:
+            return False
+        lins = (L.r_proj, L.k_proj, L.v_proj)
+        if not all(isinstance(l, QuantLinear) and is_blocked(l.m.w_blk) for l in lins):
+            return False
+        if len({(l.in_features, l.out_features) for l in lins}) != 1:
+            return False
+        D = lins[0].in_features
+        return all(d.dtype == self.dtype and d.dim() == 2 and int(d.shape[1]) == D and d.is_contiguous()
+                   and int(d.shape[0]) <= 256 for d in L.lora_down)
 
     def _mix_fusable(self, B) -> bool:
         """True when every layer's R/K/V and FFN-key products can take the LN-mix prologue."""
@@ -1014,13 +1037,22 @@ class NativeRWKV7ForCausalLM:
                 parts = None
             if (self.fused_lora_decode and not self.lora_side_stream
                     and fused_lora_decode_supported([int(d.shape[0]) for d in L.lora_down], B)):
-                # LoRA down (split-K launch), then the up projections inside the wkv kernel
+                # LoRA down (its own split-K launch, or tail workgroups of the
+                # R/K/V launch), then the up projections inside the wkv kernel
+                down_sums, down_splits = (bufs["ldown"], 1) if fmix else (None, 1)
                 if not fmix:
-                    QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv), (rkv[0], rkv[1], rkv[2]))
+                    if self._rkv_lora_fusable(L, B):
+                        down_sums, down_splits = bufs["ldown_tail"], self.RKV_LORA_SPLITS
+                        mm8_matmul_multi_lora_into([xr, xk, xv], [L.r_proj.m, L.k_proj.m, L.v_proj.m],
+                                                   [rkv[0], rkv[1], rkv[2]], [xw, xa, xg, xv][:n], L.lora_down,
+                                                   down_sums, splits=down_splits)
+                    else:
+                        QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv),
+                                                (rkv[0], rkv[1], rkv[2]))
                 fused_wavg_lora_output_prepare_raw(
                     rkv[0], rkv[1], rkv[2], [xw, xa, xg, xv][:n], L.lora_down, L.lora_up, L.lora_bias, state[i],
                     L.k_k, L.k_a, L.r_k, L.gn[0], L.gn[1], eps=N * 1e-5, out=prep, state_out=state[i],
-                    v_first=v_first, v_mode=1 if i == 0 else 2, down_sums=bufs["ldown"] if fmix else None)
+                    v_first=v_first, v_mode=1 if i == 0 else 2, down_sums=down_sums, down_splits=down_splits)
             else:
                 if self.lora_side_stream:
                     # the LoRA projections depend only on the mixes: a second stream

@@ -229,6 +229,51 @@ def mm8_matmul_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
     return outs
 
 
+def mm8_matmul_multi_lora_into(xs, mods, outs, lora_xs, lora_downs, lora_part, *, splits: int = 4):
+    """:func:`mm8_matmul_multi_into` (at most 16 rows, no split K) with the
+    decode LoRA down projections in the same launch, on the workgroups the
+    products leave free: ``lora_part`` (fp32, contiguous) receives
+    ``[p][z][row][n] = sum_{k in range z} lora_xs[p][row, k] lora_downs[p][n, k]``
+    over ``splits`` K ranges, the layout the fused wkv decode kernel reads
+    (``down_splits=splits``)."""
+    k = len(mods)
+    if not 1 <= k <= 4 or len(xs) != k or len(outs) != k:
+        raise ValueError("mm8_matmul_multi_lora_into: 1..4 problems")
+    rows, n = (int(s) for s in xs[0].shape)
+    m = int(mods[0].out_features)
+    kl = len(lora_xs)
+    if not 1 <= kl <= 4 or len(lora_downs) != kl:
+        raise ValueError("mm8_matmul_multi_lora_into: 1..4 LoRA problems")
+    for x2, mod, out in zip(xs, mods, outs):
+        if tuple(x2.shape) != (rows, n) or not x2.is_contiguous() or x2.dtype != xs[0].dtype:
+            raise ValueError("mm8_matmul_multi_lora_into: inputs must share one contiguous shape and dtype")
+        if mod.in_features != n or mod.out_features != m or not is_blocked(mod.w_blk):
+            raise ValueError("mm8_matmul_multi_lora_into: modules must be blocked MM8Linear of one shape")
+        _check_out(x2, m, out, None)
+    for lx, wd in zip(lora_xs, lora_downs):
+        if tuple(lx.shape) != (rows, n) or not lx.is_contiguous() or lx.dtype != xs[0].dtype:
+            raise ValueError("mm8_matmul_multi_lora_into: LoRA inputs must match the products' rows, width and dtype")
+        if wd.dim() != 2 or int(wd.shape[1]) != n or not wd.is_contiguous() or wd.dtype != xs[0].dtype:
+            raise ValueError("mm8_matmul_multi_lora_into: LoRA down weights must be contiguous [rank, in]")
+    ranks = [int(wd.shape[0]) for wd in lora_downs]
+    need = int(splits) * rows * sum(ranks)
+    if (lora_part.dtype != torch.float32 or not lora_part.is_contiguous() or int(lora_part.numel()) < need):
+        raise ValueError("mm8_matmul_multi_lora_into: lora_part must be contiguous fp32 with "
+                         "splits * rows * sum(ranks) values")
+    _lib.require_gpu(*xs, *outs, *lora_xs, *lora_downs, lora_part, name="mm8_matmul_multi_lora")
+    arr = lambda ts: _lib.ptr_array(ts)
+    eps = (ctypes.c_int * k)(*([_lib.EPI_NONE] * k))
+    _lib.call(
+        "rwkv7mi_mm8t_matmul_multi_lora", k, arr(xs), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
+        arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),
+        arr([md.bias for md in mods]), arr([None] * k), arr(outs), eps,
+        rows, n, m, _lib.dtype_code(xs[0]), _lib.dtype_code(mods[0].mx), kl, arr(lora_xs), arr(lora_downs),
+        (ctypes.c_int64 * kl)(*ranks), int(splits), _lib.ptr(lora_part), int(lora_part.numel()) * 4,
+        _lib.stream_of(xs[0]),
+    )
+    return outs
+
+
 def mm8_matmul_partials(x2, mod):
     """The split-K products of ``x2 [rows, N] @ mod`` left as fp32 partials for the
     consumer to add (no reduce launch): returns ``(part [S, rows, M], S)``, a view

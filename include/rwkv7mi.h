@@ -260,6 +260,30 @@ int rwkv7mi_mm8t_matmul_multi_ws(int nprob, const void* const* x,
                                  void* workspace, size_t workspace_bytes,
                                  void* stream);
 
+/* rwkv7mi_mm8t_matmul_multi (no split K, at most 16 rows) with the decode
+ * LoRA down projections in the same launch: workgroups past the products
+ * compute lora_part[p][z][row][n] = sum_{k in range z} lora_x[p][row,k]
+ * lora_w_down[p][n,k] over lora_splits K ranges of I inputs (the layout
+ * rwkv7mi_wkv7_decode_lora_output_prepare reads with lora_splits = that count),
+ * for up to four problems of lora_ranks[p] (multiples of 8, at most 256),
+ * lora_x in act_dtype [rows, I].  The products are those of the plain call.
+ * Replaces the grouped R/K/V dispatch plus fused_wavg_lora's down launch of
+ * the decode step (rwkv7_hf/native_jit_graph_dispatch.py:449-801,
+ * rwkv7_hf/fused_lora.py:706). */
+int rwkv7mi_mm8t_matmul_multi_lora(int nprob, const void* const* x,
+                                   const uint8_t* const* w_blk,
+                                   const void* const* mx, const void* const* rx,
+                                   const void* const* my, const void* const* ry,
+                                   const void* const* bias,
+                                   const void* const* residual, void* const* y,
+                                   const int* epilogue, int64_t rows, int64_t I,
+                                   int64_t O, int act_dtype, int meta_dtype,
+                                   int64_t lora_nprob, const void* const* lora_x,
+                                   const void* const* lora_w_down,
+                                   const int64_t* lora_ranks, int64_t lora_splits,
+                                   float* lora_part, size_t lora_part_bytes,
+                                   void* stream);
+
 /* The split-K products of rwkv7mi_mm8t_matmul_multi_ws for one problem
  * without the second launch: the ranges' fp32 partials stay in `workspace`
  * as part[(s * rows + row) * O + o] (s < *splits), each already carrying its

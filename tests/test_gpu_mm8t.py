@@ -193,6 +193,65 @@ def test_mm8t_multi_equals_single(rows):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("rows,I,O,ranks,splits", [(8, 4096, 4096, (64, 64, 128, 32), 4), (2, 512, 384, (64, 64, 128), 4),
+                                                   (16, 1024, 256, (16, 8, 256, 24), 3), (3, 4096, 1024, (64,), 1)])
+def test_mm8t_multi_lora_tail(rows, I, O, ranks, splits):
+    """The grouped GEMV with the LoRA down projections as tail workgroups: the
+    products equal the plain grouped launch bit for bit, and the down partials
+    summed over the K ranges match an fp32 torch product (the reference's
+    ``x @ W_down^T``, rwkv7_hf/fused_lora.py:795-803) on the same fp16 operands."""
+    from rwkv7mi import MM8Linear
+    from rwkv7mi.native_quant_mm8 import mm8_matmul_multi_into, mm8_matmul_multi_lora_into
+
+    rng = np.random.default_rng(rows * 131 + I + len(ranks))
+    mods, xs = [], []
+    for p in range(3):
+        lin = torch.nn.Linear(I, O, bias=(p == 1)).to(device="cuda", dtype=torch.float16)
+        with torch.no_grad():
+            lin.weight.copy_(_cuda(rng.standard_normal((O, I)) * 0.02, torch.float16))
+        mods.append(MM8Linear(lin))
+        xs.append(_cuda(rng.standard_normal((rows, I)), torch.float16))
+    lxs = [_cuda(rng.standard_normal((rows, I)), torch.float16) for _ in ranks]
+    lws = [_cuda(rng.standard_normal((r, I)) * 0.05, torch.float16) for r in ranks]
+    part = torch.full((splits * rows * sum(ranks) + 7,), float("nan"), device="cuda", dtype=torch.float32)
+    outs = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(3)]
+    plain = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(3)]
+    mm8_matmul_multi_lora_into(xs, mods, outs, lxs, lws, part, splits=splits)
+    mm8_matmul_multi_into(xs, mods, plain)
+    torch.cuda.synchronize()
+    for a, b in zip(outs, plain):
+        assert torch.equal(a, b)
+    off = 0
+    for lx, lw, r in zip(lxs, lws, ranks):
+        got = part[off:off + splits * rows * r].view(splits, rows, r).sum(0)
+        ref = lx.float() @ lw.float().t()
+        err = (got - ref).abs().max().item() / ref.abs().max().item()
+        assert err < 1e-5, (r, err)
+        off += splits * rows * r
+    assert torch.isnan(part[off:]).all()  # nothing past the partials
+
+
+def test_mm8t_multi_lora_rejects():
+    from rwkv7mi import MM8Linear
+    from rwkv7mi.native_quant_mm8 import mm8_matmul_multi_lora_into
+
+    I, O = 256, 128
+    lin = torch.nn.Linear(I, O, bias=False).to(device="cuda", dtype=torch.float16)
+    m = MM8Linear(lin)
+    x = torch.randn(2, I, device="cuda", dtype=torch.float16)
+    out = torch.empty(2, O, device="cuda", dtype=torch.float16)
+    lw = torch.randn(64, I, device="cuda", dtype=torch.float16)
+    with pytest.raises(ValueError):  # partial buffer too small
+        mm8_matmul_multi_lora_into([x], [m], [out], [x], [lw], torch.empty(10, device="cuda"), splits=4)
+    with pytest.raises(ValueError):  # rank not a multiple of 8
+        mm8_matmul_multi_lora_into([x], [m], [out], [x], [lw[:60].contiguous()],
+                                   torch.empty(4096, device="cuda"), splits=4)
+    x17 = torch.randn(17, I, device="cuda", dtype=torch.float16)
+    with pytest.raises(ValueError):  # more than 16 rows
+        mm8_matmul_multi_lora_into([x17], [m], [torch.empty(17, O, device="cuda", dtype=torch.float16)], [x17], [lw],
+                                   torch.empty(8192, device="cuda"), splits=4)
+
+
 @pytest.mark.parametrize("IO", [(256, 512), (4096, 1024)])
 def test_mm8t_dequant_equals_rowmajor(IO):
     from rwkv7mi import _lib
