@@ -82,6 +82,8 @@ SIGNATURES = {
     "rwkv7mi_attn_mix_lora_chunks": (_i32, [_i64]),
     "rwkv7mi_slot_copy": (_i32, [_c_p, _i64, _i64, _c_p, _c_p, _i64, _i64, _c_p, _c_p, _i64, _i64, _i64, _c_p]),
     "rwkv7mi_argmax_rows": (_i32, [_c_p, _i64, _i64, _i64, _i32, _c_p, _c_p, _c_p]),
+    "rwkv7mi_argmax_workspace_bytes": (_sz, [_i64, _i64, _i32]),
+    "rwkv7mi_argmax_rows_ws": (_i32, [_c_p, _i64, _i64, _i64, _i32, _c_p, _c_p, _c_p, _sz, _c_p]),
     "rwkv7mi_mm8t_matmul_partials": (_i32, [_c_p] * 6 + [_i64, _i64, _i64, _i32, _i32, _c_p, _sz, ctypes.POINTER(_i32), _c_p]),
     "rwkv7mi_attn_norm_mix6_parts": (_i32, [_c_p] * 6 + [_i64, _c_p, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _c_p]),
     "rwkv7mi_lora_workspace_bytes": (_sz, [_i64, _c_p, _i64, _i64]),

@@ -32,7 +32,7 @@ from .fused_output import fused_attn_output_prepare
 from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
-from .sampling import argmax_rows
+from .sampling import argmax_rows, argmax_workspace_bytes
 from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_prefill_multi_into,
                                mm8_gemm_workspace_bytes, mm8_lnmix_multi_into, mm8_matmul_multi_into,
                                mm8_matmul_multi_lora_into,
@@ -1410,6 +1410,8 @@ class NativeGraphRunner:
         self.tokens = torch.zeros(self.batch, dtype=torch.long, device=dev)
         self.logits = torch.empty(self.batch, model.config.vocab_size, device=dev, dtype=model.dtype)
         self.next_tokens = torch.zeros(self.batch, dtype=torch.long, device=dev)
+        self.argmax_ws = torch.empty(argmax_workspace_bytes(self.batch, model.config.vocab_size, model.dtype),
+                                     device=dev, dtype=torch.uint8)
         self.bufs = model._decode_buffers(self.batch)
         snapshot = self.cache.clone()
         side = torch.cuda.Stream(device=dev)
@@ -1427,7 +1429,7 @@ class NativeGraphRunner:
     def _step(self) -> None:
         """The captured work: one decode step, then the greedy tokens."""
         self.model.decode_step_(self.tokens, self.cache, self.logits, self.bufs)
-        argmax_rows(self.logits, out=self.next_tokens, out2=self.tokens)
+        argmax_rows(self.logits, out=self.next_tokens, out2=self.tokens, workspace=self.argmax_ws)
 
     def _copy_into(self, cache: NativeRWKV7Cache) -> None:
         s, a, f, v = self.cache

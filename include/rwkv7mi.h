@@ -484,6 +484,15 @@ int rwkv7mi_slot_copy(const void* src, int64_t src_layer_stride,
 int rwkv7mi_argmax_rows(const void* x, int64_t rows, int64_t n, int64_t ld,
                         int dtype, int64_t* out, int64_t* out2, void* stream);
 
+/* rwkv7mi_argmax_rows in two launches over many workgroups per row (slices
+ * of 4096 fp16 / 2048 fp32 entries, then one wave per row over the slices'
+ * bests), with the same result and rules; `workspace` (8-byte aligned) holds
+ * rwkv7mi_argmax_workspace_bytes(rows, n, dtype).  rows <= 65535. */
+size_t rwkv7mi_argmax_workspace_bytes(int64_t rows, int64_t n, int dtype);
+int rwkv7mi_argmax_rows_ws(const void* x, int64_t rows, int64_t n, int64_t ld,
+                           int dtype, int64_t* out, int64_t* out2,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ LoRA */
 
 /* Bytes of workspace rwkv7mi_lora_multi needs (fp32 split-K partials). */

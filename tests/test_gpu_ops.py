@@ -251,12 +251,21 @@ def test_argmax_rows_matches_torch(dtype, rows, n):
         x[1, -1] = 60.0  # the last element
         x[2, n // 4] = float("nan")
         x[2, n // 2] = float("nan")
+    if rows >= 8:
+        x[3] = float("-inf")  # every entry equal: index 0
+        x[4, 4095] = x[4, 4096] = 70.0  # a tie across two slices of the many-workgroup form
     got = argmax_rows(x)
     out2 = torch.full((rows,), -1, device="cuda", dtype=torch.int64)
     got2 = argmax_rows(x, out2=out2)
+    # the single-workgroup entry point gives the same indices
+    from rwkv7mi import _lib
+    one = torch.full((rows,), -1, device="cuda", dtype=torch.int64)
+    _lib.call("rwkv7mi_argmax_rows", _lib.ptr(x), rows, n, int(x.stride(0)), _lib.dtype_code(x), _lib.ptr(one),
+              None, _lib.stream_of(x))
     torch.cuda.synchronize()
     ref = x.argmax(-1)
     assert torch.equal(got, ref)
     assert torch.equal(got2, ref) and torch.equal(out2, ref)
+    assert torch.equal(one, ref)
     if rows >= 3:
         assert int(got[0]) == n // 3 and int(got[1]) == n - 1 and int(got[2]) == n // 4
