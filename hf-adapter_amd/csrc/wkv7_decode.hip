@@ -459,7 +459,7 @@ extern "C" int rwkv7mi_wkv7_decode_lora_output_prepare(
   if (N != HEAD) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: head size must be 64");
   if (B < 0 || H <= 0 || D <= 0) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: bad B/H/D");
   if (B == 0) return RWKV7MI_OK;
-  if (B > LORA_ROWS) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: at most 32 rows");
+  if (B > LORA_ROWS) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: at most 64 rows");
   if (!r || !k_raw || !v || !lora_part || !ranks || !w_up || !act_down || !act_up || !state_in || !state_out ||
       !k_k || !k_a || !r_k || !gn_w || !gn_b || !out)
     return fail(RWKV7MI_EINVAL, "wkv7 decode lora: null pointer");

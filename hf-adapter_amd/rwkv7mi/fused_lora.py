@@ -62,7 +62,7 @@ def lora_multi(xs, downs, ups, biases, outs, acts_down, acts_up):
 def fused_lora_decode_supported(ranks, rows: int) -> bool:
     """Whether ``fused_wavg_lora_output_prepare_raw`` takes these shapes."""
     ranks = [int(r) for r in ranks]
-    return 0 < int(rows) <= 32 and len(ranks) in (3, 4) and all(0 < r <= 128 and r % 8 == 0 for r in ranks)
+    return 0 < int(rows) <= 64 and len(ranks) in (3, 4) and all(0 < r <= 128 and r % 8 == 0 for r in ranks)
 
 
 def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, state, k_k, k_a, r_k,
@@ -85,7 +85,7 @@ def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, stat
     rows, D = (int(s) for s in xs[0].shape)
     ranks = [int(d.shape[0]) for d in downs]
     if not fused_lora_decode_supported(ranks, rows):
-        raise ValueError("fused LoRA decode: rows <= 32, 3 or 4 ranks, multiples of 8 up to 128")
+        raise ValueError("fused LoRA decode: rows <= 64, 3 or 4 ranks, multiples of 8 up to 128")
     B, H, N = (int(x) for x in state.shape[:3])
     if rows != B or int(r.numel()) != B * H * N:
         raise ValueError("fused LoRA decode: rows must match the state batch")

@@ -108,7 +108,7 @@ int rwkv7mi_wkv7_decode_output_prepare_raw(
  * w_up[p] [H*N, rank_p], b_up[p] [H*N] or NULL, activations 0 none, 1 tanh,
  * 2 sigmoid.  Each (batch, head) workgroup computes its own 64 channels of
  * every up projection, rounded to act_dtype as the reference's tensors are.
- * B <= 32; ranks multiples of 8, at most 128; nprob 3 or 4 (4 when
+ * B <= 64; ranks multiples of 8, at most 128; nprob 3 or 4 (4 when
  * v_mode == 2).  lora_splits: the number of K ranges in lora_part (0: the
  * split rwkv7mi_lora_down_multi uses for these ranks and D; 1: the whole-K
  * sums of rwkv7mi_mm8t_lnmix_multi). */
@@ -517,7 +517,7 @@ int rwkv7mi_lora_multi(int64_t nprob, const void* const* xs,
 /* The down projections of rwkv7mi_lora_multi alone (the first half of
  * fused_wavg_lora, rwkv7_hf/fused_lora.py:706): fp32 partial sums
  * [problem][ks][rows][rank] in the workspace, for
- * rwkv7mi_wkv7_decode_lora_output_prepare.  rows <= 32. */
+ * rwkv7mi_wkv7_decode_lora_output_prepare.  rows <= 64. */
 int rwkv7mi_lora_down_multi(int64_t nprob, const void* const* xs,
                             const void* const* w_down, const int64_t* ranks,
                             const int* act_down, int64_t rows, int64_t D,

@@ -141,7 +141,7 @@ def test_decode_output_prepare_raw(oracle, v_mode):
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("B,v_mode,nl", [(1, 2, 4), (3, 2, 4), (8, 1, 3), (32, 2, 4), (2, 0, 3)])
+@pytest.mark.parametrize("B,v_mode,nl", [(1, 2, 4), (3, 2, 4), (8, 1, 3), (32, 2, 4), (64, 2, 4), (2, 0, 3)])
 @pytest.mark.parametrize("ranks", [(64, 64, 128, 32), (24, 128, 8, 96)])
 def test_decode_fused_lora(oracle, dt, B, v_mode, nl, ranks):
     """LoRA up projections fused into the decode kernel == the fp64 oracle composition
@@ -224,7 +224,8 @@ def test_decode_fused_lora_rejects_unsupported():
     from rwkv7mi.fused_lora import fused_lora_decode_supported
 
     assert fused_lora_decode_supported((64, 64, 128, 32), 8)
-    assert not fused_lora_decode_supported((64, 64, 128, 32), 33)
+    assert fused_lora_decode_supported((64, 64, 128, 32), 64)
+    assert not fused_lora_decode_supported((64, 64, 128, 32), 65)
     assert fused_lora_decode_supported((64, 64, 120, 40), 1)
     assert not fused_lora_decode_supported((64, 64, 124, 32), 1)
     assert not fused_lora_decode_supported((64, 64, 256, 32), 1)
