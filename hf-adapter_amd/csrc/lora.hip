@@ -442,8 +442,8 @@ int rwkv7mi::lora_down_batch(int64_t nprob, const void* const* xs, const void* c
                              int64_t rows, int64_t D, int ks, int act_dtype, LoraBatch* out, int* tiles) {
   if (nprob < 1 || nprob > 4) return fail(RWKV7MI_EINVAL, "lora down: 1..4 problems");
   if (!xs || !w_down || !ranks || !out || !tiles) return fail(RWKV7MI_EINVAL, "lora down: null array");
-  if (rows < 1 || rows > 16 || D <= 0 || D % 8 || D > (1 << 20) || ks < 1 || ks > D / 8)
-    return fail(RWKV7MI_EINVAL, "lora down: 1..16 rows, D a positive multiple of 8, 1 <= ks <= D / 8");
+  if (rows < 1 || rows > LORA_ROWS || D <= 0 || D % 8 || D > (1 << 20) || ks < 1 || ks > D / 8)
+    return fail(RWKV7MI_EINVAL, "lora down: 1..64 rows, D a positive multiple of 8, 1 <= ks <= D / 8");
   if (!valid_dtype(act_dtype)) return fail(RWKV7MI_EINVAL, "lora down: bad dtype");
   LoraBatch b{};
   int td = 0;

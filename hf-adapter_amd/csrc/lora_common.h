@@ -66,14 +66,16 @@ __device__ __forceinline__ int lora_find(const LoraBatch& B, int tile, bool up) 
   return pi;
 }
 
-// One (down tile, K range z) of the split-K down projection:
+// One (down tile, K range z, rows row0 .. row0 + 16 MT - 1) of the split-K
+// down projection:
 //   partial[p][z][row][n] = sum_{k in range z} x[row,k] Wd[n,k]
 // run by the 256 lanes tid = 0..255 of a workgroup (or of one half of a larger
 // one); s_red is this half's [4][16 MT][17] floats of LDS.  Every caller lane
 // reaches the one barrier; !valid tiles load and store nothing.
 template <int MT, typename TA>
 __device__ __forceinline__ void lora_down_tile(const LoraBatch& B, int rows, float* __restrict__ part, int tile,
-                                               int z, int tid, bool valid, float (*s_red)[16 * MT][17]) {
+                                               int z, int tid, bool valid, float (*s_red)[16 * MT][17],
+                                               int row0 = 0) {
   constexpr bool SPLIT = !std::is_same<TA, __half>::value;
   const LoraProb& P = B.p[lora_find(B, tile, false)];
   const int D = B.D;
@@ -99,7 +101,7 @@ __device__ __forceinline__ void lora_down_tile(const LoraBatch& B, int rows, flo
       lora_load8<TA>(wr, (uint32_t)((n0 + l16) * D + kk), kok && n0 + l16 < P.r, bh[it], bl[it]);
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        const int row = 16 * t + l16;
+        const int row = row0 + 16 * t + l16;
         lora_load8<TA>(xr, (uint32_t)(row * D + kk), kok && row < rows, ah[it][t], al[it][t]);
       }
     }
@@ -121,16 +123,17 @@ __device__ __forceinline__ void lora_down_tile(const LoraBatch& B, int rows, flo
   __syncthreads();
   if (valid) {
     float* dst = part + P.part_off + (int64_t)z * rows * P.r;
-    for (int idx = tid; idx < rows * 16; idx += 256) {
+    const int nr = min(16 * MT, rows - row0);
+    for (int idx = tid; idx < nr * 16; idx += 256) {
       const int row = idx >> 4, nn = idx & 15;
       if (n0 + nn < P.r)
-        dst[(int64_t)row * P.r + n0 + nn] =
+        dst[(int64_t)(row0 + row) * P.r + n0 + nn] =
             ((s_red[0][row][nn] + s_red[1][row][nn]) + s_red[2][row][nn]) + s_red[3][row][nn];
     }
   }
 }
 
-// Host: the down-projection batch of up to four problems over `rows` (<= 16)
+// Host: the down-projection batch of up to four problems over `rows` (<= 64)
 // rows of D inputs in ks K ranges, partials packed [p][z][row][r_p] from
 // `part`; returns RWKV7MI_OK or an error (recorded by fail()).  *tiles: down
 // tiles over all problems.

@@ -5,6 +5,7 @@
 #include <mutex>
 
 #include "mm8t_common.h"
+#include "lora_common.h"
 
 // ---------------------------------------------------------------------------
 // Many-row MM8 dequant GEMM over the blocked layout (17..256 rows: bsz-64
@@ -49,7 +50,27 @@ struct Mm8gBatch {
   float* part;   // [S][nprob][rows][O] fp32 partial products (S > 1)
   int rows, I, O, KB, S, ctiles, nprob;
   int cw;  // workgroups per (problem, split, row tile): column-tile stride
+  // Tail workgroups x >= cw S: the decode LoRA down projections (inputs ready
+  // when the launch starts) on the CUs the tiles leave free (0: none)
+  LoraBatch tl;
+  float* tl_part;
+  int tl_tiles, tl_wgs;
 };
+
+// The tail workgroups' share of the (16-row tile, down tile, K range) units.
+// Every lane runs the same trip count (one barrier each).
+template <typename TA>
+__device__ __forceinline__ void mm8g_lora_tail(const Mm8gBatch& B, char* smem) {
+  float(*s_red)[16][17] = reinterpret_cast<float(*)[16][17]>(smem);
+  const int per_z = B.tl_tiles * ((B.rows + 15) / 16);
+  const int nu = per_z * B.tl.ks;
+  for (int u = (int)blockIdx.x - B.cw * B.S; u < nu; u += B.tl_wgs) {
+    const int z = u / per_z, rem = u % per_z;
+    lora_down_tile<1, TA>(B.tl, B.rows, B.tl_part, rem % B.tl_tiles, z, (int)threadIdx.x, true, s_red,
+                          16 * (rem / B.tl_tiles));
+    __syncthreads();  // the next unit reuses s_red
+  }
+}
 
 // bytes (d0, d1) = rows r..r+7 of one column -> fp16 (w - 128) x 8 (exact)
 __device__ __forceinline__ f16x8 mm8g_b_operand(uint32_t d0, uint32_t d1) {
@@ -171,6 +192,10 @@ __global__ __launch_bounds__(256, 2) void mm8g_kernel(const Mm8gBatch B) {
   const int ngroups = (O + MM8T_COLS - 1) / MM8T_COLS;
   constexpr int XS = 128 * NKP + 8;  // LDS row stride (halfs): rows land 16 bytes apart in the banks
   extern __shared__ __align__(16) char smem[];
+  if (B.tl_wgs > 0 && (int)blockIdx.x >= B.cw * B.S) {  // a LoRA-down tail workgroup
+    if (blockIdx.y == 0 && blockIdx.z == 0) mm8g_lora_tail<TA>(B, smem);
+    return;
+  }
   _Float16* xs = reinterpret_cast<_Float16*>(smem);
   _Float16* xsl = xs + TROWS * XS;  // the lo rows (LO only)
   (void)I;
@@ -404,7 +429,8 @@ static int mm8g_run(const char* who, int nprob, const void* const* x, const uint
                     const void* const* mx, const void* const* rx, const void* const* my, const void* const* ry,
                     const void* const* bias, const void* const* residual, void* const* y, const int* epilogue,
                     int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype, int splits, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    size_t workspace_bytes, void* stream, const LoraBatch* tl = nullptr, float* tl_part = nullptr,
+                    int tl_tiles = 0) {
   const std::string w(who);
   if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
   if (!x || !w_blk || !mx || !rx || !my || !ry || !y || !epilogue) return fail(RWKV7MI_EINVAL, w + ": null array");
@@ -457,7 +483,19 @@ static int mm8g_run(const char* who, int nprob, const void* const* x, const uint
   const int64_t cwmax = std::max<int64_t>(1, slots / ((int64_t)S * nprob * rtiles));
   const int64_t per = (b.ctiles + cwmax - 1) / cwmax;  // tiles per workgroup
   b.cw = (int)((b.ctiles + per - 1) / per);
-  const dim3 grid((unsigned)(b.cw * S), (unsigned)nprob, (unsigned)rtiles);
+  int64_t tail = 0;
+  if (tl) {
+    if (rows > LORA_ROWS || !tl_part || tl_tiles <= 0)
+      return fail(RWKV7MI_EINVAL, w + ": the LoRA-down tail takes at most 64 rows");
+    const int64_t units = (int64_t)tl_tiles * tl->ks * ((rows + 15) / 16);
+    const int64_t free_slots = slots - (int64_t)b.cw * S * nprob * rtiles;
+    tail = std::min<int64_t>(units, std::max<int64_t>(free_slots, 8));
+    b.tl = *tl;
+    b.tl_part = tl_part;
+    b.tl_tiles = tl_tiles;
+    b.tl_wgs = (int)tail;
+  }
+  const dim3 grid((unsigned)(b.cw * S + tail), (unsigned)nprob, (unsigned)rtiles);
   return dispatch_dtype(act_dtype, [&](auto ta) {
     using TA = decltype(ta);
     return dispatch_dtype(meta_dtype, [&](auto tm) {
@@ -500,6 +538,32 @@ extern "C" int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x, const ui
                                        size_t workspace_bytes, void* stream) {
   return mm8g_run("mm8t_gemm_multi", nprob, x, w_blk, mx, rx, my, ry, bias, residual, y, epilogue, rows, I, O,
                   act_dtype, meta_dtype, splits, workspace, workspace_bytes, stream);
+}
+
+extern "C" int rwkv7mi_mm8t_gemm_multi_lora(int nprob, const void* const* x, const uint8_t* const* w_blk,
+                                            const void* const* mx, const void* const* rx, const void* const* my,
+                                            const void* const* ry, const void* const* bias,
+                                            const void* const* residual, void* const* y, const int* epilogue,
+                                            int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype,
+                                            int splits, void* workspace, size_t workspace_bytes,
+                                            int64_t lora_nprob, const void* const* lora_x,
+                                            const void* const* lora_w_down, const int64_t* lora_ranks,
+                                            int64_t lora_splits, float* lora_part, size_t lora_part_bytes,
+                                            void* stream) {
+  const char* who = "mm8t_gemm_multi_lora";
+  if (rows == 0) return RWKV7MI_OK;
+  if (lora_splits < 1 || lora_splits > 64) return fail(RWKV7MI_EINVAL, std::string(who) + ": lora_splits 1..64");
+  LoraBatch lb{};
+  int tiles = 0;
+  if (int rc = lora_down_batch(lora_nprob, lora_x, lora_w_down, lora_ranks, rows, I, (int)lora_splits, act_dtype,
+                               &lb, &tiles))
+    return rc;
+  size_t need = 0;
+  for (int64_t i = 0; i < lora_nprob; ++i) need += (size_t)lora_splits * (size_t)rows * (size_t)lora_ranks[i] * 4u;
+  if (!lora_part || lora_part_bytes < need || (reinterpret_cast<uintptr_t>(lora_part) & 15))
+    return fail(RWKV7MI_ESIZE, std::string(who) + ": LoRA partial buffer missing, unaligned or too small");
+  return mm8g_run(who, nprob, x, w_blk, mx, rx, my, ry, bias, residual, y, epilogue, rows, I, O, act_dtype,
+                  meta_dtype, splits, workspace, workspace_bytes, stream, &lb, lora_part, tiles);
 }
 
 // ---- allocation-free form: the scratch lives in this file's device array

@@ -58,6 +58,9 @@ SIGNATURES = {
     "rwkv7mi_mm8t_matmul_multi": (_i32, [_i32] + [_c_p] * 10 + [_i64, _i64, _i64, _i32, _i32, _c_p]),
     "rwkv7mi_mm8t_matmul_workspace_bytes": (_sz, [_i32, _i64, _i64, _i64]),
     "rwkv7mi_mm8t_matmul_multi_ws": (_i32, [_i32] + [_c_p] * 10 + [_i64, _i64, _i64, _i32, _i32, _c_p, _sz, _c_p]),
+    "rwkv7mi_mm8t_gemm_multi_lora": (
+        _i32, [_i32] + [_c_p] * 10 + [_i64, _i64, _i64, _i32, _i32, _i32, _c_p, _sz, _i64, _c_p, _c_p, _c_p, _i64,
+                                      _c_p, _sz, _c_p]),
     "rwkv7mi_mm8t_matmul_multi_lora": (
         _i32, [_i32] + [_c_p] * 10 + [_i64, _i64, _i64, _i32, _i32, _i64, _c_p, _c_p, _c_p, _i64, _c_p, _sz, _c_p]),
     "rwkv7mi_mm8t_dequant": (_i32, [_c_p] * 6 + [_i64, _i64, _i32, _i32, _c_p]),

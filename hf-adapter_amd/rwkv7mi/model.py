@@ -686,8 +686,8 @@ class NativeRWKV7ForCausalLM:
         # 3..16 rows: the FFN value's split-K partials are added by the next
         # layer's norm-mix kernel instead of a reduce launch of their own
         self.defer_value_reduce = True
-        # 2..16 rows: the LoRA down projections run as tail workgroups of the
-        # R/K/V launch instead of a launch of their own
+        # up to 64 rows (without the LN-mix prologue): the LoRA down projections
+        # run as tail workgroups of the R/K/V launch instead of a launch of their own
         self.rkv_lora_tail = True
         self._replaced = 0
         self.layers = []
@@ -953,19 +953,25 @@ class NativeRWKV7ForCausalLM:
             "hffn": torch.empty(cfg.num_hidden_layers, B, D, device=dev, dtype=dt),
             # the decode LoRA's down projections summed over K (fused-mix route)
             "ldown": torch.empty(B * sum(ranks), device=dev, dtype=torch.float32),
-            "ldown_tail": torch.empty(self.RKV_LORA_SPLITS * B * sum(ranks), device=dev, dtype=torch.float32),
+            "ldown_tail": torch.empty(self._rkv_lora_splits(B) * B * sum(ranks), device=dev, dtype=torch.float32),
             # 2..8 rows: the fused attention-side launch's LoRA-down K-chunk sums
             "lpart": torch.empty(4 * B * sum(ranks), device=dev, dtype=torch.float32),
         }
 
-    # K ranges of the LoRA down projections run in the R/K/V launch's tail
+    # K ranges of the LoRA down projections run in the R/K/V launch's tail (the
+    # fused wkv kernel adds them): measured best at 8 up to 16 rows, 4 above
     RKV_LORA_SPLITS = 8
+    RKV_LORA_SPLITS_MANY = 4
+
+    def _rkv_lora_splits(self, B: int) -> int:
+        return self.RKV_LORA_SPLITS if B <= GEMV_ROWS else self.RKV_LORA_SPLITS_MANY
 
     def _rkv_lora_fusable(self, L, B: int) -> bool:
-        """2..16 rows: the LoRA down projections can run as tail workgroups of
-        the grouped R/K/V GEMV (blocked MM8 of one shape, LoRA inputs in the
-        activation dtype and of the model width)."""
-        if not self.rkv_lora_tail or not 1 <= B <= GEMV_ROWS:
+        """Up to 64 rows: the LoRA down projections can run as tail workgroups
+        of the grouped R/K/V launch (the GEMV up to 16 rows, the tile GEMM
+        above; blocked MM8 of one shape, LoRA inputs in the activation dtype
+        and of the model width)."""
+        if not self.rkv_lora_tail or not 1 <= B <= 64:
             return False
         lins = (L.r_proj, L.k_proj, L.v_proj)
         if not all(isinstance(l, QuantLinear) and is_blocked(l.m.w_blk) for l in lins):
@@ -1042,7 +1048,7 @@ class NativeRWKV7ForCausalLM:
                 down_sums, down_splits = (bufs["ldown"], 1) if fmix else (None, 1)
                 if not fmix:
                     if self._rkv_lora_fusable(L, B):
-                        down_sums, down_splits = bufs["ldown_tail"], self.RKV_LORA_SPLITS
+                        down_sums, down_splits = bufs["ldown_tail"], self._rkv_lora_splits(B)
                         mm8_matmul_multi_lora_into([xr, xk, xv], [L.r_proj.m, L.k_proj.m, L.v_proj.m],
                                                    [rkv[0], rkv[1], rkv[2]], [xw, xa, xg, xv][:n], L.lora_down,
                                                    down_sums, splits=down_splits)

@@ -230,9 +230,10 @@ def mm8_matmul_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
 
 
 def mm8_matmul_multi_lora_into(xs, mods, outs, lora_xs, lora_downs, lora_part, *, splits: int = 4):
-    """:func:`mm8_matmul_multi_into` (at most 16 rows, no split K) with the
-    decode LoRA down projections in the same launch, on the workgroups the
-    products leave free: ``lora_part`` (fp32, contiguous) receives
+    """:func:`mm8_matmul_multi_into` (at most 16 rows, no split K) or, for
+    17..64 rows, :func:`mm8_gemm_multi_into`, with the decode LoRA down
+    projections in the same launch, on the workgroups the products leave free:
+    ``lora_part`` (fp32, contiguous) receives
     ``[p][z][row][n] = sum_{k in range z} lora_xs[p][row, k] lora_downs[p][n, k]``
     over ``splits`` K ranges, the layout the fused wkv decode kernel reads
     (``down_splits=splits``)."""
@@ -263,6 +264,17 @@ def mm8_matmul_multi_lora_into(xs, mods, outs, lora_xs, lora_downs, lora_part, *
     _lib.require_gpu(*xs, *outs, *lora_xs, *lora_downs, lora_part, name="mm8_matmul_multi_lora")
     arr = lambda ts: _lib.ptr_array(ts)
     eps = (ctypes.c_int * k)(*([_lib.EPI_NONE] * k))
+    if rows > GEMV_ROWS:
+        ws = _ws.reserve(xs[0].device, mm8_gemm_workspace_bytes(k, rows, n, m, 0), slot="mm8g")
+        _lib.call(
+            "rwkv7mi_mm8t_gemm_multi_lora", k, arr(xs), arr([md.w_blk for md in mods]),
+            arr([md.mx for md in mods]), arr([md.rx for md in mods]), arr([md.my for md in mods]),
+            arr([md.ry for md in mods]), arr([md.bias for md in mods]), arr([None] * k), arr(outs), eps,
+            rows, n, m, _lib.dtype_code(xs[0]), _lib.dtype_code(mods[0].mx), 0, _lib.ptr(ws), int(ws.numel()),
+            kl, arr(lora_xs), arr(lora_downs), (ctypes.c_int64 * kl)(*ranks), int(splits), _lib.ptr(lora_part),
+            int(lora_part.numel()) * 4, _lib.stream_of(xs[0]),
+        )
+        return outs
     _lib.call(
         "rwkv7mi_mm8t_matmul_multi_lora", k, arr(xs), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
         arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),

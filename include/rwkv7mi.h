@@ -321,6 +321,28 @@ int rwkv7mi_mm8t_gemm_multi(int nprob, const void* const* x,
                             int splits, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* rwkv7mi_mm8t_gemm_multi (17..64 rows) with the decode LoRA down
+ * projections as tail workgroups of the tile launch, the same partial layout
+ * as rwkv7mi_mm8t_matmul_multi_lora.  The products are those of the plain
+ * call.  Replaces the grouped R/K/V dispatch plus fused_wavg_lora's down
+ * launch of the decode step (rwkv7_hf/native_jit_graph_dispatch.py:449-801,
+ * rwkv7_hf/fused_lora.py:706). */
+int rwkv7mi_mm8t_gemm_multi_lora(int nprob, const void* const* x,
+                                 const uint8_t* const* w_blk,
+                                 const void* const* mx, const void* const* rx,
+                                 const void* const* my, const void* const* ry,
+                                 const void* const* bias,
+                                 const void* const* residual, void* const* y,
+                                 const int* epilogue, int64_t rows, int64_t I,
+                                 int64_t O, int act_dtype, int meta_dtype,
+                                 int splits, void* workspace,
+                                 size_t workspace_bytes, int64_t lora_nprob,
+                                 const void* const* lora_x,
+                                 const void* const* lora_w_down,
+                                 const int64_t* lora_ranks, int64_t lora_splits,
+                                 float* lora_part, size_t lora_part_bytes,
+                                 void* stream);
+
 /* Prefill GEMM over the blocked layout for many rows (long prompts): up to
  * four problems of one shape, y = epilogue(x @ W_hat (+ bias)), on 256 x 256
  * MFMA tiles that dequantise the MM8 bytes in registers -- the weight is

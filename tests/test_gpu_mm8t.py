@@ -194,14 +194,16 @@ def test_mm8t_multi_equals_single(rows):
 
 
 @pytest.mark.parametrize("rows,I,O,ranks,splits", [(8, 4096, 4096, (64, 64, 128, 32), 4), (2, 512, 384, (64, 64, 128), 4),
-                                                   (16, 1024, 256, (16, 8, 256, 24), 3), (3, 4096, 1024, (64,), 1)])
+                                                   (16, 1024, 256, (16, 8, 256, 24), 3), (3, 4096, 1024, (64,), 1),
+                                                   (64, 4096, 4096, (64, 64, 128, 32), 8), (24, 1024, 512, (64, 64, 128), 4),
+                                                   (41, 2048, 384, (16, 8, 256, 24), 3)])
 def test_mm8t_multi_lora_tail(rows, I, O, ranks, splits):
-    """The grouped GEMV with the LoRA down projections as tail workgroups: the
-    products equal the plain grouped launch bit for bit, and the down partials
+    """The grouped GEMV (up to 16 rows) or tile GEMM (17..64) with the LoRA down
+    projections as tail workgroups: the products equal the plain grouped launch bit for bit, and the down partials
     summed over the K ranges match an fp32 torch product (the reference's
     ``x @ W_down^T``, rwkv7_hf/fused_lora.py:795-803) on the same fp16 operands."""
     from rwkv7mi import MM8Linear
-    from rwkv7mi.native_quant_mm8 import mm8_matmul_multi_into, mm8_matmul_multi_lora_into
+    from rwkv7mi.native_quant_mm8 import mm8_gemm_multi_into, mm8_matmul_multi_into, mm8_matmul_multi_lora_into
 
     rng = np.random.default_rng(rows * 131 + I + len(ranks))
     mods, xs = [], []
@@ -217,7 +219,7 @@ def test_mm8t_multi_lora_tail(rows, I, O, ranks, splits):
     outs = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(3)]
     plain = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(3)]
     mm8_matmul_multi_lora_into(xs, mods, outs, lxs, lws, part, splits=splits)
-    mm8_matmul_multi_into(xs, mods, plain)
+    (mm8_matmul_multi_into if rows <= 16 else mm8_gemm_multi_into)(xs, mods, plain)
     torch.cuda.synchronize()
     for a, b in zip(outs, plain):
         assert torch.equal(a, b)
@@ -246,10 +248,10 @@ def test_mm8t_multi_lora_rejects():
     with pytest.raises(ValueError):  # rank not a multiple of 8
         mm8_matmul_multi_lora_into([x], [m], [out], [x], [lw[:60].contiguous()],
                                    torch.empty(4096, device="cuda"), splits=4)
-    x17 = torch.randn(17, I, device="cuda", dtype=torch.float16)
-    with pytest.raises(ValueError):  # more than 16 rows
-        mm8_matmul_multi_lora_into([x17], [m], [torch.empty(17, O, device="cuda", dtype=torch.float16)], [x17], [lw],
-                                   torch.empty(8192, device="cuda"), splits=4)
+    x65 = torch.randn(65, I, device="cuda", dtype=torch.float16)
+    with pytest.raises(ValueError):  # more than 64 rows
+        mm8_matmul_multi_lora_into([x65], [m], [torch.empty(65, O, device="cuda", dtype=torch.float16)], [x65], [lw],
+                                   torch.empty(65536, device="cuda"), splits=4)
 
 
 @pytest.mark.parametrize("IO", [(256, 512), (4096, 1024)])
