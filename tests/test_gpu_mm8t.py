@@ -197,27 +197,31 @@ def test_mm8t_multi_equals_single(rows):
                                                    (16, 1024, 256, (16, 8, 256, 24), 3), (3, 4096, 1024, (64,), 1),
                                                    (64, 4096, 4096, (64, 64, 128, 32), 8), (24, 1024, 512, (64, 64, 128), 4),
                                                    (41, 2048, 384, (16, 8, 256, 24), 3)])
-def test_mm8t_multi_lora_tail(rows, I, O, ranks, splits):
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+def test_mm8t_multi_lora_tail(rows, I, O, ranks, splits, dt):
     """The grouped GEMV (up to 16 rows) or tile GEMM (17..64) with the LoRA down
     projections as tail workgroups: the products equal the plain grouped launch bit for bit, and the down partials
     summed over the K ranges match an fp32 torch product (the reference's
-    ``x @ W_down^T``, rwkv7_hf/fused_lora.py:795-803) on the same fp16 operands."""
+    ``x @ W_down^T``, rwkv7_hf/fused_lora.py:795-803) on the same operands
+    (fp32 and bf16 ones split into fp16 hi + lo, ~2^-22 relative)."""
     from rwkv7mi import MM8Linear
     from rwkv7mi.native_quant_mm8 import mm8_gemm_multi_into, mm8_matmul_multi_into, mm8_matmul_multi_lora_into
 
+    if dt != torch.float16 and rows not in (8, 24):
+        pytest.skip("bf16 / fp32 at one GEMV and one tile-GEMM shape")
     rng = np.random.default_rng(rows * 131 + I + len(ranks))
     mods, xs = [], []
     for p in range(3):
-        lin = torch.nn.Linear(I, O, bias=(p == 1)).to(device="cuda", dtype=torch.float16)
+        lin = torch.nn.Linear(I, O, bias=(p == 1)).to(device="cuda", dtype=dt)
         with torch.no_grad():
-            lin.weight.copy_(_cuda(rng.standard_normal((O, I)) * 0.02, torch.float16))
+            lin.weight.copy_(_cuda(rng.standard_normal((O, I)) * 0.02, dt))
         mods.append(MM8Linear(lin))
-        xs.append(_cuda(rng.standard_normal((rows, I)), torch.float16))
-    lxs = [_cuda(rng.standard_normal((rows, I)), torch.float16) for _ in ranks]
-    lws = [_cuda(rng.standard_normal((r, I)) * 0.05, torch.float16) for r in ranks]
+        xs.append(_cuda(rng.standard_normal((rows, I)), dt))
+    lxs = [_cuda(rng.standard_normal((rows, I)), dt) for _ in ranks]
+    lws = [_cuda(rng.standard_normal((r, I)) * 0.05, dt) for r in ranks]
     part = torch.full((splits * rows * sum(ranks) + 7,), float("nan"), device="cuda", dtype=torch.float32)
-    outs = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(3)]
-    plain = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(3)]
+    outs = [torch.empty(rows, O, device="cuda", dtype=dt) for _ in range(3)]
+    plain = [torch.empty(rows, O, device="cuda", dtype=dt) for _ in range(3)]
     mm8_matmul_multi_lora_into(xs, mods, outs, lxs, lws, part, splits=splits)
     (mm8_matmul_multi_into if rows <= 16 else mm8_gemm_multi_into)(xs, mods, plain)
     torch.cuda.synchronize()
