@@ -193,11 +193,17 @@ def test_mm8t_multi_equals_single(rows):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("rows,I,O,ranks,splits", [(8, 4096, 4096, (64, 64, 128, 32), 4), (2, 512, 384, (64, 64, 128), 4),
-                                                   (16, 1024, 256, (16, 8, 256, 24), 3), (3, 4096, 1024, (64,), 1),
-                                                   (64, 4096, 4096, (64, 64, 128, 32), 8), (24, 1024, 512, (64, 64, 128), 4),
-                                                   (41, 2048, 384, (16, 8, 256, 24), 3)])
-@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+_LORA_TAIL_CASES = [(8, 4096, 4096, (64, 64, 128, 32), 4), (2, 512, 384, (64, 64, 128), 4),
+                    (16, 1024, 256, (16, 8, 256, 24), 3), (3, 4096, 1024, (64,), 1),
+                    (64, 4096, 4096, (64, 64, 128, 32), 8), (24, 1024, 512, (64, 64, 128), 4),
+                    (41, 2048, 384, (16, 8, 256, 24), 3)]
+
+
+# fp16 at every shape; bf16 and fp32 at one GEMV (8 rows) and one tile-GEMM (24 rows) shape
+@pytest.mark.parametrize("rows,I,O,ranks,splits,dt",
+                         [c + (torch.float16,) for c in _LORA_TAIL_CASES]
+                         + [c + (dt,) for c in _LORA_TAIL_CASES if c[0] in (8, 24)
+                            for dt in (torch.bfloat16, torch.float32)])
 def test_mm8t_multi_lora_tail(rows, I, O, ranks, splits, dt):
     """The grouped GEMV (up to 16 rows) or tile GEMM (17..64) with the LoRA down
     projections as tail workgroups: the products equal the plain grouped launch bit for bit, and the down partials
@@ -207,8 +213,6 @@ def test_mm8t_multi_lora_tail(rows, I, O, ranks, splits, dt):
     from rwkv7mi import MM8Linear
     from rwkv7mi.native_quant_mm8 import mm8_gemm_multi_into, mm8_matmul_multi_into, mm8_matmul_multi_lora_into
 
-    if dt != torch.float16 and rows not in (8, 24):
-        pytest.skip("bf16 / fp32 at one GEMV and one tile-GEMM shape")
     rng = np.random.default_rng(rows * 131 + I + len(ranks))
     mods, xs = [], []
     for p in range(3):
