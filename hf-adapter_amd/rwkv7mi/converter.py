@@ -52,51 +52,60 @@ _ALLOWED_MISSING = ("model.layers.0.pre_norm.weight", "model.layers.0.pre_norm.b
 
 # ------------------------------------------------------------- inference
 def tensor_shape(weights: Dict[str, torch.Tensor], name: str) -> tuple:
-    if name not in weights:
-        raise KeyError(f"Missing required RWKV-7 weight: {name}")
-    return tuple(int(v) for v in weights[name].shape)
+    """The shape of checkpoint entry ``name`` (KeyError when it is absent)."""
+    t = weights.get(name)
+    if t is None:
+        raise KeyError(f"checkpoint lacks {name}")
+    return tuple(map(int, t.shape))
+
+
+_BLOCK_KEY = re.compile(r"blocks\.(\d+)\.ffn\.key\.weight")
 
 
 def infer_num_layers(weights: Dict[str, torch.Tensor]) -> int:
-    """Contiguous block indices from ``blocks.*.ffn.key.weight``."""
-    layers = sorted(int(m.group(1)) for name in weights if (m := re.match(r"blocks\.(\d+)\.ffn\.key\.weight$", name)))
-    if not layers:
-        raise KeyError("No blocks.*.ffn.key.weight tensors found in checkpoint")
-    if layers != list(range(layers[-1] + 1)):
-        raise ValueError(f"RWKV block indices must be contiguous from 0: got {layers[:20]} ...")
-    return len(layers)
+    """Layer count: the FFN key matrices must be numbered 0 .. L-1 with no gap."""
+    found = {int(m.group(1)) for m in map(_BLOCK_KEY.fullmatch, weights) if m}
+    if not found:
+        raise KeyError("checkpoint has no blocks.<i>.ffn.key.weight entries")
+    n = max(found) + 1
+    gaps = sorted(set(range(n)) - found)
+    if gaps:
+        raise ValueError(f"block numbering is not contiguous from 0 (absent: {gaps[:8]})")
+    return n
 
 
 def infer_attention_shape(weights: Dict[str, torch.Tensor]) -> tuple:
-    """(H, N, A) from ``blocks.0.att.r_k`` (trailing [H, N])."""
+    """``(heads, head_dim, heads * head_dim)``, read from the last two
+    dimensions of layer 0's ``r_k``."""
     rk = tensor_shape(weights, "blocks.0.att.r_k")
-    if len(rk) < 2:
-        raise ValueError(f"Cannot infer attention shape from blocks.0.att.r_k={rk}")
-    h, n = (int(v) for v in rk[-2:])
-    if h <= 0 or n <= 0:
-        raise ValueError(f"Invalid attention shape from blocks.0.att.r_k={rk}")
-    return h, n, h * n
+    heads, head_dim = (rk[-2], rk[-1]) if len(rk) >= 2 else (0, 0)
+    if heads < 1 or head_dim < 1:
+        raise ValueError(f"blocks.0.att.r_k {rk} does not end in (heads, head_dim)")
+    return heads, head_dim, heads * head_dim
 
 
-def _expect(weights, name, shape):
-    got = tensor_shape(weights, name)
-    if got != tuple(shape):
-        raise ValueError(f"{name} has shape {got}; expected {tuple(shape)}")
+def _layer_expectations(i: int, hidden: int, attn: int) -> dict:
+    """The exact shapes every layer's projections and group norm must have."""
+    att = f"blocks.{i}.att."
+    return {att + "receptance.weight": (attn, hidden), att + "key.weight": (attn, hidden),
+            att + "value.weight": (attn, hidden), att + "output.weight": (hidden, attn),
+            att + "ln_x.weight": (attn,), att + "ln_x.bias": (attn,)}
 
 
 def validate_layer_shapes(weights, num_layers, hidden, heads, head_dim, attn):
+    """Check every layer against layer 0's geometry: FFN key input width,
+    ``r_k`` = [1 .., heads, head_dim], and the table of projection shapes."""
     for i in range(num_layers):
         fk = tensor_shape(weights, f"blocks.{i}.ffn.key.weight")
         if len(fk) != 2 or fk[1] != hidden:
-            raise ValueError(f"blocks.{i}.ffn.key.weight has inconsistent shape {fk}")
+            raise ValueError(f"blocks.{i}.ffn.key.weight {fk}: input width is not {hidden}")
         rk = tensor_shape(weights, f"blocks.{i}.att.r_k")
-        if len(rk) < 2 or rk[-2:] != (heads, head_dim) or any(d != 1 for d in rk[:-2]):
-            raise ValueError(f"blocks.{i}.att.r_k has shape {rk}; expected trailing ({heads}, {head_dim})")
-        for proj in ("receptance", "key", "value"):
-            _expect(weights, f"blocks.{i}.att.{proj}.weight", (attn, hidden))
-        _expect(weights, f"blocks.{i}.att.output.weight", (hidden, attn))
-        for aff in ("weight", "bias"):
-            _expect(weights, f"blocks.{i}.att.ln_x.{aff}", (attn,))
+        if rk[-2:] != (heads, head_dim) or set(rk[:-2]) - {1}:
+            raise ValueError(f"blocks.{i}.att.r_k {rk}: not [1.., {heads}, {head_dim}]")
+        for name, want in _layer_expectations(i, hidden, attn).items():
+            got = tensor_shape(weights, name)
+            if got != want:
+                raise ValueError(f"{name} {got}: this geometry needs {want}")
 
 
 def infer_config(weights: Dict[str, torch.Tensor]):
@@ -328,6 +337,8 @@ def validate_manifest(manifest: dict, cfg, dtype: torch.dtype) -> None:
 
     if manifest.get("format") != PREPACKED_FORMAT:
         raise ValueError(f"unsupported prepacked format {manifest.get('format')!r} (expected {PREPACKED_FORMAT})")
+    if manifest.get("packer_version") != PACKER_VERSION:
+        raise ValueError(f"prepacked by {manifest.get('packer_version')!r}; this build reads {PACKER_VERSION!r}")
     from .model import parameter_shapes
 
     shapes = parameter_shapes(cfg)
@@ -343,16 +354,25 @@ def validate_manifest(manifest: dict, cfg, dtype: torch.dtype) -> None:
             raise ValueError(f"{name}: features {(e.get('input_features'), e.get('output_features'))} vs ({i}, {o})")
         if list(e.get("blocked_shape", [])) != list(mm8_block_shape(i, o)):
             raise ValueError(f"{name}: blocked shape {e.get('blocked_shape')} vs {list(mm8_block_shape(i, o))}")
-        if e.get("activation_dtype") != str(dtype).replace("torch.", ""):
+        dname = str(dtype).replace("torch.", "")
+        if e.get("activation_dtype") != dname:
             raise ValueError(f"{name}: packed for {e.get('activation_dtype')} activations, loading {dtype}")
+        if e.get("scale_dtype") != dname:  # the kernels read mx / rx / my / ry in the activation dtype
+            raise ValueError(f"{name}: scales stored as {e.get('scale_dtype')}, the kernels need {dname}")
+        if e.get("packer_version") != PACKER_VERSION:
+            raise ValueError(f"{name}: packer {e.get('packer_version')!r}, this build reads {PACKER_VERSION!r}")
         if name in seen:
             raise ValueError(f"{name}: listed twice")
         seen.add(name)
 
 
-def load_prepacked(path, *, device="cuda", dtype=torch.float16):
+def load_prepacked(path, *, device="cuda", dtype=torch.float16,
+                   source_state: Dict[str, torch.Tensor] | None = None):
     """The model from a prepacked directory: the manifest is validated, then
-    the MM8 modules are built from the stored bytes (no quantisation)."""
+    the MM8 modules are built from the stored bytes (no quantisation).  Each
+    stored tensor must have the dtype the manifest declares.  With
+    ``source_state`` (the unquantised HF state dict), every module's
+    ``source_weight_sha256`` is checked against it."""
     from safetensors.torch import load_file
 
     from .model import NativeRWKV7ForCausalLM
@@ -371,7 +391,20 @@ def load_prepacked(path, *, device="cuda", dtype=torch.float16):
     prebuilt = {}
     for e in manifest["modules"]:
         n = e["module"]
+        missing = [f for f in ("w_blk", "mx", "rx", "my", "ry") if f"{n}.{f}" not in packed]
+        if missing:
+            raise ValueError(f"{n}: prepacked.safetensors lacks {missing}")
         t = {f: packed[f"{n}.{f}"] for f in ("w_blk", "mx", "rx", "my", "ry")}
+        for f in ("mx", "rx", "my", "ry"):
+            if str(t[f].dtype).replace("torch.", "") != e["scale_dtype"]:
+                raise ValueError(f"{n}.{f}: stored as {t[f].dtype}, manifest says {e['scale_dtype']}")
+        if source_state is not None:
+            want = e.get("source_weight_sha256")
+            src = source_state.get(n + ".weight")
+            if want is None or src is None:
+                raise ValueError(f"{n}: cannot verify the source weight (no digest or no source tensor)")
+            if _sha256(src) != want:
+                raise ValueError(f"{n}: source weight digest differs from the one it was packed from")
         prebuilt[n] = MM8Linear.from_packed(t["w_blk"].to(device), t["mx"].to(device), t["rx"].to(device),
                                            t["my"].to(device), t["ry"].to(device), e["input_features"],
                                            e["output_features"])

@@ -38,7 +38,7 @@ from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_
                                mm8_matmul_multi_lora_into,
                                mm8_matmul_partials, mm8t_workspace_bytes)
 from .native_quant_policy import should_quantize_linear
-from .self_chunk_rwkv7 import _run_chunk
+from .self_chunk_rwkv7 import _run_chunk, check_wkv7_chunk_status
 
 EXP_HALF = 0.606531
 
@@ -1235,6 +1235,12 @@ class NativeRWKV7ForCausalLM:
         self.lm_head.apply(h, logits)
         cache.seen_tokens = cache.seen_tokens + T
         cache._invalidate_native_graph_binding()
+        if not torch.cuda.is_current_stream_capturing():
+            # the chunk kernel's bounded inter-wave waits report a give-up in a
+            # sticky status word; an eager prefill raises on it (one device
+            # synchronisation per call).  A captured prefill is checked after
+            # each replay (NativePrefillGraphRunner.replay).
+            check_wkv7_chunk_status()
         return logits.view(B, keep, cfg.vocab_size)
 
     # ------------------------------------------------------------- API
@@ -1431,6 +1437,7 @@ class NativeGraphRunner:
             self._step()
         self._copy_into(snapshot)
         self.replays = 0
+        self._bound_cache_ref = None
 
     def _step(self) -> None:
         """The captured work: one decode step, then the greedy tokens."""
@@ -1443,12 +1450,34 @@ class NativeGraphRunner:
         for dst, src in zip((*s, *a, *f, v), (*s2, *a2, *f2, v2)):
             dst.copy_(src)
 
+    def detach_bound_cache(self, keep: NativeRWKV7Cache | None = None) -> None:
+        """Give the cache bound to this runner (unless it is ``keep``) its own
+        copy of the runner's buffers and unbind it, before anything else
+        writes those buffers: another cache's copy-in, or a state pool's
+        gather (rwkv7_hf/native_graph_runtime.py:618-630).  The copy keeps the
+        layer-major storage of :meth:`NativeRWKV7Cache.zeros`."""
+        prev = self._bound_cache_ref() if self._bound_cache_ref is not None else None
+        if prev is not None and prev is keep:
+            return
+        self._bound_cache_ref = None
+        if prev is None or not prev._native_graph_bound_to(self):
+            return
+        s, a, f, v = self.cache
+        prev._state = list(torch.stack(s).unbind(0))
+        prev._xpa = list(torch.stack(a).unbind(0))
+        prev._xpf = list(torch.stack(f).unbind(0))
+        prev._v_first = v.clone()
+        prev._invalidate_native_graph_binding()
+
     def bind_cache(self, cache: NativeRWKV7Cache) -> None:
-        """The cache's tensors become this runner's buffers (no copies per step)."""
+        """The cache's tensors become this runner's buffers (no copies per
+        step).  A different cache bound before keeps its state as a copy."""
+        self.detach_bound_cache(keep=cache)
         cache._state, cache._xpa, cache._xpf, cache._v_first = (
             list(self.cache._state), list(self.cache._xpa), list(self.cache._xpf), self.cache._v_first)
         cache._invalidate_native_graph_binding()
         cache._bind_native_graph_runner(self)
+        self._bound_cache_ref = weakref.ref(cache)
 
     def reorder_batch_inplace(self, indices: torch.Tensor) -> bool:
         """Permute the bound batch rows in place (beam search on a bound cache)."""
@@ -1464,6 +1493,7 @@ class NativeGraphRunner:
         if cache.get_batch_size() not in (None, self.batch):
             raise ValueError(f"graph runner for batch {self.batch} got a cache of batch {cache.get_batch_size()}")
         if not cache._native_graph_bound_to(self):
+            self.detach_bound_cache(keep=cache)
             self._copy_into(cache)
             self.bind_cache(cache)
         self.tokens.copy_(tokens.reshape(-1))
@@ -1556,6 +1586,7 @@ class NativePrefillGraphRunner:
         self.ids.copy_(input_ids)
         self.graph.replay()
         self.replays += 1
+        check_wkv7_chunk_status()
         if not copy:
             out = NativeRWKV7Cache(list(self.cache._state), list(self.cache._xpa), list(self.cache._xpf),
                                    self.cache._v_first, seen + self.tokens_n)

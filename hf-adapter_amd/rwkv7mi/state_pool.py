@@ -315,6 +315,7 @@ class PooledDecoder:
         tok[:n] = torch.as_tensor(tokens, dtype=torch.long, device=self.pool.device).reshape(-1)
         if self.use_graph:
             runner = self.model.graph_runner(b)
+            runner.detach_bound_cache()  # a user cache bound to this bucket keeps its own state
             cache = runner.cache  # the captured graph's own (layer-major) buffers
             self.pool.gather_cache(rows, cache, allow_scratch=True)
             runner.tokens.copy_(tok)
@@ -324,7 +325,7 @@ class PooledDecoder:
             cache = self.pool.gather_cache(rows, allow_scratch=True)
             logits = self.model(tok[:, None], past_key_values=cache, use_graph=False).logits[:, -1]
         self.pool.scatter_cache(rows, cache, active, advance=1)
-        return logits[:n]
+        return logits[:n].clone()  # the runner's buffer is overwritten by the bucket's next replay
 
 
 __all__ = ["RWKV7StatePool", "PooledDecoder", "LAYOUT_VERSION"]

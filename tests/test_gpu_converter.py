@@ -52,7 +52,8 @@ def test_prepacked_round_trip(tmp_path):
 
 
 @pytest.mark.parametrize("field,value", [("input_features", 7), ("format", "other.v0"),
-                                         ("activation_dtype", "bfloat16"), ("blocked_shape", [1, 1, 2048])])
+                                         ("activation_dtype", "bfloat16"), ("blocked_shape", [1, 1, 2048]),
+                                         ("packer_version", "rwkv7mi-mm8-0"), ("scale_dtype", "float32")])
 def test_prepacked_manifest_rejects(tmp_path, field, value):
     from rwkv7mi import converter as conv
     from rwkv7mi.model import NativeRWKV7ForCausalLM, random_weights
@@ -82,3 +83,23 @@ def test_converted_directory_loads(tmp_path):
     m2 = NativeRWKV7ForCausalLM(cfg, w, device="cuda", dtype=torch.float16)
     ids = torch.randint(0, cfg.vocab_size, (1, 5), device="cuda")
     assert torch.equal(m1(ids, use_graph=False).logits, m2(ids, use_graph=False).logits)
+
+
+def test_prepacked_source_digest_checked(tmp_path):
+    """load_prepacked(source_state=...) accepts the weights a directory was
+    packed from and refuses a changed one."""
+    from rwkv7mi import converter as conv
+    from rwkv7mi.model import NativeRWKV7ForCausalLM, random_weights
+
+    cfg = _cfg()
+    w = random_weights(cfg, seed=4, dtype=torch.float16)
+    cfg.use_native_mm8 = True
+    model = NativeRWKV7ForCausalLM(cfg, w, device="cuda", dtype=torch.float16)
+    man = conv.save_prepacked(model, tmp_path, source_state=w)
+    conv.load_prepacked(tmp_path, device="cuda", dtype=torch.float16, source_state=w)
+    name = man["modules"][0]["module"] + ".weight"
+    changed = dict(w)
+    changed[name] = w[name].clone()
+    changed[name].view(-1)[0] += 1
+    with pytest.raises(ValueError, match="digest"):
+        conv.load_prepacked(tmp_path, device="cuda", dtype=torch.float16, source_state=changed)

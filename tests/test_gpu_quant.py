@@ -252,3 +252,67 @@ def test_w4_stream_gemv_epilogues(oracle, rows):
     rr = np.maximum(base, 0) ** 2
     assert np.abs(_np(r2) - rr).max() <= 4e-3 * np.abs(rr).max()
     assert np.abs(_np(res) - want_res).max() <= 2e-3 * np.abs(want_res).max()
+
+
+# ---------------------------------------------------------------- reference bytes
+# The device packers against the reference packers' own outputs
+# (tests/golden/quant_packers.npz, written by tests/golden/make_quant_golden.py
+# from rwkv7_hf/native_quant_mm8.py:62-97, native_quant_mm4.py:77-105 and
+# sm70_quant.py:502-519): every byte and every scale bit.
+import quant_golden as qg  # noqa: E402
+
+
+def _dt(W):
+    return torch.float16 if W.dtype == np.float16 else torch.float32
+
+
+def _assert_bits(got, ref, what):
+    got = _np(got)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    np.testing.assert_array_equal(qg.bits(got), qg.bits(ref), err_msg=what)
+
+
+@pytest.mark.parametrize("name", qg.cases("mm8"))
+def test_mm8_device_packers_match_reference_bytes(name):
+    from rwkv7mi.native_quant_mm8 import MM8Linear, quantize_mm8
+
+    c = qg.case("mm8", name)
+    W = _cuda(c["W"], _dt(c["W"]))
+    for got, key in zip(quantize_mm8(W), ("w_u8", "mx", "rx", "my", "ry")):
+        _assert_bits(got, c[key], f"{name} {key}")
+    # the module's blocked packer (nn.Linear.weight = W^T) materialises the same reference tensors
+    lin = torch.nn.Linear(W.shape[0], W.shape[1], bias=False, device="cuda", dtype=W.dtype)
+    with torch.no_grad():
+        lin.weight.copy_(W.t())
+    mod = MM8Linear(lin)
+    for key in ("w_u8", "mx", "rx", "my", "ry"):
+        _assert_bits(getattr(mod, key), c[key], f"{name} MM8Linear {key}")
+
+
+@pytest.mark.parametrize("name", qg.cases("mm4"))
+def test_mm4_device_packers_match_reference_bytes(name):
+    from rwkv7mi.native_quant_mm4 import outmajor_to_reference, quantize_mm4, quantize_mm4_outmajor
+
+    c = qg.case("mm4", name)
+    W = _cuda(c["W"], _dt(c["W"]))
+    packed, mx, rx, my, ry, m_orig, m_pad = quantize_mm4(W)
+    assert [m_orig, m_pad] == c["m"].tolist()
+    for got, key in ((packed, "packed"), (mx, "mx"), (rx, "rx"), (my, "my"), (ry, "ry")):
+        _assert_bits(got, c[key], f"{name} {key}")
+    if W.shape[0] % 2 == 0:  # the module's out-major packer needs an even in_features
+        pt, mx2, rx2, my2, ry2, _, _ = quantize_mm4_outmajor(W.t().contiguous())
+        _assert_bits(outmajor_to_reference(pt, W.shape[0]), c["packed"], f"{name} out-major packed")
+        for got, key in ((mx2, "mx"), (rx2, "rx"), (my2, "my"), (ry2, "ry")):
+            _assert_bits(got, c[key], f"{name} out-major {key}")
+
+
+@pytest.mark.parametrize("name", qg.cases("w4g"))
+def test_w4g_device_packer_matches_reference_bytes(name):
+    from rwkv7mi import quantize_w4_groupwise
+
+    c = qg.case("w4g", name)
+    group, k = c["group"].tolist()
+    packed, scales, kk = quantize_w4_groupwise(_cuda(c["W"], _dt(c["W"])), group_size=group)
+    assert kk == k
+    _assert_bits(packed, c["packed"], f"{name} packed")
+    _assert_bits(scales, c["scales"], f"{name} scales")

@@ -166,3 +166,38 @@ def test_continuous_batching_matches_isolated_runs(model):
                        use_graph=False).logits[0, -1].float()
             ref = got[r][j]
             assert (lg - ref).abs().max().item() <= 2e-2 * max(1.0, lg.abs().max().item()), (r, j)
+
+
+def test_two_bound_caches_alternate_and_pool_step_between(model):
+    """Two bsz-1 caches alternating through the bsz-1 decode graph each keep
+    their own state: rebinding the runner gives the previously bound cache a
+    copy of the runner's buffers (rwkv7_hf/native_graph_runtime.py:618-630).
+    A pooled step on the same bucket in between leaves a bound cache's state
+    alone, and its returned logits survive the bucket's next replay."""
+    from rwkv7mi.state_pool import PooledDecoder, RWKV7StatePool
+
+    cfg = model.config
+    rng = np.random.default_rng(5)
+    prompts = [torch.tensor(rng.integers(0, cfg.vocab_size, (1, T)), device="cuda") for T in (6, 4)]
+    toks = rng.integers(0, cfg.vocab_size, (2, 4))
+    graph_caches = [model(p).past_key_values for p in prompts]
+    eager_caches = [model(p).past_key_values for p in prompts]
+    pool = RWKV7StatePool(cfg, 2, device="cuda")
+    dec = PooledDecoder(model, pool)
+    (slot, gen), = pool.allocate(["x"])
+    dec.prefill([slot], [gen], prompts[1])
+    kept = None
+    for j in range(4):
+        for i in (0, 1):
+            t = torch.tensor([[int(toks[i, j])]], device="cuda")
+            got = model(t, past_key_values=graph_caches[i], use_graph=True).logits
+            ref = model(t, past_key_values=eager_caches[i], use_graph=False).logits
+            assert torch.equal(got, ref), (i, j)
+        if j == 1:  # a pooled step on the bsz-1 bucket while cache 1 is bound to it
+            kept = dec.step([slot], [gen], [int(toks[1, 0])])
+            kept_copy = kept.clone()
+    torch.cuda.synchronize()
+    assert torch.equal(kept, kept_copy)  # not overwritten by later replays of the bucket
+    for gc, ec in zip(graph_caches, eager_caches):
+        for l in range(cfg.num_hidden_layers):
+            assert torch.equal(gc._state[l], ec._state[l]) and torch.equal(gc._xpa[l], ec._xpa[l])

@@ -150,3 +150,98 @@ def test_w4a_pack_closed_forms(oracle):
     planted = (np.clip(np.rint(W.reshape(O, -1, G) / s32.reshape(O, -1, G)[..., :1]), -8, 7)
                * s32.reshape(O, -1, G)[..., :1]).reshape(O, I)
     assert (np.abs(planted - W) > bound).any()
+
+
+# ---------------------------------------------------------------- reference bytes
+# tests/golden/quant_packers.npz holds the reference packers' own outputs
+# (rwkv7_hf/native_quant_mm8.py:62-97, native_quant_mm4.py:77-105,
+# sm70_quant.py:502-519) on seeded and edge inputs, fp16 and fp32, both branch
+# orders, odd MM4 widths and groups 128 / 256.  The oracle must reproduce every
+# byte and every scale bit.
+import quant_golden as qg  # noqa: E402
+
+
+def _np_dtype(W):
+    return np.float16 if W.dtype == np.float16 else np.float32
+
+
+@pytest.mark.parametrize("name", qg.cases("mm8"))
+def test_mm8_pack_matches_reference_bytes(oracle, name):
+    c = qg.case("mm8", name)
+    got = oracle.mm8_pack(c["W"].astype(np.float32), out_dtype=_np_dtype(c["W"]))
+    for g, key in zip(got, ("w_u8", "mx", "rx", "my", "ry")):
+        assert g.shape == c[key].shape, key
+        np.testing.assert_array_equal(qg.bits(g), qg.bits(c[key]), err_msg=f"{name} {key}")
+
+
+@pytest.mark.parametrize("name", qg.cases("mm4"))
+def test_mm4_pack_matches_reference_bytes(oracle, name):
+    c = qg.case("mm4", name)
+    packed, mx, rx, my, ry, m_orig, m_pad = oracle.mm4_pack(c["W"].astype(np.float32), out_dtype=_np_dtype(c["W"]))
+    assert [m_orig, m_pad] == c["m"].tolist()
+    for g, key in ((packed, "packed"), (mx, "mx"), (rx, "rx"), (my, "my"), (ry, "ry")):
+        assert g.shape == c[key].shape, key
+        np.testing.assert_array_equal(qg.bits(g), qg.bits(c[key]), err_msg=f"{name} {key}")
+
+
+@pytest.mark.parametrize("name", qg.cases("w4g"))
+def test_w4g_pack_matches_reference_bytes(oracle, name):
+    c = qg.case("w4g", name)
+    group, k = c["group"].tolist()
+    packed, scales, kk = oracle.w4g_pack(c["W"].astype(np.float32), group, out_dtype=_np_dtype(c["W"]))
+    assert kk == k
+    np.testing.assert_array_equal(packed, c["packed"], err_msg=name)
+    np.testing.assert_array_equal(qg.bits(scales), qg.bits(c["scales"]), err_msg=name)
+
+
+def _affine_pack_planted(W, levels, mistake):
+    """numpy fp32 restatement of the affine packers with one planted mistake;
+    used only to show that the reference fixtures reject it."""
+    w = W.astype(np.float32)
+    n, m = w.shape
+    rows_first = n > m
+    if mistake == "branch":
+        rows_first = not rows_first
+    if rows_first:
+        my = w.min(1, keepdims=True); w = w - my
+        mx = w.min(0); w = w - mx
+    else:
+        mx = w.min(0); w = w - mx
+        my = w.min(1, keepdims=True); w = w - my
+    eps = np.float32(1e-8)
+    if mistake == "ry_before_rx":
+        ry = np.maximum(w.max(1, keepdims=True), eps); w = w / ry
+        rx = np.maximum(w.max(0), eps); w = w / rx
+    else:
+        rx = np.maximum(w.max(0), eps); w = w / rx
+        ry = np.maximum(w.max(1, keepdims=True), eps); w = w / ry
+    if mistake == "round":
+        return np.clip(np.rint(w * np.float32(levels)), 0, levels - 1).astype(np.uint8)
+    return np.clip(np.floor(w * np.float32(levels)), 0, levels - 1).astype(np.uint8)
+
+
+def test_mm8_fixtures_reject_planted_packers():
+    """The unplanted restatement reproduces the fixtures' bytes; normalising
+    rows before columns, swapping the branch order or rounding to nearest each
+    changes bytes in most cases (invariant pins alone pass such packers)."""
+    names = [n for n in qg.cases("mm8") if "edge" not in n and "33x33" not in n]
+    for name in names:
+        c = qg.case("mm8", name)
+        np.testing.assert_array_equal(_affine_pack_planted(c["W"], 256, None), c["w_u8"])
+    for mistake in ("ry_before_rx", "branch", "round"):
+        caught = sum(not np.array_equal(_affine_pack_planted(qg.case("mm8", n)["W"], 256, mistake),
+                                        qg.case("mm8", n)["w_u8"]) for n in names)
+        assert caught >= len(names) - 2, (mistake, caught, len(names))
+
+
+def test_w4g_fixtures_reject_planted_rounding():
+    """Round half away from zero (instead of torch.round's half to even) must
+    change the edge case's bytes: its group holds exact k + 0.5 quotients."""
+    c = qg.case("w4g", "f32_edge6x256_g128")
+    W = c["W"].astype(np.float32)
+    s = np.maximum(np.abs(W.reshape(6, 2, 128)).max(-1) / np.float32(7), np.float32(1e-6))
+    t = W.reshape(6, 2, 128) / s[..., None]
+    for rnd, ok in ((np.rint, True), (lambda x: np.sign(x) * np.floor(np.abs(x) + 0.5), False)):
+        q = (np.clip(rnd(t), -7, 7).astype(np.int16) + 8).reshape(6, 256)
+        packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+        assert np.array_equal(packed, c["packed"]) == ok
