@@ -18,7 +18,7 @@ from __future__ import annotations
 
 import weakref
 import zlib
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 import torch
 
@@ -43,37 +43,71 @@ from .self_chunk_rwkv7 import _run_chunk, check_wkv7_chunk_status
 EXP_HALF = 0.606531
 
 
-@dataclass
-class NativeRWKV7Config:
-    """Subset of rwkv7_hf NativeRWKV7Config that shapes the inference path."""
+try:
+    from transformers import GenerationMixin as _GenerationMixin
+    from transformers import PretrainedConfig as _PretrainedConfig
+    from transformers import PreTrainedModel as _PreTrainedModel
+except Exception:  # pragma: no cover - transformers absent: plain bases
+    _PretrainedConfig = object
 
-    vocab_size: int = 65536
-    hidden_size: int = 768
-    num_hidden_layers: int = 12
-    head_dim: int = 64
-    num_heads: int | None = None
-    intermediate_size: int | None = None
-    decay_low_rank_dim: int = 64
-    a_low_rank_dim: int = 64
-    gate_low_rank_dim: int = 128
-    v_low_rank_dim: int = 32
-    norm_eps: float = 1e-5
-    use_native_mm8: bool = False
-    native_mm8_min_params: int = 8_000_000
-    native_mm8_policy: str = "memory"
-    extra: dict = field(default_factory=dict)
+    class _PreTrainedModel(torch.nn.Module):  # type: ignore[no-redef]
+        def __init__(self, config):
+            super().__init__()
+            self.config = config
 
-    def __post_init__(self):
-        if self.num_heads is None:
-            self.num_heads = self.hidden_size // self.head_dim
-        if self.intermediate_size is None:
-            self.intermediate_size = 4 * self.hidden_size
+    class _GenerationMixin:  # type: ignore[no-redef]
+        pass
+
+
+class NativeRWKV7Config(_PretrainedConfig):
+    """The fields of the reference's ``NativeRWKV7Config`` that shape the
+    inference path (rwkv7_hf/model_config.py:25-101), as a Hugging Face
+    config of the same ``model_type``, so converted directories and
+    ``AutoConfig`` read it.  Only head size 64 has kernels here."""
+
+    model_type = "rwkv7_native"
+
+    def __init__(self, vocab_size: int = 65536, hidden_size: int = 768, num_hidden_layers: int = 12,
+                 head_dim: int = 64, num_heads: int | None = None, intermediate_size: int | None = None,
+                 decay_low_rank_dim: int = 64, a_low_rank_dim: int = 64, gate_low_rank_dim: int = 128,
+                 v_low_rank_dim: int = 32, norm_eps: float = 1e-5, use_native_mm8: bool = False,
+                 native_mm8_min_params: int = 8_000_000, native_mm8_policy: str = "memory",
+                 attention_hidden_size: int | None = None, extra: dict | None = None, **kwargs):
+        kwargs.setdefault("tie_word_embeddings", False)  # RWKV keeps an independent output head
+        kwargs.pop("num_attention_heads", None)
+        if _PretrainedConfig is not object:
+            super().__init__(**kwargs)
+        self.vocab_size = int(vocab_size)
+        self.hidden_size = int(hidden_size)
+        self.num_hidden_layers = int(num_hidden_layers)
+        self.head_dim = int(head_dim)
         if self.head_dim != 64:
             raise ValueError("rwkv7mi kernels require head_dim = 64")
+        if num_heads is None:
+            num_heads = (attention_hidden_size or self.hidden_size) // self.head_dim
+        self.num_heads = int(num_heads)
+        if attention_hidden_size is not None and int(attention_hidden_size) != self.num_heads * self.head_dim:
+            raise ValueError("attention_hidden_size must equal num_heads * head_dim")
+        self.num_attention_heads = self.num_heads
+        self.intermediate_size = int(intermediate_size) if intermediate_size is not None else 4 * self.hidden_size
+        self.decay_low_rank_dim = int(decay_low_rank_dim)
+        self.a_low_rank_dim = int(a_low_rank_dim)
+        self.gate_low_rank_dim = int(gate_low_rank_dim)
+        self.v_low_rank_dim = int(v_low_rank_dim)
+        self.norm_eps = float(norm_eps)
+        self.use_native_mm8 = bool(use_native_mm8)
+        self.native_mm8_min_params = int(native_mm8_min_params)
+        self.native_mm8_policy = native_mm8_policy
+        self.extra = dict(extra or {})
 
     @property
     def attention_hidden_size(self) -> int:
         return self.num_heads * self.head_dim
+
+    def to_dict(self) -> dict:
+        d = super().to_dict() if _PretrainedConfig is not object else dict(self.__dict__)
+        d["attention_hidden_size"] = self.attention_hidden_size
+        return d
 
 
 # ------------------------------------------------------------------ weights
@@ -667,13 +701,43 @@ class _Layer:
     pass
 
 
-class NativeRWKV7ForCausalLM:
-    """RWKV-7 causal LM (inference) over the HIP kernels; see the module docstring."""
+class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
+    """RWKV-7 causal LM (inference) over the HIP kernels; see the module docstring.
+
+    A Hugging Face ``PreTrainedModel`` + ``GenerationMixin`` like the
+    reference's (rwkv7_hf/native_model.py:371-406), registered for
+    ``AutoConfig`` / ``AutoModelForCausalLM`` under ``model_type``
+    ``"rwkv7_native"``: ``generate()`` drives :meth:`forward`, whose prefill is
+    the chunked-scan route and whose one-token steps replay the captured
+    decode graph.  The weights live in the kernels' own layouts (plain
+    tensors and MM8 modules, not ``nn.Parameter`` s); ``from_pretrained`` /
+    ``save_pretrained`` read and write converted directories.
+    """
+
+    config_class = NativeRWKV7Config
+    base_model_prefix = "model"
+    main_input_name = "input_ids"
+    _tied_weights_keys: dict = {}
+    _is_stateful = True  # a recurrent cache: no KV cropping or assisted decoding
+
+    @classmethod
+    def _supports_default_dynamic_cache(cls) -> bool:
+        # the recurrent state is not a KV cache: GenerationMixin must not pre-build one
+        return False
+
+    @property
+    def device(self) -> torch.device:
+        return self._device
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self._dtype
 
     def _init_common(self, config, device, dtype):
+        _PreTrainedModel.__init__(self, config)
         self.config = config
-        self.device = torch.device(device)
-        self.dtype = dtype
+        self._device = torch.device(device)
+        self._dtype = dtype
         # run the decode LoRA projections on a second stream beside R/K/V
         self.lora_side_stream = False
         # decode: LoRA up projections inside the wkv kernel (when the shapes allow)
@@ -697,11 +761,15 @@ class NativeRWKV7ForCausalLM:
         self._rwkv7_native_mm_replaced_modules = self._replaced
         self._graph_runners: dict[int, "NativeGraphRunner"] = {}
 
-    def __init__(self, config: NativeRWKV7Config, weights: dict[str, torch.Tensor], *, device="cuda",
-                 dtype=torch.float16, prepacked: dict | None = None):
-        """``weights``: HF-named parameters (see :func:`parameter_shapes`).
-        ``prepacked``: module name -> :class:`MM8Linear` built from a
-        prepacked checkpoint; those modules' ``.weight`` entries are not read."""
+    def __init__(self, config: NativeRWKV7Config, weights: dict[str, torch.Tensor] | None = None, *,
+                 device="cuda", dtype=torch.float16, prepacked: dict | None = None):
+        """``weights``: HF-named parameters (see :func:`parameter_shapes`);
+        None gives the seeded random init (as ``cls(config)`` does for the
+        reference).  ``prepacked``: module name -> :class:`MM8Linear` built
+        from a prepacked checkpoint; those modules' ``.weight`` entries are not
+        read."""
+        if weights is None:
+            weights = _LazyWeights(config, 0, device, dtype)
         self._init_common(config, device, dtype)
         cfg = config
         dev = self.device
@@ -1367,9 +1435,92 @@ class NativeRWKV7ForCausalLM:
             self._graph_runners[batch] = r
         return r
 
+    # ------------------------------------------------ Hugging Face generation contract
+    def prepare_inputs_for_generation(self, input_ids, past_key_values=None, inputs_embeds=None,
+                                      return_legacy_cache: bool | None = None, **kwargs):
+        """GenerationMixin's per-step inputs (rwkv7_hf/model_generation.py:38-97):
+        the whole prompt on the first step, then only the last token with the
+        recurrent cache (which the decode graph then replays)."""
+        cached = _as_native_cache(past_key_values) is not None
+        last = (lambda t: t[:, -1:]) if cached else (lambda t: t)
+        out: dict = {}
+        if inputs_embeds is not None and not cached:
+            out["inputs_embeds"] = inputs_embeds
+        elif input_ids is not None:
+            out["input_ids"] = last(input_ids)
+        else:
+            out["inputs_embeds"] = last(inputs_embeds)
+        use_cache = kwargs.get("use_cache", True)
+        out["past_key_values"] = past_key_values
+        out["use_cache"] = True if use_cache is None else use_cache
+        if return_legacy_cache is not None:
+            out["return_legacy_cache"] = return_legacy_cache
+        if kwargs.get("attention_mask") is not None:
+            out["attention_mask"] = last(kwargs["attention_mask"])
+        for k in ("logits_to_keep", "num_logits_to_keep", "output_hidden_states", "output_attentions",
+                  "return_dict"):
+            if k in kwargs:
+                out[k] = kwargs[k]
+        return out
+
+    @staticmethod
+    def _reorder_cache(past_key_values, beam_idx: torch.LongTensor):
+        """Beam reordering of the recurrent cache (rwkv7_hf/model_generation.py:15-35)."""
+        cache = _as_native_cache(past_key_values)
+        if cache is None:
+            return None
+        out = cache.reorder_cache(beam_idx)
+        return out.to_legacy_cache() if isinstance(past_key_values, tuple) else out
+
+    @classmethod
+    def from_pretrained(cls, pretrained_model_name_or_path, *model_args, config=None, device=None,
+                        device_map=None, torch_dtype=None, dtype=None, use_native_mm8: bool | None = None,
+                        native_mm8_policy: str | None = None, native_mm8_min_params: int | None = None,
+                        **kwargs):
+        """A model from a converted directory (``config.json`` +
+        ``*.safetensors``, or a prepacked MM8 directory with ``manifest.json``),
+        as ``AutoModelForCausalLM.from_pretrained`` would give the reference's.
+        ``dtype`` / ``torch_dtype``: ``"auto"`` reads ``config.json``;
+        default fp16.  ``device`` / a single-device ``device_map``: default
+        ``cuda``.  The ``use_native_mm8`` family overrides the config."""
+        import json
+        from pathlib import Path
+
+        from .converter import load_pretrained
+
+        path = Path(pretrained_model_name_or_path)
+        want = dtype if dtype is not None else torch_dtype
+        if want is None or want == "auto":
+            name = json.loads((path / "config.json").read_text()).get("torch_dtype") if want == "auto" else None
+            want = getattr(torch, name) if isinstance(name, str) else torch.float16
+        elif isinstance(want, str):
+            want = getattr(torch, want)
+        if device is None:
+            device = device_map if isinstance(device_map, (str, torch.device)) and device_map != "auto" else "cuda"
+        if config is not None and use_native_mm8 is None:
+            use_native_mm8 = getattr(config, "use_native_mm8", None)
+        return load_pretrained(path, device=device, dtype=want, use_native_mm8=use_native_mm8,
+                               native_mm8_policy=native_mm8_policy, native_mm8_min_params=native_mm8_min_params)
+
+    def save_pretrained(self, save_directory, **kwargs):
+        """Write a directory :meth:`from_pretrained` reads: a prepacked MM8
+        directory when any projection is quantised, else ``config.json`` +
+        ``model.safetensors``."""
+        from .converter import save_hf_directory, save_prepacked
+
+        if self._replaced:
+            save_prepacked(self, save_directory)
+        else:
+            save_hf_directory(save_directory, self.config, self.dense_state_dict(),
+                              dtype_name=str(self.dtype).replace("torch.", ""))
+
     @torch.no_grad()
-    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, *, use_graph: bool = True):
-        """Greedy generation; returns ``[B, T + max_new_tokens]``."""
+    def generate_greedy(self, input_ids: torch.Tensor, max_new_tokens: int, *, use_graph: bool = True):
+        """Greedy generation without GenerationMixin's per-step host work: the
+        decode graph computes each step's argmax and feeds it to its own next
+        replay.  Returns ``[B, T + max_new_tokens]``, the ids
+        ``generate(input_ids, max_new_tokens=..., do_sample=False)`` gives
+        with no end-of-sequence token."""
         B = int(input_ids.shape[0])
         out0 = self.forward(input_ids)
         logits, cache = out0.logits, out0.past_key_values
@@ -1598,6 +1749,16 @@ class NativePrefillGraphRunner:
             dst.copy_(src)
         out.seen_tokens = seen + self.tokens_n
         return self.logits.clone(), out
+
+
+try:  # AutoConfig / AutoModelForCausalLM resolve model_type "rwkv7_native" to these classes
+    from transformers import AutoConfig as _AutoConfig
+    from transformers import AutoModelForCausalLM as _AutoModelForCausalLM
+
+    _AutoConfig.register(NativeRWKV7Config.model_type, NativeRWKV7Config, exist_ok=True)
+    _AutoModelForCausalLM.register(NativeRWKV7Config, NativeRWKV7ForCausalLM, exist_ok=True)
+except Exception:  # pragma: no cover - transformers absent or too old
+    pass
 
 
 __all__ = ["NativeRWKV7Config", "NativeRWKV7Cache", "NativeRWKV7ForCausalLM", "NativeGraphRunner",

@@ -109,6 +109,71 @@ class ModelOracle:
         hN = _ln(x, w["model.norm.weight"], w["model.norm.bias"], c.norm_eps)
         return self._linear("lm_head", hN)
 
+    def run_seq(self, ids, st=None, keep: int = 1):
+        """The same model as :meth:`step`, with every token-parallel product
+        (norms, shift mixes, projections, LoRAs, GroupNorm, FFN) taken over
+        the whole sequence at once and only the DPLR recurrence per token, as
+        the reference's sequence prefill orders it
+        (rwkv7_hf/native_jit_prefill.py:223-1057); fp64 like :meth:`step`.
+        Feeds ids [B, T]; returns (logits of the last ``keep`` tokens
+        [B, keep, V], state)."""
+        c, w = self.cfg, self.w
+        H, N, D = c.num_heads, c.head_dim, c.hidden_size
+        ids = np.asarray(ids)
+        B, T = ids.shape
+        st = st if st is not None else self.new_state(B)
+        x = w["model.embeddings.weight"][ids]  # [B, T, D]
+        for i in range(c.num_hidden_layers):
+            p = f"model.layers.{i}."
+            if i == 0:
+                x = _ln(x, w[p + "pre_norm.weight"], w[p + "pre_norm.bias"], c.norm_eps)
+            h = _ln(x, w[p + "attn_norm.weight"], w[p + "attn_norm.bias"], c.norm_eps)
+            prev = np.concatenate([st["xpa"][i][:, None], h[:, :-1]], 1)
+            st["xpa"][i] = h[:, -1].copy()
+            xr, xw, xk, xv, xa, xg = (h + (prev - h) * w[p + "attn." + m].reshape(1, 1, -1)
+                                      for m in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g"))
+            r = self._linear(p + "attn.r_proj", xr)
+            k = self._linear(p + "attn.k_proj", xk)
+            v = self._linear(p + "attn.v_proj", xv)
+            lw = lambda n, q: q @ w[p + f"attn.{n}.lora.0.weight"].T
+            up = lambda n, q: q @ w[p + f"attn.{n}.lora.2.weight"].T + w.get(p + f"attn.{n}.lora.2.bias", 0.0)
+            wd = up("w_lora", np.tanh(lw("w_lora", xw)))
+            a = _sigmoid(up("a_lora", lw("a_lora", xa)))
+            g = up("g_lora", _sigmoid(lw("g_lora", xg)))
+            kk = (k * w[p + "attn.k_k"].reshape(1, 1, -1)).reshape(B, T, H, N)
+            kk = kk / np.maximum(np.linalg.norm(kk, axis=-1, keepdims=True), 1e-12)
+            k = k * (1 + (a - 1) * w[p + "attn.k_a"].reshape(1, 1, -1))
+            if i == 0:
+                st["v_first"] = v[:, -1].copy()
+                vfirst = v.copy()
+            else:
+                v = v + (vfirst - v) * _sigmoid(up("v_lora", lw("v_lora", xv)))
+            dec = np.exp(-EXP_HALF * _sigmoid(wd))
+            kk4, a4, k4, v4, r4, d4 = (t.reshape(B, T, H, N) for t in (kk, a, k, v, r, dec))
+            S = st["state"][i]
+            y = np.empty((B, T, H, N), S.dtype)
+            for t in range(T):
+                dot = np.einsum("bhij,bhj->bhi", S, kk4[:, t])
+                S = (S * d4[:, t, :, None, :] - dot[..., None] * (kk4[:, t] * a4[:, t])[:, :, None, :]
+                     + v4[:, t, :, :, None] * k4[:, t, :, None, :])
+                y[:, t] = np.einsum("bhij,bhj->bhi", S, r4[:, t])
+            st["state"][i] = S
+            mu = y.mean(-1, keepdims=True)
+            var = ((y - mu) ** 2).mean(-1, keepdims=True)
+            y = ((y - mu) / np.sqrt(var + N * 1e-5)).reshape(B, T, H * N)
+            y = y * w[p + "attn.g_norm.weight"] + w[p + "attn.g_norm.bias"]
+            sk = (r4 * k4 * w[p + "attn.r_k"].reshape(1, 1, H, N)).sum(-1, keepdims=True)
+            y = y + (sk * v4).reshape(B, T, H * N)
+            x = x + self._linear(p + "attn.o_proj", y * g)
+            h2 = _ln(x, w[p + "ffn_norm.weight"], w[p + "ffn_norm.bias"], c.norm_eps)
+            prev2 = np.concatenate([st["xpf"][i][:, None], h2[:, :-1]], 1)
+            st["xpf"][i] = h2[:, -1].copy()
+            fk = h2 + (prev2 - h2) * w[p + "ffn.x_k"].reshape(1, 1, -1)
+            kf = np.maximum(self._linear(p + "ffn.key", fk), 0.0) ** 2
+            x = x + self._linear(p + "ffn.value", kf)
+        hN = _ln(x[:, T - keep:], w["model.norm.weight"], w["model.norm.bias"], c.norm_eps)
+        return self._linear("lm_head", hN), st
+
     def run(self, ids, st=None):
         """Feed ids [B, T] token by token; returns (logits [B, T, V], state)."""
         ids = np.asarray(ids)

@@ -10,8 +10,12 @@ H = 64, F = 16384, V = 65536, LoRA 64/64/128/32) with MM8 weights under the
 * The B = 8 x T = 4096 prefill once, and its cache against a prompt split into
   two prefills of 2048 tokens (the cache-continuation contract).
 
-Tolerances: logits max-abs <= 2e-2 x max|logit| with ids equal wherever the
-oracle's top-2 margin exceeds twice that; recurrent state relative <= 2e-2.
+Tolerances (about 2x the errors measured on an MI355X: logits <= 9.1e-4 x
+max|logit| and <= 5.3e-3 absolute, state <= 1.1e-3 relative, over prefills of
+12 and 300 tokens and graph decode): logits max-abs <= 2e-3 x max|logit| and
+<= 1e-2 absolute, with the argmax equal wherever the oracle's top-2 margin
+exceeds twice the measured error; recurrent state relative <= 2.5e-3.  The
+split-prompt test compares two GPU runs whose chunk boundaries coincide.
 """
 from __future__ import annotations
 
@@ -21,7 +25,10 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-LOGIT_REL = 2e-2
+LOGIT_REL = 2e-3
+LOGIT_ABS = 1e-2  # the north star's bound on fp16 outputs
+STATE_REL = 2.5e-3
+SPLIT_REL = 2e-2
 
 
 def _cfg(layers):
@@ -32,13 +39,24 @@ def _cfg(layers):
                              use_native_mm8=True, native_mm8_min_params=8_000_000, native_mm8_policy="memory")
 
 
-def _close(got, ref):
+def _close(got, ref, what=""):
     got = got.float().cpu().numpy().astype(np.float64)
     scale = np.abs(ref).max()
-    assert np.abs(got - ref).max() <= LOGIT_REL * scale, (np.abs(got - ref).max(), scale)
+    err = np.abs(got - ref).max()
+    print(f"PARITY 7.2B slice {what}: logits max-abs {err:.3e}, max|logit| {scale:.3f}, rel {err / scale:.2e}",
+          flush=True)
+    assert err <= LOGIT_REL * scale and err <= LOGIT_ABS, (err, scale)
     top2 = np.sort(ref, -1)[:, -2:]
-    sure = top2[:, 1] - top2[:, 0] > 2 * LOGIT_REL * scale
+    sure = top2[:, 1] - top2[:, 0] > 2 * err
     np.testing.assert_array_equal(got.argmax(-1)[sure], ref.argmax(-1)[sure])
+
+
+def _state_close(cache, st, what):
+    for i in range(len(st["state"])):
+        s = cache._state[i].double().cpu().numpy()
+        rel = np.abs(s - st["state"][i]).max() / np.abs(st["state"][i]).max()
+        print(f"PARITY 7.2B slice {what} layer {i}: state rel {rel:.2e}", flush=True)
+        assert rel <= STATE_REL, (i, rel)
 
 
 def test_7p2b_two_layer_slice_matches_oracle():
@@ -65,23 +83,25 @@ def test_7p2b_two_layer_slice_matches_oracle():
     ora = ModelOracle(cfg, ref_w, override)
     del ref_w, override
     rng = np.random.default_rng(4)
-    for B in (1, 3):
-        print(f"7.2B slice: B={B} prefill 12 tokens + 3 graph decode steps", flush=True)
-        ids = rng.integers(0, cfg.vocab_size, (B, 12))
-        ref_logits, st = ora.run(ids)
+    # 12-token prompts run the many-row tile GEMM (<= 256 rows); B=1 x 300 runs the
+    # prefill GEMM (> 256 rows), the fused many-row LoRA and the chunk kernel over a
+    # ragged tail, against the sequence form of the oracle
+    for B, T in ((1, 12), (3, 12), (1, 300)):
+        print(f"7.2B slice: B={B} prefill {T} tokens + 3 graph decode steps", flush=True)
+        ids = rng.integers(0, cfg.vocab_size, (B, T))
+        ref_last, st = ora.run_seq(ids, keep=1)
         out = model(torch.tensor(ids, device="cuda"))
         torch.cuda.synchronize()
-        _close(out.logits[:, -1], ref_logits[:, -1])
+        _close(out.logits[:, -1], ref_last[:, -1], f"B={B} T={T} prefill")
         cache = out.past_key_values
-        for i in range(cfg.num_hidden_layers):
-            s = cache._state[i].double().cpu().numpy()
-            assert np.abs(s - st["state"][i]).max() <= 2e-2 * np.abs(st["state"][i]).max()
-        for _ in range(3):
+        _state_close(cache, st, f"B={B} T={T} prefill")
+        for j in range(3):
             nxt = rng.integers(0, cfg.vocab_size, (B,))
             r = ora.step(nxt, st)
             lg = model(torch.tensor(nxt[:, None], device="cuda"), past_key_values=cache).logits
             torch.cuda.synchronize()
-            _close(lg[:, -1], r)
+            _close(lg[:, -1], r, f"B={B} T={T} decode {j}")
+        _state_close(cache, st, f"B={B} T={T} after decode")
 
 
 @pytest.fixture(scope="module")
@@ -133,15 +153,19 @@ def test_7p2b_prefill_b8_t4096_split_continuation(full_model):
     assert one.past_key_values.seen_tokens == two.past_key_values.seen_tokens == 4096
     a, b = one.logits.float(), two.logits.float()
     assert torch.isfinite(a).all()
-    assert (a - b).abs().max().item() <= LOGIT_REL * a.abs().max().item()
+    worst = {"logits": (a - b).abs().max().item() / a.abs().max().item(), "state": 0.0, "shift": 0.0}
     ca, cb = one.past_key_values, two.past_key_values
     for i in range(32):
         sa, sb = ca._state[i], cb._state[i]
         assert torch.isfinite(sa).all()
-        assert ((sa - sb).abs().max() / sa.abs().max()).item() <= 2e-2, i
+        worst["state"] = max(worst["state"], ((sa - sb).abs().max() / sa.abs().max()).item())
         for xa_, xb_ in ((ca._xpa[i], cb._xpa[i]), (ca._xpf[i], cb._xpf[i])):
-            assert (xa_.float() - xb_.float()).abs().max().item() <= 2e-2 * max(1.0, xa_.float().abs().max().item())
+            worst["shift"] = max(worst["shift"], (xa_.float() - xb_.float()).abs().max().item()
+                                 / max(1.0, xa_.float().abs().max().item()))
     tok = ids[:, -1:]
     la = model(tok, past_key_values=ca, use_graph=False).logits.float()
     lb = model(tok, past_key_values=cb, use_graph=False).logits.float()
-    assert (la - lb).abs().max().item() <= LOGIT_REL * la.abs().max().item()
+    worst["next logits"] = (la - lb).abs().max().item() / la.abs().max().item()
+    print("PARITY 7.2B B=8 T=4096 one prefill vs 2 x 2048: " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()),
+          flush=True)
+    assert all(v <= SPLIT_REL for v in worst.values()), worst

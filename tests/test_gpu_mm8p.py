@@ -52,8 +52,9 @@ def _ref(oracle, x, mod):
 TOL = 3e-3
 
 
-@pytest.mark.parametrize("IO", [(4096, 4096), (1024, 300), (144, 40), (2064, 520), (16384, 256), (80, 16)])
-@pytest.mark.parametrize("rows", [257, 600, 1024])
+@pytest.mark.parametrize("IO,rows", [(io, r) for io in [(4096, 4096), (1024, 300), (144, 40), (2064, 520),
+                                                        (16384, 256), (80, 16)] for r in (257, 600, 1024)]
+                         + [((4096, 16384), 300), ((16384, 4096), 300), ((4096, 16384), 1100)])
 def test_mm8p_matches_oracle(oracle, IO, rows):
     from rwkv7mi.native_quant_mm8 import mm8_gemm_prefill_multi_into
 

@@ -1,9 +1,10 @@
 """GPU parity of the end-to-end RWKV-7 model (prefill, eager decode, graph decode)
 against the fp64 per-token oracle (oracle/model_oracle.py), with and without MM8.
 
-Tolerance: logits max-abs error <= 2e-2 x max|logit| (fp16 activations through
-the whole stack); greedy ids must agree wherever the oracle's top-2 margin
-exceeds that tolerance.
+Tolerance: logits max-abs error <= 2e-3 x max|logit| (fp16 activations through
+the whole stack; the largest error measured on an MI355X over these tests was
+8.1e-4 x max|logit|); greedy ids must agree wherever the oracle's top-2 margin
+exceeds twice that tolerance.
 """
 from __future__ import annotations
 
@@ -13,7 +14,7 @@ import torch
 
 pytestmark = pytest.mark.gpu
 
-LOGIT_REL = 2e-2
+LOGIT_REL = 2e-3
 
 
 def _cfg(mm8: bool, layers=2, D=128, F=256):
@@ -47,10 +48,11 @@ def _build(mm8: bool, layers=2, seed=0, D=128, F=256):
     return cfg, model, ref
 
 
-def _close(got, ref):
+def _close(got, ref, what="model"):
     got = got.float().cpu().numpy().astype(np.float64)
     scale = np.abs(ref).max()
     err = np.abs(got - ref).max()
+    print(f"PARITY {what}: logits max-abs {err:.3e}, max|logit| {scale:.3f}, rel {err / scale:.2e}", flush=True)
     assert err <= LOGIT_REL * scale, (err, scale)
     top2 = np.sort(ref, -1)[:, -2:]
     margin = top2[:, 1] - top2[:, 0]
@@ -174,7 +176,7 @@ def test_generate_greedy_matches_oracle():
     cfg, model, ref = _build(True)
     rng = np.random.default_rng(3)
     ids = rng.integers(0, cfg.vocab_size, (2, 12))
-    out = model.generate(torch.tensor(ids, device="cuda"), 6).cpu().numpy()
+    out = model.generate_greedy(torch.tensor(ids, device="cuda"), 6).cpu().numpy()
     st = ref.new_state(2)
     lg, st = ref.run(ids, st)
     seq = [ids]
@@ -213,8 +215,8 @@ def test_model_matches_reference_golden(name, dtype):
     """Prefill + greedy decode against the reference model's own logits and
     greedy ids (tests/golden/make_model_golden.py; c1 = BASELINE configs[0]:
     the 0.1B architecture, 512-token prompt, 64 greedy steps).  fp32: logits
-    max-abs <= 1e-3 x max|logit| and every greedy id bit-exact; fp16: logits
-    within 2e-2 x max|logit| at every step and the greedy ids,
+    max-abs <= 1e-5 x max|logit| (measured: 3.3e-6) and every greedy id bit-exact; fp16: logits
+    within 4e-3 x max|logit| at every step (measured: 1.8e-3 at c1) and the greedy ids,
     teacher-forced along the reference's greedy tokens, equal to the
     reference's id at every step whose reference top-2 margin exceeds twice the
     measured fp16 logit error of that step."""
@@ -225,12 +227,15 @@ def test_model_matches_reference_golden(name, dtype):
     model = NativeRWKV7ForCausalLM(cfg, w, device="cuda", dtype=dtype)
     ids = torch.tensor(g["ids"], device="cuda")
     logits = model(ids).logits
-    out = model.generate(ids, len(g["greedy"])).cpu().numpy()[0, ids.shape[1]:]
+    out = model.generate_greedy(ids, len(g["greedy"])).cpu().numpy()[0, ids.shape[1]:]
     torch.cuda.synchronize()
     ref = g["logits"].astype(np.float64)
     got = logits[0, -1].double().cpu().numpy()
-    tol = 1e-3 if dtype == torch.float32 else LOGIT_REL
-    assert np.abs(got - ref).max() <= tol * np.abs(ref).max()
+    tol = 1e-5 if dtype == torch.float32 else 4e-3
+    err0 = np.abs(got - ref).max()
+    print(f"PARITY golden {name} {str(dtype)[6:]}: prompt logits max-abs {err0:.3e}, max|logit| "
+          f"{np.abs(ref).max():.3f}, rel {err0 / np.abs(ref).max():.2e}", flush=True)
+    assert err0 <= tol * np.abs(ref).max()
     if dtype == torch.float32:
         np.testing.assert_array_equal(out, g["greedy"])
         return
@@ -243,7 +248,7 @@ def test_model_matches_reference_golden(name, dtype):
     c16, c32 = o16.past_key_values, o32.past_key_values
     l16, l32 = o16.logits[:, -1], o32.logits[:, -1]
     greedy = [int(v) for v in g["greedy"]]
-    checked = 0
+    checked, worst = 0, 0.0
     for t in range(len(greedy)):
         if t > 0:
             tok = torch.tensor([[greedy[t - 1]]], device="cuda")
@@ -251,13 +256,15 @@ def test_model_matches_reference_golden(name, dtype):
             l32 = m32(tok, past_key_values=c32).logits[:, -1]
         a, b = l16[0].double().cpu().numpy(), l32[0].double().cpu().numpy()
         err = np.abs(a - b).max()
+        worst = max(worst, err / g["scale"][t])
         assert err <= tol * g["scale"][t], (t, err)
         assert int(b.argmax()) == greedy[t], t
         if g["margins"][t] > 2 * err:
             assert int(a.argmax()) == greedy[t], (t, err, g["margins"][t])
             checked += 1
-    print(f"{name} fp16: {checked} of {len(greedy)} teacher-forced greedy ids decided by the margins", flush=True)
-    assert checked >= len(greedy) // 2
+    print(f"PARITY golden {name} fp16: {checked} of {len(greedy)} teacher-forced greedy ids decided by the margins; "
+          f"worst step logit error {worst:.2e} x max|logit|", flush=True)
+    assert checked >= len(greedy) * 7 // 8  # measured: 61 of 64 at c1, 8 of 8 at tiny
 
 
 @pytest.mark.parametrize("mm8,B", [(False, 1), (True, 3)])
@@ -317,3 +324,43 @@ def test_deferred_value_reduce_equals_reduce(B):
     got = runner.replay(tok, c2).clone()
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_hf_generate_matches_golden(dtype):
+    """transformers' GenerationMixin.generate drives the model (prefill, then
+    one-token steps that replay the decode graph): on BASELINE configs[0]
+    (the 0.1B architecture, a 512-token prompt, 64 greedy steps) it returns
+    the reference's own greedy ids in fp32 (tests/golden/model_c1.npz), and in
+    fp16 the same ids as the graph-internal greedy loop."""
+    from rwkv7mi.model import NativeRWKV7ForCausalLM
+    from test_oracle_model import golden_case
+
+    cfg, w, g = golden_case("c1")
+    model = NativeRWKV7ForCausalLM(cfg, w, device="cuda", dtype=dtype)
+    ids = torch.tensor(g["ids"], device="cuda")
+    n = len(g["greedy"])
+    out = model.generate(ids, max_new_tokens=n, do_sample=False)
+    assert tuple(out.shape) == (1, ids.shape[1] + n)
+    got = out[0, ids.shape[1]:].cpu().numpy()
+    if dtype == torch.float32:
+        np.testing.assert_array_equal(got, g["greedy"])
+    np.testing.assert_array_equal(got, model.generate_greedy(ids, n).cpu().numpy()[0, ids.shape[1]:])
+
+
+def test_auto_model_from_pretrained_generates_golden(tmp_path):
+    """The drop-in load path: a converted directory read by
+    AutoModelForCausalLM.from_pretrained, then generate(), gives the
+    reference's greedy ids (tiny golden config, fp32)."""
+    from transformers import AutoModelForCausalLM
+
+    from rwkv7mi.converter import save_hf_directory
+    from test_oracle_model import golden_case
+
+    cfg, w, g = golden_case("tiny")
+    save_hf_directory(tmp_path, cfg, w, dtype_name="float32")
+    model = AutoModelForCausalLM.from_pretrained(tmp_path, dtype="auto")
+    assert model.dtype == torch.float32 and model.device.type == "cuda"
+    ids = torch.tensor(g["ids"], device="cuda")
+    out = model.generate(ids, max_new_tokens=len(g["greedy"]), do_sample=False, eos_token_id=None)
+    np.testing.assert_array_equal(out[0, ids.shape[1]:].cpu().numpy(), g["greedy"])

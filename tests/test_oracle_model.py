@@ -45,3 +45,24 @@ def test_model_oracle_matches_reference_golden(name):
         seq.append(nxt)
         nxt = int(ora.step(np.array([nxt]), st)[0].argmax())
     np.testing.assert_array_equal(seq, g["greedy"])
+
+
+def test_sequence_oracle_equals_per_token_oracle():
+    """run_seq (token-parallel products, per-token recurrence) is the same
+    model as the per-token step: logits and every cache tensor agree to fp64
+    rounding, from zero state and continuing a cache."""
+    from oracle.model_oracle import ModelOracle
+
+    cfg, w, _ = golden_case("tiny")
+    ora = ModelOracle(cfg, {k: v.numpy() for k, v in w.items()})
+    ids = np.random.default_rng(2).integers(0, cfg.vocab_size, (2, 11))
+    lg, st = ora.run(ids[:, :7])
+    lg2, st2 = ora.run_seq(ids[:, :7], keep=7)
+    np.testing.assert_allclose(lg2, lg, rtol=0, atol=1e-10 * np.abs(lg).max())
+    lg, st = ora.run(ids[:, 7:], st)
+    lg2, st2 = ora.run_seq(ids[:, 7:], st2, keep=1)
+    np.testing.assert_allclose(lg2[:, -1], lg[:, -1], rtol=0, atol=1e-10 * np.abs(lg).max())
+    for key in ("state", "xpa", "xpf"):
+        for a, b in zip(st[key], st2[key]):
+            np.testing.assert_allclose(b, a, rtol=0, atol=1e-10 * max(1.0, np.abs(a).max()))
+    np.testing.assert_allclose(st2["v_first"], st["v_first"], rtol=0, atol=1e-10)
