@@ -437,7 +437,9 @@ def run_gemv_c3(reps=20):
             x = torch.randn(rows, I, device="cuda", dtype=torch.float16)
             ys = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in mods]
             calls = [(lambda m=m, y=y: m.rwkv7_forward_into(x, y)) for m, y in zip(mods, ys)]
+            torch.cuda.nvtx.range_push(f"MM8 {I}x{O} b{rows}")  # labels the cell in a profiler trace
             ms = time_graph(calls, reps)
+            torch.cuda.nvtx.range_pop()
             nb = mm8_bytes(I, O, rows)
             gbs = nb / (ms / 1e3) / 1e9
             out[f"{I}x{O}/b{rows}"] = {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
@@ -469,10 +471,14 @@ def run_gemv_c4(reps=20):
             ys = [torch.empty(rows, O, device="cuda", dtype=torch.float16) for _ in range(n)]
             calls = [(lambda p=p, y=y: w4_affine_groupwise_linear(x, p[0], p[1], p[2], O, I, out=y))
                      for p, y in zip(packs_a, ys)]
+            torch.cuda.nvtx.range_push(f"W4 asym {I}x{O} b{rows}")
             ms = time_graph(calls, reps)
+            torch.cuda.nvtx.range_pop()
             gbs = w4_bytes(I, O, rows, affine=True) / (ms / 1e3) / 1e9
             calls_s = [(lambda p=p, y=y: w4_groupwise_linear(x, p[0], p[1], O, I, out=y)) for p, y in zip(packs_s, ys)]
+            torch.cuda.nvtx.range_push(f"W4 sym {I}x{O} b{rows}")
             ms_s = time_graph(calls_s, reps)
+            torch.cuda.nvtx.range_pop()
             gbs_s = w4_bytes(I, O, rows, affine=False) / (ms_s / 1e3) / 1e9
             out[f"{I}x{O}/b{rows}"] = {"asym_us": round(ms * 1e3, 2), "asym_gbs": round(gbs, 1),
                                        "asym_frac": round(gbs / HBM_PEAK_GBS, 4), "sym_us": round(ms_s * 1e3, 2),
@@ -482,9 +488,113 @@ def run_gemv_c4(reps=20):
     return out
 
 
+def cpu_gemv_baseline(shapes, batch=1, kind="mm8", min_seconds=1.0):
+    """The reference's CPU forms, restated in fp32 numpy and timed on the host
+    cores: mm8_matmul dequantises the whole weight and multiplies
+    (rwkv7_hf/native_quant_mm8.py:100-119); the sm70 W4 torch fallback does the
+    same for the symmetric group format (sm70_quant.py:598-610).  Each shape is
+    repeated for about ``min_seconds``; returns microseconds per call."""
+    import numpy as np
+
+    rng = np.random.default_rng(0)
+    out = {}
+    for I, O in shapes:
+        x = rng.standard_normal((batch, I)).astype(np.float32)
+        if kind == "mm8":
+            q = rng.integers(0, 256, (I, O), dtype=np.uint8)
+            mx, rx = (rng.random(O, dtype=np.float32) * 0.01 for _ in range(2))
+            my, ry = (rng.random((I, 1), dtype=np.float32) * 0.01 for _ in range(2))
+            call = lambda: x @ ((q.astype(np.float32) + np.float32(0.5)) * ry * rx + my + mx)
+        else:
+            pk = rng.integers(0, 256, (O, I // 2), dtype=np.uint8)
+            sc = rng.random((O, I // 128), dtype=np.float32) * 0.01
+
+            def call():
+                w = np.empty((O, I), np.float32)
+                w[:, 0::2] = (pk & 15).astype(np.float32) - 8
+                w[:, 1::2] = (pk >> 4).astype(np.float32) - 8
+                w *= np.repeat(sc, 128, axis=1)
+                return x @ w.T
+        call()
+        n, t0 = 0, time.perf_counter()
+        while n < 2 or time.perf_counter() - t0 < min_seconds:
+            call()
+            n += 1
+        out[f"{I}x{O}/b{batch}"] = round((time.perf_counter() - t0) / n * 1e6, 1)
+    return out
+
+
+def run_c1(prompt=512, steps=64):
+    """the RWKV-7 0.1B architecture (L=12, D=768, H=12, FFN 3072,
+    vocab 65536), random init seed 0, fp32, bsz 1: a 512-token uniform-random
+    prompt, then 64 greedy steps (the decode graph).  Times the prefill and the
+    greedy steps separately on the GPU, and the same work with the fp32 numpy
+    restatement (oracle/model_oracle.py: sequence-form prefill, per-token
+    steps) on the host."""
+    import numpy as np
+    import torch
+    from rwkv7mi.model import NativeRWKV7Config, NativeRWKV7ForCausalLM, parameter_shapes, random_weights
+
+    cfg = NativeRWKV7Config(vocab_size=65536, hidden_size=768, num_hidden_layers=12, intermediate_size=3072,
+                            decay_low_rank_dim=64, a_low_rank_dim=64, gate_low_rank_dim=128, v_low_rank_dim=32)
+    w = random_weights(cfg, seed=0, device="cpu", dtype=torch.float32)
+    model = NativeRWKV7ForCausalLM(cfg, w, device="cuda", dtype=torch.float32)
+    ids = torch.tensor(np.random.default_rng(0).integers(0, cfg.vocab_size, (1, prompt)), device="cuda")
+    out = model.generate_greedy(ids, steps)  # warm-up: captures the graphs
+    torch.cuda.synchronize()
+    pre_ms, _ = time_events(lambda: model(ids), 5, 1)
+    o = model(ids)
+    cache, nxt = o.past_key_values, o.logits[:, -1].argmax(-1)
+    runner = model.graph_runner(1)
+    runner.replay_greedy(cache, nxt)
+    dec_ms, _ = time_events(lambda: runner.replay_greedy(cache), steps, 3)
+    shapes = parameter_shapes(cfg)
+    nbytes = sum(int(np.prod(s)) * 4 for n, s in shapes.items() if n != "model.embeddings.weight")
+    nbytes += cfg.hidden_size * 4 + cfg.num_hidden_layers * (cfg.num_heads * 64 * 64 * 4 * 2
+                                                              + 2 * cfg.hidden_size * 4 * 2) + cfg.vocab_size * 4
+    gbs = nbytes / (dec_ms / 1e3) / 1e9
+    total_ms = pre_ms + steps * dec_ms
+    res = {"config": f"0.1B fp32, bsz 1, prompt {prompt} + {steps} greedy steps",
+           "prefill_ms": round(pre_ms, 3), "prefill_tok_s": round(prompt / (pre_ms / 1e3), 1),
+           "decode_ms_per_step": round(dec_ms, 4), "decode_tok_s": round(1e3 / dec_ms, 1),
+           "generate_ms": round(total_ms, 2), "generate_tok_s": round(steps / (total_ms / 1e3), 1),
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "decode step (graph)",
+                        "step_bytes": nbytes},
+           "greedy_ids_head": out[0, prompt:prompt + 8].tolist()}
+    del model
+    torch.cuda.empty_cache()
+    # host: the fp32 restatement, same prompt and step count
+    from oracle.model_oracle import ModelOracle
+
+    ora = ModelOracle(cfg, {k: v.numpy() for k, v in w.items()}, dtype=np.float32)
+    del w
+    t0 = time.perf_counter()
+    lg, st = ora.run_seq(ids.cpu().numpy(), keep=1)
+    t1 = time.perf_counter()
+    tok = np.array([int(lg[0, -1].argmax())])
+    for _ in range(steps):
+        tok = np.array([int(ora.step(tok, st)[0].argmax())])
+    t2 = time.perf_counter()
+    res["cpu_baseline"] = {"value": round(steps / (t2 - t0), 2), "unit": "generated tok/s", "cores": host_cores(),
+                           "kind": "port", "cpu": cpu_model(),
+                           "sample": f"the whole configs[0] run: fp32 numpy restatement (oracle/model_oracle.py), "
+                                     f"prefill {prompt} tokens in {t1 - t0:.2f} s, {steps} greedy steps in "
+                                     f"{t2 - t1:.2f} s"}
+    return res
+
+
 # ------------------------------------------------------------------ counter workloads
 TRAFFIC_JSON = ROOT / "profiles" / "traffic.json"
 COPY_BYTES = 256 << 20
+
+
+def _traffic_gemv(key):
+    """HBM bytes per launch of a configs[2]/[3] head cell from profiles/traffic_gemv.json, or None."""
+    try:
+        return json.loads((ROOT / "profiles" / "traffic_gemv.json").read_text())["traffic_bytes_per_launch"][key]
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def _traffic():
@@ -580,7 +690,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "decode", "scan", "gemv", "prefill", "traffic", "scan_traffic"])
+                    choices=["all", "decode", "scan", "gemv", "prefill", "c1", "traffic", "scan_traffic"])
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write a traffic summary from two rocprofv3 --pmc counter CSVs and exit")
     ap.add_argument("--traffic-kernel", default="mm8t_kernel")
@@ -632,12 +742,16 @@ def main(argv=None):
                  f"{pre['roofline']['achieved']} TFLOP/s")
         del model
         torch.cuda.empty_cache()
-    c3 = c4 = None
+    c3 = c4 = c1 = None
     if wl in ("all", "gemv"):
         c3 = run_gemv_c3()
         _log("bench: configs[2] MM8: " + ", ".join(f"{k} {v['us']}us" for k, v in c3.items()))
         c4 = run_gemv_c4()
         _log("bench: configs[3] W4: " + ", ".join(f"{k} {v['asym_us']}us" for k, v in c4.items()))
+    if wl in ("all", "c1"):
+        c1 = run_c1()
+        _log(f"bench: configs[0] 0.1B fp32: prefill {c1['prefill_ms']} ms, decode {c1['decode_ms_per_step']} ms/step, "
+             f"generate {c1['generate_tok_s']} tok/s (host restatement {c1['cpu_baseline']['value']} tok/s)")
 
     out: dict = {}
     if dec is not None and 1 in dec:
@@ -682,11 +796,34 @@ def main(argv=None):
         out["wkv7_decode_form_step"] = step
     if pre:
         out["prefill_c5"] = pre
+    c3_shapes = ((2048, 2048), (2048, 8192), (8192, 2048), (2048, 65536))
+    c4_shapes = ((4096, 4096), (4096, 16384), (16384, 4096), (4096, 65536))
     if c3:
-        out["mm8_c3"] = c3
+        head = c3["2048x65536/b1"]
+        out["mm8_c3"] = {"shapes": c3, "roofline": {
+            "bound": "hbm", "achieved": head["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": head["frac"],
+            "traffic": _traffic_gemv("mm8t_kernel MM8 2048x65536 b1"), "kernel": "mm8t_kernel", "shape": "2048x65536/b1",
+            "bytes_per_launch": mm8_bytes(2048, 65536, 1), "avg_launch_us": head["us"]}}
     if c4:
-        out["w4_c4"] = c4
+        head = c4["4096x65536/b1"]
+        out["w4_c4"] = {"shapes": c4, "roofline": {
+            "bound": "hbm", "achieved": head["asym_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": head["asym_frac"], "traffic": _traffic_gemv("w4t_kernel W4 asym 4096x65536 b1"), "kernel": "w4t_kernel",
+            "shape": "4096x65536/b1 asymmetric",
+            "bytes_per_launch": w4_bytes(4096, 65536, 1, affine=True), "avg_launch_us": head["asym_us"]}}
+    if c1:
+        out["c1_0p1b"] = c1
     if not args.no_cpu and out:
+        for key, shapes, kind, bytes_of in (("mm8_c3", c3_shapes, "mm8", lambda i, o: mm8_bytes(i, o, 1)),
+                                            ("w4_c4", c4_shapes, "w4", lambda i, o: w4_bytes(i, o, 1, affine=False))):
+            if key in out:
+                us = cpu_gemv_baseline(shapes, kind=kind)
+                tot = sum(us.values())
+                out[key]["cpu_baseline"] = {
+                    "value": round(sum(bytes_of(i, o) for i, o in shapes) / (tot / 1e6) / 1e9, 2), "unit": "GB/s",
+                    "cores": host_cores(), "kind": "port", "cpu": cpu_model(), "us_per_call": us,
+                    "sample": ("fp32 numpy dequantise + matmul per call (the reference's CPU form), each shape "
+                               "at batch 1 for about 1 s" + ("" if kind == "mm8" else "; symmetric group-128 W4"))}
         if dec is not None:
             out["cpu_baseline"] = cpu_decode_baseline()
         if scans:
