@@ -18,7 +18,14 @@ from .fused_recurrent_update import (
 )
 from .self_chunk_rwkv7 import dplr_chunk_scan, self_chunk_rwkv7
 from .native_quant_mm8 import MM8Linear, mm8_matmul, mm8_matmul_triton, quantize_mm8, quantize_model_mm8
-from .native_quant_mm4 import MM4Linear, dequantize_mm4, mm4_matmul, quantize_mm4, quantize_model_mm4
+from .native_quant_mm4 import (
+    MM4Linear,
+    dequantize_mm4,
+    mm4_matmul,
+    mm4_matmul_triton,
+    quantize_mm4,
+    quantize_model_mm4,
+)
 from .sm70_quant import quantize_w4_groupwise, w4_groupwise_linear
 from .sampling import argmax_rows
 from . import ops as _ops
@@ -43,6 +50,7 @@ __all__ = [
     "quantize_mm4",
     "dequantize_mm4",
     "mm4_matmul",
+    "mm4_matmul_triton",
     "MM4Linear",
     "quantize_model_mm4",
     "quantize_w4_groupwise",

@@ -80,6 +80,8 @@ SIGNATURES = {
     "rwkv7mi_mm4_pack_t": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "rwkv7mi_mm4t_matmul": (_i32, [_c_p] * 9 + [_i64, _i64, _i64, _i32, _i32, _i32, _c_p]),
     "rwkv7mi_mm4_dequant": (_i32, [_c_p] * 6 + [_i64, _i64, _i32, _i32, _c_p]),
+    "rwkv7mi_mm4_matmul_workspace_bytes": (_sz, [_i64, _i64]),
+    "rwkv7mi_mm4_matmul": (_i32, [_c_p] * 9 + [_i64, _i64, _i64, _i64, _i32, _i32, _i32, _c_p, _sz, _c_p]),
     "rwkv7mi_attn_mix_lora": (
         _i32, [_c_p] * 10 + [_i64, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _f32, _i32, _i32, _c_p]),
     "rwkv7mi_attn_mix_lora_chunks": (_i32, [_i64]),

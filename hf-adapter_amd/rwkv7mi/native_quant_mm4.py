@@ -12,14 +12,17 @@ Packing runs as gfx950 kernels that reproduce the reference's fp32 op sequence
 bit for bit.  ``MM4Linear`` keeps its affine nibbles packed along the inputs
 (``packed_t [out, in/2]``), the layout the fused HIP GEMV streams; its
 ``state_dict`` holds the reference's ``packed [in, ceil(out/2)]``, converted on
-save and load.  The functional reference-layout calls dequantise and use a
-library GEMM, as the reference's own ``mm4_matmul`` does.  GPU tensors only.
+save and load.  The Triton-named functional calls run a fused MFMA kernel
+straight over the reference layout (``rwkv7mi_mm4_matmul``); ``mm4_matmul``
+dequantises and uses a library GEMM, as the reference's own does.  GPU
+tensors only.
 """
 from __future__ import annotations
 
 import torch
 
 from . import _lib
+from . import workspace as _ws
 from .native_quant_policy import normalize_native_mm_policy, should_quantize_linear
 from .sm70_quant import quantize_w4_groupwise, w4_groupwise_linear, w4_groupwise_linear_into
 
@@ -99,17 +102,93 @@ def mm4_gemv_available(device=None) -> bool:
     return torch.cuda.is_available()
 
 
-def mm4_gemv_triton(x, packed, mx, rx_s, my, ry_s, m_orig):
-    """Reference name of the B=1 GEMV; reference-layout weights take the dequant route."""
-    return mm4_matmul(x, packed, mx, rx_s, my, ry_s, m_orig)
+# Rows above which the reference-layout matmul dequantises once and runs a
+# library GEMM: the fused kernel streams the packed bytes once per 16 rows.
+MM4_FUSED_MAX_ROWS = 64
 
 
-def mm4_batched_gemv_triton(x, packed, mx, rx_s, my, ry_s, m_orig):
-    return mm4_matmul(x, packed, mx, rx_s, my, ry_s, m_orig)
+def mm4_workspace_bytes(n: int, m_padded: int) -> int:
+    """K-range partials of the reference-layout kernel (the ``"mm4"`` slot)."""
+    return int(_lib.load().rwkv7mi_mm4_matmul_workspace_bytes(int(n), int(m_padded)))
+
+
+def mm4_matmul_into(x2, packed, mx, rx_s, my, ry_s, out, *, bias=None, residual=None, epilogue=_lib.EPI_NONE):
+    """Fused product over the reference layout ``packed [N, M_pad/2]``:
+    ``out [rows, M] = epilogue(x2 [rows, N] @ dequant(W)[:, :M])``, M <= M_pad."""
+    if x2.dim() != 2 or packed.dim() != 2:
+        raise ValueError("mm4: x2 must be [rows, N] and packed [N, M_pad/2]")
+    rows, n = (int(s) for s in x2.shape)
+    if int(packed.shape[0]) != n:
+        raise ValueError(f"input width {n} does not match quantized weight width {packed.shape[0]}")
+    mp = 2 * int(packed.shape[1])
+    m = int(out.shape[-1])
+    if m > mp or int(mx.numel()) < m or int(rx_s.numel()) < m or int(my.numel()) != n or int(ry_s.numel()) != n:
+        raise ValueError(f"mm4: scales do not match packed {tuple(packed.shape)} and {m} outputs")
+    if tuple(out.shape) != (rows, m) or not out.is_contiguous() or out.dtype != x2.dtype:
+        raise ValueError("mm4: out must be a contiguous [rows, M] tensor of x's dtype")
+    if residual is not None:
+        residual = residual.reshape(rows, m)
+        if not residual.is_contiguous() or residual.dtype != x2.dtype:
+            raise ValueError("mm4: residual must be contiguous with x's dtype")
+    _lib.require_gpu(x2, packed, out, name="mm4_matmul")
+    x2 = x2.contiguous()
+    packed = packed.contiguous()
+    mdt = mx.dtype
+    meta = [t.reshape(-1).to(mdt).contiguous() for t in (mx, rx_s, my, ry_s)]
+    if bias is not None:
+        bias = bias.reshape(-1).to(mdt).contiguous()
+    ws = _ws.reserve(x2.device, mm4_workspace_bytes(n, mp), slot="mm4")
+    _lib.call("rwkv7mi_mm4_matmul", _lib.ptr(x2), _lib.ptr(packed), *(_lib.ptr(t) for t in meta), _lib.ptr(bias),
+              _lib.ptr(residual), _lib.ptr(out), rows, n, m, mp, int(epilogue), _lib.dtype_code(x2),
+              _lib.dtype_code(meta[0]), _lib.ptr(ws), int(ws.numel()), _lib.stream_of(x2))
+    return out
+
+
+def _fused(x2, packed, mx, rx_s, my, ry_s, m_orig):
+    out = torch.empty((int(x2.shape[0]), int(m_orig)), device=x2.device, dtype=x2.dtype)
+    return mm4_matmul_into(x2, packed, mx, rx_s, my, ry_s, out)
+
+
+def mm4_gemv_triton(x, packed, mx, rx_s, my, ry_s, m_orig, *, block_pairs=None, block_n=None):
+    """Fused dequant GEMV ``x [N] -> [M_orig]`` (rwkv7_hf/native_quant_mm4.py:458-471).
+    ``block_pairs`` / ``block_n`` are the reference's Triton tile knobs and are
+    accepted for signature parity; the HIP kernel picks its own tiling."""
+    _lib.require_gpu(x, packed, name="mm4_gemv_triton")
+    return _fused(x.reshape(1, -1), packed, mx, rx_s, my, ry_s, m_orig).reshape(-1)
+
+
+def mm4_batched_gemv_triton(x, packed, mx, rx_s, my, ry_s, m_orig, *, block_pairs=None, block_n=None):
+    """Fused GEMV for a small ``[B, N]`` decode batch (rwkv7_hf/native_quant_mm4.py:474-491)."""
+    if not (x.is_cuda and x.dim() == 2):
+        raise RuntimeError("mm4_batched_gemv_triton requires a 2-D CUDA input")
+    return _fused(x, packed, mx, rx_s, my, ry_s, m_orig)
+
+
+def mm4_batched_dot_triton(x, packed, mx, rx_s, my, ry_s, m_orig, *, block_b=None, block_pairs=None, block_n=None,
+                           num_warps=None):
+    """The fp16 matrix-core batch path (rwkv7_hf/native_quant_mm4.py:494-542);
+    the same MFMA kernel as every other row count here."""
+    if not (x.is_cuda and x.dim() == 2):
+        raise RuntimeError("mm4_batched_dot_triton requires a 2-D CUDA input")
+    if x.dtype != torch.float16:
+        raise TypeError("mm4_batched_dot_triton currently requires fp16 input")
+    return _fused(x, packed, mx, rx_s, my, ry_s, m_orig)
 
 
 def mm4_matmul_triton(x, packed, mx, rx_s, my, ry_s, m_orig, *, max_gemv_rows: int | None = None):
-    return mm4_matmul(x, packed, mx, rx_s, my, ry_s, m_orig)
+    """Routed matmul (rwkv7_hf/native_quant_mm4.py:545-578): 1-D and 2-D inputs
+    of at most ``max_gemv_rows`` rows (default ``MM4_FUSED_MAX_ROWS``) run the
+    fused kernel; more rows, or more than two dimensions, dequantise once and
+    run a library GEMM."""
+    _lib.require_gpu(x, packed, name="mm4_matmul_triton")
+    if x.dim() == 1:
+        return mm4_gemv_triton(x, packed, mx, rx_s, my, ry_s, m_orig)
+    if x.dim() != 2:
+        return mm4_matmul(x, packed, mx, rx_s, my, ry_s, m_orig)
+    limit = MM4_FUSED_MAX_ROWS if max_gemv_rows is None else min(max(1, int(max_gemv_rows)), 65536)
+    if int(x.shape[0]) > limit:
+        return mm4_matmul(x, packed, mx, rx_s, my, ry_s, m_orig)
+    return _fused(x, packed, mx, rx_s, my, ry_s, m_orig)
 
 
 def mm4t_matmul_into(x2, packed_t, mx, rx_s, my, ry_s, out, *, bias=None, residual=None, epilogue=_lib.EPI_NONE):
@@ -296,7 +375,8 @@ def quantize_model_mm4(model, *, min_params: int = 8_000_000, fused: bool = True
 
 __all__ = [
     "quantize_mm4", "quantize_mm4_outmajor", "dequantize_mm4", "mm4_matmul", "mm4_linear", "mm4_gemv_available",
-    "mm4_gemv_triton", "mm4_batched_gemv_triton", "mm4_matmul_triton", "mm4t_matmul_into", "MM4Linear",
+    "mm4_gemv_triton", "mm4_batched_gemv_triton", "mm4_batched_dot_triton", "mm4_matmul_triton", "mm4_matmul_into",
+    "mm4_workspace_bytes", "MM4_FUSED_MAX_ROWS", "mm4t_matmul_into", "MM4Linear",
     "quantize_model_mm4", "normalize_native_mm4_group_policy", "native_mm4_group_size_for_module",
     "NATIVE_MM4_GROUP_POLICIES", "outmajor_to_reference", "reference_to_outmajor",
 ]

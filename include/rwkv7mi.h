@@ -452,6 +452,24 @@ int rwkv7mi_mm4_dequant(const uint8_t* packed, const void* mx, const void* rx_s,
                         const void* my, const void* ry_s, void* out, int64_t I,
                         int64_t O, int meta_dtype, int out_dtype, void* stream);
 
+/* y[rows,O] = epilogue(x @ dequant(W)) straight from the reference layout
+ * packed [I, Mp/2] (nibble pairs along the outputs; Mp even, O <= Mp):
+ * rx_s * sum x*ry_s*(u4+0.5) on MFMA with fp32 accumulation (x*ry_s split
+ * into fp16 hi + lo), plus sum x*my + mx * sum x in fp32.  Replaces the fused
+ * mm4_gemv_triton / mm4_batched_gemv_triton / mm4_batched_dot_triton /
+ * mm4_matmul_triton kernels (rwkv7_hf/native_quant_mm4.py:158-288,
+ * :458-578).  rows are taken 16 at a time; workspace of
+ * rwkv7mi_mm4_matmul_workspace_bytes(I, Mp), 16-byte aligned, holds the
+ * K-range partials (reduced in a fixed order, no atomics); y may alias
+ * residual. */
+size_t rwkv7mi_mm4_matmul_workspace_bytes(int64_t I, int64_t Mp);
+int rwkv7mi_mm4_matmul(const void* x, const uint8_t* packed, const void* mx,
+                       const void* rx_s, const void* my, const void* ry_s,
+                       const void* bias, const void* residual, void* y,
+                       int64_t rows, int64_t I, int64_t O, int64_t Mp,
+                       int epilogue, int act_dtype, int meta_dtype,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* Decode attention-side entry for 1..8 rows, fp16 / bf16: layer 0's
  * pre-norm (pre_w / pre_b; the normalised row goes to x_out), h = LayerNorm
  * (h_out), the r / k / v mixed rows of mixes {r, w, k, v, a, g} (outs[3]),

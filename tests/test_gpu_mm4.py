@@ -178,3 +178,127 @@ def test_mm4_head_shape_c4(oracle, rows):
     deq = oracle.mm4_dequant(*(_np(t) for t in ref_layout[:5]), m_orig)
     ref = x.astype(np.float64) @ deq
     assert _rel_err(_np(out).astype(np.float64), ref) <= 2e-3
+
+
+# ---------------------------------------------------- reference-layout fused kernel
+# Tolerances (relative to max|y|), about twice the largest error measured on an
+# MI355X over the cases below (fp32 9e-7, fp16 4e-4, bf16 2.5e-3): x*ry_s enters
+# the MFMA as fp16 hi + lo (~2^-22 per product) with fp32 sums, so the fp16 /
+# bf16 figures are their one output rounding.
+_TOL = {torch.float32: 2e-6, torch.float16: 1e-3, torch.bfloat16: 5e-3}
+
+
+def _fused_case(oracle, I, O, rows, dtype, seed):
+    from rwkv7mi import quantize_mm4
+
+    rng = np.random.default_rng(seed)
+    W = _cuda(rng.standard_normal((I, O)) * 0.02, dtype)
+    q = quantize_mm4(W)
+    x = rng.standard_normal((rows, I)).astype(np.float32)
+    xd = _cuda(x, dtype)
+    deq = oracle.mm4_dequant(_np(q[0]), *(_np(t.float()) for t in q[1:5]), q[5])
+    return q, xd, _np(xd.float()).astype(np.float64) @ deq
+
+
+@pytest.mark.parametrize("IO", [(4096, 4096), (1024, 4097), (16384, 512), (96, 40), (300, 24), (5, 3)])
+@pytest.mark.parametrize("rows", [1, 5, 16, 33, 64])
+def test_mm4_reference_layout_fused_matches_oracle(oracle, IO, rows):
+    """mm4_matmul_triton over packed [I, Mp/2]: aligned rows (Mp % 16 == 0),
+    bytewise rows (odd O, narrow O), ragged K ranges and 16-row tiles."""
+    from rwkv7mi import mm4_matmul_triton
+
+    I, O = IO
+    q, xd, ref = _fused_case(oracle, I, O, rows, torch.float16, I + 7 * O + rows)
+    y = mm4_matmul_triton(xd, *q[:5], q[5])
+    torch.cuda.synchronize()
+    assert y.shape == (rows, O) and y.dtype == torch.float16
+    err = _rel_err(_np(y).astype(np.float64), ref)
+    print(f"PARITY mm4 reference layout I={I} O={O} rows={rows} f16: rel {err:.2e}", flush=True)
+    assert err <= _TOL[torch.float16]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("IO", [(2048, 1536), (640, 77)])
+def test_mm4_reference_layout_fused_dtypes(oracle, IO, dtype):
+    from rwkv7mi.native_quant_mm4 import mm4_batched_gemv_triton, mm4_gemv_triton
+
+    I, O = IO
+    q, xd, ref = _fused_case(oracle, I, O, 7, dtype, I + O)
+    y = mm4_batched_gemv_triton(xd, *q[:5], q[5])
+    y1 = mm4_gemv_triton(xd[3], *q[:5], q[5])
+    torch.cuda.synchronize()
+    assert y1.shape == (O,)
+    assert torch.equal(y1, y[3])  # a row's result does not depend on the other rows of its tile
+    err = _rel_err(_np(y.float()).astype(np.float64), ref)
+    print(f"PARITY mm4 reference layout I={I} O={O} rows=7 {dtype}: rel {err:.2e}", flush=True)
+    assert err <= _TOL[dtype]
+
+
+def test_mm4_reference_layout_epilogues(oracle):
+    from rwkv7mi._lib import EPI_RELU2, EPI_RESIDUAL
+    from rwkv7mi.native_quant_mm4 import mm4_matmul_into
+
+    I, O, rows = 1024, 1000, 9
+    q, xd, ref = _fused_case(oracle, I, O, rows, torch.float16, 11)
+    rng = np.random.default_rng(12)
+    bias = _cuda(rng.standard_normal(O) * 0.1, torch.float16)
+    res = _cuda(rng.standard_normal((rows, O)), torch.float16)
+    ref_b = ref + _np(bias.float()).astype(np.float64)
+    out = torch.empty(rows, O, device="cuda", dtype=torch.float16)
+    mm4_matmul_into(xd, *q[:5], out, bias=bias, epilogue=EPI_RELU2)
+    torch.cuda.synchronize()
+    r2 = np.maximum(ref_b, 0) ** 2
+    assert _rel_err(_np(out).astype(np.float64), r2) <= _TOL[torch.float16]
+    out2 = res.clone()  # y aliases the residual
+    mm4_matmul_into(xd, *q[:5], out2, bias=bias, residual=out2, epilogue=EPI_RESIDUAL)
+    torch.cuda.synchronize()
+    ra = ref_b + _np(res.float()).astype(np.float64)
+    assert _rel_err(_np(out2).astype(np.float64), ra) <= _TOL[torch.float16]
+
+
+@pytest.mark.parametrize("name", ["f16_24x41", "f16_41x23", "f16_7x5", "f32_33x33", "f32_256x128"])
+def test_mm4_reference_layout_on_reference_packed_bytes(oracle, name):
+    """The fused kernel over the bytes and scales the reference packer wrote
+    (committed fixture), against the fp64 dequantisation of those bytes."""
+    from quant_golden import case, cases
+    from rwkv7mi import mm4_matmul_triton
+
+    if name not in cases("mm4"):
+        pytest.skip(f"fixture has no case {name}")
+    c = case("mm4", name)
+    dtype = torch.float16 if name.startswith("f16") else torch.float32
+    m, m_pad = (int(v) for v in c["m"])
+    I = int(c["packed"].shape[0])
+    assert int(c["packed"].shape[1]) * 2 == m_pad
+    rng = np.random.default_rng(I * 31 + m)
+    x = _cuda(rng.standard_normal((3, I)), dtype)
+    meta = [_cuda(c[k], dtype) for k in ("mx", "rx", "my", "ry")]
+    y = mm4_matmul_triton(x, _cuda(c["packed"], torch.uint8), *meta, m)
+    torch.cuda.synchronize()
+    ref = _np(x.float()).astype(np.float64) @ oracle.mm4_dequant(c["packed"], c["mx"], c["rx"], c["my"], c["ry"], m)
+    assert _rel_err(_np(y.float()).astype(np.float64), ref) <= _TOL[dtype]
+
+
+def test_mm4_reference_layout_routing(oracle):
+    from rwkv7mi import mm4_matmul, mm4_matmul_triton
+    from rwkv7mi.native_quant_mm4 import MM4_FUSED_MAX_ROWS, mm4_batched_dot_triton
+
+    I, O = 512, 96
+    q, xd, ref = _fused_case(oracle, I, O, MM4_FUSED_MAX_ROWS + 3, torch.float16, 21)
+    big = mm4_matmul_triton(xd, *q[:5], q[5])  # above the fused row limit: dequantise + GEMM
+    assert torch.equal(big, mm4_matmul(xd, *q[:5], q[5]))
+    capped = mm4_matmul_triton(xd[:8], *q[:5], q[5], max_gemv_rows=4)
+    assert torch.equal(capped, mm4_matmul(xd[:8], *q[:5], q[5]))
+    fused = mm4_matmul_triton(xd[:8], *q[:5], q[5])
+    x3 = xd[:8].reshape(2, 4, I)
+    y3 = mm4_matmul_triton(x3, *q[:5], q[5])
+    torch.cuda.synchronize()
+    assert y3.shape == (2, 4, O)
+    for y in (big, fused):
+        assert _rel_err(_np(y).astype(np.float64), ref[: y.shape[0]]) <= _TOL[torch.float16]
+    with pytest.raises(TypeError):
+        mm4_batched_dot_triton(xd.float(), *q[:5], q[5])
+    with pytest.raises(RuntimeError):
+        mm4_batched_dot_triton(xd[0], *q[:5], q[5])
+    with pytest.raises(ValueError):
+        mm4_matmul_triton(xd[:8, :-2], *q[:5], q[5])
