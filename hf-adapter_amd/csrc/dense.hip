@@ -11,6 +11,7 @@
 // 16-feature tile; its 4 waves take interleaved 32-wide k-steps and are
 // reduced through LDS.  fp16 operands are used as-is; fp32 / bf16 operands are
 // split into fp16 hi + lo (three MFMAs) so accuracy stays fp32-class.
+// One to four rows take a GEMV form instead (dense_gemv_kernel below).
 #include "common.h"
 
 namespace rwkv7mi {
@@ -121,6 +122,102 @@ __global__ __launch_bounds__(256) void dense_kernel(DenseBatch batch, int rows) 
   }
 }
 
+// ---------------------------------------------------------------- 1..4 rows
+// GEMV form: one wave per output feature n, a workgroup owns four features
+// of one problem (a problem's features start at a multiple of four tiles).
+// Lanes split K in 16-byte runs of W's row n and of the x rows at the same k;
+// a pass is GV_U runs per lane, and the next pass's runs load while this one
+// multiplies.  Plain fp32 FMAs, then a fixed-order wave reduction per row:
+// every output is an fp32 dot product whatever the dtype.
+constexpr int GV_U = 4;  // 16-byte runs per lane per pass
+
+// 16 raw bytes -> the run's VE elements as fp32
+template <typename TA>
+__device__ __forceinline__ void gv_cvt(const u32x4& a, float (&o)[16 / sizeof(TA)]) {
+  if constexpr (sizeof(TA) == 4) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = __uint_as_float(a[q]);
+  } else if constexpr (std::is_same<TA, __half>::value) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t w = a[q];
+      f16x2_to_f32(w, o[2 * q], o[2 * q + 1]);
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      o[2 * q] = __uint_as_float(a[q] << 16);
+      o[2 * q + 1] = __uint_as_float(a[q] & 0xffff0000u);
+    }
+  }
+}
+
+template <typename TA, int R>
+__global__ __launch_bounds__(256) void dense_gemv_kernel(DenseBatch batch, int rows) {
+  constexpr int VE = 16 / (int)sizeof(TA);  // elements per run
+  int pi = 0;
+#pragma unroll
+  for (int q = 1; q < 4; ++q)
+    if (q < batch.nprob && (int)blockIdx.x >= batch.p[q].tile0) pi = q;
+  const DenseProb P = batch.p[pi];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int n = ((int)blockIdx.x - P.tile0) * 4 + wave;
+  if (n >= P.N) return;  // wave-uniform; no barrier follows
+  const int K = P.K;
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(reinterpret_cast<const TA*>(P.W) + (int64_t)n * K, (uint32_t)K * (uint32_t)sizeof(TA));
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(P.x, (uint32_t)rows * (uint32_t)K * (uint32_t)sizeof(TA));
+  const int PASS = 64 * GV_U * VE;  // elements of K per pass
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  // two register sets of raw runs in turn (named, so every index is static);
+  // runs convert to fp32 as they are multiplied
+  u32x4 wa[GV_U], xa[R][GV_U], wb[GV_U], xb[R][GV_U];
+  auto issue = [&](u32x4 (&w)[GV_U], u32x4 (&x)[R][GV_U], int k0) {
+#pragma unroll
+    for (int u = 0; u < GV_U; ++u) {
+      const int k = k0 + (u * 64 + lane) * VE;
+      const bool ok = k < K;  // K % 8 == 0: a run is all in or all out
+      w[u] = buf_ld16(rw, ok ? (uint32_t)k * (uint32_t)sizeof(TA) : BUF_OOB);
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        x[r][u] = buf_ld16(rx, ok && r < rows ? (uint32_t)(r * K + k) * (uint32_t)sizeof(TA) : BUF_OOB);
+    }
+  };
+  auto fma_pass = [&](const u32x4 (&w)[GV_U], const u32x4 (&x)[R][GV_U]) {
+#pragma unroll
+    for (int u = 0; u < GV_U; ++u) {
+      float wf[VE];
+      gv_cvt<TA>(w[u], wf);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float xf[VE];
+        gv_cvt<TA>(x[r][u], xf);
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[r] = __builtin_fmaf(xf[e], wf[e], acc[r]);
+      }
+    }
+  };
+  issue(wa, xa, 0);
+  for (int k0 = 0; k0 < K; k0 += 2 * PASS) {
+    if (k0 + PASS < K) issue(wb, xb, k0 + PASS);
+    fma_pass(wa, xa);
+    if (k0 + PASS >= K) break;
+    if (k0 + 2 * PASS < K) issue(wa, xa, k0 + 2 * PASS);
+    fma_pass(wb, xb);
+  }
+  const TA* bias = reinterpret_cast<const TA*>(P.bias);
+  const float b = bias ? to_f32(bias[n]) : 0.f;
+  TA* y = reinterpret_cast<TA*>(P.y);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float v = wave_sum(acc[r]);
+    if (lane == r && r < rows) y[(int64_t)r * P.N + n] = from_f32<TA>(apply_act(v + b, P.act));
+  }
+}
+
 }  // namespace rwkv7mi
 
 using namespace rwkv7mi;
@@ -147,6 +244,27 @@ extern "C" int rwkv7mi_dense_multi(const void* const* xs, const void* const* Ws,
   }
   batch.nprob = (int)nprob;
   const size_t esz = act_dtype == RWKV7MI_F32 ? 4 : 2;
+  if (rows <= 4) {  // the GEMV form: tiles of four features, one wave each
+    DenseBatch gb = batch;
+    int gt = 0;
+    for (int i = 0; i < nprob; ++i) {
+      gb.p[i].tile0 = gt;
+      gt += (int)((Ns[i] + 3) / 4);
+    }
+    for (int i = 0; i < nprob; ++i)
+      if ((int64_t)rows * Ks[i] * (int64_t)esz > INT32_MAX || Ks[i] * (int64_t)esz > INT32_MAX)
+        return fail(RWKV7MI_EINVAL, "dense_multi: too large for 32-bit offsets");
+    return dispatch_dtype(act_dtype, [&](auto ta) {
+      using TA = decltype(ta);
+      if (rows == 1)
+        hipLaunchKernelGGL((dense_gemv_kernel<TA, 1>), dim3(gt), dim3(256), 0, as_stream(stream), gb, (int)rows);
+      else if (rows == 2)
+        hipLaunchKernelGGL((dense_gemv_kernel<TA, 2>), dim3(gt), dim3(256), 0, as_stream(stream), gb, (int)rows);
+      else
+        hipLaunchKernelGGL((dense_gemv_kernel<TA, 4>), dim3(gt), dim3(256), 0, as_stream(stream), gb, (int)rows);
+      return check_launch("dense_gemv_kernel");
+    });
+  }
   for (int64_t r0 = 0; r0 < rows; r0 += 64) {
     const int64_t nr = rows - r0 > 64 ? 64 : rows - r0;
     DenseBatch bb = batch;

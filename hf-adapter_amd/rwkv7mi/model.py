@@ -189,8 +189,12 @@ def random_weights(cfg: NativeRWKV7Config, *, seed: int = 0, device="cpu", dtype
 
 # ------------------------------------------------------------------ linears
 class DenseLinear:
-    """fp16/bf16 Linear ``y = x W^T`` on the HIP dense kernel (decode sizes) or a
-    library GEMM (long prefills)."""
+    """Unquantised Linear ``y = x W^T`` (projections below the MM8 size
+    threshold, and every projection of an unquantised model such as the fp32
+    0.1B one): the HIP dense kernel up to 256 rows; above that a plain library
+    GEMM (hipBLASLt through torch), with the relu^2 / residual epilogue as torch
+    elementwise ops -- a dense prefill product is MFMA-bound, where the library
+    GEMM is the right tool."""
 
     def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None = None):
         self.weight = weight.contiguous()
@@ -217,10 +221,11 @@ class DenseLinear:
 
 
 class QuantLinear:
-    """MM8 Linear: the fused out-major dequant GEMV for up to ``GEMV_ROWS``
-    rows, the 64-row MFMA tile GEMM (split K) up to ``GEMM_ROWS`` rows, and a
-    dequantise + library GEMM route above that (long prefills, where the
-    products are MFMA-bound and the library GEMM's tiling pays)."""
+    """MM8 Linear, all on HIP kernels: the fused blocked dequant GEMV for up to
+    ``GEMV_ROWS`` rows, the 64-row MFMA tile GEMM (split K) up to ``GEMM_ROWS``
+    rows, and the dequant-in-register 256 x 256 prefill GEMM above that
+    (``mm8_gemm_prefill_multi_into``).  Modules whose bytes are not blocked
+    take MM8Linear's own route."""
 
     GEMV_ROWS = GEMV_ROWS
     GEMM_ROWS = GEMM_ROWS

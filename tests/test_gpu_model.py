@@ -15,6 +15,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 LOGIT_REL = 2e-3
+STATE_REL = 2.5e-3  # recurrent state after an fp16 prefill, as the 7.2B slice
 
 
 def _cfg(mm8: bool, layers=2, D=128, F=256):
@@ -75,7 +76,9 @@ def test_prefill_then_decode_matches_oracle(mm8, B):
     # the cache matches the oracle's recurrent state after the prompt
     for i in range(cfg.num_hidden_layers):
         s = cache._state[i].double().cpu().numpy()
-        assert np.abs(s - st["state"][i]).max() <= 2e-2 * np.abs(st["state"][i]).max()
+        rel = np.abs(s - st["state"][i]).max() / np.abs(st["state"][i]).max()
+        print(f"PARITY small model prefill layer {i}: state rel {rel:.2e}", flush=True)
+        assert rel <= STATE_REL, (i, rel)
     nxt = ids[:, -1]
     for step in range(4):
         nxt = rng.integers(0, cfg.vocab_size, (B,))

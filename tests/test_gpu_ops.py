@@ -119,6 +119,42 @@ def test_ffn_add_norm_mix(oracle):
     _ok(prev, h)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 17])
+def test_dense_multi_matches_fp64(rows, dt):
+    """Grouped dense products (rwkv7mi_dense_multi): the GEMV form at 1..4 rows
+    (one wave per feature, fp32 FMAs) and the MFMA form above, with bias and
+    every activation, K not a multiple of a pass and N not a multiple of the
+    tiles, against fp64.  Bound: 1e-5 of the row's sum |x||W| in fp32 (the
+    MFMA form splits fp32 into fp16 hi + lo), else one output rounding."""
+    from rwkv7mi.fused_lora import dense_multi
+
+    rng = np.random.default_rng(rows * 7 + {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[dt])
+    shapes = [(768, 768, 0), (3070, 776, 3), (37, 4096, 1), (130, 3072, 2)]  # (N, K, act)
+    probs, refs = [], []
+    for N, K, act in shapes:
+        x = _t(rng.standard_normal((rows, K)), dt)
+        W = _t(rng.standard_normal((N, K)) / np.sqrt(K), dt)
+        b = _t(rng.standard_normal(N) * 0.1, dt) if act != 2 else None
+        y = torch.full((rows, N), float("nan"), device="cuda", dtype=dt)
+        probs.append((x, W, b, y, act))
+        z = _f(x) @ _f(W).T + (0 if b is None else _f(b))
+        mag = np.abs(_f(x)) @ np.abs(_f(W)).T
+        ref = {0: z, 1: np.tanh(z), 2: 1 / (1 + np.exp(-z)), 3: np.maximum(z, 0) ** 2}[act]
+        refs.append((ref, mag, act, z))
+    dense_multi(probs, rows)
+    torch.cuda.synchronize()
+    for (x, W, b, y, act), (ref, mag, a, z) in zip(probs, refs):
+        got = _f(y)
+        assert np.isfinite(got).all()
+        err = np.abs(got - ref)
+        # the pre-activation error bound, carried through the activation's slope
+        slope = {0: 1.0, 1: 1.0, 2: 0.25, 3: 2 * np.abs(z) + 1e-3}[a]
+        pre = 1e-5 * mag if dt == torch.float32 else 0.0
+        out_round = (2.0 ** -8 if dt == torch.bfloat16 else 2.0 ** -11) * np.abs(ref) if dt != torch.float32 else 0.0
+        assert (err <= pre * slope + out_round + 1e-6).all(), (rows, a, err.max())
+
+
 @pytest.mark.parametrize("B,T,D", [(2, 33, 768), (1, 1, 4096), (3, 5, 256)])
 def test_sequence_shift_mix(oracle, B, T, D):
     from rwkv7mi.fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
