@@ -165,8 +165,11 @@ __global__ __launch_bounds__(256) void w4g_kernel(const TA* __restrict__ x, cons
 //
 // A workgroup (NW waves) owns 16 output columns at a time and loops over
 // column groups g = blockIdx.x, + gridDim.x, ... (persistent).  K is walked in
-// 256-input steps (128 bytes of each column): wave w takes steps w, w + NW,
-// ...; lane (n = l%16, kg = l/16) loads bytes 16kg.. and 64 + 16kg.. of
+// 256-input steps (128 bytes of each column): in each chunk wave w takes the
+// CSW consecutive steps w CSW .. w CSW + CSW - 1, so its scale (and bias)
+// entries are one short run per column, loaded once per (group, chunk) in
+// 16-byte loads (the next group's while this one runs) rather than per step;
+// lane (n = l%16, kg = l/16) loads bytes 16kg.. and 64 + 16kg.. of
 // column n's step, two 16-byte loads whose dwords are the B operands of 8
 // MFMAs (nibbles widened to fp16 q - 8, exact).  Each 128-input half of a
 // step lies in one scale group (group 128: its own; group 256: half of one),
@@ -188,6 +191,7 @@ struct W4tArgs {
   const void* residual; // [rows, O] or null
   void* y;              // [rows, O]
   int rows, I, O, G, gshift, epilogue;  // gshift: log2(group / 128)
+  int svec;  // every wave's scale run starts on a 16-byte boundary
 };
 
 template <typename TS>
@@ -207,6 +211,49 @@ __device__ __forceinline__ float w4t_raw_f32(uint32_t v) {
   else
     return __uint_as_float(v << 16);
 }
+
+// A wave's scale (and bias) entries of one (column group, chunk): its CSW
+// steps are consecutive (steps wave*CSW .. +CSW-1 of the chunk), so their
+// 2*CSW 128-input blocks fall in 2*CSW (group 128) or CSW (group 256)
+// consecutive groups of the lane's column: raw 16-byte loads of that row of
+// the scale matrix, packed TS values.
+template <typename TS, int CSW>
+struct W4tScales {
+  static constexpr int NV = 2 * CSW;                                   // values loaded
+  static constexpr int NQ = (NV * (int)sizeof(TS) + 15) / 16;          // 16-byte loads
+  u32x4 q[NQ];
+  // vec: the run starts on a 16-byte boundary (host-checked for the whole
+  // launch); otherwise the values load one by one into the same packing
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t e0, bool ok, bool vec) {
+    if (vec) {
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) q[i] = buf_ld16(r, ok ? e0 * (uint32_t)sizeof(TS) + 16u * i : BUF_OOB);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) q[i] = (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        const uint32_t x = w4t_ld_raw<TS>(r, e0 + (uint32_t)v, ok);
+        if constexpr (sizeof(TS) == 4) q[v >> 2][v & 3] = x;
+        else q[v >> 3][(v >> 1) & 3] |= x << (16 * (v & 1));
+      }
+    }
+  }
+  // value of 128-input block bi (0 .. 2*CSW-1) of the wave's range
+  __device__ __forceinline__ float get(int bi, int gshift) const {
+    const int v0 = bi, v1 = bi >> 1;  // both compile-time under unrolling
+    const uint32_t a = raw(v0), b = raw(v1);
+    return w4t_raw_f32<TS>(gshift ? b : a);
+  }
+  __device__ __forceinline__ uint32_t raw(int v) const {
+    if constexpr (sizeof(TS) == 4) {
+      return q[v >> 2][v & 3];
+    } else {
+      const uint32_t d = q[v >> 3][(v >> 1) & 3];
+      return (v & 1) ? d >> 16 : d & 0xffffu;
+    }
+  }
+};
 
 template <typename TA, typename TS, int NW, int CSW, bool AFF>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void w4t_kernel(const W4tArgs A) {
@@ -247,23 +294,23 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void w4t_kernel(const W4tArgs A) {
                     AFF ? (uint32_t)(nc * G * sizeof(TS)) : 0u);
     return r;
   };
-  // ring slot: weights, and the raw scale (and bias) bits of the step's halves
+  // global step of local step jl of chunk c for this wave
+  auto gstep = [&](int c, int jl) { return c * (NW * CSW) + wave * CSW + jl; };
+  // ring slot: the step's weights
   u32x4 buf[DEPTH][2];
-  uint32_t sraw[DEPTH][2], braw[DEPTH][2];
   auto load_step = [&](const Res& r, int j, int d) {
-    const int c = j / CSW, jl = j % CSW;
-    const int gs = c * (NW * CSW) + wave + NW * jl;  // global step of this wave
+    const int gs = gstep(j / CSW, j % CSW);
     const int b0 = 128 * gs + 16 * kg;
     buf[d][0] = buf_ld16(r.w, b0 < bcol ? lane_off + 128u * (uint32_t)gs : BUF_OOB);
     buf[d][1] = buf_ld16(r.w, b0 + 64 < bcol ? lane_off + 128u * (uint32_t)gs + 64u : BUF_OOB);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int blk = 2 * gs + h;  // 128-input block
-      const int grp = blk >> gshift;
-      const bool ok = 128 * blk < I;
-      sraw[d][h] = w4t_ld_raw<TS>(r.s, (uint32_t)(n * G + grp), ok);
-      if constexpr (AFF) braw[d][h] = w4t_ld_raw<TS>(r.b, (uint32_t)(n * G + grp), ok);
-    }
+  };
+  // the wave's scale / bias entries of chunk c of the group behind r
+  W4tScales<TS, CSW> sc_cur, sc_next, bi_cur, bi_next;
+  auto load_scales = [&](const Res& r, int c, W4tScales<TS, CSW>& sv, W4tScales<TS, CSW>& bv) {
+    const int grp0 = (2 * gstep(c, 0)) >> gshift;
+    const bool ok = 2 * gstep(c, 0) * 128 < I;
+    sv.load(r.s, (uint32_t)(n * G + grp0), ok, A.svec != 0);
+    if constexpr (AFF) bv.load(r.b, (uint32_t)(n * G + grp0), ok, A.svec != 0);
   };
 
   // staging of chunk c: 8-input items (row r, q), 64 consecutive items per
@@ -319,6 +366,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void w4t_kernel(const W4tArgs A) {
   Res wr = group_res(g), wn = group_res(g + gridDim.x);
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) load_step(wr, d, d);  // DEPTH <= CSW <= J
+  load_scales(wr, 0, sc_cur, bi_cur);
   if (nchunks == 1) {
     stage(0);
     __syncthreads();
@@ -326,9 +374,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void w4t_kernel(const W4tArgs A) {
   const TS* bias = reinterpret_cast<const TS*>(A.bias);
   for (; g < ngroups; g += gridDim.x) {
     f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+    // the next column group's entries (one chunk), in flight during this group
+    if (nchunks == 1) load_scales(wn, 0, sc_next, bi_next);
     for (int c = 0; c < nchunks; ++c) {
       if (nchunks > 1) {
         __syncthreads();  // the previous chunk's (or group's) LDS reads are done
+        if (c > 0) load_scales(wr, c, sc_cur, bi_cur);
         stage(c);
         __syncthreads();
       }
@@ -342,8 +393,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void w4t_kernel(const W4tArgs A) {
           bv[q] = w4_nibbles_to_f16(buf[d][0][q]);
           bv[4 + q] = w4_nibbles_to_f16(buf[d][1][q]);
         }
-        const uint32_t s0 = sraw[d][0], s1 = sraw[d][1];
-        const uint32_t z0 = AFF ? braw[d][0] : 0u, z1 = AFF ? braw[d][1] : 0u;
         // refill the slot (from the next column group past the last step)
         const int t = c * CSW + jl + DEPTH;
         if (!last_chunk || jl + DEPTH < CSW)
@@ -351,7 +400,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void w4t_kernel(const W4tArgs A) {
         else
           load_step(wn, t - J, d);
         __builtin_amdgcn_sched_barrier(0);
-        const int kl = 256 * (wave + NW * jl);  // chunk-local first input of the step
+        const int kl = 256 * (wave * CSW + jl);  // chunk-local first input of the step
         f32x4 gh[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -363,15 +412,15 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void w4t_kernel(const W4tArgs A) {
             if constexpr (HL) gh[h] = mfma16x16x32(*reinterpret_cast<const f16x8*>(al + off), bv[4 * h + q], gh[h]);
           }
         }
-        const float sc0 = w4t_raw_f32<TS>(s0), sc1 = w4t_raw_f32<TS>(s1);
+        const float sc0 = sc_cur.get(2 * jl, gshift), sc1 = sc_cur.get(2 * jl + 1, gshift);
         acc += sc0 * gh[0];
         acc += sc1 * gh[1];
         if constexpr (AFF) {
           const int blk = kl / 128;  // chunk-local 128-input block of half 0
           const f32x4 x0 = *reinterpret_cast<const f32x4*>(gsum + blk * 16 + 4 * kg);
           const f32x4 x1 = *reinterpret_cast<const f32x4*>(gsum + (blk + 1) * 16 + 4 * kg);
-          acc += (8.f * sc0 + w4t_raw_f32<TS>(z0)) * x0;
-          acc += (8.f * sc1 + w4t_raw_f32<TS>(z1)) * x1;
+          acc += (8.f * sc0 + bi_cur.get(2 * jl, gshift)) * x0;
+          acc += (8.f * sc1 + bi_cur.get(2 * jl + 1, gshift)) * x1;
         }
       }
     }
@@ -401,6 +450,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void w4t_kernel(const W4tArgs A) {
     }
     wr = wn;
     wn = group_res(g + 2 * gridDim.x);
+    if (nchunks == 1) {
+      sc_cur = sc_next;
+      if constexpr (AFF) bi_cur = bi_next;
+    } else {
+      load_scales(wr, 0, sc_cur, bi_cur);
+    }
   }
 }
 
@@ -582,8 +637,14 @@ static int w4_matmul(const char* who, const void* x, const uint8_t* packed, cons
     const bool hl = act_dtype != RWKV7MI_F16, aff = gbias != nullptr;
     const size_t lds = w4t_plan(rows, I, O, hl, aff, &nw, &csw);
     if (lds) {
-      W4tArgs a{x, packed, scales, gbias, bias, residual, y, (int)rows, (int)I, (int)O, (int)(I / group),
-                group == 256 ? 1 : 0, epilogue};
+      const int G = (int)(I / group), gsh = group == 256 ? 1 : 0;
+      const size_t ssz = scale_dtype == RWKV7MI_F32 ? 4 : 2;
+      // a wave's run starts at n G + (2 CSW (c NW + w) >> gshift) entries
+      const bool svec = (G * ssz) % 16 == 0 && (((size_t)(2 * csw) >> gsh) * ssz) % 16 == 0 &&
+                        (reinterpret_cast<uintptr_t>(scales) & 15) == 0 &&
+                        (!gbias || (reinterpret_cast<uintptr_t>(gbias) & 15) == 0);
+      W4tArgs a{x, packed, scales, gbias, bias, residual, y, (int)rows, (int)I, (int)O, G, gsh, epilogue,
+                svec ? 1 : 0};
       const int64_t ngroups = (O + 15) / 16;
       const int64_t per_cu = nw == 4 && lds <= 64 * 1024 ? 2 : 1;
       const int64_t gx = std::min<int64_t>(ngroups, mm8t_cus() * per_cu);
