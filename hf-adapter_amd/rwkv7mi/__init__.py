@@ -27,6 +27,13 @@ from .native_quant_mm4 import (
     quantize_model_mm4,
 )
 from .sm70_quant import quantize_w4_groupwise, w4_groupwise_linear
+from .native_wkv_fp16 import (
+    native_fp16_recurrent_available,
+    native_fp16_recurrent_build_error,
+    native_fp16_recurrent_output_prepare_raw,
+    native_fp16_recurrent_should_use,
+    native_fp16_sequence,
+)
 from .sampling import argmax_rows
 from . import ops as _ops
 
@@ -56,4 +63,9 @@ __all__ = [
     "quantize_w4_groupwise",
     "w4_groupwise_linear",
     "argmax_rows",
+    "native_fp16_recurrent_should_use",
+    "native_fp16_recurrent_available",
+    "native_fp16_recurrent_build_error",
+    "native_fp16_recurrent_output_prepare_raw",
+    "native_fp16_sequence",
 ]

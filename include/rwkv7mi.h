@@ -155,6 +155,39 @@ int rwkv7mi_wkv7_chunk_prefill(const void* r, const void* w, const void* k,
  * reference's Triton scans have no cross-wave waits). */
 int rwkv7mi_wkv7_chunk_status(int clear, int* status);
 
+/* ------------------------------------------- wkv7 with an fp16 state (opt-in) */
+
+/* The optional fp16-state lane.  Every tensor is fp16 except elapsed (int32
+ * [B]); state [B,H,64,64] fp16 is updated in place; N must be 64.  The state
+ * math is packed fp16 FMAs in a fixed order (one rounding each) and the decay
+ * enters as wd = exp(-e^-1/2 sigmoid(w)) - 1 + 2^-41 int32(0x9E3779B9 phase),
+ * phase = elapsed[b] + 64 h + i (+ token index).
+ *
+ * Decode from raw projections [B,H,64] with GroupNorm, bonus and gate, out
+ * [B,H,64]; k_k, k_a, r_k, gn_w, gn_b [H*64].  advance_elapsed != 0 adds 1 to
+ * every elapsed[b] after all heads have read it (a second launch on the same
+ * stream).  Replaces rwkv7_native_fp16_recurrent_output_raw_cuda
+ * (rwkv7_hf/native_wkv_fp16.py:463-514, kernel :200-336) behind
+ * native_fp16_recurrent_output_prepare_raw (:678). */
+int rwkv7mi_wkv7_fp16_decode_output_prepare_raw(
+    const void* r, const void* w_raw, const void* k_raw, const void* v,
+    const void* a, void* state, const void* g, const void* k_k,
+    const void* k_a, const void* r_k, const void* gn_w, const void* gn_b,
+    int32_t* elapsed, int advance_elapsed, void* out, int64_t B, int64_t H,
+    int64_t N, float eps, void* stream);
+
+/* T >= 1 tokens of prepared vectors [B,T,H,64]: w raw (plus w0 [H*64] in
+ * fp32 when w0 != NULL), neg_kk = -kk, kka = kk*a; out [B,T,H,64] is the raw
+ * readout y.  elapsed is read, not advanced.  Inputs and state 16-byte
+ * aligned.  Replaces rwkv7_native_fp16_sequence_cuda
+ * (rwkv7_hf/native_wkv_fp16.py:516-583, kernel :338-436) behind
+ * native_fp16_sequence (:756). */
+int rwkv7mi_wkv7_fp16_sequence(const void* r, const void* w, const void* w0,
+                               const void* k, const void* v, const void* neg_kk,
+                               const void* kka, void* state,
+                               const int32_t* elapsed, void* out, int64_t B,
+                               int64_t T, int64_t H, int64_t N, void* stream);
+
 /* ------------------------------------------------------------------- MM8 */
 
 /* Device packer of the uint8 affine format.  weight [I,O] (= Linear.weight.T)
