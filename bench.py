@@ -18,6 +18,8 @@ Workloads (synthetic inputs, random-init weights; nothing is downloaded):
             configs[3], group-128 W4 (asymmetric min/max affine, and the
             reference's symmetric form) at the 7.2B shapes x batch 1/4/16.
   prefill : configs[4]'s prefill, B=8 x T=4096 through the 7.2B model.
+  fp16state: the opt-in fp16-state lane: its sequence kernel at B=8, T=4096,
+            H=64 and its decode kernel at H=64 for bsz 1/8/64.
 The default run measures all of them and prints ONE JSON line.
 
     python bench.py [--steps K] [--warmup W] [--workload all|decode|scan|gemv|prefill|...] [--no-cpu]
@@ -205,6 +207,70 @@ def run_decode_form_step(B=8, H=32, reps=20):
     return {"us_per_step": round(ms * 1e3, 3), "bytes": nbytes, "gbs": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "tok_s": round(B / (ms / 1e3), 1),
             "config": f"B={B} H={H} N={N}, one token, fp32 state in HBM"}
+
+
+def fp16_sequence_bytes(B, T, H, N):
+    """Algorithmic HBM bytes of one fp16-state sequence call: per (token, head,
+    channel) r, w, k, v, -kk, kk*a in and y out, fp16 (14 B); plus the fp16
+    state read and written once."""
+    return B * T * H * N * 14 + 2 * B * H * N * N * 2
+
+
+def fp16_decode_bytes(B, H, N):
+    """One fp16-state decode launch: the fp16 state read and written, six fp16
+    vectors in (r, w, k, v, a, g) and out, five fp16 per-channel parameters."""
+    return B * H * (2 * N * N * 2 + 7 * N * 2) + 5 * H * N * 2 + 4 * B
+
+
+def run_fp16_state(steps=20, warmup=3):
+    """The opt-in fp16-state lane: the sequence kernel at the scan benchmark's
+    shape (B=8, T=4096, H=64) and the decode kernel at a 7.2B layer's heads
+    (H=64) for bsz 1/8/64, hipGraph-replayed over 16 rotating states."""
+    import torch
+    from rwkv7mi import native_fp16_recurrent_output_prepare_raw, native_fp16_sequence
+
+    N, H = 64, 64
+    res = {}
+    B, T = 8, 4096
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    rn = lambda *s: torch.randn(*s, generator=g, device="cuda")
+    r, v = rn(B, T, H, N).half(), rn(B, T, H, N).half()
+    w = (rn(B, T, H, N) * 0.5 - 0.5).half()
+    k = (rn(B, T, H, N) * 0.3).half()
+    kk = torch.nn.functional.normalize(rn(B, T, H, N), dim=-1)
+    a = torch.sigmoid(rn(B, T, H, N))
+    nkk, kka = (-kk).half().contiguous(), (kk * a).half().contiguous()
+    st = torch.zeros(B, H, N, N, device="cuda", dtype=torch.float16)
+    el = torch.zeros(B, device="cuda", dtype=torch.int32)
+    ms, _ = time_events(lambda: native_fp16_sequence(r, w, k, v, nkk, kka, st, el), steps, warmup)
+    nbytes = fp16_sequence_bytes(B, T, H, N)
+    gbs = nbytes / (ms / 1e3) / 1e9
+    res["sequence"] = {"config": f"B={B} T={T} H={H} N={N}, fp16 state", "ms_per_call": round(ms, 4),
+                       "tok_s": round(B * T / (ms / 1e3), 1), "ns_per_token_per_head": round(ms * 1e6 / T, 2),
+                       "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                    "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
+                                    "kernel": "wkv7_f16_sequence_kernel"}}
+    del r, v, w, k, kk, a, nkk, kka
+    dec = {}
+    for B in (1, 8, 64):
+        vec = lambda: rn(B, H, N).half()
+        rr, ww, kr, vv, aa, gg = vec(), vec(), vec(), vec(), torch.sigmoid(rn(B, H, N)).half(), vec()
+        par = lambda: (1.0 + 0.1 * rn(H * N)).half()
+        kk_, ka_, rk_, gw_, gb_ = par(), par(), par(), par(), par()
+        states = [torch.zeros(B, H, N, N, device="cuda", dtype=torch.float16) for _ in range(16)]
+        elapsed = torch.zeros(B, device="cuda", dtype=torch.int32)
+        calls = [(lambda s=s: native_fp16_recurrent_output_prepare_raw(
+            rr, ww, kr, vv, aa, s, gg, kk_, ka_, rk_, gw_, gb_, elapsed, advance_elapsed=False, eps=1e-5))
+            for s in states]
+        ms = time_graph(calls, 20)
+        nbytes = fp16_decode_bytes(B, H, N)
+        gbs = nbytes / (ms / 1e3) / 1e9
+        dec[str(B)] = {"us_per_launch": round(ms * 1e3, 3), "bytes": nbytes, "gbs": round(gbs, 1),
+                       "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del states
+    res["decode_H64"] = dec
+    return res
 
 
 def cpu_scan_baseline(B=8, H=32, N=64, T_sample=1024, seed=0, min_seconds=10.0):
@@ -690,7 +756,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "decode", "scan", "gemv", "prefill", "c1", "traffic", "scan_traffic"])
+                    choices=["all", "decode", "scan", "gemv", "prefill", "c1", "fp16state", "traffic",
+                             "scan_traffic"])
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write a traffic summary from two rocprofv3 --pmc counter CSVs and exit")
     ap.add_argument("--traffic-kernel", default="mm8t_kernel")
@@ -748,6 +815,12 @@ def main(argv=None):
         _log("bench: configs[2] MM8: " + ", ".join(f"{k} {v['us']}us" for k, v in c3.items()))
         c4 = run_gemv_c4()
         _log("bench: configs[3] W4: " + ", ".join(f"{k} {v['asym_us']}us" for k, v in c4.items()))
+    f16 = None
+    if wl in ("all", "fp16state"):
+        f16 = run_fp16_state()
+        _log(f"bench: fp16-state sequence {f16['sequence']['config']}: {f16['sequence']['ms_per_call']} ms "
+             f"({100 * f16['sequence']['roofline']['frac']:.1f}% of HBM); decode H=64: "
+             + ", ".join(f"bsz{b} {d['us_per_launch']}us" for b, d in f16["decode_H64"].items()))
     if wl in ("all", "c1"):
         c1 = run_c1()
         _log(f"bench: configs[0] 0.1B fp32: prefill {c1['prefill_ms']} ms, decode {c1['decode_ms_per_step']} ms/step, "
@@ -813,6 +886,8 @@ def main(argv=None):
             "bytes_per_launch": w4_bytes(4096, 65536, 1, affine=True), "avg_launch_us": head["asym_us"]}}
     if c1:
         out["c1_0p1b"] = c1
+    if f16:
+        out["wkv7_fp16_state"] = f16
     if not args.no_cpu and out:
         for key, shapes, kind, bytes_of in (("mm8_c3", c3_shapes, "mm8", lambda i, o: mm8_bytes(i, o, 1)),
                                             ("w4_c4", c4_shapes, "w4", lambda i, o: w4_bytes(i, o, 1, affine=False))):

@@ -44,10 +44,11 @@ __device__ __forceinline__ float f16_dither(uint32_t phase) {
 }
 
 // exp(-e^-1/2 sigmoid(wv)) - 1 + dither, in fp32, rounded to fp16
+// (hardware 2^x and 1/x, each within about an ulp of fp32)
 __device__ __forceinline__ _Float16 f16_decay_delta(float wv, uint32_t phase) {
-  const float t = exp2f(-F16_LOG2E * wv);
-  const float d = exp2f(-F16_DECAY_LOG2 / (1.0f + t)) - 1.0f + f16_dither(phase);
-  return (_Float16)d;
+  const float t = __builtin_amdgcn_exp2f(-F16_LOG2E * wv);
+  const float e = __builtin_amdgcn_exp2f(-F16_DECAY_LOG2 * __builtin_amdgcn_rcpf(1.0f + t));
+  return (_Float16)(e - 1.0f + f16_dither(phase));
 }
 
 // 16-byte LDS row read -> 4 half pairs
@@ -90,40 +91,98 @@ __device__ __forceinline__ void f16_row_put(_Float16* s_st, int lane, const h2 (
         make_uint4(h2_u32(s[4 * m]), h2_u32(s[4 * m + 1]), h2_u32(s[4 * m + 2]), h2_u32(s[4 * m + 3]));
 }
 
-// One token on the lane's row.  rv/wv/kv/nv/bv: the token's r, wd, k, -kk,
-// kk*a (64 halves each, LDS, read as broadcasts); vi = v[row].  Returns y[row].
-__device__ __forceinline__ _Float16 f16_row_step(h2 (&s)[32], const _Float16* rv, const _Float16* wv,
-                                                 const _Float16* kv, const _Float16* nv, const _Float16* bv,
-                                                 _Float16 vi) {
-  h2 sa2 = {(_Float16)0.0f, (_Float16)0.0f};
+// 64 halves of a token vector in LDS -> 32 half pairs
+__device__ __forceinline__ void lds_h2x32(const _Float16* p, h2 (&o)[32]) {
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-    h2 n[4];
-    lds_h2x4(nv + 8 * m, n);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) sa2 = pk_fma(n[u], s[4 * m + u], sa2);
+    h2 q[4];
+    lds_h2x4(p + 8 * m, q);
+    o[4 * m] = q[0]; o[4 * m + 1] = q[1]; o[4 * m + 2] = q[2]; o[4 * m + 3] = q[3];
   }
-  const _Float16 sa = sa2.x + sa2.y;
+}
+
+// sa = S[row,:] . (-kk): even and odd key columns in two fp16 chains, then added
+__device__ __forceinline__ _Float16 f16_row_sa(const h2 (&s)[32], const h2 (&n)[32]) {
+  h2 sa2 = {(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+  for (int j = 0; j < 32; ++j) sa2 = pk_fma(n[j], s[j], sa2);
+  return sa2.x + sa2.y;
+}
+
+// The row update and readout given sa, on the token's r, wd, k, kk*a as half
+// pairs; vi = v[row].  Returns y[row].
+__device__ __forceinline__ _Float16 f16_row_update(h2 (&s)[32], _Float16 sa, const h2 (&r2)[32],
+                                                   const h2 (&w2)[32], const h2 (&k2)[32], const h2 (&b2)[32],
+                                                   _Float16 vi) {
   const h2 sab = {sa, sa};
   const h2 vv = {vi, vi};
   h2 y2 = {(_Float16)0.0f, (_Float16)0.0f};
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    h2 w4[4], k4[4], b4[4], r4[4];
-    lds_h2x4(wv + 8 * m, w4);
-    lds_h2x4(kv + 8 * m, k4);
-    lds_h2x4(bv + 8 * m, b4);
-    lds_h2x4(rv + 8 * m, r4);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      h2 x = s[4 * m + u];
-      x = pk_fma(x, w4[u], pk_fma(k4[u], vv, pk_fma(sab, b4[u], x)));
-      s[4 * m + u] = x;
-      y2 = pk_fma(x, r4[u], y2);
-    }
+  for (int j = 0; j < 32; ++j) {
+    h2 x = s[j];
+    x = pk_fma(x, w2[j], pk_fma(k2[j], vv, pk_fma(sab, b2[j], x)));
+    s[j] = x;
+    y2 = pk_fma(x, r2[j], y2);
   }
   return y2.x + y2.y;
 }
+
+// Pairs 4m .. 4m+3 of a token vector in LDS -> the same pairs of o (m is a
+// constant once the callers' loops are unrolled)
+__device__ __forceinline__ void lds_group(const _Float16* p, int m, h2 (&o)[32]) {
+  h2 q[4];
+  lds_h2x4(p + 8 * m, q);
+  o[4 * m] = q[0]; o[4 * m + 1] = q[1]; o[4 * m + 2] = q[2]; o[4 * m + 3] = q[3];
+}
+template <int M0, int M1>
+__device__ __forceinline__ void lds_pairs(const _Float16* p, h2 (&o)[32]) {
+#pragma unroll
+  for (int m = M0; m < M1; ++m) lds_group(p, m, o);
+}
+// The update operands b, k, wd of pairs 4*M0 .. 4*M1-1, group by group in the
+// order the update consumes them.  vec: a token's r; vector q at vec + q*stride.
+template <int M0, int M1>
+__device__ __forceinline__ void lds_bkw(const _Float16* vec, int stride, h2 (&b2)[32], h2 (&k2)[32],
+                                        h2 (&w2)[32]) {
+#pragma unroll
+  for (int m = M0; m < M1; ++m) {
+    lds_group(vec + 4 * stride, m, b2);
+    lds_group(vec + 2 * stride, m, k2);
+    lds_group(vec + 1 * stride, m, w2);
+  }
+}
+// pairs J0 .. J1-1 of the state update (no readout), written four pairs at a
+// stage so that no FMA directly follows the one it depends on
+template <int J0, int J1>
+__device__ __forceinline__ void f16_update_pairs(h2 (&s)[32], h2 sab, h2 vv, const h2 (&w2)[32],
+                                                 const h2 (&k2)[32], const h2 (&b2)[32]) {
+#pragma unroll
+  for (int j = J0; j < J1; j += 4) {
+    h2 u[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) u[q] = pk_fma(sab, b2[j + q], s[j + q]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) u[q] = pk_fma(k2[j + q], vv, u[q]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s[j + q] = pk_fma(s[j + q], w2[j + q], u[q]);
+  }
+}
+// Two independent fp16 chains over the updated row: this token's readout
+// y = S'.r and the next token's sa = S'.(-kk), interleaved step by step.
+__device__ __forceinline__ void f16_row_y_sa(const h2 (&s)[32], const h2 (&r2)[32], const h2 (&n)[32],
+                                             _Float16& y, _Float16& sa) {
+  h2 y2 = {(_Float16)0.0f, (_Float16)0.0f};
+  h2 sa2 = {(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    y2 = pk_fma(s[j], r2[j], y2);
+    sa2 = pk_fma(n[j], s[j], sa2);
+  }
+  y = y2.x + y2.y;
+  sa = sa2.x + sa2.y;
+}
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt left at their maxima)
+__device__ __forceinline__ void wait_lds_all() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // ---------------------------------------------------------------- decode
 // One token from raw projections, then the per-head GroupNorm, bonus and gate
@@ -165,9 +224,14 @@ __global__ __launch_bounds__(64) void wkv7_f16_decode_kernel(
   s_vec[4][i] = (_Float16)((float)kkh * af);
   __syncthreads();
 
-  h2 s[32];
+  h2 s[32], n[32], r2[32], w2[32], k2[32], b2[32];
   f16_row_get(s_st, i, s);
-  const _Float16 yh = f16_row_step(s, s_vec[0], s_vec[1], s_vec[2], s_vec[3], s_vec[4], vh);
+  lds_h2x32(s_vec[3], n);
+  lds_h2x32(s_vec[0], r2);
+  lds_h2x32(s_vec[1], w2);
+  lds_h2x32(s_vec[2], k2);
+  lds_h2x32(s_vec[4], b2);
+  const _Float16 yh = f16_row_update(s, f16_row_sa(s, n), r2, w2, k2, b2, vh);
   f16_row_put(s_st, i, s);
 
   const float y = (float)yh;
@@ -190,9 +254,10 @@ __global__ __launch_bounds__(64) void wkv7_f16_advance_kernel(int* __restrict__ 
 // T tokens of prepared vectors [B, T, H, 64] (w raw, + w0 when given; -kk and
 // kk*a precomputed) with the state resident in registers
 // (rwkv7_hf/native_wkv_fp16.py:338-436).  Slabs of F16_SLAB tokens are loaded
-// one slab ahead (lane l: vector q, token l/8, channels 8(l%8)..+7 — one
-// 16-byte load per vector), the slab's decay deltas are computed at staging,
-// and each token's output row is stored as it is produced.
+// two slabs ahead into registers (lane l: vector q, token l/8, channels
+// 8(l%8)..+7 — one 16-byte load per vector) and staged in LDS one slab ahead,
+// the slab's decay deltas are computed at staging, and each token's output
+// row is stored as it is produced.
 template <bool ADD_W0>
 __global__ __launch_bounds__(64) void wkv7_f16_sequence_kernel(
     const _Float16* __restrict__ r, const _Float16* __restrict__ w, const _Float16* __restrict__ w0,
@@ -256,21 +321,70 @@ __global__ __launch_bounds__(64) void wkv7_f16_sequence_kernel(
   h2 s[32];
   f16_row_get(s_st, lane, s);
   stage_slab(0, 0);
-  if (F16_SLAB < T) load_slab(F16_SLAB);
+  if (F16_SLAB < T) {
+    load_slab(F16_SLAB);
+    stage_slab(1, F16_SLAB);
+    if (2 * F16_SLAB < T) load_slab(2 * F16_SLAB);
+  }
+  __syncthreads();
 
+  // Token t lives in buffer (t / F16_SLAB) & 1, row t % F16_SLAB.  While slab
+  // S is processed, slab S + 1 is staged in the other buffer (and slab S + 2
+  // is in flight in registers).
+  //
+  // Per token the readout chain y(t) = S'(t).r(t) runs interleaved with the
+  // next token's chain sa(t+1) = S'(t).(-kk(t+1)): two independent chains
+  // keep the packed FMA pipeline busy where one would stall on every step.
+  // LDS reads are issued at fixed points (scheduling barriers) so that each
+  // consumer waits on at most 15 younger reads (the LDS wait counter's range):
+  //   [b,k,wd pairs 0-15 of t in registers]  read b,k,wd pairs 16-31
+  //   update pairs 0-15   | read r(t), -kk(t+1)
+  //   update pairs 16-31  | read b,k,wd pairs 0-15 and v of t+1
+  //   y(t) / sa(t+1) chains; store y(t)
+  constexpr int VSTRIDE = F16_SLAB * F16_N;  // halves between vectors of one buffer
+  h2 n[32], r2[32], w2[32], k2[32], b2[32];
+  _Float16 sa, vi;
+  lds_h2x32(s_slab[0][3][0], n);
+  wait_lds_all();
+  {
+    h2 sa2 = {(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+    for (int j = 0; j < 32; ++j) sa2 = pk_fma(n[j], s[j], sa2);
+    sa = sa2.x + sa2.y;
+  }
+  lds_bkw<0, 4>(&s_slab[0][0][0][0], VSTRIDE, b2, k2, w2);
+  vi = s_slab[0][5][0][lane];
   _Float16* orow = out + first + lane;
-  for (int t0 = 0, buf = 0; t0 < T; t0 += F16_SLAB, buf ^= 1) {
-    __syncthreads();  // slab t0 staged; slab t0 - F16_SLAB's buffer is free
-    if (t0 + F16_SLAB < T) {
-      stage_slab(buf ^ 1, t0 + F16_SLAB);
-      if (t0 + 2 * F16_SLAB < T) load_slab(t0 + 2 * F16_SLAB);
+  for (int t = 0; t < T; ++t) {
+    const int buf = (t / F16_SLAB) & 1;
+    const int tt = t % F16_SLAB;
+    if (tt == 0 && t > 0) {
+      if (t + F16_SLAB < T) {
+        stage_slab(buf ^ 1, t + F16_SLAB);
+        if (t + 2 * F16_SLAB < T) load_slab(t + 2 * F16_SLAB);
+      }
+      __syncthreads();
     }
-    const int nt = min(F16_SLAB, T - t0);
-    for (int tt = 0; tt < nt; ++tt) {
-      const _Float16 yh = f16_row_step(s, s_slab[buf][0][tt], s_slab[buf][1][tt], s_slab[buf][2][tt],
-                                       s_slab[buf][3][tt], s_slab[buf][4][tt], s_slab[buf][5][tt][lane]);
-      orow[(int64_t)(t0 + tt) * H * F16_N] = yh;
-    }
+    const _Float16* vec = &s_slab[buf][0][tt][0];
+    const int tn = min(t + 1, T - 1);
+    const _Float16* vnext = &s_slab[(tn / F16_SLAB) & 1][0][tn % F16_SLAB][0];
+    lds_bkw<4, 8>(vec, VSTRIDE, b2, k2, w2);
+    __builtin_amdgcn_sched_barrier(0);
+    const h2 sab = {sa, sa};
+    const h2 vv = {vi, vi};
+    f16_update_pairs<0, 16>(s, sab, vv, w2, k2, b2);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_pairs<0, 8>(vec, r2);
+    lds_pairs<0, 8>(vnext + 3 * VSTRIDE, n);
+    __builtin_amdgcn_sched_barrier(0);
+    f16_update_pairs<16, 32>(s, sab, vv, w2, k2, b2);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_bkw<0, 4>(vnext, VSTRIDE, b2, k2, w2);
+    vi = vnext[5 * VSTRIDE + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    _Float16 y;
+    f16_row_y_sa(s, r2, n, y, sa);
+    orow[(int64_t)t * H * F16_N] = y;
   }
 
   f16_row_put(s_st, lane, s);
