@@ -16,6 +16,7 @@ library GEMMs of dense (unquantised) projections (rocBLAS through torch).
 """
 from __future__ import annotations
 
+import os
 import weakref
 import zlib
 from dataclasses import dataclass
@@ -31,6 +32,8 @@ from .fused_lora import (ACT_NONE, ACT_SIGMOID, ACT_TANH, dense_multi, fused_lor
 from .fused_output import fused_attn_output_prepare
 from .fused_prefill import fused_prefill_state_prep
 from .fused_recurrent_update import fused_recurrent_output_prepare_raw
+from .native_wkv_fp16 import (native_fp16_recurrent_output_prepare_raw, native_fp16_recurrent_should_use,
+                              native_fp16_sequence)
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
 from .sampling import argmax_rows, argmax_workspace_bytes
 from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_prefill_multi_into,
@@ -313,7 +316,10 @@ class NativeRWKV7Cache(_HFCache):
     Holds ``(state, xpa, xpf, v_first)``: per-layer ``state[l] [B, H, N, N]``
     fp32 (value x key), per-layer token-shift rows ``xpa[l]``, ``xpf[l]``
     ``[B, D]`` and the cross-layer ``v_first [B, A]``, plus ``seen_tokens``.
-    Iterable as that 4-tuple.  Batch edits (select / reorder / repeat), device
+    Iterable as that 4-tuple.  An opt-in fp16 state (``zeros(...,
+    state_dtype=torch.float16)``) also carries ``fp16_elapsed`` (int32 ``[B]``,
+    the phase of the fp16 recurrence's decay dither), which follows the batch
+    edits but is not part of the legacy tuple.  Batch edits (select / reorder / repeat), device
     moves, detach, crop-to-empty and legacy-tuple conversion follow the
     reference.  A graph runner that replays the decode step binds the cache
     (its tensors become the runner's buffers); any edit that replaces the
@@ -326,6 +332,9 @@ class NativeRWKV7Cache(_HFCache):
     def __init__(self, state=None, xpa=None, xpf=None, v_first=None, seen_tokens: int = 0):
         # (the HF base initialiser builds KV layer objects a recurrent cache does not use)
         self._state, self._xpa, self._xpf, self._v_first = state, xpa, xpf, v_first
+        self._elapsed = None
+        if state is not None and len(state) and state[0].dtype == torch.float16:
+            self._elapsed = torch.zeros(int(state[0].shape[0]), device=state[0].device, dtype=torch.int32)
         self._seen_tokens = int(seen_tokens)
         self.layers = []
         self._rwkv7_cache_metrics = {k: 0 for k in _METRIC_KEYS}
@@ -334,13 +343,20 @@ class NativeRWKV7Cache(_HFCache):
         self._bound_version = None
 
     @classmethod
-    def zeros(cls, cfg: "NativeRWKV7Config", batch: int, device, dtype=torch.float16):
+    def zeros(cls, cfg: "NativeRWKV7Config", batch: int, device, dtype=torch.float16,
+              state_dtype=torch.float32):
         """A zero cache whose per-layer tensors are views of layer-major
-        storage ([L, B, H, N, N] fp32 state, [L, B, D] shift rows): each layer
+        storage ([L, B, H, N, N] state, [L, B, D] shift rows): each layer
         is contiguous and the layers are equally spaced, so one slot-copy
-        launch can move a batch row of every layer."""
+        launch can move a batch row of every layer.  ``state_dtype`` is fp32,
+        or fp16 for the opt-in fp16-state lane (fp16 activations, head size 64)."""
         H, N, D, A, L = cfg.num_heads, cfg.head_dim, cfg.hidden_size, cfg.attention_hidden_size, cfg.num_hidden_layers
-        S = torch.zeros(L, batch, H, N, N, device=device, dtype=torch.float32)
+        if state_dtype not in (torch.float32, torch.float16):
+            raise ValueError(f"state_dtype must be float32 or float16; got {state_dtype}")
+        if state_dtype == torch.float16 and not native_fp16_recurrent_should_use(
+                state_dtype=state_dtype, input_dtype=dtype, head_dim=N):
+            raise ValueError("an fp16 recurrent state needs fp16 activations and head size 64")
+        S = torch.zeros(L, batch, H, N, N, device=device, dtype=state_dtype)
         xa = torch.zeros(L, batch, D, device=device, dtype=dtype)
         xf = torch.zeros(L, batch, D, device=device, dtype=dtype)
         return cls(list(S.unbind(0)), list(xa.unbind(0)), list(xf.unbind(0)),
@@ -377,6 +393,24 @@ class NativeRWKV7Cache(_HFCache):
 
     def __iter__(self):
         return iter((self._state, self._xpa, self._xpf, self._v_first))
+
+    @property
+    def fp16_elapsed(self) -> torch.Tensor | None:
+        """int32 [B] phase of the fp16-state lane (None for an fp32 state)."""
+        return self._elapsed
+
+    @property
+    def state_dtype(self) -> torch.dtype | None:
+        return None if not self._state else self._state[0].dtype
+
+    def _all_tensors(self) -> list:
+        """Every tensor of the cache in a fixed order (fp16_elapsed last, when present)."""
+        out = [*(self._state or ()), *(self._xpa or ()), *(self._xpf or ())]
+        if self._v_first is not None:
+            out.append(self._v_first)
+        if self._elapsed is not None:
+            out.append(self._elapsed)
+        return out
 
     def __len__(self) -> int:
         return 4
@@ -486,10 +520,12 @@ class NativeRWKV7Cache(_HFCache):
         self._xpa = None if self._xpa is None else [fn(t) for t in self._xpa]
         self._xpf = None if self._xpf is None else [fn(t) for t in self._xpf]
         self._v_first = None if self._v_first is None else fn(self._v_first)
+        self._elapsed = None if self._elapsed is None else fn(self._elapsed)
 
     def clone(self) -> "NativeRWKV7Cache":
         out = type(self)(seen_tokens=self._seen_tokens)
         out._state, out._xpa, out._xpf, out._v_first = self._state, self._xpa, self._xpf, self._v_first
+        out._elapsed = self._elapsed
         out._map(lambda t: t.clone())
         out._rwkv7_cache_metrics = dict(self._rwkv7_cache_metrics)
         out._rwkv7_cache_metrics["clones"] += 1
@@ -498,16 +534,14 @@ class NativeRWKV7Cache(_HFCache):
     def reset(self) -> None:
         """Drop the state (the reference's reset: the next forward starts fresh)."""
         self._invalidate_native_graph_binding()
-        self._state = self._xpa = self._xpf = self._v_first = None
+        self._state = self._xpa = self._xpf = self._v_first = self._elapsed = None
         self._seen_tokens = 0
         self._rwkv7_cache_metrics["resets"] += 1
 
     def zero_(self) -> "NativeRWKV7Cache":
         """Zero the state in place, keeping the tensors (and any graph binding)."""
-        for t in (*(self._state or ()), *(self._xpa or ()), *(self._xpf or ())):
+        for t in self._all_tensors():
             t.zero_()
-        if self._v_first is not None:
-            self._v_first.zero_()
         self._seen_tokens = 0
         return self
 
@@ -521,7 +555,7 @@ class NativeRWKV7Cache(_HFCache):
     def to(self, device=None, dtype=None, *, non_blocking: bool = False, copy: bool = False,
            inplace: bool = True) -> "NativeRWKV7Cache":
         """Move the cache; ``dtype`` applies to the token-shift rows and
-        ``v_first`` (the recurrent state stays fp32, as the kernels require)."""
+        ``v_first`` (the recurrent state keeps its dtype, as the kernels require)."""
         target = self if inplace else self.clone()
         target._invalidate_native_graph_binding()
 
@@ -540,6 +574,7 @@ class NativeRWKV7Cache(_HFCache):
         target._xpa = None if target._xpa is None else [move(t) for t in target._xpa]
         target._xpf = None if target._xpf is None else [move(t) for t in target._xpf]
         target._v_first = None if target._v_first is None else move(target._v_first)
+        target._elapsed = None if target._elapsed is None else move(target._elapsed)
         target._rwkv7_cache_metrics["device_moves"] += 1
         return target
 
@@ -549,6 +584,7 @@ class NativeRWKV7Cache(_HFCache):
             target = self
         else:
             target = type(self)(self._state, self._xpa, self._xpf, self._v_first, seen_tokens=self._seen_tokens)
+            target._elapsed = self._elapsed
             target._rwkv7_cache_metrics = dict(self._rwkv7_cache_metrics)
         runner = target._native_graph_bound_runner() if inplace else None
         if runner is not None and target.get_batch_size() == int(idx.numel()) and runner.reorder_batch_inplace(idx):
@@ -702,6 +738,27 @@ def _slice_logits(logits: torch.Tensor, keep):
 
 
 # ------------------------------------------------------------------ model
+def _env_on(name: str) -> bool:
+    return os.environ.get(name, "0").strip().lower() in {"1", "true", "yes", "on"}
+
+
+def native_graph_state_dtype(model_dtype: torch.dtype) -> torch.dtype:
+    """Recurrent-state dtype of new caches from the reference's switches
+    (rwkv7_hf/native_graph_runtime.py:119-147, :312-316):
+    RWKV7_NATIVE_GRAPH_STATE_DTYPE = fp32 (default) or fp16; fp16 applies to
+    fp16 models only and needs RWKV7_NATIVE_GRAPH_FP16_RECURRENT=1."""
+    raw = os.environ.get("RWKV7_NATIVE_GRAPH_STATE_DTYPE", "fp32").strip().lower()
+    if raw in {"fp32", "float32"}:
+        return torch.float32
+    if raw in {"fp16", "float16", "half"}:
+        if model_dtype != torch.float16:
+            return torch.float32
+        if not _env_on("RWKV7_NATIVE_GRAPH_FP16_RECURRENT"):
+            raise RuntimeError("FP16 native graph state requires RWKV7_NATIVE_GRAPH_FP16_RECURRENT=1")
+        return torch.float16
+    raise ValueError(f"RWKV7_NATIVE_GRAPH_STATE_DTYPE must be fp32 or fp16; got {raw!r}")
+
+
 class _Layer:
     pass
 
@@ -758,6 +815,10 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
         # up to 64 rows (without the LN-mix prologue): the LoRA down projections
         # run as tail workgroups of the R/K/V launch instead of a launch of their own
         self.rkv_lora_tail = True
+        # recurrent-state dtype of the caches this model creates: fp32, or fp16
+        # for the opt-in fp16-state lane (a cache's own state dtype picks the
+        # route, so either kind of cache runs on either setting)
+        self.state_dtype = native_graph_state_dtype(dtype)
         self._replaced = 0
         self.layers = []
 
@@ -929,7 +990,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
         return cls(config, _LazyWeights(config, seed, device, dtype), device=device, dtype=dtype)
 
     def new_cache(self, batch: int) -> NativeRWKV7Cache:
-        return NativeRWKV7Cache.zeros(self.config, batch, self.device, self.dtype)
+        return NativeRWKV7Cache.zeros(self.config, batch, self.device, self.dtype, state_dtype=self.state_dtype)
 
     def reserve_workspace(self, rows: int) -> None:
         """Grow the per-device scratch slots for ``rows``-row decode steps (before capture)."""
@@ -1018,6 +1079,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
             "lora": torch.empty(4, B, A, device=dev, dtype=dt),
             "mids": [torch.empty(B, r, device=dev, dtype=dt) for r in ranks],
             "prep": torch.empty(B, A, device=dev, dtype=dt),
+            "vtmp": torch.empty(B, A, device=dev, dtype=dt),
             "fk": torch.empty(B, D, device=dev, dtype=dt),
             "kf": torch.empty(B, cfg.intermediate_size, device=dev, dtype=dt),
             "h": torch.empty(B, D, device=dev, dtype=dt),
@@ -1081,16 +1143,18 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
         B = int(tokens.shape[0])
         if bufs is None:
             bufs = self._decode_buffers(B)
-        if self._mix_lora_route(B):
+        state, xpa, xpf, v_first = cache
+        # an fp16 state takes the unfused route into the fp16-state kernel
+        f16 = state[0].dtype == torch.float16
+        if self._mix_lora_route(B) and not f16:
             return self._decode_mix_lora_(tokens, cache, logits, bufs)
         x = bufs["x"]
         torch.index_select(self.emb, 0, tokens, out=x)
-        state, xpa, xpf, v_first = cache
         H, N, eps = cfg.num_heads, cfg.head_dim, cfg.norm_eps
         mixb, rkv, lora, prep = bufs["mix"], bufs["rkv"], bufs["lora"], bufs["prep"]
         main = torch.cuda.current_stream(x.device)
         side, ev_in, ev_out = self._side(x.device) if self.lora_side_stream else (None, None, None)
-        fmix = self._mix_fusable(B) and not self.lora_side_stream
+        fmix = self._mix_fusable(B) and not self.lora_side_stream and not f16
         parts = None  # the previous layer's FFN value partials, not yet added to x
         for L in self.layers:
             i = L.idx
@@ -1114,7 +1178,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                                             pre_norm_weight=L.pre[0] if L.pre else None,
                                             pre_norm_bias=L.pre[1] if L.pre else None, residual_parts=parts)
                 parts = None
-            if (self.fused_lora_decode and not self.lora_side_stream
+            if (self.fused_lora_decode and not self.lora_side_stream and not f16
                     and fused_lora_decode_supported([int(d.shape[0]) for d in L.lora_down], B)):
                 # LoRA down (its own split-K launch, or tail workgroups of the
                 # R/K/V launch), then the up projections inside the wkv kernel
@@ -1148,10 +1212,14 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                         QuantLinear.apply_group((L.r_proj, L.k_proj, L.v_proj), (xr, xk, xv),
                                                 (rkv[0], rkv[1], rkv[2]))
                     self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
-                fused_recurrent_output_prepare_raw(
-                    rkv[0], lora[0], rkv[1], rkv[2], lora[1], state[i], lora[2], L.k_k, L.k_a, L.r_k, L.gn[0],
-                    L.gn[1], eps=N * 1e-5, state_out=state[i], out=prep.view(B, H, N),
-                    v_first=v_first, v_gate=lora[3] if i > 0 else None, v_mode=1 if i == 0 else 2)
+                if f16:
+                    self._fp16_recurrence(L, rkv, lora, state[i], v_first, prep, cache.fp16_elapsed, bufs["vtmp"],
+                                          last=i == len(self.layers) - 1)
+                else:
+                    fused_recurrent_output_prepare_raw(
+                        rkv[0], lora[0], rkv[1], rkv[2], lora[1], state[i], lora[2], L.k_k, L.k_a, L.r_k, L.gn[0],
+                        L.gn[1], eps=N * 1e-5, state_out=state[i], out=prep.view(B, H, N),
+                        v_first=v_first, v_gate=lora[3] if i > 0 else None, v_mode=1 if i == 0 else 2)
             L.o_proj.apply(prep, x, residual=x)
             if fmix:
                 mm8_lnmix_multi_into(x, xpf[i], L.ln2[0], L.ln2[1], eps, [L.fx_k], [L.key.m], [bufs["kf"]],
@@ -1171,6 +1239,27 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
         layer_norm(x, self.norm[0], self.norm[1], eps, out=bufs["h"])
         self.lm_head.apply(bufs["h"], logits)
         return logits
+
+    def _fp16_recurrence(self, L, rkv, lora, state_l, v_first, prep, elapsed, vtmp, *, last: bool) -> None:
+        """One decode layer's recurrence on an fp16 state: the V interpolation in
+        the reference's fp16 torch form, v = v + (v_first - v) * v_gate
+        (rwkv7_hf/native_jit_decode.py:762-766), then the fp16-state kernel on
+        the raw projections, which advances elapsed on the last layer
+        (native_jit_decode.py:767-784)."""
+        cfg = self.config
+        H, N = cfg.num_heads, cfg.head_dim
+        B = int(rkv.shape[1])
+        v = rkv[2]
+        if L.idx == 0:
+            v_first.copy_(v)
+        else:
+            torch.sub(v_first, v, out=vtmp)
+            vtmp.mul_(lora[3])
+            v.add_(vtmp)
+        bhn = lambda t: t.view(B, H, N)
+        native_fp16_recurrent_output_prepare_raw(
+            bhn(rkv[0]), bhn(lora[0]), bhn(rkv[1]), bhn(v), bhn(lora[1]), state_l, bhn(lora[2]), L.k_k, L.k_a,
+            L.r_k, L.gn[0], L.gn[1], elapsed, advance_elapsed=last, eps=N * 1e-5, out=bhn(prep))
 
     def _value_deferrable(self, L, B) -> bool:
         """The FFN value's split reduce can move into the next layer's norm-mix
@@ -1268,6 +1357,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
             x = torch.nn.functional.embedding(input_ids.reshape(-1), self.emb).reshape(B, T, D).contiguous()
         R = B * T
         state, xpa, xpf, v_first = cache
+        f16 = state[0].dtype == torch.float16
         mixb = torch.empty(6, B, T, D, device=dev, dtype=dt)
         rkv = torch.empty(3, R, A, device=dev, dtype=dt)
         lora = torch.empty(4, R, A, device=dev, dtype=dt)
@@ -1290,8 +1380,16 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                 v_gate=lora[3] if i > 0 else None, num_heads=H, head_dim=N, w_transform="log_decay",
                 v_mode=1 if i == 0 else 2, v_out=rkv[2])
             shp = (B, T, H, N)
-            y, _ = _run_chunk(rkv[0].view(shp), w_log.view(shp), k_adj.view(shp), v_int.view(shp), kk.view(shp),
-                              lora[1].view(shp), state[i], w_is_log=1, chunk=16, state_out=state[i])
+            if f16:
+                # the fp16-state sequence recurrence on raw w (w0 already added),
+                # -kk and kk*a as the reference forms them (native_jit_prefill.py:792-804)
+                kk4 = kk.view(shp)
+                y = native_fp16_sequence(rkv[0].view(shp), lora[0].view(shp), k_adj.view(shp), v_int.view(shp),
+                                         torch.neg(kk4), kk4 * lora[1].view(shp), state[i], cache.fp16_elapsed)
+            else:
+                y, _ = _run_chunk(rkv[0].view(shp), w_log.view(shp), k_adj.view(shp), v_int.view(shp),
+                                  kk.view(shp), lora[1].view(shp), state[i], w_is_log=1, chunk=16,
+                                  state_out=state[i])
             prep = fused_attn_output_prepare(y.view(R, A), rkv[0], k_adj, v_int, lora[2], L.r_k, L.gn[0], L.gn[1],
                                              num_heads=H, head_dim=N, head_v_dim=N, eps=N * 1e-5)
             x2 = x.reshape(R, D)
@@ -1302,6 +1400,8 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
             L.key.apply(fk.reshape(R, D), kf, act=3)
             L.value.apply(kf, x2, residual=x2)
         v_first.copy_(vfirst_seq.view(B, T, A)[:, -1])
+        if f16:
+            cache.fp16_elapsed.add_(T)  # the dither phase moves on by the prompt's tokens
         keep = T if logits_to_keep is None or int(logits_to_keep) <= 0 else min(int(logits_to_keep), T)
         h = layer_norm(x[:, T - keep:].reshape(B * keep, D).contiguous(), self.norm[0], self.norm[1], eps)
         logits = torch.empty(B * keep, cfg.vocab_size, device=dev, dtype=dt)
@@ -1601,9 +1701,10 @@ class NativeGraphRunner:
         argmax_rows(self.logits, out=self.next_tokens, out2=self.tokens, workspace=self.argmax_ws)
 
     def _copy_into(self, cache: NativeRWKV7Cache) -> None:
-        s, a, f, v = self.cache
-        s2, a2, f2, v2 = cache
-        for dst, src in zip((*s, *a, *f, v), (*s2, *a2, *f2, v2)):
+        if cache.state_dtype not in (None, self.cache.state_dtype):
+            raise ValueError(f"graph runner with a {self.cache.state_dtype} state got a cache with a "
+                             f"{cache.state_dtype} state")
+        for dst, src in zip(self.cache._all_tensors(), cache._all_tensors()):
             dst.copy_(src)
 
     def detach_bound_cache(self, keep: NativeRWKV7Cache | None = None) -> None:
@@ -1623,6 +1724,7 @@ class NativeGraphRunner:
         prev._xpa = list(torch.stack(a).unbind(0))
         prev._xpf = list(torch.stack(f).unbind(0))
         prev._v_first = v.clone()
+        prev._elapsed = None if self.cache._elapsed is None else self.cache._elapsed.clone()
         prev._invalidate_native_graph_binding()
 
     def bind_cache(self, cache: NativeRWKV7Cache) -> None:
@@ -1631,6 +1733,7 @@ class NativeGraphRunner:
         self.detach_bound_cache(keep=cache)
         cache._state, cache._xpa, cache._xpf, cache._v_first = (
             list(self.cache._state), list(self.cache._xpa), list(self.cache._xpf), self.cache._v_first)
+        cache._elapsed = self.cache._elapsed
         cache._invalidate_native_graph_binding()
         cache._bind_native_graph_runner(self)
         self._bound_cache_ref = weakref.ref(cache)
@@ -1640,8 +1743,7 @@ class NativeGraphRunner:
         idx = indices.to(device=self.model.device, dtype=torch.long)
         if int(idx.numel()) != self.batch:
             return False
-        s, a, f, v = self.cache
-        for t in (*s, *a, *f, v):
+        for t in self.cache._all_tensors():
             t.copy_(t.index_select(0, idx))
         return True
 
@@ -1715,8 +1817,7 @@ class NativePrefillGraphRunner:
         self.replays = 0
 
     def _zero_state(self) -> None:
-        s, a, f, v = self.cache
-        for t in (*s, *a, *f, v):
+        for t in self.cache._all_tensors():
             t.zero_()
 
     def matches(self, batch: int, tokens: int, logits_to_keep: int, carry_state: bool) -> bool:
@@ -1732,9 +1833,9 @@ class NativePrefillGraphRunner:
         if self.carry_state and initial_cache is not None and initial_cache.is_initialized:
             if initial_cache.get_batch_size() != self.batch:
                 raise ValueError("initial cache batch differs from the captured batch")
-            s, a, f, v = self.cache
-            s2, a2, f2, v2 = initial_cache
-            for dst, src in zip((*s, *a, *f, v), (*s2, *a2, *f2, v2)):
+            if initial_cache.state_dtype != self.cache.state_dtype:
+                raise ValueError("initial cache state dtype differs from the captured one")
+            for dst, src in zip(self.cache._all_tensors(), initial_cache._all_tensors()):
                 dst.copy_(src)
             seen = initial_cache.seen_tokens
         else:
@@ -1746,11 +1847,10 @@ class NativePrefillGraphRunner:
         if not copy:
             out = NativeRWKV7Cache(list(self.cache._state), list(self.cache._xpa), list(self.cache._xpf),
                                    self.cache._v_first, seen + self.tokens_n)
+            out._elapsed = self.cache._elapsed
             return self.logits, out
         out = self.model.new_cache(self.batch)
-        s, a, f, v = out
-        s2, a2, f2, v2 = self.cache
-        for dst, src in zip((*s, *a, *f, v), (*s2, *a2, *f2, v2)):
+        for dst, src in zip(out._all_tensors(), self.cache._all_tensors()):
             dst.copy_(src)
         out.seen_tokens = seen + self.tokens_n
         return self.logits.clone(), out

@@ -59,11 +59,14 @@ def _require_library(what: str) -> None:
 def native_fp16_recurrent_output_prepare_raw(
     r: Any, w_raw: Any, k_raw: Any, v: Any, a: Any, state: Any, g: Any, k_k: Any, k_a: Any, r_k: Any,
     norm_weight: Any, norm_bias: Any, elapsed: Any, *, advance_elapsed: bool, eps: float,
+    out: Any | None = None,
 ) -> Any:
     """One decode token on an fp16 state (updated in place); returns ``out`` shaped like ``r``.
 
     ``elapsed`` (int32 ``[B]``) feeds the decay dither's phase and moves by one
-    when ``advance_elapsed`` is set.
+    when ``advance_elapsed`` is set.  ``out`` (an extension: a contiguous fp16
+    tensor with ``r``'s element count) receives the result instead of a new
+    tensor, for callers that must not allocate (a captured decode graph).
     """
     if state.dim() != 4:
         raise ValueError("state must be [B,H,64,64]")
@@ -89,7 +92,11 @@ def native_fp16_recurrent_output_prepare_raw(
             raise ValueError("per-channel tensor shape mismatch")
     if int(elapsed.numel()) != B:
         raise ValueError("elapsed must be contiguous CUDA int32 [B]")
-    out = torch.empty_like(r)
+    if out is None:
+        out = torch.empty_like(r)
+    elif not (out.is_cuda and out.dtype == torch.float16 and out.is_contiguous()
+              and int(out.numel()) == int(r.numel())):
+        raise ValueError("out must be a contiguous CUDA fp16 tensor with r's element count")
     _lib.call(
         "rwkv7mi_wkv7_fp16_decode_output_prepare_raw",
         _lib.ptr(r), _lib.ptr(w_raw), _lib.ptr(k_raw), _lib.ptr(v), _lib.ptr(a), _lib.ptr(state), _lib.ptr(g),

@@ -193,6 +193,9 @@ class RWKV7StatePool:
 
     # ------------------------------------------------------------ whole batches
     def _batch_copy(self, cache, rows, *, to_cache: bool, active=None) -> None:
+        if cache._state and cache._state[0].dtype != self.state.dtype:
+            raise ValueError(f"the state pool holds {self.state.dtype} states; got a cache with a "
+                             f"{cache._state[0].dtype} state")
         n = len(rows)
         idx = self._idx(rows)
         act = None if active is None else torch.as_tensor(active, dtype=torch.uint8).to(self.device)

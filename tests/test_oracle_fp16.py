@@ -247,3 +247,43 @@ def test_fp16_operators_reject_host_tensors():
     with pytest.raises(ValueError, match="unsupported dtype or shape"):
         native_fp16_recurrent_output_prepare_raw(v, v, v, v, v, st.float(), v, p, p, p, p, p,
                                                  torch.zeros(1, dtype=torch.int32), advance_elapsed=True, eps=1e-5)
+
+
+def test_state_dtype_switches_follow_the_reference(monkeypatch):
+    """RWKV7_NATIVE_GRAPH_STATE_DTYPE / RWKV7_NATIVE_GRAPH_FP16_RECURRENT as the
+    reference reads them (rwkv7_hf/native_graph_runtime.py:119-147, :312-316)."""
+    from rwkv7mi.model import native_graph_state_dtype
+
+    monkeypatch.delenv("RWKV7_NATIVE_GRAPH_STATE_DTYPE", raising=False)
+    monkeypatch.delenv("RWKV7_NATIVE_GRAPH_FP16_RECURRENT", raising=False)
+    assert native_graph_state_dtype(torch.float16) == torch.float32
+    monkeypatch.setenv("RWKV7_NATIVE_GRAPH_STATE_DTYPE", "fp16")
+    with pytest.raises(RuntimeError, match="RWKV7_NATIVE_GRAPH_FP16_RECURRENT"):
+        native_graph_state_dtype(torch.float16)
+    assert native_graph_state_dtype(torch.float32) == torch.float32  # fp16 state only for fp16 models
+    monkeypatch.setenv("RWKV7_NATIVE_GRAPH_FP16_RECURRENT", "1")
+    assert native_graph_state_dtype(torch.float16) == torch.float16
+    monkeypatch.setenv("RWKV7_NATIVE_GRAPH_STATE_DTYPE", "bf16")
+    with pytest.raises(ValueError):
+        native_graph_state_dtype(torch.float16)
+
+
+def test_fp16_state_cache_carries_elapsed_through_batch_edits():
+    from rwkv7mi.model import NativeRWKV7Cache, NativeRWKV7Config
+
+    cfg = NativeRWKV7Config(vocab_size=64, hidden_size=128, num_hidden_layers=2, intermediate_size=256)
+    c = NativeRWKV7Cache.zeros(cfg, 3, "cpu", torch.float16, state_dtype=torch.float16)
+    assert c.state_dtype == torch.float16 and c.fp16_elapsed.dtype == torch.int32
+    c.fp16_elapsed.copy_(torch.tensor([5, 6, 7], dtype=torch.int32))
+    c.select_batch([2, 0])
+    assert c.fp16_elapsed.tolist() == [7, 5]
+    c.batch_repeat_interleave(2)
+    assert c.fp16_elapsed.tolist() == [7, 7, 5, 5]
+    d = c.clone()
+    d.fp16_elapsed.add_(1)
+    assert c.fp16_elapsed.tolist() == [7, 7, 5, 5]
+    c.zero_()
+    assert c.fp16_elapsed.tolist() == [0, 0, 0, 0]
+    assert NativeRWKV7Cache.zeros(cfg, 2, "cpu", torch.float16).fp16_elapsed is None
+    with pytest.raises(ValueError, match="fp16 activations"):
+        NativeRWKV7Cache.zeros(cfg, 2, "cpu", torch.float32, state_dtype=torch.float16)
