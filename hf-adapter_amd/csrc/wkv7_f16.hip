@@ -22,6 +22,13 @@
 // are staged in LDS and read back as broadcasts.
 #include "common.h"
 
+// No implicit fusing in this file: every fp32 expression that ends in an fp16
+// value (decay delta, k, kk*a, the V interpolation) is rounded to fp32 first
+// and then to fp16, as the reference computes it; a multiply-add fused into a
+// mixed-precision FMA with an fp16 result would round once instead.  The
+// state's FMAs are explicit.
+#pragma clang fp contract(off)
+
 namespace rwkv7mi {
 
 constexpr int F16_N = 64;
@@ -38,6 +45,15 @@ __device__ __forceinline__ h2 h2_bits(uint32_t u) { return __builtin_bit_cast(h2
 __device__ __forceinline__ uint32_t h2_u32(h2 x) { return __builtin_bit_cast(uint32_t, x); }
 __device__ __forceinline__ _Float16 h_bits(unsigned short u) { return __builtin_bit_cast(_Float16, u); }
 
+// fp32 -> fp16, round to nearest even, of the fp32 value itself: the empty asm
+// pins x as an fp32 register so that the conversion is not folded into the
+// instruction producing x (a mixed-precision FMA with an fp16 result would
+// round the exact value once instead of the fp32 value)
+__device__ __forceinline__ _Float16 f16_rn(float x) {
+  asm volatile("" : "+v"(x));
+  return (_Float16)x;
+}
+
 // 2^-41 * int32(0x9E3779B9 * phase)
 __device__ __forceinline__ float f16_dither(uint32_t phase) {
   return 0x1p-41f * (float)(int32_t)(0x9E3779B9u * phase);
@@ -48,7 +64,7 @@ __device__ __forceinline__ float f16_dither(uint32_t phase) {
 __device__ __forceinline__ _Float16 f16_decay_delta(float wv, uint32_t phase) {
   const float t = __builtin_amdgcn_exp2f(-F16_LOG2E * wv);
   const float e = __builtin_amdgcn_exp2f(-F16_DECAY_LOG2 * __builtin_amdgcn_rcpf(1.0f + t));
-  return (_Float16)(e - 1.0f + f16_dither(phase));
+  return f16_rn(e - 1.0f + f16_dither(phase));
 }
 
 // 16-byte LDS row read -> 4 half pairs
@@ -189,12 +205,17 @@ __device__ __forceinline__ void wait_lds_all() { __builtin_amdgcn_s_waitcnt(0xC0
 // in fp32 (rwkv7_hf/native_wkv_fp16.py:200-336):
 //   kk = fp16(normalize(k_raw * k_k)),  k = fp16(k_raw * (1 + (a - 1) k_a)),
 //   b = fp16(kk * a),  out = (GN(y) * gn_w + gn_b + (sum r k r_k) v) * g.
+// v_mode (an extension of this build): 1 copies v into v_first (layer 0);
+// 2 first forms v + (v_first - v) * v_gate with an fp16 rounding after each
+// operation, the values the reference's fp16 torch form gives
+// (rwkv7_hf/native_jit_decode.py:762-766).
 __global__ __launch_bounds__(64) void wkv7_f16_decode_kernel(
     const _Float16* __restrict__ r, const _Float16* __restrict__ w_raw, const _Float16* __restrict__ k_raw,
     const _Float16* __restrict__ v, const _Float16* __restrict__ a, _Float16* __restrict__ state,
     const _Float16* __restrict__ g, const _Float16* __restrict__ k_k, const _Float16* __restrict__ k_a,
     const _Float16* __restrict__ r_k, const _Float16* __restrict__ gn_w, const _Float16* __restrict__ gn_b,
-    const int* __restrict__ elapsed, _Float16* __restrict__ out, int H, float eps) {
+    const int* __restrict__ elapsed, _Float16* __restrict__ out, _Float16* __restrict__ v_first,
+    const _Float16* __restrict__ v_gate, int v_mode, int H, float eps) {
   __shared__ __align__(16) _Float16 s_st[F16_N * F16_RS];
   __shared__ __align__(16) _Float16 s_vec[5][F16_N];  // r, wd, k, -kk, kk*a
 
@@ -207,7 +228,16 @@ __global__ __launch_bounds__(64) void wkv7_f16_decode_kernel(
   _Float16* sg = state + (int64_t)bh * F16_N * F16_N;
 
   f16_state_in(sg, s_st, i);
-  const _Float16 rh = r[e], vh = v[e];
+  const _Float16 rh = r[e];
+  _Float16 vh = v[e];
+  if (v_mode == 1) {
+    v_first[e] = vh;
+  } else if (v_mode == 2) {
+    // three roundings, as three fp16 tensor operations give
+    const _Float16 d = f16_rn((float)v_first[e] - (float)vh);
+    const _Float16 m = f16_rn((float)d * (float)v_gate[e]);
+    vh = f16_rn((float)vh + (float)m);
+  }
   const float kr = (float)k_raw[e], af = (float)a[e], wr = (float)w_raw[e], gf = (float)g[e];
   const float kkw = (float)k_k[pc], kaw = (float)k_a[pc], rkw = (float)r_k[pc];
   const float gw = (float)gn_w[pc], gb = (float)gn_b[pc];
@@ -215,13 +245,13 @@ __global__ __launch_bounds__(64) void wkv7_f16_decode_kernel(
 
   const float kku = kr * kkw;
   const float kkv = kku / fmaxf(sqrtf(wave_sum(kku * kku)), 1.0e-12f);
-  const _Float16 kh = (_Float16)(kr * fmaf(af, kaw, 1.0f - kaw));
-  const _Float16 kkh = (_Float16)kkv;
+  const _Float16 kh = f16_rn(kr * fmaf(af, kaw, 1.0f - kaw));
+  const _Float16 kkh = f16_rn(kkv);
   s_vec[0][i] = rh;
   s_vec[1][i] = f16_decay_delta(wr, phase);
   s_vec[2][i] = kh;
   s_vec[3][i] = -kkh;
-  s_vec[4][i] = (_Float16)((float)kkh * af);
+  s_vec[4][i] = f16_rn((float)kkh * af);
   __syncthreads();
 
   h2 s[32], n[32], r2[32], w2[32], k2[32], b2[32];
@@ -239,7 +269,7 @@ __global__ __launch_bounds__(64) void wkv7_f16_decode_kernel(
   const float cen = y - mean;
   const float var = wave_sum(cen * cen) * (1.0f / F16_N);
   const float corr = wave_sum((float)rh * (float)kh * rkw);
-  out[e] = (_Float16)((cen * rsqrtf(var + eps) * gw + gb + corr * (float)vh) * gf);
+  out[e] = f16_rn((cen * rsqrtf(var + eps) * gw + gb + corr * (float)vh) * gf);
 
   __syncthreads();
   f16_state_out(sg, s_st, i);
@@ -403,8 +433,8 @@ bool f16_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15)
 extern "C" int rwkv7mi_wkv7_fp16_decode_output_prepare_raw(
     const void* r, const void* w_raw, const void* k_raw, const void* v, const void* a, void* state,
     const void* g, const void* k_k, const void* k_a, const void* r_k, const void* gn_w, const void* gn_b,
-    int32_t* elapsed, int advance_elapsed, void* out, int64_t B, int64_t H, int64_t N, float eps,
-    void* stream) {
+    int32_t* elapsed, int advance_elapsed, void* out, void* v_first, const void* v_gate, int v_mode, int64_t B,
+    int64_t H, int64_t N, float eps, void* stream) {
   if (N != F16_N) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode: head size must be 64");
   if (B < 0 || H <= 0) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode: bad B/H");
   if (B == 0) return RWKV7MI_OK;
@@ -413,12 +443,15 @@ extern "C" int rwkv7mi_wkv7_fp16_decode_output_prepare_raw(
       !elapsed || !out)
     return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode: null pointer");
   if (!f16_aligned16(state)) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode: state must be 16-byte aligned");
+  if (v_mode < 0 || v_mode > 2) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode: v_mode must be 0, 1 or 2");
+  if ((v_mode >= 1 && !v_first) || (v_mode == 2 && !v_gate))
+    return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode: v_mode 1 needs v_first, 2 needs v_first and v_gate");
   hipStream_t st = as_stream(stream);
   hipLaunchKernelGGL(wkv7_f16_decode_kernel, dim3((unsigned)(B * H)), dim3(64), 0, st, (const _Float16*)r,
                      (const _Float16*)w_raw, (const _Float16*)k_raw, (const _Float16*)v, (const _Float16*)a,
                      (_Float16*)state, (const _Float16*)g, (const _Float16*)k_k, (const _Float16*)k_a,
                      (const _Float16*)r_k, (const _Float16*)gn_w, (const _Float16*)gn_b, (const int*)elapsed,
-                     (_Float16*)out, (int)H, eps);
+                     (_Float16*)out, (_Float16*)v_first, (const _Float16*)v_gate, v_mode, (int)H, eps);
   int rc = check_launch("wkv7_f16_decode_kernel");
   if (rc != RWKV7MI_OK || !advance_elapsed) return rc;
   // Every head of the step reads elapsed[b] before it moves: the increment is

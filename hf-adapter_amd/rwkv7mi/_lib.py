@@ -48,7 +48,7 @@ SIGNATURES = {
     "rwkv7mi_wkv7_chunk_status": (_i32, [_i32, ctypes.POINTER(_i32)]),
     "rwkv7mi_wkv7_fp16_decode_output_prepare_raw": (
         _i32,
-        [_c_p] * 12 + [_c_p, _i32, _c_p, _i64, _i64, _i64, _f32, _c_p],
+        [_c_p] * 12 + [_c_p, _i32, _c_p, _c_p, _c_p, _i32, _i64, _i64, _i64, _f32, _c_p],
     ),
     "rwkv7mi_wkv7_fp16_sequence": (_i32, [_c_p] * 10 + [_i64, _i64, _i64, _i64, _c_p]),
     "rwkv7mi_mm8_pack": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),

@@ -1079,7 +1079,6 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
             "lora": torch.empty(4, B, A, device=dev, dtype=dt),
             "mids": [torch.empty(B, r, device=dev, dtype=dt) for r in ranks],
             "prep": torch.empty(B, A, device=dev, dtype=dt),
-            "vtmp": torch.empty(B, A, device=dev, dtype=dt),
             "fk": torch.empty(B, D, device=dev, dtype=dt),
             "kf": torch.empty(B, cfg.intermediate_size, device=dev, dtype=dt),
             "h": torch.empty(B, D, device=dev, dtype=dt),
@@ -1154,7 +1153,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
         mixb, rkv, lora, prep = bufs["mix"], bufs["rkv"], bufs["lora"], bufs["prep"]
         main = torch.cuda.current_stream(x.device)
         side, ev_in, ev_out = self._side(x.device) if self.lora_side_stream else (None, None, None)
-        fmix = self._mix_fusable(B) and not self.lora_side_stream and not f16
+        fmix = self._mix_fusable(B) and not self.lora_side_stream
         parts = None  # the previous layer's FFN value partials, not yet added to x
         for L in self.layers:
             i = L.idx
@@ -1166,7 +1165,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                 if L.pre is not None:
                     layer_norm(x, L.pre[0], L.pre[1], eps, out=x)
                 aux = [L.mix[1], L.mix[4], L.mix[5], L.mix[3]][:n]
-                flora = self.fused_lora_decode and fused_lora_decode_supported(
+                flora = self.fused_lora_decode and not f16 and fused_lora_decode_supported(
                     [int(d.shape[0]) for d in L.lora_down], B)
                 mm8_lnmix_multi_into(x, xpa[i], L.ln1[0], L.ln1[1], eps, [L.mix[0], L.mix[2], L.mix[3]],
                                      [L.r_proj.m, L.k_proj.m, L.v_proj.m], [rkv[0], rkv[1], rkv[2]],
@@ -1213,7 +1212,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                                                 (rkv[0], rkv[1], rkv[2]))
                     self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
                 if f16:
-                    self._fp16_recurrence(L, rkv, lora, state[i], v_first, prep, cache.fp16_elapsed, bufs["vtmp"],
+                    self._fp16_recurrence(L, rkv, lora, state[i], v_first, prep, cache.fp16_elapsed,
                                           last=i == len(self.layers) - 1)
                 else:
                     fused_recurrent_output_prepare_raw(
@@ -1240,26 +1239,19 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
         self.lm_head.apply(bufs["h"], logits)
         return logits
 
-    def _fp16_recurrence(self, L, rkv, lora, state_l, v_first, prep, elapsed, vtmp, *, last: bool) -> None:
-        """One decode layer's recurrence on an fp16 state: the V interpolation in
-        the reference's fp16 torch form, v = v + (v_first - v) * v_gate
-        (rwkv7_hf/native_jit_decode.py:762-766), then the fp16-state kernel on
-        the raw projections, which advances elapsed on the last layer
-        (native_jit_decode.py:767-784)."""
+    def _fp16_recurrence(self, L, rkv, lora, state_l, v_first, prep, elapsed, *, last: bool) -> None:
+        """One decode layer's recurrence on an fp16 state: the fp16-state kernel
+        on the raw projections (rwkv7_hf/native_jit_decode.py:767-784), with the
+        V interpolation v + (v_first - v) * v_gate (:762-766) formed in-kernel in
+        the reference's fp16 roundings; it advances elapsed on the last layer."""
         cfg = self.config
         H, N = cfg.num_heads, cfg.head_dim
         B = int(rkv.shape[1])
-        v = rkv[2]
-        if L.idx == 0:
-            v_first.copy_(v)
-        else:
-            torch.sub(v_first, v, out=vtmp)
-            vtmp.mul_(lora[3])
-            v.add_(vtmp)
         bhn = lambda t: t.view(B, H, N)
         native_fp16_recurrent_output_prepare_raw(
-            bhn(rkv[0]), bhn(lora[0]), bhn(rkv[1]), bhn(v), bhn(lora[1]), state_l, bhn(lora[2]), L.k_k, L.k_a,
-            L.r_k, L.gn[0], L.gn[1], elapsed, advance_elapsed=last, eps=N * 1e-5, out=bhn(prep))
+            bhn(rkv[0]), bhn(lora[0]), bhn(rkv[1]), bhn(rkv[2]), bhn(lora[1]), state_l, bhn(lora[2]), L.k_k,
+            L.k_a, L.r_k, L.gn[0], L.gn[1], elapsed, advance_elapsed=last, eps=N * 1e-5, out=bhn(prep),
+            v_first=v_first, v_gate=lora[3] if L.idx > 0 else None, v_mode=1 if L.idx == 0 else 2)
 
     def _value_deferrable(self, L, B) -> bool:
         """The FFN value's split reduce can move into the next layer's norm-mix

@@ -59,14 +59,18 @@ def _require_library(what: str) -> None:
 def native_fp16_recurrent_output_prepare_raw(
     r: Any, w_raw: Any, k_raw: Any, v: Any, a: Any, state: Any, g: Any, k_k: Any, k_a: Any, r_k: Any,
     norm_weight: Any, norm_bias: Any, elapsed: Any, *, advance_elapsed: bool, eps: float,
-    out: Any | None = None,
+    out: Any | None = None, v_first: Any | None = None, v_gate: Any | None = None, v_mode: int = 0,
 ) -> Any:
     """One decode token on an fp16 state (updated in place); returns ``out`` shaped like ``r``.
 
     ``elapsed`` (int32 ``[B]``) feeds the decay dither's phase and moves by one
-    when ``advance_elapsed`` is set.  ``out`` (an extension: a contiguous fp16
-    tensor with ``r``'s element count) receives the result instead of a new
-    tensor, for callers that must not allocate (a captured decode graph).
+    when ``advance_elapsed`` is set.  Extensions beyond the reference: ``out``
+    (a contiguous fp16 tensor with ``r``'s element count) receives the result
+    instead of a new tensor, for callers that must not allocate (a captured
+    decode graph); ``v_mode`` 1 copies ``v`` into ``v_first`` (layer 0), 2 uses
+    ``v + (v_first - v) * v_gate`` in place of ``v``, rounded to fp16 after each
+    operation as the reference's torch form before this call
+    (rwkv7_hf/native_jit_decode.py:762-766).  ``v`` itself is not written.
     """
     if state.dim() != 4:
         raise ValueError("state must be [B,H,64,64]")
@@ -97,11 +101,19 @@ def native_fp16_recurrent_output_prepare_raw(
     elif not (out.is_cuda and out.dtype == torch.float16 and out.is_contiguous()
               and int(out.numel()) == int(r.numel())):
         raise ValueError("out must be a contiguous CUDA fp16 tensor with r's element count")
+    if v_mode not in (0, 1, 2):
+        raise ValueError("v_mode must be 0, 1 or 2")
+    for t, name, need in ((v_first, "v_first", v_mode >= 1), (v_gate, "v_gate", v_mode == 2)):
+        if need and (t is None or not (t.is_cuda and t.dtype == torch.float16 and t.is_contiguous()
+                                       and int(t.numel()) == int(r.numel()))):
+            raise ValueError(f"v_mode {v_mode} needs a contiguous CUDA fp16 {name} with r's element count")
     _lib.call(
         "rwkv7mi_wkv7_fp16_decode_output_prepare_raw",
         _lib.ptr(r), _lib.ptr(w_raw), _lib.ptr(k_raw), _lib.ptr(v), _lib.ptr(a), _lib.ptr(state), _lib.ptr(g),
         _lib.ptr(k_k), _lib.ptr(k_a), _lib.ptr(r_k), _lib.ptr(norm_weight), _lib.ptr(norm_bias),
-        _lib.ptr(elapsed), int(bool(advance_elapsed)), _lib.ptr(out), B, H, N, float(eps), _lib.stream_of(r),
+        _lib.ptr(elapsed), int(bool(advance_elapsed)), _lib.ptr(out),
+        _lib.ptr(v_first if v_mode >= 1 else None), _lib.ptr(v_gate if v_mode == 2 else None), int(v_mode),
+        B, H, N, float(eps), _lib.stream_of(r),
     )
     return out
 

@@ -166,15 +166,20 @@ int rwkv7mi_wkv7_chunk_status(int clear, int* status);
  * Decode from raw projections [B,H,64] with GroupNorm, bonus and gate, out
  * [B,H,64]; k_k, k_a, r_k, gn_w, gn_b [H*64].  advance_elapsed != 0 adds 1 to
  * every elapsed[b] after all heads have read it (a second launch on the same
- * stream).  Replaces rwkv7_native_fp16_recurrent_output_raw_cuda
+ * stream).  v_mode (this build's extension, as in
+ * rwkv7mi_wkv7_decode_output_prepare_raw): 0 = v as given; 1 = copy v into
+ * v_first; 2 = v + (v_first - v) * v_gate with fp16 rounding after each
+ * operation (v_first / v_gate may be NULL when unused).
+ * Replaces rwkv7_native_fp16_recurrent_output_raw_cuda
  * (rwkv7_hf/native_wkv_fp16.py:463-514, kernel :200-336) behind
  * native_fp16_recurrent_output_prepare_raw (:678). */
 int rwkv7mi_wkv7_fp16_decode_output_prepare_raw(
     const void* r, const void* w_raw, const void* k_raw, const void* v,
     const void* a, void* state, const void* g, const void* k_k,
     const void* k_a, const void* r_k, const void* gn_w, const void* gn_b,
-    int32_t* elapsed, int advance_elapsed, void* out, int64_t B, int64_t H,
-    int64_t N, float eps, void* stream);
+    int32_t* elapsed, int advance_elapsed, void* out, void* v_first,
+    const void* v_gate, int v_mode, int64_t B, int64_t H, int64_t N, float eps,
+    void* stream);
 
 /* T >= 1 tokens of prepared vectors [B,T,H,64]: w raw (plus w0 [H*64] in
  * fp32 when w0 != NULL), neg_kk = -kk, kka = kk*a; out [B,T,H,64] is the raw

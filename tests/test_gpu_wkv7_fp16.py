@@ -197,3 +197,28 @@ def test_fp16_sequence_one_token_matches_decode_state():
                          _t(c["elapsed"], torch.int32))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(_np(st), st_dec)
+
+
+def test_fp16_decode_v_interpolation_in_kernel_equals_torch_form():
+    """v_mode 2 forms v + (v_first - v) * v_gate in-kernel with the roundings of
+    the reference's fp16 torch ops; v_mode 1 stores v as v_first."""
+    from rwkv7mi import native_fp16_recurrent_output_prepare_raw as op
+
+    rng = np.random.default_rng(41)
+    B, H = 3, 8
+    c = _decode_case(rng, B, H, safe=False)
+    vf = _t(rng.standard_normal((B, H, 64)))
+    gate = _t(rng.uniform(0, 1, (B, H, 64)))
+    args = lambda st, v: (_t(c["r"]), _t(c["w_raw"]), _t(c["k_raw"]), v, _t(c["a"]), st, _t(c["g"]), _t(c["k_k"]),
+                          _t(c["k_a"]), _t(c["r_k"]), _t(c["gn_w"]), _t(c["gn_b"]), _t(c["elapsed"], torch.int32))
+    v = _t(c["v"])
+    st_a, st_b = _t(c["state"]), _t(c["state"])
+    mixed = v + (vf - v) * gate  # fp16 torch ops, one rounding each
+    out_a = op(*args(st_a, mixed.contiguous()), advance_elapsed=False, eps=1e-5)
+    out_b = op(*args(st_b, v.clone()), advance_elapsed=False, eps=1e-5, v_first=vf, v_gate=gate, v_mode=2)
+    vf1 = torch.zeros_like(v)
+    st_c = _t(c["state"])
+    op(*args(st_c, v), advance_elapsed=False, eps=1e-5, v_first=vf1, v_mode=1)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b) and torch.equal(st_a, st_b)
+    assert torch.equal(vf1, v)
