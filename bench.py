@@ -70,10 +70,11 @@ def scan_bytes(B, T, H, N):
     return B * T * H * N * 16 + 2 * B * H * N * N * 4
 
 
-def decode_step_bytes(cfg, B, quantized: set[str], shapes: dict):
+def decode_step_bytes(cfg, B, quantized: set[str], shapes: dict, state_bytes: int = 4):
     """Algorithmic HBM bytes of one decode step: every weight read once (MM8:
     1 B/weight + fp16 row/col metadata; others fp16), the recurrent state read +
-    written, shift states read + written, embedding rows and logits."""
+    written (``state_bytes`` per element), shift states read + written,
+    embedding rows and logits."""
     total = 0
     for name, shp in shapes.items():
         if name == "model.embeddings.weight":
@@ -89,7 +90,7 @@ def decode_step_bytes(cfg, B, quantized: set[str], shapes: dict):
         else:
             total += n * 2
     L, H, N, D = cfg.num_hidden_layers, cfg.num_heads, cfg.head_dim, cfg.hidden_size
-    total += L * B * H * N * N * 4 * 2          # state read + write
+    total += L * B * H * N * N * state_bytes * 2  # state read + write
     total += L * 2 * B * D * 2 * 2               # xpa / xpf read + write
     total += B * cfg.vocab_size * 2               # logits
     return total
@@ -335,6 +336,7 @@ def run_decode(model, cfg, quantized, batches=(1, 8, 64), steps=64, warmup=5):
     from rwkv7mi.model import parameter_shapes
 
     shapes = parameter_shapes(cfg)
+    sbytes = torch.empty(0, dtype=model.state_dtype).element_size()
     res = {}
     g = torch.Generator(device="cuda")
     g.manual_seed(0)
@@ -351,11 +353,11 @@ def run_decode(model, cfg, quantized, batches=(1, 8, 64), steps=64, warmup=5):
             runner.replay_greedy(cache)
 
         ms, wall = time_events(step, steps, warmup)
-        nbytes = decode_step_bytes(cfg, B, quantized, shapes)
+        nbytes = decode_step_bytes(cfg, B, quantized, shapes, sbytes)
         gbs = nbytes / (ms / 1e3) / 1e9
         res[B] = {"tok_s": B / (ms / 1e3), "ms": ms, "wall_s": wall, "bytes": nbytes, "gbs": gbs,
                   "frac": gbs / HBM_PEAK_GBS}
-        _log(f"bench: decode bsz {B}: {ms:.3f} ms/step, {B / (ms / 1e3):.1f} tok/s, {gbs:.0f} GB/s "
+        _log(f"bench: decode bsz {B} ({'fp16' if sbytes == 2 else 'fp32'} state): {ms:.3f} ms/step, {B / (ms / 1e3):.1f} tok/s, {gbs:.0f} GB/s "
              f"({100 * gbs / HBM_PEAK_GBS:.1f}% of the step roofline)")
         del model._graph_runners[B]
     return res
@@ -795,7 +797,7 @@ def main(argv=None):
                  f"{100 * s['frac']:.1f}% of HBM roofline")
         step = run_decode_form_step()
         _log(f"bench: decode-form step {step['config']}: {step['us_per_step']} us ({100 * step['frac']:.1f}%)")
-    dec = mk = pre = None
+    dec = mk = pre = dec16 = None
     if wl in ("all", "decode", "prefill"):
         cfg, model, quantized = build_7p2b()
         if wl in ("all", "decode"):
@@ -803,6 +805,12 @@ def main(argv=None):
                              args.warmup)
             mk = run_mm8_roofline(model, cfg)
             _log(f"bench: MM8 launches of a bsz-1 step: {mk['avg_us']:.2f} us avg, {mk['gbs']:.0f} GB/s")
+            # the opt-in fp16-state lane through the same model (the reference's
+            # own comparison is 7.2B B8 decode with fp32 vs fp16 state)
+            model.state_dtype = torch.float16
+            dec16 = run_decode(model, cfg, quantized, tuple(int(b) for b in args.batches.split(",")),
+                               min(args.steps, 32), min(args.warmup, 3))
+            model.state_dtype = torch.float32
         if wl in ("all", "prefill"):
             pre = run_prefill(model, cfg)
             _log(f"bench: prefill {pre['config']}: {pre['ms']:.1f} ms, {pre['tok_s']:.0f} tok/s, "
@@ -886,8 +894,13 @@ def main(argv=None):
             "bytes_per_launch": w4_bytes(4096, 65536, 1, affine=True), "avg_launch_us": head["asym_us"]}}
     if c1:
         out["c1_0p1b"] = c1
-    if f16:
-        out["wkv7_fp16_state"] = f16
+    if f16 or dec16:
+        out["wkv7_fp16_state"] = dict(f16 or {})
+        if dec16:
+            out["wkv7_fp16_state"]["decode_7p2b"] = {
+                str(b): {"tok_s": round(d["tok_s"], 2), "ms_per_step": round(d["ms"], 4),
+                         "fp32_state_ms_per_step": round(dec[b]["ms"], 4) if dec and b in dec else None,
+                         "step_roofline_frac": round(d["frac"], 4)} for b, d in dec16.items()}
     if not args.no_cpu and out:
         for key, shapes, kind, bytes_of in (("mm8_c3", c3_shapes, "mm8", lambda i, o: mm8_bytes(i, o, 1)),
                                             ("w4_c4", c4_shapes, "w4", lambda i, o: w4_bytes(i, o, 1, affine=False))):
