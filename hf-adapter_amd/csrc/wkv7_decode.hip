@@ -12,6 +12,7 @@
 //   S'[i,j] = S[i,j] * w[j] - (S[i,:] . kk) * kk[j] * a[j] + v[i] * k[j]
 //   y[i]    = S'[i,:] . r
 #include "common.h"
+#include "decode_lora.h"
 
 namespace rwkv7mi {
 
@@ -176,35 +177,9 @@ __global__ __launch_bounds__(256) void wkv7_decode_kernel(
 
 // ---------------------------------------------------------------------------
 // Decode with the W/A/G/V LoRA up projections fused in (rwkv7_hf/fused_lora.py
-// :706 fused_wavg_lora, then fused_recurrent_output_prepare_raw).  The down
-// projections' fp32 partials (lora.hip, [problem][ks][rows][rank]) are summed
-// in fixed order, act_down applied and rounded to the activation dtype (the
-// reference's mid tensor); each (batch, head) workgroup then computes only its
-// own 64 channels of every up projection, y_p = act_up_p(mid_p Wu_p^T + b_p),
-// rounded to the activation dtype as the reference's tensors are.
-// Problems: 0 w_raw, 1 a, 2 g, 3 v_gate (the last only with v_mode 2).
-// Wave p handles problem p end to end (lane c = output channel h*64 + c), so
-// its pointers and rank are wave-uniform and it needs no barrier until the
-// four results meet for the state update.
-constexpr int DL_MAXR = 128;  // largest rank on this route
-constexpr int DL_ZB = 16;     // K-split partials loaded per batch (1 when the sums arrive whole)
-
-struct DecLora {
-  const float* part;
-  const void* wu[4];
-  const void* bu[4];
-  int64_t part_off[4];  // floats
-  int64_t part_total;   // floats of the whole partial buffer
-  int rank[4], act_d[4], act_u[4];
-  int nprob, ks, rows;
-};
-
-__device__ __forceinline__ float dl_act(float v, int act) {
-  if (act == 1) return tanhf(v);
-  if (act == 2) return 1.0f / (1.0f + expf(-v));
-  return v;
-}
-
+// :706 fused_wavg_lora, then fused_recurrent_output_prepare_raw): the four
+// waves compute the head's channels of the up projections (dl_up,
+// decode_lora.h), then the state update and output prep as in MODE_RAW.
 template <typename TA, typename TP, int ZB>
 __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
     const TA* __restrict__ r, const TA* __restrict__ k, const TA* __restrict__ v, const DecLora LA,
@@ -228,131 +203,33 @@ __global__ __launch_bounds__(256) void wkv7_decode_lora_kernel(
   const int j0 = (tid & 3) * 16;
   const int64_t soff = ((int64_t)bh * HEAD + i) * HEAD + j0;
 
-  const bool active = wave < LA.nprob;  // wave-uniform
-  const int rp = active ? LA.rank[wave] : 0;
-  // the LoRA down partials first: the up projections wait on them, the state
-  // only at the update (loads complete in issue order)
-  float pt0[2][ZB];
-  {
-    const __amdgpu_buffer_rsrc_t pr = make_rsrc(LA.part, (uint32_t)LA.part_total * 4u);
-    const uint32_t zs = (uint32_t)(LA.rows * rp);
-    const uint32_t base = (uint32_t)((active ? LA.part_off[wave] : 0) + (int64_t)b * rp);
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int zz = 0; zz < ZB; ++zz) {
-        const bool ok = lane + 64 * u < rp && zz < LA.ks;
-        pt0[u][zz] = buf_ldf(pr, ok ? (base + (uint32_t)zz * zs + lane + 64u * u) * 4u : BUF_OOB);
-      }
-  }
   // state rows, per-row output parameters and channel `lane` of this head's
   // vectors (every wave loads them; only the first uses them) — no branches,
-  // so all of these loads are in flight together with the LoRA loads
+  // so all of these loads are in flight together with the LoRA loads; v_first
+  // (v_mode 2) is issued with them rather than where it is used (it would add
+  // a memory round trip there)
   float s[16];
-  {
+  float gnw_i, gnb_i, rv, kraw, vv, kkw, kaw, rkw, vf_pre;
+  dl_up<TA, ZB>(LA, b, h, H, wave, lane, s_mid, s_lo, [&] {
     const float4* src = reinterpret_cast<const float4*>(state_in + soff);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       float4 t4 = src[q];
       s[4 * q + 0] = t4.x; s[4 * q + 1] = t4.y; s[4 * q + 2] = t4.z; s[4 * q + 3] = t4.w;
     }
-  }
-  const int64_t pi = (int64_t)h * HEAD + i;
-  const float gnw_i = ld(gn_w, pi), gnb_i = ld(gn_b, pi);
-  const int64_t pc = (int64_t)h * HEAD + lane;
-  const float rv = ld(r, vec + lane), kraw = ld(k, vec + lane), vv = ld(v, vec + lane);
-  const float kkw = ld(k_k, pc), kaw = ld(k_a, pc), rkw = ld(r_k, pc);
-
-  // v_first (v_mode 2) and this wave's up-projection bias, issued with the rest
-  // rather than where they are used (each would add a memory round trip there)
-  const float vf_pre = buf_ld1<TA>(make_rsrc(v_first ? v_first + vec : nullptr, v_first ? HEAD * (uint32_t)sizeof(TA) : 0u),
-                                   (uint32_t)lane, v_mode == 2);
-  // Up projection of this wave's problem, loaded coalesced: a row of Wu_p
-  // (rank elements) is spread over L lanes, 8 elements each (L = rank / 8
-  // rounded up to a power of two), so load i reads the 64 / L consecutive
-  // rows i * 64 / L .. of the head as one contiguous run.  The lane's row
-  // segments are dotted with its 8 mid values and the L lanes of a row then
-  // reduce-scatter, which leaves channel c = lq * (64 / L) + lr in lane
-  // (lr, lq), lane = lr * L + lq.
-  const int r8 = rp >> 3;
-  const int L = r8 <= 1 ? 1 : r8 <= 2 ? 2 : r8 <= 4 ? 4 : r8 <= 8 ? 8 : 16;  // wave-uniform
-  const int lq = lane & (L - 1), lr = lane / L, rpi = HEAD / L;
-  const int cu = lq * rpi + lr;  // the channel this lane finishes
-  const void* bu_w = active ? LA.bu[wave] : nullptr;
-  const float bias_pre = buf_ld1<TA>(
-      make_rsrc(bu_w ? reinterpret_cast<const TA*>(bu_w) + (int64_t)h * HEAD : nullptr, bu_w ? HEAD * (uint32_t)sizeof(TA) : 0u),
-      (uint32_t)cu, bu_w != nullptr);
-  float wseg[DL_MAXR / 8][8];
-  {
-    const __amdgpu_buffer_rsrc_t wr =
-        make_rsrc(active ? LA.wu[wave] : LA.wu[0], (uint32_t)((int64_t)H * HEAD * rp * (int64_t)sizeof(TA)));
-#pragma unroll
-    for (int i = 0; i < DL_MAXR / 8; ++i) {
-      const uint32_t e0 = (uint32_t)((int64_t)(h * HEAD + i * rpi + lr) * rp + 8 * lq);
-      buf_ld8(wr, e0, i < L && lq < r8, (const TA*)nullptr, wseg[i]);
-    }
-  }
-  // mid_p[kk] for kk = lane, lane + 64: the rest of the K-split partials (the
-  // first ZB splits are in flight since the kernel's start), summed in z order
-  {
-    const __amdgpu_buffer_rsrc_t pr = make_rsrc(LA.part, (uint32_t)LA.part_total * 4u);
-    const uint32_t zs = (uint32_t)(LA.rows * rp);
-    const uint32_t base = (uint32_t)((active ? LA.part_off[wave] : 0) + (int64_t)b * rp);
-    float acc[2] = {0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int zz = 0; zz < ZB; ++zz) acc[u] += pt0[u][zz];  // past-the-end terms are +0
-    for (int z0 = ZB; z0 < LA.ks; z0 += ZB) {
-      float t[2][ZB];
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int zz = 0; zz < ZB; ++zz) {
-          const bool ok = lane + 64 * u < rp && z0 + zz < LA.ks;
-          t[u][zz] = buf_ldf(pr, ok ? (base + (uint32_t)(z0 + zz) * zs + lane + 64u * u) * 4u : BUF_OOB);
-        }
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int zz = 0; zz < ZB; ++zz) acc[u] += t[u][zz];
-    }
-    // every entry of the wave's row is written (zeros past the rank), so the
-    // up projection's segments past the rank read zeros
-    const int ad = active ? LA.act_d[wave] : 0;
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-      s_mid[wave][lane + 64 * u] = lane + 64 * u < rp ? to_f32(from_f32<TA>(dl_act(acc[u], ad))) : 0.f;
-  }
-  // this wave's problem (the wave reads its own s_mid row: LDS operations of
-  // one wave complete in order, so no barrier is needed)
-  if (active) {
-    const float4 m0 = *reinterpret_cast<const float4*>(&s_mid[wave][8 * lq]);
-    const float4 m1 = *reinterpret_cast<const float4*>(&s_mid[wave][8 * lq + 4]);
-    float pt[DL_MAXR / 8];
-#pragma unroll
-    for (int i = 0; i < DL_MAXR / 8; ++i)
-      pt[i] = ((m0.x * wseg[i][0] + m0.y * wseg[i][1]) + (m0.z * wseg[i][2] + m0.w * wseg[i][3])) +
-              ((m1.x * wseg[i][4] + m1.y * wseg[i][5]) + (m1.z * wseg[i][6] + m1.w * wseg[i][7]));
-    // reduce-scatter over the row's L lanes: at distance d the lane with bit d
-    // of lq set keeps the upper half of its window; pt[0] ends as the total of
-    // load lq's row (loads past L read zeros)
-#pragma unroll
-    for (int d = DL_MAXR / 16; d >= 1; d >>= 1) {
-      if (d < L) {
-        const bool up = (lq & d) != 0;
-#pragma unroll
-        for (int j = 0; j < d; ++j) {
-          const float keep = up ? pt[j + d] : pt[j];
-          const float give = up ? pt[j] : pt[j + d];
-          pt[j] = keep + __shfl_xor(give, d, 64);
-        }
-      }
-    }
-    float acc = pt[0];
-    if (bu_w) acc += bias_pre;
-    s_lo[wave][cu] = to_f32(from_f32<TA>(dl_act(acc, LA.act_u[wave])));
-  }
+    const int64_t pi = (int64_t)h * HEAD + i;
+    gnw_i = ld(gn_w, pi);
+    gnb_i = ld(gn_b, pi);
+    const int64_t pc = (int64_t)h * HEAD + lane;
+    rv = ld(r, vec + lane);
+    kraw = ld(k, vec + lane);
+    vv = ld(v, vec + lane);
+    kkw = ld(k_k, pc);
+    kaw = ld(k_a, pc);
+    rkw = ld(r_k, pc);
+    vf_pre = buf_ld1<TA>(make_rsrc(v_first ? v_first + vec : nullptr, v_first ? HEAD * (uint32_t)sizeof(TA) : 0u),
+                         (uint32_t)lane, v_mode == 2);
+  });
   __syncthreads();
 
   if (tid < HEAD)
@@ -445,10 +322,6 @@ extern "C" int rwkv7mi_wkv7_decode_output_prepare_raw(
                                  act_dtype, act_dtype, param_dtype, stream);
 }
 
-static int lora_splits_for(int64_t nprob, const int64_t* ranks, int64_t D) {
-  return lora_splits(lora_tiles(nprob, ranks), D);
-}
-
 extern "C" int rwkv7mi_wkv7_decode_lora_output_prepare(
     const void* r, const void* k_raw, const void* v, const float* lora_part, int64_t nprob,
     const int64_t* ranks, const void* const* w_up, const void* const* b_up, const int* act_down,
@@ -460,39 +333,18 @@ extern "C" int rwkv7mi_wkv7_decode_lora_output_prepare(
   if (B < 0 || H <= 0 || D <= 0) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: bad B/H/D");
   if (B == 0) return RWKV7MI_OK;
   if (B > LORA_ROWS) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: at most 64 rows");
-  if (!r || !k_raw || !v || !lora_part || !ranks || !w_up || !act_down || !act_up || !state_in || !state_out ||
-      !k_k || !k_a || !r_k || !gn_w || !gn_b || !out)
+  if (!r || !k_raw || !v || !state_in || !state_out || !k_k || !k_a || !r_k || !gn_w || !gn_b || !out)
     return fail(RWKV7MI_EINVAL, "wkv7 decode lora: null pointer");
   if (v_mode < 0 || v_mode > 2) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: bad v_mode");
-  if (nprob != 3 && nprob != 4) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: 3 or 4 LoRA problems");
   if (v_mode == 2 && nprob != 4) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: v_mode 2 needs the v LoRA");
   if (v_mode != 0 && !v_first) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: v_mode needs v_first");
   if ((reinterpret_cast<uintptr_t>(state_in) | reinterpret_cast<uintptr_t>(state_out)) & 15)
     return fail(RWKV7MI_EINVAL, "wkv7 decode lora: state must be 16-byte aligned");
   if (B * H > INT32_MAX) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: B*H too large");
-  DecLora la{};
-  la.part = lora_part;
-  la.nprob = (int)nprob;
-  la.rows = (int)B;
-  if (lora_splits < 0 || lora_splits > 4096) return fail(RWKV7MI_EINVAL, "wkv7 decode lora: bad lora_splits");
-  la.ks = lora_splits ? (int)lora_splits : lora_splits_for(nprob, ranks, D);
-  int64_t off = 0;
-  for (int p = 0; p < nprob; ++p) {
-    if (ranks[p] <= 0 || ranks[p] % 8 || ranks[p] > DL_MAXR || !w_up[p])
-      return fail(RWKV7MI_EINVAL, "wkv7 decode lora: ranks must be positive multiples of 8, at most 128");
-    if (act_down[p] < 0 || act_down[p] > 2 || act_up[p] < 0 || act_up[p] > 2)
-      return fail(RWKV7MI_EINVAL, "wkv7 decode lora: activation must be 0 none, 1 tanh or 2 sigmoid");
-    if (reinterpret_cast<uintptr_t>(w_up[p]) & 15)
-      return fail(RWKV7MI_EINVAL, "wkv7 decode lora: up weights must be 16-byte aligned");
-    la.wu[p] = w_up[p];
-    la.bu[p] = b_up ? b_up[p] : nullptr;
-    la.rank[p] = (int)ranks[p];
-    la.act_d[p] = act_down[p];
-    la.act_u[p] = act_up[p];
-    la.part_off[p] = off;
-    off += (int64_t)la.ks * B * ranks[p];
-  }
-  la.part_total = off;
+  DecLora la;
+  if (int rc = dl_build(la, "wkv7 decode lora", lora_part, nprob, ranks, w_up, b_up, act_down, act_up, D,
+                        lora_splits, B))
+    return rc;
   return dispatch_dtype(act_dtype, [&](auto ta) {
     using TA = decltype(ta);
     return dispatch_dtype(param_dtype, [&](auto tp) {
