@@ -21,6 +21,7 @@
 // consecutive lanes on consecutive addresses); the per-token key-side vectors
 // are staged in LDS and read back as broadcasts.
 #include "common.h"
+#include "decode_lora.h"
 
 // No implicit fusing in this file: every fp32 expression that ends in an fp16
 // value (decay delta, k, kk*a, the V interpolation) is rounded to fp32 first
@@ -73,23 +74,30 @@ __device__ __forceinline__ void lds_h2x4(const _Float16* p, h2 (&o)[4]) {
   o[0] = h2_bits(u.x); o[1] = h2_bits(u.y); o[2] = h2_bits(u.z); o[3] = h2_bits(u.w);
 }
 
-// Head state [64][64] fp16 at g -> s_st (row stride F16_RS) with coalesced
-// 16-byte loads: lane l, pass q moves 8 halves of row 8q + l/8 at column 8(l%8).
-__device__ __forceinline__ void f16_state_in(const _Float16* g, _Float16* s_st, int lane) {
-  uint4 t[8];
+// Head state [64][64] fp16 at g <-> s_st (row stride F16_RS) with coalesced
+// 16-byte accesses by NT threads: thread t, pass q moves the 8 halves of 16-byte
+// chunk c = q NT + t, row c/8, column 8(c%8).
+template <int NT = 64>
+__device__ __forceinline__ void f16_state_in(const _Float16* g, _Float16* s_st, int t) {
+  uint4 v[512 / NT];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) t[q] = reinterpret_cast<const uint4*>(g)[q * 64 + lane];
+  for (int q = 0; q < 512 / NT; ++q) v[q] = reinterpret_cast<const uint4*>(g)[q * NT + t];
 #pragma unroll
-  for (int q = 0; q < 8; ++q)
-    *reinterpret_cast<uint4*>(s_st + (q * 8 + (lane >> 3)) * F16_RS + (lane & 7) * 8) = t[q];
+  for (int q = 0; q < 512 / NT; ++q) {
+    const int c = q * NT + t;
+    *reinterpret_cast<uint4*>(s_st + (c >> 3) * F16_RS + (c & 7) * 8) = v[q];
+  }
 }
-__device__ __forceinline__ void f16_state_out(_Float16* g, const _Float16* s_st, int lane) {
-  uint4 t[8];
+template <int NT = 64>
+__device__ __forceinline__ void f16_state_out(_Float16* g, const _Float16* s_st, int t) {
+  uint4 v[512 / NT];
 #pragma unroll
-  for (int q = 0; q < 8; ++q)
-    t[q] = *reinterpret_cast<const uint4*>(s_st + (q * 8 + (lane >> 3)) * F16_RS + (lane & 7) * 8);
+  for (int q = 0; q < 512 / NT; ++q) {
+    const int c = q * NT + t;
+    v[q] = *reinterpret_cast<const uint4*>(s_st + (c >> 3) * F16_RS + (c & 7) * 8);
+  }
 #pragma unroll
-  for (int q = 0; q < 8; ++q) reinterpret_cast<uint4*>(g)[q * 64 + lane] = t[q];
+  for (int q = 0; q < 512 / NT; ++q) reinterpret_cast<uint4*>(g)[q * NT + t] = v[q];
 }
 // the lane's own row (row `lane`) <-> 32 half pairs
 __device__ __forceinline__ void f16_row_get(const _Float16* s_st, int lane, h2 (&s)[32]) {
@@ -209,6 +217,58 @@ __device__ __forceinline__ void wait_lds_all() { __builtin_amdgcn_s_waitcnt(0xC0
 // 2 first forms v + (v_first - v) * v_gate with an fp16 rounding after each
 // operation, the values the reference's fp16 torch form gives
 // (rwkv7_hf/native_jit_decode.py:762-766).
+__device__ __forceinline__ _Float16 f16_v_mix(_Float16 vh, _Float16* v_first, int64_t e, float v_gate, int v_mode) {
+  if (v_mode == 1) {
+    v_first[e] = vh;
+  } else if (v_mode == 2) {
+    // three roundings, as three fp16 tensor operations give
+    const _Float16 d = f16_rn((float)v_first[e] - (float)vh);
+    const _Float16 m = f16_rn((float)d * v_gate);
+    vh = f16_rn((float)vh + (float)m);
+  }
+  return vh;
+}
+
+// The head's update by one wave: lane i = channel i = state row i, whose row
+// is in s_st (written by this wave, or by the workgroup before a barrier);
+// leaves the updated row in s_st and returns out[i].  vh is v after the
+// interpolation; the other inputs are the lane's channel values.
+__device__ __forceinline__ _Float16 f16_decode_head(int i, _Float16 rh, float wr, float kr, _Float16 vh, float af,
+                                                    float gf, float kkw, float kaw, float rkw, float gw, float gb,
+                                                    uint32_t phase, float eps, _Float16* s_st,
+                                                    _Float16 (&s_vec)[5][F16_N]) {
+  const float kku = kr * kkw;
+  const float kkv = kku / fmaxf(sqrtf(wave_sum(kku * kku)), 1.0e-12f);
+  const _Float16 kh = f16_rn(kr * fmaf(af, kaw, 1.0f - kaw));
+  const _Float16 kkh = f16_rn(kkv);
+  s_vec[0][i] = rh;
+  s_vec[1][i] = f16_decay_delta(wr, phase);
+  s_vec[2][i] = kh;
+  s_vec[3][i] = -kkh;
+  s_vec[4][i] = f16_rn((float)kkh * af);
+  // every lane's LDS writes (the vectors, and the state rows when this wave
+  // staged them) are complete before any lane reads another's
+  wait_lds_all();
+  __builtin_amdgcn_wave_barrier();
+
+  h2 s[32], n[32], r2[32], w2[32], k2[32], b2[32];
+  f16_row_get(s_st, i, s);
+  lds_h2x32(s_vec[3], n);
+  lds_h2x32(s_vec[0], r2);
+  lds_h2x32(s_vec[1], w2);
+  lds_h2x32(s_vec[2], k2);
+  lds_h2x32(s_vec[4], b2);
+  const _Float16 yh = f16_row_update(s, f16_row_sa(s, n), r2, w2, k2, b2, vh);
+  f16_row_put(s_st, i, s);
+
+  const float y = (float)yh;
+  const float mean = wave_sum(y) * (1.0f / F16_N);
+  const float cen = y - mean;
+  const float var = wave_sum(cen * cen) * (1.0f / F16_N);
+  const float corr = wave_sum((float)rh * (float)kh * rkw);
+  return f16_rn((cen * rsqrtf(var + eps) * gw + gb + corr * (float)vh) * gf);
+}
+
 __global__ __launch_bounds__(64) void wkv7_f16_decode_kernel(
     const _Float16* __restrict__ r, const _Float16* __restrict__ w_raw, const _Float16* __restrict__ k_raw,
     const _Float16* __restrict__ v, const _Float16* __restrict__ a, _Float16* __restrict__ state,
@@ -228,51 +288,79 @@ __global__ __launch_bounds__(64) void wkv7_f16_decode_kernel(
   _Float16* sg = state + (int64_t)bh * F16_N * F16_N;
 
   f16_state_in(sg, s_st, i);
-  const _Float16 rh = r[e];
-  _Float16 vh = v[e];
-  if (v_mode == 1) {
-    v_first[e] = vh;
-  } else if (v_mode == 2) {
-    // three roundings, as three fp16 tensor operations give
-    const _Float16 d = f16_rn((float)v_first[e] - (float)vh);
-    const _Float16 m = f16_rn((float)d * (float)v_gate[e]);
-    vh = f16_rn((float)vh + (float)m);
-  }
-  const float kr = (float)k_raw[e], af = (float)a[e], wr = (float)w_raw[e], gf = (float)g[e];
-  const float kkw = (float)k_k[pc], kaw = (float)k_a[pc], rkw = (float)r_k[pc];
-  const float gw = (float)gn_w[pc], gb = (float)gn_b[pc];
-  const uint32_t phase = (uint32_t)elapsed[b] + (uint32_t)pc;
-
-  const float kku = kr * kkw;
-  const float kkv = kku / fmaxf(sqrtf(wave_sum(kku * kku)), 1.0e-12f);
-  const _Float16 kh = f16_rn(kr * fmaf(af, kaw, 1.0f - kaw));
-  const _Float16 kkh = f16_rn(kkv);
-  s_vec[0][i] = rh;
-  s_vec[1][i] = f16_decay_delta(wr, phase);
-  s_vec[2][i] = kh;
-  s_vec[3][i] = -kkh;
-  s_vec[4][i] = f16_rn((float)kkh * af);
-  __syncthreads();
-
-  h2 s[32], n[32], r2[32], w2[32], k2[32], b2[32];
-  f16_row_get(s_st, i, s);
-  lds_h2x32(s_vec[3], n);
-  lds_h2x32(s_vec[0], r2);
-  lds_h2x32(s_vec[1], w2);
-  lds_h2x32(s_vec[2], k2);
-  lds_h2x32(s_vec[4], b2);
-  const _Float16 yh = f16_row_update(s, f16_row_sa(s, n), r2, w2, k2, b2, vh);
-  f16_row_put(s_st, i, s);
-
-  const float y = (float)yh;
-  const float mean = wave_sum(y) * (1.0f / F16_N);
-  const float cen = y - mean;
-  const float var = wave_sum(cen * cen) * (1.0f / F16_N);
-  const float corr = wave_sum((float)rh * (float)kh * rkw);
-  out[e] = f16_rn((cen * rsqrtf(var + eps) * gw + gb + corr * (float)vh) * gf);
-
+  const _Float16 vh = f16_v_mix(v[e], v_first, e, v_mode == 2 ? (float)v_gate[e] : 0.f, v_mode);
+  out[e] = f16_decode_head(i, r[e], (float)w_raw[e], (float)k_raw[e], vh, (float)a[e], (float)g[e], (float)k_k[pc],
+                           (float)k_a[pc], (float)r_k[pc], (float)gn_w[pc], (float)gn_b[pc],
+                           (uint32_t)elapsed[b] + (uint32_t)pc, eps, s_st, s_vec);
   __syncthreads();
   f16_state_out(sg, s_st, i);
+}
+
+// The same update with the W/A/G/V LoRA up projections inside (the second
+// half of fused_wavg_lora, rwkv7_hf/fused_lora.py:706): four waves compute the
+// head's 64 channels of w_raw, a, g and v_gate (dl_up, decode_lora.h) while the
+// fp16 state and the channel inputs load, then wave 0 updates the head.
+template <int ZB>
+__global__ __launch_bounds__(256) void wkv7_f16_decode_lora_kernel(
+    const _Float16* __restrict__ r, const _Float16* __restrict__ k_raw, const _Float16* __restrict__ v,
+    const DecLora LA, _Float16* __restrict__ state, const _Float16* __restrict__ k_k,
+    const _Float16* __restrict__ k_a, const _Float16* __restrict__ r_k, const _Float16* __restrict__ gn_w,
+    const _Float16* __restrict__ gn_b, const int* __restrict__ elapsed, _Float16* __restrict__ out,
+    _Float16* __restrict__ v_first, int v_mode, int H, float eps) {
+  __shared__ __align__(16) _Float16 s_st[F16_N * F16_RS];
+  __shared__ __align__(16) _Float16 s_vec[5][F16_N];
+  __shared__ __align__(16) float s_mid[4][DL_MAXR];
+  __shared__ float s_lo[4][DL_HEAD];
+
+  const int bh = blockIdx.x;
+  const int b = bh / H;
+  const int h = bh - b * H;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int64_t e = (int64_t)bh * F16_N + lane;
+  const int pc = h * F16_N + lane;
+  _Float16* sg = state + (int64_t)bh * F16_N * F16_N;
+
+  // The state and channel loads are issued behind the first LoRA partials and
+  // land in registers, so the up weights' loads follow without a wait; the
+  // state goes to LDS once dl_up is done.
+  uint4 sv0, sv1;
+  _Float16 rh, kh, vh, vfh;
+  float kkw, kaw, rkw, gw, gb;
+  uint32_t phase;
+  dl_up<__half, ZB>(LA, b, h, H, wave, lane, s_mid, s_lo, [&] {
+    sv0 = reinterpret_cast<const uint4*>(sg)[tid];
+    sv1 = reinterpret_cast<const uint4*>(sg)[256 + tid];
+    // channel `lane` of this head (every wave loads; wave 0 uses them)
+    rh = r[e];
+    kh = k_raw[e];
+    vh = v[e];
+    vfh = v_mode == 2 ? v_first[e] : (_Float16)0.0f;
+    kkw = (float)k_k[pc];
+    kaw = (float)k_a[pc];
+    rkw = (float)r_k[pc];
+    gw = (float)gn_w[pc];
+    gb = (float)gn_b[pc];
+    phase = (uint32_t)elapsed[b] + (uint32_t)pc;
+  });
+  *reinterpret_cast<uint4*>(s_st + (tid >> 3) * F16_RS + (tid & 7) * 8) = sv0;
+  *reinterpret_cast<uint4*>(s_st + ((256 + tid) >> 3) * F16_RS + (tid & 7) * 8) = sv1;
+  __syncthreads();  // the state rows and the four up projections are in LDS
+  if (wave == 0) {
+    _Float16 vm = vh;
+    if (v_mode == 1) {
+      v_first[e] = vh;
+    } else if (v_mode == 2) {
+      const _Float16 d = f16_rn((float)vfh - (float)vh);
+      const _Float16 m = f16_rn((float)d * s_lo[3][lane]);
+      vm = f16_rn((float)vh + (float)m);
+    }
+    out[e] = f16_decode_head(lane, rh, s_lo[0][lane], (float)kh, vm, s_lo[1][lane], s_lo[2][lane], kkw, kaw, rkw,
+                             gw, gb, phase, eps, s_st, s_vec);
+  }
+  __syncthreads();
+  f16_state_out<256>(sg, s_st, tid);
 }
 
 __global__ __launch_bounds__(64) void wkv7_f16_advance_kernel(int* __restrict__ elapsed, int B) {
@@ -456,6 +544,47 @@ extern "C" int rwkv7mi_wkv7_fp16_decode_output_prepare_raw(
   if (rc != RWKV7MI_OK || !advance_elapsed) return rc;
   // Every head of the step reads elapsed[b] before it moves: the increment is
   // a second launch on the same stream.
+  hipLaunchKernelGGL(wkv7_f16_advance_kernel, dim3((unsigned)((B + 63) / 64)), dim3(64), 0, st, (int*)elapsed,
+                     (int)B);
+  return check_launch("wkv7_f16_advance_kernel");
+}
+
+extern "C" int rwkv7mi_wkv7_fp16_decode_lora_output_prepare(
+    const void* r, const void* k_raw, const void* v, const float* lora_part, int64_t nprob, const int64_t* ranks,
+    const void* const* w_up, const void* const* b_up, const int* act_down, const int* act_up, int64_t D,
+    int64_t lora_splits, void* state, const void* k_k, const void* k_a, const void* r_k, const void* gn_w,
+    const void* gn_b, int32_t* elapsed, int advance_elapsed, void* out, void* v_first, int v_mode, int64_t B,
+    int64_t H, int64_t N, float eps, void* stream) {
+  if (N != F16_N) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode lora: head size must be 64");
+  if (B < 0 || H <= 0 || D <= 0) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode lora: bad B/H/D");
+  if (B == 0) return RWKV7MI_OK;
+  if (B > LORA_ROWS) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode lora: at most 64 rows");
+  if (!r || !k_raw || !v || !state || !k_k || !k_a || !r_k || !gn_w || !gn_b || !elapsed || !out)
+    return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode lora: null pointer");
+  if (!f16_aligned16(state)) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode lora: state must be 16-byte aligned");
+  if (v_mode < 0 || v_mode > 2) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode lora: v_mode must be 0, 1 or 2");
+  if (v_mode == 2 && nprob != 4) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode lora: v_mode 2 needs the v LoRA");
+  if (v_mode != 0 && !v_first) return fail(RWKV7MI_EINVAL, "wkv7 fp16 decode lora: v_mode needs v_first");
+  DecLora la;
+  if (int rc = dl_build(la, "wkv7 fp16 decode lora", lora_part, nprob, ranks, w_up, b_up, act_down, act_up, D,
+                        lora_splits, B))
+    return rc;
+  hipStream_t st = as_stream(stream);
+  // sums that arrive whole (one split) need one partial load per lane, not a batch
+  if (la.ks == 1)
+    hipLaunchKernelGGL((wkv7_f16_decode_lora_kernel<1>), dim3((unsigned)(B * H)), dim3(256), 0, st,
+                       (const _Float16*)r, (const _Float16*)k_raw, (const _Float16*)v, la, (_Float16*)state,
+                       (const _Float16*)k_k, (const _Float16*)k_a, (const _Float16*)r_k, (const _Float16*)gn_w,
+                       (const _Float16*)gn_b, (const int*)elapsed, (_Float16*)out, (_Float16*)v_first, v_mode,
+                       (int)H, eps);
+  else
+    hipLaunchKernelGGL((wkv7_f16_decode_lora_kernel<DL_ZB>), dim3((unsigned)(B * H)), dim3(256), 0, st,
+                       (const _Float16*)r, (const _Float16*)k_raw, (const _Float16*)v, la, (_Float16*)state,
+                       (const _Float16*)k_k, (const _Float16*)k_a, (const _Float16*)r_k, (const _Float16*)gn_w,
+                       (const _Float16*)gn_b, (const int*)elapsed, (_Float16*)out, (_Float16*)v_first, v_mode,
+                       (int)H, eps);
+  int rc = check_launch("wkv7_f16_decode_lora_kernel");
+  if (rc != RWKV7MI_OK || !advance_elapsed) return rc;
   hipLaunchKernelGGL(wkv7_f16_advance_kernel, dim3((unsigned)((B + 63) / 64)), dim3(64), 0, st, (int*)elapsed,
                      (int)B);
   return check_launch("wkv7_f16_advance_kernel");

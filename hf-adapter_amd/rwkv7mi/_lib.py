@@ -50,6 +50,11 @@ SIGNATURES = {
         _i32,
         [_c_p] * 12 + [_c_p, _i32, _c_p, _c_p, _c_p, _i32, _i64, _i64, _i64, _f32, _c_p],
     ),
+    "rwkv7mi_wkv7_fp16_decode_lora_output_prepare": (
+        _i32,
+        [_c_p] * 4 + [_i64] + [_c_p] * 5 + [_i64, _i64] + [_c_p] * 7 + [_i32, _c_p, _c_p, _i32, _i64, _i64, _i64, _f32,
+                                                                         _c_p],
+    ),
     "rwkv7mi_wkv7_fp16_sequence": (_i32, [_c_p] * 10 + [_i64, _i64, _i64, _i64, _c_p]),
     "rwkv7mi_mm8_pack": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "rwkv7mi_mm8_workspace_bytes": (_sz, [_i64, _i64, _i64]),

@@ -67,7 +67,8 @@ def fused_lora_decode_supported(ranks, rows: int) -> bool:
 
 def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, state, k_k, k_a, r_k,
                                        group_norm_weight, group_norm_bias, *, eps: float, out, state_out=None,
-                                       v_first=None, v_mode: int = 0, down_sums=None, down_splits: int = 1):
+                                       v_first=None, v_mode: int = 0, down_sums=None, down_splits: int = 1,
+                                       elapsed=None, advance_elapsed: bool = False):
     """``fused_wavg_lora`` (rwkv7_hf/fused_lora.py:706) followed by
     ``fused_recurrent_output_prepare_raw`` (fused_recurrent_update.py:1089) in two
     launches: the split-K down projections, then one decode kernel in which each
@@ -80,7 +81,15 @@ def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, stat
     ``lora_downs``, or :func:`fused_decode_norm_mix.attn_mix_lora_decode`): the
     down projections already summed over K, or over ``down_splits`` K-chunks
     (``[problem][split][row][rank]``); ``xs`` and the down launch are then
-    skipped."""
+    skipped.
+
+    An fp16 ``state`` (``[B, H, 64, 64]``, fp16 activations and parameters)
+    runs the fp16-state kernel instead (the reference's fp16 decode,
+    rwkv7_hf/native_jit_decode.py:762-784, with
+    ``native_fp16_recurrent_output_prepare_raw``'s semantics): the state is
+    updated in place (``state_out`` None or ``state`` itself), ``elapsed``
+    (int32 ``[B]``) feeds the decay dither and moves by one when
+    ``advance_elapsed`` is set."""
     k = len(xs)
     rows, D = (int(s) for s in xs[0].shape)
     ranks = [int(d.shape[0]) for d in downs]
@@ -92,7 +101,22 @@ def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, stat
     acts_down = [ACT_TANH, ACT_NONE, ACT_SIGMOID, ACT_NONE][:k]
     acts_up = [ACT_NONE, ACT_SIGMOID, ACT_NONE, ACT_SIGMOID][:k]
     hidden = H * N
-    pdt = k_k.dtype
+    f16 = state.dtype == torch.float16
+    if f16:
+        if not (r.dtype == k_raw.dtype == v.dtype == out.dtype == torch.float16 and int(N) == 64
+                and int(state.shape[3]) == 64 and state.is_contiguous()):
+            raise ValueError("fused LoRA decode on an fp16 state: fp16 activations, contiguous [B,H,64,64] state")
+        if state_out is not None and state_out.data_ptr() != state.data_ptr():
+            raise ValueError("fused LoRA decode on an fp16 state: the state is updated in place")
+        if elapsed is None or not (elapsed.is_cuda and elapsed.dtype == torch.int32 and elapsed.is_contiguous()
+                                   and int(elapsed.numel()) == B):
+            raise ValueError("fused LoRA decode on an fp16 state: elapsed must be contiguous CUDA int32 [B]")
+        if any(u.dtype != torch.float16 for u in ups) or any(
+                b is not None and b.dtype != torch.float16 for b in biases):
+            raise ValueError("fused LoRA decode on an fp16 state: fp16 up weights and biases")
+        if v_mode and (v_first is None or v_first.dtype != torch.float16):
+            raise ValueError("fused LoRA decode on an fp16 state: v_first must be fp16")
+    pdt = torch.float16 if f16 else k_k.dtype
     kk_s, ka, rk, gnw, gnb = (t.reshape(hidden).to(pdt).contiguous()
                               for t in (k_k, k_a, r_k, group_norm_weight, group_norm_bias))
     _lib.require_gpu(r, k_raw, v, *xs, *downs, *ups, state, out, name="fused_wavg_lora_output_prepare_raw")
@@ -109,6 +133,14 @@ def fused_wavg_lora_output_prepare_raw(r, k_raw, v, xs, downs, ups, biases, stat
         splits = 0
         _lib.call("rwkv7mi_lora_down_multi", k, _lib.ptr_array(xs), _lib.ptr_array(downs), rk_arr,
                   (ctypes.c_int * k)(*acts_down), rows, D, _lib.dtype_code(xs[0]), _lib.ptr(ws), int(ws.numel()), s)
+    if f16:
+        _lib.call("rwkv7mi_wkv7_fp16_decode_lora_output_prepare",
+                  _lib.ptr(r), _lib.ptr(k_raw), _lib.ptr(v), _lib.ptr(ws), k, rk_arr, _lib.ptr_array(ups),
+                  _lib.ptr_array(biases), (ctypes.c_int * k)(*acts_down), (ctypes.c_int * k)(*acts_up), D, splits,
+                  _lib.ptr(state), _lib.ptr(kk_s), _lib.ptr(ka), _lib.ptr(rk), _lib.ptr(gnw), _lib.ptr(gnb),
+                  _lib.ptr(elapsed), int(bool(advance_elapsed)), _lib.ptr(out), _lib.ptr(v_first), int(v_mode),
+                  B, H, N, float(eps), s)
+        return out, state
     new_state = state if state_out is None else state_out
     _lib.call("rwkv7mi_wkv7_decode_lora_output_prepare",
               _lib.ptr(r), _lib.ptr(k_raw), _lib.ptr(v), _lib.ptr(ws), k, rk_arr, _lib.ptr_array(ups),

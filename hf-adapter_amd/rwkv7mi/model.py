@@ -1143,9 +1143,12 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
         if bufs is None:
             bufs = self._decode_buffers(B)
         state, xpa, xpf, v_first = cache
-        # an fp16 state takes the unfused route into the fp16-state kernel
+        # an fp16 state runs the fp16-state kernels (with or without the LoRA
+        # up projections inside), which also advance the dither phase
         f16 = state[0].dtype == torch.float16
-        if self._mix_lora_route(B) and not f16:
+        el16 = cache.fp16_elapsed if f16 else None
+        last_i = len(self.layers) - 1
+        if self._mix_lora_route(B):
             return self._decode_mix_lora_(tokens, cache, logits, bufs)
         x = bufs["x"]
         torch.index_select(self.emb, 0, tokens, out=x)
@@ -1165,7 +1168,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                 if L.pre is not None:
                     layer_norm(x, L.pre[0], L.pre[1], eps, out=x)
                 aux = [L.mix[1], L.mix[4], L.mix[5], L.mix[3]][:n]
-                flora = self.fused_lora_decode and not f16 and fused_lora_decode_supported(
+                flora = self.fused_lora_decode and fused_lora_decode_supported(
                     [int(d.shape[0]) for d in L.lora_down], B)
                 mm8_lnmix_multi_into(x, xpa[i], L.ln1[0], L.ln1[1], eps, [L.mix[0], L.mix[2], L.mix[3]],
                                      [L.r_proj.m, L.k_proj.m, L.v_proj.m], [rkv[0], rkv[1], rkv[2]],
@@ -1177,7 +1180,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                                             pre_norm_weight=L.pre[0] if L.pre else None,
                                             pre_norm_bias=L.pre[1] if L.pre else None, residual_parts=parts)
                 parts = None
-            if (self.fused_lora_decode and not self.lora_side_stream and not f16
+            if (self.fused_lora_decode and not self.lora_side_stream
                     and fused_lora_decode_supported([int(d.shape[0]) for d in L.lora_down], B)):
                 # LoRA down (its own split-K launch, or tail workgroups of the
                 # R/K/V launch), then the up projections inside the wkv kernel
@@ -1194,7 +1197,8 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                 fused_wavg_lora_output_prepare_raw(
                     rkv[0], rkv[1], rkv[2], [xw, xa, xg, xv][:n], L.lora_down, L.lora_up, L.lora_bias, state[i],
                     L.k_k, L.k_a, L.r_k, L.gn[0], L.gn[1], eps=N * 1e-5, out=prep, state_out=state[i],
-                    v_first=v_first, v_mode=1 if i == 0 else 2, down_sums=down_sums, down_splits=down_splits)
+                    v_first=v_first, v_mode=1 if i == 0 else 2, down_sums=down_sums, down_splits=down_splits,
+                    elapsed=el16, advance_elapsed=f16 and i == last_i)
             else:
                 if self.lora_side_stream:
                     # the LoRA projections depend only on the mixes: a second stream
@@ -1212,8 +1216,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                                                 (rkv[0], rkv[1], rkv[2]))
                     self._lora(L, xw, xa, xg, xv, B, [lora[q] for q in range(4)], bufs["mids"])
                 if f16:
-                    self._fp16_recurrence(L, rkv, lora, state[i], v_first, prep, cache.fp16_elapsed,
-                                          last=i == len(self.layers) - 1)
+                    self._fp16_recurrence(L, rkv, lora, state[i], v_first, prep, el16, last=i == last_i)
                 else:
                     fused_recurrent_output_prepare_raw(
                         rkv[0], lora[0], rkv[1], rkv[2], lora[1], state[i], lora[2], L.k_k, L.k_a, L.r_k, L.gn[0],
@@ -1289,6 +1292,8 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
         x = bufs["x"]
         torch.index_select(self.emb, 0, tokens, out=x)
         state, xpa, xpf, v_first = cache
+        f16 = state[0].dtype == torch.float16
+        el16 = cache.fp16_elapsed if f16 else None
         mixb, rkv, prep = bufs["mix"], bufs["rkv"], bufs["prep"]
         for L in self.layers:
             i = L.idx
@@ -1308,7 +1313,8 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
             fused_wavg_lora_output_prepare_raw(
                 rkv[0], rkv[1], rkv[2], [xw, xa, xg, xv][:n], L.lora_down, L.lora_up, L.lora_bias, state[i],
                 L.k_k, L.k_a, L.r_k, L.gn[0], L.gn[1], eps=N * 1e-5, out=prep, state_out=state[i],
-                v_first=v_first, v_mode=1 if i == 0 else 2, down_sums=bufs["lpart"], down_splits=splits)
+                v_first=v_first, v_mode=1 if i == 0 else 2, down_sums=bufs["lpart"], down_splits=splits,
+                elapsed=el16, advance_elapsed=f16 and i == len(self.layers) - 1)
             L.o_proj.apply(prep, x, residual=x)
             fused_ffn_add_norm_mix_decode(x, None, xpf[i], L.ln2[0], L.ln2[1], L.fx_k, eps=eps, mixed=bufs["fk"])
             L.key.apply(bufs["fk"], bufs["kf"], act=3)

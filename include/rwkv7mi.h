@@ -181,6 +181,26 @@ int rwkv7mi_wkv7_fp16_decode_output_prepare_raw(
     const void* v_gate, int v_mode, int64_t B, int64_t H, int64_t N, float eps,
     void* stream);
 
+/* The same decode with the W/A/G[/V] LoRA up projections inside the kernel,
+ * as rwkv7mi_wkv7_decode_lora_output_prepare does for an fp32 state: the
+ * down projections' fp32 partials lora_part ([problem][split][B][rank], from
+ * rwkv7mi_lora_down_multi with lora_splits = 0, or whole sums / K-chunk sums
+ * with lora_splits >= 1) are summed and activated per problem, rounded to
+ * fp16, and each (batch, head) workgroup computes its 64 channels of w_raw,
+ * a, g and v_gate, each rounded to fp16, before the fp16-state update above.
+ * B <= 64; ranks multiples of 8 up to 128; v_mode 2 needs nprob 4.
+ * Replaces fused_wavg_lora's up half (rwkv7_hf/fused_lora.py:706) followed by
+ * native_fp16_recurrent_output_prepare_raw (rwkv7_hf/native_wkv_fp16.py:678)
+ * in the reference's fp16 decode (rwkv7_hf/native_jit_decode.py:762-784). */
+int rwkv7mi_wkv7_fp16_decode_lora_output_prepare(
+    const void* r, const void* k_raw, const void* v, const float* lora_part,
+    int64_t nprob, const int64_t* ranks, const void* const* w_up,
+    const void* const* b_up, const int* act_down, const int* act_up, int64_t D,
+    int64_t lora_splits, void* state, const void* k_k, const void* k_a,
+    const void* r_k, const void* gn_w, const void* gn_b, int32_t* elapsed,
+    int advance_elapsed, void* out, void* v_first, int v_mode, int64_t B,
+    int64_t H, int64_t N, float eps, void* stream);
+
 /* T >= 1 tokens of prepared vectors [B,T,H,64]: w raw (plus w0 [H*64] in
  * fp32 when w0 != NULL), neg_kk = -kk, kka = kk*a; out [B,T,H,64] is the raw
  * readout y.  elapsed is read, not advanced.  Inputs and state 16-byte

@@ -98,3 +98,33 @@ def test_fp16_state_prefill_graph_equals_eager():
     for a, b in zip(c_eager._all_tensors(), c_graph._all_tensors()):
         assert torch.equal(a, b)
     assert c_graph.fp16_elapsed.tolist() == [T] * B
+
+
+@pytest.mark.parametrize("B", [1, 4, 16])
+def test_fp16_state_fused_lora_decode_tracks_unfused(B):
+    """The decode with the LoRA up projections inside the fp16-state kernel
+    (the default route) against the route with separate LoRA launches: the
+    LoRA sums run in another order, so logits agree within LOGIT_REL; the
+    dither phase advances once per step on both."""
+    cfg, model, _ = _fp16_model(True, seed=2)
+    rng = np.random.default_rng(17)
+    ids = torch.tensor(rng.integers(0, cfg.vocab_size, (B, 19)), device="cuda")
+    out = model(ids, use_graph=False)
+    c_fused = out.past_key_values
+    c_plain = c_fused.clone()
+    lg_f = torch.empty(B, cfg.vocab_size, device="cuda", dtype=torch.float16)
+    lg_p = torch.empty_like(lg_f)
+    for s in range(4):
+        nxt = torch.tensor(rng.integers(0, cfg.vocab_size, B), device="cuda")
+        model.fused_lora_decode = True
+        model.decode_step_(nxt, c_fused, lg_f)
+        model.fused_lora_decode = False
+        model.decode_step_(nxt, c_plain, lg_p)
+        model.fused_lora_decode = True
+        torch.cuda.synchronize()
+        ref = lg_p.float().cpu().numpy().astype(np.float64)
+        err = np.abs(lg_f.float().cpu().numpy() - ref).max()
+        print(f"PARITY fp16-state fused LoRA decode B={B} step {s}: logits max-abs {err:.3e}, "
+              f"max|logit| {np.abs(ref).max():.3f}", flush=True)
+        assert err <= LOGIT_REL * np.abs(ref).max()
+    assert c_fused.fp16_elapsed.tolist() == c_plain.fp16_elapsed.tolist() == [19 + 4] * B
