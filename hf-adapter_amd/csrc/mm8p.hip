@@ -19,8 +19,14 @@
 // tiles would need 256 and spill).  K advances 64 inputs per step (one 1 KB
 // half of each 2 KB blocked tile):
 //  * every operand of a step goes global -> LDS directly (buffer loads with
-//    the lds flag, no registers) into one of three stages, two steps ahead
-//    of the MFMAs, with one barrier per step;
+//    the lds flag, no registers) into one of three stages; the one barrier
+//    per step sits between its two 32-input sub-steps, after which the next
+//    step's loads have landed and the previous step's stage takes the loads
+//    of the step after next (each step's loads have one step to land);
+//  * the MFMAs never wait on a conversion or an LDS read in line: A operands
+//    are read two M tiles ahead, the second sub-step's B operands are built
+//    between the first sub-step's MFMA groups and the next step's first
+//    sub-step operands between the second's;
 //  * x rows: a row is 128 bytes whose 16-byte chunk c sits at position
 //    c ^ (row % 8), so the 8 lanes of an MFMA A read phase hit 8 different
 //    chunk positions (all 32 banks once);
@@ -167,57 +173,97 @@ __global__ __launch_bounds__(512, 1) void mm8p_kernel(const Mm8pBatch B) {
     const f16x8 c8 = (f16x8){c, c, c, c, c, c, c, c};
     *reinterpret_cast<f16x8*>(vs(tid >> 4) + 2 * MM8P_KS + 8 * j) = c8;
   }
-  // prologue: steps 0 and 1 in flight, step 0 landed before the first barrier
+  const int xsel = 64 * (n < 3 ? n : 3);  // this lane's extra column: ry, my, ones or zeros
+  // The lane's raw B bytes of step s (4 column groups, 16 bytes each) and the
+  // B operands of one sub-step h built from them (the lane's 8 inputs
+  // 16 kg + 8 h .. +7 of the step).
+  auto ldb = [&](int s, u32x4 (&braw)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) braw[q] = bs(s % MM8P_NST)[64 * (4 * wn + q) + lane];
+  };
+  auto ry_of = [&](int s, int h) {
+    return *reinterpret_cast<const f16x8*>(vs(s % MM8P_NST) + 16 * kg + 8 * h);
+  };
+
+  // prologue: steps 0 and 1 in flight, step 0 landed before the first
+  // barrier, its sub-step 0 B operands built
   issue(0);
   issue(1);
   wait_one_step();
   __syncthreads();
+  u32x4 braw[4];
+  f16x8 bv0[4], bv1[4];
+  ldb(0, braw);
+  {
+    const f16x8 ry0 = ry_of(0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv0[q] = mm8p_b_operand(braw[q][0], braw[q][1], ry0);
+  }
 
-  const int xsel = 64 * (n < 3 ? n : 3);  // this lane's extra column: ry, my, ones or zeros
+  // Step s: sub-step 0's MFMAs (sub-step 1's B operands built between them),
+  // then the barrier after which step s + 1 has landed and step s - 1's stage
+  // is free, the loads of step s + 2 into it, and sub-step 1's MFMAs with step
+  // s + 1's raw B reads and sub-step 0 conversions between them.  Step s + 1's
+  // loads are in flight from the middle of step s - 1 to the middle of step s.
   for (int s = 0; s < nsteps; ++s) {
-    issue(s + 2);  // into the stage step s - 1 used (every wave is past it: the last barrier)
     const int st = s % MM8P_NST;
     const _Float16* xb = xs(st);
     const _Float16* vb = vs(st);
-    u32x4 braw[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) braw[q] = bs(st)[64 * (4 * wn + q) + lane];
-    // B operands of sub-step h (the lane's 8 inputs 16 kg + 8 h .. +7 of the
-    // step); sub-step 1's are converted while sub-step 0's MFMAs run
-    auto convert = [&](int h, f16x8 (&bv)[4]) {
-      const f16x8 ry8 = *reinterpret_cast<const f16x8*>(vb + 16 * kg + 8 * h);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) bv[q] = mm8p_b_operand(braw[q][2 * h], braw[q][2 * h + 1], ry8);
-    };
-    auto mfmas = [&](int h, const f16x8 (&bv)[4]) {
+    // A operands of sub-step h: reads 0..7 are the wave's eight M tiles, 8 and
+    // 9 its two extra-column tiles (M tiles 2wn, 2wn + 1, read again)
+    auto lda = [&](int h, int i) {
       const int ka = 8 * ((2 * kg + h) ^ (n & 7));  // swizzled chunk of A row (... + n): row % 8 = n % 8
+      const int mt = i < 8 ? i : 2 * wn + (i - 8);
+      return *reinterpret_cast<const f16x8*>(xb + (128 * wm + 16 * mt + n) * MM8P_XS + ka);
+    };
+    // the sub-step's ten A reads run two ahead of the MFMAs that use them
+    // (the read of tile i + 2 is issued before tile i's MFMAs, so its LDS
+    // latency hides behind two tiles' MFMAs); `between(i)` runs after tile
+    // i's MFMAs
+    auto mfmas = [&](int h, const f16x8 (&bv)[4], auto&& between) {
       const f16x8 bx = *reinterpret_cast<const f16x8*>(vb + xsel + 16 * kg + 8 * h);
+      f16x8 a = lda(h, 0), an = lda(h, 1);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(xb + (128 * wm + 16 * i + n) * MM8P_XS + ka);
+      for (int i = 0; i < 10; ++i) {
+        f16x8 ann = an;
+        if (i < 8) ann = lda(h, i + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < 8) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[i][q] = mfma16x16x32(a, bv[q], acc[i][q]);
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(xb + (128 * wm + 16 * (2 * wn + j) + n) * MM8P_XS + ka);
-        ex[j] = mfma16x16x32(a, bx, ex[j]);
+          for (int q = 0; q < 4; ++q) acc[i][q] = mfma16x16x32(a, bv[q], acc[i][q]);
+        } else {
+          ex[i - 8] = mfma16x16x32(a, bx, ex[i - 8]);
+        }
+        between(i);
+        __builtin_amdgcn_sched_barrier(0);
+        a = an;
+        an = ann;
       }
     };
-    f16x8 bv0[4], bv1[4];
-    convert(0, bv0);
-    mfmas(0, bv0);
-    convert(1, bv1);
-    // interleave: sub-step 1's conversions between sub-step 0's MFMA groups
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read (an A operand)
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // its MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU (conversions)
-    }
-    mfmas(1, bv1);
-    wait_one_step();  // step s + 1 has landed (step s + 2 may still be in flight)
+    const f16x8 ry1 = ry_of(s, 1);
+    mfmas(0, bv0, [&](int i) {
+      if (i < 4) {
+        bv1[i] = mm8p_b_operand(braw[i][2], braw[i][3], ry1);
+        // keep the conversion here, between the MFMAs (the compiler would
+        // otherwise sink it past the barrier to its first use)
+        asm volatile("" : "+v"(bv1[i]));
+      }
+    });
+    // vmcnt(0): this wave's loads of step s + 1 have landed (step s + 2 is not
+    // issued yet); the barrier makes every wave's loads visible and puts every
+    // wave past step s - 1's reads
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
+    issue(s + 2);
+    f16x8 ry0;
+    mfmas(1, bv1, [&](int i) {
+      if (i == 0) {
+        ldb(s + 1, braw);
+        ry0 = ry_of(s + 1, 0);
+      } else if (i >= 2 && i < 6) {
+        bv0[i - 2] = mm8p_b_operand(braw[i - 2][0], braw[i - 2][1], ry0);
+      }
+    });
   }
 
   // ---- the extra columns -> LDS row sums (reusing stage 0)
