@@ -7,12 +7,14 @@
 //          (rwkv7_hf/fused_decode_norm_mix.py:161-293, torch form :203-241)
 //   ffn:   x = residual (+ attn_out);  h = LN(x);  out = h + (prev - h) * mix;  prev <- h
 //          (rwkv7_hf/fused_decode_norm_mix.py:296-348)
-// Sequence ([B,T,D]; one workgroup per (b,t), which also normalises token t-1
-// so no intermediate buffer is needed; the carried previous row is read from
-// prev_in and token T-1's LN is written to prev_out):
+// Sequence ([B,T,D]; one workgroup per run of consecutive tokens, each
+// normalised once, the first run's shift input read from prev_in and token
+// T-1's LN written to prev_out; no intermediate buffer):
 //   (rwkv7_hf/fused_time_mix.py:413-515, torch form native_jit_prefill.py:533-540, :955-961)
 // All statistics in fp32 (two-pass variance), biased variance as F.layer_norm.
+#include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "common.h"
 
@@ -54,7 +56,8 @@ __device__ __forceinline__ void st_slots(T* row, int D, const float (&v)[MIX_SLO
 }
 
 // In-place LayerNorm of the slots (two-pass fp32 statistics, biased variance);
-// w/b are the already loaded weight and bias slots.
+// w/b are the already loaded weight and bias slots.  The fused multiply-adds
+// are written out, so every kernel that normalises a row gets the same bits.
 __device__ __forceinline__ void ln_slots(float (&v)[MIX_SLOTS][MIX_VEC], int D, const float (&w)[MIX_SLOTS][MIX_VEC],
                                          const float (&b)[MIX_SLOTS][MIX_VEC], float eps, float* red) {
   float s1 = 0.f;
@@ -70,13 +73,13 @@ __device__ __forceinline__ void ln_slots(float (&v)[MIX_SLOTS][MIX_VEC], int D, 
 #pragma unroll
       for (int e = 0; e < MIX_VEC; ++e) {
         const float c = v[s][e] - mean;
-        s2 += c * c;
+        s2 = fmaf(c, c, s2);
       }
   const float inv = rsqrtf(block_sum(s2, red) / (float)D + eps);
 #pragma unroll
   for (int s = 0; s < MIX_SLOTS; ++s)
 #pragma unroll
-    for (int e = 0; e < MIX_VEC; ++e) v[s][e] = (v[s][e] - mean) * inv * w[s][e] + b[s][e];
+    for (int e = 0; e < MIX_VEC; ++e) v[s][e] = fmaf((v[s][e] - mean) * inv, w[s][e], b[s][e]);
 }
 
 struct Mix6 {
@@ -524,50 +527,114 @@ __global__ __launch_bounds__(256) void attn_mix_lora_kernel(
   }
 }
 
-// Sequence form: workgroup (b, t) normalises x[b,t] and x[b,t-1] (or takes prev_in[b]).
-template <typename TA, typename TP>
-__global__ __launch_bounds__(MIX_THREADS) void seq_norm_mix_kernel(
+// Sequence norm-mix: one workgroup per run of `run` consecutive tokens of one
+// sequence (1..16, chosen so that long prompts get 16 and short ones still
+// fill the GPU).  The LayerNorm and mixing parameters are loaded once per run;
+// each token is normalised once by the loop below and its normalised row
+// carried in registers as the next token's shift input; a run after the first
+// starts one token early (its lead-in is normalised by the same loop code, so
+// every run length gives the same bits); the next row's loads are in flight
+// while a row is reduced.  NS = slots in use (D <= 2048 NS).
+constexpr int SEQ_ROWS = 16;
+
+template <int NS, typename T>
+__device__ __forceinline__ void ld_ns(const T* row, int D, float (&v)[NS][MIX_VEC], bool active = true) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(row, active ? (uint32_t)(D * sizeof(T)) : 0u);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) buf_ld8(r, (uint32_t)mix_base(s), active && mix_base(s) < D, (const T*)nullptr, v[s]);
+}
+
+template <int NS>
+__device__ __forceinline__ void ln_ns(float (&v)[NS][MIX_VEC], int D, const float (&w)[NS][MIX_VEC],
+                                      const float (&b)[NS][MIX_VEC], float eps, float* red) {
+  float s1 = 0.f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int e = 0; e < MIX_VEC; ++e) s1 += v[s][e];
+  const float mean = block_sum(s1, red) / (float)D;
+  float s2 = 0.f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    if (mix_base(s) < D)
+#pragma unroll
+      for (int e = 0; e < MIX_VEC; ++e) {
+        const float c = v[s][e] - mean;
+        s2 = fmaf(c, c, s2);
+      }
+  const float inv = rsqrtf(block_sum(s2, red) / (float)D + eps);
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int e = 0; e < MIX_VEC; ++e) v[s][e] = fmaf((v[s][e] - mean) * inv, w[s][e], b[s][e]);
+}
+
+template <typename TA, typename TP, int NS>
+__global__ __launch_bounds__(MIX_THREADS) void seq_norm_mix_rows_kernel(
     const TA* __restrict__ x, const TA* __restrict__ prev_in, TA* __restrict__ prev_out,
-    const TP* __restrict__ ln_w, const TP* __restrict__ ln_b, Mix6 m, int T, int D, int nmix,
-    float eps) {
+    const TP* __restrict__ ln_w, const TP* __restrict__ ln_b, Mix6 m, int T, int D, int nmix, int run, float eps) {
   __shared__ float red[4];
-  const int b = blockIdx.x / T;
-  const int t = blockIdx.x % T;
-  const int64_t row = (int64_t)b * T + t;
-  float v[MIX_SLOTS][MIX_VEC], pv[MIX_SLOTS][MIX_VEC], w[MIX_SLOTS][MIX_VEC], bb[MIX_SLOTS][MIX_VEC];
-  float mx[6][MIX_SLOTS][MIX_VEC];
-  // ln_w == null: x is already normalised (the reference's calling convention,
-  // rwkv7_hf/fused_time_mix.py:413-515) and is mixed as given
+  const int runs = (T + run - 1) / run;
+  const int b = blockIdx.x / runs;
+  const int t0 = (blockIdx.x % runs) * run;
+  const int t1 = min(T, t0 + run);
   const bool norm = ln_w != nullptr;
-  ld_slots(x + row * D, D, v);
-  ld_slots(t > 0 ? x + (row - 1) * D : prev_in + (int64_t)b * D, D, pv);
+  float w[NS][MIX_VEC], bb[NS][MIX_VEC], v[NS][MIX_VEC], pv[NS][MIX_VEC];
+  Raw8<TP> mx[6][NS];  // the mixes as loaded (two per register for 16-bit types)
+  const int64_t rb = (int64_t)b * T;
+  // a run after the first starts one token early: that token is normalised by
+  // the same loop code as every other row (and as the run before it did) and
+  // only becomes the shift input of the run's first token
+  int t = t0 > 0 ? t0 - 1 : t0;
+  ld_ns<NS>(prev_in + (int64_t)b * D, D, pv, t0 == 0);
+  ld_ns<NS>(x + (rb + t) * D, D, v);
   if (norm) {
-    ld_slots(ln_w, D, w);
-    ld_slots(ln_b, D, bb);
+    ld_ns<NS>(ln_w, D, w);
+    ld_ns<NS>(ln_b, D, bb);
   }
-#pragma unroll
-  for (int i = 0; i < 6; ++i) ld_slots(reinterpret_cast<const TP*>(m.mix[i]), D, mx[i], i < nmix);
-  if (norm) {
-    ln_slots(v, D, w, bb, eps, red);
-    if (t > 0) {
-      ln_slots(pv, D, w, bb, eps, red);
-#pragma unroll
-      for (int s = 0; s < MIX_SLOTS; ++s) round8<TA>(pv[s]);
-    }
-  }
-  if (t == T - 1) st_slots(prev_out + (int64_t)b * D, D, v);
-#pragma unroll
-  for (int s = 0; s < MIX_SLOTS; ++s) round8<TA>(v[s]);  // the reference keeps h in TA before mixing
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
-    if (i < nmix) {
-      float o[MIX_SLOTS][MIX_VEC];
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(m.mix[i], i < nmix ? (uint32_t)(D * sizeof(TP)) : 0u);
 #pragma unroll
-      for (int s = 0; s < MIX_SLOTS; ++s)
+    for (int s = 0; s < NS; ++s) mx[i][s] = raw8<TP>(r, mix_base(s), i < nmix && mix_base(s) < D);
+  }
+  for (; t < t1; ++t) {
+    float nx[NS][MIX_VEC];
+    ld_ns<NS>(x + (rb + t + 1) * D, D, nx, t + 1 < t1);  // the next row, in flight during this one
+    if (norm) ln_ns<NS>(v, D, w, bb, eps, red);
 #pragma unroll
-        for (int e = 0; e < MIX_VEC; ++e) o[s][e] = v[s][e] + (pv[s][e] - v[s][e]) * mx[i][s][e];
-      st_slots(reinterpret_cast<TA*>(m.out[i]) + row * D, D, o);
+    for (int s = 0; s < NS; ++s) round8<TA>(v[s]);  // the reference keeps h in TA before mixing
+    if (t >= t0) {  // the lead-in token of a run writes nothing
+      if (t == T - 1)
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          if (mix_base(s) < D) st8(prev_out + (int64_t)b * D + mix_base(s), v[s]);
+#pragma unroll
+      for (int i = 0; i < 6; ++i) {
+        if (i < nmix) {
+          TA* orow = reinterpret_cast<TA*>(m.out[i]) + (rb + t) * D;
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            if (mix_base(s) < D) {
+              float mf[MIX_VEC], o[MIX_VEC];
+              // converted per row (kept packed across the loop, not hoisted)
+              asm volatile("" : "+v"(mx[i][s].u[0]));
+              unraw8<TP>(mx[i][s], mf);
+#pragma unroll
+              for (int e = 0; e < MIX_VEC; ++e) o[e] = fmaf(pv[s][e] - v[s][e], mf[e], v[s][e]);
+              st8(orow + mix_base(s), o);
+            }
+          }
+        }
+      }
     }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int e = 0; e < MIX_VEC; ++e) {
+        pv[s][e] = v[s][e];
+        v[s][e] = nx[s][e];
+      }
   }
 }
 
@@ -757,10 +824,21 @@ extern "C" int rwkv7mi_seq_norm_mix(const void* x, const void* prev_in, void* pr
     using TA = decltype(ta);
     return dispatch_dtype(param_dtype, [&](auto tp) {
       using TP = decltype(tp);
-      hipLaunchKernelGGL((seq_norm_mix_kernel<TA, TP>), dim3((unsigned)(B * T)), dim3(MIX_THREADS), 0,
-                         as_stream(stream), (const TA*)x, (const TA*)prev_in, (TA*)prev_out, (const TP*)ln_w,
-                         (const TP*)ln_b, m, (int)T, (int)D, (int)nmix, eps);
-      return check_launch("seq_norm_mix_kernel");
+      // tokens per workgroup: 16 from 16k tokens, fewer below (at least ~1k workgroups)
+      const int run = (int)std::min<int64_t>(SEQ_ROWS, std::max<int64_t>(1, B * T / 1024));
+      const unsigned grid = (unsigned)(B * ((T + run - 1) / run));
+      auto go = [&](auto ns) {
+        constexpr int NS = decltype(ns)::value;
+        hipLaunchKernelGGL((seq_norm_mix_rows_kernel<TA, TP, NS>), dim3(grid), dim3(MIX_THREADS), 0,
+                           as_stream(stream), (const TA*)x, (const TA*)prev_in, (TA*)prev_out, (const TP*)ln_w,
+                           (const TP*)ln_b, m, (int)T, (int)D, (int)nmix, run, eps);
+        return check_launch("seq_norm_mix_rows_kernel");
+      };
+      const int64_t ns = (D + MIX_THREADS * MIX_VEC - 1) / (MIX_THREADS * MIX_VEC);
+      if (ns == 1) return go(std::integral_constant<int, 1>{});
+      if (ns == 2) return go(std::integral_constant<int, 2>{});
+      if (ns == 3) return go(std::integral_constant<int, 3>{});
+      return go(std::integral_constant<int, 4>{});
     });
   });
 }

@@ -175,6 +175,39 @@ def test_sequence_shift_mix(oracle, B, T, D):
     _ok(last_f, ref_last)
 
 
+@pytest.mark.parametrize("D,dt,norm", [(768, torch.float16, True), (4096, torch.float16, True),
+                                       (4096, torch.bfloat16, False), (5000, torch.float32, True),
+                                       (8192, torch.float16, True)])
+def test_sequence_shift_mix_runs_equal_one_token_calls(D, dt, norm):
+    """A sequence call runs several tokens per workgroup (8 here: B*T/1024),
+    each token normalised once and carried to the next as its shift input; the
+    same tokens fed one per call (one token per workgroup, the shift state
+    threaded between the calls) give the same bits, for six mixes and one."""
+    from rwkv7mi.fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
+
+    rng = np.random.default_rng(D + int(norm))
+    B, T = 100, 83
+    x = torch.tensor(rng.standard_normal((B, T, D)), dtype=dt, device="cuda")
+    prev = torch.tensor(rng.standard_normal((B, D)), dtype=dt, device="cuda")
+    w = torch.tensor(1 + 0.1 * rng.standard_normal(D), dtype=dt, device="cuda") if norm else None
+    b = torch.tensor(0.1 * rng.standard_normal(D), dtype=dt, device="cuda") if norm else None
+    mixes = [torch.tensor(rng.random(D), dtype=dt, device="cuda") for _ in range(6)]
+    *whole, last = fused_attn_sequence_shift_mix(x, prev, *mixes, norm_weight=w, norm_bias=b)
+    fk, last_f = fused_ffn_sequence_shift_mix(x, prev, mixes[0], norm_weight=w, norm_bias=b)
+    parts, pk, p6, p1 = [], [], prev, prev
+    for t in range(T):
+        xc = x[:, t:t + 1].contiguous()
+        *o, p6 = fused_attn_sequence_shift_mix(xc, p6, *mixes, norm_weight=w, norm_bias=b)
+        k, p1 = fused_ffn_sequence_shift_mix(xc, p1, mixes[0], norm_weight=w, norm_bias=b)
+        parts.append(o)
+        pk.append(k)
+    torch.cuda.synchronize()
+    for i in range(6):
+        assert torch.equal(whole[i], torch.cat([p[i] for p in parts], 1)), i
+    assert torch.equal(fk, torch.cat(pk, 1))
+    assert torch.equal(last, p6) and torch.equal(last_f, p1)
+
+
 # rows above 256 take the fused many-row kernel (prefills)
 @pytest.mark.parametrize("rows,D", [(1, 4096), (8, 2048), (40, 768), (64, 4096), (100, 2048), (300, 256),
                                     (257, 512), (1000, 4096)])
