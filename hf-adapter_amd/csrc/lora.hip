@@ -392,6 +392,8 @@ static int lora_run(bool up, int64_t nprob, const void* const* xs, const void* c
     if (rows * std::max(D, A) * (int64_t)esz > INT32_MAX || A * LORA_MAXR * (int64_t)esz > INT32_MAX)
       return fail(RWKV7MI_EINVAL, "lora_multi: too large");
     const int rt = (rmax + 15) / 16;
+    // fp16 with ranks that are multiples of 32: weights shared through LDS, 256 rows per workgroup
+    if (act_dtype == RWKV7MI_F16 && lora_seq_supported(batch, rows)) return lora_seq_run(batch, rows, stream);
     return dispatch_dtype(act_dtype, [&](auto ta) {
       using TA = decltype(ta);
       // two row tiles per wave (each weight operand feeds two MFMAs); one for

@@ -25,6 +25,10 @@ struct LoraBatch {
   int tpw;  // up kernel: output tiles of 16 columns per workgroup
 };
 
+// Many-row fp16 form (lora_seq.hip): whether it takes these shapes, and its launch.
+bool lora_seq_supported(const LoraBatch& b, int64_t rows);
+int lora_seq_run(const LoraBatch& b, int64_t rows, void* stream);
+
 __device__ __forceinline__ float lora_act(float v, int act) {
   if (act == LORA_ACT_TANH) return tanhf(v);
   if (act == LORA_ACT_SIGMOID) return 1.0f / (1.0f + expf(-v));

@@ -209,15 +209,21 @@ def test_sequence_shift_mix_runs_equal_one_token_calls(D, dt, norm):
 
 
 # rows above 256 take the fused many-row kernel (prefills)
-@pytest.mark.parametrize("rows,D", [(1, 4096), (8, 2048), (40, 768), (64, 4096), (100, 2048), (300, 256),
-                                    (257, 512), (1000, 4096)])
-def test_wavg_lora(oracle, rows, D):
+@pytest.mark.parametrize("rows,D,ranks", [(1, 4096, (64, 64, 128, 32)), (8, 2048, (64, 64, 128, 32)),
+                                          (40, 768, (64, 64, 128, 32)), (64, 4096, (64, 64, 128, 32)),
+                                          (100, 2048, (64, 64, 128, 32)), (300, 256, (64, 64, 128, 32)),
+                                          (257, 512, (64, 64, 128, 32)), (1000, 4096, (64, 64, 128, 32)),
+                                          (513, 768, (96, 32, 64, 128)), (700, 320, (64, 48, 128, 32))])
+def test_wavg_lora(oracle, rows, D, ranks):
+    """fp16 W/A/G/V LoRA against the fp64 oracle: decode sizes (split-K down,
+    up kernel), and above 256 rows the many-row kernels (ranks that are
+    multiples of 32 with D a multiple of 64: the LDS-shared form; the last case
+    the per-row-tile form)."""
     from rwkv7mi.fused_lora import fused_wavg_lora
 
     rng = np.random.default_rng(rows + D)
     A = D
     xs = [_t(rng.standard_normal((rows, D))) for _ in range(4)]
-    ranks = (64, 64, 128, 32)
     downs = [_t(rng.standard_normal((r, D)) * 0.02) for r in ranks]
     ups = [_t(rng.standard_normal((A, r)) * 0.1) for r in ranks]
     biases = [_t(rng.standard_normal(A) * 0.01), _t(rng.standard_normal(A) * 0.01), None,
