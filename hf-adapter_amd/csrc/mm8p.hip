@@ -33,7 +33,8 @@
 //  * the MM8 bytes: the step's 1 KB half of each of the tile's 16 column
 //    groups, as stored (a lane's 16 bytes are the B operands of two
 //    consecutive MFMAs), loaded once per workgroup for both row halves;
-//  * ry and my of the step's inputs, followed by 64 ones and 64 zeros, so
+//  * ry and my of the step's inputs, followed by 64 ones and 64 zeros (rows
+//    of 144 bytes, so the four a read touches lie on different banks), so
 //    the extra columns' B operand is one LDS read per lane (column 0 reads
 //    ry, 1 my, 2 ones, the rest zeros).
 // Wave (wm, wn) also computes the extra columns for its M tiles 2wn, 2wn+1
@@ -51,7 +52,9 @@ constexpr int MM8P_M = 256, MM8P_N = 256, MM8P_KS = 64;
 constexpr int MM8P_XS = MM8P_KS;                        // LDS row (halfs): 128 bytes, 16-byte chunks XOR-swizzled
 constexpr int MM8P_ABYTES = MM8P_M * MM8P_XS * 2;       // x rows of one step (32 KB)
 constexpr int MM8P_BBYTES = 16 * 1024;                  // MM8 bytes of one step: 16 column groups x 1 KB
-constexpr int MM8P_VBYTES = 4 * MM8P_KS * 2;            // ry, my of one step, then ones, zeros (fp16)
+constexpr int MM8P_VROW = MM8P_KS + 8;                  // v rows (halfs): 144 bytes, so the four rows the
+                                                        // extra-column read touches sit on different banks
+constexpr int MM8P_VBYTES = 4 * MM8P_VROW * 2;          // ry, my of one step, then ones, zeros (fp16)
 constexpr int MM8P_STAGE = MM8P_ABYTES + MM8P_BBYTES + MM8P_VBYTES;
 constexpr int MM8P_NST = 3;                             // pipeline stages (two steps of loads in flight)
 constexpr int MM8P_LDS = MM8P_NST * MM8P_STAGE;
@@ -141,13 +144,11 @@ __global__ __launch_bounds__(512, 1) void mm8p_kernel(const Mm8pBatch B) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wdma[q], (lds_ptr)(bs(st) + 64 * (2 * wave + q)), 16, boff, 0, 0, 0);
-    if (wave == 0 && lane < 16) {
-      const int k = s * MM8P_KS + 8 * (lane & 7);
+    if (wave == 0 && lane < 8) {
+      const int k = s * MM8P_KS + 8 * lane;
       const int off = k < I ? k * 2 : (int)MM8T_OOB;
-      if (lane < 8)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ryr, (lds_ptr)vs(st), 16, off, 0, 0, 0);
-      else
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(myr, (lds_ptr)vs(st), 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ryr, (lds_ptr)vs(st), 16, off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(myr, (lds_ptr)(vs(st) + MM8P_VROW), 16, off, 0, 0, 0);
     }
   };
   // wait until only the newest step's loads may be pending (s_waitcnt
@@ -166,14 +167,14 @@ __global__ __launch_bounds__(512, 1) void mm8p_kernel(const Mm8pBatch B) {
     for (int q = 0; q < 4; ++q) acc[i][q] = (f32x4){0.f, 0.f, 0.f, 0.f};
   f32x4 ex[2] = {(f32x4){0.f, 0.f, 0.f, 0.f}, (f32x4){0.f, 0.f, 0.f, 0.f}};
 
-  // constant tails of the v part of every stage: 64 ones, 64 zeros
+  // constant rows of the v part of every stage: 64 ones, 64 zeros
   if (tid < 16 * MM8P_NST) {  // stage tid / 16, 8-half run j = tid % 16 (runs 0..7 ones, 8..15 zeros)
     const int j = tid & 15;
     const _Float16 c = j < 8 ? (_Float16)1.0f : (_Float16)0.0f;
     const f16x8 c8 = (f16x8){c, c, c, c, c, c, c, c};
-    *reinterpret_cast<f16x8*>(vs(tid >> 4) + 2 * MM8P_KS + 8 * j) = c8;
+    *reinterpret_cast<f16x8*>(vs(tid >> 4) + (2 + (j >> 3)) * MM8P_VROW + 8 * (j & 7)) = c8;
   }
-  const int xsel = 64 * (n < 3 ? n : 3);  // this lane's extra column: ry, my, ones or zeros
+  const int xsel = MM8P_VROW * (n < 3 ? n : 3);  // this lane's extra column: ry, my, ones or zeros
   // The lane's raw B bytes of step s (4 column groups, 16 bytes each) and the
   // B operands of one sub-step h built from them (the lane's 8 inputs
   // 16 kg + 8 h .. +7 of the step).
