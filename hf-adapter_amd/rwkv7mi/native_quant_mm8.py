@@ -357,14 +357,15 @@ _PREFILL_MAX_BYTES = (1 << 31) - 1
 
 def mm8_gemm_prefill_multi_into(xs, mods, outs, *, residuals=None, epilogues=None):
     """Prefill form (more than ``GEMM_ROWS`` rows) of :func:`mm8_matmul_multi_into`:
-    up to four blocked ``MM8Linear`` products of one shape on the 256 x 256
-    MFMA GEMM that dequantises the MM8 bytes in registers, the route
-    ``mm8_matmul_triton`` takes by materialising the dequantised weight for
-    rows above ``fused_max_rows`` (rwkv7_hf/native_quant_mm8.py:468-507) and
+    up to four blocked ``MM8Linear`` products of one shape, the route
+    ``mm8_matmul_triton`` takes for rows above ``fused_max_rows``
+    (rwkv7_hf/native_quant_mm8.py:468-507): the fp16 dequantised weight is
+    materialised (into the device's ``"mm8p"`` workspace slot, in MFMA operand
+    order) and one fp16 MFMA GEMM with the epilogue fused runs over it, as in
     the prefill projections of rwkv7_hf/native_jit_prefill.py:542-631,
     955-1013.  fp16 activations with fp16 metadata; other dtypes run the
-    64-row tile GEMM over 256-row chunks (also without a dequantised weight).
-    No workspace."""
+    64-row tile GEMM over 256-row chunks (without a dequantised weight).
+    Reserve the workspace (one eager call) before capturing a graph."""
     k = len(mods)
     if not 1 <= k <= 4 or len(xs) != k or len(outs) != k:
         raise ValueError("mm8_gemm_prefill_multi_into: 1..4 problems")
@@ -394,11 +395,13 @@ def mm8_gemm_prefill_multi_into(xs, mods, outs, *, residuals=None, epilogues=Non
             else:
                 mm8_matmul_multi_into(xc, mods, oc, residuals=rc, epilogues=epilogues)
             continue
+        need = int(_lib.load().rwkv7mi_mm8t_gemm_prefill_ws_bytes(k, n, m))
+        ws = _ws.reserve(xs[0].device, need, "mm8p")
         _lib.call(
-            "rwkv7mi_mm8t_gemm_prefill", k, arr(xc), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
+            "rwkv7mi_mm8t_gemm_prefill_ws", k, arr(xc), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
             arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),
             arr([md.bias for md in mods]), arr(rc), arr(oc), eps, r1 - r0, n, m, _lib.F16, _lib.F16,
-            _lib.stream_of(xs[0]),
+            _lib.ptr(ws), need, _lib.stream_of(xs[0]),
         )
     return outs
 

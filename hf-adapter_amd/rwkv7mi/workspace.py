@@ -6,7 +6,8 @@ so one zero-initialised buffer per device can be reused by every call issued
 on one stream.  Slot ``"mm8t"`` holds the blocked GEMV's split-K partials
 (written before they are read).  Slot ``"mm8g"`` holds the many-row MM8 GEMM's x', row sums and
 split partials (each call writes them before reading).  Slot ``"lora"`` holds
-the LoRA kernels' fp32 partials.  Slots never share memory, so one kernel
+the LoRA kernels' fp32 partials.  Slot ``"mm8p"`` holds the prefill GEMM's
+fp16 dequantised weights (each call writes them before reading).  Slots never share memory, so one kernel
 family cannot disturb another's counters.  Calls that run concurrently on
 different streams of the same device must not share a slot (the decode step
 issues all of them on one stream).

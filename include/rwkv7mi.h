@@ -419,6 +419,31 @@ int rwkv7mi_mm8t_gemm_prefill(int nprob, const void* const* x,
                               int64_t O, int act_dtype, int meta_dtype,
                               void* stream);
 
+/* Workspace bytes rwkv7mi_mm8t_gemm_prefill_ws needs for nprob problems of
+ * in_features I, out_features O: nprob * ceil(O / 16) * ceil(I / 64) * 2048
+ * (each problem's fp16 dequantised weight); 0 for a bad shape. */
+int64_t rwkv7mi_mm8t_gemm_prefill_ws_bytes(int nprob, int64_t I, int64_t O);
+
+/* The prefill GEMM as the reference computes it, the faster form on gfx950:
+ * the fp16 dequantised weight W_hat = fp16((w + 0.5) ry rx + my + mx) (the
+ * bytes rwkv7mi_mm8_dequant writes) is materialised into the workspace in
+ * MFMA operand order, then y = epilogue(x @ W_hat (+ bias)) runs on 256 x
+ * 256 fp16 MFMA tiles.  Same arguments as rwkv7mi_mm8t_gemm_prefill plus the
+ * workspace (16-byte aligned, at least rwkv7mi_mm8t_gemm_prefill_ws_bytes;
+ * its contents are overwritten).  Replaces mm8_matmul_triton's route for
+ * rows > fused_max_rows, dequantize_mm8 then x @ W_hat
+ * (rwkv7_hf/native_quant_mm8.py:468-507, :100-119), used by the prefill
+ * projections (rwkv7_hf/native_jit_prefill.py:542-631, 955-1013). */
+int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x,
+                                 const uint8_t* const* w_blk,
+                                 const void* const* mx, const void* const* rx,
+                                 const void* const* my, const void* const* ry,
+                                 const void* const* bias,
+                                 const void* const* residual, void* const* y,
+                                 const int* epilogue, int64_t rows, int64_t I,
+                                 int64_t O, int act_dtype, int meta_dtype,
+                                 void* ws, int64_t ws_bytes, void* stream);
+
 /* Allocation-free form of rwkv7mi_mm8t_gemm_multi (same arguments and results,
  * no workspace argument).  No counterpart in the reference: it is for callers
  * that cannot allocate (code under hipGraph capture, tight serving loops,

@@ -1,8 +1,10 @@
-"""GPU parity of the prefill MM8 GEMM (more than 256 rows over blocked
-weights, the weight never materialised): against the fp64 oracle on the
-dequantised weights for ragged rows / columns and in_features that end
-mid-tile, grouped launches, bias / relu^2 / residual epilogues, the
-non-fp16 chunked route, and the module routes that take it."""
+"""GPU parity of the prefill MM8 GEMMs (more than 256 rows over blocked
+weights): the route that materialises the fp16 dequantised weight in MFMA
+operand order (its workspace bit-equal to rwkv7mi_mm8_dequant) and the
+in-register dequantising entry, against the fp64 oracle on the dequantised
+weights for ragged rows / columns and in_features that end mid-tile, grouped
+launches, bias / relu^2 / residual epilogues, the non-fp16 chunked route, and
+the module routes that take it."""
 from __future__ import annotations
 
 import types
@@ -131,9 +133,65 @@ def test_mm8p_module_routes(oracle):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("IO", [(4096, 4096), (144, 40), (2064, 520), (80, 16)])
+def test_mm8p_workspace_is_the_dequantised_weight(IO):
+    """The workspace the prefill GEMM reads holds rwkv7mi_mm8_dequant's fp16
+    weight bit for bit: record (group g, step sb, sub-step h, lane n + 16 kg,
+    j) is W_hat[64 sb + 16 kg + 8 h + j, 16 g + n], zero past I or O."""
+    from rwkv7mi import _lib
+    from rwkv7mi import workspace as _ws
+    from rwkv7mi.native_quant_mm8 import dequantize_mm8, mm8_gemm_prefill_multi_into, mm8_unblock
+
+    I, O = IO
+    rng = np.random.default_rng(7 * I + O)
+    mod = _packed(rng, I, O)
+    x = _cuda(rng.standard_normal((300, I)), torch.float16)
+    y = torch.empty((300, O), device="cuda", dtype=torch.float16)
+    print(f"mm8p workspace: I={I} O={O}", flush=True)
+    mm8_gemm_prefill_multi_into([x], [mod], [y])
+    need = int(_lib.load().rwkv7mi_mm8t_gemm_prefill_ws_bytes(1, I, O))
+    G, SB = (O + 15) // 16, (I + 63) // 64
+    assert need == G * SB * 2048
+    ws = _ws.reserve(x.device, need, "mm8p")
+    torch.cuda.synchronize()
+    got = _np(ws[:need].view(torch.float16)).reshape(G, SB, 2, 4, 16, 8)  # g, sb, h, kg, n, j
+    got = got.transpose(1, 3, 2, 5, 0, 4).reshape(SB * 64, G * 16)      # (sb, kg, h, j) x (g, n)
+    w_u8 = mm8_unblock(mod.w_blk, I, O)
+    want = _np(dequantize_mm8(w_u8, mod.mx, mod.rx, mod.my.reshape(-1, 1), mod.ry.reshape(-1, 1),
+                              out_dtype=torch.float16))
+    assert np.array_equal(got[:I, :O].view(np.uint16), want.view(np.uint16))
+    assert not got[I:].any() and not got[:, O:].any()
+
+
+@pytest.mark.parametrize("IO,rows", [((4096, 4096), 600), ((2064, 520), 257), ((144, 40), 1024)])
+def test_mm8p_in_register_entry_matches_oracle(oracle, IO, rows):
+    """rwkv7mi_mm8t_gemm_prefill (the weight dequantised in registers, no
+    workspace) stays available beside the workspace route."""
+    import ctypes
+
+    from rwkv7mi import _lib
+
+    I, O = IO
+    rng = np.random.default_rng(3 * I + O + rows)
+    mod = _packed(rng, I, O, bias=True)
+    x = _cuda(rng.standard_normal((rows, I)), torch.float16)
+    y = torch.full((rows, O), float("nan"), device="cuda", dtype=torch.float16)
+    print(f"mm8p in-register: I={I} O={O} rows={rows}", flush=True)
+    arr = lambda ts: _lib.ptr_array(ts)
+    _lib.call("rwkv7mi_mm8t_gemm_prefill", 1, arr([x]), arr([mod.w_blk]), arr([mod.mx]), arr([mod.rx]),
+              arr([mod.my]), arr([mod.ry]), arr([mod.bias]), arr([None]), arr([y]), (ctypes.c_int * 1)(0),
+              rows, I, O, _lib.F16, _lib.F16, _lib.stream_of(x))
+    torch.cuda.synchronize()
+    err = _rel_err(_np(y).astype(np.float64), _ref(oracle, x, mod))
+    assert err <= TOL, (IO, rows, err)
+
+
 def test_mm8p_rejects():
     from rwkv7mi import _lib
 
     with pytest.raises(ValueError):
         _lib.call("rwkv7mi_mm8t_gemm_prefill", 0, None, None, None, None, None, None, None, None, None, None,
                   300, 128, 16, _lib.F16, _lib.F16, None)
+    with pytest.raises(ValueError):
+        _lib.call("rwkv7mi_mm8t_gemm_prefill_ws", 1, None, None, None, None, None, None, None, None, None, None,
+                  300, 128, 16, _lib.F16, _lib.F16, None, 0, None)
