@@ -8,15 +8,22 @@
 //    + my[k] + mx[o]) (fp32 arithmetic, one rounding: the bytes
 //    rwkv7mi_mm8_dequant writes) into a workspace, in MFMA B-operand order:
 //    [column group g of 16][64-input step sb][sub-step h][lane][8 halfs],
-//    lane n + 16 kg holding column 16 g + n, inputs 64 sb + 16 kg + 8 h .. +7.
-//    That is the lane order of the blocked MM8 layout the decode kernels read
-//    (a lane's 16 bytes there are inputs 16 kg .. +15 of the step), so each
-//    thread turns one lane's 16 bytes into its two 16-byte records.
+//    lane n + 16 kg holding inputs 64 sb + 16 kg + 8 h .. +7 of column
+//    col(g, n) = 32 (g / 2) + 8 (n / 4) + 4 (g % 2) + n % 4: each pair of
+//    groups covers 32 columns, permuted so that the GEMM's output lanes hold
+//    8 consecutive columns.  The input order is the lane order of the blocked
+//    MM8 layout the decode kernels read (a lane's 16 bytes there are inputs
+//    16 kg .. +15 of the step), so each thread turns one such lane's 16 bytes
+//    into its two 16-byte records.  O is padded to whole 32-column pairs.
 // 2. mm8h_gemm_kernel: y = x W_hat (+ bias) (relu^2 | + residual).  A
 //    256-lane workgroup (four waves, one per SIMD) computes 256 rows x 256
 //    columns; wave w owns all 256 rows x columns 64 w .. 64 w + 63 (16 x 4
 //    tiles of v_mfma_f32_16x16x32_f16, 256 fp32 accumulators per lane in the
-//    accumulation registers).  K advances 64 inputs per step:
+//    accumulation registers).  The MFMAs take W_hat as the A operand and x as
+//    B, so a lane holds one row (16 i + n) and, across a pair of groups, the
+//    8 consecutive columns 32 p + 8 kg .. +7: the epilogue is one 16-byte
+//    store (and residual load) per M tile and pair.  K advances 64 inputs
+//    per step:
 //    * W_hat: each wave loads its own four column groups global -> registers
 //      (8 x 16 bytes per lane and step), one step ahead, in two register sets
 //      (the loop is unrolled by two; no LDS, no wave reads another's bytes);
@@ -58,6 +65,7 @@ struct MhProb {
   const void* residual;
   void* y;
   int epilogue;
+  int vec;  // O % 8 == 0 and y (and the residual) 16-byte aligned: 16-byte output rows
 };
 struct MhBatch {
   MhProb p[MM8T_MAXPROB];
@@ -83,17 +91,19 @@ struct MhDeqBatch {
 __global__ __launch_bounds__(256) void mm8h_dequant_kernel(const MhDeqBatch D) {
   const MhDeqProb& P = D.p[blockIdx.y];
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int ngroups = (D.O + 15) / 16;
+  const int ngroups = 2 * ((D.O + 31) / 32);
   if (t >= (int64_t)ngroups * D.SB * 64) return;
   const int lane = (int)(t & 63);
   const int64_t gs = t >> 6;
   const int sb = (int)(gs % D.SB), g = (int)(gs / D.SB);
   const int n = lane & 15, kg = lane >> 4;
-  const int o = 16 * g + n;
+  const int o = 32 * (g >> 1) + 8 * (n >> 2) + 4 * (g & 1) + (n & 3);
   const int k0 = 64 * sb + 16 * kg;
-  const u32x4 raw = *reinterpret_cast<const u32x4*>(P.w + ((int64_t)g * D.KB + (sb >> 1)) * 2048 + (sb & 1) * 1024 +
-                                                    16 * lane);
   const bool ocol = o < D.O;
+  // column o's bytes: blocked group o / 16, lane (o % 16) + 16 kg
+  const u32x4 raw = ocol ? *reinterpret_cast<const u32x4*>(P.w + ((int64_t)(o >> 4) * D.KB + (sb >> 1)) * 2048 +
+                                                            (sb & 1) * 1024 + 16 * ((o & 15) + 16 * kg))
+                         : (u32x4){0u, 0u, 0u, 0u};
   const float rxo = ocol ? __half2float(P.rx[o]) : 0.f, mxo = ocol ? __half2float(P.mx[o]) : 0.f;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -145,7 +155,7 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
 
   // ---- global sources (raw buffer loads; out-of-range offsets read zeros)
   const __amdgpu_buffer_rsrc_t xr = mm8t_rsrc(P.x, (uint32_t)((int64_t)M * I * 2));
-  const int ngroups = (O + 15) / 16;
+  const int ngroups = 2 * ((O + 31) / 32);
   const int g0 = n0 / 16 + 4 * wave;  // this wave's first column group
   const int gcount = g0 < ngroups ? (ngroups - g0 < 4 ? ngroups - g0 : 4) : 0;
   const __amdgpu_buffer_rsrc_t wr =
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
       an[i] = lda(st_n, h_n, i);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[i][q] = mfma16x16x32(a[i], bw[q][h], acc[i][q]);
+      for (int q = 0; q < 4; ++q) acc[i][q] = mfma16x16x32(bw[q][h], a[i], acc[i][q]);
       if (i % 2 == 0) load(i / 2);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -259,30 +269,60 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the trailing loads have landed before the waves exit
 
-  // ---- epilogue: lane holds column n of each group, rows 16 i + 4 kg + e
+  // ---- epilogue: lane holds row 16 i + n and, in groups 2 p and 2 p + 1,
+  // columns c0 = 32 p + 8 kg .. +3 and c0 + 4 .. +7 of the wave's 64
   const __half* bp = reinterpret_cast<const __half*>(P.bias);
+  const bool vec = P.vec;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int o = n0 + 64 * wave + 16 * q + n;
-    if (o >= O) continue;
-    const float bo = bp ? __half2float(bp[o]) : 0.f;
+  for (int p = 0; p < 2; ++p) {
+    const int c0 = n0 + 64 * wave + 32 * p + 8 * kg;
+    if (c0 >= O) continue;
+    float bo[8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int e = 0; e < 8; ++e) bo[e] = bp && c0 + e < O ? __half2float(bp[c0 + e]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t row = m0 + 16 * i + n;
+      if (row >= M) continue;
+      float v[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t row = m0 + 16 * i + 4 * kg + e;
-        if (row < M) {
-          float v = acc[i][q][e] + bo;
-          const int64_t oi = row * O + o;
+        v[e] = acc[i][2 * p][e] + bo[e];
+        v[4 + e] = acc[i][2 * p + 1][e] + bo[4 + e];
+      }
+      const int64_t oi = row * O + c0;
+      if (vec && c0 + 8 <= O) {
+        if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
+          const f16x8 r = *reinterpret_cast<const f16x8*>(reinterpret_cast<const TA*>(P.residual) + oi);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] += (float)r[e];
+        }
+        f16x8 o8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float w = v[e];
           if (P.epilogue == RWKV7MI_EPI_RELU2) {
-            v = fmaxf(v, 0.f);
-            v = v * v;
-          } else if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
-            v += ld(reinterpret_cast<const TA*>(P.residual), oi);
+            w = fmaxf(w, 0.f);
+            w = w * w;
           }
-          reinterpret_cast<TA*>(P.y)[oi] = from_f32<TA>(v);
+          o8[e] = (_Float16)w;
+        }
+        *reinterpret_cast<f16x8*>(reinterpret_cast<TA*>(P.y) + oi) = o8;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (c0 + e >= O) continue;
+          float w = v[e];
+          if (P.epilogue == RWKV7MI_EPI_RELU2) {
+            w = fmaxf(w, 0.f);
+            w = w * w;
+          } else if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
+            w += ld(reinterpret_cast<const TA*>(P.residual), oi + e);
+          }
+          reinterpret_cast<TA*>(P.y)[oi + e] = from_f32<TA>(w);
         }
       }
+    }
   }
 }
 
@@ -292,7 +332,7 @@ using namespace rwkv7mi;
 
 extern "C" int64_t rwkv7mi_mm8t_gemm_prefill_ws_bytes(int nprob, int64_t I, int64_t O) {
   if (nprob < 1 || I <= 0 || O <= 0) return 0;
-  return (int64_t)nprob * ((O + 15) / 16) * ((I + 63) / 64) * MH_REC;
+  return (int64_t)nprob * (2 * ((O + 31) / 32)) * ((I + 63) / 64) * MH_REC;
 }
 
 extern "C" int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x, const uint8_t* const* w_blk,
@@ -331,7 +371,10 @@ extern "C" int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x, con
     __half* out = reinterpret_cast<__half*>(static_cast<char*>(ws) + per_prob * i);
     d.p[i] = MhDeqProb{w_blk[i], (const __half*)mx[i], (const __half*)rx[i], (const __half*)my[i],
                        (const __half*)ry[i], out};
-    b.p[i] = MhProb{x[i], out, bias ? bias[i] : nullptr, residual ? residual[i] : nullptr, y[i], epilogue[i]};
+    const void* res = residual ? residual[i] : nullptr;
+    const int vec = O % 8 == 0 && !(reinterpret_cast<uintptr_t>(y[i]) & 15) &&
+                    !(epilogue[i] == RWKV7MI_EPI_RESIDUAL && (reinterpret_cast<uintptr_t>(res) & 15));
+    b.p[i] = MhProb{x[i], out, bias ? bias[i] : nullptr, res, y[i], epilogue[i], vec};
   }
   d.I = b.I = (int)I;
   d.O = b.O = (int)O;
@@ -344,7 +387,7 @@ extern "C" int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x, con
   b.gn = std::min(b.nt, 8);
   const int64_t T = (int64_t)((b.mt + b.gm - 1) / b.gm) * b.gm * ((b.nt + b.gn - 1) / b.gn) * b.gn;
   if (T > (int64_t)INT32_MAX / 2) return fail(RWKV7MI_EINVAL, w + ": too many tiles");
-  const int64_t recs = ((O + 15) / 16) * (int64_t)d.SB * 64;
+  const int64_t recs = (2 * ((O + 31) / 32)) * (int64_t)d.SB * 64;
   hipLaunchKernelGGL(mm8h_dequant_kernel, dim3((unsigned)((recs + 255) / 256), (unsigned)nprob), dim3(256), 0,
                      as_stream(stream), d);
   if (int rc = check_launch("mm8h_dequant_kernel")) return rc;

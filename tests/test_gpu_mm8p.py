@@ -137,7 +137,8 @@ def test_mm8p_module_routes(oracle):
 def test_mm8p_workspace_is_the_dequantised_weight(IO):
     """The workspace the prefill GEMM reads holds rwkv7mi_mm8_dequant's fp16
     weight bit for bit: record (group g, step sb, sub-step h, lane n + 16 kg,
-    j) is W_hat[64 sb + 16 kg + 8 h + j, 16 g + n], zero past I or O."""
+    j) is W_hat[64 sb + 16 kg + 8 h + j, 32 (g // 2) + 8 (n // 4) + 4 (g % 2)
+    + n % 4], zero past I or O."""
     from rwkv7mi import _lib
     from rwkv7mi import workspace as _ws
     from rwkv7mi.native_quant_mm8 import dequantize_mm8, mm8_gemm_prefill_multi_into, mm8_unblock
@@ -150,12 +151,13 @@ def test_mm8p_workspace_is_the_dequantised_weight(IO):
     print(f"mm8p workspace: I={I} O={O}", flush=True)
     mm8_gemm_prefill_multi_into([x], [mod], [y])
     need = int(_lib.load().rwkv7mi_mm8t_gemm_prefill_ws_bytes(1, I, O))
-    G, SB = (O + 15) // 16, (I + 63) // 64
+    G, SB = 2 * ((O + 31) // 32), (I + 63) // 64
     assert need == G * SB * 2048
     ws = _ws.reserve(x.device, need, "mm8p")
     torch.cuda.synchronize()
-    got = _np(ws[:need].view(torch.float16)).reshape(G, SB, 2, 4, 16, 8)  # g, sb, h, kg, n, j
-    got = got.transpose(1, 3, 2, 5, 0, 4).reshape(SB * 64, G * 16)      # (sb, kg, h, j) x (g, n)
+    # g = 2 p + b, n = 4 a + c: column 32 p + 8 a + 4 b + c
+    got = _np(ws[:need].view(torch.float16)).reshape(G // 2, 2, SB, 2, 4, 4, 4, 8)  # p, b, sb, h, kg, a, c, j
+    got = got.transpose(2, 4, 3, 7, 0, 5, 1, 6).reshape(SB * 64, G * 16)          # (sb, kg, h, j) x (p, a, b, c)
     w_u8 = mm8_unblock(mod.w_blk, I, O)
     want = _np(dequantize_mm8(w_u8, mod.mx, mod.rx, mod.my.reshape(-1, 1), mod.ry.reshape(-1, 1),
                               out_dtype=torch.float16))
