@@ -37,7 +37,7 @@ from .native_wkv_fp16 import (native_fp16_recurrent_output_prepare_raw, native_f
 from .fused_time_mix import fused_attn_sequence_shift_mix, fused_ffn_sequence_shift_mix
 from .sampling import argmax_rows, argmax_workspace_bytes
 from .native_quant_mm8 import (GEMM_ROWS, GEMV_ROWS, MM8Linear, is_blocked, mm8_gemm_multi_into, mm8_gemm_prefill_multi_into,
-                               mm8_gemm_workspace_bytes, mm8_lnmix_multi_into, mm8_matmul_multi_into,
+                               mm8_gemm_workspace_bytes, mm8_prefill_workspace_bytes, mm8_lnmix_multi_into, mm8_matmul_multi_into,
                                mm8_matmul_multi_lora_into,
                                mm8_matmul_partials, mm8t_workspace_bytes)
 from .native_quant_policy import should_quantize_linear
@@ -993,7 +993,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
         return NativeRWKV7Cache.zeros(self.config, batch, self.device, self.dtype, state_dtype=self.state_dtype)
 
     def reserve_workspace(self, rows: int) -> None:
-        """Grow the per-device scratch slots for ``rows``-row decode steps (before capture)."""
+        """Grow the per-device scratch slots for ``rows``-row steps (before capture)."""
         if 0 < rows <= QuantLinear.GEMV_ROWS:
             tneed = 0
             for L in self.layers:
@@ -1013,6 +1013,16 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                     gneed = max(gneed, mm8_gemm_workspace_bytes(1, rows, lin.in_features, lin.out_features))
             if gneed:
                 _ws.reserve(self.device, gneed, slot="mm8g")
+        if rows > QuantLinear.GEMM_ROWS:  # prefill: the fp16 dequantised weights of the widest launch
+            pneed = 0
+            for L in self.layers:
+                if isinstance(L.r_proj, QuantLinear):
+                    pneed = max(pneed, mm8_prefill_workspace_bytes(3, L.r_proj.in_features, L.r_proj.out_features))
+            for lin in self._linears():
+                if isinstance(lin, QuantLinear):
+                    pneed = max(pneed, mm8_prefill_workspace_bytes(1, lin.in_features, lin.out_features))
+            if pneed:
+                _ws.reserve(self.device, pneed, slot="mm8p")
         cfg = self.config
         ranks = [cfg.decay_low_rank_dim, cfg.a_low_rank_dim, cfg.gate_low_rank_dim, cfg.v_low_rank_dim]
         _ws.reserve(self.device, lora_workspace_bytes(ranks, rows, cfg.hidden_size), slot="lora")

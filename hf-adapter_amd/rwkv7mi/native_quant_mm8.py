@@ -131,6 +131,12 @@ def mm8_workspace_bytes(rows: int, n: int, m: int) -> int:
     return int(_lib.load().rwkv7mi_mm8_workspace_bytes(int(rows), int(n), int(m)))
 
 
+def mm8_prefill_workspace_bytes(nprob: int, n: int, m: int) -> int:
+    """Bytes of the ``"mm8p"`` slot a prefill GEMM of ``nprob`` ``[n -> m]``
+    problems needs: their fp16 dequantised weights in MFMA operand order."""
+    return int(_lib.load().rwkv7mi_mm8t_gemm_prefill_ws_bytes(int(nprob), int(n), int(m)))
+
+
 def mm8t_workspace_bytes(nprob: int, rows: int, n: int, m: int) -> int:
     """Split-K partials the blocked GEMV needs for ``rows`` rows (the ``"mm8t"``
     slot); 0 when the rows' x' fits one LDS chunk."""
@@ -395,7 +401,7 @@ def mm8_gemm_prefill_multi_into(xs, mods, outs, *, residuals=None, epilogues=Non
             else:
                 mm8_matmul_multi_into(xc, mods, oc, residuals=rc, epilogues=epilogues)
             continue
-        need = int(_lib.load().rwkv7mi_mm8t_gemm_prefill_ws_bytes(k, n, m))
+        need = mm8_prefill_workspace_bytes(k, n, m)
         ws = _ws.reserve(xs[0].device, need, "mm8p")
         _lib.call(
             "rwkv7mi_mm8t_gemm_prefill_ws", k, arr(xc), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
