@@ -28,8 +28,10 @@
 //    between the first sub-step's MFMA groups and the next step's first
 //    sub-step operands between the second's;
 //  * x rows: a row is 128 bytes whose 16-byte chunk c sits at position
-//    c ^ (row % 8), so the 8 lanes of an MFMA A read phase hit 8 different
-//    chunk positions (all 32 banks once);
+//    c ^ key(row), key(r) = (r % 8) ^ ((r / 8) % 2).  An MFMA A read (lane
+//    n + 16 kg: row r0 + n, r0 % 16 == 0, chunk 2 kg + h) then has no LDS
+//    bank conflict on gfx950; the plain key r % 8 cost about 4 conflict
+//    cycles per read (measured with the SQ_LDS_BANK_CONFLICT counter);
 //  * the MM8 bytes: the step's 1 KB half of each of the tile's 16 column
 //    groups, as stored (a lane's 16 bytes are the B operands of two
 //    consecutive MFMAs), loaded once per workgroup for both row halves;
@@ -65,6 +67,9 @@ struct Mm8pBatch {
   int mt, nt;              // row / column tiles
   int gm, gn;              // XCD tile group: gm row tiles x gn column tiles
 };
+
+// x row r's 16-byte chunk c sits at position c ^ mm8p_key(r)
+__device__ __forceinline__ int mm8p_key(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // bytes (d0, d1) = 8 consecutive inputs of one column -> fp16 (w - 128) * ry
 __device__ __forceinline__ f16x8 mm8p_b_operand(uint32_t d0, uint32_t d1, f16x8 ry) {
@@ -125,7 +130,7 @@ __global__ __launch_bounds__(512, 1) void mm8p_kernel(const Mm8pBatch B) {
   // loads of step s into stage s % 3 (the LDS writes complete with vmcnt):
   //  * x: wave w, round u writes rows 64 u + 8 w .. +7 (1 KB; lane l lands
   //    at row + l / 8, chunk position l % 8, so it fetches input chunk
-  //    (l % 8) ^ (l / 8) of that row); rows past M, inputs past I read zeros;
+  //    (l % 8) ^ key(row + l / 8)); rows past M, inputs past I read zeros;
   //  * B: wave w loads column groups 2w, 2w + 1 (1 KB each);
   //  * ry (lanes 0..7) and my (lanes 8..15): wave 0.
   // Per wave and step: 6 loads, 8 on wave 0.
@@ -135,7 +140,7 @@ __global__ __launch_bounds__(512, 1) void mm8p_kernel(const Mm8pBatch B) {
     for (int u = 0; u < 4; ++u) {
       const int r0 = 64 * u + 8 * wave;
       const int r = r0 + (lane >> 3);
-      const int k = s * MM8P_KS + 8 * ((lane & 7) ^ (lane >> 3));
+      const int k = s * MM8P_KS + 8 * ((lane & 7) ^ mm8p_key(r));
       const bool ok = m0 + r < M && k < I;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(xs(st) + r0 * MM8P_XS), 16,
                                                ok ? (int)(((int64_t)(m0 + r) * I + k) * 2) : (int)MM8T_OOB, 0, 0, 0);
@@ -213,7 +218,7 @@ __global__ __launch_bounds__(512, 1) void mm8p_kernel(const Mm8pBatch B) {
     // A operands of sub-step h: reads 0..7 are the wave's eight M tiles, 8 and
     // 9 its two extra-column tiles (M tiles 2wn, 2wn + 1, read again)
     auto lda = [&](int h, int i) {
-      const int ka = 8 * ((2 * kg + h) ^ (n & 7));  // swizzled chunk of A row (... + n): row % 8 = n % 8
+      const int ka = 8 * ((2 * kg + h) ^ mm8p_key(n));  // swizzled chunk of A row (16 j + n): key(n)
       const int mt = i < 8 ? i : 2 * wn + (i - 8);
       return *reinterpret_cast<const f16x8*>(xb + (128 * wm + 16 * mt + n) * MM8P_XS + ka);
     };
