@@ -88,6 +88,37 @@ struct MhDeqBatch {
 
 // one thread per (column group, step, lane): the lane's 16 MM8 bytes ->
 // its two 8-half records
+// The same operand order for an fp16 nn.Linear weight W [O, I] (W_hat[k, o]
+// = W[o, k]): one thread per (column group, step, lane) copies the 16
+// inputs 16 kg .. +15 of its column into its two records.
+struct MhRelBatch {
+  const __half* w[MM8T_MAXPROB];
+  __half* out[MM8T_MAXPROB];
+  int I, O, SB;
+};
+__global__ __launch_bounds__(256) void mm8h_relayout_kernel(const MhRelBatch R) {
+  const int p = blockIdx.y;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int ngroups = 2 * ((R.O + 31) / 32);
+  if (t >= (int64_t)ngroups * R.SB * 64) return;
+  const int lane = (int)(t & 63);
+  const int64_t gs = t >> 6;
+  const int sb = (int)(gs % R.SB), g = (int)(gs / R.SB);
+  const int n = lane & 15, kg = lane >> 4;
+  const int o = 32 * (g >> 1) + 8 * (n >> 2) + 4 * (g & 1) + (n & 3);
+  const int k0 = 64 * sb + 16 * kg;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    f16x8 v;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = k0 + 8 * h + j;
+      v[j] = o < R.O && k < R.I ? (_Float16)__half2float(R.w[p][(int64_t)o * R.I + k]) : (_Float16)0.f;
+    }
+    *reinterpret_cast<f16x8*>(R.out[p] + (gs * MH_REC + h * 1024 + 16 * lane) / 2) = v;
+  }
+}
+
 __global__ __launch_bounds__(256) void mm8h_dequant_kernel(const MhDeqBatch D) {
   const MhDeqProb& P = D.p[blockIdx.y];
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -335,62 +366,20 @@ extern "C" int64_t rwkv7mi_mm8t_gemm_prefill_ws_bytes(int nprob, int64_t I, int6
   return (int64_t)nprob * (2 * ((O + 31) / 32)) * ((I + 63) / 64) * MH_REC;
 }
 
-extern "C" int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x, const uint8_t* const* w_blk,
-                                            const void* const* mx, const void* const* rx, const void* const* my,
-                                            const void* const* ry, const void* const* bias,
-                                            const void* const* residual, void* const* y, const int* epilogue,
-                                            int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype,
-                                            void* ws, int64_t ws_bytes, void* stream) {
-  const std::string w("mm8t_gemm_prefill_ws");
-  if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
-  if (!x || !w_blk || !mx || !rx || !my || !ry || !y || !epilogue) return fail(RWKV7MI_EINVAL, w + ": null array");
-  if (rows < 0 || I <= 0 || O <= 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
-  if (rows == 0) return RWKV7MI_OK;
-  if (act_dtype != RWKV7MI_F16 || meta_dtype != RWKV7MI_F16)
-    return fail(RWKV7MI_EINVAL, w + ": fp16 activations and fp16 metadata only");
-  if (I % 16) return fail(RWKV7MI_EINVAL, w + ": in_features must be a multiple of 16");
-  // x's descriptor spans rows * I * 2 bytes and out-of-range offsets start at 2^31;
-  // one wave's W_hat descriptor spans 4 groups x SB records
-  if (rows * I * 2 >= (int64_t)MM8T_OOB || 4 * ((I + 63) / 64) * MH_REC >= (int64_t)MM8T_OOB || O > INT32_MAX ||
-      rows * O > ((int64_t)1 << 40))
-    return fail(RWKV7MI_EINVAL, w + ": too large (split the rows)");
-  const int64_t per_prob = rwkv7mi_mm8t_gemm_prefill_ws_bytes(1, I, O);
-  if (!ws || ws_bytes < per_prob * nprob)
-    return fail(RWKV7MI_EINVAL, w + ": workspace too small (rwkv7mi_mm8t_gemm_prefill_ws_bytes)");
-  if (reinterpret_cast<uintptr_t>(ws) & 15) return fail(RWKV7MI_EINVAL, w + ": workspace must be 16-byte aligned");
-  MhBatch b{};
-  MhDeqBatch d{};
-  for (int i = 0; i < nprob; ++i) {
-    if (!x[i] || !w_blk[i] || !mx[i] || !rx[i] || !my[i] || !ry[i] || !y[i])
-      return fail(RWKV7MI_EINVAL, w + ": null pointer");
-    if ((reinterpret_cast<uintptr_t>(x[i]) | reinterpret_cast<uintptr_t>(w_blk[i])) & 15)
-      return fail(RWKV7MI_EINVAL, w + ": x and the weights must be 16-byte aligned");
-    if (epilogue[i] < 0 || epilogue[i] > 2) return fail(RWKV7MI_EINVAL, w + ": bad epilogue");
-    if (epilogue[i] == RWKV7MI_EPI_RESIDUAL && !(residual && residual[i]))
-      return fail(RWKV7MI_EINVAL, w + ": residual missing");
-    __half* out = reinterpret_cast<__half*>(static_cast<char*>(ws) + per_prob * i);
-    d.p[i] = MhDeqProb{w_blk[i], (const __half*)mx[i], (const __half*)rx[i], (const __half*)my[i],
-                       (const __half*)ry[i], out};
-    const void* res = residual ? residual[i] : nullptr;
-    const int vec = O % 8 == 0 && !(reinterpret_cast<uintptr_t>(y[i]) & 15) &&
-                    !(epilogue[i] == RWKV7MI_EPI_RESIDUAL && (reinterpret_cast<uintptr_t>(res) & 15));
-    b.p[i] = MhProb{x[i], out, bias ? bias[i] : nullptr, res, y[i], epilogue[i], vec};
-  }
-  d.I = b.I = (int)I;
-  d.O = b.O = (int)O;
-  d.SB = b.SB = (int)((I + 63) / 64);
-  d.KB = (int)((I + 127) / 128);
+namespace rwkv7mi {
+// the GEMM over prepared W_hat records (b.p[i].wt), with the tile grid set here
+static int mh_gemm_launch(MhBatch& b, int nprob, int64_t rows, int64_t I, int64_t O, void* stream,
+                          const std::string& w) {
   b.rows = (int)rows;
+  b.I = (int)I;
+  b.O = (int)O;
+  b.SB = (int)((I + 63) / 64);
   b.mt = (int)((rows + MH_M - 1) / MH_M);
   b.nt = (int)((O + MH_N - 1) / MH_N);
   b.gm = std::min(b.mt, 4);
   b.gn = std::min(b.nt, 8);
   const int64_t T = (int64_t)((b.mt + b.gm - 1) / b.gm) * b.gm * ((b.nt + b.gn - 1) / b.gn) * b.gn;
   if (T > (int64_t)INT32_MAX / 2) return fail(RWKV7MI_EINVAL, w + ": too many tiles");
-  const int64_t recs = (2 * ((O + 31) / 32)) * (int64_t)d.SB * 64;
-  hipLaunchKernelGGL(mm8h_dequant_kernel, dim3((unsigned)((recs + 255) / 256), (unsigned)nprob), dim3(256), 0,
-                     as_stream(stream), d);
-  if (int rc = check_launch("mm8h_dequant_kernel")) return rc;
   const int64_t per = (T + 7) / 8;
   auto launch = [&](auto kern, std::atomic<uint64_t>& raised) {
     if (int rc = raise_dynamic_lds(reinterpret_cast<const void*>(kern), MH_LDS, raised, "mm8h_gemm_kernel"))
@@ -401,4 +390,102 @@ extern "C" int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x, con
   };
   static std::atomic<uint64_t> raised_full{0}, raised_part{0};
   return I % 64 == 0 ? launch(&mm8h_gemm_kernel<true>, raised_full) : launch(&mm8h_gemm_kernel<false>, raised_part);
+}
+
+// shape, workspace and per-problem checks shared by the two entries
+static int mh_check(const std::string& w, int nprob, int64_t rows, int64_t I, int64_t O, void* ws, int64_t ws_bytes) {
+  if (nprob < 1 || nprob > MM8T_MAXPROB) return fail(RWKV7MI_EINVAL, w + ": 1..4 problems per launch");
+  if (rows < 0 || I <= 0 || O <= 0) return fail(RWKV7MI_EINVAL, w + ": bad shape");
+  if (I % 16) return fail(RWKV7MI_EINVAL, w + ": in_features must be a multiple of 16");
+  // x's descriptor spans rows * I * 2 bytes and out-of-range offsets start at 2^31;
+  // one wave's W_hat descriptor spans 4 groups x SB records
+  if (rows * I * 2 >= (int64_t)MM8T_OOB || 4 * ((I + 63) / 64) * MH_REC >= (int64_t)MM8T_OOB || O > INT32_MAX ||
+      rows * O > ((int64_t)1 << 40))
+    return fail(RWKV7MI_EINVAL, w + ": too large (split the rows)");
+  if (rows == 0) return RWKV7MI_OK;
+  const int64_t per_prob = (2 * ((O + 31) / 32)) * ((I + 63) / 64) * MH_REC;
+  if (!ws || ws_bytes < per_prob * nprob)
+    return fail(RWKV7MI_EINVAL, w + ": workspace too small (rwkv7mi_mm8t_gemm_prefill_ws_bytes)");
+  if (reinterpret_cast<uintptr_t>(ws) & 15) return fail(RWKV7MI_EINVAL, w + ": workspace must be 16-byte aligned");
+  return RWKV7MI_OK;
+}
+
+static int mh_prob(const std::string& w, MhProb& q, const void* x, const __half* out, const void* bias,
+                   const void* res, void* y, int epi, int64_t O) {
+  if (!x || !y) return fail(RWKV7MI_EINVAL, w + ": null pointer");
+  if (reinterpret_cast<uintptr_t>(x) & 15) return fail(RWKV7MI_EINVAL, w + ": x must be 16-byte aligned");
+  if (epi < 0 || epi > 2) return fail(RWKV7MI_EINVAL, w + ": bad epilogue");
+  if (epi == RWKV7MI_EPI_RESIDUAL && !res) return fail(RWKV7MI_EINVAL, w + ": residual missing");
+  const int vec = O % 8 == 0 && !(reinterpret_cast<uintptr_t>(y) & 15) &&
+                  !(epi == RWKV7MI_EPI_RESIDUAL && (reinterpret_cast<uintptr_t>(res) & 15));
+  q = MhProb{x, out, bias, res, y, epi, vec};
+  return RWKV7MI_OK;
+}
+}  // namespace rwkv7mi
+
+extern "C" int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x, const uint8_t* const* w_blk,
+                                            const void* const* mx, const void* const* rx, const void* const* my,
+                                            const void* const* ry, const void* const* bias,
+                                            const void* const* residual, void* const* y, const int* epilogue,
+                                            int64_t rows, int64_t I, int64_t O, int act_dtype, int meta_dtype,
+                                            void* ws, int64_t ws_bytes, void* stream) {
+  const std::string w("mm8t_gemm_prefill_ws");
+  if (!x || !w_blk || !mx || !rx || !my || !ry || !y || !epilogue) return fail(RWKV7MI_EINVAL, w + ": null array");
+  if (act_dtype != RWKV7MI_F16 || meta_dtype != RWKV7MI_F16)
+    return fail(RWKV7MI_EINVAL, w + ": fp16 activations and fp16 metadata only");
+  if (int rc = mh_check(w, nprob, rows, I, O, ws, ws_bytes)) return rc;
+  if (rows == 0) return RWKV7MI_OK;
+  const int64_t per_prob = rwkv7mi_mm8t_gemm_prefill_ws_bytes(1, I, O);
+  MhBatch b{};
+  MhDeqBatch d{};
+  for (int i = 0; i < nprob; ++i) {
+    if (!w_blk[i] || !mx[i] || !rx[i] || !my[i] || !ry[i]) return fail(RWKV7MI_EINVAL, w + ": null pointer");
+    if (reinterpret_cast<uintptr_t>(w_blk[i]) & 15) return fail(RWKV7MI_EINVAL, w + ": the weights must be 16-byte aligned");
+    __half* out = reinterpret_cast<__half*>(static_cast<char*>(ws) + per_prob * i);
+    if (int rc = mh_prob(w, b.p[i], x[i], out, bias ? bias[i] : nullptr, residual ? residual[i] : nullptr, y[i],
+                         epilogue[i], O))
+      return rc;
+    d.p[i] = MhDeqProb{w_blk[i], (const __half*)mx[i], (const __half*)rx[i], (const __half*)my[i],
+                       (const __half*)ry[i], out};
+  }
+  d.I = (int)I;
+  d.O = (int)O;
+  d.SB = (int)((I + 63) / 64);
+  d.KB = (int)((I + 127) / 128);
+  const int64_t recs = (2 * ((O + 31) / 32)) * (int64_t)d.SB * 64;
+  hipLaunchKernelGGL(mm8h_dequant_kernel, dim3((unsigned)((recs + 255) / 256), (unsigned)nprob), dim3(256), 0,
+                     as_stream(stream), d);
+  if (int rc = check_launch("mm8h_dequant_kernel")) return rc;
+  return mh_gemm_launch(b, nprob, rows, I, O, stream, w);
+}
+
+extern "C" int rwkv7mi_dense_gemm_prefill_ws(int nprob, const void* const* x, const void* const* W,
+                                             const void* const* bias, const void* const* residual, void* const* y,
+                                             const int* epilogue, int64_t rows, int64_t I, int64_t O, int act_dtype,
+                                             void* ws, int64_t ws_bytes, void* stream) {
+  const std::string w("dense_gemm_prefill_ws");
+  if (!x || !W || !y || !epilogue) return fail(RWKV7MI_EINVAL, w + ": null array");
+  if (act_dtype != RWKV7MI_F16) return fail(RWKV7MI_EINVAL, w + ": fp16 activations and weights only");
+  if (int rc = mh_check(w, nprob, rows, I, O, ws, ws_bytes)) return rc;
+  if (rows == 0) return RWKV7MI_OK;
+  const int64_t per_prob = rwkv7mi_mm8t_gemm_prefill_ws_bytes(1, I, O);
+  MhBatch b{};
+  MhRelBatch r{};
+  for (int i = 0; i < nprob; ++i) {
+    if (!W[i]) return fail(RWKV7MI_EINVAL, w + ": null pointer");
+    __half* out = reinterpret_cast<__half*>(static_cast<char*>(ws) + per_prob * i);
+    if (int rc = mh_prob(w, b.p[i], x[i], out, bias ? bias[i] : nullptr, residual ? residual[i] : nullptr, y[i],
+                         epilogue[i], O))
+      return rc;
+    r.w[i] = static_cast<const __half*>(W[i]);
+    r.out[i] = out;
+  }
+  r.I = (int)I;
+  r.O = (int)O;
+  r.SB = (int)((I + 63) / 64);
+  const int64_t recs = (2 * ((O + 31) / 32)) * (int64_t)r.SB * 64;
+  hipLaunchKernelGGL(mm8h_relayout_kernel, dim3((unsigned)((recs + 255) / 256), (unsigned)nprob), dim3(256), 0,
+                     as_stream(stream), r);
+  if (int rc = check_launch("mm8h_relayout_kernel")) return rc;
+  return mh_gemm_launch(b, nprob, rows, I, O, stream, w);
 }

@@ -80,6 +80,7 @@ SIGNATURES = {
     "rwkv7mi_mm8t_gemm_prefill": (_i32, [_i32] + [_c_p] * 10 + [_i64, _i64, _i64, _i32, _i32, _c_p]),
     "rwkv7mi_mm8t_gemm_prefill_ws": (_i32, [_i32] + [_c_p] * 10 + [_i64, _i64, _i64, _i32, _i32, _c_p, _i64, _c_p]),
     "rwkv7mi_mm8t_gemm_prefill_ws_bytes": (_i64, [_i32, _i64, _i64]),
+    "rwkv7mi_dense_gemm_prefill_ws": (_i32, [_i32] + [_c_p] * 6 + [_i64, _i64, _i64, _i32, _c_p, _i64, _c_p]),
     "rwkv7mi_mm8t_blocked_bytes": (_sz, [_i64, _i64]),
     "rwkv7mi_mm8t_block": (_i32, [_c_p, _i64, _i64, _i64, _i64, _c_p, _c_p]),
     "rwkv7mi_mm8t_unblock": (_i32, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p]),

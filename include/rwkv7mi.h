@@ -444,6 +444,20 @@ int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x,
                                  int64_t O, int act_dtype, int meta_dtype,
                                  void* ws, int64_t ws_bytes, void* stream);
 
+/* The same prefill GEMM for unquantised fp16 nn.Linear weights W [O, I]
+ * (y = epilogue(x @ W^T (+ bias))): W is copied into the workspace in MFMA
+ * operand order, then the 256 x 256 fp16 MFMA GEMM runs with the epilogue
+ * fused.  fp16 activations and weights, I % 16 == 0, the workspace as for
+ * rwkv7mi_mm8t_gemm_prefill_ws (rwkv7mi_mm8t_gemm_prefill_ws_bytes).
+ * Replaces the unquantised projections' torch GEMM of the prefill
+ * (rwkv7_hf/native_jit_prefill.py:542-631, 955-1013). */
+int rwkv7mi_dense_gemm_prefill_ws(int nprob, const void* const* x,
+                                  const void* const* W, const void* const* bias,
+                                  const void* const* residual, void* const* y,
+                                  const int* epilogue, int64_t rows, int64_t I,
+                                  int64_t O, int act_dtype, void* ws,
+                                  int64_t ws_bytes, void* stream);
+
 /* Allocation-free form of rwkv7mi_mm8t_gemm_multi (same arguments and results,
  * no workspace argument).  No counterpart in the reference: it is for callers
  * that cannot allocate (code under hipGraph capture, tight serving loops,
