@@ -240,8 +240,8 @@ class DenseLinear:
 class QuantLinear:
     """MM8 Linear, all on HIP kernels: the fused blocked dequant GEMV for up to
     ``GEMV_ROWS`` rows, the 64-row MFMA tile GEMM (split K) up to ``GEMM_ROWS``
-    rows, and the dequant-in-register 256 x 256 prefill GEMM above that
-    (``mm8_gemm_prefill_multi_into``).  Modules whose bytes are not blocked
+    rows, and above that the prefill GEMM over the materialised fp16
+    dequantised weight (``mm8_gemm_prefill_multi_into``).  Modules whose bytes are not blocked
     take MM8Linear's own route."""
 
     GEMV_ROWS = GEMV_ROWS
