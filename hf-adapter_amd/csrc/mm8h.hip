@@ -4,10 +4,11 @@
 // native_quant_mm8.py:100-108, then x @ W_hat), as do the prefill projections
 // of rwkv7_hf/native_jit_prefill.py:542-631, 955-1013.
 //
-// 1. mm8h_dequant_kernel writes W_hat[k, o] = fp16(((w + 0.5) ry[k]) rx[o]
-//    + my[k] + mx[o]) (fp32 arithmetic, one rounding: the bytes
-//    rwkv7mi_mm8_dequant writes) into a workspace, in MFMA B-operand order:
-//    [column group g of 16][64-input step sb][sub-step h][lane][8 halfs],
+// 1. mm8h_dequant_kernel writes W_hat[k, o] = ((w + 0.5) ry[k]) rx[o]
+//    + my[k] + mx[o] in the activation type, fp16 or bf16 (fp32 arithmetic,
+//    one rounding: the bytes rwkv7mi_mm8_dequant writes) into a workspace,
+//    in MFMA operand order:
+//    [column group g of 16][64-input step sb][sub-step h][lane][8 values],
 //    lane n + 16 kg holding inputs 64 sb + 16 kg + 8 h .. +7 of column
 //    col(g, n) = 32 (g / 2) + 8 (n / 4) + 4 (g % 2) + n % 4: each pair of
 //    groups covers 32 columns, permuted so that the GEMM's output lanes hold
@@ -60,7 +61,7 @@ constexpr int64_t MH_REC = 2048;                // W_hat bytes per (column group
 
 struct MhProb {
   const void* x;
-  const __half* wt;  // W_hat in MFMA order (the workspace)
+  const void* wt;    // W_hat in MFMA order (the workspace)
   const void* bias;
   const void* residual;
   void* y;
@@ -76,10 +77,20 @@ struct MhBatch {
 
 __device__ __forceinline__ int mh_key(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+// element and 8-vector types of fp16 (__half) and bf16 (__hip_bfloat16) data
+template <typename T> struct MhTypes {
+  using E = _Float16;
+  typedef _Float16 V __attribute__((ext_vector_type(8)));
+};
+template <> struct MhTypes<__hip_bfloat16> {
+  using E = __bf16;
+  typedef __bf16 V __attribute__((ext_vector_type(8)));
+};
+
 struct MhDeqProb {
   const uint8_t* w;  // blocked MM8 bytes: [ceil(O/16)][ceil(I/128)][2048]
-  const __half *mx, *rx, *my, *ry;
-  __half* out;       // [ceil(O/16)][SB][2][64][8]
+  const void *mx, *rx, *my, *ry;
+  void* out;         // [2 ceil(O/32)][SB][2][64][8] of the activation type
 };
 struct MhDeqBatch {
   MhDeqProb p[MM8T_MAXPROB];
@@ -92,11 +103,14 @@ struct MhDeqBatch {
 // = W[o, k]): one thread per (column group, step, lane) copies the 16
 // inputs 16 kg .. +15 of its column into its two records.
 struct MhRelBatch {
-  const __half* w[MM8T_MAXPROB];
-  __half* out[MM8T_MAXPROB];
+  const void* w[MM8T_MAXPROB];
+  void* out[MM8T_MAXPROB];
   int I, O, SB;
 };
+template <typename TA>
 __global__ __launch_bounds__(256) void mm8h_relayout_kernel(const MhRelBatch R) {
+  using E = typename MhTypes<TA>::E;
+  using V = typename MhTypes<TA>::V;
   const int p = blockIdx.y;
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int ngroups = 2 * ((R.O + 31) / 32);
@@ -109,18 +123,23 @@ __global__ __launch_bounds__(256) void mm8h_relayout_kernel(const MhRelBatch R) 
   const int k0 = 64 * sb + 16 * kg;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    f16x8 v;
+    V v;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int k = k0 + 8 * h + j;
-      v[j] = o < R.O && k < R.I ? (_Float16)__half2float(R.w[p][(int64_t)o * R.I + k]) : (_Float16)0.f;
+      v[j] = o < R.O && k < R.I ? static_cast<const E*>(R.w[p])[(int64_t)o * R.I + k] : (E)0.f;
     }
-    *reinterpret_cast<f16x8*>(R.out[p] + (gs * MH_REC + h * 1024 + 16 * lane) / 2) = v;
+    *reinterpret_cast<V*>(static_cast<char*>(R.out[p]) + gs * MH_REC + h * 1024 + 16 * lane) = v;
   }
 }
 
+template <typename TA>
 __global__ __launch_bounds__(256) void mm8h_dequant_kernel(const MhDeqBatch D) {
+  using E = typename MhTypes<TA>::E;
+  using V = typename MhTypes<TA>::V;
   const MhDeqProb& P = D.p[blockIdx.y];
+  const TA *mx = static_cast<const TA*>(P.mx), *rx = static_cast<const TA*>(P.rx);
+  const TA *my = static_cast<const TA*>(P.my), *ry = static_cast<const TA*>(P.ry);
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int ngroups = 2 * ((D.O + 31) / 32);
   if (t >= (int64_t)ngroups * D.SB * 64) return;
@@ -135,10 +154,10 @@ __global__ __launch_bounds__(256) void mm8h_dequant_kernel(const MhDeqBatch D) {
   const u32x4 raw = ocol ? *reinterpret_cast<const u32x4*>(P.w + ((int64_t)(o >> 4) * D.KB + (sb >> 1)) * 2048 +
                                                             (sb & 1) * 1024 + 16 * ((o & 15) + 16 * kg))
                          : (u32x4){0u, 0u, 0u, 0u};
-  const float rxo = ocol ? __half2float(P.rx[o]) : 0.f, mxo = ocol ? __half2float(P.mx[o]) : 0.f;
+  const float rxo = ocol ? to_f32(rx[o]) : 0.f, mxo = ocol ? to_f32(mx[o]) : 0.f;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    f16x8 v;
+    V v;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int k = k0 + 8 * h + j;
@@ -146,18 +165,19 @@ __global__ __launch_bounds__(256) void mm8h_dequant_kernel(const MhDeqBatch D) {
       float x = 0.f;
       if (ocol && k < D.I) {
         const float wq = (float)byte + 0.5f;
-        x = wq * __half2float(P.ry[k]) * rxo + __half2float(P.my[k]) + mxo;
+        x = wq * to_f32(ry[k]) * rxo + to_f32(my[k]) + mxo;
       }
-      v[j] = (_Float16)x;
+      v[j] = (E)x;
     }
-    *reinterpret_cast<f16x8*>(P.out + (gs * MH_REC + h * 1024 + 16 * lane) / 2) = v;
+    *reinterpret_cast<V*>(static_cast<char*>(P.out) + gs * MH_REC + h * 1024 + 16 * lane) = v;
   }
 }
 
 // FULLK: I is a multiple of 64 (no step ends inside a 16-byte chunk's range)
-template <bool FULLK>
+template <bool FULLK, typename TA>
 __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch B) {
-  using TA = __half;
+  using E = typename MhTypes<TA>::E;
+  using V = typename MhTypes<TA>::V;
   const MhProb& P = B.p[blockIdx.y];
   const int I = B.I, O = B.O, M = B.rows;
   // ---- XCD-aware tile number: linear id L on XCD L % 8; XCD x takes the
@@ -192,7 +212,7 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
   const __amdgpu_buffer_rsrc_t wr =
       mm8t_rsrc(reinterpret_cast<const char*>(P.wt) + (int64_t)(g0 < ngroups ? g0 : 0) * SB * MH_REC,
                 (uint32_t)((int64_t)gcount * SB * MH_REC));
-  auto xs = [&](int st) { return reinterpret_cast<_Float16*>(smem + st * MH_STAGE); };
+  auto xs = [&](int st) { return reinterpret_cast<E*>(smem + st * MH_STAGE); };
   typedef __attribute__((address_space(3))) void* lds_ptr;
 
   // x of step s into stage s % 3: wave w, round u writes rows 32 u + 8 w ..
@@ -220,9 +240,9 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
   };
   // W_hat of step s for the wave's group j = 0..3, sub-step h (load 2 j + h
   // of 8): lane offset 16 lane, the rest a scalar offset
-  auto issue_w = [&](int s, int j, int h, f16x8 (&bw)[4][2]) {
+  auto issue_w = [&](int s, int j, int h, V (&bw)[4][2]) {
     const int so = s < SB ? (j * SB + s) * (int)MH_REC + h * 1024 : (int)MM8T_OOB;
-    bw[j][h] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * lane, so, 0));
+    bw[j][h] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(wr, 16 * lane, so, 0));
   };
 
   f32x4 acc[16][4];
@@ -236,7 +256,7 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
   const int abase0 = n * MH_XS + 8 * ((2 * kg) ^ key);
   const int abase1 = n * MH_XS + 8 * ((2 * kg + 1) ^ key);
   auto lda = [&](int st, int h, int i) {
-    return *reinterpret_cast<const f16x8*>(xs(st) + (h ? abase1 : abase0) + 16 * i * MH_XS);
+    return *reinterpret_cast<const V*>(xs(st) + (h ? abase1 : abase0) + 16 * i * MH_XS);
   };
   // One sub-step: MFMAs of the 16 M tiles over A operands `a` (read during
   // the previous sub-step) while the next sub-step's 16 A operands are read
@@ -244,8 +264,8 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
   // of MFMAs to land.  `load(u)` issues the u-th of the sub-step's eight
   // global loads, one after every other M tile's MFMAs (a burst of loads
   // would stall the wave's issue while its MFMAs drain).
-  f16x8 a0[16], a1[16];  // A operands of sub-steps 0 and 1
-  auto substep = [&](const f16x8 (&a)[16], const f16x8 (&bw)[4][2], int h, f16x8 (&an)[16], int st_n, int h_n,
+  V a0[16], a1[16];  // A operands of sub-steps 0 and 1
+  auto substep = [&](const V (&a)[16], const V (&bw)[4][2], int h, V (&an)[16], int st_n, int h_n,
                      auto&& load) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -265,7 +285,7 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
   // the barrier that makes every wave's rows visible and puts every wave past
   // step s - 1's reads, x of step s + 2 into step s - 1's stage, and sub-step
   // 1 with step s + 1's sub-step 0 A reads.
-  auto step = [&](int s, const f16x8 (&bw)[4][2], f16x8 (&bwn)[4][2]) {
+  auto step = [&](int s, const V (&bw)[4][2], V (&bwn)[4][2]) {
     __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
     __builtin_amdgcn_sched_barrier(0);
     substep(a0, bw, 0, a1, s % MH_NST, 1, [&](int u) { issue_w(s + 1, u >> 1, u & 1, bwn); });
@@ -278,7 +298,7 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
   // prologue: W_hat of step 0, x of steps 0 and 1 in flight; step 0's rows
   // landed (only step 1's x loads may be pending) and visible, its sub-step
   // 0 A operands read
-  f16x8 bw0[4][2], bw1[4][2];
+  V bw0[4][2], bw1[4][2];
 #pragma unroll
   for (int u = 0; u < 8; ++u) issue_w(0, u >> 1, u & 1, bw0);
 #pragma unroll
@@ -302,7 +322,7 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
 
   // ---- epilogue: lane holds row 16 i + n and, in groups 2 p and 2 p + 1,
   // columns c0 = 32 p + 8 kg .. +3 and c0 + 4 .. +7 of the wave's 64
-  const __half* bp = reinterpret_cast<const __half*>(P.bias);
+  const TA* bp = reinterpret_cast<const TA*>(P.bias);
   const bool vec = P.vec;
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
@@ -310,7 +330,7 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
     if (c0 >= O) continue;
     float bo[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) bo[e] = bp && c0 + e < O ? __half2float(bp[c0 + e]) : 0.f;
+    for (int e = 0; e < 8; ++e) bo[e] = bp && c0 + e < O ? to_f32(bp[c0 + e]) : 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int64_t row = m0 + 16 * i + n;
@@ -324,11 +344,11 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
       const int64_t oi = row * O + c0;
       if (vec && c0 + 8 <= O) {
         if (P.epilogue == RWKV7MI_EPI_RESIDUAL) {
-          const f16x8 r = *reinterpret_cast<const f16x8*>(reinterpret_cast<const TA*>(P.residual) + oi);
+          const V r = *reinterpret_cast<const V*>(reinterpret_cast<const TA*>(P.residual) + oi);
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] += (float)r[e];
         }
-        f16x8 o8;
+        V o8;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float w = v[e];
@@ -336,9 +356,9 @@ __global__ __launch_bounds__(MH_THREADS, 1) void mm8h_gemm_kernel(const MhBatch 
             w = fmaxf(w, 0.f);
             w = w * w;
           }
-          o8[e] = (_Float16)w;
+          o8[e] = (E)w;
         }
-        *reinterpret_cast<f16x8*>(reinterpret_cast<TA*>(P.y) + oi) = o8;
+        *reinterpret_cast<V*>(reinterpret_cast<TA*>(P.y) + oi) = o8;
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -368,6 +388,7 @@ extern "C" int64_t rwkv7mi_mm8t_gemm_prefill_ws_bytes(int nprob, int64_t I, int6
 
 namespace rwkv7mi {
 // the GEMM over prepared W_hat records (b.p[i].wt), with the tile grid set here
+template <typename TA>
 static int mh_gemm_launch(MhBatch& b, int nprob, int64_t rows, int64_t I, int64_t O, void* stream,
                           const std::string& w) {
   b.rows = (int)rows;
@@ -389,7 +410,8 @@ static int mh_gemm_launch(MhBatch& b, int nprob, int64_t rows, int64_t I, int64_
     return check_launch("mm8h_gemm_kernel");
   };
   static std::atomic<uint64_t> raised_full{0}, raised_part{0};
-  return I % 64 == 0 ? launch(&mm8h_gemm_kernel<true>, raised_full) : launch(&mm8h_gemm_kernel<false>, raised_part);
+  return I % 64 == 0 ? launch(&mm8h_gemm_kernel<true, TA>, raised_full)
+                      : launch(&mm8h_gemm_kernel<false, TA>, raised_part);
 }
 
 // shape, workspace and per-problem checks shared by the two entries
@@ -410,7 +432,7 @@ static int mh_check(const std::string& w, int nprob, int64_t rows, int64_t I, in
   return RWKV7MI_OK;
 }
 
-static int mh_prob(const std::string& w, MhProb& q, const void* x, const __half* out, const void* bias,
+static int mh_prob(const std::string& w, MhProb& q, const void* x, const void* out, const void* bias,
                    const void* res, void* y, int epi, int64_t O) {
   if (!x || !y) return fail(RWKV7MI_EINVAL, w + ": null pointer");
   if (reinterpret_cast<uintptr_t>(x) & 15) return fail(RWKV7MI_EINVAL, w + ": x must be 16-byte aligned");
@@ -431,8 +453,8 @@ extern "C" int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x, con
                                             void* ws, int64_t ws_bytes, void* stream) {
   const std::string w("mm8t_gemm_prefill_ws");
   if (!x || !w_blk || !mx || !rx || !my || !ry || !y || !epilogue) return fail(RWKV7MI_EINVAL, w + ": null array");
-  if (act_dtype != RWKV7MI_F16 || meta_dtype != RWKV7MI_F16)
-    return fail(RWKV7MI_EINVAL, w + ": fp16 activations and fp16 metadata only");
+  if (!((act_dtype == RWKV7MI_F16 || act_dtype == RWKV7MI_BF16) && meta_dtype == act_dtype))
+    return fail(RWKV7MI_EINVAL, w + ": fp16 or bf16 activations with metadata of the same type");
   if (int rc = mh_check(w, nprob, rows, I, O, ws, ws_bytes)) return rc;
   if (rows == 0) return RWKV7MI_OK;
   const int64_t per_prob = rwkv7mi_mm8t_gemm_prefill_ws_bytes(1, I, O);
@@ -441,22 +463,26 @@ extern "C" int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x, con
   for (int i = 0; i < nprob; ++i) {
     if (!w_blk[i] || !mx[i] || !rx[i] || !my[i] || !ry[i]) return fail(RWKV7MI_EINVAL, w + ": null pointer");
     if (reinterpret_cast<uintptr_t>(w_blk[i]) & 15) return fail(RWKV7MI_EINVAL, w + ": the weights must be 16-byte aligned");
-    __half* out = reinterpret_cast<__half*>(static_cast<char*>(ws) + per_prob * i);
+    void* out = static_cast<char*>(ws) + per_prob * i;
     if (int rc = mh_prob(w, b.p[i], x[i], out, bias ? bias[i] : nullptr, residual ? residual[i] : nullptr, y[i],
                          epilogue[i], O))
       return rc;
-    d.p[i] = MhDeqProb{w_blk[i], (const __half*)mx[i], (const __half*)rx[i], (const __half*)my[i],
-                       (const __half*)ry[i], out};
+    d.p[i] = MhDeqProb{w_blk[i], mx[i], rx[i], my[i], ry[i], out};
   }
   d.I = (int)I;
   d.O = (int)O;
   d.SB = (int)((I + 63) / 64);
   d.KB = (int)((I + 127) / 128);
   const int64_t recs = (2 * ((O + 31) / 32)) * (int64_t)d.SB * 64;
-  hipLaunchKernelGGL(mm8h_dequant_kernel, dim3((unsigned)((recs + 255) / 256), (unsigned)nprob), dim3(256), 0,
-                     as_stream(stream), d);
+  const dim3 dgrid((unsigned)((recs + 255) / 256), (unsigned)nprob);
+  if (act_dtype == RWKV7MI_BF16) {
+    hipLaunchKernelGGL(mm8h_dequant_kernel<__hip_bfloat16>, dgrid, dim3(256), 0, as_stream(stream), d);
+    if (int rc = check_launch("mm8h_dequant_kernel")) return rc;
+    return mh_gemm_launch<__hip_bfloat16>(b, nprob, rows, I, O, stream, w);
+  }
+  hipLaunchKernelGGL(mm8h_dequant_kernel<__half>, dgrid, dim3(256), 0, as_stream(stream), d);
   if (int rc = check_launch("mm8h_dequant_kernel")) return rc;
-  return mh_gemm_launch(b, nprob, rows, I, O, stream, w);
+  return mh_gemm_launch<__half>(b, nprob, rows, I, O, stream, w);
 }
 
 extern "C" int rwkv7mi_dense_gemm_prefill_ws(int nprob, const void* const* x, const void* const* W,
@@ -465,7 +491,8 @@ extern "C" int rwkv7mi_dense_gemm_prefill_ws(int nprob, const void* const* x, co
                                              void* ws, int64_t ws_bytes, void* stream) {
   const std::string w("dense_gemm_prefill_ws");
   if (!x || !W || !y || !epilogue) return fail(RWKV7MI_EINVAL, w + ": null array");
-  if (act_dtype != RWKV7MI_F16) return fail(RWKV7MI_EINVAL, w + ": fp16 activations and weights only");
+  if (act_dtype != RWKV7MI_F16 && act_dtype != RWKV7MI_BF16)
+    return fail(RWKV7MI_EINVAL, w + ": fp16 or bf16 activations and weights");
   if (int rc = mh_check(w, nprob, rows, I, O, ws, ws_bytes)) return rc;
   if (rows == 0) return RWKV7MI_OK;
   const int64_t per_prob = rwkv7mi_mm8t_gemm_prefill_ws_bytes(1, I, O);
@@ -473,19 +500,24 @@ extern "C" int rwkv7mi_dense_gemm_prefill_ws(int nprob, const void* const* x, co
   MhRelBatch r{};
   for (int i = 0; i < nprob; ++i) {
     if (!W[i]) return fail(RWKV7MI_EINVAL, w + ": null pointer");
-    __half* out = reinterpret_cast<__half*>(static_cast<char*>(ws) + per_prob * i);
+    void* out = static_cast<char*>(ws) + per_prob * i;
     if (int rc = mh_prob(w, b.p[i], x[i], out, bias ? bias[i] : nullptr, residual ? residual[i] : nullptr, y[i],
                          epilogue[i], O))
       return rc;
-    r.w[i] = static_cast<const __half*>(W[i]);
+    r.w[i] = W[i];
     r.out[i] = out;
   }
   r.I = (int)I;
   r.O = (int)O;
   r.SB = (int)((I + 63) / 64);
   const int64_t recs = (2 * ((O + 31) / 32)) * (int64_t)r.SB * 64;
-  hipLaunchKernelGGL(mm8h_relayout_kernel, dim3((unsigned)((recs + 255) / 256), (unsigned)nprob), dim3(256), 0,
-                     as_stream(stream), r);
+  const dim3 rgrid((unsigned)((recs + 255) / 256), (unsigned)nprob);
+  if (act_dtype == RWKV7MI_BF16) {
+    hipLaunchKernelGGL(mm8h_relayout_kernel<__hip_bfloat16>, rgrid, dim3(256), 0, as_stream(stream), r);
+    if (int rc = check_launch("mm8h_relayout_kernel")) return rc;
+    return mh_gemm_launch<__hip_bfloat16>(b, nprob, rows, I, O, stream, w);
+  }
+  hipLaunchKernelGGL(mm8h_relayout_kernel<__half>, rgrid, dim3(256), 0, as_stream(stream), r);
   if (int rc = check_launch("mm8h_relayout_kernel")) return rc;
-  return mh_gemm_launch(b, nprob, rows, I, O, stream, w);
+  return mh_gemm_launch<__half>(b, nprob, rows, I, O, stream, w);
 }

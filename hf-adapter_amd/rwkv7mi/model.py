@@ -195,10 +195,10 @@ def random_weights(cfg: NativeRWKV7Config, *, seed: int = 0, device="cpu", dtype
 class DenseLinear:
     """Unquantised Linear ``y = x W^T`` (projections below the MM8 size
     threshold, and every projection of an unquantised model such as the fp32
-    0.1B one): the HIP dense kernel up to 256 rows; above that, for fp16, the
-    prefill MFMA GEMM (``rwkv7mi_dense_gemm_prefill_ws``: W copied into the
-    ``"mm8p"`` workspace in operand order, relu^2 / residual fused), and for
-    fp32 / bf16 weights a plain library GEMM (hipBLASLt through torch) with
+    0.1B one): the HIP dense kernel up to 256 rows; above that, for fp16 and
+    bf16, the prefill MFMA GEMM (``rwkv7mi_dense_gemm_prefill_ws``: W copied
+    into the ``"mm8p"`` workspace in operand order, relu^2 / residual fused),
+    and for fp32 weights a plain library GEMM (hipBLASLt through torch) with
     the epilogue as torch elementwise ops."""
 
     def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None = None):
@@ -208,7 +208,7 @@ class DenseLinear:
 
     def apply(self, x2, out, *, act=ACT_NONE, residual=None):
         rows = int(x2.shape[0])
-        if (rows > 256 and x2.dtype == torch.float16 and self.weight.dtype == torch.float16
+        if (rows > 256 and x2.dtype in (torch.float16, torch.bfloat16) and self.weight.dtype == x2.dtype
                 and self.in_features % 16 == 0 and act in (0, 3) and not (act == 3 and residual is not None)
                 and x2.is_contiguous() and out.is_contiguous()):
             epi = _lib.EPI_RELU2 if act == 3 else (_lib.EPI_RESIDUAL if residual is not None else _lib.EPI_NONE)
@@ -217,7 +217,7 @@ class DenseLinear:
             res = None if residual is None else residual.reshape(out.shape).contiguous()
             arr = _lib.ptr_array
             _lib.call("rwkv7mi_dense_gemm_prefill_ws", 1, arr([x2]), arr([self.weight]), arr([self.bias]), arr([res]),
-                      arr([out]), (ctypes.c_int * 1)(epi), rows, self.in_features, self.out_features, _lib.F16,
+                      arr([out]), (ctypes.c_int * 1)(epi), rows, self.in_features, self.out_features, _lib.dtype_code(x2),
                       _lib.ptr(ws), need, _lib.stream_of(x2))
             return out
         if rows > 256:
@@ -1033,7 +1033,7 @@ class NativeRWKV7ForCausalLM(_PreTrainedModel, _GenerationMixin):
                 if isinstance(L.r_proj, QuantLinear):
                     pneed = max(pneed, mm8_prefill_workspace_bytes(3, L.r_proj.in_features, L.r_proj.out_features))
             for lin in self._linears():
-                if isinstance(lin, QuantLinear) or (isinstance(lin, DenseLinear) and lin.weight.dtype == torch.float16):
+                if isinstance(lin, QuantLinear) or (isinstance(lin, DenseLinear) and lin.weight.dtype != torch.float32):
                     pneed = max(pneed, mm8_prefill_workspace_bytes(1, lin.in_features, lin.out_features))
             if pneed:
                 _ws.reserve(self.device, pneed, slot="mm8p")

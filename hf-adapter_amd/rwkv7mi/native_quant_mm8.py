@@ -369,8 +369,8 @@ def mm8_gemm_prefill_multi_into(xs, mods, outs, *, residuals=None, epilogues=Non
     materialised (into the device's ``"mm8p"`` workspace slot, in MFMA operand
     order) and one fp16 MFMA GEMM with the epilogue fused runs over it, as in
     the prefill projections of rwkv7_hf/native_jit_prefill.py:542-631,
-    955-1013.  fp16 activations with fp16 metadata; other dtypes run the
-    64-row tile GEMM over 256-row chunks (without a dequantised weight).
+    955-1013.  fp16 or bf16 activations with metadata of the same type; fp32
+    runs the 64-row tile GEMM over 256-row chunks (without a dequantised weight).
     Reserve the workspace (one eager call) before capturing a graph."""
     k = len(mods)
     if not 1 <= k <= 4 or len(xs) != k or len(outs) != k:
@@ -386,7 +386,7 @@ def mm8_gemm_prefill_multi_into(xs, mods, outs, *, residuals=None, epilogues=Non
             raise ValueError("mm8_gemm_prefill_multi_into: modules must be blocked MM8Linear of one shape")
         _check_out(x2, m, out, r)
     _lib.require_gpu(*xs, *outs, name="mm8_gemm_prefill_multi")
-    fast = xs[0].dtype == torch.float16 and all(md.mx.dtype == torch.float16 for md in mods)
+    fast = xs[0].dtype in (torch.float16, torch.bfloat16) and all(md.mx.dtype == xs[0].dtype for md in mods)
     chunk = max(1, _PREFILL_MAX_BYTES // (2 * n)) if fast else GEMM_ROWS
     eps = (ctypes.c_int * k)(*[int(e) for e in epilogues])
     arr = lambda ts: _lib.ptr_array(ts)
@@ -406,8 +406,8 @@ def mm8_gemm_prefill_multi_into(xs, mods, outs, *, residuals=None, epilogues=Non
         _lib.call(
             "rwkv7mi_mm8t_gemm_prefill_ws", k, arr(xc), arr([md.w_blk for md in mods]), arr([md.mx for md in mods]),
             arr([md.rx for md in mods]), arr([md.my for md in mods]), arr([md.ry for md in mods]),
-            arr([md.bias for md in mods]), arr(rc), arr(oc), eps, r1 - r0, n, m, _lib.F16, _lib.F16,
-            _lib.ptr(ws), need, _lib.stream_of(xs[0]),
+            arr([md.bias for md in mods]), arr(rc), arr(oc), eps, r1 - r0, n, m, _lib.dtype_code(xs[0]),
+            _lib.dtype_code(xs[0]), _lib.ptr(ws), need, _lib.stream_of(xs[0]),
         )
     return outs
 

@@ -425,10 +425,11 @@ int rwkv7mi_mm8t_gemm_prefill(int nprob, const void* const* x,
 int64_t rwkv7mi_mm8t_gemm_prefill_ws_bytes(int nprob, int64_t I, int64_t O);
 
 /* The prefill GEMM as the reference computes it, the faster form on gfx950:
- * the fp16 dequantised weight W_hat = fp16((w + 0.5) ry rx + my + mx) (the
- * bytes rwkv7mi_mm8_dequant writes) is materialised into the workspace in
- * MFMA operand order, then y = epilogue(x @ W_hat (+ bias)) runs on 256 x
- * 256 fp16 MFMA tiles.  Same arguments as rwkv7mi_mm8t_gemm_prefill plus the
+ * the dequantised weight W_hat = (w + 0.5) ry rx + my + mx, rounded once to
+ * the activation type (the bytes rwkv7mi_mm8_dequant writes), is
+ * materialised into the workspace in MFMA operand order, then
+ * y = epilogue(x @ W_hat (+ bias)) runs on 256 x 256 MFMA tiles.  fp16 or
+ * bf16 activations with metadata of the same type.  Same arguments as rwkv7mi_mm8t_gemm_prefill plus the
  * workspace (16-byte aligned, at least rwkv7mi_mm8t_gemm_prefill_ws_bytes;
  * its contents are overwritten).  Replaces mm8_matmul_triton's route for
  * rows > fused_max_rows, dequantize_mm8 then x @ W_hat
@@ -444,10 +445,11 @@ int rwkv7mi_mm8t_gemm_prefill_ws(int nprob, const void* const* x,
                                  int64_t O, int act_dtype, int meta_dtype,
                                  void* ws, int64_t ws_bytes, void* stream);
 
-/* The same prefill GEMM for unquantised fp16 nn.Linear weights W [O, I]
+/* The same prefill GEMM for unquantised fp16 or bf16 nn.Linear weights W [O, I]
  * (y = epilogue(x @ W^T (+ bias))): W is copied into the workspace in MFMA
- * operand order, then the 256 x 256 fp16 MFMA GEMM runs with the epilogue
- * fused.  fp16 activations and weights, I % 16 == 0, the workspace as for
+ * operand order, then the 256 x 256 MFMA GEMM runs with the epilogue
+ * fused.  Activations and weights of one type (fp16 or bf16), I % 16 == 0,
+ * the workspace as for
  * rwkv7mi_mm8t_gemm_prefill_ws (rwkv7mi_mm8t_gemm_prefill_ws_bytes).
  * Replaces the unquantised projections' torch GEMM of the prefill
  * (rwkv7_hf/native_jit_prefill.py:542-631, 955-1013). */
